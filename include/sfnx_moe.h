@@ -1,0 +1,116 @@
+/*
+ * sfnx_amd: the quantized mixture-of-experts hot path for MI355X (gfx950), behind a C ABI.
+ *
+ * Every entry point is stream-asynchronous on `st` (a hipStream_t passed as void*, null = the default stream), takes
+ * device pointers only, allocates nothing, never synchronises the host and is safe to capture into a HIP graph
+ * (unless its comment says otherwise).  Each returns 0 on success or a negative status; sfnx_last_error() then holds
+ * the message (thread-local).  The C++ header sfnx_amd/include/sfnx/kernels.hpp wraps these under the reference
+ * engine's own names, throwing std::runtime_error as the reference's wrappers do (src/kernels.cu:31-34).
+ *
+ * Citations are johnfink8/sfnx paths; each entry point names the reference interface it replaces.
+ *
+ * Weight matrices are the "planar" store (sfnx_store_pack): per matrix of R rows x C columns,
+ *   Q4_K: a nibble plane of R x C/2 bytes, then a header plane of R x C/256 x 16 bytes (f16 d, f16 dmin, 12 scale
+ *         bytes, byte-identical to the GGUF super-block's first 16 bytes).  Within each 256-byte run of a row's nibble
+ *         plane (the quants of two super-blocks), the 16-byte halves are ordered [half][group of 64 values], so a
+ *         wavefront's 16-byte loads cover whole 128-byte lines.
+ *   Q8_0: an int8 plane of R x C bytes (16-byte halves of each 512-byte run ordered [half][block]), then an f16 scale
+ *         plane of R x C/32.
+ * The planar matrix has exactly the GGUF matrix's size; experts sit at base + e * stride.  C % 512 == 0.
+ */
+#ifndef SFNX_MOE_H
+#define SFNX_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SFNX_MAXT 16     /* rows of a decode window (src/model.hpp:48 MAXT) */
+#define SFNX_PF_JOB 64   /* rows of a prompt-path job (src/kernels.hpp:26 PF_JOB) */
+
+enum { SFNX_Q8_0 = 8, SFNX_Q4_K = 12 }; /* GgmlType ids, src/gguf.hpp:22-25 */
+
+/* src/kernels.hpp:18-23: one expert's matrix applied to up to SFNX_MAXT activation rows */
+typedef struct sfnx_job {
+    int w;                    /* expert */
+    int n;                    /* rows */
+    int y[SFNX_MAXT];         /* activation rows */
+    int out[SFNX_MAXT];       /* output rows */
+} sfnx_job;
+
+/* src/kernels.hpp:25-32 */
+typedef struct sfnx_bigjob {
+    int w;
+    int n;
+    int y[SFNX_PF_JOB];
+    int out[SFNX_PF_JOB];
+} sfnx_bigjob;
+
+/* ---------------------------------------------------------------------------------------------- errors */
+const char* sfnx_last_error(void);
+int sfnx_abi_version(void);
+
+/* ---------------------------------------------------------------------------------------------- weight store */
+/* bytes of one row of `cols` values (src/gguf.cpp:19-37 type_info: Q4_K 256/144, Q8_0 32/34) */
+size_t sfnx_row_bytes(uint32_t type, int cols);
+/* seeded synthetic values: out[i] = std * IrwinHall12(seed, offset + i) (splitmix64 draws) */
+int sfnx_synth_normal(float* out, size_t n, uint64_t seed, uint64_t offset, float std, void* st);
+/* fp32 rows -> GGUF blocks (Q4_K: the library's quantizer; Q8_0: tools/mtp_experts.py:44-55) */
+int sfnx_quantize_weights(uint32_t type, const float* x, void* gguf, int64_t rows, int cols, void* st);
+/* GGUF blocks of n_mat matrices [rows][cols] <-> the planar store (replaces the loader's slicing into DW,
+ * src/model.cpp:554-606; the store keeps every block's bytes, only their places change) */
+int sfnx_store_pack(uint32_t type, const void* gguf, void* planar, int64_t n_mat, int rows, int cols, void* st);
+int sfnx_store_unpack(uint32_t type, const void* planar, void* gguf, int64_t n_mat, int rows, int cols, void* st);
+/* planar -> fp32 (d sc q - dmin m; d q) and -> f16 bits as the tensor-core path makes them (src/moe_mma.cuh:67-216) */
+int sfnx_dequantize(uint32_t type, const void* planar, float* y, int64_t n_mat, int rows, int cols, void* st);
+int sfnx_dequantize_f16(uint32_t type, const void* planar, uint16_t* y, int64_t n_mat, int rows, int cols, void* st);
+
+/* ---------------------------------------------------------------------------------------------- activations */
+/* src/kernels.hpp:36 quantize_q8_1: fp32 rows of n -> q8_1 blocks (36 bytes per 32 values) */
+int sfnx_quantize_q8_1(const float* x, void* q, int n, int rows, void* st);
+
+/* ---------------------------------------------------------------------------------------------- routing */
+/* src/kernels.hpp:269-278 router_route (decode window, 1 <= T <= 16).  logits [T][E + 1] = W [E + 1][H] . x[t] (row E
+ * gates the shared expert); top-K per token among the first E by logit, ties to the lower index; weights the selected
+ * softmax renormalised; jobs: one per distinct expert in first-pick order, rows in pair order (pair p = t K + k:
+ * gu.y = t, gu.out = dn.y = dn.out = p).  shared != 0: one more job, expert E, rows t -> T K + t.  njobs[0] = job
+ * count; njobs[1] is the launch's block counter and must be 0 before the first call (every call leaves it 0).
+ * H % 256 == 0, H <= 4096; E % 64 == 0, E <= 1024; 1 <= K <= 16.  Pick rounds with nothing left (NaN / -inf logits)
+ * write topi -1, topw 0 and leave the pair out of the jobs. */
+int sfnx_router_route(const float* W, const float* x, float* logits, int T, int H, int E, int K, int* topi, float* topw,
+                      sfnx_job* jobs_gu, sfnx_job* jobs_dn, int* njobs, int shared, void* st);
+/* the router's logits alone, [T][L] = W [L][H] . x[t], any T (the prompt path's sgemm, src/prefill.cu:1163) */
+int sfnx_router_logits(const float* W, const float* x, float* logits, int T, int H, int L, void* st);
+/* src/prefill.cu:189-279 (k_pf_top10, k_pf_count, k_pf_jobbase, k_pf_fill): top-K of rows of E + 1 logits, cnt[E],
+ * jbase[E] (exclusive scan of ceil(cnt / 64)), BigJobs of each expert's pairs in pair order.  shared != 0: ceil(C/64)
+ * more jobs of expert E, rows t -> C K + t.  Job capacity needed: C K / 64 + E + ceil(C / 64). */
+int sfnx_pf_route(const float* logits, int C, int E, int K, int* topi, float* topw, int* cnt, int* jbase,
+                  sfnx_bigjob* jobs_gu, sfnx_bigjob* jobs_dn, int* njobs, int shared, void* st);
+
+/* ---------------------------------------------------------------------------------------------- routed experts */
+/* src/kernels.hpp:281-282 moe_gate_up: gu[job.out[j]][r] = A_e[r] . xq[job.y[j]] for r < n_out, jobs [0, *njobs);
+ * A: planar experts (n_out rows of n_in, stride sa bytes); xq: q8_1 rows of n_in; T: the most rows a job holds */
+int sfnx_moe_gate_up(const void* A, size_t sa, uint32_t type, int n_in, int n_out, const sfnx_job* jobs,
+                     const int* njobs, int njobs_max, int T, const void* xq, float* gu, void* st);
+/* src/kernels.hpp:305 moe_down: h = silu(gate) * up of gu rows job.y[j] ([gate (n_in) | up (n_in)]) as q8_1, then
+ * part[job.out[j]][r] = A_e[r] . h (the Q4_K down the reference refuses, src/moe.cuh:473-474, included) */
+int sfnx_moe_down(const void* A, size_t sa, uint32_t type, int n_in, int n_out, const sfnx_job* jobs, const int* njobs,
+                  int njobs_max, int T, const float* gu, float* part, void* st);
+/* src/kernels.hpp:286-287 moe_gate_up_big / moe_down_big: the same arithmetic over BigJobs (the q8 prompt path) */
+int sfnx_moe_gate_up_big(const void* A, size_t sa, uint32_t type, int n_in, int n_out, const sfnx_bigjob* jobs,
+                         const int* njobs, int njobs_cap, const void* xq, float* gu, void* st);
+int sfnx_moe_down_big(const void* A, size_t sa, uint32_t type, int n_in, int n_out, const sfnx_bigjob* jobs,
+                      const int* njobs, int njobs_cap, const float* gu, float* part, void* st);
+/* the weighted sum (src/kernels.cu:797-803 ring_x, src/prefill.cu:476-484 k_pfr_addend):
+ * y[t][i] = fmaf(sigmoid(logits[t][E]), part[T K + t][i], sum_k fmaf(topw[t K + k], part[t K + k][i], .)) in k order;
+ * shared == 0 drops the shared term; pairs with topi < 0 are skipped */
+int sfnx_moe_combine(const float* part, const float* topw, const int* topi, const float* logits, float* y, int T, int H,
+                     int E, int K, int shared, void* st);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,614 @@
+/*
+ * CPU oracle for the quantized MoE layer.  TEST INFRASTRUCTURE ONLY (see oracle.h): never linked into the product.
+ * Built with -ffp-contract=off so every float expression rounds exactly as written; fused steps call fmaf.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#include <time.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ------------------------------------------------------------------------------------------------ f16 */
+float orc_f16_to_f32(uint16_t h) {
+    const uint32_t s = (uint32_t) (h & 0x8000u) << 16, e = (h >> 10) & 31u, m = h & 0x3ffu;
+    uint32_t bits;
+    if (e == 0) {
+        if (m == 0) bits = s;
+        else {   /* subnormal: m * 2^-24, exact in fp32 */
+            float v = (float) m * 5.9604644775390625e-8f;
+            memcpy(&bits, &v, 4);
+            bits |= s;
+        }
+    } else if (e == 31) bits = s | 0x7f800000u | (m << 13);
+    else bits = s | ((e + 112u) << 23) | (m << 13);
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+/* round-to-nearest-even of sign * mag * 2^e to f16 */
+static uint16_t f16_round(int neg, unsigned __int128 mag, int e) {
+    const uint16_t sg = neg ? 0x8000u : 0u;
+    if (mag == 0) return sg;
+    int hb = 127;
+    while (!((mag >> hb) & 1)) --hb;
+    int q = hb + e - 10;   /* exponent of the result's last mantissa bit */
+    if (q < -24) q = -24;
+    const int shift = q - e;
+    unsigned __int128 r;
+    if (shift <= 0) r = mag << (-shift);
+    else {
+        r = mag >> shift;
+        const unsigned __int128 rem = mag - (r << shift), half = (unsigned __int128) 1 << (shift - 1);
+        if (rem > half || (rem == half && (r & 1))) ++r;
+    }
+    if (r >= 2048) {   /* the rounding carried into a new bit */
+        r >>= 1;
+        ++q;
+    }
+    if (r < 1024) return (uint16_t) (sg | (uint16_t) r);   /* subnormal (q == -24) */
+    const int E = q + 25;
+    if (E >= 31) return (uint16_t) (sg | 0x7c00u);
+    return (uint16_t) (sg | (uint16_t) (E << 10) | (uint16_t) (r & 0x3ffu));
+}
+
+uint16_t orc_f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const int neg = (x >> 31) & 1;
+    const uint32_t ax = x & 0x7fffffffu;
+    if (ax >= 0x7f800000u) return (uint16_t) ((neg ? 0x8000u : 0u) | (ax > 0x7f800000u ? 0x7e00u : 0x7c00u));
+    if (ax == 0) return neg ? 0x8000u : 0u;
+    const int ef = (int) (ax >> 23);
+    const uint32_t m = ef ? ((ax & 0x7fffffu) | 0x800000u) : (ax & 0x7fffffu);
+    return f16_round(neg, m, (ef ? ef : 1) - 150);
+}
+
+/* an f16 as sign, integer mantissa and exponent: |v| = M 2^E; returns 0 for inf / NaN */
+static int f16_parts(uint16_t h, int* neg, int64_t* M, int* E) {
+    const int e = (h >> 10) & 31, m = h & 0x3ff;
+    *neg = (h >> 15) & 1;
+    if (e == 31) return 0;
+    if (e == 0) {
+        *M = m;
+        *E = -24;
+    } else {
+        *M = m | 0x400;
+        *E = e - 25;
+    }
+    return 1;
+}
+
+uint16_t orc_f16_fma(uint16_t a, uint16_t b, uint16_t c) {
+    int na, nb, nc, ea, eb, ec;
+    int64_t ma, mb, mc;
+    if (!f16_parts(a, &na, &ma, &ea) || !f16_parts(b, &nb, &mb, &eb) || !f16_parts(c, &nc, &mc, &ec))
+        return orc_f32_to_f16(fmaf(orc_f16_to_f32(a), orc_f16_to_f32(b), orc_f16_to_f32(c)));
+    const int np = na ^ nb, ep = ea + eb;
+    const int64_t mp = ma * mb;
+    if (mp == 0 && mc == 0) return (np && nc) ? 0x8000u : 0u;
+    const int e0 = ep < ec ? ep : ec;
+    __int128 sp = (__int128) mp << (ep - e0), sc = (__int128) mc << (ec - e0);
+    if (np) sp = -sp;
+    if (nc) sc = -sc;
+    const __int128 s = sp + sc;
+    if (s == 0) return 0u;   /* exact cancellation: +0 under round-to-nearest */
+    return f16_round(s < 0, (unsigned __int128) (s < 0 ? -s : s), e0);
+}
+
+uint16_t orc_f16_mul(uint16_t a, uint16_t b) {
+    int na, nb, ea, eb;
+    int64_t ma, mb;
+    if (!f16_parts(a, &na, &ma, &ea) || !f16_parts(b, &nb, &mb, &eb))
+        return orc_f32_to_f16(orc_f16_to_f32(a) * orc_f16_to_f32(b));
+    return f16_round(na ^ nb, (unsigned __int128) (ma * mb), ea + eb);
+}
+
+/* ------------------------------------------------------------------------------------------------ synthetic data */
+static inline uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+static inline float synth_one(uint64_t seed, uint64_t i, float std) {
+    int64_t s = 0;
+    for (int m = 0; m < 6; ++m) {
+        const uint64_t r = mix64(seed + (6 * i + (uint64_t) m + 1) * 0x9e3779b97f4a7c15ull);
+        s += (int64_t) (r & 0xffffffu) + (int64_t) ((r >> 32) & 0xffffffu);
+    }
+    const float z = (float) (int32_t) (s - 6 * (1ll << 24)) * 5.9604644775390625e-8f;
+    return z * std;
+}
+void orc_synth_normal(float* out, size_t n, uint64_t seed, uint64_t offset, float std) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < (int64_t) n; ++i) out[i] = synth_one(seed, offset + (uint64_t) i, std);
+}
+
+/* ------------------------------------------------------------------------------------------------ weight formats */
+void orc_q4k_scale_min(const uint8_t* s, int j, int* sc, int* m) {
+    if (j < 4) {
+        *sc = s[j] & 63;
+        *m = s[j + 4] & 63;
+    } else {
+        *sc = (s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4);
+        *m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+    }
+}
+
+static inline int clampi(int v, int lo, int hi) { return v < lo ? lo : v > hi ? hi : v; }
+
+static void quant_q4k_block(const float* x, uint8_t* b) {
+    float scale[8], mn8[8], max_scale = 0.f, max_min = 0.f;
+    for (int j = 0; j < 8; ++j) {
+        float mn = x[32 * j], mx = x[32 * j];
+        for (int l = 1; l < 32; ++l) {
+            if (x[32 * j + l] < mn) mn = x[32 * j + l];
+            if (x[32 * j + l] > mx) mx = x[32 * j + l];
+        }
+        if (mn > 0.f) mn = 0.f;
+        scale[j] = (mx - mn) / 15.0f;
+        mn8[j] = mn < 0.f ? -mn : 0.f;
+        if (scale[j] > max_scale) max_scale = scale[j];
+        if (mn8[j] > max_min) max_min = mn8[j];
+    }
+    const uint16_t dh = orc_f32_to_f16(max_scale / 63.0f), mh = orc_f32_to_f16(max_min / 63.0f);
+    const float df = orc_f16_to_f32(dh), mf = orc_f16_to_f32(mh);
+    int sc[8], m[8];
+    for (int j = 0; j < 8; ++j) {
+        sc[j] = df > 0.f ? clampi((int) roundf(scale[j] / df), 0, 63) : 0;
+        m[j] = mf > 0.f ? clampi((int) roundf(mn8[j] / mf), 0, 63) : 0;
+    }
+    memcpy(b, &dh, 2);
+    memcpy(b + 2, &mh, 2);
+    uint8_t* s = b + 4;
+    for (int j = 0; j < 4; ++j) {
+        s[j] = (uint8_t) ((sc[j] & 63) | ((sc[j + 4] >> 4) << 6));
+        s[j + 4] = (uint8_t) ((m[j] & 63) | ((m[j + 4] >> 4) << 6));
+        s[j + 8] = (uint8_t) ((sc[j + 4] & 0xF) | ((m[j + 4] & 0xF) << 4));
+    }
+    uint8_t* qs = b + 16;
+    memset(qs, 0, 128);
+    for (int j = 0; j < 8; ++j) {
+        const float dl = df * (float) sc[j], ml = mf * (float) m[j];
+        for (int l = 0; l < 32; ++l) {
+            const int q = dl > 0.f ? clampi((int) roundf((x[32 * j + l] + ml) / dl), 0, 15) : 0;
+            qs[32 * (j / 2) + l] |= (uint8_t) (q << (4 * (j % 2)));
+        }
+    }
+}
+
+void orc_quantize_q4_k(const float* x, void* dst, int64_t rows, int cols) {
+    const int nb = cols / 256;
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; ++r)
+        for (int b = 0; b < nb; ++b)
+            quant_q4k_block(x + r * cols + 256 * b, (uint8_t*) dst + (r * nb + b) * ORC_Q4K_BYTES);
+}
+
+void orc_quantize_q8_0(const float* x, void* dst, int64_t rows, int cols) {
+    const int64_t nblk = rows * (cols / 32);
+#pragma omp parallel for schedule(static)
+    for (int64_t k = 0; k < nblk; ++k) {
+        const float* v = x + 32 * k;
+        uint8_t* b = (uint8_t*) dst + k * ORC_Q80_BYTES;
+        float amax = 0.f;
+        for (int l = 0; l < 32; ++l) amax = fabsf(v[l]) > amax ? fabsf(v[l]) : amax;
+        const float d = amax / 127.0f, idv = d != 0.f ? 1.0f / d : 0.f;
+        const uint16_t dh = orc_f32_to_f16(d);
+        memcpy(b, &dh, 2);
+        for (int l = 0; l < 32; ++l) {
+            const float t = v[l] * idv;
+            const float a = floorf(fabsf(t) + 0.5f);
+            b[2 + l] = (uint8_t) (int8_t) (int) (t < 0.f ? -a : a);
+        }
+    }
+}
+
+void orc_dequant_q4_k(const void* src, float* y, int64_t rows, int cols) {
+    const int64_t nblk = rows * (cols / 256);
+    for (int64_t k = 0; k < nblk; ++k) {
+        const uint8_t* p = (const uint8_t*) src + k * ORC_Q4K_BYTES;
+        uint16_t dh, mh;
+        memcpy(&dh, p, 2);
+        memcpy(&mh, p + 2, 2);
+        const float d = orc_f16_to_f32(dh), dmin = orc_f16_to_f32(mh);
+        for (int j = 0; j < 8; ++j) {
+            int sc, m;
+            orc_q4k_scale_min(p + 4, j, &sc, &m);
+            const float d1 = d * (float) sc, m1 = dmin * (float) m;
+            const uint8_t* q = p + 16 + 32 * (j / 2);
+            for (int l = 0; l < 32; ++l) y[256 * k + 32 * j + l] = d1 * (float) ((q[l] >> (4 * (j % 2))) & 0xF) - m1;
+        }
+    }
+}
+
+void orc_dequant_q4_k_f16(const void* src, uint16_t* y, int64_t rows, int cols) {
+    const int64_t nblk = rows * (cols / 256);
+    for (int64_t k = 0; k < nblk; ++k) {
+        const uint8_t* p = (const uint8_t*) src + k * ORC_Q4K_BYTES;
+        uint16_t dh, mh;
+        memcpy(&dh, p, 2);
+        memcpy(&mh, p + 2, 2);
+        const float d = orc_f16_to_f32(dh), dmin = orc_f16_to_f32(mh);
+        for (int j = 0; j < 8; ++j) {
+            int sc, m;
+            orc_q4k_scale_min(p + 4, j, &sc, &m);
+            const uint16_t d1 = orc_f32_to_f16(d * (float) sc), nm1 = orc_f32_to_f16(-(dmin * (float) m));
+            const uint8_t* q = p + 16 + 32 * (j / 2);
+            for (int l = 0; l < 32; ++l) {
+                const uint16_t qh = orc_f32_to_f16((float) ((q[l] >> (4 * (j % 2))) & 0xF));
+                y[256 * k + 32 * j + l] = orc_f16_fma(qh, d1, nm1);
+            }
+        }
+    }
+}
+
+void orc_dequant_q8_0(const void* src, float* y, int64_t rows, int cols) {
+    const int64_t nblk = rows * (cols / 32);
+    for (int64_t k = 0; k < nblk; ++k) {
+        const uint8_t* p = (const uint8_t*) src + k * ORC_Q80_BYTES;
+        uint16_t dh;
+        memcpy(&dh, p, 2);
+        const float d = orc_f16_to_f32(dh);
+        for (int l = 0; l < 32; ++l) y[32 * k + l] = d * (float) (int8_t) p[2 + l];
+    }
+}
+
+void orc_dequant_q8_0_f16(const void* src, uint16_t* y, int64_t rows, int cols) {
+    const int64_t nblk = rows * (cols / 32);
+    for (int64_t k = 0; k < nblk; ++k) {
+        const uint8_t* p = (const uint8_t*) src + k * ORC_Q80_BYTES;
+        uint16_t dh;
+        memcpy(&dh, p, 2);
+        for (int l = 0; l < 32; ++l) y[32 * k + l] = orc_f16_mul(orc_f32_to_f16((float) (int8_t) p[2 + l]), dh);
+    }
+}
+
+/* ------------------------------------------------------------------------------------------------ activations */
+/* a xor butterfly over n lanes (n a power of two): every lane ends with the same value, lane 0's is returned */
+static float butterfly_sum(const float* v, int n) {
+    float a[64], b[64];
+    memcpy(a, v, (size_t) n * sizeof(float));
+    for (int o = n / 2; o; o >>= 1) {
+        for (int l = 0; l < n; ++l) b[l] = a[l] + a[l ^ o];
+        memcpy(a, b, (size_t) n * sizeof(float));
+    }
+    return a[0];
+}
+
+static void q8_1_block(const float* x, uint8_t* blk) {
+    float amax = 0.f;
+    for (int l = 0; l < 32; ++l) amax = fabsf(x[l]) > amax ? fabsf(x[l]) : amax;
+    const float sum = butterfly_sum(x, 32);
+    const float d = amax / 127.0f;
+    for (int l = 0; l < 32; ++l) blk[4 + l] = (uint8_t) (int8_t) (amax == 0.f ? 0 : (int) roundf(x[l] / d));
+    const uint16_t dh = orc_f32_to_f16(d), sh = orc_f32_to_f16(sum);
+    memcpy(blk, &dh, 2);
+    memcpy(blk + 2, &sh, 2);
+}
+
+void orc_quantize_q8_1(const float* x, void* q, int n, int rows) {
+    for (int64_t r = 0; r < rows; ++r)
+        for (int b = 0; b < n / 32; ++b) q8_1_block(x + r * n + 32 * b, (uint8_t*) q + (r * (n / 32) + b) * ORC_Q81_BYTES);
+}
+
+static inline float silu_(float x) { return x / (1.0f + expf(-x)); }
+static inline float sigm_(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+void orc_swiglu_q8_1(const float* gu, int ff, void* hq) {
+    float h[32];
+    for (int b = 0; b < ff / 32; ++b) {
+        for (int l = 0; l < 32; ++l) h[l] = silu_(gu[32 * b + l]) * gu[ff + 32 * b + l];
+        q8_1_block(h, (uint8_t*) hq + (size_t) b * ORC_Q81_BYTES);
+    }
+}
+
+/* ------------------------------------------------------------------------------------------------ routing */
+static float router_dot(const float* w, const float* x, int H) {
+    float lane[64];
+    for (int l = 0; l < 64; ++l) {
+        float a = 0.f;
+        for (int c = l; c < H / 4; c += 64)
+            for (int u = 0; u < 4; ++u) a = fmaf(w[4 * c + u], x[4 * c + u], a);
+        lane[l] = a;
+    }
+    return butterfly_sum(lane, 64);
+}
+
+void orc_router_logits(const float* W, const float* x, float* logits, int T, int H, int L) {
+#pragma omp parallel for schedule(static)
+    for (int r = 0; r < L; ++r)
+        for (int t = 0; t < T; ++t) logits[(size_t) t * L + r] = router_dot(W + (size_t) r * H, x + (size_t) t * H, H);
+}
+
+int orc_topk(const float* logits, int T, int E, int ld, int K, int* topi, float* topw) {
+    int missing = 0;
+    unsigned char* taken = (unsigned char*) malloc((size_t) E);
+    for (int t = 0; t < T; ++t) {
+        const float* v = logits + (size_t) t * ld;
+        memset(taken, 0, (size_t) E);
+        float top0 = 0.f, z = 0.f, ek[64];
+        for (int k = 0; k < K; ++k) {
+            float bv = -INFINITY;
+            int bi = -1;
+            for (int i = 0; i < E; ++i)
+                if (!taken[i] && v[i] > bv) {
+                    bv = v[i];
+                    bi = i;
+                }
+            topi[t * K + k] = bi;
+            if (bi < 0) {
+                ek[k] = 0.f;
+                ++missing;
+                continue;
+            }
+            taken[bi] = 1;
+            if (k == 0) top0 = bv;
+            ek[k] = expf(bv - top0);
+            z += ek[k];
+        }
+        for (int k = 0; k < K; ++k) topw[t * K + k] = topi[t * K + k] < 0 ? 0.f : ek[k] / z;
+    }
+    free(taken);
+    return missing;
+}
+
+int orc_jobs_decode(const int* topi, int T, int K, int E, int shared, orc_job* gu, orc_job* dn) {
+    int nj = 0;
+    for (int p = 0; p < T * K; ++p) {
+        const int e = topi[p];
+        if (e < 0) continue;
+        int j = 0;
+        while (j < nj && gu[j].w != e) ++j;
+        if (j == nj) {
+            memset(&gu[j], 0, sizeof(orc_job));
+            memset(&dn[j], 0, sizeof(orc_job));
+            gu[j].w = dn[j].w = e;
+            ++nj;
+        }
+        const int s = gu[j].n++;
+        dn[j].n++;
+        gu[j].y[s] = p / K;
+        gu[j].out[s] = dn[j].y[s] = dn[j].out[s] = p;
+    }
+    if (shared) {
+        memset(&gu[nj], 0, sizeof(orc_job));
+        memset(&dn[nj], 0, sizeof(orc_job));
+        gu[nj].w = dn[nj].w = E;
+        gu[nj].n = dn[nj].n = T;
+        for (int t = 0; t < T; ++t) {
+            gu[nj].y[t] = t;
+            gu[nj].out[t] = dn[nj].y[t] = dn[nj].out[t] = T * K + t;
+        }
+        ++nj;
+    }
+    return nj;
+}
+
+int orc_jobs_prefill(const int* topi, int C, int K, int E, int shared, int* cnt, int* jbase, orc_bigjob* gu,
+                     orc_bigjob* dn) {
+    const int P = C * K;
+    memset(cnt, 0, (size_t) E * sizeof(int));
+    for (int p = 0; p < P; ++p)
+        if (topi[p] >= 0) cnt[topi[p]]++;
+    int acc = 0;
+    for (int e = 0; e < E; ++e) {
+        jbase[e] = acc;
+        acc += (cnt[e] + ORC_PF_JOB - 1) / ORC_PF_JOB;
+    }
+    int* fill = (int*) calloc((size_t) E, sizeof(int));
+    for (int p = 0; p < P; ++p) {
+        const int e = topi[p];
+        if (e < 0) continue;
+        const int s = fill[e]++, j = jbase[e] + s / ORC_PF_JOB, k = s % ORC_PF_JOB;
+        if (k == 0) {
+            memset(&gu[j], 0, sizeof(orc_bigjob));
+            memset(&dn[j], 0, sizeof(orc_bigjob));
+            gu[j].w = dn[j].w = e;
+            gu[j].n = dn[j].n = cnt[e] - (s / ORC_PF_JOB) * ORC_PF_JOB < ORC_PF_JOB ? cnt[e] - (s / ORC_PF_JOB) * ORC_PF_JOB
+                                                                                    : ORC_PF_JOB;
+        }
+        gu[j].y[k] = p / K;
+        gu[j].out[k] = p;
+        dn[j].y[k] = p;
+        dn[j].out[k] = p;
+    }
+    free(fill);
+    if (shared)
+        for (int t0 = 0; t0 < C; t0 += ORC_PF_JOB) {
+            const int j = acc++;
+            memset(&gu[j], 0, sizeof(orc_bigjob));
+            memset(&dn[j], 0, sizeof(orc_bigjob));
+            gu[j].w = dn[j].w = E;
+            gu[j].n = dn[j].n = C - t0 < ORC_PF_JOB ? C - t0 : ORC_PF_JOB;
+            for (int k = 0; k < gu[j].n; ++k) {
+                gu[j].y[k] = t0 + k;
+                gu[j].out[k] = dn[j].y[k] = dn[j].out[k] = P + t0 + k;
+            }
+        }
+    return acc;
+}
+
+/* ------------------------------------------------------------------------------------------------ expert dots */
+static float q4k_group_term(const uint8_t* blk, int jg, const uint8_t* ya, const uint8_t* yb) {
+    uint16_t dh, mh, d8a, d8b;
+    memcpy(&dh, blk, 2);
+    memcpy(&mh, blk + 2, 2);
+    memcpy(&d8a, ya, 2);
+    memcpy(&d8b, yb, 2);
+    const float d = orc_f16_to_f32(dh), dmin = orc_f16_to_f32(mh);
+    int sc0i, m0i, sc1i, m1i;
+    orc_q4k_scale_min(blk + 4, 2 * jg, &sc0i, &m0i);
+    orc_q4k_scale_min(blk + 4, 2 * jg + 1, &sc1i, &m1i);
+    const float sc0 = (float) sc0i, m0 = (float) m0i, sc1 = (float) sc1i, m1 = (float) m1i;
+    const uint8_t* q = blk + 16 + 32 * jg;
+    int dl = 0, dhi = 0, sl = 0, sh = 0;
+    for (int l = 0; l < 32; ++l) {
+        const int al = (int8_t) ya[4 + l], ah = (int8_t) yb[4 + l];
+        dl += (q[l] & 15) * al;
+        dhi += (q[l] >> 4) * ah;
+        sl += al;
+        sh += ah;
+    }
+    const float d8l = orc_f16_to_f32(d8a), d8h = orc_f16_to_f32(d8b);
+    return d * (d8l * (sc0 * (float) dl) + d8h * (sc1 * (float) dhi)) -
+           dmin * (d8l * (m0 * (float) sl) + d8h * (m1 * (float) sh));
+}
+
+float orc_dot_q4_k(const uint8_t* wrow, const uint8_t* yq, int K) {
+    const int gpl = K / 64 / 8;
+    float lane[8];
+    for (int l8 = 0; l8 < 8; ++l8) {
+        float tmp = 0.f;
+        for (int i = 0; i < gpl; ++i) {
+            const int g = l8 + 8 * i, b = g >> 2, jg = g & 3;
+            const uint8_t* ya = yq + (size_t) (b * 8 + jg * 2) * ORC_Q81_BYTES;
+            tmp += q4k_group_term(wrow + (size_t) b * ORC_Q4K_BYTES, jg, ya, ya + ORC_Q81_BYTES);
+        }
+        lane[l8] = tmp;
+    }
+    return butterfly_sum(lane, 8);
+}
+
+float orc_dot_q8_0(const uint8_t* wrow, const uint8_t* yq, int K) {
+    const int nb = K / 32;
+    float lane[16];
+    for (int l = 0; l < 16; ++l) {
+        float acc = 0.f;
+        for (int b = l; b < nb; b += 16) {
+            const uint8_t* w = wrow + (size_t) b * ORC_Q80_BYTES;
+            const uint8_t* a = yq + (size_t) b * ORC_Q81_BYTES;
+            uint16_t dw, da;
+            memcpy(&dw, w, 2);
+            memcpy(&da, a, 2);
+            int s = 0;
+            for (int k = 0; k < 32; ++k) s += (int) (int8_t) w[2 + k] * (int) (int8_t) a[4 + k];
+            acc += (orc_f16_to_f32(dw) * orc_f16_to_f32(da)) * (float) s;
+        }
+        lane[l] = acc;
+    }
+    return butterfly_sum(lane, 16);
+}
+
+float orc_dot(int type, const uint8_t* wrow, const uint8_t* yq, int K) {
+    return type == ORC_Q4_K ? orc_dot_q4_k(wrow, yq, K) : orc_dot_q8_0(wrow, yq, K);
+}
+
+static size_t row_bytes(int type, int cols) {
+    return type == ORC_Q4_K ? (size_t) cols / 256 * ORC_Q4K_BYTES : (size_t) cols / 32 * ORC_Q80_BYTES;
+}
+
+/* ------------------------------------------------------------------------------------------------ the layer */
+void orc_layer_decode(const orc_layer* L, const float* x, int T, float* y, float* logits_out, int* topi_out,
+                      float* topw_out, float* gu_out, float* part_out, int nthreads) {
+    const int H = L->H, E = L->E, K = L->K, ff = L->ff, P = T * K, NP = P + (L->shared ? T : 0);
+    const size_t gurb = row_bytes(L->type, H), dnrb = row_bytes(L->type, ff);
+    uint8_t* xq = (uint8_t*) malloc((size_t) T * (H / 32) * ORC_Q81_BYTES);
+    float* logits = logits_out ? logits_out : (float*) malloc((size_t) T * (E + 1) * sizeof(float));
+    int* topi = topi_out ? topi_out : (int*) malloc((size_t) P * sizeof(int));
+    float* topw = topw_out ? topw_out : (float*) malloc((size_t) P * sizeof(float));
+    float* gu = gu_out ? gu_out : (float*) malloc((size_t) NP * 2 * ff * sizeof(float));
+    float* part = part_out ? part_out : (float*) malloc((size_t) NP * H * sizeof(float));
+    uint8_t* hq = (uint8_t*) malloc((size_t) NP * (ff / 32) * ORC_Q81_BYTES);
+    int* pe = (int*) malloc((size_t) NP * sizeof(int));
+#ifdef _OPENMP
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+#endif
+    orc_quantize_q8_1(x, xq, H, T);
+#pragma omp parallel for schedule(static) if (nthreads > 1)
+    for (int r = 0; r < E + 1; ++r)
+        for (int t = 0; t < T; ++t) logits[(size_t) t * (E + 1) + r] = router_dot(L->W + (size_t) r * H, x + (size_t) t * H, H);
+    orc_topk(logits, T, E, E + 1, K, topi, topw);
+    for (int p = 0; p < NP; ++p) pe[p] = p < P ? topi[p] : E;
+    const int64_t ngu = (int64_t) NP * 2 * ff;
+#pragma omp parallel for schedule(static) if (nthreads > 1)
+    for (int64_t q = 0; q < ngu; ++q) {
+        const int p = (int) (q / (2 * ff)), r = (int) (q % (2 * ff)), t = p < P ? p / K : p - P;
+        if (pe[p] < 0) continue;
+        const uint8_t* w = L->gu_w + (size_t) pe[p] * L->gu_stride + (size_t) r * gurb;
+        gu[q] = orc_dot(L->type, w, xq + (size_t) t * (H / 32) * ORC_Q81_BYTES, H);
+    }
+    for (int p = 0; p < NP; ++p)
+        if (pe[p] >= 0) orc_swiglu_q8_1(gu + (size_t) p * 2 * ff, ff, hq + (size_t) p * (ff / 32) * ORC_Q81_BYTES);
+    const int64_t ndn = (int64_t) NP * H;
+#pragma omp parallel for schedule(static) if (nthreads > 1)
+    for (int64_t q = 0; q < ndn; ++q) {
+        const int p = (int) (q / H), r = (int) (q % H);
+        if (pe[p] < 0) continue;
+        const uint8_t* w = L->dn_w + (size_t) pe[p] * L->dn_stride + (size_t) r * dnrb;
+        part[q] = orc_dot(L->type, w, hq + (size_t) p * (ff / 32) * ORC_Q81_BYTES, ff);
+    }
+    for (int t = 0; t < T; ++t) {
+        const float g = L->shared ? sigm_(logits[(size_t) t * (E + 1) + E]) : 0.f;
+        for (int i = 0; i < H; ++i) {
+            float s = 0.f;
+            for (int k = 0; k < K; ++k)
+                if (topi[t * K + k] >= 0) s = fmaf(topw[t * K + k], part[(size_t) (t * K + k) * H + i], s);
+            y[(size_t) t * H + i] = L->shared ? fmaf(g, part[(size_t) (P + t) * H + i], s) : s;
+        }
+    }
+    free(xq);
+    free(hq);
+    free(pe);
+    if (!logits_out) free(logits);
+    if (!topi_out) free(topi);
+    if (!topw_out) free(topw);
+    if (!gu_out) free(gu);
+    if (!part_out) free(part);
+}
+
+/* ------------------------------------------------------------------------------------------------ f16 path */
+void orc_mma_matvec(const uint8_t* w, int type, int n_in, int n_out, const uint16_t* x16, double* out) {
+    uint16_t* row = (uint16_t*) malloc((size_t) n_in * 2);
+    const size_t rb = row_bytes(type, n_in);
+    for (int r = 0; r < n_out; ++r) {
+        if (type == ORC_Q4_K) orc_dequant_q4_k_f16(w + (size_t) r * rb, row, 1, n_in);
+        else orc_dequant_q8_0_f16(w + (size_t) r * rb, row, 1, n_in);
+        double s = 0.0;
+        for (int k = 0; k < n_in; ++k) s += (double) orc_f16_to_f32(row[k]) * (double) orc_f16_to_f32(x16[k]);
+        out[r] = s;
+    }
+    free(row);
+}
+
+void orc_swiglu_h16(const float* gu, int ff, uint16_t* h16) {
+    for (int i = 0; i < ff; ++i) h16[i] = orc_f32_to_f16(silu_(gu[i]) * gu[ff + i]);
+}
+
+/* ------------------------------------------------------------------------------------------------ CPU baseline */
+static double now_us(void) {
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (double) ts.tv_sec * 1e6 + (double) ts.tv_nsec * 1e-3;
+}
+static int cmp_d(const void* a, const void* b) {
+    const double x = *(const double*) a, y = *(const double*) b;
+    return x < y ? -1 : x > y;
+}
+double orc_time_layer_decode(const orc_layer* L, const float* x, int nthreads, int reps, size_t sweep_bytes, float* y) {
+    double* t = (double*) malloc((size_t) reps * sizeof(double));
+    uint64_t* sweep = sweep_bytes ? (uint64_t*) malloc(sweep_bytes) : NULL;
+    if (sweep) memset(sweep, 1, sweep_bytes);
+    volatile uint64_t sink = 0;
+    for (int r = 0; r < reps; ++r) {
+        if (sweep) {
+            uint64_t s = 0;
+#pragma omp parallel for reduction(+ : s) schedule(static)
+            for (int64_t i = 0; i < (int64_t) (sweep_bytes / 8); i += 8) s += sweep[i];
+            sink += s;
+        }
+        const double t0 = now_us();
+        orc_layer_decode(L, x, 1, y, NULL, NULL, NULL, NULL, NULL, nthreads);
+        t[r] = now_us() - t0;
+    }
+    (void) sink;
+    qsort(t, (size_t) reps, sizeof(double), cmp_d);
+    const double med = t[reps / 2];
+    free(t);
+    free(sweep);
+    return med;
+}

@@ -1,0 +1,69 @@
+"""ctypes bindings of the C ABI in include/sfnx_moe.h (libsfnx_moe.so, built in-tree by sfnx_amd/build.py).
+
+Loading fails loudly when the library is missing: there is no fallback path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import re
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+LIB_PATH = PKG / "libsfnx_moe.so"
+HEADER = PKG.parent / "include" / "sfnx_moe.h"
+
+Q8_0, Q4_K = 8, 12
+MAXT, PF_JOB = 16, 64
+JOB_INTS = 2 + 2 * MAXT        # sfnx_job: w, n, y[16], out[16]
+BIGJOB_INTS = 2 + 2 * PF_JOB   # sfnx_bigjob
+
+vp, i32, i64, sz, f32, u32, u64 = C.c_void_p, C.c_int, C.c_int64, C.c_size_t, C.c_float, C.c_uint32, C.c_uint64
+
+SIGNATURES = {
+    "sfnx_last_error": (C.c_char_p, []),
+    "sfnx_abi_version": (i32, []),
+    "sfnx_row_bytes": (sz, [u32, i32]),
+    "sfnx_synth_normal": (i32, [vp, sz, u64, u64, f32, vp]),
+    "sfnx_quantize_weights": (i32, [u32, vp, vp, i64, i32, vp]),
+    "sfnx_store_pack": (i32, [u32, vp, vp, i64, i32, i32, vp]),
+    "sfnx_store_unpack": (i32, [u32, vp, vp, i64, i32, i32, vp]),
+    "sfnx_dequantize": (i32, [u32, vp, vp, i64, i32, i32, vp]),
+    "sfnx_dequantize_f16": (i32, [u32, vp, vp, i64, i32, i32, vp]),
+    "sfnx_quantize_q8_1": (i32, [vp, vp, i32, i32, vp]),
+    "sfnx_router_route": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, vp, vp, i32, vp]),
+    "sfnx_router_logits": (i32, [vp, vp, vp, i32, i32, i32, vp]),
+    "sfnx_pf_route": (i32, [vp, i32, i32, i32, vp, vp, vp, vp, vp, vp, vp, i32, vp]),
+    "sfnx_moe_gate_up": (i32, [vp, sz, u32, i32, i32, vp, vp, i32, i32, vp, vp, vp]),
+    "sfnx_moe_down": (i32, [vp, sz, u32, i32, i32, vp, vp, i32, i32, vp, vp, vp]),
+    "sfnx_moe_gate_up_big": (i32, [vp, sz, u32, i32, i32, vp, vp, i32, vp, vp, vp]),
+    "sfnx_moe_down_big": (i32, [vp, sz, u32, i32, i32, vp, vp, i32, vp, vp, vp]),
+    "sfnx_moe_combine": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp]),
+}
+
+
+def declared_symbols() -> list[str]:
+    """Every function the C header declares."""
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"\b(sfnx_[a-z0-9_]+)\s*\(", text)))
+
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is not built: run __graft_entry__.build() (or python sfnx_amd/build.py)")
+        L = C.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(status: int) -> None:
+    if status != 0:
+        raise RuntimeError(lib().sfnx_last_error().decode())

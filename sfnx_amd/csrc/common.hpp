@@ -1,0 +1,109 @@
+// Shared device helpers and the C-ABI error plumbing of the sfnx_amd library (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+#include "../../include/sfnx_moe.h"
+
+namespace sfnx {
+
+constexpr int WAVE = 64;
+constexpr int Q4K_BYTES = 144, Q80_BYTES = 34, Q81_BYTES = 36;
+
+// ------------------------------------------------------------------------------------------------ errors
+void set_error(const std::string& msg);
+// runs f, mapping a thrown error (or a failed launch) to a negative status and the thread's message
+template <typename F> int guarded(const char* what, F&& f) {
+    try {
+        f();
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) throw std::runtime_error(std::string("launch failed: ") + hipGetErrorString(e));
+        return 0;
+    } catch (const std::exception& ex) {
+        set_error(std::string(what) + ": " + ex.what());
+        return -1;
+    }
+}
+inline void require(bool ok, const char* msg) {
+    if (!ok) throw std::runtime_error(msg);
+}
+inline hipStream_t stream_of(void* st) { return reinterpret_cast<hipStream_t>(st); }
+
+// ------------------------------------------------------------------------------------------------ device helpers
+__device__ __forceinline__ float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
+__device__ __forceinline__ uint16_t f2h(float f) { return __half_as_ushort(__float2half_rn(f)); }
+
+// lanes xor-reduced within groups of G (G a power of two <= 64): the tree every lane of a group ends with
+template <int G> __device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int o = G / 2; o; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+template <int G> __device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+    for (int o = G / 2; o; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+template <int G> __device__ __forceinline__ int group_isum(int v) {
+#pragma unroll
+    for (int o = G / 2; o; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+__device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+// silu and sigmoid as the reference writes them (src/kernels.cu:46-47), exp by the device library
+__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+__device__ __forceinline__ float sigm_f(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// get_scale_min_k4 on the 16-byte header held in h (bytes 4..15 are the scales; src/moe_q4k.cuh:15-23)
+__device__ __forceinline__ unsigned hdr_byte(const uint4& h, int k) {
+    const unsigned w = k < 4 ? h.y : k < 8 ? h.z : h.w;
+    return (w >> (8 * (k & 3))) & 0xFFu;
+}
+__device__ __forceinline__ void q4k_scale_min(const uint4& h, int j, float& sc, float& m) {
+    if (j < 4) {
+        sc = (float) (hdr_byte(h, j) & 63);
+        m = (float) (hdr_byte(h, j + 4) & 63);
+    } else {
+        sc = (float) ((hdr_byte(h, j + 4) & 0xF) | ((hdr_byte(h, j - 4) >> 6) << 4));
+        m = (float) ((hdr_byte(h, j + 4) >> 4) | ((hdr_byte(h, j) >> 6) << 4));
+    }
+}
+
+// agent-scope loads for data another workgroup wrote earlier in the same launch
+__device__ __forceinline__ float load_agent(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ------------------------------------------------------------------------------------------------ planar store
+// byte offsets of row r's pieces inside one planar matrix of R rows x C columns
+struct Q4kPlanes {
+    const uint8_t* nib;   // R x C/2
+    const uint8_t* hdr;   // R x C/256 x 16
+    __device__ __forceinline__ const uint8_t* nib_row(int r, int C) const { return nib + (size_t) r * (C / 2); }
+    __device__ __forceinline__ const uint8_t* hdr_row(int r, int C) const { return hdr + (size_t) r * (C / 256) * 16; }
+};
+__host__ __device__ __forceinline__ Q4kPlanes q4k_planes(const void* mat, int R, int C) {
+    const uint8_t* p = (const uint8_t*) mat;
+    return Q4kPlanes{p, p + (size_t) R * (C / 2)};
+}
+struct Q80Planes {
+    const uint8_t* q;     // R x C
+    const uint16_t* d;    // R x C/32
+};
+__host__ __device__ __forceinline__ Q80Planes q80_planes(const void* mat, int R, int C) {
+    const uint8_t* p = (const uint8_t*) mat;
+    return Q80Planes{p, (const uint16_t*) (p + (size_t) R * C)};
+}
+
+inline size_t row_bytes(uint32_t type, int cols) {
+    return type == SFNX_Q4_K ? (size_t) cols / 256 * Q4K_BYTES : (size_t) cols / 32 * Q80_BYTES;
+}
+
+}  // namespace sfnx

@@ -1,0 +1,84 @@
+// C++ face of libsfnx_moe.so under the reference engine's names (src/kernels.hpp:18-36, 269-313): the calls an engine
+// makes for its MoE half, each a thin inline wrapper over the C ABI (include/sfnx_moe.h) that throws
+// std::runtime_error with the library's message on failure, as the reference's wrappers do (src/kernels.cu:31-34).
+//
+// The reference fixes the hidden size, expert count and top-k at compile time (src/model.hpp:40-45: N, NEXP, TOPK);
+// here they are a runtime MoeShape.  The weights are the planar store (sfnx_store_pack) rather than raw GGUF rows.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <stdexcept>
+
+#include "sfnx_moe.h"
+
+namespace sfnx {
+
+using Job = sfnx_job;         // src/kernels.hpp:18-23
+using BigJob = sfnx_bigjob;   // src/kernels.hpp:25-32
+constexpr int MAXT = SFNX_MAXT, PF_JOB = SFNX_PF_JOB;
+enum GgmlType : uint32_t { T_Q8_0 = SFNX_Q8_0, T_Q4_K = SFNX_Q4_K };   // src/gguf.hpp:22-25
+
+// src/model.hpp:78-87 DW: one matrix (or expert 0's of a stack), n_out rows of n_in
+struct DW {
+    const void* p = nullptr;
+    uint32_t type = 0;
+    int n_in = 0, n_out = 0;
+};
+
+// the sizes the reference compiles in
+struct MoeShape {
+    int H = 2048;    // N
+    int E = 512;     // NEXP
+    int K = 10;      // TOPK
+};
+
+inline void ck(int status) {
+    if (status != 0) throw std::runtime_error(sfnx_last_error());
+}
+
+constexpr size_t q8_1_bytes(int n) { return (size_t) (n / 32) * 36; }   // src/kernels.hpp:34
+
+inline void quantize_q8_1(const float* x, void* q, int n, int rows, void* st) { ck(sfnx_quantize_q8_1(x, q, n, rows, st)); }
+
+// src/kernels.hpp:276-278; shared: the shared expert (expert E of the stacks) rides as the last job
+inline void router_route(const MoeShape& s, const float* W, const float* x, float* logits, int T, int* topi, float* topw,
+                         Job* jobs_gu, Job* jobs_dn, int* njobs, void* st, bool shared = true) {
+    ck(sfnx_router_route(W, x, logits, T, s.H, s.E, s.K, topi, topw, jobs_gu, jobs_dn, njobs, shared ? 1 : 0, st));
+}
+// src/kernels.hpp:281-282; T: the window's rows (the reference derives it as njobs_max / TOPK)
+inline void moe_gate_up(const DW& A, size_t sa, const Job* jobs, const int* njobs, int njobs_max, const void* xq, float* gu,
+                        void* st, int T) {
+    ck(sfnx_moe_gate_up(A.p, sa, A.type, A.n_in, A.n_out, jobs, njobs, njobs_max, T, xq, gu, st));
+}
+// src/kernels.hpp:305
+inline void moe_down(const DW& A, size_t sa, const Job* jobs, const int* njobs, int njobs_max, const float* gu, float* part,
+                     void* st, int T) {
+    ck(sfnx_moe_down(A.p, sa, A.type, A.n_in, A.n_out, jobs, njobs, njobs_max, T, gu, part, st));
+}
+// src/kernels.hpp:286-287
+inline void moe_gate_up_big(const DW& A, size_t sa, const BigJob* jobs, const int* njobs, int njobs_cap, const void* xq,
+                            float* gu, void* st) {
+    ck(sfnx_moe_gate_up_big(A.p, sa, A.type, A.n_in, A.n_out, jobs, njobs, njobs_cap, xq, gu, st));
+}
+inline void moe_down_big(const DW& A, size_t sa, const BigJob* jobs, const int* njobs, int njobs_cap, const float* gu,
+                         float* part, void* st) {
+    ck(sfnx_moe_down_big(A.p, sa, A.type, A.n_in, A.n_out, jobs, njobs, njobs_cap, gu, part, st));
+}
+// the prompt path's routing (src/prefill.cu:1163-1167: router sgemm, k_pf_top10, k_pf_count, k_pf_jobbase, k_pf_fill)
+inline void router_logits(const float* W, const float* x, float* logits, int T, int H, int L, void* st) {
+    ck(sfnx_router_logits(W, x, logits, T, H, L, st));
+}
+inline void pf_route(const MoeShape& s, const float* logits, int C, int* topi, float* topw, int* cnt, int* jbase,
+                     BigJob* jobs_gu, BigJob* jobs_dn, int* njobs, void* st, bool shared = true) {
+    ck(sfnx_pf_route(logits, C, s.E, s.K, topi, topw, cnt, jbase, jobs_gu, jobs_dn, njobs, shared ? 1 : 0, st));
+}
+// the weighted combine the reference folds into its ring sum (src/kernels.cu:797-803, RingMoe src/kernels.hpp:309-313)
+inline void moe_combine(const MoeShape& s, const float* part, const float* topw, const int* topi, const float* logits,
+                        float* y, int T, void* st, bool shared = true) {
+    ck(sfnx_moe_combine(part, topw, topi, logits, y, T, s.H, s.E, s.K, shared ? 1 : 0, st));
+}
+
+static_assert(sizeof(Job) == 136 && sizeof(BigJob) == 520, "job layouts match the reference's");
+
+}  // namespace sfnx

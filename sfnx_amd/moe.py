@@ -1,0 +1,226 @@
+"""Python host mirror of the reference engine's MoE entry points (src/kernels.hpp:269-313) over the C ABI.
+
+torch supplies device memory and the current stream; every computation is a call into libsfnx_moe.so.  Functions keep
+the reference's names and argument meaning; shapes that the reference fixes at compile time (N, NEXP, TOPK) are
+arguments here.  Errors from the library raise RuntimeError, as the reference's wrappers throw (src/kernels.cu:31-34).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _abi
+from ._abi import BIGJOB_INTS, JOB_INTS, Q4_K, Q8_0, check, lib
+
+
+def _p(t):
+    return None if t is None else t.data_ptr()
+
+
+def _st():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def row_bytes(wtype: int, cols: int) -> int:
+    return lib().sfnx_row_bytes(wtype, cols)
+
+
+# ---------------------------------------------------------------------------------------------------- store
+def synth_normal(out: torch.Tensor, seed: int, std: float, offset: int = 0) -> None:
+    check(lib().sfnx_synth_normal(_p(out), out.numel(), seed, offset, std, _st()))
+
+
+def quantize_weights(wtype: int, x: torch.Tensor, gguf: torch.Tensor) -> None:
+    rows, cols = x.shape
+    check(lib().sfnx_quantize_weights(wtype, _p(x), _p(gguf), rows, cols, _st()))
+
+
+def store_pack(wtype: int, gguf: torch.Tensor, planar: torch.Tensor, n_mat: int, rows: int, cols: int) -> None:
+    check(lib().sfnx_store_pack(wtype, _p(gguf), _p(planar), n_mat, rows, cols, _st()))
+
+
+def store_unpack(wtype: int, planar: torch.Tensor, gguf: torch.Tensor, n_mat: int, rows: int, cols: int) -> None:
+    check(lib().sfnx_store_unpack(wtype, _p(planar), _p(gguf), n_mat, rows, cols, _st()))
+
+
+def dequantize(wtype: int, planar: torch.Tensor, y: torch.Tensor, n_mat: int, rows: int, cols: int) -> None:
+    check(lib().sfnx_dequantize(wtype, _p(planar), _p(y), n_mat, rows, cols, _st()))
+
+
+def dequantize_f16(wtype: int, planar: torch.Tensor, y: torch.Tensor, n_mat: int, rows: int, cols: int) -> None:
+    check(lib().sfnx_dequantize_f16(wtype, _p(planar), _p(y), n_mat, rows, cols, _st()))
+
+
+# ---------------------------------------------------------------------------------------------------- routing
+def quantize_q8_1(x: torch.Tensor, q: torch.Tensor) -> None:
+    rows, n = x.shape
+    check(lib().sfnx_quantize_q8_1(_p(x), _p(q), n, rows, _st()))
+
+
+def router_route(W, x, logits, topi, topw, jobs_gu, jobs_dn, njobs, E: int, K: int, shared: bool = True) -> None:
+    T, H = x.shape
+    check(lib().sfnx_router_route(_p(W), _p(x), _p(logits), T, H, E, K, _p(topi), _p(topw), _p(jobs_gu), _p(jobs_dn),
+                                  _p(njobs), int(shared), _st()))
+
+
+def router_logits(W, x, logits) -> None:
+    T, H = x.shape
+    check(lib().sfnx_router_logits(_p(W), _p(x), _p(logits), T, H, W.shape[0], _st()))
+
+
+def pf_route(logits, topi, topw, cnt, jbase, jobs_gu, jobs_dn, njobs, E: int, K: int, shared: bool = True) -> None:
+    C = logits.shape[0]
+    check(lib().sfnx_pf_route(_p(logits), C, E, K, _p(topi), _p(topw), _p(cnt), _p(jbase), _p(jobs_gu), _p(jobs_dn),
+                              _p(njobs), int(shared), _st()))
+
+
+# ---------------------------------------------------------------------------------------------------- experts
+def moe_gate_up(A, sa, wtype, n_in, n_out, jobs, njobs, njobs_max, T, xq, gu) -> None:
+    check(lib().sfnx_moe_gate_up(_p(A), sa, wtype, n_in, n_out, _p(jobs), _p(njobs), njobs_max, T, _p(xq), _p(gu), _st()))
+
+
+def moe_down(A, sa, wtype, n_in, n_out, jobs, njobs, njobs_max, T, gu, part) -> None:
+    check(lib().sfnx_moe_down(_p(A), sa, wtype, n_in, n_out, _p(jobs), _p(njobs), njobs_max, T, _p(gu), _p(part), _st()))
+
+
+def moe_gate_up_big(A, sa, wtype, n_in, n_out, jobs, njobs, njobs_cap, xq, gu) -> None:
+    check(lib().sfnx_moe_gate_up_big(_p(A), sa, wtype, n_in, n_out, _p(jobs), _p(njobs), njobs_cap, _p(xq), _p(gu), _st()))
+
+
+def moe_down_big(A, sa, wtype, n_in, n_out, jobs, njobs, njobs_cap, gu, part) -> None:
+    check(lib().sfnx_moe_down_big(_p(A), sa, wtype, n_in, n_out, _p(jobs), _p(njobs), njobs_cap, _p(gu), _p(part), _st()))
+
+
+def moe_combine(part, topw, topi, logits, y, E: int, K: int, shared: bool = True) -> None:
+    T, H = y.shape
+    check(lib().sfnx_moe_combine(_p(part), _p(topw), _p(topi), _p(logits), _p(y), T, H, E, K, int(shared), _st()))
+
+
+# ---------------------------------------------------------------------------------------------------- a layer
+@dataclass
+class LayerShape:
+    H: int = 2048
+    E: int = 512
+    K: int = 10
+    ff: int = 512
+    wtype: int = Q4_K
+    shared: bool = True
+
+
+class MoeLayer:
+    """One MoE layer's weights resident in HBM (planar store) plus the buffers its entry points write.
+
+    gu_w: experts' gate|up [E+1][2 ff][H] (expert E is the shared one), dn_w: down [E+1][H][ff], W: router [E+1][H].
+    """
+
+    def __init__(self, shape: LayerShape, W: torch.Tensor, gu_w: torch.Tensor, dn_w: torch.Tensor):
+        self.s = shape
+        self.W, self.gu_w, self.dn_w = W, gu_w, dn_w
+        self.gu_stride = 2 * shape.ff * row_bytes(shape.wtype, shape.H)
+        self.dn_stride = shape.H * row_bytes(shape.wtype, shape.ff)
+
+    @staticmethod
+    def planar_from_gguf(shape: LayerShape, W: torch.Tensor, gu_gguf: torch.Tensor, dn_gguf: torch.Tensor) -> "MoeLayer":
+        s = shape
+        gu = torch.empty_like(gu_gguf)
+        dn = torch.empty_like(dn_gguf)
+        store_pack(s.wtype, gu_gguf, gu, s.E + 1, 2 * s.ff, s.H)
+        store_pack(s.wtype, dn_gguf, dn, s.E + 1, s.H, s.ff)
+        return MoeLayer(s, W, gu, dn)
+
+    @staticmethod
+    def synthetic(shape: LayerShape, seed: int, device="cuda", chunk_experts: int = 64) -> "MoeLayer":
+        """Seeded layer: router N(0, 0.02) fp32; experts N(0, 0.02) quantized by the library's quantizer and packed."""
+        s = shape
+        E1 = s.E + 1
+        W = torch.empty((E1, s.H), dtype=torch.float32, device=device)
+        synth_normal(W, seed * 1000 + 1, 0.02)
+        gu_stride = 2 * s.ff * row_bytes(s.wtype, s.H)
+        dn_stride = s.H * row_bytes(s.wtype, s.ff)
+        gu = torch.empty(E1 * gu_stride, dtype=torch.uint8, device=device)
+        dn = torch.empty(E1 * dn_stride, dtype=torch.uint8, device=device)
+        vals = 2 * s.ff * s.H   # values per expert matrix (gate|up and down hold the same count)
+        tmp = torch.empty(chunk_experts * vals, dtype=torch.float32, device=device)
+        blk = torch.empty(chunk_experts * gu_stride, dtype=torch.uint8, device=device)
+        for mat, (rows, cols, stride, dst, sd) in enumerate(
+                [(2 * s.ff, s.H, gu_stride, gu, seed * 1000 + 2), (s.H, s.ff, dn_stride, dn, seed * 1000 + 3)]):
+            for e0 in range(0, E1, chunk_experts):
+                ne = min(chunk_experts, E1 - e0)
+                t = tmp[: ne * rows * cols]
+                synth_normal(t, sd, 0.02, offset=e0 * rows * cols)
+                b = blk[: ne * stride]
+                quantize_weights(s.wtype, t.view(ne * rows, cols), b)
+                store_pack(s.wtype, b, dst[e0 * stride:(e0 + ne) * stride], ne, rows, cols)
+        del tmp, blk
+        return MoeLayer(s, W, gu, dn)
+
+
+class DecodeBuffers:
+    """The decode window's buffers (src/engine.cu:174-206), T rows at most."""
+
+    def __init__(self, shape: LayerShape, T: int, device="cuda"):
+        s = shape
+        P = T * s.K
+        NP = P + (T if s.shared else 0)
+        nj = P + 1
+        i32 = dict(dtype=torch.int32, device=device)
+        self.T = T
+        self.xq = torch.empty(T * (s.H // 32) * 36, dtype=torch.uint8, device=device)
+        self.logits = torch.empty((T, s.E + 1), dtype=torch.float32, device=device)
+        self.topi = torch.empty((T, s.K), **i32)
+        self.topw = torch.empty((T, s.K), dtype=torch.float32, device=device)
+        self.jobs_gu = torch.zeros(nj * JOB_INTS, **i32)
+        self.jobs_dn = torch.zeros(nj * JOB_INTS, **i32)
+        self.njobs = torch.zeros(2, **i32)
+        self.njobs_max = nj
+        self.gu = torch.zeros((NP, 2 * s.ff), dtype=torch.float32, device=device)
+        self.part = torch.zeros((NP, s.H), dtype=torch.float32, device=device)
+
+
+def decode_layer(L: MoeLayer, x: torch.Tensor, y: torch.Tensor, b: DecodeBuffers) -> None:
+    """One decode window (T <= 16 rows) through the layer: the engine's ffn_half (src/engine.cu:933-978) on one GPU."""
+    s = L.s
+    T = x.shape[0]
+    quantize_q8_1(x, b.xq)
+    router_route(L.W, x, b.logits, b.topi, b.topw, b.jobs_gu, b.jobs_dn, b.njobs, s.E, s.K, s.shared)
+    moe_gate_up(L.gu_w, L.gu_stride, s.wtype, s.H, 2 * s.ff, b.jobs_gu, b.njobs, b.njobs_max, T, b.xq, b.gu)
+    moe_down(L.dn_w, L.dn_stride, s.wtype, s.ff, s.H, b.jobs_dn, b.njobs, b.njobs_max, T, b.gu, b.part)
+    moe_combine(b.part, b.topw, b.topi, b.logits, y, s.E, s.K, s.shared)
+
+
+class PrefillBuffers:
+    """The prompt path's buffers for C tokens (src/prefill.cu:1145-1180)."""
+
+    def __init__(self, shape: LayerShape, C: int, device="cuda"):
+        s = shape
+        P = C * s.K
+        NP = P + (C if s.shared else 0)
+        self.C = C
+        self.cap = P // 64 + s.E + (C + 63) // 64 + 1
+        i32 = dict(dtype=torch.int32, device=device)
+        self.xq = torch.empty(C * (s.H // 32) * 36, dtype=torch.uint8, device=device)
+        self.logits = torch.empty((C, s.E + 1), dtype=torch.float32, device=device)
+        self.topi = torch.empty((C, s.K), **i32)
+        self.topw = torch.empty((C, s.K), dtype=torch.float32, device=device)
+        self.cnt = torch.zeros(s.E, **i32)
+        self.jbase = torch.zeros(s.E, **i32)
+        self.jobs_gu = torch.zeros(self.cap * BIGJOB_INTS, **i32)
+        self.jobs_dn = torch.zeros(self.cap * BIGJOB_INTS, **i32)
+        self.njobs = torch.zeros(2, **i32)
+        self.gu = torch.zeros((NP, 2 * s.ff), dtype=torch.float32, device=device)
+        self.part = torch.zeros((NP, s.H), dtype=torch.float32, device=device)
+
+
+def prefill_layer_q8(L: MoeLayer, x: torch.Tensor, y: torch.Tensor, b: PrefillBuffers) -> None:
+    """A prompt chunk through the layer on the int8 (q8_1) arithmetic, FNX_PF_MOE_Q8 (src/prefill.cu:1156-1166)."""
+    s = L.s
+    quantize_q8_1(x, b.xq)
+    router_logits(L.W, x, b.logits)
+    pf_route(b.logits, b.topi, b.topw, b.cnt, b.jbase, b.jobs_gu, b.jobs_dn, b.njobs, s.E, s.K, s.shared)
+    moe_gate_up_big(L.gu_w, L.gu_stride, s.wtype, s.H, 2 * s.ff, b.jobs_gu, b.njobs, b.cap, b.xq, b.gu)
+    moe_down_big(L.dn_w, L.dn_stride, s.wtype, s.ff, s.H, b.jobs_dn, b.njobs, b.cap, b.gu, b.part)
+    moe_combine(b.part, b.topw, b.topi, b.logits, y, s.E, s.K, s.shared)
+
+
+__all__ = [n for n in dir() if not n.startswith("_")] + ["_abi"]

@@ -1,0 +1,47 @@
+"""Helpers for the GPU parity tests: seeded layers built on the device (synthetic values, the library's quantizer,
+the planar store) with the same GGUF bytes copied to the host for the oracle."""
+import numpy as np
+import torch
+
+from oracle import oracle as orc
+from sfnx_amd import moe
+
+
+def job_array(t: torch.Tensor, big: bool = False) -> np.ndarray:
+    dt = orc.BIGJOB_DTYPE if big else orc.JOB_DTYPE
+    return t.cpu().numpy().view(dt)
+
+
+def make_layer(shape: moe.LayerShape, seed: int, device="cuda"):
+    """(device MoeLayer, oracle LayerWeights) holding the same weights"""
+    s = shape
+    E1 = s.E + 1
+    gu_stride = 2 * s.ff * moe.row_bytes(s.wtype, s.H)
+    dn_stride = s.H * moe.row_bytes(s.wtype, s.ff)
+    W = torch.empty((E1, s.H), dtype=torch.float32, device=device)
+    moe.synth_normal(W, seed * 1000 + 1, 0.02)
+    gu_g = torch.empty(E1 * gu_stride, dtype=torch.uint8, device=device)
+    dn_g = torch.empty(E1 * dn_stride, dtype=torch.uint8, device=device)
+    for rows, cols, dst, sd in ((E1 * 2 * s.ff, s.H, gu_g, seed * 1000 + 2), (E1 * s.H, s.ff, dn_g, seed * 1000 + 3)):
+        chunk = 1 << 24
+        total = rows * cols
+        per = max(cols, chunk // cols * cols)
+        tmp = torch.empty(per, dtype=torch.float32, device=device)
+        rb = moe.row_bytes(s.wtype, cols)
+        for off in range(0, total, per):
+            n = min(per, total - off)
+            moe.synth_normal(tmp[:n], sd, 0.02, offset=off)
+            r0 = off // cols
+            moe.quantize_weights(s.wtype, tmp[:n].view(n // cols, cols), dst[r0 * rb:(r0 + n // cols) * rb])
+    L = moe.MoeLayer.planar_from_gguf(s, W, gu_g, dn_g)
+    torch.cuda.synchronize()
+    host = orc.LayerWeights(W.cpu().numpy(), gu_g.cpu().numpy(), dn_g.cpu().numpy(), s.wtype, s.H, s.E, s.K, s.ff,
+                            s.shared)
+    return L, host
+
+
+def max_rel(got, want) -> float:
+    """max |got - want| over max |want| (the tolerance measure of tools/moe_mma_bench.cu:197-220)"""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    return float(np.max(np.abs(got - want)) / max(np.max(np.abs(want)), 1e-30))

@@ -1,0 +1,59 @@
+"""The C-ABI library: it loads, exports every symbol include/sfnx_moe.h declares, and rejects bad arguments with a
+status and a message before touching the GPU (src/kernels.cu:31-34 and src/moe.cuh:473-494 throw on the same)."""
+import ctypes as C
+
+import pytest
+
+from sfnx_amd import _abi
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _abi.lib()
+    declared = _abi.declared_symbols()
+    assert len(declared) >= 18
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert set(declared) == set(_abi.SIGNATURES), "bindings and header disagree"
+    assert lib.sfnx_abi_version() == 1
+
+
+def test_row_bytes():
+    lib = _abi.lib()
+    assert lib.sfnx_row_bytes(_abi.Q4_K, 2048) == 1152
+    assert lib.sfnx_row_bytes(_abi.Q4_K, 512) == 288
+    assert lib.sfnx_row_bytes(_abi.Q8_0, 2048) == 2176
+
+
+@pytest.mark.parametrize("call, msg", [
+    (lambda L: L.sfnx_router_route(None, None, None, 0, 2048, 512, 10, None, None, None, None, None, 1, None), "T out of range"),
+    (lambda L: L.sfnx_router_route(None, None, None, 17, 2048, 512, 10, None, None, None, None, None, 1, None), "T out of range"),
+    (lambda L: L.sfnx_router_route(None, None, None, 1, 2048, 500, 10, None, None, None, None, None, 1, None), "E must be"),
+    (lambda L: L.sfnx_router_route(None, None, None, 1, 2048, 512, 17, None, None, None, None, None, 1, None), "K out of range"),
+    (lambda L: L.sfnx_moe_gate_up(None, 1 << 30, 5, 2048, 1024, None, None, 11, 1, None, None, None), "Q4_K (12) or Q8_0 (8)"),
+    (lambda L: L.sfnx_moe_gate_up(None, 1 << 30, 12, 2000, 1024, None, None, 11, 1, None, None, None), "multiple of 512"),
+    (lambda L: L.sfnx_moe_gate_up(None, 1000, 12, 2048, 1024, None, None, 11, 1, None, None, None), "stride smaller"),
+    (lambda L: L.sfnx_moe_down(None, 1 << 30, 12, 512, 2048, None, None, 11, 0, None, None, None), "T out of range"),
+    (lambda L: L.sfnx_store_pack(12, None, None, 1, 4, 256, None), "multiple of 512"),
+    (lambda L: L.sfnx_quantize_q8_1(None, None, 30, 1, None), "multiple of 32"),
+    (lambda L: L.sfnx_pf_route(None, 0, 512, 10, None, None, None, None, None, None, None, 1, None), "C must be positive"),
+])
+def test_bad_arguments_are_refused(call, msg):
+    lib = _abi.lib()
+    assert call(lib) == -1
+    assert msg in lib.sfnx_last_error().decode()
+
+
+def test_cpp_header_compiles():
+    """the C++ mirror of the reference's entry points compiles against the C header (host only)"""
+    import subprocess
+    import tempfile
+    from pathlib import Path
+    root = Path(__file__).resolve().parent.parent
+    src = '#include "sfnx/kernels.hpp"\nint main() { return sizeof(sfnx::Job) == 136 && sizeof(sfnx::BigJob) == 520 ? 0 : 1; }\n'
+    with tempfile.TemporaryDirectory() as d:
+        f = Path(d) / "t.cpp"
+        f.write_text(src)
+        r = subprocess.run(["g++", "-std=c++17", "-fsyntax-only", f"-I{root / 'sfnx_amd' / 'include'}",
+                            f"-I{root / 'include'}", "-I/opt/rocm/include", "-D__HIP_PLATFORM_AMD__", str(f)],
+                           capture_output=True, text=True)
+        assert r.returncode == 0, r.stderr
