@@ -1,0 +1,256 @@
+"""Benchmark of the quantized MoE hot path on one MI355X (BASELINE.json metric and configs).
+
+Headline (value): config 1, Q4_K decode at batch 1 through 48 stacked MoE layers (hidden 2048, 512 experts x FF 512,
+top-10 + shared; each layer's weights seeded independently, 0.908 GB a layer resident in HBM), one token per step.
+The layers are chained as an engine chains them: x_{l+1} = x_l + MoE_l(rmsnorm(x_l)).  A step is one HIP-graph replay
+of sfnx_moe_decode over the 48 layers (three launches a layer).  value = achieved algorithmic HBM GB/s: per
+token-layer the router's fp32 rows plus the 11 experts' Q4_K bytes (23,666,688 B), over the measured step time.
+
+Also in the JSON line: us/token-layer; each decode kernel's time from HIP events on the launch stream (eager, one
+layer at a time) and the dominant one's roofline; the prompt path (config 3: 2048 tokens, Zipf-skewed routing); the
+CPU baseline (the oracle on config 0, on the host's cores) with the GPU's parity against it for that token.
+
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers 48] [--no-prefill] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+F16_MFMA_PEAK_TFLOPS = 2500.0
+INT8_MFMA_PEAK_TOPS = 5000.0
+ZIPF_S, ZIPF_ALPHA, ZIPF_SEED = 1.1, 0.125, 7   # config 3: logits[:, e] += ALPHA * -S ln(rank_e), max rows/expert ~200
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--layers", type=int, default=48)
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    return ap.parse_args()
+
+
+def expert_bytes(s, moe):
+    return 2 * s.ff * moe.row_bytes(s.wtype, s.H) + s.H * moe.row_bytes(s.wtype, s.ff)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU: every GPU box here has one, and no multi-GPU path is "
+                                   "built (DESIGN.md describes how the path would shard)", "n_gpus": args.gpus}))
+        return 2
+    import torch
+
+    from sfnx_amd import moe
+
+    torch.cuda.set_device(0)
+    dev = "cuda"
+    s = moe.LayerShape(H=2048, E=512, K=10, ff=512, wtype=moe.Q4_K, shared=True)
+    NL = args.layers
+    t0 = time.time()
+    layers = [moe.MoeLayer.synthetic(s, seed=1000 + l) for l in range(NL)]
+    torch.cuda.synchronize()
+    log(f"generated {NL} layers in {time.time() - t0:.1f}s")
+
+    # ------------------------------------------------------------------ decode, config 1
+    T = 1
+    x0 = torch.empty((T, s.H), dtype=torch.float32, device=dev)
+    moe.synth_normal(x0, 4242, 1.0)
+    x = x0.clone()
+    f = moe.FusedDecode(layers, T)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        f(x)   # warm: loads every kernel's code object
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        x.copy_(x0)
+        f(x)
+    for _ in range(args.warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(args.steps):
+        g.replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    ms_step = ev0.elapsed_time(ev1) / args.steps
+    nj = int(f.piece("njobs", torch.int32, (2,))[0])
+    assert nj == s.K + 1, nj   # 10 distinct routed experts + the shared one in the last layer
+    assert torch.isfinite(x).all()
+    eb = expert_bytes(s, moe)
+    bytes_tl = (s.E + 1) * s.H * 4 + (s.K + 1) * eb
+    us_tl = ms_step * 1000 / NL
+    gbs = bytes_tl * NL / (ms_step * 1e-3) / 1e9
+    log(f"decode: {ms_step:.3f} ms/step, {us_tl:.2f} us/token-layer, {gbs:.0f} GB/s")
+
+    # ------------------------------------------------------------------ each kernel alone (HIP events, launch stream)
+    names = {1: "k_dec_router", 2: "k_dec_experts", 4: "k_dec_down"}
+    alg = {1: (s.E + 1) * s.H * 4, 2: (s.K + 1) * 2 * s.ff * moe.row_bytes(s.wtype, s.H),
+           4: (s.K + 1) * s.H * moe.row_bytes(s.wtype, s.ff)}
+    tot = {k: 0.0 for k in names}
+    reps = 3
+    evs = []
+    for _ in range(reps):
+        x.copy_(x0)
+        for l in range(NL):
+            for ph in (1, 2, 4):
+                a, z = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                f(x, layer0=l, n_layers=1, phases=ph)
+                z.record()
+                evs.append((ph, a, z))
+    torch.cuda.synchronize()
+    for ph, a, z in evs:
+        tot[ph] += a.elapsed_time(z) * 1000
+    avg_us = {names[k]: tot[k] / (reps * NL) for k in names}
+    dom = max(names, key=lambda k: tot[k])
+    ach = alg[dom] / (tot[dom] / (reps * NL) * 1e-6) / 1e9
+    log("per-kernel avg us (eager, events around each launch): " + ", ".join(f"{n} {v:.2f}" for n, v in avg_us.items()))
+
+    out = {
+        "metric": "Q4_K MoE-layer µs/token + HBM GB/s (decode); TFLOPS at 2k-token prefill",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_k x q8_1 (int8 dot4), fp32 accumulate",
+        "data": "synthetic: seeded Irwin-Hall(12) normals, weights N(0,0.02) quantized by the library's Q4_K quantizer",
+        "config": {"workload": "config 1: Q4_K decode, batch 1, 48 stacked MoE layers", "hidden": s.H, "experts": s.E,
+                   "ff": s.ff, "topk": s.K, "shared_expert": True, "layers": NL, "tokens_per_step": T,
+                   "parallelism": "none (1 GPU, every expert resident in HBM)"},
+        "us_per_token_layer": round(us_tl, 3),
+        "us_per_token": round(ms_step * 1000, 2),
+        "bytes_per_token_layer": bytes_tl,
+        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "kernel_avg_us": {n: round(v, 3) for n, v in avg_us.items()},
+        "roofline": {"kernel": names[dom], "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": alg[dom]},
+    }
+    if not args.no_prefill:
+        out["prefill"] = bench_prefill(layers[0], s, moe, torch)
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(layers[0], s, moe, torch, x0, args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def zipf_bias(E):
+    import numpy as np
+    rank = np.random.default_rng(ZIPF_SEED).permutation(E) + 1
+    return (ZIPF_ALPHA * -ZIPF_S * np.log(rank)).astype(np.float32)
+
+
+def bench_prefill(L, s, moe, torch, C=2048, reps=10):
+    """config 3: 2048 tokens through layer 0, a seeded Zipf(1.1) bias on the routed logits; the expert kernels timed"""
+    dev = "cuda"
+    x = torch.empty((C, s.H), dtype=torch.float32, device=dev)
+    moe.synth_normal(x, 777, 1.0)
+    xn = torch.empty_like(x)
+    moe.residual_rmsnorm(x, None, xn)
+    b = moe.PrefillBuffers(s, C)
+    bias = torch.from_numpy(zipf_bias(s.E)).to(dev)
+    moe.quantize_q8_1(xn, b.xq)
+    moe.router_logits(L.W, xn, b.logits)
+    b.logits[:, : s.E] += bias
+    moe.pf_route(b.logits, b.topi, b.topw, b.cnt, b.jbase, b.jobs_gu, b.jobs_dn, b.njobs, s.E, s.K, s.shared)
+    torch.cuda.synchronize()
+    cnt = b.cnt.cpu()
+    gu_call = lambda: moe.moe_gate_up_big(L.gu_w, L.gu_stride, s.wtype, s.H, 2 * s.ff, b.jobs_gu, b.njobs, b.cap, b.xq, b.gu)
+    dn_call = lambda: moe.moe_down_big(L.dn_w, L.dn_stride, s.wtype, s.ff, s.H, b.jobs_dn, b.njobs, b.cap, b.gu, b.part)
+    for _ in range(2):
+        gu_call()
+        dn_call()
+    torch.cuda.synchronize()
+    e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    e[0].record()
+    for _ in range(reps):
+        gu_call()
+    e[1].record()
+    for _ in range(reps):
+        dn_call()
+    e[2].record()
+    torch.cuda.synchronize()
+    t_gu = e[0].elapsed_time(e[1]) / reps * 1e3
+    t_dn = e[1].elapsed_time(e[2]) / reps * 1e3
+    P = C * s.K
+    ops = 2 * (P + C) * (2 * s.ff * s.H + s.H * s.ff)   # 2 ops per multiply-add, routed + shared pairs
+    touched = int((cnt > 0).sum()) + 1
+    wbytes = touched * expert_bytes(s, moe)
+    t = (t_gu + t_dn) * 1e-6
+    return {"workload": "config 3: 2048 tokens, Zipf(1.1)-skewed routing, Q4_K experts, q8_1 int8-dot BigJob kernels",
+            "us_gate_up": round(t_gu, 1), "us_down": round(t_dn, 1), "tops": round(ops / t / 1e12, 2),
+            "int8_peak_frac": round(ops / t / 1e12 / INT8_MFMA_PEAK_TOPS, 4),
+            "weight_gbs": round(wbytes / t / 1e9, 1), "hbm_frac": round(wbytes / t / 1e9 / HBM_PEAK_GBS, 4),
+            "experts_touched": touched, "max_rows_per_expert": int(cnt.max()), "ops": ops}
+
+
+def cpu_baseline(L, s, moe, torch, x0, seconds):
+    """the oracle (the reference's arithmetic restated in C) on config 0: one token through layer 0 on the host's
+    cores, against the GPU's output for the same token"""
+    import numpy as np
+
+    from oracle import oracle as orc
+    E1 = s.E + 1
+    gu_g = torch.empty_like(L.gu_w)
+    dn_g = torch.empty_like(L.dn_w)
+    moe.store_unpack(s.wtype, L.gu_w, gu_g, E1, 2 * s.ff, s.H)
+    moe.store_unpack(s.wtype, L.dn_w, dn_g, E1, s.H, s.ff)
+    xn = torch.empty_like(x0)
+    moe.residual_rmsnorm(x0.clone(), None, xn)
+    y = torch.empty_like(x0)
+    b = moe.DecodeBuffers(s, 1)
+    moe.decode_layer(L, xn, y, b)
+    torch.cuda.synchronize()
+    host = orc.LayerWeights(L.W.cpu().numpy(), gu_g.cpu().numpy(), dn_g.cpu().numpy(), s.wtype, s.H, s.E, s.K, s.ff, True)
+    x = xn.cpu().numpy()
+    threads = min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", "16")), 16)
+    us1, _ = orc.time_layer_decode(host, x, threads, 3, 0)   # one short run to size the sample
+    reps = max(5, min(200, int(seconds * 1e6 / max(us1, 1.0) / 2)))
+    us, _ = orc.time_layer_decode(host, x, threads, reps, 1 << 30)
+    oy, _, oi, _, _, _ = orc.layer_decode(host, x, threads)
+    err = float(np.max(np.abs(y.cpu().numpy() - oy)) / np.max(np.abs(oy)))
+    bytes_tl = E1 * s.H * 4 + (s.K + 1) * expert_bytes(s, moe)
+    cpu = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(us, 1), "unit": "us/token-layer", "cores": threads, "kind": "port",
+            "sample": f"config 0: one token through one layer (layer 0 of the bench), median of {reps} runs, "
+                      f"a 1 GiB sweep between runs",
+            "gbs": round(bytes_tl / (us * 1e-6) / 1e9, 2), "cpu_model": cpu,
+            "gpu_vs_cpu_max_rel_err": err, "gpu_vs_cpu_topi_equal": bool(np.array_equal(b.topi.cpu().numpy(), oi))}
+
+
+if __name__ == "__main__":
+    sys.exit(main())

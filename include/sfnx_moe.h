@@ -110,6 +110,38 @@ int sfnx_moe_down_big(const void* A, size_t sa, uint32_t type, int n_in, int n_o
 int sfnx_moe_combine(const float* part, const float* topw, const int* topi, const float* logits, float* y, int T, int H,
                      int E, int K, int shared, void* st);
 
+/* ---------------------------------------------------------------------------------------------- fused decode */
+/* one layer's weights: router W [E + 1][H] fp32 (row E gates the shared expert), planar gate|up experts (E + 1 of
+ * [2 ff][H], the shared expert last) and planar down experts (E + 1 of [H][ff]) */
+typedef struct sfnx_moe_layer_w {
+    const float* W;
+    const void* gu;
+    size_t gu_stride;
+    const void* dn;
+    size_t dn_stride;
+} sfnx_moe_layer_w;
+
+/* bytes of the workspace sfnx_moe_decode needs for windows of up to T rows; offsets (may be null) receives the byte
+ * offsets of its pieces: logits [T][E+1] f32, xq [T][H/32] q8_1, topi [T][K] i32, topw [T][K] f32, jobs_gu and
+ * jobs_dn [T K + 1] sfnx_job, njobs [2] i32, gu [T K + T][2 ff] f32, hq_q [T K + T][ff] i8, hq_d and hq_s
+ * [T K + T][ff / 32] (f32 scale, i32 sum), y [T][H] f32, then the total (13 values) */
+size_t sfnx_moe_decode_workspace(int T, int H, int E, int K, int ff, size_t* offsets);
+
+/* A decode window (1 <= T <= 16 rows) through n_layers stacked MoE layers, replacing the engine's per-layer calls
+ * router_route + moe_gate_up + moe_down + the combine (src/engine.cu:933-978, src/kernels.hpp:269-313) with three
+ * launches a layer.  x [T][H] is the residual stream, updated in place: per layer x += MoE(norm ? rmsnorm(x) : x)
+ * (rmsnorm as sfnx_residual_rmsnorm).  The workspace keeps the last layer's routing and intermediates (see
+ * sfnx_moe_decode_workspace).  Same arithmetic, value for value, as the unfused entry points.  H in {1024, 2048,
+ * 2560, 4096}, ff in {512, 1024}.  phases: 0 runs everything; otherwise a mask of the launches to issue per layer
+ * (1 router, 2 gate|up, 4 down + combine), for timing each one alone. */
+int sfnx_moe_decode(const sfnx_moe_layer_w* layers, int n_layers, uint32_t type, int H, int E, int K, int ff, int shared,
+                    float* x, int T, int norm, float eps, void* ws, size_t ws_bytes, int phases, void* st);
+
+/* the stacked-layer driver's glue between layers (no reference counterpart on the MoE path: the engine's
+ * hyper-connection read, src/hc.cuh, normalises the MoE input): x += y (y may be null), then
+ * xn = x / sqrt(mean(x^2) + eps) per row of H */
+int sfnx_residual_rmsnorm(float* x, const float* y, float* xn, int T, int H, float eps, void* st);
+
 #ifdef __cplusplus
 }
 #endif

@@ -5,11 +5,12 @@ Loading fails loudly when the library is missing: there is no fallback path.
 from __future__ import annotations
 
 import ctypes as C
+import os
 import re
 from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
-LIB_PATH = PKG / "libsfnx_moe.so"
+LIB_PATH = Path(os.environ.get("SFNX_LIB", PKG / "libsfnx_moe.so"))   # SFNX_LIB: a library built elsewhere
 HEADER = PKG.parent / "include" / "sfnx_moe.h"
 
 Q8_0, Q4_K = 8, 12
@@ -38,7 +39,15 @@ SIGNATURES = {
     "sfnx_moe_gate_up_big": (i32, [vp, sz, u32, i32, i32, vp, vp, i32, vp, vp, vp]),
     "sfnx_moe_down_big": (i32, [vp, sz, u32, i32, i32, vp, vp, i32, vp, vp, vp]),
     "sfnx_moe_combine": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp]),
+    "sfnx_residual_rmsnorm": (i32, [vp, vp, vp, i32, i32, f32, vp]),
+    "sfnx_moe_decode_workspace": (sz, [i32, i32, i32, i32, i32, vp]),
+    "sfnx_moe_decode": (i32, [vp, i32, u32, i32, i32, i32, i32, i32, vp, i32, i32, f32, vp, sz, i32, vp]),
 }
+
+
+class LayerW(C.Structure):
+    """sfnx_moe_layer_w"""
+    _fields_ = [("W", vp), ("gu", vp), ("gu_stride", sz), ("dn", vp), ("dn_stride", sz)]
 
 
 def declared_symbols() -> list[str]:

@@ -57,6 +57,25 @@ template <int G> __device__ __forceinline__ int group_isum(int v) {
 
 __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
+// 1 / sqrt(mean(x^2) + eps) of a row of H values (H % 256 == 0) by one wavefront, in the router's partition: lane l
+// sums the squares of its float4 chunks l, l + 64, ... in order (fmaf), then a xor butterfly; every lane returns the
+// same value.  rms_from_sum finishes it from the lane sums.
+__device__ __forceinline__ float rms_lane_add(float4 v, float ss) {
+    ss = fmaf(v.x, v.x, ss);
+    ss = fmaf(v.y, v.y, ss);
+    ss = fmaf(v.z, v.z, ss);
+    return fmaf(v.w, v.w, ss);
+}
+__device__ __forceinline__ float rms_from_sum(float ss, int H, float eps) {
+    ss = group_sum<WAVE>(ss);
+    return 1.0f / sqrtf(ss / (float) H + eps);
+}
+__device__ __forceinline__ float wave_rms_scale(const float* x, int H, int lane, float eps) {
+    float ss = 0.f;
+    for (int c = lane; c < H / 4; c += WAVE) ss = rms_lane_add(reinterpret_cast<const float4*>(x)[c], ss);
+    return rms_from_sum(ss, H, eps);
+}
+
 // silu and sigmoid as the reference writes them (src/kernels.cu:46-47), exp by the device library
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
 __device__ __forceinline__ float sigm_f(float x) { return 1.0f / (1.0f + expf(-x)); }

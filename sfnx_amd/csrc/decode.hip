@@ -1,0 +1,509 @@
+// The decode window's MoE layers as three launches each, no atomics and no device-wide fences (a grid barrier costs
+// several kernel boundaries on this chip, and an agent-scope fence writes back the whole L2):
+//
+//   K1 k_dec_router: RMSNorm of the residual stream on the fly, the router's logits (a row a wavefront), and the
+//      normalised activations as q8_1 (every block a share of the 32-blocks).
+//   K2 k_dec_experts: every block takes the top-K of the logits itself and numbers the jobs (the same deterministic
+//      first-pick order as router_route); a block is one unit (job, 32 FF indices): 32 gate rows and the 32 matching up
+//      rows dotted with the job's rows, SwiGLU in registers, h quantized to q8_1 per 32 (k_moe_h, src/moe.cuh:284-295).
+//   K3 k_dec_down: a block owns 8 output rows: the down rows of every job for those outputs, then the weighted combine
+//      in the reference's fmaf order (src/kernels.cu:797-803) and the residual add.
+//
+// The arithmetic of every value is the unfused entry points' (router_route, moe_gate_up, moe_down, moe_combine), so the
+// two paths agree bit for bit.
+#include "mv.hpp"
+#ifdef SFNX_PHASE_PROF
+#define SFNX_TOPK_STAMP if (lane == 0 && blockIdx.x == 0) { uint64_t sink = 0; for (int i = 0; i < NV; ++i) sink += key[i]; if (sink == 12345) key[0] = 0; g_prof_topk = wall_clock64(); }
+__device__ unsigned long long g_prof_topk;
+#endif
+#include "topk.hpp"
+
+namespace sfnx {
+namespace {
+
+// SFNX_PHASE_PROF (off in the product build): wall-clock stamps of the kernels' phases, blocks 0 and 100, for
+// finding where a launch's time goes
+#ifdef SFNX_PHASE_PROF
+__device__ unsigned long long g_prof[8][16];
+#define PROF(k, i)                                                                  \
+    if (threadIdx.x == 0 && (blockIdx.x == 0 || blockIdx.x == 100)) g_prof[2 * (k) + (blockIdx.x != 0)][i] = wall_clock64();
+#else
+#define PROF(k, i)
+#endif
+
+constexpr int D1_THREADS = 128, D1_WAVES = D1_THREADS / WAVE;   // K1: a router row per wavefront
+constexpr int D3_THREADS = 256, D3_ROWS = 8;                    // K3: output rows per block
+template <int TYPE> constexpr int lpr_of() { return TYPE == SFNX_Q4_K ? 8 : 16; }
+template <int TYPE> constexpr int d2_threads() { return 32 * lpr_of<TYPE>(); }   // K2: 32 FF indices a block
+
+struct DecLayout {
+    size_t logits, xq, topi, topw, jg, jd, njobs, gu, hq_q, hq_d, hq_s, y, total;
+};
+DecLayout dec_layout(int T, int H, int E, int K, int ff) {
+    const size_t P = (size_t) T * K, NP = P + T, nj = P + 1;
+    size_t o = 0;
+    auto take = [&](size_t bytes) {
+        const size_t r = o;
+        o += (bytes + 255) / 256 * 256;
+        return r;
+    };
+    DecLayout L;
+    L.logits = take((size_t) T * (E + 1) * 4);
+    L.xq = take((size_t) T * (H / 32) * Q81_BYTES);
+    L.topi = take(P * 4);
+    L.topw = take(P * 4);
+    L.jg = take(nj * sizeof(sfnx_job));
+    L.jd = take(nj * sizeof(sfnx_job));
+    L.njobs = take(8);
+    L.gu = take(NP * 2 * ff * 4);
+    L.hq_q = take(NP * ff);
+    L.hq_d = take(NP * (ff / 32) * 4);
+    L.hq_s = take(NP * (ff / 32) * 4);
+    L.y = take((size_t) T * H * 4);
+    L.total = o;
+    return L;
+}
+
+// ------------------------------------------------------------------------------------------------ K1
+template <int NC, int TT>
+__global__ void __launch_bounds__(D1_THREADS) k_dec_router(const float* __restrict__ W, const float* __restrict__ x, int T,
+                                                          int E, float eps, int norm, float* __restrict__ logits,
+                                                          uint8_t* __restrict__ xq) {
+    constexpr int H = NC * 4 * WAVE, NQ = 2;
+    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE, L = E + 1;
+    const int row = blockIdx.x * D1_WAVES + wave;
+    // every load of the launch issued up front: the router row, each token's chunks, this half-wave's q8_1 blocks
+    const int nb = H / 32, hw = threadIdx.x / 32, l = threadIdx.x % 32, nslot = gridDim.x * (D1_THREADS / 32);
+    float xqv[NQ];
+#pragma unroll
+    for (int k = 0; k < NQ; ++k) {
+        const int q = blockIdx.x * (D1_THREADS / 32) + hw + k * nslot;
+        xqv[k] = q < T * nb ? x[(size_t) (q / nb) * H + 32 * (q % nb) + l] : 0.f;
+    }
+    const bool live = row < L;
+    float4 wv[NC];
+#pragma unroll
+    for (int i = 0; i < NC; ++i) wv[i] = reinterpret_cast<const float4*>(W + (size_t) (live ? row : 0) * H)[i * WAVE + lane];
+    __shared__ float rs[SFNX_MAXT];
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+        if (t >= T) break;
+        const float4* x4 = reinterpret_cast<const float4*>(x + (size_t) t * H);
+        float4 xv[NC];
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < NC; ++i) {
+            xv[i] = x4[i * WAVE + lane];
+            ss = rms_lane_add(xv[i], ss);
+        }
+        const float r = norm ? rms_from_sum(ss, H, eps) : 1.0f;
+        if (threadIdx.x == 0) rs[t] = r;
+        float a = 0.f;
+#pragma unroll
+        for (int i = 0; i < NC; ++i) {
+            a = fmaf(wv[i].x, xv[i].x * r, a);
+            a = fmaf(wv[i].y, xv[i].y * r, a);
+            a = fmaf(wv[i].z, xv[i].z * r, a);
+            a = fmaf(wv[i].w, xv[i].w * r, a);
+        }
+        a = group_sum<WAVE>(a);
+        if (live && lane == 0) logits[(size_t) t * L + row] = a;
+    }
+    __syncthreads();
+    // the normalised rows as q8_1 (k_quantize's arithmetic), a half-wave per 32-block, spread over the grid
+#pragma unroll
+    for (int k = 0; k < NQ; ++k) {
+        const int q = blockIdx.x * (D1_THREADS / 32) + hw + k * nslot;
+        if (q >= T * nb) break;
+        const int t = q / nb;
+        const float xi = xqv[k] * rs[t];
+        const float amax = group_max<32>(fabsf(xi)), sum = group_sum<32>(xi);
+        const float d = amax / 127.0f;
+        uint8_t* blk = xq + (size_t) q * Q81_BYTES;
+        blk[4 + l] = (uint8_t) (int8_t) (amax == 0.0f ? 0 : (int) roundf(xi / d));
+        if (l == 0) *reinterpret_cast<uint32_t*>(blk) = (uint32_t) f2h(d) | ((uint32_t) f2h(sum) << 16);
+    }
+    // small grids: the blocks past the preloaded ones
+    for (int q = blockIdx.x * (D1_THREADS / 32) + hw + NQ * nslot; q < T * nb; q += nslot) {
+        const int t = q / nb;
+        const float xi = x[(size_t) t * H + 32 * (q % nb) + l] * rs[t];
+        const float amax = group_max<32>(fabsf(xi)), sum = group_sum<32>(xi);
+        const float d = amax / 127.0f;
+        uint8_t* blk = xq + (size_t) q * Q81_BYTES;
+        blk[4 + l] = (uint8_t) (int8_t) (amax == 0.0f ? 0 : (int) roundf(xi / d));
+        if (l == 0) *reinterpret_cast<uint32_t*>(blk) = (uint32_t) f2h(d) | ((uint32_t) f2h(sum) << 16);
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ K2
+template <int TYPE, int G> struct RowOf;
+template <int G> struct RowOf<SFNX_Q4_K, G> {
+    using R = Q4kRow<G>;
+    static __device__ __forceinline__ void load(R& w, const uint8_t* mat, int nrows, int row, int C, int ln) {
+        w.load(q4k_planes(mat, nrows, C), row, C, ln);
+    }
+};
+template <int G> struct RowOf<SFNX_Q8_0, G> {
+    using R = Q80Row<G>;
+    static __device__ __forceinline__ void load(R& w, const uint8_t* mat, int nrows, int row, int C, int ln) {
+        w.load(q80_planes(mat, nrows, C), row, C, ln);
+    }
+};
+
+template <int TYPE, int G, int TT>
+__global__ void __launch_bounds__(d2_threads<TYPE>()) k_dec_experts(
+    const uint8_t* __restrict__ A, size_t sa, int T, int H, int E, int K, int ff, int shared, const float* __restrict__ logits,
+    const uint8_t* __restrict__ xq, int* __restrict__ topi_g, float* __restrict__ topw_g, sfnx_job* __restrict__ jg,
+    sfnx_job* __restrict__ jd, int* __restrict__ njobs_g, float* __restrict__ gu, int8_t* __restrict__ hq_q,
+    float* __restrict__ hq_d, int* __restrict__ hq_s) {
+    constexpr int LPR = lpr_of<TYPE>(), NTH = d2_threads<TYPE>(), NW = NTH / WAVE, RPW = WAVE / LPR;
+    const int NFB = ff / 32, myjob = blockIdx.x / NFB, fb = blockIdx.x % NFB;
+    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE, p = threadIdx.x, P = T * K;
+    __shared__ int ex[MAX_P];
+    __shared__ float sw[MAX_P];
+    __shared__ unsigned char first[MAX_P];
+    __shared__ int jobof[MAX_E];
+    __shared__ sfnx_job jb;
+    __shared__ float hbuf[SFNX_MAXT][32];
+    extern __shared__ __align__(16) unsigned char lds[];
+    PROF(1, 0)
+    // every token's activations into LDS first: their loads overlap the top-k
+    const Acts a = acts_in(lds, TT, H);
+    stage_q8_1(a, xq, nullptr, T);
+    PROF(1, 7)
+    for (int t = wave; t < T; t += NW) {
+        int pick;
+        float w;
+        topk_wave_e(logits + (size_t) t * (E + 1), E, K, lane, pick, w);
+        if (lane < K) {
+            ex[t * K + lane] = pick;
+            sw[t * K + lane] = w;
+        }
+        PROF(1, 8)
+    }
+    __syncthreads();
+    PickSlot ps;
+    __shared__ int s_nr;
+    if (P <= WAVE) {
+        // every pick in one wavefront: the numbering in registers (readlane loops), no LDS loops
+        if (wave == 0) {
+            ps.e = lane < P ? ex[lane] : -1;
+            int firstq = P;
+            for (int q = 0; q < P; ++q) {
+                const int eq = __builtin_amdgcn_readlane(ps.e, q);
+                const bool same = ps.e >= 0 && eq == ps.e;
+                ps.cnt += same;
+                ps.slot += same && q < lane;
+                firstq = same && q < firstq ? q : firstq;
+            }
+            const uint64_t fm = __ballot(ps.e >= 0 && ps.slot == 0);
+            ps.job = ps.e >= 0 ? __popcll(fm & ((1ull << firstq) - 1ull)) : -1;
+            if (lane == 0) s_nr = __popcll(fm);
+        }
+        __syncthreads();
+    } else {
+        const int n = pick_slots(ex, P, first, jobof, ps);
+        if (threadIdx.x == 0) s_nr = n;
+        __syncthreads();
+    }
+    const int nr = s_nr;
+    PROF(1, 1)
+    const int nj = nr + (shared ? 1 : 0);
+    if (blockIdx.x == 0) {   // the routing, published for K3 and the caller
+        if (p < P) {
+            topi_g[p] = ex[p];
+            topw_g[p] = sw[p];
+            if (ps.e >= 0) {
+                const int j = ps.job;
+                if (ps.slot == 0) {
+                    jg[j].w = jd[j].w = ps.e;
+                    jg[j].n = jd[j].n = ps.cnt;
+                }
+                jg[j].y[ps.slot] = p / K;
+                jg[j].out[ps.slot] = jd[j].y[ps.slot] = jd[j].out[ps.slot] = p;
+            }
+        }
+        if (shared) {
+            if (p == 0) {
+                jg[nr].w = jd[nr].w = E;
+                jg[nr].n = jd[nr].n = T;
+            }
+            if (p < T) {
+                jg[nr].y[p] = p;
+                jg[nr].out[p] = jd[nr].y[p] = jd[nr].out[p] = P + p;
+            }
+        }
+        if (p == 0) {
+            njobs_g[0] = nj;
+            njobs_g[1] = 0;
+        }
+    }
+    if (myjob >= nj) return;
+    PROF(1, 2)
+    if (myjob < nr) {
+        if (p < P && ps.job == myjob) {
+            if (ps.slot == 0) {
+                jb.w = ps.e;
+                jb.n = ps.cnt;
+            }
+            jb.y[ps.slot] = p / K;
+            jb.out[ps.slot] = p;
+        }
+    } else {
+        if (p == 0) {
+            jb.w = E;
+            jb.n = T;
+        }
+        if (p < T) {
+            jb.y[p] = p;
+            jb.out[p] = P + p;
+        }
+    }
+    __syncthreads();
+    PROF(1, 3)
+    const int rw = lane / LPR, ln = lane % LPR, f = fb * 32 + wave * RPW + rw;
+    const uint8_t* mat = A + (size_t) jb.w * sa;
+    typename RowOf<TYPE, G>::R wg, wu;
+    RowOf<TYPE, G>::load(wg, mat, 2 * ff, f, H, ln);
+    RowOf<TYPE, G>::load(wu, mat, 2 * ff, ff + f, H, ln);
+    for (int s = 0; s < jb.n; ++s) {
+        const int t = jb.y[s];
+        const float gv = group_sum<LPR>(wg.dot(a, t, ln)), uv = group_sum<LPR>(wu.dot(a, t, ln));
+        if (ln == 0) {
+            const int o = jb.out[s];
+            gu[(size_t) o * 2 * ff + f] = gv;
+            gu[(size_t) o * 2 * ff + ff + f] = uv;
+            hbuf[s][wave * RPW + rw] = silu_f(gv) * uv;
+        }
+    }
+    __syncthreads();
+    PROF(1, 5)
+    for (int s = threadIdx.x / 32; s < jb.n; s += NTH / 32) {
+        const int l = threadIdx.x % 32, o = jb.out[s];
+        const float v = hbuf[s][l];
+        const float amax = group_max<32>(fabsf(v));
+        const float d = amax / 127.0f;
+        const int q = amax == 0.0f ? 0 : (int) roundf(v / d);
+        const int qs = group_isum<32>(q);
+        hq_q[(size_t) o * ff + 32 * fb + l] = (int8_t) q;
+        if (l == 0) {
+            hq_d[(size_t) o * NFB + fb] = h2f(f2h(d));
+            hq_s[(size_t) o * NFB + fb] = qs;
+        }
+    }
+    PROF(1, 6)
+}
+
+// ------------------------------------------------------------------------------------------------ K3
+template <int TYPE, int G2, int NB>
+__global__ void __launch_bounds__(D3_THREADS) k_dec_down(const uint8_t* __restrict__ A, size_t sa, int T, int H, int E, int K,
+                                                        int ff, int shared, const float* __restrict__ logits,
+                                                        const int* __restrict__ topi, const float* __restrict__ topw,
+                                                        const sfnx_job* __restrict__ jd, const int* __restrict__ njobs,
+                                                        const int8_t* __restrict__ hq_q, const float* __restrict__ hq_d,
+                                                        const int* __restrict__ hq_s, float* __restrict__ y,
+                                                        float* __restrict__ x, int hq_in_lds) {
+    constexpr int LPR = lpr_of<TYPE>(), GROUPS = D3_THREADS / LPR;
+    const int row0 = blockIdx.x * D3_ROWS, nj = njobs[0], P = T * K, NP = P + T, nbh = ff / 32;
+    PROF(2, 0)
+    __shared__ int jw[MAX_P + 1], jn[MAX_P + 1], jout[MAX_P + 1][SFNX_MAXT];
+    __shared__ float part[MAX_P + SFNX_MAXT][D3_ROWS];
+    __shared__ int ti[MAX_P];
+    __shared__ float tw[MAX_P], sg[SFNX_MAXT];
+    extern __shared__ __align__(16) unsigned char lds[];   // every pair's h, when the launch gave room for it
+    for (int i = threadIdx.x; i < nj; i += D3_THREADS) {
+        jw[i] = jd[i].w;
+        jn[i] = jd[i].n;
+        for (int s = 0; s < jd[i].n; ++s) jout[i][s] = jd[i].out[s];
+    }
+    for (int i = threadIdx.x; i < P; i += D3_THREADS) {
+        ti[i] = topi[i];
+        tw[i] = topw[i];
+    }
+    __shared__ float xr[SFNX_MAXT][D3_ROWS];   // the residual rows this block adds to, read with everything else
+    for (int i = threadIdx.x; i < T * D3_ROWS; i += D3_THREADS) xr[i / D3_ROWS][i % D3_ROWS] = x[(size_t) (i / D3_ROWS) * H + row0 + i % D3_ROWS];
+    if (shared)
+        for (int t = threadIdx.x; t < T; t += D3_THREADS) sg[t] = sigm_f(logits[(size_t) t * (E + 1) + E]);
+    Acts a;
+    const bool staged = hq_in_lds != 0;
+    if (staged) {
+        a = acts_in(lds, NP, ff);
+        const int4* src = reinterpret_cast<const int4*>(hq_q);
+        for (int i = threadIdx.x; i < NP * ff / 16; i += D3_THREADS) reinterpret_cast<int4*>(a.q)[i] = src[i];
+        for (int i = threadIdx.x; i < NP * nbh; i += D3_THREADS) {
+            a.d[i] = hq_d[i];
+            a.s[i] = hq_s[i];
+        }
+    } else {
+        a.q = const_cast<int8_t*>(hq_q);
+        a.d = const_cast<float*>(hq_d);
+        a.s = const_cast<int*>(hq_s);
+        a.K = ff;
+    }
+    __syncthreads();
+    const int g = threadIdx.x / LPR, ln = threadIdx.x % LPR, ntask = nj * D3_ROWS;
+    PROF(2, 1)
+    for (int t0 = g; t0 < ntask; t0 += GROUPS * NB) {
+        typename RowOf<TYPE, G2>::R w[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const int task = t0 + b * GROUPS;
+            if (task < ntask) {
+                const int j = task / D3_ROWS, r = task % D3_ROWS;
+                RowOf<TYPE, G2>::load(w[b], A + (size_t) jw[j] * sa, H, row0 + r, ff, ln);
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const int task = t0 + b * GROUPS;
+            if (task < ntask) {
+                const int j = task / D3_ROWS, r = task % D3_ROWS;
+                for (int s = 0; s < jn[j]; ++s) {
+                    const int pp = jout[j][s];
+                    const float v = group_sum<LPR>(w[b].dot(a, pp, ln));
+                    if (ln == 0) part[pp][r] = v;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    PROF(2, 2)
+    for (int i = threadIdx.x; i < T * D3_ROWS; i += D3_THREADS) {
+        const int t = i / D3_ROWS, r = i % D3_ROWS, row = row0 + r;
+        float pw[MAX_K], pv[MAX_K];
+#pragma unroll
+        for (int k = 0; k < MAX_K; ++k) {   // every operand read first, then the chain
+            const bool use = k < K && ti[t * K + k] >= 0;
+            pw[k] = use ? tw[t * K + k] : 0.f;
+            pv[k] = use ? part[t * K + k][r] : 0.f;
+        }
+        float s = 0.f;
+#pragma unroll
+        for (int k = 0; k < MAX_K; ++k)
+            if (k < K && ti[t * K + k] >= 0) s = fmaf(pw[k], pv[k], s);
+        if (shared) s = fmaf(sg[t], part[P + t][r], s);
+        y[(size_t) t * H + row] = s;
+        x[(size_t) t * H + row] = xr[t][r] + s;
+    }
+    PROF(2, 3)
+}
+
+// ------------------------------------------------------------------------------------------------ launch
+struct DecArgs {
+    uint32_t type;
+    int H, E, K, ff, shared, T, norm;
+    float eps;
+    int phases;
+};
+
+template <int NC, int TT>
+void launch_k1(const DecArgs& d, const sfnx_moe_layer_w& w, float* x, const DecLayout& L, char* ws, hipStream_t s) {
+    const int rows = d.E + 1;
+    k_dec_router<NC, TT><<<(rows + D1_WAVES - 1) / D1_WAVES, D1_THREADS, 0, s>>>(
+        w.W, x, d.T, d.E, d.eps, d.norm, (float*) (ws + L.logits), (uint8_t*) (ws + L.xq));
+}
+template <int TYPE, int G, int TT>
+void launch_k2(const DecArgs& d, const sfnx_moe_layer_w& w, const DecLayout& L, char* ws, hipStream_t s) {
+    const int njmax = d.T * d.K + (d.shared ? 1 : 0);
+    k_dec_experts<TYPE, G, TT><<<njmax * (d.ff / 32), d2_threads<TYPE>(), acts_bytes(TT, d.H), s>>>(
+        (const uint8_t*) w.gu, w.gu_stride, d.T, d.H, d.E, d.K, d.ff, d.shared, (const float*) (ws + L.logits),
+        (const uint8_t*) (ws + L.xq), (int*) (ws + L.topi), (float*) (ws + L.topw), (sfnx_job*) (ws + L.jg),
+        (sfnx_job*) (ws + L.jd), (int*) (ws + L.njobs), (float*) (ws + L.gu), (int8_t*) (ws + L.hq_q),
+        (float*) (ws + L.hq_d), (int*) (ws + L.hq_s));
+}
+template <int TYPE, int G2, int NB>
+void launch_k3(const DecArgs& d, const sfnx_moe_layer_w& w, float* x, const DecLayout& L, char* ws, hipStream_t s) {
+    const int NP = d.T * d.K + d.T;
+    const size_t hq_lds = acts_bytes(NP, d.ff);
+    const bool staged = hq_lds <= 32 * 1024;
+    k_dec_down<TYPE, G2, NB><<<d.H / D3_ROWS, D3_THREADS, staged ? hq_lds : 0, s>>>(
+        (const uint8_t*) w.dn, w.dn_stride, d.T, d.H, d.E, d.K, d.ff, d.shared, (const float*) (ws + L.logits),
+        (const int*) (ws + L.topi), (const float*) (ws + L.topw), (const sfnx_job*) (ws + L.jd), (const int*) (ws + L.njobs),
+        (const int8_t*) (ws + L.hq_q), (const float*) (ws + L.hq_d), (const int*) (ws + L.hq_s), (float*) (ws + L.y), x,
+        staged ? 1 : 0);
+}
+
+template <int TT>
+void launch_layer_tt(const DecArgs& d, const sfnx_moe_layer_w& w, float* x, const DecLayout& L, char* ws, hipStream_t s) {
+    if (d.phases & 1) switch (d.H) {
+        case 1024: launch_k1<4, TT>(d, w, x, L, ws, s); break;
+        case 2048: launch_k1<8, TT>(d, w, x, L, ws, s); break;
+        case 2560: launch_k1<10, TT>(d, w, x, L, ws, s); break;
+        case 4096: launch_k1<16, TT>(d, w, x, L, ws, s); break;
+        default: throw std::runtime_error("hidden size must be 1024, 2048, 2560 or 4096");
+    }
+    const int G = d.H / 512;
+#define SFNX_K2(TY)                                                       \
+    switch (G) {                                                          \
+        case 2: launch_k2<TY, 2, TT>(d, w, L, ws, s); break;              \
+        case 4: launch_k2<TY, 4, TT>(d, w, L, ws, s); break;              \
+        case 5: launch_k2<TY, 5, TT>(d, w, L, ws, s); break;              \
+        case 8: launch_k2<TY, 8, TT>(d, w, L, ws, s); break;              \
+        default: throw std::runtime_error("hidden size must be 1024, 2048, 2560 or 4096"); \
+    }
+    if (d.phases & 2) {
+        if (d.type == SFNX_Q4_K) { SFNX_K2(SFNX_Q4_K) } else { SFNX_K2(SFNX_Q8_0) }
+    }
+#undef SFNX_K2
+    // down tasks a lane group loads together: every job's 8 rows in one batch at T = 1
+    constexpr int NB = TT == 1 ? 3 : 4;
+    if (!(d.phases & 4)) return;
+    if (d.type == SFNX_Q4_K) {
+        if (d.ff == 512) launch_k3<SFNX_Q4_K, 1, NB>(d, w, x, L, ws, s);
+        else launch_k3<SFNX_Q4_K, 2, NB>(d, w, x, L, ws, s);
+    } else {
+        if (d.ff == 512) launch_k3<SFNX_Q8_0, 1, NB>(d, w, x, L, ws, s);
+        else launch_k3<SFNX_Q8_0, 2, NB>(d, w, x, L, ws, s);
+    }
+}
+
+}  // namespace
+}  // namespace sfnx
+
+using namespace sfnx;
+
+#ifdef SFNX_PHASE_PROF
+extern "C" int sfnx_prof_read(unsigned long long* out) {
+    if (hipMemcpyFromSymbol(out, HIP_SYMBOL(g_prof), sizeof(g_prof)) != hipSuccess) return -1;
+    return hipMemcpyFromSymbol(out + 128, HIP_SYMBOL(g_prof_topk), 8) == hipSuccess ? 0 : -1;
+}
+#endif
+
+extern "C" size_t sfnx_moe_decode_workspace(int T, int H, int E, int K, int ff, size_t* offsets) {
+    const DecLayout L = dec_layout(T, H, E, K, ff);
+    if (offsets) {
+        const size_t o[13] = {L.logits, L.xq, L.topi, L.topw, L.jg, L.jd, L.njobs, L.gu, L.hq_q, L.hq_d, L.hq_s, L.y, L.total};
+        for (int i = 0; i < 13; ++i) offsets[i] = o[i];
+    }
+    return L.total;
+}
+
+extern "C" int sfnx_moe_decode(const sfnx_moe_layer_w* layers, int n_layers, uint32_t type, int H, int E, int K, int ff,
+                               int shared, float* x, int T, int norm, float eps, void* ws, size_t ws_bytes, int phases,
+                               void* st) {
+    return guarded("sfnx_moe_decode", [&] {
+        require(type == SFNX_Q4_K || type == SFNX_Q8_0, "expert type must be Q4_K (12) or Q8_0 (8)");
+        require(T >= 1 && T <= SFNX_MAXT, "T out of range (1..16)");
+        require(E >= WAVE && E % WAVE == 0 && E <= MAX_E, "E must be a multiple of 64, at most 1024");
+        require(K >= 1 && K <= MAX_K && K <= E, "K out of range (1..16)");
+        require(H == 1024 || H == 2048 || H == 2560 || H == 4096, "hidden size must be 1024, 2048, 2560 or 4096");
+        require(ff == 512 || ff == 1024, "FF must be 512 or 1024");
+        require(T * K <= (type == SFNX_Q4_K ? 256 : 512), "T K picks exceed the block");
+        const DecLayout L = dec_layout(T, H, E, K, ff);
+        require(ws != nullptr && ws_bytes >= L.total, "workspace smaller than sfnx_moe_decode_workspace()");
+        require(n_layers >= 0 && (n_layers == 0 || layers != nullptr), "no layers");
+        for (int l = 0; l < n_layers; ++l) {
+            require(layers[l].W && layers[l].gu && layers[l].dn, "a layer's weights are missing");
+            require(layers[l].gu_stride >= row_bytes(type, H) * 2 * (size_t) ff, "gate|up stride smaller than a matrix");
+            require(layers[l].dn_stride >= row_bytes(type, ff) * (size_t) H, "down stride smaller than a matrix");
+        }
+        const DecArgs d{type, H, E, K, ff, shared ? 1 : 0, T, norm ? 1 : 0, eps, phases ? phases : 7};
+        hipStream_t s = stream_of(st);
+        char* w = (char*) ws;
+        for (int l = 0; l < n_layers; ++l) {
+            if (T == 1) launch_layer_tt<1>(d, layers[l], x, L, w, s);
+            else if (T <= 4) launch_layer_tt<4>(d, layers[l], x, L, w, s);
+            else launch_layer_tt<16>(d, layers[l], x, L, w, s);
+        }
+    });
+}

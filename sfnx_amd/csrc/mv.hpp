@@ -1,0 +1,160 @@
+// Device building blocks of the expert kernels: jobs and activations in LDS, and a lane group's share of one Q4_K or
+// Q8_0 weight row dotted with int8 activations (v_dot4_i32_i8).  The arithmetic per (row, activation row):
+//   Q4_K: 8 lanes a row, lane l8 the 64-value groups l8 + 8 i in order (src/moe_q4k.cuh:30-86), each group
+//         d (d8l (sc0 dl) + d8h (sc1 dh)) - dmin (d8l (m0 sl) + d8h (m1 sh)), then xor 4, 2, 1 (src/moe.cuh:224-235).
+//   Q8_0: 16 lanes a row, lane l16 the 32-blocks l16 + 16 i in order, each (d_w d_a) sum(q_w q_a), then xor 8 .. 1.
+#pragma once
+#include "common.hpp"
+
+namespace sfnx {
+
+
+
+// a job into LDS (BigJob or Job)
+template <typename J> __device__ __forceinline__ void load_job(J& jb, const J* src) {
+    for (int k = threadIdx.x; k < (int) (sizeof(J) / 4); k += blockDim.x) reinterpret_cast<int*>(&jb)[k] = reinterpret_cast<const int*>(src)[k];
+}
+
+// LDS activations for up to TT rows of K values: int8 values, the f16-rounded block scale as float, the block's sum
+struct Acts {
+    int8_t* q;
+    float* d;
+    int* s;
+    int K;
+    __device__ __forceinline__ const int4* q4(int j, int blk) const { return reinterpret_cast<const int4*>(q + (size_t) j * K + 32 * blk); }
+};
+__device__ __forceinline__ Acts acts_in(unsigned char* lds, int TT, int K) {
+    Acts a;
+    a.q = reinterpret_cast<int8_t*>(lds);
+    a.d = reinterpret_cast<float*>(lds + (size_t) TT * K);
+    a.s = reinterpret_cast<int*>(lds + (size_t) TT * K + (size_t) TT * (K / 32) * 4);
+    a.K = K;
+    return a;
+}
+inline size_t acts_bytes(int TT, int K) { return (size_t) TT * K + (size_t) TT * (K / 32) * 8; }
+
+// rows ys[0..n) (rows 0..n-1 when ys is null) of q8_1 activations (36-byte blocks) into LDS: a thread per (row, block)
+__device__ inline void stage_q8_1(const Acts& a, const uint8_t* __restrict__ xq, const int* ys, int n) {
+    const int nb = a.K / 32;
+    for (int it = threadIdx.x; it < n * nb; it += blockDim.x) {
+        const int j = it / nb, b = it % nb;
+        const uint8_t* blk = xq + ((size_t) (ys ? ys[j] : j) * nb + b) * Q81_BYTES;
+        const int* src = reinterpret_cast<const int*>(blk + 4);
+        int w[8], s = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            w[k] = src[k];
+            s = dot4(w[k], 0x01010101, s);
+        }
+        int4* dst = reinterpret_cast<int4*>(a.q + (size_t) j * a.K + 32 * b);
+        dst[0] = make_int4(w[0], w[1], w[2], w[3]);
+        dst[1] = make_int4(w[4], w[5], w[6], w[7]);
+        a.d[j * nb + b] = h2f(*reinterpret_cast<const uint16_t*>(blk));
+        a.s[j * nb + b] = s;
+    }
+}
+
+// h = silu(gate) * up of gu rows ys[0..n) ([gate (K) | up (K)]) as q8_1 in LDS (k_moe_h, src/moe.cuh:284-295): a
+// half-wave per (row, 32 columns)
+__device__ inline void stage_swiglu(const Acts& a, const float* __restrict__ gu, const int* ys, int n) {
+    const int nb = a.K / 32, hw = threadIdx.x / 32, l = threadIdx.x % 32, nhw = blockDim.x / 32;
+    for (int it = hw; it < n * nb; it += nhw) {
+        const int j = it / nb, b = it % nb;
+        const float* g = gu + (size_t) ys[j] * 2 * a.K;
+        const float xi = silu_f(g[32 * b + l]) * g[a.K + 32 * b + l];
+        const float amax = group_max<32>(fabsf(xi));
+        const float d = amax / 127.0f;
+        const int q = amax == 0.0f ? 0 : (int) roundf(xi / d);
+        const int s = group_isum<32>(q);
+        a.q[(size_t) j * a.K + 32 * b + l] = (int8_t) q;
+        if (l == 0) {
+            a.d[j * nb + b] = h2f(f2h(d));
+            a.s[j * nb + b] = s;
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ Q4_K
+template <int GPL> struct Q4kRow {
+    uint4 q0[GPL], q1[GPL];
+    float d[GPL], dmin[GPL], sc0[GPL], m0[GPL], sc1[GPL], m1[GPL];
+    __device__ __forceinline__ void load(const Q4kPlanes& P, int row, int C, int l8) {
+        const uint8_t* nib = P.nib_row(row, C);
+        const uint8_t* hdr = P.hdr_row(row, C);
+        uint4 h[GPL];
+#pragma unroll
+        for (int i = 0; i < GPL; ++i) {
+            q0[i] = *reinterpret_cast<const uint4*>(nib + 256 * i + 16 * l8);
+            q1[i] = *reinterpret_cast<const uint4*>(nib + 256 * i + 128 + 16 * l8);
+            h[i] = *reinterpret_cast<const uint4*>(hdr + 16 * (2 * i + (l8 >> 2)));
+        }
+#pragma unroll
+        for (int i = 0; i < GPL; ++i) {
+            d[i] = h2f((uint16_t) (h[i].x & 0xffff));
+            dmin[i] = h2f((uint16_t) (h[i].x >> 16));
+            q4k_scale_min(h[i], 2 * (l8 & 3), sc0[i], m0[i]);
+            q4k_scale_min(h[i], 2 * (l8 & 3) + 1, sc1[i], m1[i]);
+        }
+    }
+    // this lane's share of row . activation row j
+    __device__ __forceinline__ float dot(const Acts& a, int j, int l8) const {
+        float tmp = 0.f;
+#pragma unroll
+        for (int i = 0; i < GPL; ++i) {
+            const int kb0 = (2 * i + (l8 >> 2)) * 8 + 2 * (l8 & 3);
+            const int4 a00 = a.q4(j, kb0)[0], a01 = a.q4(j, kb0)[1], a10 = a.q4(j, kb0 + 1)[0], a11 = a.q4(j, kb0 + 1)[1];
+            const unsigned qw[8] = {q0[i].x, q0[i].y, q0[i].z, q0[i].w, q1[i].x, q1[i].y, q1[i].z, q1[i].w};
+            const int al[8] = {a00.x, a00.y, a00.z, a00.w, a01.x, a01.y, a01.z, a01.w};
+            const int ah[8] = {a10.x, a10.y, a10.z, a10.w, a11.x, a11.y, a11.z, a11.w};
+            int dl = 0, dh = 0;
+#pragma unroll
+            for (int w = 0; w < 8; ++w) {
+                dl = dot4((int) (qw[w] & 0x0F0F0F0Fu), al[w], dl);
+                dh = dot4((int) ((qw[w] >> 4) & 0x0F0F0F0Fu), ah[w], dh);
+            }
+            const int nb = a.K / 32;
+            const float d8l = a.d[j * nb + kb0], d8h = a.d[j * nb + kb0 + 1];
+            const float sl = (float) a.s[j * nb + kb0], sh = (float) a.s[j * nb + kb0 + 1];
+            tmp += d[i] * (d8l * (sc0[i] * (float) dl) + d8h * (sc1[i] * (float) dh)) -
+                   dmin[i] * (d8l * (m0[i] * sl) + d8h * (m1[i] * sh));
+        }
+        return tmp;
+    }
+};
+
+// ------------------------------------------------------------------------------------------------ Q8_0
+template <int BPL> struct Q80Row {
+    uint4 qa[BPL], qb[BPL];
+    float dw[BPL];
+    __device__ __forceinline__ void load(const Q80Planes& P, int row, int C, int l16) {
+        const uint8_t* q = P.q + (size_t) row * C;
+        const uint16_t* d = P.d + (size_t) row * (C / 32);
+#pragma unroll
+        for (int i = 0; i < BPL; ++i) {
+            qa[i] = *reinterpret_cast<const uint4*>(q + 512 * i + 16 * l16);
+            qb[i] = *reinterpret_cast<const uint4*>(q + 512 * i + 256 + 16 * l16);
+            dw[i] = h2f(d[l16 + 16 * i]);
+        }
+    }
+    __device__ __forceinline__ float dot(const Acts& a, int j, int l16) const {
+        float acc = 0.f;
+        const int nb = a.K / 32;
+#pragma unroll
+        for (int i = 0; i < BPL; ++i) {
+            const int b = l16 + 16 * i;
+            const int4 a0 = a.q4(j, b)[0], a1 = a.q4(j, b)[1];
+            int s = dot4((int) qa[i].x, a0.x, 0);
+            s = dot4((int) qa[i].y, a0.y, s);
+            s = dot4((int) qa[i].z, a0.z, s);
+            s = dot4((int) qa[i].w, a0.w, s);
+            s = dot4((int) qb[i].x, a1.x, s);
+            s = dot4((int) qb[i].y, a1.y, s);
+            s = dot4((int) qb[i].z, a1.z, s);
+            s = dot4((int) qb[i].w, a1.w, s);
+            acc += (dw[i] * a.d[j * nb + b]) * (float) s;
+        }
+        return acc;
+    }
+};
+
+}  // namespace sfnx

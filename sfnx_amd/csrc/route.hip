@@ -1,6 +1,6 @@
 // Activations and routing: q8_1 quantization, the decode router (logits, top-k, jobs in one launch), the prompt path's
 // router logits and permutation, and the weighted combine.
-#include "common.hpp"
+#include "topk.hpp"
 
 namespace sfnx {
 namespace {
@@ -46,54 +46,6 @@ __device__ __forceinline__ float row_dot(const float4 (&wv)[NC], const float* __
 }
 
 constexpr int RR_THREADS = 256, RR_WAVES = RR_THREADS / WAVE;
-constexpr int MAX_E = 1024, MAX_K = 16, MAX_P = SFNX_MAXT * MAX_K;
-
-// the top-K of one token's E logits by one wavefront (lane l holds experts l + 64 i): K rounds of the largest untaken
-// value (strictly greater, so the lowest index among equal values in a lane; across lanes a tie goes to the lower
-// index; NaN and -inf are never taken).  Weights exp(l - l_top1) / sum in pick order (src/moe.cuh:128-162).
-__device__ void topk_wave(const float* lg, int E, int K, int lane, int* topi, float* topw, int* ex) {
-    float v[MAX_E / WAVE];
-    const int epl = E / WAVE;
-#pragma unroll
-    for (int i = 0; i < MAX_E / WAVE; ++i) v[i] = i < epl ? load_agent(lg + lane + WAVE * i) : -INFINITY;
-    unsigned taken = 0;
-    float top0 = 0.f, z = 0.f, wk = 0.f;
-    int ik = -1;
-    for (int k = 0; k < K; ++k) {
-        float bv = -INFINITY;
-        int bi = 0x7fffffff;
-#pragma unroll
-        for (int i = 0; i < MAX_E / WAVE; ++i)
-            if (!(taken >> i & 1u) && v[i] > bv) {
-                bv = v[i];
-                bi = lane + WAVE * i;
-            }
-#pragma unroll
-        for (int o = WAVE / 2; o; o >>= 1) {
-            const float ov = __shfl_xor(bv, o);
-            const int oi = __shfl_xor(bi, o);
-            if (ov > bv || (ov == bv && oi < bi)) {
-                bv = ov;
-                bi = oi;
-            }
-        }
-        const bool found = bi != 0x7fffffff;
-        if (found && (bi % WAVE) == lane) taken |= 1u << (bi / WAVE);
-        if (k == 0) top0 = bv;
-        const float ek = found ? expf(bv - top0) : 0.f;
-        z += ek;
-        if (lane == k) {
-            wk = ek;
-            ik = found ? bi : -1;
-        }
-    }
-    if (lane < K) {
-        topi[lane] = ik;
-        topw[lane] = ik < 0 ? 0.f : wk / z;
-        ex[lane] = ik;
-    }
-}
-
 // src/moe.cuh:73-202 k_router_route: the router's rows a wavefront each, the shared gate row E included; the last
 // block to finish takes the top-K of every token and builds the jobs (first-pick order, rows in pair order)
 template <int NC, int TT>
@@ -123,45 +75,34 @@ __global__ void __launch_bounds__(RR_THREADS) k_router_route(const float* __rest
     if (!last) return;
     __threadfence();
     __shared__ int ex[MAX_P];
-    for (int t = wave; t < T; t += RR_WAVES) topk_wave(logits + (size_t) t * L, E, K, lane, topi + t * K, topw + t * K, ex + t * K);
+    for (int t = wave; t < T; t += RR_WAVES) {
+        int pick;
+        float w;
+        topk_wave_e<true>(logits + (size_t) t * L, E, K, lane, pick, w);
+        if (lane < K) {
+            topi[t * K + lane] = pick;
+            topw[t * K + lane] = w;
+            ex[t * K + lane] = pick;
+        }
+    }
     __syncthreads();
-    // jobs: pair p's expert ex[p]; its slot = earlier pairs of the same expert; a job per expert's first pair
+    // jobs: a job per distinct expert in first-pick order, rows in pair order
     const int P = T * K;
     __shared__ unsigned char first[MAX_P];
-    __shared__ int jobof[MAX_E], nfirst;
+    __shared__ int jobof[MAX_E];
+    PickSlot ps;
+    const int nr = pick_slots(ex, P, first, jobof, ps);
     const int p = threadIdx.x;
-    int e = -1, slot = 0, cnt = 0;
-    if (p < P) {
-        e = ex[p];
-        if (e >= 0) {
-            for (int q = 0; q < P; ++q) {
-                const bool same = ex[q] == e;
-                slot += same && q < p;
-                cnt += same;
-            }
+    if (p < P && ps.e >= 0) {
+        const int j = ps.job;
+        if (ps.slot == 0) {
+            gu[j].w = dn[j].w = ps.e;
+            gu[j].n = dn[j].n = ps.cnt;
         }
-        first[p] = e >= 0 && slot == 0;
+        gu[j].y[ps.slot] = p / K;
+        gu[j].out[ps.slot] = dn[j].y[ps.slot] = dn[j].out[ps.slot] = p;
     }
-    __syncthreads();
-    if (p < P && first[p]) {
-        int j = 0;
-        for (int q = 0; q < p; ++q) j += first[q];
-        jobof[e] = j;
-        gu[j].w = dn[j].w = e;
-        gu[j].n = dn[j].n = cnt;
-    }
-    if (p == 0) {
-        int n = 0;
-        for (int q = 0; q < P; ++q) n += first[q];
-        nfirst = n;
-    }
-    __syncthreads();
-    if (p < P && e >= 0) {
-        const int j = jobof[e];
-        gu[j].y[slot] = p / K;
-        gu[j].out[slot] = dn[j].y[slot] = dn[j].out[slot] = p;
-    }
-    const int nj = nfirst;
+    const int nj = nr;
     if (shared) {
         if (p == 0) {
             gu[nj].w = dn[nj].w = E;
@@ -198,10 +139,15 @@ __global__ void __launch_bounds__(RR_THREADS) k_router_logits(const float* __res
 // src/prefill.cu:191-221 k_pf_top10: a wavefront per token
 __global__ void __launch_bounds__(RR_THREADS) k_pf_topk(const float* __restrict__ logits, int C, int E, int K,
                                                        int* __restrict__ topi, float* __restrict__ topw) {
-    __shared__ int ex[RR_WAVES * MAX_K];
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE, t = blockIdx.x * RR_WAVES + wave;
     if (t >= C) return;
-    topk_wave(logits + (size_t) t * (E + 1), E, K, lane, topi + (size_t) t * K, topw + (size_t) t * K, ex + wave * MAX_K);
+    int pick;
+    float w;
+    topk_wave_e(logits + (size_t) t * (E + 1), E, K, lane, pick, w);
+    if (lane < K) {
+        topi[(size_t) t * K + lane] = pick;
+        topw[(size_t) t * K + lane] = w;
+    }
 }
 __global__ void k_fill_int(int* p, int n, int v) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -299,6 +245,33 @@ __global__ void k_combine(const float* __restrict__ part, const float* __restric
     }
 }
 
+// the stacked-layer driver's glue between MoE layers: x += y, then xn = x / sqrt(mean(x^2) + eps) (an RMSNorm without
+// gain, standing in for the engine's hyper-connection read, src/hc.cuh, that normalises the MoE input); a block per
+// token, the mean square by one wavefront in the order of wave_rms_scale
+constexpr int RN_THREADS = 256;
+__global__ void __launch_bounds__(RN_THREADS) k_residual_rmsnorm(float* __restrict__ x, const float* __restrict__ y,
+                                                                float* __restrict__ xn, int H, float eps) {
+    extern __shared__ __align__(16) float xs[];
+    __shared__ float rs;
+    const int t = blockIdx.x;
+    float* xr = x + (size_t) t * H;
+    for (int i = threadIdx.x; i < H; i += RN_THREADS) {
+        float v = xr[i];
+        if (y) {
+            v += y[(size_t) t * H + i];
+            xr[i] = v;
+        }
+        xs[i] = v;
+    }
+    __syncthreads();
+    if (threadIdx.x < WAVE) {
+        const float r = wave_rms_scale(xs, H, threadIdx.x, eps);
+        if (threadIdx.x == 0) rs = r;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < H; i += RN_THREADS) xn[(size_t) t * H + i] = xs[i] * rs;
+}
+
 template <int TT>
 void launch_router_tt(int nc, dim3 g, hipStream_t s, const float* W, const float* x, float* logits, int T, int E, int K,
                       int* topi, float* topw, sfnx_job* gu, sfnx_job* dn, int* njobs, int shared) {
@@ -383,5 +356,14 @@ extern "C" int sfnx_moe_combine(const float* part, const float* topw, const int*
         const size_t n = (size_t) T * H;
         k_combine<<<(unsigned) std::min<size_t>((n + 255) / 256, 8192), 256, 0, stream_of(st)>>>(part, topw, topi, logits, y, T,
                                                                                                  H, E, K, shared);
+    });
+}
+
+extern "C" int sfnx_residual_rmsnorm(float* x, const float* y, float* xn, int T, int H, float eps, void* st) {
+    return guarded("sfnx_residual_rmsnorm", [&] {
+        require(H > 0, "H must be positive");
+        if (T <= 0) return;
+        require(H > 0 && H % 256 == 0 && H <= 16384, "H must be a multiple of 256, at most 16384");
+        k_residual_rmsnorm<<<T, RN_THREADS, H * sizeof(float), stream_of(st)>>>(x, y, xn, H, eps);
     });
 }

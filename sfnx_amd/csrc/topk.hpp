@@ -1,0 +1,162 @@
+// Routing building blocks: a wavefront's top-K of one token's expert logits, and the decode job numbering.
+#pragma once
+#include "common.hpp"
+
+namespace sfnx {
+
+constexpr int MAX_E = 1024, MAX_K = 16, MAX_P = SFNX_MAXT * MAX_K;
+
+// Wavefront reductions by DPP row operations (quad swaps, half-row and row mirrors, then the row broadcasts 15 and 31);
+// lane 63 holds the result, returned to every lane.  wave_max ignores NaN (v_max_f32's maxNum rule).
+template <int CTRL, int ROWS = 0xf> __device__ __forceinline__ int dpp_mov(int v) {
+    return __builtin_amdgcn_update_dpp(v, v, CTRL, ROWS, 0xf, false);
+}
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, __int_as_float(dpp_mov<0xB1>(__float_as_int(v))));          // quad_perm [1, 0, 3, 2]
+    v = fmaxf(v, __int_as_float(dpp_mov<0x4E>(__float_as_int(v))));          // quad_perm [2, 3, 0, 1]
+    v = fmaxf(v, __int_as_float(dpp_mov<0x141>(__float_as_int(v))));         // row_half_mirror
+    v = fmaxf(v, __int_as_float(dpp_mov<0x140>(__float_as_int(v))));         // row_mirror
+    v = fmaxf(v, __int_as_float(dpp_mov<0x142, 0xa>(__float_as_int(v))));    // row_bcast:15 into rows 1 and 3
+    v = fmaxf(v, __int_as_float(dpp_mov<0x143, 0xc>(__float_as_int(v))));    // row_bcast:31 into rows 2 and 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+__device__ __forceinline__ int wave_min(int v) {
+    v = min(v, dpp_mov<0xB1>(v));
+    v = min(v, dpp_mov<0x4E>(v));
+    v = min(v, dpp_mov<0x141>(v));
+    v = min(v, dpp_mov<0x140>(v));
+    v = min(v, dpp_mov<0x142, 0xa>(v));
+    v = min(v, dpp_mov<0x143, 0xc>(v));
+    return __builtin_amdgcn_readlane(v, 63);
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
+#define SFNX_KSTAGE(CTRL, ROWS)                                                                              \
+    {                                                                                                        \
+        const uint32_t hi = (uint32_t) dpp_mov<CTRL, ROWS>((int) (k >> 32)), lo = (uint32_t) dpp_mov<CTRL, ROWS>((int) k); \
+        const uint64_t o = ((uint64_t) hi << 32) | lo;                                                       \
+        k = o > k ? o : k;                                                                                   \
+    }
+    SFNX_KSTAGE(0xB1, 0xf)
+    SFNX_KSTAGE(0x4E, 0xf)
+    SFNX_KSTAGE(0x141, 0xf)
+    SFNX_KSTAGE(0x140, 0xf)
+    SFNX_KSTAGE(0x142, 0xa)
+    SFNX_KSTAGE(0x143, 0xc)
+#undef SFNX_KSTAGE
+    const uint32_t hi = (uint32_t) __builtin_amdgcn_readlane((int) (k >> 32), 63);
+    const uint32_t lo = (uint32_t) __builtin_amdgcn_readlane((int) k, 63);
+    return ((uint64_t) hi << 32) | lo;
+}
+
+// a logit and its index as one 64-bit key whose unsigned order is the pick order: the float's bits made monotone
+// (-0 taken as +0, so equal values compare equal) above the complemented index (the lower index wins a tie); NaN and
+// -inf, never taken, become 0
+__device__ __forceinline__ uint64_t pick_key(float v, int idx) {
+    if (v != v || v == -INFINITY) return 0;
+    const uint32_t u = __float_as_uint(v + 0.0f);
+    const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t) ord << 32) | (uint32_t) ~idx;
+}
+__device__ __forceinline__ float key_value(uint64_t k) {
+    const uint32_t ord = (uint32_t) (k >> 32);
+    return __uint_as_float((ord & 0x80000000u) ? (ord & 0x7fffffffu) : ~ord);
+}
+
+// The top-K of one token's E = 64 NV logits by one wavefront (lane l holds experts l + 64 i): K rounds of the largest
+// untaken value, the lowest index among equal values (the reference's strict `>` scan, then `oi < bi` across lanes);
+// NaN and -inf are never taken (src/moe.cuh:128-162, src/prefill.cu:191-221).  Each lane sorts its keys once; a round
+// is one DPP maximum over the lanes' heads, the winner's lane moving to its next key.  Weights exp(l_k - l_top1) / z
+// with z summed in pick order.  A round with nothing left gives index -1, weight 0.  Lane k < K returns pick k.
+// AGENT: the logits were written earlier in the same launch.
+template <int NV, bool AGENT = false>
+__device__ inline void topk_wave(const float* lg, int nv, int K, int lane, int& pick, float& weight) {
+    uint64_t key[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const float t = i >= nv ? NAN : AGENT ? load_agent(lg + lane + WAVE * i) : lg[lane + WAVE * i];
+        key[i] = pick_key(t, lane + WAVE * i);
+    }
+#ifdef SFNX_TOPK_STAMP
+    SFNX_TOPK_STAMP
+#endif
+    // descending bitonic sort of the lane's keys
+#pragma unroll
+    for (int k = 2; k <= NV; k *= 2)
+#pragma unroll
+        for (int j = k / 2; j > 0; j /= 2)
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+                const int l = i ^ j;
+                if (l > i) {
+                    const bool desc = (i & k) == 0;
+                    const uint64_t a = key[i], b = key[l];
+                    const bool sw = desc ? a < b : a > b;
+                    key[i] = sw ? b : a;
+                    key[l] = sw ? a : b;
+                }
+            }
+    uint64_t mine = 0;
+    for (int k = 0; k < K; ++k) {
+        const uint64_t best = wave_max_u64(key[0]);
+        if (best == 0) break;   // nothing left: the remaining picks stay -1
+        const bool won = key[0] == best;
+#pragma unroll
+        for (int i = 0; i + 1 < NV; ++i) key[i] = won ? key[i + 1] : key[i];
+        key[NV - 1] = won ? 0 : key[NV - 1];
+        if (lane == k) mine = best;
+    }
+    const int myi = mine ? (int) ~(uint32_t) mine : -1;
+    const float myv = key_value(mine);
+    const float v0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(myv), 0));
+    const float ek = myi >= 0 ? expf(myv - v0) : 0.f;
+    float z = 0.f;
+    for (int k = 0; k < K; ++k) z += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ek), k));
+    pick = myi;
+    weight = myi < 0 ? 0.f : ek / z;
+}
+// E at run time (a multiple of 64, at most 1024): the smallest instantiation that holds E / 64 values a lane
+template <bool AGENT = false>
+__device__ inline void topk_wave_e(const float* lg, int E, int K, int lane, int& pick, float& weight) {
+    const int nv = E / WAVE;
+    if (nv <= 1) topk_wave<1, AGENT>(lg, nv, K, lane, pick, weight);
+    else if (nv <= 2) topk_wave<2, AGENT>(lg, nv, K, lane, pick, weight);
+    else if (nv <= 4) topk_wave<4, AGENT>(lg, nv, K, lane, pick, weight);
+    else if (nv <= 8) topk_wave<8, AGENT>(lg, nv, K, lane, pick, weight);
+    else topk_wave<16, AGENT>(lg, nv, K, lane, pick, weight);
+}
+
+// Decode jobs (src/moe.cuh:164-198, tools/kbench.cu:77-95): one job per distinct expert numbered in the order of each
+// expert's first pick, a job's rows in pair order.  Thread p < P (one per pick, blockDim.x >= P) learns its pick's
+// expert, its slot among the earlier picks of that expert, the expert's pick count and its job; returns the number of
+// routed jobs.  ex: the picks (LDS); first: P bytes of LDS; jobof: E ints of LDS.
+struct PickSlot {
+    int e = -1, slot = 0, cnt = 0, job = -1;
+};
+__device__ inline int pick_slots(const int* ex, int P, unsigned char* first, int* jobof, PickSlot& ps) {
+    const int p = threadIdx.x;
+    ps = PickSlot{};
+    if (p < P) {
+        ps.e = ex[p];
+        if (ps.e >= 0)
+            for (int q = 0; q < P; ++q) {
+                const bool same = ex[q] == ps.e;
+                ps.slot += same && q < p;
+                ps.cnt += same;
+            }
+        first[p] = ps.e >= 0 && ps.slot == 0;
+    }
+    __syncthreads();
+    if (p < P && first[p]) {
+        int j = 0;
+        for (int q = 0; q < p; ++q) j += first[q];
+        jobof[ps.e] = j;
+    }
+    int n = 0;
+    for (int q = 0; q < P; ++q) n += first[q];
+    __syncthreads();
+    if (p < P && ps.e >= 0) ps.job = jobof[ps.e];
+    return n;
+}
+
+}  // namespace sfnx

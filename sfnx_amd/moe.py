@@ -6,6 +6,7 @@ arguments here.  Errors from the library raise RuntimeError, as the reference's 
 """
 from __future__ import annotations
 
+import ctypes as C
 from dataclasses import dataclass
 
 import torch
@@ -95,6 +96,12 @@ def moe_down_big(A, sa, wtype, n_in, n_out, jobs, njobs, njobs_cap, gu, part) ->
 def moe_combine(part, topw, topi, logits, y, E: int, K: int, shared: bool = True) -> None:
     T, H = y.shape
     check(lib().sfnx_moe_combine(_p(part), _p(topw), _p(topi), _p(logits), _p(y), T, H, E, K, int(shared), _st()))
+
+
+def residual_rmsnorm(x, y, xn, eps: float = 1e-6) -> None:
+    """x += y (y may be None), xn = x / sqrt(mean(x^2) + eps): the glue between stacked layers"""
+    T, H = x.shape
+    check(lib().sfnx_residual_rmsnorm(_p(x), _p(y), _p(xn), T, H, eps, _st()))
 
 
 # ---------------------------------------------------------------------------------------------------- a layer
@@ -187,6 +194,41 @@ def decode_layer(L: MoeLayer, x: torch.Tensor, y: torch.Tensor, b: DecodeBuffers
     moe_gate_up(L.gu_w, L.gu_stride, s.wtype, s.H, 2 * s.ff, b.jobs_gu, b.njobs, b.njobs_max, T, b.xq, b.gu)
     moe_down(L.dn_w, L.dn_stride, s.wtype, s.ff, s.H, b.jobs_dn, b.njobs, b.njobs_max, T, b.gu, b.part)
     moe_combine(b.part, b.topw, b.topi, b.logits, y, s.E, s.K, s.shared)
+
+
+DECODE_PIECES = ["logits", "xq", "topi", "topw", "jobs_gu", "jobs_dn", "njobs", "gu", "hq_q", "hq_d", "hq_s", "y"]
+
+
+class FusedDecode:
+    """The fused decode path (sfnx_moe_decode): a window of up to T rows through a stack of layers, three launches a
+    layer; owns its workspace and the layer table."""
+
+    def __init__(self, layers: list, T: int, device="cuda"):
+        s = layers[0].s
+        self.s, self.T, self.layers = s, T, layers
+        off = (C.c_size_t * 13)()
+        total = lib().sfnx_moe_decode_workspace(T, s.H, s.E, s.K, s.ff, off)
+        self.off = list(off)
+        self.ws = torch.zeros(total, dtype=torch.uint8, device=device)
+        self.table = (_abi.LayerW * len(layers))(*[
+            _abi.LayerW(L.W.data_ptr(), L.gu_w.data_ptr(), L.gu_stride, L.dn_w.data_ptr(), L.dn_stride) for L in layers])
+
+    def __call__(self, x: torch.Tensor, norm: bool = True, eps: float = 1e-6, layer0: int = 0,
+                 n_layers: int | None = None, phases: int = 0) -> None:
+        s = self.s
+        n = len(self.layers) - layer0 if n_layers is None else n_layers
+        table = C.cast(self.table, C.c_void_p).value + layer0 * C.sizeof(_abi.LayerW)
+        check(lib().sfnx_moe_decode(table, n, s.wtype, s.H, s.E, s.K, s.ff, int(s.shared), _p(x), x.shape[0],
+                                    int(norm), eps, _p(self.ws), self.ws.numel(), phases, _st()))
+
+    def piece(self, name: str, dtype, shape) -> torch.Tensor:
+        """a view of one workspace piece (the last layer's value)"""
+        i = DECODE_PIECES.index(name)
+        n = 1
+        for d in shape:
+            n *= d
+        nbytes = n * torch.tensor([], dtype=dtype).element_size()
+        return self.ws[self.off[i]: self.off[i] + nbytes].view(dtype).view(*shape)
 
 
 class PrefillBuffers:

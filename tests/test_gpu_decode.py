@@ -1,0 +1,95 @@
+"""The fused decode path (sfnx_moe_decode: three launches a layer) against the unfused entry points (router_route,
+moe_gate_up, moe_down, moe_combine), bit for bit, and against the oracle within BASELINE's 2e-3."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from sfnx_amd import moe
+from tests.gpu_util import job_array, make_layer, max_rel
+
+pytestmark = pytest.mark.gpu
+
+
+def bits(t):
+    return t.detach().cpu().numpy().view(np.uint32)
+
+
+def unfused_chain(layers, x, norm, bufs):
+    """x += MoE(rmsnorm(x)) per layer with the unfused entry points; returns the last layer's y"""
+    xn = torch.empty_like(x)
+    y = torch.empty_like(x)
+    for L, b in zip(layers, bufs):
+        if norm:
+            moe.residual_rmsnorm(x, None, xn)
+        else:
+            xn.copy_(x)
+        moe.decode_layer(L, xn, y, b)
+        x.add_(y)
+    return y
+
+
+@pytest.mark.parametrize("wtype", [orc.Q4_K, orc.Q8_0])
+@pytest.mark.parametrize("T", [1, 3, 16])
+def test_fused_layer_equals_unfused(wtype, T):
+    shape = moe.LayerShape(H=1024, E=64, K=6, ff=512, wtype=wtype, shared=True)
+    L, host = make_layer(shape, 30 + T)
+    x0 = torch.from_numpy(orc.synth(T * shape.H, 800 + T, 1.0).reshape(T, shape.H)).cuda()
+    b = moe.DecodeBuffers(shape, T)
+    xu = x0.clone()
+    yu = unfused_chain([L], xu, False, [b])
+    f = moe.FusedDecode([L], T)
+    xf = x0.clone()
+    f(xf, norm=False)
+    torch.cuda.synchronize()
+    E1, K, P = shape.E + 1, shape.K, T * shape.K
+    assert np.array_equal(bits(f.piece("logits", torch.float32, (T, E1))), bits(b.logits))
+    assert np.array_equal(f.piece("topi", torch.int32, (T, K)).cpu().numpy(), b.topi.cpu().numpy())
+    assert np.array_equal(bits(f.piece("topw", torch.float32, (T, K))), bits(b.topw))
+    n = int(f.piece("njobs", torch.int32, (2,))[0])
+    assert n == int(b.njobs[0])
+    jf = job_array(f.piece("jobs_gu", torch.int32, (P + 1, 34)).reshape(-1))[:n]
+    ju = job_array(b.jobs_gu)[:n]
+    for a, c in zip(jf, ju):
+        assert a["w"] == c["w"] and a["n"] == c["n"]
+        assert np.array_equal(a["y"][: a["n"]], c["y"][: c["n"]]) and np.array_equal(a["out"][: a["n"]], c["out"][: c["n"]])
+    rows = [p for p in range(P) if b.topi.reshape(-1)[p] >= 0] + list(range(P, P + T))
+    gf = f.piece("gu", torch.float32, (P + T, 2 * shape.ff))
+    assert np.array_equal(bits(gf[rows]), bits(b.gu[rows]))
+    assert np.array_equal(bits(f.piece("y", torch.float32, (T, shape.H))), bits(yu))
+    assert np.array_equal(bits(xf), bits(xu))
+    # and the oracle
+    oy = orc.layer_decode(host, x0.cpu().numpy())[0]
+    assert max_rel(yu.cpu().numpy(), oy) < 2e-3
+
+
+@pytest.mark.parametrize("wtype", [orc.Q4_K, orc.Q8_0])
+def test_fused_chain_with_norm_equals_unfused(wtype):
+    shape = moe.LayerShape(H=2048, E=512, K=10, ff=512, wtype=wtype, shared=True)
+    layers = [moe.MoeLayer.synthetic(shape, seed=50 + i) for i in range(3)]
+    for T in (1, 16):
+        x0 = torch.from_numpy(orc.synth(T * shape.H, 900 + T, 1.0).reshape(T, shape.H)).cuda()
+        xu = x0.clone()
+        yu = unfused_chain(layers, xu, True, [moe.DecodeBuffers(shape, T) for _ in layers])
+        f = moe.FusedDecode(layers, T)
+        xf = x0.clone()
+        f(xf, norm=True)
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(f.piece("y", torch.float32, (T, shape.H))), bits(yu))
+        assert np.array_equal(bits(xf), bits(xu))
+        # graph capture and replay give the same result, replay after replay
+        xg = x0.clone()
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            f(xg, norm=True)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g):
+            f(xg, norm=True)
+        for _ in range(3):
+            xg.copy_(x0)
+            g.replay()
+            torch.cuda.synchronize()
+            assert np.array_equal(bits(xg), bits(xu))
