@@ -168,47 +168,55 @@ def zipf_bias(E):
 
 
 def bench_prefill(L, s, moe, torch, C=2048, reps=10):
-    """config 3: 2048 tokens through layer 0, a seeded Zipf(1.1) bias on the routed logits; the expert kernels timed"""
+    """config 3: 2048 tokens through layer 0, a seeded Zipf(1.1) bias on the routed logits; the routed + shared experts
+    on the matrix cores (f16 MFMA, the reference's default prompt arithmetic) and on the int8 dot kernels (q8_1)"""
     dev = "cuda"
     x = torch.empty((C, s.H), dtype=torch.float32, device=dev)
     moe.synth_normal(x, 777, 1.0)
     xn = torch.empty_like(x)
     moe.residual_rmsnorm(x, None, xn)
+    y = torch.empty_like(x)
     b = moe.PrefillBuffers(s, C)
     bias = torch.from_numpy(zipf_bias(s.E)).to(dev)
+    moe.prefill_route(L, xn, b, bias)
     moe.quantize_q8_1(xn, b.xq)
-    moe.router_logits(L.W, xn, b.logits)
-    b.logits[:, : s.E] += bias
-    moe.pf_route(b.logits, b.topi, b.topw, b.cnt, b.jbase, b.jobs_gu, b.jobs_dn, b.njobs, s.E, s.K, s.shared)
+    moe.to_f16(xn, b.xh)
     torch.cuda.synchronize()
     cnt = b.cnt.cpu()
-    gu_call = lambda: moe.moe_gate_up_big(L.gu_w, L.gu_stride, s.wtype, s.H, 2 * s.ff, b.jobs_gu, b.njobs, b.cap, b.xq, b.gu)
-    dn_call = lambda: moe.moe_down_big(L.dn_w, L.dn_stride, s.wtype, s.ff, s.H, b.jobs_dn, b.njobs, b.cap, b.gu, b.part)
-    for _ in range(2):
-        gu_call()
-        dn_call()
-    torch.cuda.synchronize()
-    e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
-    e[0].record()
-    for _ in range(reps):
-        gu_call()
-    e[1].record()
-    for _ in range(reps):
-        dn_call()
-    e[2].record()
-    torch.cuda.synchronize()
-    t_gu = e[0].elapsed_time(e[1]) / reps * 1e3
-    t_dn = e[1].elapsed_time(e[2]) / reps * 1e3
+    calls = {
+        "mma_gate_up": lambda: moe.moe_gate_up_mma(L.gu_w, L.gu_stride, s.wtype, s.H, 2 * s.ff, b.jobs_gu, b.njobs, b.cap,
+                                                   b.xh, b.gu),
+        "swiglu_h16": lambda: moe.swiglu_h16(b.gu, b.h16, s.ff),
+        "mma_down": lambda: moe.moe_down_mma(L.dn_w, L.dn_stride, s.wtype, s.ff, s.H, b.jobs_dn, b.njobs, b.cap, b.h16,
+                                             b.part),
+        "q8_gate_up": lambda: moe.moe_gate_up_big(L.gu_w, L.gu_stride, s.wtype, s.H, 2 * s.ff, b.jobs_gu, b.njobs, b.cap,
+                                                  b.xq, b.gu),
+        "q8_down": lambda: moe.moe_down_big(L.dn_w, L.dn_stride, s.wtype, s.ff, s.H, b.jobs_dn, b.njobs, b.cap, b.gu, b.part),
+    }
+    us = {}
+    for name, c in calls.items():
+        c()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            c()
+        e1.record()
+        torch.cuda.synchronize()
+        us[name] = e0.elapsed_time(e1) / reps * 1e3
     P = C * s.K
-    ops = 2 * (P + C) * (2 * s.ff * s.H + s.H * s.ff)   # 2 ops per multiply-add, routed + shared pairs
+    flops = 2 * (P + C) * (2 * s.ff * s.H + s.H * s.ff)   # 2 per multiply-add, routed + shared pairs
     touched = int((cnt > 0).sum()) + 1
     wbytes = touched * expert_bytes(s, moe)
-    t = (t_gu + t_dn) * 1e-6
-    return {"workload": "config 3: 2048 tokens, Zipf(1.1)-skewed routing, Q4_K experts, q8_1 int8-dot BigJob kernels",
-            "us_gate_up": round(t_gu, 1), "us_down": round(t_dn, 1), "tops": round(ops / t / 1e12, 2),
-            "int8_peak_frac": round(ops / t / 1e12 / INT8_MFMA_PEAK_TOPS, 4),
-            "weight_gbs": round(wbytes / t / 1e9, 1), "hbm_frac": round(wbytes / t / 1e9 / HBM_PEAK_GBS, 4),
-            "experts_touched": touched, "max_rows_per_expert": int(cnt.max()), "ops": ops}
+    t_mma = (us["mma_gate_up"] + us["swiglu_h16"] + us["mma_down"]) * 1e-6
+    t_q8 = (us["q8_gate_up"] + us["q8_down"]) * 1e-6
+    return {"workload": "config 3: 2048 tokens, Zipf(1.1)-skewed routing (max rows/expert ~200), Q4_K experts + shared",
+            "us": {k: round(v, 1) for k, v in us.items()},
+            "tflops": round(flops / t_mma / 1e12, 1), "f16_mfma_peak_frac": round(flops / t_mma / 1e12 / F16_MFMA_PEAK_TFLOPS, 4),
+            "int8_peak_frac_equiv": round(flops / t_mma / 1e12 / INT8_MFMA_PEAK_TOPS, 4),
+            "weight_gbs": round(wbytes / t_mma / 1e9, 1), "hbm_frac": round(wbytes / t_mma / 1e9 / HBM_PEAK_GBS, 4),
+            "q8_dot_tops": round(flops / t_q8 / 1e12, 2),
+            "experts_touched": touched, "max_rows_per_expert": int(cnt.max()), "flops": flops, "weight_bytes": wbytes}
 
 
 def cpu_baseline(L, s, moe, torch, x0, seconds):

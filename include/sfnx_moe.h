@@ -110,6 +110,20 @@ int sfnx_moe_down_big(const void* A, size_t sa, uint32_t type, int n_in, int n_o
 int sfnx_moe_combine(const float* part, const float* topw, const int* topi, const float* logits, float* y, int T, int H,
                      int E, int K, int shared, void* st);
 
+/* ---------------------------------------------------------------------------------------------- matrix cores */
+/* src/kernels.hpp:290-292 moe_gate_up_mma / swiglu_h16 / moe_down_mma: the prompt path's experts as f16 x f16 products
+ * with fp32 accumulation on MFMA (src/moe_mma.cuh): weights dequantized to f16 as the reference does (Q4_K:
+ * hfma2(q, f16(d sc), f16(-(dmin m))); Q8_0: hmul2(q, d)), activations f16 rows (xh: [tokens][n_in]; h16: [pairs][ff]).
+ * out[job.out[m]][r] for r < n_out (a multiple of 256), jobs [0, *njobs) of at most njobs_cap. */
+int sfnx_moe_gate_up_mma(const void* A, size_t sa, uint32_t type, int n_in, int n_out, const sfnx_bigjob* jobs,
+                         const int* njobs, int njobs_cap, const uint16_t* xh, float* gu, void* st);
+int sfnx_swiglu_h16(const float* gu, int ffs, int P, uint16_t* h16, void* st);
+int sfnx_moe_down_mma(const void* A, size_t sa, uint32_t type, int n_in, int n_out, const sfnx_bigjob* jobs,
+                      const int* njobs, int njobs_cap, const uint16_t* h16, float* part, void* st);
+/* fp32 -> f16 (round to nearest even), n values: the activations the matrix-core path reads (the reference's hc read
+ * writes them, src/prefill.cu:1160) */
+int sfnx_to_f16(const float* x, uint16_t* y, size_t n, void* st);
+
 /* ---------------------------------------------------------------------------------------------- fused decode */
 /* one layer's weights: router W [E + 1][H] fp32 (row E gates the shared expert), planar gate|up experts (E + 1 of
  * [2 ff][H], the shared expert last) and planar down experts (E + 1 of [H][ff]) */

@@ -93,6 +93,22 @@ def moe_down_big(A, sa, wtype, n_in, n_out, jobs, njobs, njobs_cap, gu, part) ->
     check(lib().sfnx_moe_down_big(_p(A), sa, wtype, n_in, n_out, _p(jobs), _p(njobs), njobs_cap, _p(gu), _p(part), _st()))
 
 
+def moe_gate_up_mma(A, sa, wtype, n_in, n_out, jobs, njobs, njobs_cap, xh, gu) -> None:
+    check(lib().sfnx_moe_gate_up_mma(_p(A), sa, wtype, n_in, n_out, _p(jobs), _p(njobs), njobs_cap, _p(xh), _p(gu), _st()))
+
+
+def swiglu_h16(gu, h16, ff: int) -> None:
+    check(lib().sfnx_swiglu_h16(_p(gu), ff, gu.shape[0], _p(h16), _st()))
+
+
+def moe_down_mma(A, sa, wtype, n_in, n_out, jobs, njobs, njobs_cap, h16, part) -> None:
+    check(lib().sfnx_moe_down_mma(_p(A), sa, wtype, n_in, n_out, _p(jobs), _p(njobs), njobs_cap, _p(h16), _p(part), _st()))
+
+
+def to_f16(x, y) -> None:
+    check(lib().sfnx_to_f16(_p(x), _p(y), x.numel(), _st()))
+
+
 def moe_combine(part, topw, topi, logits, y, E: int, K: int, shared: bool = True) -> None:
     T, H = y.shape
     check(lib().sfnx_moe_combine(_p(part), _p(topw), _p(topi), _p(logits), _p(y), T, H, E, K, int(shared), _st()))
@@ -252,6 +268,29 @@ class PrefillBuffers:
         self.njobs = torch.zeros(2, **i32)
         self.gu = torch.zeros((NP, 2 * s.ff), dtype=torch.float32, device=device)
         self.part = torch.zeros((NP, s.H), dtype=torch.float32, device=device)
+        self.xh = torch.zeros((C, s.H), dtype=torch.float16, device=device)
+        self.h16 = torch.zeros((NP, s.ff), dtype=torch.float16, device=device)
+
+
+def prefill_route(L: "MoeLayer", x: torch.Tensor, b: "PrefillBuffers", bias: torch.Tensor | None = None) -> None:
+    """the prompt path's routing: router logits, an optional bias on the routed logits (the benchmark's skew), then
+    top-k and the BigJob permutation (src/prefill.cu:1163-1167)"""
+    s = L.s
+    router_logits(L.W, x, b.logits)
+    if bias is not None:
+        b.logits[:, : s.E] += bias
+    pf_route(b.logits, b.topi, b.topw, b.cnt, b.jbase, b.jobs_gu, b.jobs_dn, b.njobs, s.E, s.K, s.shared)
+
+
+def prefill_experts_mma(L: "MoeLayer", x: torch.Tensor, y: torch.Tensor, b: "PrefillBuffers") -> None:
+    """the routed experts on the matrix cores after prefill_route: f16 activations, gate|up, SwiGLU to f16, down, the
+    combine (the reference's default prompt path, src/prefill.cu:1167-1171)"""
+    s = L.s
+    to_f16(x, b.xh)
+    moe_gate_up_mma(L.gu_w, L.gu_stride, s.wtype, s.H, 2 * s.ff, b.jobs_gu, b.njobs, b.cap, b.xh, b.gu)
+    swiglu_h16(b.gu, b.h16, s.ff)
+    moe_down_mma(L.dn_w, L.dn_stride, s.wtype, s.ff, s.H, b.jobs_dn, b.njobs, b.cap, b.h16, b.part)
+    moe_combine(b.part, b.topw, b.topi, b.logits, y, s.E, s.K, s.shared)
 
 
 def prefill_layer_q8(L: MoeLayer, x: torch.Tensor, y: torch.Tensor, b: PrefillBuffers) -> None:

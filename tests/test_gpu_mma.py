@@ -1,0 +1,98 @@
+"""The matrix-core prompt path (moe_gate_up_mma, swiglu_h16, moe_down_mma) against float64 products of the f16
+weights and f16 activations, sampled as tools/moe_mma_bench.cu:197-220 samples them (max error over the sample's largest
+value), and the whole f16 layer against a float64 restatement of it.  Tolerance: BASELINE's 2e-3 (fp32 accumulation
+measures ~1e-6 here)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from sfnx_amd import moe
+from tests.gpu_util import job_array, make_layer, max_rel
+
+pytestmark = pytest.mark.gpu
+
+
+def f16_of(a):
+    return np.asarray(a, np.float32).astype(np.float16)
+
+
+def expert_rows(host, e, down):
+    rb = orc.row_bytes(host.type, host.ff if down else host.H)
+    if down:
+        return host.dn_w[e * host.dn_stride:(e + 1) * host.dn_stride], rb
+    return host.gu_w[e * host.gu_stride:(e + 1) * host.gu_stride], rb
+
+
+def run_prefill(shape, seed, C, dup=False, bias=None):
+    L, host = make_layer(shape, seed)
+    x = orc.synth(C * shape.H, seed + 7, 1.0).reshape(C, shape.H)
+    if dup:
+        x[40:140] = x[39]   # one token 100 times: its experts' jobs fill all 64 rows
+    xd = torch.from_numpy(x).cuda()
+    y = torch.empty_like(xd)
+    b = moe.PrefillBuffers(shape, C)
+    moe.prefill_route(L, xd, b, None if bias is None else torch.from_numpy(bias).cuda())
+    moe.prefill_experts_mma(L, xd, y, b)
+    torch.cuda.synchronize()
+    return L, host, x, y.cpu().numpy(), b
+
+
+def check_sampled(host, x, b, nsample, rng):
+    s = host
+    topi = b.topi.cpu().numpy()
+    C, K = topi.shape
+    P = C * K
+    gu = b.gu.cpu().numpy()
+    h16 = b.h16.cpu().numpy()
+    part = b.part.cpu().numpy()
+    x16 = f16_of(x)
+    eg, mg, ed, md = 0.0, 0.0, 0.0, 0.0
+    for _ in range(nsample):
+        p = int(rng.integers(0, P + C))
+        if p < P:
+            e, t = int(topi.reshape(-1)[p]), p // K
+        else:
+            e, t = s.E, p - P
+        w, rb = expert_rows(host, e, False)
+        ref = orc.mma_matvec(s.type, w, s.H, 2 * s.ff, x16[t].view(np.uint16))
+        mg = max(mg, np.abs(ref).max())
+        eg = max(eg, np.abs(ref - gu[p]).max())
+        wd, _ = expert_rows(host, e, True)
+        refd = orc.mma_matvec(s.type, wd, s.ff, s.H, h16[p].view(np.uint16))
+        md = max(md, np.abs(refd).max())
+        ed = max(ed, np.abs(refd - part[p]).max())
+        # h16 is f16(silu(g) u) of the kernel's own gate|up row
+        hh = orc.swiglu_h16(gu[p], s.ff).view(np.float16).astype(np.float32)
+        assert np.max(np.abs(hh - h16[p].astype(np.float32))) <= 2 ** -10 * np.max(np.abs(hh)) + 1e-7
+    return eg / mg, ed / md
+
+
+@pytest.mark.parametrize("wtype", [orc.Q4_K, orc.Q8_0])
+def test_mma_small_layer_with_full_jobs(wtype):
+    shape = moe.LayerShape(H=1024, E=64, K=6, ff=512, wtype=wtype, shared=True)
+    L, host, x, y, b = run_prefill(shape, 70 + wtype, 200, dup=True)
+    assert int(b.cnt.max()) > 64          # some experts split over several 64-row jobs
+    jobs = job_array(b.jobs_gu, True)[: int(b.njobs[0])]
+    assert (jobs["n"] == 64).any() and (jobs["n"] < 33).any()
+    eg, ed = check_sampled(host, x, b, 40, np.random.default_rng(1))
+    assert eg < 2e-3 and ed < 2e-3, (eg, ed)
+    # the layer: the combine of the kernel's own rows
+    topi, topw = b.topi.cpu().numpy(), b.topw.cpu().numpy().astype(np.float64)
+    part = b.part.cpu().numpy().astype(np.float64)
+    C, K = topi.shape
+    lg = b.logits.cpu().numpy()
+    sig = 1 / (1 + np.exp(-lg[:, shape.E].astype(np.float64)))
+    want = np.einsum("tk,tkh->th", topw, part[: C * K].reshape(C, K, -1)) + sig[:, None] * part[C * K:]
+    assert max_rel(y, want) < 1e-5
+
+
+def test_mma_baseline_prefill_shape():
+    """2048 tokens, hidden 2048, 512 experts x FF 512, top-10 + shared, Zipf-skewed routing"""
+    shape = moe.LayerShape(H=2048, E=512, K=10, ff=512, wtype=orc.Q4_K, shared=True)
+    rank = np.random.default_rng(7).permutation(512) + 1
+    bias = (0.125 * -1.1 * np.log(rank)).astype(np.float32)
+    L, host, x, y, b = run_prefill(shape, 3, 2048, bias=bias)
+    assert 150 < int(b.cnt.max()) < 260
+    eg, ed = check_sampled(host, x, b, 24, np.random.default_rng(2))
+    assert eg < 2e-3 and ed < 2e-3, (eg, ed)
