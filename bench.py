@@ -43,6 +43,9 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="only copy 1 GiB device-to-device 3 times: the known-size kernel that scales rocprofv3's "
+                         "FETCH_SIZE / WRITE_SIZE to bytes")
     return ap.parse_args()
 
 
@@ -58,6 +61,14 @@ def main():
         return 2
     import torch
 
+    if args.copy_calib:
+        a = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calib_bytes_per_copy": a.numel() * 4}), flush=True)
+        return 0
     from sfnx_amd import moe
 
     torch.cuda.set_device(0)
@@ -104,29 +115,30 @@ def main():
     gbs = bytes_tl * NL / (ms_step * 1e-3) / 1e9
     log(f"decode: {ms_step:.3f} ms/step, {us_tl:.2f} us/token-layer, {gbs:.0f} GB/s")
 
-    # ------------------------------------------------------------------ each kernel alone (HIP events, launch stream)
-    names = {1: "k_dec_router", 2: "k_dec_experts", 4: "k_dec_down"}
-    alg = {1: (s.E + 1) * s.H * 4, 2: (s.K + 1) * 2 * s.ff * moe.row_bytes(s.wtype, s.H),
-           4: (s.K + 1) * s.H * moe.row_bytes(s.wtype, s.ff)}
-    tot = {k: 0.0 for k in names}
+    # ------------------------------------------------------------------ each kernel's own duration
+    # The library's kernel clock launches each decode kernel with a start/stop event pair on the launch stream that
+    # the runtime stamps at that dispatch's begin and end (hipExtLaunchKernel), so a duration excludes launch gaps
+    # and agrees with rocprofv3's kernel trace.  One eager pass over the 48 layers, 3 repetitions.
+    names = ["k_dec_router", "k_dec_experts", "k_dec_down"]
+    alg = [(s.E + 1) * s.H * 4, (s.K + 1) * 2 * s.ff * moe.row_bytes(s.wtype, s.H),
+           (s.K + 1) * s.H * moe.row_bytes(s.wtype, s.ff)]
     reps = 3
-    evs = []
-    for _ in range(reps):
-        x.copy_(x0)
-        for l in range(NL):
-            for ph in (1, 2, 4):
-                a, z = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                a.record()
-                f(x, layer0=l, n_layers=1, phases=ph)
-                z.record()
-                evs.append((ph, a, z))
-    torch.cuda.synchronize()
-    for ph, a, z in evs:
-        tot[ph] += a.elapsed_time(z) * 1000
-    avg_us = {names[k]: tot[k] / (reps * NL) for k in names}
-    dom = max(names, key=lambda k: tot[k])
-    ach = alg[dom] / (tot[dom] / (reps * NL) * 1e-6) / 1e9
-    log("per-kernel avg us (eager, events around each launch): " + ", ".join(f"{n} {v:.2f}" for n, v in avg_us.items()))
+    tot = [0.0, 0.0, 0.0]
+    moe.kernel_clock(True)
+    try:
+        for _ in range(reps):
+            x.copy_(x0)
+            for l in range(NL):
+                f(x, layer0=l, n_layers=1)
+                for i, v in enumerate(moe.kernel_clock_read()):
+                    tot[i] += v
+    finally:
+        moe.kernel_clock(False)
+    avg_us = {names[i]: tot[i] / (reps * NL) for i in range(3)}
+    dom = max(range(3), key=lambda i: tot[i])
+    ach = alg[dom] / (avg_us[names[dom]] * 1e-6) / 1e9
+    traffic = measured_traffic(names[dom])
+    log("per-kernel avg us (dispatch-stamped events): " + ", ".join(f"{n} {v:.2f}" for n, v in avg_us.items()))
 
     out = {
         "metric": "Q4_K MoE-layer µs/token + HBM GB/s (decode); TFLOPS at 2k-token prefill",
@@ -150,7 +162,7 @@ def main():
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "kernel_avg_us": {n: round(v, 3) for n, v in avg_us.items()},
         "roofline": {"kernel": names[dom], "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "algorithmic_bytes_per_launch": alg[dom]},
     }
     if not args.no_prefill:
@@ -159,6 +171,19 @@ def main():
         out["cpu_baseline"] = cpu_baseline(layers[0], s, moe, torch, x0, args.cpu_seconds)
     print(json.dumps(out), flush=True)
     return 0
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` on this workload, from the rocprofv3 FETCH_SIZE / WRITE_SIZE passes recorded
+    in profiles/traffic.txt (each counter scaled by what it reads for a copy of known size), or None"""
+    p = ROOT / "profiles" / "traffic.txt"
+    if not p.exists():
+        return None
+    for line in p.read_text().splitlines():
+        f = line.split()
+        if len(f) == 4 and f[0] == "traffic" and f[1] == kernel:
+            return int(float(f[2]) + float(f[3]))
+    return None
 
 
 def zipf_bias(E):

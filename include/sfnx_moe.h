@@ -156,6 +156,13 @@ int sfnx_moe_decode(const sfnx_moe_layer_w* layers, int n_layers, uint32_t type,
  * xn = x / sqrt(mean(x^2) + eps) per row of H */
 int sfnx_residual_rmsnorm(float* x, const float* y, float* xn, int T, int H, float eps, void* st);
 
+/* Measurement hook (no reference counterpart: for benchmarks that need each kernel's own duration).  While enabled,
+ * sfnx_moe_decode launches its three kernels with start/stop events that the runtime stamps at the dispatch's
+ * begin and end; sfnx_kernel_clock_read waits for the last such launches and writes their durations in us
+ * (router, gate|up, down + combine) to us[3].  Process-wide; not for concurrent callers. */
+int sfnx_kernel_clock(int enable);
+int sfnx_kernel_clock_read(float* us);
+
 #ifdef __cplusplus
 }
 #endif

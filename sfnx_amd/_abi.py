@@ -40,6 +40,8 @@ SIGNATURES = {
     "sfnx_moe_down_big": (i32, [vp, sz, u32, i32, i32, vp, vp, i32, vp, vp, vp]),
     "sfnx_moe_combine": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp]),
     "sfnx_residual_rmsnorm": (i32, [vp, vp, vp, i32, i32, f32, vp]),
+    "sfnx_kernel_clock": (i32, [i32]),
+    "sfnx_kernel_clock_read": (i32, [vp]),
     "sfnx_moe_gate_up_mma": (i32, [vp, sz, u32, i32, i32, vp, vp, i32, vp, vp, vp]),
     "sfnx_swiglu_h16": (i32, [vp, i32, i32, vp, vp]),
     "sfnx_moe_down_mma": (i32, [vp, sz, u32, i32, i32, vp, vp, i32, vp, vp, vp]),

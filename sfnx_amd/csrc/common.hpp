@@ -32,6 +32,9 @@ template <typename F> int guarded(const char* what, F&& f) {
 inline void require(bool ok, const char* msg) {
     if (!ok) throw std::runtime_error(msg);
 }
+inline void check(hipError_t e, const char* what) {
+    if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
 inline hipStream_t stream_of(void* st) { return reinterpret_cast<hipStream_t>(st); }
 
 // ------------------------------------------------------------------------------------------------ device helpers

@@ -11,6 +11,7 @@
 //
 // The arithmetic of every value is the unfused entry points' (router_route, moe_gate_up, moe_down, moe_combine), so the
 // two paths agree bit for bit.
+#include <hip/hip_ext.h>
 #include "mv.hpp"
 #ifdef SFNX_PHASE_PROF
 #define SFNX_TOPK_STAMP if (lane == 0 && blockIdx.x == 0) { uint64_t sink = 0; for (int i = 0; i < NV; ++i) sink += key[i]; if (sink == 12345) key[0] = 0; g_prof_topk = wall_clock64(); }
@@ -396,16 +397,32 @@ struct DecArgs {
     int phases;
 };
 
+// Optional kernel clock: when on, each decode kernel is launched with a start/stop event pair that the runtime
+// stamps at that dispatch's own begin and end, so the elapsed time is the kernel's duration (no launch gaps).
+struct KernelClock {
+    bool on = false;
+    hipEvent_t a[3]{}, b[3]{};
+};
+KernelClock g_clock;
+
+template <typename F, typename... A>
+void launch(int idx, F kern, dim3 grid, dim3 block, size_t shmem, hipStream_t s, A... args) {
+    if (g_clock.on)
+        hipExtLaunchKernelGGL(kern, grid, block, (uint32_t) shmem, s, g_clock.a[idx], g_clock.b[idx], 0, args...);
+    else
+        hipLaunchKernelGGL(kern, grid, block, shmem, s, args...);
+}
+
 template <int NC, int TT>
 void launch_k1(const DecArgs& d, const sfnx_moe_layer_w& w, float* x, const DecLayout& L, char* ws, hipStream_t s) {
     const int rows = d.E + 1;
-    k_dec_router<NC, TT><<<(rows + D1_WAVES - 1) / D1_WAVES, D1_THREADS, 0, s>>>(
+    launch(0, k_dec_router<NC, TT>, dim3((rows + D1_WAVES - 1) / D1_WAVES), dim3(D1_THREADS), 0, s,
         w.W, x, d.T, d.E, d.eps, d.norm, (float*) (ws + L.logits), (uint8_t*) (ws + L.xq));
 }
 template <int TYPE, int G, int TT>
 void launch_k2(const DecArgs& d, const sfnx_moe_layer_w& w, const DecLayout& L, char* ws, hipStream_t s) {
     const int njmax = d.T * d.K + (d.shared ? 1 : 0);
-    k_dec_experts<TYPE, G, TT><<<njmax * (d.ff / 32), d2_threads<TYPE>(), acts_bytes(TT, d.H), s>>>(
+    launch(1, k_dec_experts<TYPE, G, TT>, dim3(njmax * (d.ff / 32)), dim3(d2_threads<TYPE>()), acts_bytes(TT, d.H), s,
         (const uint8_t*) w.gu, w.gu_stride, d.T, d.H, d.E, d.K, d.ff, d.shared, (const float*) (ws + L.logits),
         (const uint8_t*) (ws + L.xq), (int*) (ws + L.topi), (float*) (ws + L.topw), (sfnx_job*) (ws + L.jg),
         (sfnx_job*) (ws + L.jd), (int*) (ws + L.njobs), (float*) (ws + L.gu), (int8_t*) (ws + L.hq_q),
@@ -416,7 +433,7 @@ void launch_k3(const DecArgs& d, const sfnx_moe_layer_w& w, float* x, const DecL
     const int NP = d.T * d.K + d.T;
     const size_t hq_lds = acts_bytes(NP, d.ff);
     const bool staged = hq_lds <= 32 * 1024;
-    k_dec_down<TYPE, G2, NB><<<d.H / D3_ROWS, D3_THREADS, staged ? hq_lds : 0, s>>>(
+    launch(2, k_dec_down<TYPE, G2, NB>, dim3(d.H / D3_ROWS), dim3(D3_THREADS), staged ? hq_lds : 0, s,
         (const uint8_t*) w.dn, w.dn_stride, d.T, d.H, d.E, d.K, d.ff, d.shared, (const float*) (ws + L.logits),
         (const int*) (ws + L.topi), (const float*) (ws + L.topw), (const sfnx_job*) (ws + L.jd), (const int*) (ws + L.njobs),
         (const int8_t*) (ws + L.hq_q), (const float*) (ws + L.hq_d), (const int*) (ws + L.hq_s), (float*) (ws + L.y), x,
@@ -468,6 +485,29 @@ extern "C" int sfnx_prof_read(unsigned long long* out) {
     return hipMemcpyFromSymbol(out + 128, HIP_SYMBOL(g_prof_topk), 8) == hipSuccess ? 0 : -1;
 }
 #endif
+
+extern "C" int sfnx_kernel_clock(int enable) {
+    return guarded("sfnx_kernel_clock", [&] {
+        if (enable && !g_clock.a[0])
+            for (int i = 0; i < 3; ++i) {
+                check(hipEventCreate(&g_clock.a[i]), "hipEventCreate");
+                check(hipEventCreate(&g_clock.b[i]), "hipEventCreate");
+            }
+        g_clock.on = enable != 0;
+    });
+}
+
+extern "C" int sfnx_kernel_clock_read(float* us) {
+    return guarded("sfnx_kernel_clock_read", [&] {
+        require(g_clock.a[0] != nullptr && us != nullptr, "kernel clock never enabled");
+        for (int i = 0; i < 3; ++i) {
+            check(hipEventSynchronize(g_clock.b[i]), "hipEventSynchronize");
+            float ms = 0.f;
+            check(hipEventElapsedTime(&ms, g_clock.a[i], g_clock.b[i]), "hipEventElapsedTime");
+            us[i] = ms * 1000.f;
+        }
+    });
+}
 
 extern "C" size_t sfnx_moe_decode_workspace(int T, int H, int E, int K, int ff, size_t* offsets) {
     const DecLayout L = dec_layout(T, H, E, K, ff);

@@ -120,6 +120,18 @@ def residual_rmsnorm(x, y, xn, eps: float = 1e-6) -> None:
     check(lib().sfnx_residual_rmsnorm(_p(x), _p(y), _p(xn), T, H, eps, _st()))
 
 
+def kernel_clock(enable: bool) -> None:
+    """stamp each decode kernel's own begin/end (a measurement aid; see kernel_clock_read)"""
+    check(lib().sfnx_kernel_clock(int(enable)))
+
+
+def kernel_clock_read() -> list:
+    """durations in us of the last clocked decode launches: [router, gate|up, down + combine]"""
+    us = (C.c_float * 3)()
+    check(lib().sfnx_kernel_clock_read(C.cast(us, C.c_void_p)))
+    return list(us)
+
+
 # ---------------------------------------------------------------------------------------------------- a layer
 @dataclass
 class LayerShape:
