@@ -1,4 +1,4 @@
-"""Benchmark of the quantized MoE hot path on one MI355X (BASELINE.json metric and configs).
+"""Benchmark of the quantized MoE hot path on one MI355X: Q4_K MoE-layer us/token + HBM GB/s (decode), TFLOPS at a 2k-token prefill.
 
 Headline (value): config 1, Q4_K decode at batch 1 through 48 stacked MoE layers (hidden 2048, 512 experts x FF 512,
 top-10 + shared; each layer's weights seeded independently, 0.908 GB a layer resident in HBM), one token per step.
@@ -57,7 +57,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: every GPU box here has one, and no multi-GPU path is "
-                                   "built (DESIGN.md describes how the path would shard)", "n_gpus": args.gpus}))
+                                   "built (the path would shard by experts or by FF slices; this bench measures one GPU's share)", "n_gpus": args.gpus}))
         return 2
     import torch
 

@@ -1,5 +1,5 @@
 """The fused decode path (sfnx_moe_decode: three launches a layer) against the unfused entry points (router_route,
-moe_gate_up, moe_down, moe_combine), bit for bit, and against the oracle within BASELINE's 2e-3."""
+moe_gate_up, moe_down, moe_combine), bit for bit, and against the oracle within max relative error 2e-3."""
 import numpy as np
 import pytest
 import torch

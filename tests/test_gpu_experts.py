@@ -2,7 +2,7 @@
 
 Bit-exact: gate|up outputs (integer dots and the fp32 combine in the oracle's order), top-k indices, jobs.
 Within tolerance: down outputs and the layer output, because silu / sigmoid / softmax use the device's expf where the
-oracle uses libm's (the reference itself uses fast-math __expf); the bar is BASELINE's max relative error 2e-3,
+oracle uses libm's (the reference itself uses fast-math __expf); the bar is a max relative error of 2e-3 (fp32 accumulation),
 measured as max |err| / max |ref| over each output.
 """
 import numpy as np
@@ -68,7 +68,7 @@ def test_prefill_q8_layer(wtype):
 
 @pytest.mark.parametrize("wtype", [orc.Q4_K, orc.Q8_0])
 def test_decode_layer_baseline_shapes(wtype):
-    """BASELINE config 0/1/4: hidden 2048, 512 experts x FF 512, top-10 + shared, one token and a 16-row window"""
+    """The benchmark layer shape (configs 0/1/4): hidden 2048, 512 experts x FF 512, top-10 + shared, one token and a 16-row window"""
     shape = moe.LayerShape(H=2048, E=512, K=10, ff=512, wtype=wtype, shared=True)
     L, host = make_layer(shape, 1)
     for T in (1, 16):
