@@ -41,21 +41,51 @@ inline hipStream_t stream_of(void* st) { return reinterpret_cast<hipStream_t>(st
 __device__ __forceinline__ float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
 __device__ __forceinline__ uint16_t f2h(float f) { return __half_as_ushort(__float2half_rn(f)); }
 
-// lanes xor-reduced within groups of G (G a power of two <= 64): the tree every lane of a group ends with
-template <int G> __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int o = G / 2; o; o >>= 1) v += __shfl_xor(v, o);
+// the value of lane (this lane xor O), O a power of two below 64, without the LDS crossbar: DPP quad permutes for 1
+// and 2, row shifts for 4, a row rotation for 8, and gfx950's permlane swaps across rows for 16 and 32
+template <int CTRL, int ROWS = 0xf> __device__ __forceinline__ int dpp_mov(int v) {
+    return __builtin_amdgcn_update_dpp(v, v, CTRL, ROWS, 0xf, false);
+}
+template <int O> __device__ __forceinline__ int lane_xor(int v) {
+    if constexpr (O == 1) {
+        return dpp_mov<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+    } else if constexpr (O == 2) {
+        return dpp_mov<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+    } else if constexpr (O == 4) {
+        const int up = dpp_mov<0x104>(v), down = dpp_mov<0x114>(v);   // row_shl:4 (lane + 4), row_shr:4 (lane - 4)
+        return (__lane_id() & 4) ? down : up;
+    } else if constexpr (O == 8) {
+        return dpp_mov<0x128>(v);   // row_ror:8
+    } else if constexpr (O == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap((unsigned) v, (unsigned) v, false, false);
+        return (int) ((__lane_id() & 16) ? r[0] : r[1]);
+    } else {
+        static_assert(O == 32, "lane_xor: O in 1 .. 32");
+        const auto r = __builtin_amdgcn_permlane32_swap((unsigned) v, (unsigned) v, false, false);
+        return (int) ((__lane_id() & 32) ? r[0] : r[1]);
+    }
+}
+template <int O> __device__ __forceinline__ float lane_xor(float v) { return __int_as_float(lane_xor<O>(__float_as_int(v))); }
+
+// lanes xor-reduced within groups of G (G a power of two <= 64): the tree every lane of a group ends with, partner
+// values exactly those of __shfl_xor
+template <int G, typename T, typename F> __device__ __forceinline__ T group_reduce(T v, F op) {
+    if constexpr (G >= 64) v = op(v, lane_xor<32>(v));
+    if constexpr (G >= 32) v = op(v, lane_xor<16>(v));
+    if constexpr (G >= 16) v = op(v, lane_xor<8>(v));
+    if constexpr (G >= 8) v = op(v, lane_xor<4>(v));
+    if constexpr (G >= 4) v = op(v, lane_xor<2>(v));
+    if constexpr (G >= 2) v = op(v, lane_xor<1>(v));
     return v;
+}
+template <int G> __device__ __forceinline__ float group_sum(float v) {
+    return group_reduce<G>(v, [](float a, float b) { return a + b; });
 }
 template <int G> __device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-    for (int o = G / 2; o; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
+    return group_reduce<G>(v, [](float a, float b) { return fmaxf(a, b); });
 }
 template <int G> __device__ __forceinline__ int group_isum(int v) {
-#pragma unroll
-    for (int o = G / 2; o; o >>= 1) v += __shfl_xor(v, o);
-    return v;
+    return group_reduce<G>(v, [](int a, int b) { return a + b; });
 }
 
 __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }

@@ -14,8 +14,8 @@
 #include <hip/hip_ext.h>
 #include "mv.hpp"
 #ifdef SFNX_PHASE_PROF
-#define SFNX_TOPK_STAMP if (lane == 0 && blockIdx.x == 0) { uint64_t sink = 0; for (int i = 0; i < NV; ++i) sink += key[i]; if (sink == 12345) key[0] = 0; g_prof_topk = wall_clock64(); }
-__device__ unsigned long long g_prof_topk;
+#define SFNX_TOPK_STAMP(i) if (lane == 0 && blockIdx.x == 0) { g_prof_topk[i] = wall_clock64(); }
+__device__ unsigned long long g_prof_topk[4];
 #endif
 #include "topk.hpp"
 
@@ -28,8 +28,12 @@ namespace {
 __device__ unsigned long long g_prof[8][16];
 #define PROF(k, i)                                                                  \
     if (threadIdx.x == 0 && (blockIdx.x == 0 || blockIdx.x == 100)) g_prof[2 * (k) + (blockIdx.x != 0)][i] = wall_clock64();
+__device__ unsigned long long g_blk[3][1024][2];   // every block's first and last stamp, per kernel
+#define PROFB(k, i) \
+    if (threadIdx.x == 0 && blockIdx.x < 1024) g_blk[k][blockIdx.x][i] = wall_clock64();
 #else
 #define PROF(k, i)
+#define PROFB(k, i)
 #endif
 
 constexpr int D1_THREADS = 128, D1_WAVES = D1_THREADS / WAVE;   // K1: a router row per wavefront
@@ -73,6 +77,7 @@ __global__ void __launch_bounds__(D1_THREADS) k_dec_router(const float* __restri
     constexpr int H = NC * 4 * WAVE, NQ = 2;
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE, L = E + 1;
     const int row = blockIdx.x * D1_WAVES + wave;
+    PROFB(0, 0)
     // every load of the launch issued up front: the router row, each token's chunks, this half-wave's q8_1 blocks
     const int nb = H / 32, hw = threadIdx.x / 32, l = threadIdx.x % 32, nslot = gridDim.x * (D1_THREADS / 32);
     float xqv[NQ];
@@ -134,6 +139,7 @@ __global__ void __launch_bounds__(D1_THREADS) k_dec_router(const float* __restri
         blk[4 + l] = (uint8_t) (int8_t) (amax == 0.0f ? 0 : (int) roundf(xi / d));
         if (l == 0) *reinterpret_cast<uint32_t*>(blk) = (uint32_t) f2h(d) | ((uint32_t) f2h(sum) << 16);
     }
+    PROFB(0, 1)
 }
 
 // ------------------------------------------------------------------------------------------------ K2
@@ -143,11 +149,17 @@ template <int G> struct RowOf<SFNX_Q4_K, G> {
     static __device__ __forceinline__ void load(R& w, const uint8_t* mat, int nrows, int row, int C, int ln) {
         w.load(q4k_planes(mat, nrows, C), row, C, ln);
     }
+    static __device__ __forceinline__ void issue(R& w, const uint8_t* mat, int nrows, int row, int C, int ln) {
+        w.issue(q4k_planes(mat, nrows, C), row, C, ln);
+    }
 };
 template <int G> struct RowOf<SFNX_Q8_0, G> {
     using R = Q80Row<G>;
     static __device__ __forceinline__ void load(R& w, const uint8_t* mat, int nrows, int row, int C, int ln) {
         w.load(q80_planes(mat, nrows, C), row, C, ln);
+    }
+    static __device__ __forceinline__ void issue(R& w, const uint8_t* mat, int nrows, int row, int C, int ln) {
+        w.issue(q80_planes(mat, nrows, C), row, C, ln);
     }
 };
 
@@ -168,6 +180,7 @@ __global__ void __launch_bounds__(d2_threads<TYPE>()) k_dec_experts(
     __shared__ float hbuf[SFNX_MAXT][32];
     extern __shared__ __align__(16) unsigned char lds[];
     PROF(1, 0)
+    PROFB(1, 0)
     // every token's activations into LDS first: their loads overlap the top-k
     const Acts a = acts_in(lds, TT, H);
     stage_q8_1(a, xq, nullptr, T);
@@ -293,6 +306,89 @@ __global__ void __launch_bounds__(d2_threads<TYPE>()) k_dec_experts(
         }
     }
     PROF(1, 6)
+    PROFB(1, 1)
+}
+
+// K2 for a window of one row (the batch-1 decode): the picks of one token are distinct experts, so job j is pick j
+// (n = 1, row 0, output pair j) and the shared expert's job is the last; no numbering is needed.  Every wavefront takes
+// the top-K itself from registers, so the weight loads wait on no barrier after the routing.
+template <int TYPE, int G, int NV>
+__global__ void __launch_bounds__(d2_threads<TYPE>()) k_dec_experts1(
+    const uint8_t* __restrict__ A, size_t sa, int H, int E, int K, int ff, int shared, const float* __restrict__ logits,
+    const uint8_t* __restrict__ xq, int* __restrict__ topi_g, float* __restrict__ topw_g, sfnx_job* __restrict__ jg,
+    sfnx_job* __restrict__ jd, int* __restrict__ njobs_g, float* __restrict__ gu, int8_t* __restrict__ hq_q,
+    float* __restrict__ hq_d, int* __restrict__ hq_s) {
+    constexpr int LPR = lpr_of<TYPE>(), NTH = d2_threads<TYPE>(), RPW = WAVE / LPR;
+    const int NFB = ff / 32, myjob = blockIdx.x / NFB, fb = blockIdx.x % NFB;
+    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    __shared__ float hbuf[32];
+    extern __shared__ __align__(16) unsigned char lds[];
+    PROF(1, 0)
+    PROFB(1, 0)
+    // the logits and the activations requested together
+    float lv[NV];
+    topk_load<NV>(logits, E / WAVE, lane, lv);
+    const Acts a = acts_in(lds, 1, H);
+    stage_q8_1(a, xq, nullptr, 1);
+    PROF(1, 7)
+    int pick;
+    float w;
+    topk_core<NV>(lv, K, lane, pick, w);
+    const int nr = __popcll(__ballot(lane < K && pick >= 0));
+    const int nj = nr + (shared ? 1 : 0);
+    PROF(1, 1)
+    if (blockIdx.x == 0 && wave == 0) {   // the routing, published for K3 and the caller
+        if (lane < K) {
+            topi_g[lane] = pick;
+            topw_g[lane] = w;
+        }
+        if (lane < nj) {
+            const int e = lane < nr ? pick : E, o = lane < nr ? lane : K;
+            jg[lane].w = jd[lane].w = e;
+            jg[lane].n = jd[lane].n = 1;
+            jg[lane].y[0] = 0;
+            jg[lane].out[0] = jd[lane].y[0] = jd[lane].out[0] = o;
+        }
+        if (lane == 0) {
+            njobs_g[0] = nj;
+            njobs_g[1] = 0;
+        }
+    }
+    if (myjob >= nj) return;
+    const int ex = myjob < nr ? __builtin_amdgcn_readlane(pick, myjob) : E, out = myjob < nr ? myjob : K;
+    const int rw = lane / LPR, ln = lane % LPR, f = fb * 32 + wave * RPW + rw;
+    const uint8_t* mat = A + (size_t) ex * sa;
+    typename RowOf<TYPE, G>::R wg, wu;
+    RowOf<TYPE, G>::issue(wg, mat, 2 * ff, f, H, ln);
+    RowOf<TYPE, G>::issue(wu, mat, 2 * ff, ff + f, H, ln);
+    __syncthreads();   // the staged activations
+    wg.prepare(ln);
+    wu.prepare(ln);
+    PROF(1, 3)
+    const float gv = group_sum<LPR>(wg.dot(a, 0, ln)), uv = group_sum<LPR>(wu.dot(a, 0, ln));
+    if (ln == 0) {
+        gu[(size_t) out * 2 * ff + f] = gv;
+        gu[(size_t) out * 2 * ff + ff + f] = uv;
+        hbuf[wave * RPW + rw] = silu_f(gv) * uv;
+    }
+    __syncthreads();
+    PROF(1, 5)
+    if (threadIdx.x < 32) {
+        const int l = threadIdx.x;
+        const float v = hbuf[l];
+        const float amax = group_max<32>(fabsf(v));
+        const float d = amax / 127.0f;
+        const int q = amax == 0.0f ? 0 : (int) roundf(v / d);
+        const int qs = group_isum<32>(q);
+        hq_q[(size_t) out * ff + 32 * fb + l] = (int8_t) q;
+        if (l == 0) {
+            hq_d[(size_t) out * NFB + fb] = h2f(f2h(d));
+            hq_s[(size_t) out * NFB + fb] = qs;
+        }
+    }
+    PROF(1, 6)
+    PROFB(1, 1)
+    (void) NTH;
 }
 
 // ------------------------------------------------------------------------------------------------ K3
@@ -307,6 +403,7 @@ __global__ void __launch_bounds__(D3_THREADS) k_dec_down(const uint8_t* __restri
     constexpr int LPR = lpr_of<TYPE>(), GROUPS = D3_THREADS / LPR;
     const int row0 = blockIdx.x * D3_ROWS, nj = njobs[0], P = T * K, NP = P + T, nbh = ff / 32;
     PROF(2, 0)
+    PROFB(2, 0)
     __shared__ int jw[MAX_P + 1], jn[MAX_P + 1], jout[MAX_P + 1][SFNX_MAXT];
     __shared__ float part[MAX_P + SFNX_MAXT][D3_ROWS];
     __shared__ int ti[MAX_P];
@@ -387,6 +484,107 @@ __global__ void __launch_bounds__(D3_THREADS) k_dec_down(const uint8_t* __restri
         x[(size_t) t * H + row] = xr[t][r] + s;
     }
     PROF(2, 3)
+    PROFB(2, 1)
+}
+
+// K3 for a window of one row: pair k is pick k, so a task's expert comes straight from the picks (job j = pick j, the
+// shared expert's job last) and its weight loads are issued before the activations are staged; every other request
+// of the block (picks, weights, the shared gate's logit, h, the residual rows) is issued up front, with one wait.
+template <int TYPE, int G2, int NB>
+__global__ void __launch_bounds__(D3_THREADS) k_dec_down1(const uint8_t* __restrict__ A, size_t sa, int H, int E, int K,
+                                                         int ff, int shared, const float* __restrict__ logits,
+                                                         const int* __restrict__ topi, const float* __restrict__ topw,
+                                                         const int8_t* __restrict__ hq_q, const float* __restrict__ hq_d,
+                                                         const int* __restrict__ hq_s, float* __restrict__ y,
+                                                         float* __restrict__ x) {
+    constexpr int LPR = lpr_of<TYPE>(), GROUPS = D3_THREADS / LPR, HQ4 = 5, HQS = 3;
+    const int row0 = blockIdx.x * D3_ROWS, nbh = ff / 32, lane = threadIdx.x % WAVE, tid = threadIdx.x;
+    const int g = tid / LPR, ln = tid % LPR;
+    PROF(2, 0)
+    PROFB(2, 0)
+    __shared__ float part[MAX_K + 1][D3_ROWS];
+    extern __shared__ __align__(16) unsigned char lds[];
+    // every request first
+    const int tp = lane < K ? topi[lane] : -1;
+    const float twv = lane < K ? topw[lane] : 0.f;
+    const float gl = shared ? logits[E] : 0.f;
+    const float xr = tid < D3_ROWS ? x[row0 + tid] : 0.f;
+    const int NP = K + 1, nq = NP * ff / 16, ns = NP * nbh;
+    int4 hv[HQ4];
+    float dv[HQS];
+    int sv[HQS];
+#pragma unroll
+    for (int r = 0; r < HQ4; ++r) hv[r] = reinterpret_cast<const int4*>(hq_q)[min(tid + r * D3_THREADS, nq - 1)];
+#pragma unroll
+    for (int r = 0; r < HQS; ++r) {
+        const int i = min(tid + r * D3_THREADS, ns - 1);
+        dv[r] = hq_d[i];
+        sv[r] = hq_s[i];
+    }
+    // the picks, then this group's weight rows: task (j, r) = job j's row row0 + r
+    const int nr = __popcll(__ballot(lane < K && tp >= 0)), nj = nr + (shared ? 1 : 0), ntask = nj * D3_ROWS;
+    typename RowOf<TYPE, G2>::R w[NB];
+    int pp[NB], ex[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const int j = (g + b * GROUPS) / D3_ROWS;
+        ex[b] = __shfl(tp, j < nr ? j : 0);
+        pp[b] = j < nr ? j : K;
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const int task = g + b * GROUPS, r = task % D3_ROWS;
+        if (task < ntask) RowOf<TYPE, G2>::issue(w[b], A + (size_t) (pp[b] < K ? ex[b] : E) * sa, H, row0 + r, ff, ln);
+    }
+    // the staged activations
+    const Acts a = acts_in(lds, NP, ff);
+    // (unconditional: a thread past the end writes the last element's own value again, so no load sinks into a branch)
+#pragma unroll
+    for (int r = 0; r < HQ4; ++r) reinterpret_cast<int4*>(a.q)[min(tid + r * D3_THREADS, nq - 1)] = hv[r];
+#pragma unroll
+    for (int r = 0; r < HQS; ++r) {
+        const int i = min(tid + r * D3_THREADS, ns - 1);
+        a.d[i] = dv[r];
+        a.s[i] = sv[r];
+    }
+    __syncthreads();
+    PROF(2, 1)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const int task = g + b * GROUPS;
+        if (task < ntask) {
+            w[b].prepare(ln);
+            const float v = group_sum<LPR>(w[b].dot(a, pp[b], ln));
+            if (ln == 0) part[pp[b]][task % D3_ROWS] = v;
+        }
+    }
+    // windows with more tasks than one batch (K > 11): the rest, a batch at a time
+    for (int t0 = g + NB * GROUPS; t0 < ntask; t0 += GROUPS) {
+        const int j = t0 / D3_ROWS, r = t0 % D3_ROWS, e = __shfl(tp, j < nr ? j : 0), q = j < nr ? j : K;
+        typename RowOf<TYPE, G2>::R w1;
+        RowOf<TYPE, G2>::load(w1, A + (size_t) (j < nr ? e : E) * sa, H, row0 + r, ff, ln);
+        const float v = group_sum<LPR>(w1.dot(a, q, ln));
+        if (ln == 0) part[q][r] = v;
+    }
+    __syncthreads();
+    PROF(2, 2)
+    // the weighted sum in the reference's fmaf order, then the residual
+    if (tid < WAVE) {
+        const int r = tid % D3_ROWS;
+        float s = 0.f;
+        for (int k = 0; k < K; ++k) {
+            const int pk = __builtin_amdgcn_readlane(tp, k);
+            const float wk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(twv), k));
+            if (pk >= 0) s = fmaf(wk, part[k][r], s);
+        }
+        if (shared) s = fmaf(sigm_f(gl), part[K][r], s);
+        if (tid < D3_ROWS) {
+            y[row0 + r] = s;
+            x[row0 + r] = xr + s;
+        }
+    }
+    PROF(2, 3)
+    PROFB(2, 1)
 }
 
 // ------------------------------------------------------------------------------------------------ launch
@@ -419,17 +617,49 @@ void launch_k1(const DecArgs& d, const sfnx_moe_layer_w& w, float* x, const DecL
     launch(0, k_dec_router<NC, TT>, dim3((rows + D1_WAVES - 1) / D1_WAVES), dim3(D1_THREADS), 0, s,
         w.W, x, d.T, d.E, d.eps, d.norm, (float*) (ws + L.logits), (uint8_t*) (ws + L.xq));
 }
+template <int TYPE, int G> void launch_k2_tt1(const DecArgs&, const sfnx_moe_layer_w&, const DecLayout&, char*, hipStream_t);
 template <int TYPE, int G, int TT>
 void launch_k2(const DecArgs& d, const sfnx_moe_layer_w& w, const DecLayout& L, char* ws, hipStream_t s) {
-    const int njmax = d.T * d.K + (d.shared ? 1 : 0);
-    launch(1, k_dec_experts<TYPE, G, TT>, dim3(njmax * (d.ff / 32)), dim3(d2_threads<TYPE>()), acts_bytes(TT, d.H), s,
-        (const uint8_t*) w.gu, w.gu_stride, d.T, d.H, d.E, d.K, d.ff, d.shared, (const float*) (ws + L.logits),
+    if constexpr (TT == 1) {
+        launch_k2_tt1<TYPE, G>(d, w, L, ws, s);
+    } else {
+        const int njmax = d.T * d.K + (d.shared ? 1 : 0);
+        launch(1, k_dec_experts<TYPE, G, TT>, dim3(njmax * (d.ff / 32)), dim3(d2_threads<TYPE>()), acts_bytes(TT, d.H), s,
+            (const uint8_t*) w.gu, w.gu_stride, d.T, d.H, d.E, d.K, d.ff, d.shared, (const float*) (ws + L.logits),
+            (const uint8_t*) (ws + L.xq), (int*) (ws + L.topi), (float*) (ws + L.topw), (sfnx_job*) (ws + L.jg),
+            (sfnx_job*) (ws + L.jd), (int*) (ws + L.njobs), (float*) (ws + L.gu), (int8_t*) (ws + L.hq_q),
+            (float*) (ws + L.hq_d), (int*) (ws + L.hq_s));
+    }
+}
+template <int TYPE, int G, int NV>
+void launch_k2_one(const DecArgs& d, const sfnx_moe_layer_w& w, const DecLayout& L, char* ws, hipStream_t s) {
+    const int njmax = d.K + (d.shared ? 1 : 0);
+    launch(1, k_dec_experts1<TYPE, G, NV>, dim3(njmax * (d.ff / 32)), dim3(d2_threads<TYPE>()), acts_bytes(1, d.H), s,
+        (const uint8_t*) w.gu, w.gu_stride, d.H, d.E, d.K, d.ff, d.shared, (const float*) (ws + L.logits),
         (const uint8_t*) (ws + L.xq), (int*) (ws + L.topi), (float*) (ws + L.topw), (sfnx_job*) (ws + L.jg),
         (sfnx_job*) (ws + L.jd), (int*) (ws + L.njobs), (float*) (ws + L.gu), (int8_t*) (ws + L.hq_q),
         (float*) (ws + L.hq_d), (int*) (ws + L.hq_s));
 }
+template <int TYPE, int G>
+void launch_k2_tt1(const DecArgs& d, const sfnx_moe_layer_w& w, const DecLayout& L, char* ws, hipStream_t s) {
+    if (d.E <= 256) launch_k2_one<TYPE, G, 4>(d, w, L, ws, s);
+    else if (d.E <= 512) launch_k2_one<TYPE, G, 8>(d, w, L, ws, s);
+    else launch_k2_one<TYPE, G, 16>(d, w, L, ws, s);
+}
+template <int TYPE, int G2>
+void launch_k3_one(const DecArgs& d, const sfnx_moe_layer_w& w, float* x, const DecLayout& L, char* ws, hipStream_t s) {
+    constexpr int NB = TYPE == SFNX_Q4_K ? 3 : 6;   // 11 jobs x 8 rows in one batch
+    launch(2, k_dec_down1<TYPE, G2, NB>, dim3(d.H / D3_ROWS), dim3(D3_THREADS), acts_bytes(d.K + 1, d.ff), s,
+        (const uint8_t*) w.dn, w.dn_stride, d.H, d.E, d.K, d.ff, d.shared, (const float*) (ws + L.logits),
+        (const int*) (ws + L.topi), (const float*) (ws + L.topw), (const int8_t*) (ws + L.hq_q),
+        (const float*) (ws + L.hq_d), (const int*) (ws + L.hq_s), (float*) (ws + L.y), x);
+}
 template <int TYPE, int G2, int NB>
 void launch_k3(const DecArgs& d, const sfnx_moe_layer_w& w, float* x, const DecLayout& L, char* ws, hipStream_t s) {
+    if (d.T == 1) {
+        launch_k3_one<TYPE, G2>(d, w, x, L, ws, s);
+        return;
+    }
     const int NP = d.T * d.K + d.T;
     const size_t hq_lds = acts_bytes(NP, d.ff);
     const bool staged = hq_lds <= 32 * 1024;
@@ -482,7 +712,8 @@ using namespace sfnx;
 #ifdef SFNX_PHASE_PROF
 extern "C" int sfnx_prof_read(unsigned long long* out) {
     if (hipMemcpyFromSymbol(out, HIP_SYMBOL(g_prof), sizeof(g_prof)) != hipSuccess) return -1;
-    return hipMemcpyFromSymbol(out + 128, HIP_SYMBOL(g_prof_topk), 8) == hipSuccess ? 0 : -1;
+    if (hipMemcpyFromSymbol(out + 129, HIP_SYMBOL(g_blk), sizeof(g_blk)) != hipSuccess) return -1;
+    return hipMemcpyFromSymbol(out + 128 + 3 * 2048 + 1, HIP_SYMBOL(g_prof_topk), 32) == hipSuccess ? 0 : -1;
 }
 #endif
 

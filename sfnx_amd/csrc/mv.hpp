@@ -77,17 +77,21 @@ __device__ inline void stage_swiglu(const Acts& a, const float* __restrict__ gu,
 // ------------------------------------------------------------------------------------------------ Q4_K
 template <int GPL> struct Q4kRow {
     uint4 q0[GPL], q1[GPL];
+    uint4 h[GPL];
     float d[GPL], dmin[GPL], sc0[GPL], m0[GPL], sc1[GPL], m1[GPL];
-    __device__ __forceinline__ void load(const Q4kPlanes& P, int row, int C, int l8) {
+    // the loads alone (issue several rows' before any prepare, so that their latencies overlap)
+    __device__ __forceinline__ void issue(const Q4kPlanes& P, int row, int C, int l8) {
         const uint8_t* nib = P.nib_row(row, C);
         const uint8_t* hdr = P.hdr_row(row, C);
-        uint4 h[GPL];
 #pragma unroll
         for (int i = 0; i < GPL; ++i) {
             q0[i] = *reinterpret_cast<const uint4*>(nib + 256 * i + 16 * l8);
             q1[i] = *reinterpret_cast<const uint4*>(nib + 256 * i + 128 + 16 * l8);
             h[i] = *reinterpret_cast<const uint4*>(hdr + 16 * (2 * i + (l8 >> 2)));
         }
+    }
+    // the block headers decoded: d, dmin and this lane's two sub-blocks' 6-bit scales and mins
+    __device__ __forceinline__ void prepare(int l8) {
 #pragma unroll
         for (int i = 0; i < GPL; ++i) {
             d[i] = h2f((uint16_t) (h[i].x & 0xffff));
@@ -95,6 +99,10 @@ template <int GPL> struct Q4kRow {
             q4k_scale_min(h[i], 2 * (l8 & 3), sc0[i], m0[i]);
             q4k_scale_min(h[i], 2 * (l8 & 3) + 1, sc1[i], m1[i]);
         }
+    }
+    __device__ __forceinline__ void load(const Q4kPlanes& P, int row, int C, int l8) {
+        issue(P, row, C, l8);
+        prepare(l8);
     }
     // this lane's share of row . activation row j
     __device__ __forceinline__ float dot(const Acts& a, int j, int l8) const {
@@ -125,16 +133,25 @@ template <int GPL> struct Q4kRow {
 // ------------------------------------------------------------------------------------------------ Q8_0
 template <int BPL> struct Q80Row {
     uint4 qa[BPL], qb[BPL];
+    uint16_t dh[BPL];
     float dw[BPL];
-    __device__ __forceinline__ void load(const Q80Planes& P, int row, int C, int l16) {
+    __device__ __forceinline__ void issue(const Q80Planes& P, int row, int C, int l16) {
         const uint8_t* q = P.q + (size_t) row * C;
         const uint16_t* d = P.d + (size_t) row * (C / 32);
 #pragma unroll
         for (int i = 0; i < BPL; ++i) {
             qa[i] = *reinterpret_cast<const uint4*>(q + 512 * i + 16 * l16);
             qb[i] = *reinterpret_cast<const uint4*>(q + 512 * i + 256 + 16 * l16);
-            dw[i] = h2f(d[l16 + 16 * i]);
+            dh[i] = d[l16 + 16 * i];
         }
+    }
+    __device__ __forceinline__ void prepare(int) {
+#pragma unroll
+        for (int i = 0; i < BPL; ++i) dw[i] = h2f(dh[i]);
+    }
+    __device__ __forceinline__ void load(const Q80Planes& P, int row, int C, int l16) {
+        issue(P, row, C, l16);
+        prepare(l16);
     }
     __device__ __forceinline__ float dot(const Acts& a, int j, int l16) const {
         float acc = 0.f;

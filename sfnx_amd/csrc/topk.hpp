@@ -8,9 +8,6 @@ constexpr int MAX_E = 1024, MAX_K = 16, MAX_P = SFNX_MAXT * MAX_K;
 
 // Wavefront reductions by DPP row operations (quad swaps, half-row and row mirrors, then the row broadcasts 15 and 31);
 // lane 63 holds the result, returned to every lane.  wave_max ignores NaN (v_max_f32's maxNum rule).
-template <int CTRL, int ROWS = 0xf> __device__ __forceinline__ int dpp_mov(int v) {
-    return __builtin_amdgcn_update_dpp(v, v, CTRL, ROWS, 0xf, false);
-}
 __device__ __forceinline__ float wave_max(float v) {
     v = fmaxf(v, __int_as_float(dpp_mov<0xB1>(__float_as_int(v))));          // quad_perm [1, 0, 3, 2]
     v = fmaxf(v, __int_as_float(dpp_mov<0x4E>(__float_as_int(v))));          // quad_perm [2, 3, 0, 1]
@@ -63,24 +60,52 @@ __device__ __forceinline__ float key_value(uint64_t k) {
     return __uint_as_float((ord & 0x80000000u) ? (ord & 0x7fffffffu) : ~ord);
 }
 
-// The top-K of one token's E = 64 NV logits by one wavefront (lane l holds experts l + 64 i): K rounds of the largest
-// untaken value, the lowest index among equal values (the reference's strict `>` scan, then `oi < bi` across lanes);
-// NaN and -inf are never taken (src/moe.cuh:128-162, src/prefill.cu:191-221).  Each lane sorts its keys once; a round
-// is one DPP maximum over the lanes' heads, the winner's lane moving to its next key.  Weights exp(l_k - l_top1) / z
-// with z summed in pick order.  A round with nothing left gives index -1, weight 0.  Lane k < K returns pick k.
-// AGENT: the logits were written earlier in the same launch.
+// unsigned maximum / minimum over the wavefront by DPP row operations, every lane's result in lane 63, returned to all;
+// lanes a row mask leaves out read the operation's identity
+template <int CTRL, int ROWS = 0xf> __device__ __forceinline__ uint32_t dpp_or(uint32_t v, uint32_t identity) {
+    return (uint32_t) __builtin_amdgcn_update_dpp((int) identity, (int) v, CTRL, ROWS, 0xf, false);
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, dpp_or<0xB1>(v, 0u));
+    v = max(v, dpp_or<0x4E>(v, 0u));
+    v = max(v, dpp_or<0x141>(v, 0u));
+    v = max(v, dpp_or<0x140>(v, 0u));
+    v = max(v, dpp_or<0x142, 0xa>(v, 0u));
+    v = max(v, dpp_or<0x143, 0xc>(v, 0u));
+    return (uint32_t) __builtin_amdgcn_readlane((int) v, 63);
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+    v = min(v, dpp_or<0xB1>(v, ~0u));
+    v = min(v, dpp_or<0x4E>(v, ~0u));
+    v = min(v, dpp_or<0x141>(v, ~0u));
+    v = min(v, dpp_or<0x140>(v, ~0u));
+    v = min(v, dpp_or<0x142, 0xa>(v, ~0u));
+    v = min(v, dpp_or<0x143, 0xc>(v, ~0u));
+    return (uint32_t) __builtin_amdgcn_readlane((int) v, 63);
+}
+
+// one token's E = 64 NV logits into registers, lane l holding experts l + 64 i (i < nv; the rest NaN)
 template <int NV, bool AGENT = false>
-__device__ inline void topk_wave(const float* lg, int nv, int K, int lane, int& pick, float& weight) {
+__device__ __forceinline__ void topk_load(const float* lg, int nv, int lane, float (&lv)[NV]) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) lv[i] = i >= nv ? NAN : AGENT ? load_agent(lg + lane + WAVE * i) : lg[lane + WAVE * i];
+}
+
+// The top-K of one token's logits (lane l holds experts l + 64 i) by one wavefront: K rounds of the largest untaken
+// value, the lowest index among equal values (the reference's strict `>` scan, then `oi < bi` across lanes); NaN and
+// -inf are never taken (src/moe.cuh:128-162, src/prefill.cu:191-221).  Each lane sorts its keys once; a round is one
+// 32-bit DPP maximum of the lanes' head values, then a DPP minimum of the indices of the heads holding it (the lowest
+// index wins a tie), the winner moving to its next key.  Weights exp(l_k - l_top1) / z
+// with z summed in pick order.  A round with nothing left gives index -1, weight 0.  Lane k < K returns pick k.
+template <int NV>
+__device__ inline void topk_core(const float (&lv)[NV], int K, int lane, int& pick, float& weight) {
     uint64_t key[NV];
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const float t = i >= nv ? NAN : AGENT ? load_agent(lg + lane + WAVE * i) : lg[lane + WAVE * i];
-        key[i] = pick_key(t, lane + WAVE * i);
-    }
+    for (int i = 0; i < NV; ++i) key[i] = pick_key(lv[i], lane + WAVE * i);
 #ifdef SFNX_TOPK_STAMP
-    SFNX_TOPK_STAMP
+    SFNX_TOPK_STAMP(0)
 #endif
-    // descending bitonic sort of the lane's keys
+    // descending bitonic sort of the lane's keys (value, then the lower index first)
 #pragma unroll
     for (int k = 2; k <= NV; k *= 2)
 #pragma unroll
@@ -96,24 +121,54 @@ __device__ inline void topk_wave(const float* lg, int nv, int K, int lane, int& 
                     key[l] = sw ? a : b;
                 }
             }
-    uint64_t mine = 0;
-    for (int k = 0; k < K; ++k) {
-        const uint64_t best = wave_max_u64(key[0]);
-        if (best == 0) break;   // nothing left: the remaining picks stay -1
-        const bool won = key[0] == best;
+    uint32_t ord[NV], idx[NV];   // idx complemented: an empty slot holds ord 0
 #pragma unroll
-        for (int i = 0; i + 1 < NV; ++i) key[i] = won ? key[i + 1] : key[i];
-        key[NV - 1] = won ? 0 : key[NV - 1];
-        if (lane == k) mine = best;
+    for (int i = 0; i < NV; ++i) {
+        ord[i] = (uint32_t) (key[i] >> 32);
+        idx[i] = ~(uint32_t) key[i];
     }
-    const int myi = mine ? (int) ~(uint32_t) mine : -1;
-    const float myv = key_value(mine);
+#ifdef SFNX_TOPK_STAMP
+    SFNX_TOPK_STAMP(1)
+#endif
+    uint32_t mine = 0, myidx = ~0u;
+    for (int k = 0; k < K; ++k) {   // no branch in a round: an exhausted row picks ord 0, index ~0, i.e. none
+        const uint32_t best = wave_max_u32(ord[0]);
+        const uint32_t wi = wave_min_u32(ord[0] == best ? idx[0] : ~0u);
+        if (lane == k) {
+            mine = best;
+            myidx = wi;
+        }
+        const bool won = idx[0] == wi;
+#pragma unroll
+        for (int i = 0; i + 1 < NV; ++i) {
+            ord[i] = won ? ord[i + 1] : ord[i];
+            idx[i] = won ? idx[i + 1] : idx[i];
+        }
+        ord[NV - 1] = won ? 0u : ord[NV - 1];
+        idx[NV - 1] = won ? ~0u : idx[NV - 1];
+    }
+#ifdef SFNX_TOPK_STAMP
+    SFNX_TOPK_STAMP(2)
+#endif
+    const int myi = mine ? (int) myidx : -1;
+    const float myv = key_value((uint64_t) mine << 32);
     const float v0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(myv), 0));
     const float ek = myi >= 0 ? expf(myv - v0) : 0.f;
     float z = 0.f;
     for (int k = 0; k < K; ++k) z += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ek), k));
     pick = myi;
     weight = myi < 0 ? 0.f : ek / z;
+#ifdef SFNX_TOPK_STAMP
+    SFNX_TOPK_STAMP(3)
+#endif
+}
+
+// AGENT: the logits were written earlier in the same launch
+template <int NV, bool AGENT = false>
+__device__ inline void topk_wave(const float* lg, int nv, int K, int lane, int& pick, float& weight) {
+    float lv[NV];
+    topk_load<NV, AGENT>(lg, nv, lane, lv);
+    topk_core<NV>(lv, K, lane, pick, weight);
 }
 // E at run time (a multiple of 64, at most 1024): the smallest instantiation that holds E / 64 values a lane
 template <bool AGENT = false>
