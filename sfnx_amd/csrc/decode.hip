@@ -313,15 +313,15 @@ __global__ void __launch_bounds__(d2_threads<TYPE>()) k_dec_experts(
 // (n = 1, row 0, output pair j) and the shared expert's job is the last; no numbering is needed.  Every wavefront takes
 // the top-K itself from registers, so the weight loads wait on no barrier after the routing.
 template <int TYPE, int G, int NV>
-__global__ void __launch_bounds__(d2_threads<TYPE>()) k_dec_experts1(
+__global__ void __launch_bounds__(2 * d2_threads<TYPE>()) k_dec_experts1(
     const uint8_t* __restrict__ A, size_t sa, int H, int E, int K, int ff, int shared, const float* __restrict__ logits,
     const uint8_t* __restrict__ xq, int* __restrict__ topi_g, float* __restrict__ topw_g, sfnx_job* __restrict__ jg,
     sfnx_job* __restrict__ jd, int* __restrict__ njobs_g, float* __restrict__ gu, int8_t* __restrict__ hq_q,
     float* __restrict__ hq_d, int* __restrict__ hq_s) {
-    constexpr int LPR = lpr_of<TYPE>(), NTH = d2_threads<TYPE>(), RPW = WAVE / LPR;
+    constexpr int LPR = lpr_of<TYPE>(), NW = 2 * d2_threads<TYPE>() / WAVE, RPW = WAVE / LPR;
     const int NFB = ff / 32, myjob = blockIdx.x / NFB, fb = blockIdx.x % NFB;
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-    __shared__ float hbuf[32];
+    __shared__ float gbuf[32], ubuf[32];
     extern __shared__ __align__(16) unsigned char lds[];
     PROF(1, 0)
     PROFB(1, 0)
@@ -332,12 +332,21 @@ __global__ void __launch_bounds__(d2_threads<TYPE>()) k_dec_experts1(
     stage_q8_1(a, xq, nullptr, 1);
     PROF(1, 7)
     int pick;
-    float w;
-    topk_core<NV>(lv, K, lane, pick, w);
+    uint32_t pord;
+    topk_picks<NV>(lv, K, lane, pick, pord);
     const int nr = __popcll(__ballot(lane < K && pick >= 0));
     const int nj = nr + (shared ? 1 : 0);
     PROF(1, 1)
-    if (blockIdx.x == 0 && wave == 0) {   // the routing, published for K3 and the caller
+    if (myjob >= nj && blockIdx.x != 0) return;
+    const int ex = myjob < nr ? __builtin_amdgcn_readlane(pick, myjob) : E, out = myjob < nr ? myjob : K;
+    // the first half of the waves take the 32 gate rows, the second half the matching up rows
+    const bool up = wave >= NW / 2;
+    const int rw = lane / LPR, ln = lane % LPR, fl = (up ? wave - NW / 2 : wave) * RPW + rw, row = (up ? ff : 0) + fb * 32 + fl;
+    const uint8_t* mat = A + (size_t) ex * sa;
+    typename RowOf<TYPE, G>::R wr;
+    if (myjob < nj) RowOf<TYPE, G>::issue(wr, mat, 2 * ff, row, H, ln);
+    if (blockIdx.x == 0 && wave == 0) {   // the routing, published for K3 and the caller, while the rows load
+        const float w = topk_weight(pick, pord, K);
         if (lane < K) {
             topi_g[lane] = pick;
             topw_g[lane] = w;
@@ -355,27 +364,19 @@ __global__ void __launch_bounds__(d2_threads<TYPE>()) k_dec_experts1(
         }
     }
     if (myjob >= nj) return;
-    const int ex = myjob < nr ? __builtin_amdgcn_readlane(pick, myjob) : E, out = myjob < nr ? myjob : K;
-    const int rw = lane / LPR, ln = lane % LPR, f = fb * 32 + wave * RPW + rw;
-    const uint8_t* mat = A + (size_t) ex * sa;
-    typename RowOf<TYPE, G>::R wg, wu;
-    RowOf<TYPE, G>::issue(wg, mat, 2 * ff, f, H, ln);
-    RowOf<TYPE, G>::issue(wu, mat, 2 * ff, ff + f, H, ln);
     __syncthreads();   // the staged activations
-    wg.prepare(ln);
-    wu.prepare(ln);
+    wr.prepare(ln);
     PROF(1, 3)
-    const float gv = group_sum<LPR>(wg.dot(a, 0, ln)), uv = group_sum<LPR>(wu.dot(a, 0, ln));
+    const float v = group_sum<LPR>(wr.dot(a, 0, ln));
     if (ln == 0) {
-        gu[(size_t) out * 2 * ff + f] = gv;
-        gu[(size_t) out * 2 * ff + ff + f] = uv;
-        hbuf[wave * RPW + rw] = silu_f(gv) * uv;
+        gu[(size_t) out * 2 * ff + row] = v;
+        (up ? ubuf : gbuf)[fl] = v;
     }
     __syncthreads();
     PROF(1, 5)
     if (threadIdx.x < 32) {
         const int l = threadIdx.x;
-        const float v = hbuf[l];
+        const float v = silu_f(gbuf[l]) * ubuf[l];
         const float amax = group_max<32>(fabsf(v));
         const float d = amax / 127.0f;
         const int q = amax == 0.0f ? 0 : (int) roundf(v / d);
@@ -388,7 +389,6 @@ __global__ void __launch_bounds__(d2_threads<TYPE>()) k_dec_experts1(
     }
     PROF(1, 6)
     PROFB(1, 1)
-    (void) NTH;
 }
 
 // ------------------------------------------------------------------------------------------------ K3
@@ -634,7 +634,7 @@ void launch_k2(const DecArgs& d, const sfnx_moe_layer_w& w, const DecLayout& L, 
 template <int TYPE, int G, int NV>
 void launch_k2_one(const DecArgs& d, const sfnx_moe_layer_w& w, const DecLayout& L, char* ws, hipStream_t s) {
     const int njmax = d.K + (d.shared ? 1 : 0);
-    launch(1, k_dec_experts1<TYPE, G, NV>, dim3(njmax * (d.ff / 32)), dim3(d2_threads<TYPE>()), acts_bytes(1, d.H), s,
+    launch(1, k_dec_experts1<TYPE, G, NV>, dim3(njmax * (d.ff / 32)), dim3(2 * d2_threads<TYPE>()), acts_bytes(1, d.H), s,
         (const uint8_t*) w.gu, w.gu_stride, d.H, d.E, d.K, d.ff, d.shared, (const float*) (ws + L.logits),
         (const uint8_t*) (ws + L.xq), (int*) (ws + L.topi), (float*) (ws + L.topw), (sfnx_job*) (ws + L.jg),
         (sfnx_job*) (ws + L.jd), (int*) (ws + L.njobs), (float*) (ws + L.gu), (int8_t*) (ws + L.hq_q),

@@ -93,12 +93,11 @@ __device__ __forceinline__ void topk_load(const float* lg, int nv, int lane, flo
 
 // The top-K of one token's logits (lane l holds experts l + 64 i) by one wavefront: K rounds of the largest untaken
 // value, the lowest index among equal values (the reference's strict `>` scan, then `oi < bi` across lanes); NaN and
-// -inf are never taken (src/moe.cuh:128-162, src/prefill.cu:191-221).  Each lane sorts its keys once; a round is one
-// 32-bit DPP maximum of the lanes' head values, then a DPP minimum of the indices of the heads holding it (the lowest
-// index wins a tie), the winner moving to its next key.  Weights exp(l_k - l_top1) / z
+// -inf are never taken (src/moe.cuh:128-162, src/prefill.cu:191-221).  Each lane sorts its keys once; a round is a
+// DPP maximum over the lanes' heads, the winner moving to its next key.  Weights exp(l_k - l_top1) / z
 // with z summed in pick order.  A round with nothing left gives index -1, weight 0.  Lane k < K returns pick k.
 template <int NV>
-__device__ inline void topk_core(const float (&lv)[NV], int K, int lane, int& pick, float& weight) {
+__device__ inline void topk_picks(const float (&lv)[NV], int K, int lane, int& pick, uint32_t& pord) {
     uint64_t key[NV];
 #pragma unroll
     for (int i = 0; i < NV; ++i) key[i] = pick_key(lv[i], lane + WAVE * i);
@@ -121,7 +120,7 @@ __device__ inline void topk_core(const float (&lv)[NV], int K, int lane, int& pi
                     key[l] = sw ? a : b;
                 }
             }
-    uint32_t ord[NV], idx[NV];   // idx complemented: an empty slot holds ord 0
+    uint32_t ord[NV], idx[NV];   // an empty slot: ord 0, index ~0
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         ord[i] = (uint32_t) (key[i] >> 32);
@@ -131,36 +130,93 @@ __device__ inline void topk_core(const float (&lv)[NV], int K, int lane, int& pi
     SFNX_TOPK_STAMP(1)
 #endif
     uint32_t mine = 0, myidx = ~0u;
-    for (int k = 0; k < K; ++k) {   // no branch in a round: an exhausted row picks ord 0, index ~0, i.e. none
-        const uint32_t best = wave_max_u32(ord[0]);
-        const uint32_t wi = wave_min_u32(ord[0] == best ? idx[0] : ~0u);
-        if (lane == k) {
-            mine = best;
-            myidx = wi;
-        }
-        const bool won = idx[0] == wi;
+    {
+        // Fast rounds on one 32-bit key: the value's order bits above bit 10, the complemented index below (E <= 1024),
+        // so one DPP maximum finds each round's winner.  The picks are then checked exactly (descending in (value,
+        // index) order, and no lane's remaining head above the last pick); a failed check (heads sharing their upper 22
+        // order bits) redoes the selection with the exact rounds.
+        uint32_t tk[NV];
 #pragma unroll
-        for (int i = 0; i + 1 < NV; ++i) {
-            ord[i] = won ? ord[i + 1] : ord[i];
-            idx[i] = won ? idx[i + 1] : idx[i];
+        for (int i = 0; i < NV; ++i) tk[i] = ord[i] ? (ord[i] & 0xFFFFFC00u) | (1023u - idx[i]) : 0u;
+        uint32_t mk = 0;
+        int popped = 0;
+        for (int k = 0; k < K; ++k) {
+            const uint32_t best = wave_max_u32(tk[0]);
+            if (lane == k) mk = best;
+            const bool won = tk[0] == best;
+            popped += won;
+#pragma unroll
+            for (int i = 0; i + 1 < NV; ++i) tk[i] = won ? tk[i + 1] : tk[i];
+            tk[NV - 1] = won ? 0u : tk[NV - 1];
         }
-        ord[NV - 1] = won ? 0u : ord[NV - 1];
-        idx[NV - 1] = won ? ~0u : idx[NV - 1];
+        // each pick's exact order bits, from the lane and slot that held it
+        const uint32_t pi = mk ? 1023u - (mk & 1023u) : ~0u;
+        uint32_t po = 0;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const uint32_t o = (uint32_t) __shfl((int) (uint32_t) (pick_key(lv[i], 0) >> 32), (int) (pi & 63u));
+            po = (pi >> 6) == (uint32_t) i ? o : po;
+        }
+        const uint64_t pk = mk ? ((uint64_t) po << 32) | ~pi : 0;
+        // this lane's first key not taken
+        uint64_t head = 0;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) head = popped == i ? ((uint64_t) ord[i] << 32) | ~idx[i] : head;
+        head = (popped < NV && ord[popped < NV ? popped : 0]) ? head : 0;
+        const uint32_t nlo = (uint32_t) dpp_mov<0x101>((int) (uint32_t) pk), nhi = (uint32_t) dpp_mov<0x101>((int) (pk >> 32));
+        const uint64_t next = ((uint64_t) nhi << 32) | nlo;   // pick k + 1 (row_shl:1; K <= 16 keeps it in row 0)
+        const uint32_t llo = (uint32_t) __builtin_amdgcn_readlane((int) (uint32_t) pk, K - 1);
+        const uint32_t lhi = (uint32_t) __builtin_amdgcn_readlane((int) (pk >> 32), K - 1);
+        const uint64_t last = ((uint64_t) lhi << 32) | llo;
+        const bool bad = (lane + 1 < K && next != 0 && !(pk > next)) || head > last;
+        const bool clash = __ballot(bad) != 0;
+        mine = (uint32_t) (pk >> 32);
+        myidx = pk ? pi : ~0u;
+        if (clash) {   // exact rounds: the maximum value, then the lowest index holding it
+            mine = 0;
+            myidx = ~0u;
+            for (int k = 0; k < K; ++k) {
+                const uint32_t best = wave_max_u32(ord[0]);
+                const uint32_t wi = wave_min_u32(ord[0] == best ? idx[0] : ~0u);
+                if (lane == k) {
+                    mine = best;
+                    myidx = wi;
+                }
+                const bool won = idx[0] == wi;
+#pragma unroll
+                for (int i = 0; i + 1 < NV; ++i) {
+                    ord[i] = won ? ord[i + 1] : ord[i];
+                    idx[i] = won ? idx[i + 1] : idx[i];
+                }
+                ord[NV - 1] = won ? 0u : ord[NV - 1];
+                idx[NV - 1] = won ? ~0u : idx[NV - 1];
+            }
+        }
     }
 #ifdef SFNX_TOPK_STAMP
     SFNX_TOPK_STAMP(2)
 #endif
-    const int myi = mine ? (int) myidx : -1;
-    const float myv = key_value((uint64_t) mine << 32);
+    pick = mine ? (int) myidx : -1;
+    pord = mine;
+}
+// the weights of the picks topk_picks returned (pord: the pick's value as order bits, 0 for none)
+__device__ inline float topk_weight(int pick, uint32_t pord, int K) {
+    const float myv = key_value((uint64_t) pord << 32);
     const float v0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(myv), 0));
-    const float ek = myi >= 0 ? expf(myv - v0) : 0.f;
+    const float ek = pick >= 0 ? expf(myv - v0) : 0.f;
     float z = 0.f;
     for (int k = 0; k < K; ++k) z += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ek), k));
-    pick = myi;
-    weight = myi < 0 ? 0.f : ek / z;
 #ifdef SFNX_TOPK_STAMP
+    const int lane = __lane_id();
     SFNX_TOPK_STAMP(3)
 #endif
+    return pick < 0 ? 0.f : ek / z;
+}
+template <int NV>
+__device__ inline void topk_core(const float (&lv)[NV], int K, int lane, int& pick, float& weight) {
+    uint32_t po;
+    topk_picks<NV>(lv, K, lane, pick, po);
+    weight = topk_weight(pick, po, K);
 }
 
 // AGENT: the logits were written earlier in the same launch

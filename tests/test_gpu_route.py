@@ -93,6 +93,45 @@ def test_router_logits_bit_exact(T):
     assert np.array_equal(out.cpu().numpy().view(np.uint32), orc.router_logits(W, x).view(np.uint32))
 
 
+def pf_route_case(logits, E, K, shared):
+    C = logits.shape[0]
+    cap = C * K // 64 + E + (C + 63) // 64 + 1
+    i32 = dict(dtype=torch.int32, device="cuda")
+    topi, topw = torch.empty((C, K), **i32), torch.empty((C, K), dtype=torch.float32, device="cuda")
+    cnt, jbase = torch.empty(E, **i32), torch.empty(E, **i32)
+    jg, jd = torch.zeros(cap * BIGJOB_INTS, **i32), torch.zeros(cap * BIGJOB_INTS, **i32)
+    njobs = torch.zeros(2, **i32)
+    moe.pf_route(torch.from_numpy(logits).cuda(), topi, topw, cnt, jbase, jg, jd, njobs, E, K, shared)
+    torch.cuda.synchronize()
+    return topi.cpu().numpy(), topw.cpu().numpy()
+
+
+def test_topk_near_ties_across_lanes():
+    """values a few ulps apart in different lanes (the top-k's fast 32-bit rounds keep only the upper 22 order bits
+    beside the index, so these must fall back to the exact rounds), ties, and values straddling zero"""
+    E, K = 512, 10
+    rng = np.random.default_rng(5)
+    rows = []
+    for r in range(48):
+        row = rng.normal(0, 1, E + 1).astype(np.float32)
+        top = np.float32(3.0 + 0.25 * (r % 5))
+        idx = rng.choice(E, 14, replace=False)
+        if r % 3 == 0:
+            idx = np.sort(idx)   # the lower index the smaller value: the truncated key would order these wrongly
+        for k, e in enumerate(idx):
+            row[e] = np.nextafter(top, np.float32(10.0), dtype=np.float32) if k == 0 else top
+            top = np.nextafter(top, np.float32(-10.0), dtype=np.float32) if r % 2 else top
+        rows.append(row)
+    z = np.full(E + 1, -5.0, np.float32)
+    z[[3, 67, 131]] = [np.float32(-0.0), np.float32(0.0), np.float32(1e-45)]
+    rows.append(z)
+    logits = np.stack(rows)
+    topi, topw = pf_route_case(logits, E, K, True)
+    oi, ow, _ = orc.topk(logits, E, K)
+    assert np.array_equal(topi, oi)
+    assert np.allclose(topw, ow, rtol=1e-6, atol=1e-7)
+
+
 @pytest.mark.parametrize("C, shared", [(300, True), (2048, False), (1, True)])
 def test_pf_route_bit_exact(C, shared):
     E, K = 512, 10
