@@ -118,6 +118,11 @@ int sfnx_moe_combine(const float* part, const float* topw, const int* topi, cons
 int sfnx_moe_gate_up_mma(const void* A, size_t sa, uint32_t type, int n_in, int n_out, const sfnx_bigjob* jobs,
                          const int* njobs, int njobs_cap, const uint16_t* xh, float* gu, void* st);
 int sfnx_swiglu_h16(const float* gu, int ffs, int P, uint16_t* h16, void* st);
+/* moe_gate_up_mma and swiglu_h16 in one launch (src/kernels.hpp:290-291 called back to back, as the prompt path does,
+ * src/prefill.cu:1167-1169): h16[job.out[m]][f] = f16(silu(gate) * up) for the job's rows, without writing the fp32
+ * gate|up rows; equal bit for bit to the two calls.  ff a multiple of 256; the experts' rows are [gate (ff) | up (ff)]. */
+int sfnx_moe_gate_up_swiglu_mma(const void* A, size_t sa, uint32_t type, int n_in, int ff, const sfnx_bigjob* jobs,
+                                const int* njobs, int njobs_cap, const uint16_t* xh, uint16_t* h16, void* st);
 int sfnx_moe_down_mma(const void* A, size_t sa, uint32_t type, int n_in, int n_out, const sfnx_bigjob* jobs,
                       const int* njobs, int njobs_cap, const uint16_t* h16, float* part, void* st);
 /* fp32 -> f16 (round to nearest even), n values: the activations the matrix-core path reads (the reference's hc read

@@ -44,6 +44,7 @@ SIGNATURES = {
     "sfnx_kernel_clock_read": (i32, [vp]),
     "sfnx_moe_gate_up_mma": (i32, [vp, sz, u32, i32, i32, vp, vp, i32, vp, vp, vp]),
     "sfnx_swiglu_h16": (i32, [vp, i32, i32, vp, vp]),
+    "sfnx_moe_gate_up_swiglu_mma": (i32, [vp, sz, u32, i32, i32, vp, vp, i32, vp, vp, vp]),
     "sfnx_moe_down_mma": (i32, [vp, sz, u32, i32, i32, vp, vp, i32, vp, vp, vp]),
     "sfnx_to_f16": (i32, [vp, vp, sz, vp]),
     "sfnx_moe_decode_workspace": (sz, [i32, i32, i32, i32, i32, vp]),

@@ -15,6 +15,13 @@
 namespace sfnx {
 namespace {
 
+#ifdef SFNX_PHASE_PROF
+__device__ unsigned long long g_mma_prof[512][20];   // wall-clock stamps of blocks (blockIdx.y < 512, x == 0)
+#define MPROF(i) if (threadIdx.x == 0 && blockIdx.x == 0 && blockIdx.y < 512) g_mma_prof[blockIdx.y][i] = wall_clock64();
+#else
+#define MPROF(i)
+#endif
+
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float float16v __attribute__((ext_vector_type(16)));
@@ -144,6 +151,39 @@ __device__ __forceinline__ void load_x_async(_Float16* buf, const _Float16* __re
 }
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }   // vmcnt(0), others unwaited
 
+// One run's 8 steps of 64 columns on one wavefront's 32 weight rows: step j's activation fragments are read from LDS
+// first, then step j + 1's weight fragments are dequantized (VALU, covering the LDS latency) interleaved with step j's
+// MFMAs; the scheduling groups keep that order (1 MFMA, then a share of the VALU).
+template <int TYPE, int NT>
+__device__ __forceinline__ void mma_run(const RunW<TYPE>& w, const _Float16* xb, int nn, int h, float16v (&acc)[NT]) {
+    half8 bc[4], bn[4];
+    dequant_step(w, 0, bc);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        half8 ac[NT][4];
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                ac[t][c] = *reinterpret_cast<const half8*>(xb + (size_t) (32 * t + nn) * MM_XLD + run_col<TYPE>(j, c, h));
+        if (j < 7) dequant_step(w, j + 1, bn);
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int t = 0; t < NT; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ac[t][c], bc[c], acc[t], 0, 0, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 4 * NT, 0);   // the DS reads
+        __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);       // VALU while they land
+#pragma unroll
+        for (int q = 0; q < 4 * NT; ++q) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // an MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 48 / (4 * NT), 0);
+        }
+        if (j < 7)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) bc[c] = bn[c];
+    }
+}
+
 // The block's rows are G groups of 256 (a wavefront's 32 rows each); per group the runs of 512 columns, per run 8
 // steps of 64.  Weights stream one run ahead of the steps (registers); each run's activations come into the other LDS
 // buffer while this one is read.  A single run (the down projection) is staged once for every group.
@@ -158,6 +198,7 @@ __device__ __forceinline__ void mma_job(const uint8_t* mat, int R, int C, int ro
     load_run(w, mat, R, C, row_of(0), 0, h);
     float16v acc[NT];
     for (int it = 0; it < total; ++it) {
+        if (it < 16) { MPROF(2 + it) }
         const int r = it % nr;
         if (r == 0) {
 #pragma unroll
@@ -172,18 +213,7 @@ __device__ __forceinline__ void mma_job(const uint8_t* mat, int R, int C, int ro
                 load_x_async(xs + (size_t) ((it + 1) & 1) * MM_XBUF, x, ldx, jb.y, jb.n, (r + 1) % nr, wave, lane);
         }
         if (it + 1 < total) load_run(wn, mat, R, C, row_of(it + 1), (it + 1) % nr, h);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            half8 b[4];
-            dequant_step(w, j, b);
-#pragma unroll
-            for (int t = 0; t < NT; ++t)
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    const half8 a = *reinterpret_cast<const half8*>(xb + (size_t) (32 * t + nn) * MM_XLD + run_col<TYPE>(j, c, h));
-                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b[c], acc[t], 0, 0, 0);
-                }
-        }
+        mma_run<TYPE, NT>(w, xb, nn, h, acc);
         if (r == nr - 1) {
             // D[token][row]: lane (nn, h), value q at token 8 (q / 4) + 4 h + q % 4 of the tile
             const int row = row_of(it);
@@ -199,10 +229,79 @@ __device__ __forceinline__ void mma_job(const uint8_t* mat, int R, int C, int ro
     }
 }
 
+// The gate|up projection by pairs of row groups: a block owns FF indices f0 .. f0 + 255, i.e. gate rows f0 + . and the
+// matching up rows ff + f0 + .; the runs of 512 columns are the outer loop and each run's activations are staged once
+// for both groups.  Epilogue: gu (fp32 rows, when given) and h16 = f16(silu(gate) up) (when given), from the same
+// accumulators, so the fused form equals moe_gate_up_mma followed by swiglu_h16 bit for bit.
+template <int TYPE, int NT>
+__device__ __forceinline__ void mma_gu_job(const uint8_t* mat, int ff, int C, int f0, int wave, int lane,
+                                           const sfnx_bigjob& jb, const _Float16* __restrict__ x, _Float16* xs,
+                                           float* __restrict__ gu, _Float16* __restrict__ h16) {
+    const int h = lane / 32, nn = lane % 32, nr = C / MM_RUN, R = 2 * ff, f = f0 + wave * 32 + nn;
+    const int rows[2] = {f, ff + f};
+    RunW<TYPE> w, wn;
+    load_x_async(xs, x, C, jb.y, jb.n, 0, wave, lane);
+    load_run(w, mat, R, C, rows[0], 0, h);
+    float16v acc[2][NT];
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[g][t] = float16v{};
+    for (int r = 0; r < nr; ++r) {
+        _Float16* xb = xs + (size_t) (r & 1) * MM_XBUF;
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+            if (g == 0) {
+                wait_vmem();          // this run's activations and gate weights
+                __syncthreads();      // every wavefront's rows landed; every wavefront is past the previous run
+                if (r + 1 < nr) load_x_async(xs + (size_t) ((r + 1) & 1) * MM_XBUF, x, C, jb.y, jb.n, r + 1, wave, lane);
+                load_run(wn, mat, R, C, rows[1], r, h);
+            } else if (r + 1 < nr) {
+                load_run(wn, mat, R, C, rows[0], r + 1, h);
+            }
+            mma_run<TYPE, NT>(w, xb, nn, h, acc[g]);
+            w = wn;
+        }
+    }
+    if (gu) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const int m = 32 * t + 8 * (q / 4) + 4 * h + q % 4;
+                if (m < jb.n) {
+                    const size_t o = (size_t) jb.out[m];
+                    gu[o * R + rows[0]] = acc[0][t][q];
+                    gu[o * R + rows[1]] = acc[1][t][q];
+                }
+            }
+    }
+    if (h16) {
+        // h through LDS ([token][256 FF indices], the last run's buffer is free once every wavefront is past it), then
+        // 16-byte stores of whole 512-byte row pieces
+        constexpr int HLD = MM_BM + 8;
+        _Float16* hs = xs;
+        __syncthreads();
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const int m = 32 * t + 8 * (q / 4) + 4 * h + q % 4;
+                hs[m * HLD + wave * 32 + nn] = (_Float16) (silu_f(acc[0][t][q]) * acc[1][t][q]);
+            }
+        __syncthreads();
+        for (int i = threadIdx.x; i < jb.n * (MM_BM / 8); i += MM_THREADS) {
+            const int m = i / (MM_BM / 8), c = i % (MM_BM / 8);
+            *reinterpret_cast<uint4*>(h16 + (size_t) jb.out[m] * ff + f0 + 8 * c) = *reinterpret_cast<const uint4*>(hs + m * HLD + 8 * c);
+        }
+    }
+}
+
 template <int TYPE>
-__global__ void __launch_bounds__(MM_THREADS) k_moe_mma(const uint8_t* __restrict__ A, size_t sa, int R, int C, int G,
-                                                       const sfnx_bigjob* __restrict__ jobs, const int* __restrict__ njobs,
-                                                       const _Float16* __restrict__ x, float* __restrict__ out) {
+__global__ void __launch_bounds__(MM_THREADS) k_moe_mma_gu(const uint8_t* __restrict__ A, size_t sa, int ff, int C,
+                                                          const sfnx_bigjob* __restrict__ jobs, const int* __restrict__ njobs,
+                                                          const _Float16* __restrict__ x, float* __restrict__ gu,
+                                                          _Float16* __restrict__ h16) {
     const int ji = blockIdx.y;
     if (ji >= *njobs) return;
     __shared__ sfnx_bigjob jb;
@@ -212,9 +311,29 @@ __global__ void __launch_bounds__(MM_THREADS) k_moe_mma(const uint8_t* __restric
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
     const uint8_t* mat = A + (size_t) jb.w * sa;
     _Float16* xs = reinterpret_cast<_Float16*>(xs_raw);
+    if (jb.n > 32) mma_gu_job<TYPE, 2>(mat, ff, C, blockIdx.x * MM_BM, wave, lane, jb, x, xs, gu, h16);
+    else mma_gu_job<TYPE, 1>(mat, ff, C, blockIdx.x * MM_BM, wave, lane, jb, x, xs, gu, h16);
+}
+
+template <int TYPE>
+__global__ void __launch_bounds__(MM_THREADS) k_moe_mma(const uint8_t* __restrict__ A, size_t sa, int R, int C, int G,
+                                                       const sfnx_bigjob* __restrict__ jobs, const int* __restrict__ njobs,
+                                                       const _Float16* __restrict__ x, float* __restrict__ out) {
+    const int ji = blockIdx.y;
+    MPROF(0)
+    if (ji >= *njobs) return;
+    __shared__ sfnx_bigjob jb;
+    extern __shared__ __align__(16) unsigned char xs_raw[];
+    load_job(jb, jobs + ji);
+    __syncthreads();
+    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    const uint8_t* mat = A + (size_t) jb.w * sa;
+    _Float16* xs = reinterpret_cast<_Float16*>(xs_raw);
     const int row0 = blockIdx.x * G * MM_BM;
+    MPROF(1)
     if (jb.n > 32) mma_job<TYPE, 2>(mat, R, C, row0, G, wave, lane, jb, x, C, xs, out);
     else mma_job<TYPE, 1>(mat, R, C, row0, G, wave, lane, jb, x, C, xs, out);
+    MPROF(18)
 }
 
 // k_swiglu_h16 (src/moe_mma.cuh:382-388): h16 = f16(silu(gate) * up) of P rows [gate (ff) | up (ff)]
@@ -253,14 +372,51 @@ void moe_mma(uint32_t type, const void* A, size_t sa, int n_in, int n_out, const
         k_moe_mma<SFNX_Q8_0><<<grid, MM_THREADS, MM_LDS, s>>>((const uint8_t*) A, sa, n_out, n_in, G, jobs, njobs, (const _Float16*) x16, out);
 }
 
+void moe_mma_gu(uint32_t type, const void* A, size_t sa, int n_in, int ff, const sfnx_bigjob* jobs, const int* njobs,
+                int njobs_cap, const void* x16, float* gu, uint16_t* h16, void* st) {
+    require(type == SFNX_Q4_K || type == SFNX_Q8_0, "expert type must be Q4_K (12) or Q8_0 (8)");
+    require(n_in > 0 && n_in % 512 == 0, "expert input width must be a multiple of 512");
+    require(ff > 0 && ff % MM_BM == 0, "FF must be a multiple of 256");
+    require(sa >= row_bytes(type, n_in) * (size_t) (2 * ff), "expert stride smaller than a matrix");
+    require(njobs_cap >= 0 && njobs_cap <= 65535, "njobs_cap out of range");
+    if (njobs_cap == 0) return;
+    const dim3 grid(ff / MM_BM, njobs_cap);
+    hipStream_t s = stream_of(st);
+    if (type == SFNX_Q4_K)
+        k_moe_mma_gu<SFNX_Q4_K><<<grid, MM_THREADS, MM_LDS, s>>>((const uint8_t*) A, sa, ff, n_in, jobs, njobs,
+                                                                  (const _Float16*) x16, gu, (_Float16*) h16);
+    else
+        k_moe_mma_gu<SFNX_Q8_0><<<grid, MM_THREADS, MM_LDS, s>>>((const uint8_t*) A, sa, ff, n_in, jobs, njobs,
+                                                                  (const _Float16*) x16, gu, (_Float16*) h16);
+}
+
 }  // namespace
 }  // namespace sfnx
 
 using namespace sfnx;
 
+#ifdef SFNX_PHASE_PROF
+extern "C" int sfnx_mma_prof_read(unsigned long long* out) {
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(g_mma_prof), sizeof(g_mma_prof)) == hipSuccess ? 0 : -1;
+}
+#endif
+
 extern "C" int sfnx_moe_gate_up_mma(const void* A, size_t sa, uint32_t type, int n_in, int n_out, const sfnx_bigjob* jobs,
                                     const int* njobs, int njobs_cap, const uint16_t* xh, float* gu, void* st) {
-    return guarded("sfnx_moe_gate_up_mma", [&] { moe_mma(type, A, sa, n_in, n_out, jobs, njobs, njobs_cap, xh, gu, st); });
+    return guarded("sfnx_moe_gate_up_mma", [&] {
+        if (n_out % (2 * MM_BM) == 0 && n_in > MM_RUN)
+            moe_mma_gu(type, A, sa, n_in, n_out / 2, jobs, njobs, njobs_cap, xh, gu, nullptr, st);
+        else
+            moe_mma(type, A, sa, n_in, n_out, jobs, njobs, njobs_cap, xh, gu, st);
+    });
+}
+
+extern "C" int sfnx_moe_gate_up_swiglu_mma(const void* A, size_t sa, uint32_t type, int n_in, int ff, const sfnx_bigjob* jobs,
+                                           const int* njobs, int njobs_cap, const uint16_t* xh, uint16_t* h16, void* st) {
+    return guarded("sfnx_moe_gate_up_swiglu_mma", [&] {
+        require(h16 != nullptr, "h16 is required");
+        moe_mma_gu(type, A, sa, n_in, ff, jobs, njobs, njobs_cap, xh, nullptr, h16, st);
+    });
 }
 
 extern "C" int sfnx_moe_down_mma(const void* A, size_t sa, uint32_t type, int n_in, int n_out, const sfnx_bigjob* jobs,

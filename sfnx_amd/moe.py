@@ -101,6 +101,10 @@ def swiglu_h16(gu, h16, ff: int) -> None:
     check(lib().sfnx_swiglu_h16(_p(gu), ff, gu.shape[0], _p(h16), _st()))
 
 
+def moe_gate_up_swiglu_mma(A, sa, wtype, n_in, ff, jobs, njobs, njobs_cap, xh, h16) -> None:
+    check(lib().sfnx_moe_gate_up_swiglu_mma(_p(A), sa, wtype, n_in, ff, _p(jobs), _p(njobs), njobs_cap, _p(xh), _p(h16), _st()))
+
+
 def moe_down_mma(A, sa, wtype, n_in, n_out, jobs, njobs, njobs_cap, h16, part) -> None:
     check(lib().sfnx_moe_down_mma(_p(A), sa, wtype, n_in, n_out, _p(jobs), _p(njobs), njobs_cap, _p(h16), _p(part), _st()))
 

@@ -96,3 +96,16 @@ def test_mma_baseline_prefill_shape():
     assert 150 < int(b.cnt.max()) < 260
     eg, ed = check_sampled(host, x, b, 24, np.random.default_rng(2))
     assert eg < 2e-3 and ed < 2e-3, (eg, ed)
+
+
+@pytest.mark.parametrize("wtype", [orc.Q4_K, orc.Q8_0])
+def test_gate_up_swiglu_fused_equals_two_calls(wtype):
+    """sfnx_moe_gate_up_swiglu_mma against moe_gate_up_mma + swiglu_h16 on the same jobs: bit for bit"""
+    shape = moe.LayerShape(H=1024, E=64, K=6, ff=512, wtype=wtype, shared=True)
+    L, host, x, y, b = run_prefill(shape, 90 + wtype, 200, dup=True)
+    s = shape
+    fused = torch.full_like(b.h16, 7.0)
+    moe.moe_gate_up_swiglu_mma(L.gu_w, L.gu_stride, s.wtype, s.H, s.ff, b.jobs_gu, b.njobs, b.cap, b.xh, fused)
+    torch.cuda.synchronize()
+    P = int(b.topi.numel()) + 200
+    assert torch.equal(fused[:P].view(torch.int16), b.h16[:P].view(torch.int16))
