@@ -10,7 +10,10 @@ Also in the JSON line: us/token-layer; each decode kernel's time from HIP events
 layer at a time) and the dominant one's roofline; the prompt path (config 3: 2048 tokens, Zipf-skewed routing); the
 CPU baseline (the oracle on config 0, on the host's cores) with the GPU's parity against it for that token.
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers 48] [--no-prefill] [--no-cpu]
+Configs 2 (a 96-row verify window through the whole layer) and 4 (Q8_0 experts: decode through 24 stacked layers and
+a 4096-token prompt chunk) are reported beside it.
+
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers 48] [--no-prefill] [--no-cpu] [--no-extra]
 """
 from __future__ import annotations
 
@@ -43,6 +46,8 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-extra", action="store_true", help="skip configs 2 and 4 (verify window, Q8_0)")
+    ap.add_argument("--q8-layers", type=int, default=24)
     ap.add_argument("--copy-calib", action="store_true",
                     help="only copy 1 GiB device-to-device 3 times: the known-size kernel that scales rocprofv3's "
                          "FETCH_SIZE / WRITE_SIZE to bytes")
@@ -169,6 +174,9 @@ def main():
         out["prefill"] = bench_prefill(layers[0], s, moe, torch)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(layers[0], s, moe, torch, x0, args.cpu_seconds)
+    if not args.no_extra:
+        out["verify_window"] = bench_window(layers[0], s, moe, torch)
+        out["q8_0"] = bench_q8_0(moe, torch, args.q8_layers, args.steps, args.warmup)
     print(json.dumps(out), flush=True)
     return 0
 
@@ -245,6 +253,81 @@ def bench_prefill(L, s, moe, torch, C=2048, reps=10):
             "weight_gbs": round(wbytes / t_mma / 1e9, 1), "hbm_frac": round(wbytes / t_mma / 1e9 / HBM_PEAK_GBS, 4),
             "q8_dot_tops": round(flops / t_q8 / 1e12, 2),
             "experts_touched": touched, "max_rows_per_expert": int(cnt.max()), "flops": flops, "weight_bytes": wbytes}
+
+
+def time_us(torch, fn, reps):
+    fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps * 1e3
+
+
+def bench_window(L, s, moe, torch, C=96, reps=20):
+    """config 2: a verify window of 6 sequences x 16 draft rows = 96 rows through layer 0 (N(0,1) activations, no
+    skew): the whole layer on the prompt path (router, top-k, permutation, gate|up + SwiGLU, down, combine)"""
+    x = torch.empty((C, s.H), dtype=torch.float32, device="cuda")
+    moe.synth_normal(x, 779, 1.0)
+    y = torch.empty_like(x)
+    b = moe.PrefillBuffers(s, C)
+    us = time_us(torch, lambda: moe.prefill_layer_mma(L, x, y, b), reps)
+    touched = int((b.cnt.cpu() > 0).sum()) + 1
+    nbytes = touched * expert_bytes(s, moe) + (s.E + 1) * s.H * 4
+    return {"workload": "config 2: 96 rows (6 x 16), one Q4_K layer, whole layer on the prompt path", "us": round(us, 1),
+            "us_per_row": round(us / C, 2), "experts_touched": touched, "bytes": nbytes,
+            "gbs": round(nbytes / (us * 1e-6) / 1e9, 1), "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
+def bench_q8_0(moe, torch, NL, steps, warmup):
+    """config 4: the same layer shapes with Q8_0 experts: decode at batch 1 through NL stacked layers (the fused
+    path in a graph, as config 1), and a 4096-token prompt chunk through layer 0 (experts on the matrix cores)"""
+    s = moe.LayerShape(H=2048, E=512, K=10, ff=512, wtype=moe.Q8_0, shared=True)
+    layers = [moe.MoeLayer.synthetic(s, seed=5000 + l) for l in range(NL)]
+    x0 = torch.empty((1, s.H), dtype=torch.float32, device="cuda")
+    moe.synth_normal(x0, 4343, 1.0)
+    x = x0.clone()
+    f = moe.FusedDecode(layers, 1)
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        f(x)
+    torch.cuda.current_stream().wait_stream(st)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        x.copy_(x0)
+        f(x)
+    ms = time_us(torch, g.replay, max(steps, 5)) / 1e3
+    assert torch.isfinite(x).all()
+    bytes_tl = (s.E + 1) * s.H * 4 + (s.K + 1) * expert_bytes(s, moe)
+    gbs = bytes_tl * NL / (ms * 1e-3) / 1e9
+    C = 4096
+    L = layers[0]
+    xp = torch.empty((C, s.H), dtype=torch.float32, device="cuda")
+    moe.synth_normal(xp, 780, 1.0)
+    xn = torch.empty_like(xp)
+    moe.residual_rmsnorm(xp, None, xn)
+    b = moe.PrefillBuffers(s, C)
+    moe.prefill_route(L, xn, b, torch.from_numpy(zipf_bias(s.E)).cuda())
+    moe.to_f16(xn, b.xh)
+    t_gu = time_us(torch, lambda: moe.moe_gate_up_swiglu_mma(L.gu_w, L.gu_stride, s.wtype, s.H, s.ff, b.jobs_gu, b.njobs,
+                                                             b.cap, b.xh, b.h16), 5)
+    t_dn = time_us(torch, lambda: moe.moe_down_mma(L.dn_w, L.dn_stride, s.wtype, s.ff, s.H, b.jobs_dn, b.njobs, b.cap,
+                                                   b.h16, b.part), 5)
+    flops = 2 * (C * s.K + C) * 3 * s.ff * s.H
+    touched = int((b.cnt.cpu() > 0).sum()) + 1
+    wbytes = touched * expert_bytes(s, moe)
+    t = (t_gu + t_dn) * 1e-6
+    return {"workload": f"config 4: Q8_0 experts; decode batch 1 through {NL} stacked layers; 4096-token prompt chunk",
+            "decode_us_per_token_layer": round(ms * 1000 / NL, 3), "decode_gbs": round(gbs, 1),
+            "decode_hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_token_layer": bytes_tl,
+            "prefill_us": {"mma_gate_up_swiglu": round(t_gu, 1), "mma_down": round(t_dn, 1)},
+            "prefill_tflops": round(flops / t / 1e12, 1), "prefill_weight_gbs": round(wbytes / t / 1e9, 1),
+            "prefill_hbm_frac": round(wbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
 
 
 def cpu_baseline(L, s, moe, torch, x0, seconds):

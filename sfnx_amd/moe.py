@@ -309,6 +309,18 @@ def prefill_experts_mma(L: "MoeLayer", x: torch.Tensor, y: torch.Tensor, b: "Pre
     moe_combine(b.part, b.topw, b.topi, b.logits, y, s.E, s.K, s.shared)
 
 
+def prefill_layer_mma(L: "MoeLayer", x: torch.Tensor, y: torch.Tensor, b: "PrefillBuffers",
+                      bias: torch.Tensor | None = None) -> None:
+    """A prompt chunk (or a verify window of many rows) through the whole layer on the matrix cores: routing, f16
+    activations, gate|up with SwiGLU fused into its epilogue, down, the combine (src/prefill.cu:1145-1180)"""
+    s = L.s
+    prefill_route(L, x, b, bias)
+    to_f16(x, b.xh)
+    moe_gate_up_swiglu_mma(L.gu_w, L.gu_stride, s.wtype, s.H, s.ff, b.jobs_gu, b.njobs, b.cap, b.xh, b.h16)
+    moe_down_mma(L.dn_w, L.dn_stride, s.wtype, s.ff, s.H, b.jobs_dn, b.njobs, b.cap, b.h16, b.part)
+    moe_combine(b.part, b.topw, b.topi, b.logits, y, s.E, s.K, s.shared)
+
+
 def prefill_layer_q8(L: MoeLayer, x: torch.Tensor, y: torch.Tensor, b: PrefillBuffers) -> None:
     """A prompt chunk through the layer on the int8 (q8_1) arithmetic, FNX_PF_MOE_Q8 (src/prefill.cu:1156-1166)."""
     s = L.s

@@ -109,3 +109,40 @@ def test_gate_up_swiglu_fused_equals_two_calls(wtype):
     torch.cuda.synchronize()
     P = int(b.topi.numel()) + 200
     assert torch.equal(fused[:P].view(torch.int16), b.h16[:P].view(torch.int16))
+
+
+def test_verify_window_whole_layer():
+    """config 2's shape: 96 rows through the whole layer on the prompt path (fused gate|up + SwiGLU), against the
+    combine of float64 products sampled per pair and the oracle's routing"""
+    shape = moe.LayerShape(H=2048, E=512, K=10, ff=512, wtype=orc.Q4_K, shared=True)
+    L, host = make_layer(shape, 11)
+    C = 96
+    x = orc.synth(C * shape.H, 18, 1.0).reshape(C, shape.H)
+    xd = torch.from_numpy(x).cuda()
+    y = torch.empty_like(xd)
+    b = moe.PrefillBuffers(shape, C)
+    moe.prefill_layer_mma(L, xd, y, b)
+    torch.cuda.synchronize()
+    lg = orc.router_logits(host.W, x)
+    oi, ow, _ = orc.topk(lg, shape.E, shape.K)
+    assert np.array_equal(b.topi.cpu().numpy(), oi)
+    x16 = f16_of(x)
+    yo = y.cpu().numpy()
+    for t in (0, 37, 95):
+        want = np.zeros(shape.H)
+        picks = [(int(e), float(w)) for e, w in zip(oi[t], ow[t])] + [(shape.E, 1 / (1 + np.exp(-float(lg[t, shape.E]))))]
+        for e, w in picks:
+            wg, _ = expert_rows(host, e, False)
+            gu = orc.mma_matvec(shape.wtype, wg, shape.H, 2 * shape.ff, x16[t].view(np.uint16))
+            hh = orc.swiglu_h16(gu.astype(np.float32), shape.ff)
+            wd, _ = expert_rows(host, e, True)
+            want += w * orc.mma_matvec(shape.wtype, wd, shape.ff, shape.H, hh)
+        assert np.abs(yo[t] - want).max() <= 2e-3 * np.abs(want).max(), t
+
+
+def test_q8_0_prefill_4096_sampled():
+    """config 4's prompt chunk: 4096 tokens through Q8_0 experts on the matrix cores, sampled pairs"""
+    shape = moe.LayerShape(H=2048, E=512, K=10, ff=512, wtype=orc.Q8_0, shared=True)
+    L, host, x, y, b = run_prefill(shape, 23, 4096)
+    eg, ed = check_sampled(host, x, b, 16, np.random.default_rng(3))
+    assert eg < 2e-3 and ed < 2e-3, (eg, ed)
