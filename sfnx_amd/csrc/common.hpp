@@ -133,6 +133,18 @@ __device__ __forceinline__ float load_agent(const float* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// ------------------------------------------------------------------------------------------------ L2 warm-up
+// Workgroup i of a launch runs on XCD i % 8, each XCD has its own 4 MB L2, and the L2 keeps clean lines across kernel
+// boundaries: a later launch's workgroup reads lines that an earlier launch's workgroup of the same XCD read from L2
+// instead of HBM.  A kernel warms lines for a later one by loading one dword of each 128-byte line straight into LDS
+// (global_load_lds: no register is written, the load cannot be dropped or moved); warm_wait() before the wavefront
+// ends, because the LDS it writes belongs to the workgroup.  `junk` is 256 bytes of LDS whose contents nobody reads.
+constexpr int XCDS = 8, LINE = 128;
+__device__ __forceinline__ void warm_line(const void* p, void* junk) {
+    __builtin_amdgcn_global_load_lds(p, (__attribute__((address_space(3))) void*) junk, 4, 0, 0);
+}
+__device__ __forceinline__ void warm_wait() { __builtin_amdgcn_s_waitcnt(0); }
+
 // ------------------------------------------------------------------------------------------------ planar store
 // byte offsets of row r's pieces inside one planar matrix of R rows x C columns
 struct Q4kPlanes {

@@ -42,7 +42,7 @@ template <int TYPE> constexpr int lpr_of() { return TYPE == SFNX_Q4_K ? 8 : 16; 
 template <int TYPE> constexpr int d2_threads() { return 32 * lpr_of<TYPE>(); }   // K2: 32 FF indices a block
 
 struct DecLayout {
-    size_t logits, xq, topi, topw, jg, jd, njobs, gu, hq_q, hq_d, hq_s, y, total;
+    size_t logits, xq, topi, topw, jg, jd, njobs, gu, hq_q, hq_d, hq_s, y, route_x, total;
 };
 DecLayout dec_layout(int T, int H, int E, int K, int ff) {
     const size_t P = (size_t) T * K, NP = P + T, nj = P + 1;
@@ -65,6 +65,7 @@ DecLayout dec_layout(int T, int H, int E, int K, int ff) {
     L.hq_d = take(NP * (ff / 32) * 4);
     L.hq_s = take(NP * (ff / 32) * 4);
     L.y = take((size_t) T * H * 4);
+    L.route_x = take((size_t) XCDS * 2 * MAX_K * 4);   // batch 1: the picks and weights, a copy an XCD
     L.total = o;
     return L;
 }
@@ -309,19 +310,33 @@ __global__ void __launch_bounds__(d2_threads<TYPE>()) k_dec_experts(
     PROFB(1, 1)
 }
 
+// K1's workgroup b' owns the router rows [D1_WAVES b', D1_WAVES b' + D1_WAVES), on XCD b' % 8.  Workgroup b of a launch
+// whose grid is a multiple of 8 warms the next layer's router rows of the K1 workgroups b' = b (mod the grid).
+__device__ inline void warm_router_rows(const float* W, int rows, int H, void* junk) {
+    if (W == nullptr || gridDim.x % XCDS != 0) return;
+    const int per_row = H * 4 / LINE, per_blk = D1_WAVES * per_row, nk1 = (rows + D1_WAVES - 1) / D1_WAVES;
+    const int mine = (nk1 - (int) blockIdx.x + (int) gridDim.x - 1) / (int) gridDim.x;
+    for (int li = threadIdx.x; li < mine * per_blk; li += blockDim.x) {
+        const int b1 = blockIdx.x + gridDim.x * (li / per_blk), row = D1_WAVES * b1 + (li % per_blk) / per_row;
+        if (row < rows) warm_line(reinterpret_cast<const uint8_t*>(W + (size_t) row * H) + LINE * (li % per_row), junk);
+    }
+}
+
 // K2 for a window of one row (the batch-1 decode): the picks of one token are distinct experts, so job j is pick j
 // (n = 1, row 0, output pair j) and the shared expert's job is the last; no numbering is needed.  Every wavefront takes
 // the top-K itself from registers, so the weight loads wait on no barrier after the routing.
 template <int TYPE, int G, int NV>
 __global__ void __launch_bounds__(2 * d2_threads<TYPE>()) k_dec_experts1(
-    const uint8_t* __restrict__ A, size_t sa, int H, int E, int K, int ff, int shared, const float* __restrict__ logits,
+    const uint8_t* __restrict__ A, size_t sa, const float* __restrict__ Wn, int H, int E, int K, int ff, int shared,
+    const float* __restrict__ logits,
     const uint8_t* __restrict__ xq, int* __restrict__ topi_g, float* __restrict__ topw_g, sfnx_job* __restrict__ jg,
     sfnx_job* __restrict__ jd, int* __restrict__ njobs_g, float* __restrict__ gu, int8_t* __restrict__ hq_q,
-    float* __restrict__ hq_d, int* __restrict__ hq_s) {
+    float* __restrict__ hq_d, int* __restrict__ hq_s, int* __restrict__ route_x) {
     constexpr int LPR = lpr_of<TYPE>(), NW = 2 * d2_threads<TYPE>() / WAVE, RPW = WAVE / LPR;
     const int NFB = ff / 32, myjob = blockIdx.x / NFB, fb = blockIdx.x % NFB;
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
     __shared__ float gbuf[32], ubuf[32];
+    __shared__ uint32_t junk[WAVE];
     extern __shared__ __align__(16) unsigned char lds[];
     PROF(1, 0)
     PROFB(1, 0)
@@ -330,6 +345,8 @@ __global__ void __launch_bounds__(2 * d2_threads<TYPE>()) k_dec_experts1(
     topk_load<NV>(logits, E / WAVE, lane, lv);
     const Acts a = acts_in(lds, 1, H);
     stage_q8_1(a, xq, nullptr, 1);
+    // the next layer's router rows into this XCD's L2 for that layer's K1, while HBM idles through the top-k
+    warm_router_rows(Wn, E + 1, H, junk);
     PROF(1, 7)
     int pick;
     uint32_t pord;
@@ -337,7 +354,10 @@ __global__ void __launch_bounds__(2 * d2_threads<TYPE>()) k_dec_experts1(
     const int nr = __popcll(__ballot(lane < K && pick >= 0));
     const int nj = nr + (shared ? 1 : 0);
     PROF(1, 1)
-    if (myjob >= nj && blockIdx.x != 0) return;
+    if (myjob >= nj && blockIdx.x >= XCDS) {
+        warm_wait();
+        return;
+    }
     const int ex = myjob < nr ? __builtin_amdgcn_readlane(pick, myjob) : E, out = myjob < nr ? myjob : K;
     // the first half of the waves take the 32 gate rows, the second half the matching up rows
     const bool up = wave >= NW / 2;
@@ -345,7 +365,15 @@ __global__ void __launch_bounds__(2 * d2_threads<TYPE>()) k_dec_experts1(
     const uint8_t* mat = A + (size_t) ex * sa;
     typename RowOf<TYPE, G>::R wr;
     if (myjob < nj) RowOf<TYPE, G>::issue(wr, mat, 2 * ff, row, H, ln);
-    if (blockIdx.x == 0 && wave == 0) {   // the routing, published for K3 and the caller, while the rows load
+    if (blockIdx.x < XCDS && wave == 0) {   // the routing, published for K3 and the caller, while the rows load
+        const float w = topk_weight(pick, pord, K);
+        // a copy for K3's workgroups of this XCD (workgroup b on XCD b % 8), read from this XCD's L2
+        if (lane < K) {
+            route_x[blockIdx.x * 2 * MAX_K + lane] = pick;
+            route_x[blockIdx.x * 2 * MAX_K + MAX_K + lane] = __float_as_int(w);
+        }
+    }
+    if (blockIdx.x == 0 && wave == 0) {
         const float w = topk_weight(pick, pord, K);
         if (lane < K) {
             topi_g[lane] = pick;
@@ -363,11 +391,13 @@ __global__ void __launch_bounds__(2 * d2_threads<TYPE>()) k_dec_experts1(
             njobs_g[1] = 0;
         }
     }
-    if (myjob >= nj) return;
+    if (myjob >= nj) {
+        warm_wait();
+        return;
+    }
     __syncthreads();   // the staged activations
-    wr.prepare(ln);
     PROF(1, 3)
-    const float v = group_sum<LPR>(wr.dot(a, 0, ln));
+    const float v = group_sum<LPR>(wr.dot1(a, ln));   // each group as it arrives
     if (ln == 0) {
         gu[(size_t) out * 2 * ff + row] = v;
         (up ? ubuf : gbuf)[fl] = v;
@@ -387,6 +417,7 @@ __global__ void __launch_bounds__(2 * d2_threads<TYPE>()) k_dec_experts1(
             hq_s[(size_t) out * NFB + fb] = qs;
         }
     }
+    warm_wait();
     PROF(1, 6)
     PROFB(1, 1)
 }
@@ -496,7 +527,7 @@ __global__ void __launch_bounds__(D3_THREADS) k_dec_down1(const uint8_t* __restr
                                                          const int* __restrict__ topi, const float* __restrict__ topw,
                                                          const int8_t* __restrict__ hq_q, const float* __restrict__ hq_d,
                                                          const int* __restrict__ hq_s, float* __restrict__ y,
-                                                         float* __restrict__ x) {
+                                                         float* __restrict__ x, const int* __restrict__ route_x) {
     constexpr int LPR = lpr_of<TYPE>(), GROUPS = D3_THREADS / LPR, HQ4 = 5, HQS = 3;
     const int row0 = blockIdx.x * D3_ROWS, nbh = ff / 32, lane = threadIdx.x % WAVE, tid = threadIdx.x;
     const int g = tid / LPR, ln = tid % LPR;
@@ -504,9 +535,10 @@ __global__ void __launch_bounds__(D3_THREADS) k_dec_down1(const uint8_t* __restr
     PROFB(2, 0)
     __shared__ float part[MAX_K + 1][D3_ROWS];
     extern __shared__ __align__(16) unsigned char lds[];
-    // every request first
-    const int tp = lane < K ? topi[lane] : -1;
-    const float twv = lane < K ? topw[lane] : 0.f;
+    // every request first; the picks from the copy K2 left in this XCD's L2
+    const int* rx = route_x + (blockIdx.x % XCDS) * 2 * MAX_K;
+    const int tp = lane < K ? rx[lane] : -1;
+    const float twv = lane < K ? __int_as_float(rx[MAX_K + lane]) : 0.f;
     const float gl = shared ? logits[E] : 0.f;
     const float xr = tid < D3_ROWS ? x[row0 + tid] : 0.f;
     const int NP = K + 1, nq = NP * ff / 16, ns = NP * nbh;
@@ -593,6 +625,7 @@ struct DecArgs {
     int H, E, K, ff, shared, T, norm;
     float eps;
     int phases;
+    const float* Wn;   // the next layer's router (warmed into L2 for that layer's K1), or null
 };
 
 // Optional kernel clock: when on, each decode kernel is launched with a start/stop event pair that the runtime
@@ -635,10 +668,10 @@ template <int TYPE, int G, int NV>
 void launch_k2_one(const DecArgs& d, const sfnx_moe_layer_w& w, const DecLayout& L, char* ws, hipStream_t s) {
     const int njmax = d.K + (d.shared ? 1 : 0);
     launch(1, k_dec_experts1<TYPE, G, NV>, dim3(njmax * (d.ff / 32)), dim3(2 * d2_threads<TYPE>()), acts_bytes(1, d.H), s,
-        (const uint8_t*) w.gu, w.gu_stride, d.H, d.E, d.K, d.ff, d.shared, (const float*) (ws + L.logits),
+        (const uint8_t*) w.gu, w.gu_stride, d.Wn, d.H, d.E, d.K, d.ff, d.shared, (const float*) (ws + L.logits),
         (const uint8_t*) (ws + L.xq), (int*) (ws + L.topi), (float*) (ws + L.topw), (sfnx_job*) (ws + L.jg),
         (sfnx_job*) (ws + L.jd), (int*) (ws + L.njobs), (float*) (ws + L.gu), (int8_t*) (ws + L.hq_q),
-        (float*) (ws + L.hq_d), (int*) (ws + L.hq_s));
+        (float*) (ws + L.hq_d), (int*) (ws + L.hq_s), (int*) (ws + L.route_x));
 }
 template <int TYPE, int G>
 void launch_k2_tt1(const DecArgs& d, const sfnx_moe_layer_w& w, const DecLayout& L, char* ws, hipStream_t s) {
@@ -652,7 +685,7 @@ void launch_k3_one(const DecArgs& d, const sfnx_moe_layer_w& w, float* x, const 
     launch(2, k_dec_down1<TYPE, G2, NB>, dim3(d.H / D3_ROWS), dim3(D3_THREADS), acts_bytes(d.K + 1, d.ff), s,
         (const uint8_t*) w.dn, w.dn_stride, d.H, d.E, d.K, d.ff, d.shared, (const float*) (ws + L.logits),
         (const int*) (ws + L.topi), (const float*) (ws + L.topw), (const int8_t*) (ws + L.hq_q),
-        (const float*) (ws + L.hq_d), (const int*) (ws + L.hq_s), (float*) (ws + L.y), x);
+        (const float*) (ws + L.hq_d), (const int*) (ws + L.hq_s), (float*) (ws + L.y), x, (const int*) (ws + L.route_x));
 }
 template <int TYPE, int G2, int NB>
 void launch_k3(const DecArgs& d, const sfnx_moe_layer_w& w, float* x, const DecLayout& L, char* ws, hipStream_t s) {
@@ -768,13 +801,15 @@ extern "C" int sfnx_moe_decode(const sfnx_moe_layer_w* layers, int n_layers, uin
             require(layers[l].gu_stride >= row_bytes(type, H) * 2 * (size_t) ff, "gate|up stride smaller than a matrix");
             require(layers[l].dn_stride >= row_bytes(type, ff) * (size_t) H, "down stride smaller than a matrix");
         }
-        const DecArgs d{type, H, E, K, ff, shared ? 1 : 0, T, norm ? 1 : 0, eps, phases ? phases : 7};
+        const DecArgs d{type, H, E, K, ff, shared ? 1 : 0, T, norm ? 1 : 0, eps, phases ? phases : 7, nullptr};
         hipStream_t s = stream_of(st);
         char* w = (char*) ws;
         for (int l = 0; l < n_layers; ++l) {
-            if (T == 1) launch_layer_tt<1>(d, layers[l], x, L, w, s);
-            else if (T <= 4) launch_layer_tt<4>(d, layers[l], x, L, w, s);
-            else launch_layer_tt<16>(d, layers[l], x, L, w, s);
+            DecArgs dl = d;
+            dl.Wn = l + 1 < n_layers ? layers[l + 1].W : nullptr;
+            if (T == 1) launch_layer_tt<1>(dl, layers[l], x, L, w, s);
+            else if (T <= 4) launch_layer_tt<4>(dl, layers[l], x, L, w, s);
+            else launch_layer_tt<16>(dl, layers[l], x, L, w, s);
         }
     });
 }

@@ -104,28 +104,44 @@ template <int GPL> struct Q4kRow {
         issue(P, row, C, l8);
         prepare(l8);
     }
+    // prepare() and dot(a, 0, l8) in one pass: a group's header decoded as the group is reached, so the work on the
+    // first groups overlaps the arrival of the later ones (the same values as prepare() then dot())
+    __device__ __forceinline__ float dot1(const Acts& a, int l8) {
+        float tmp = 0.f;
+#pragma unroll
+        for (int i = 0; i < GPL; ++i) {
+            d[i] = h2f((uint16_t) (h[i].x & 0xffff));
+            dmin[i] = h2f((uint16_t) (h[i].x >> 16));
+            q4k_scale_min(h[i], 2 * (l8 & 3), sc0[i], m0[i]);
+            q4k_scale_min(h[i], 2 * (l8 & 3) + 1, sc1[i], m1[i]);
+            tmp += group(a, 0, l8, i);
+        }
+        return tmp;
+    }
+    // group i of this lane's share of row . activation row j
+    __device__ __forceinline__ float group(const Acts& a, int j, int l8, int i) const {
+        const int kb0 = (2 * i + (l8 >> 2)) * 8 + 2 * (l8 & 3);
+        const int4 a00 = a.q4(j, kb0)[0], a01 = a.q4(j, kb0)[1], a10 = a.q4(j, kb0 + 1)[0], a11 = a.q4(j, kb0 + 1)[1];
+        const unsigned qw[8] = {q0[i].x, q0[i].y, q0[i].z, q0[i].w, q1[i].x, q1[i].y, q1[i].z, q1[i].w};
+        const int al[8] = {a00.x, a00.y, a00.z, a00.w, a01.x, a01.y, a01.z, a01.w};
+        const int ah[8] = {a10.x, a10.y, a10.z, a10.w, a11.x, a11.y, a11.z, a11.w};
+        int dl = 0, dh = 0;
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
+            dl = dot4((int) (qw[w] & 0x0F0F0F0Fu), al[w], dl);
+            dh = dot4((int) ((qw[w] >> 4) & 0x0F0F0F0Fu), ah[w], dh);
+        }
+        const int nb = a.K / 32;
+        const float d8l = a.d[j * nb + kb0], d8h = a.d[j * nb + kb0 + 1];
+        const float sl = (float) a.s[j * nb + kb0], sh = (float) a.s[j * nb + kb0 + 1];
+        return d[i] * (d8l * (sc0[i] * (float) dl) + d8h * (sc1[i] * (float) dh)) -
+               dmin[i] * (d8l * (m0[i] * sl) + d8h * (m1[i] * sh));
+    }
     // this lane's share of row . activation row j
     __device__ __forceinline__ float dot(const Acts& a, int j, int l8) const {
         float tmp = 0.f;
 #pragma unroll
-        for (int i = 0; i < GPL; ++i) {
-            const int kb0 = (2 * i + (l8 >> 2)) * 8 + 2 * (l8 & 3);
-            const int4 a00 = a.q4(j, kb0)[0], a01 = a.q4(j, kb0)[1], a10 = a.q4(j, kb0 + 1)[0], a11 = a.q4(j, kb0 + 1)[1];
-            const unsigned qw[8] = {q0[i].x, q0[i].y, q0[i].z, q0[i].w, q1[i].x, q1[i].y, q1[i].z, q1[i].w};
-            const int al[8] = {a00.x, a00.y, a00.z, a00.w, a01.x, a01.y, a01.z, a01.w};
-            const int ah[8] = {a10.x, a10.y, a10.z, a10.w, a11.x, a11.y, a11.z, a11.w};
-            int dl = 0, dh = 0;
-#pragma unroll
-            for (int w = 0; w < 8; ++w) {
-                dl = dot4((int) (qw[w] & 0x0F0F0F0Fu), al[w], dl);
-                dh = dot4((int) ((qw[w] >> 4) & 0x0F0F0F0Fu), ah[w], dh);
-            }
-            const int nb = a.K / 32;
-            const float d8l = a.d[j * nb + kb0], d8h = a.d[j * nb + kb0 + 1];
-            const float sl = (float) a.s[j * nb + kb0], sh = (float) a.s[j * nb + kb0 + 1];
-            tmp += d[i] * (d8l * (sc0[i] * (float) dl) + d8h * (sc1[i] * (float) dh)) -
-                   dmin[i] * (d8l * (m0[i] * sl) + d8h * (m1[i] * sh));
-        }
+        for (int i = 0; i < GPL; ++i) tmp += group(a, j, l8, i);
         return tmp;
     }
 };
@@ -152,6 +168,10 @@ template <int BPL> struct Q80Row {
     __device__ __forceinline__ void load(const Q80Planes& P, int row, int C, int l16) {
         issue(P, row, C, l16);
         prepare(l16);
+    }
+    __device__ __forceinline__ float dot1(const Acts& a, int l16) {
+        prepare(l16);
+        return dot(a, 0, l16);
     }
     __device__ __forceinline__ float dot(const Acts& a, int j, int l16) const {
         float acc = 0.f;

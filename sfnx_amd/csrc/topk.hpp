@@ -93,18 +93,25 @@ __device__ __forceinline__ void topk_load(const float* lg, int nv, int lane, flo
 
 // The top-K of one token's logits (lane l holds experts l + 64 i) by one wavefront: K rounds of the largest untaken
 // value, the lowest index among equal values (the reference's strict `>` scan, then `oi < bi` across lanes); NaN and
-// -inf are never taken (src/moe.cuh:128-162, src/prefill.cu:191-221).  Each lane sorts its keys once; a round is a
-// DPP maximum over the lanes' heads, the winner moving to its next key.  Weights exp(l_k - l_top1) / z
-// with z summed in pick order.  A round with nothing left gives index -1, weight 0.  Lane k < K returns pick k.
+// -inf are never taken (src/moe.cuh:128-162, src/prefill.cu:191-221).  A round is a DPP maximum over the lanes' heads,
+// the winner moving to its next key.  Lane k < K returns pick k; a round with nothing left gives index -1.
+//
+// The rounds run on one 32-bit key: the value's order bits above bit 10 (its upper 22 bits), the complemented index
+// below (E <= 1024), each lane's keys sorted once.  Those rounds pick the top K exactly in that key's order.  The exact
+// top K can differ only if an untaken value shares its upper 22 bits with the last pick, or two picks share them (their
+// order then rests on the dropped bits): both are checked, and either one redoes the selection on exact 64-bit keys.
 template <int NV>
 __device__ inline void topk_picks(const float (&lv)[NV], int K, int lane, int& pick, uint32_t& pord) {
-    uint64_t key[NV];
+    uint32_t tk[NV];
 #pragma unroll
-    for (int i = 0; i < NV; ++i) key[i] = pick_key(lv[i], lane + WAVE * i);
+    for (int i = 0; i < NV; ++i) {
+        const uint32_t o = (uint32_t) (pick_key(lv[i], 0) >> 32);
+        tk[i] = o ? (o & 0xFFFFFC00u) | (1023u - (uint32_t) (lane + WAVE * i)) : 0u;
+    }
 #ifdef SFNX_TOPK_STAMP
     SFNX_TOPK_STAMP(0)
 #endif
-    // descending bitonic sort of the lane's keys (value, then the lower index first)
+    // descending bitonic sort of the lane's keys
 #pragma unroll
     for (int k = 2; k <= NV; k *= 2)
 #pragma unroll
@@ -113,84 +120,85 @@ __device__ inline void topk_picks(const float (&lv)[NV], int K, int lane, int& p
             for (int i = 0; i < NV; ++i) {
                 const int l = i ^ j;
                 if (l > i) {
+                    const uint32_t a = tk[i], b = tk[l];
                     const bool desc = (i & k) == 0;
-                    const uint64_t a = key[i], b = key[l];
-                    const bool sw = desc ? a < b : a > b;
-                    key[i] = sw ? b : a;
-                    key[l] = sw ? a : b;
+                    tk[i] = desc ? max(a, b) : min(a, b);
+                    tk[l] = desc ? min(a, b) : max(a, b);
                 }
             }
-    uint32_t ord[NV], idx[NV];   // an empty slot: ord 0, index ~0
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        ord[i] = (uint32_t) (key[i] >> 32);
-        idx[i] = ~(uint32_t) key[i];
-    }
 #ifdef SFNX_TOPK_STAMP
     SFNX_TOPK_STAMP(1)
 #endif
-    uint32_t mine = 0, myidx = ~0u;
-    {
-        // Fast rounds on one 32-bit key: the value's order bits above bit 10, the complemented index below (E <= 1024),
-        // so one DPP maximum finds each round's winner.  The picks are then checked exactly (descending in (value,
-        // index) order, and no lane's remaining head above the last pick); a failed check (heads sharing their upper 22
-        // order bits) redoes the selection with the exact rounds.
-        uint32_t tk[NV];
+    uint32_t mk = 0;
+    for (int k = 0; k < K; ++k) {
+        const uint32_t best = wave_max_u32(tk[0]);
+        if (lane == k) mk = best;
+        // the winner's keys move up a slot: one v_cndmask a slot on the winner mask (written as such: the compiler
+        // otherwise turns the shift into per-slot index selects, several times longer)
+        const uint64_t won = __ballot(tk[0] == best);
+        asm volatile("s_nop 2" ::"s"(won));   // the mask's VALU write before its reads as a select mask
 #pragma unroll
-        for (int i = 0; i < NV; ++i) tk[i] = ord[i] ? (ord[i] & 0xFFFFFC00u) | (1023u - idx[i]) : 0u;
-        uint32_t mk = 0;
-        int popped = 0;
-        for (int k = 0; k < K; ++k) {
-            const uint32_t best = wave_max_u32(tk[0]);
-            if (lane == k) mk = best;
-            const bool won = tk[0] == best;
-            popped += won;
+        for (int i = 0; i + 1 < NV; ++i) asm volatile("v_cndmask_b32_e64 %0, %0, %1, %2" : "+v"(tk[i]) : "v"(tk[i + 1]), "s"(won));
+        asm volatile("v_cndmask_b32_e64 %0, %0, 0, %1" : "+v"(tk[NV - 1]) : "s"(won));
+    }
+    // each pick's exact order bits, from the lane and slot that held it
+    const uint32_t pi = mk ? 1023u - (mk & 1023u) : ~0u;
+    uint32_t po = 0;
 #pragma unroll
-            for (int i = 0; i + 1 < NV; ++i) tk[i] = won ? tk[i + 1] : tk[i];
-            tk[NV - 1] = won ? 0u : tk[NV - 1];
-        }
-        // each pick's exact order bits, from the lane and slot that held it
-        const uint32_t pi = mk ? 1023u - (mk & 1023u) : ~0u;
-        uint32_t po = 0;
+    for (int i = 0; i < NV; ++i) {
+        const uint32_t o = (uint32_t) __shfl((int) (uint32_t) (pick_key(lv[i], 0) >> 32), (int) (pi & 63u));
+        po = (pi >> 6) == (uint32_t) i ? o : po;
+    }
+    const uint64_t pk = mk ? ((uint64_t) po << 32) | ~pi : 0;
+    const uint32_t nlo = (uint32_t) dpp_mov<0x101>((int) (uint32_t) pk), nhi = (uint32_t) dpp_mov<0x101>((int) (pk >> 32));
+    const uint64_t next = ((uint64_t) nhi << 32) | nlo;   // pick k + 1 (row_shl:1; K <= 16 keeps it in row 0)
+    const uint32_t last = (uint32_t) __builtin_amdgcn_readlane((int) mk, K - 1);
+    // tk[0] is now this lane's largest untaken key
+    const bool bad = (lane + 1 < K && next != 0 && !(pk > next)) || last == 0u ||
+                     (tk[0] & 0xFFFFFC00u) == (last & 0xFFFFFC00u);
+    uint32_t mine = (uint32_t) (pk >> 32), myidx = pk ? pi : ~0u;
+    if (__ballot(bad) != 0) {   // exact rounds on 64-bit keys: the maximum value, then the lowest index holding it
+        uint64_t key[NV];
+#pragma unroll
+        for (int i = 0; i < NV; ++i) key[i] = pick_key(lv[i], lane + WAVE * i);
+#pragma unroll
+        for (int k = 2; k <= NV; k *= 2)
+#pragma unroll
+            for (int j = k / 2; j > 0; j /= 2)
+#pragma unroll
+                for (int i = 0; i < NV; ++i) {
+                    const int l = i ^ j;
+                    if (l > i) {
+                        const bool desc = (i & k) == 0;
+                        const uint64_t a = key[i], b = key[l];
+                        const bool sw = desc ? a < b : a > b;
+                        key[i] = sw ? b : a;
+                        key[l] = sw ? a : b;
+                    }
+                }
+        uint32_t ord[NV], idx[NV];   // an empty slot: ord 0, index ~0
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
-            const uint32_t o = (uint32_t) __shfl((int) (uint32_t) (pick_key(lv[i], 0) >> 32), (int) (pi & 63u));
-            po = (pi >> 6) == (uint32_t) i ? o : po;
+            ord[i] = (uint32_t) (key[i] >> 32);
+            idx[i] = ~(uint32_t) key[i];
         }
-        const uint64_t pk = mk ? ((uint64_t) po << 32) | ~pi : 0;
-        // this lane's first key not taken
-        uint64_t head = 0;
-#pragma unroll
-        for (int i = 0; i < NV; ++i) head = popped == i ? ((uint64_t) ord[i] << 32) | ~idx[i] : head;
-        head = (popped < NV && ord[popped < NV ? popped : 0]) ? head : 0;
-        const uint32_t nlo = (uint32_t) dpp_mov<0x101>((int) (uint32_t) pk), nhi = (uint32_t) dpp_mov<0x101>((int) (pk >> 32));
-        const uint64_t next = ((uint64_t) nhi << 32) | nlo;   // pick k + 1 (row_shl:1; K <= 16 keeps it in row 0)
-        const uint32_t llo = (uint32_t) __builtin_amdgcn_readlane((int) (uint32_t) pk, K - 1);
-        const uint32_t lhi = (uint32_t) __builtin_amdgcn_readlane((int) (pk >> 32), K - 1);
-        const uint64_t last = ((uint64_t) lhi << 32) | llo;
-        const bool bad = (lane + 1 < K && next != 0 && !(pk > next)) || head > last;
-        const bool clash = __ballot(bad) != 0;
-        mine = (uint32_t) (pk >> 32);
-        myidx = pk ? pi : ~0u;
-        if (clash) {   // exact rounds: the maximum value, then the lowest index holding it
-            mine = 0;
-            myidx = ~0u;
-            for (int k = 0; k < K; ++k) {
-                const uint32_t best = wave_max_u32(ord[0]);
-                const uint32_t wi = wave_min_u32(ord[0] == best ? idx[0] : ~0u);
-                if (lane == k) {
-                    mine = best;
-                    myidx = wi;
-                }
-                const bool won = idx[0] == wi;
-#pragma unroll
-                for (int i = 0; i + 1 < NV; ++i) {
-                    ord[i] = won ? ord[i + 1] : ord[i];
-                    idx[i] = won ? idx[i + 1] : idx[i];
-                }
-                ord[NV - 1] = won ? 0u : ord[NV - 1];
-                idx[NV - 1] = won ? ~0u : idx[NV - 1];
+        mine = 0;
+        myidx = ~0u;
+        for (int k = 0; k < K; ++k) {
+            const uint32_t best = wave_max_u32(ord[0]);
+            const uint32_t wi = wave_min_u32(ord[0] == best ? idx[0] : ~0u);
+            if (lane == k) {
+                mine = best;
+                myidx = wi;
             }
+            const bool won = idx[0] == wi;
+#pragma unroll
+            for (int i = 0; i + 1 < NV; ++i) {
+                ord[i] = won ? ord[i + 1] : ord[i];
+                idx[i] = won ? idx[i + 1] : idx[i];
+            }
+            ord[NV - 1] = won ? 0u : ord[NV - 1];
+            idx[NV - 1] = won ? ~0u : idx[NV - 1];
         }
     }
 #ifdef SFNX_TOPK_STAMP
