@@ -16,8 +16,8 @@ namespace sfnx {
 namespace {
 
 #ifdef SFNX_PHASE_PROF
-__device__ unsigned long long g_mma_prof[512][20];   // wall-clock stamps of blocks (blockIdx.y < 512, x == 0)
-#define MPROF(i) if (threadIdx.x == 0 && blockIdx.x == 0 && blockIdx.y < 512) g_mma_prof[blockIdx.y][i] = wall_clock64();
+__device__ unsigned long long g_mma_prof[512][20];   // wall-clock stamps of blocks (job < 512, slice 0)
+#define MPROF(i) if (threadIdx.x == 0 && pj >= 0) g_mma_prof[pj][i] = wall_clock64();
 #else
 #define MPROF(i)
 #endif
@@ -190,7 +190,8 @@ __device__ __forceinline__ void mma_run(const RunW<TYPE>& w, const _Float16* xb,
 template <int TYPE, int NT>
 __device__ __forceinline__ void mma_job(const uint8_t* mat, int R, int C, int row0, int G, int wave, int lane,
                                         const sfnx_bigjob& jb, const _Float16* __restrict__ x, int ldx, _Float16* xs,
-                                        float* __restrict__ out) {
+                                        float* __restrict__ out, int pj) {
+    (void) pj;   // the job's row of phase stamps in the instrumented build, or -1
     const int h = lane / 32, nn = lane % 32, nr = C / MM_RUN, total = G * nr;
     auto row_of = [&](int it) { return row0 + (it / nr) * MM_BM + wave * 32 + nn; };
     RunW<TYPE> w, wn;
@@ -297,12 +298,24 @@ __device__ __forceinline__ void mma_gu_job(const uint8_t* mat, int ff, int C, in
     }
 }
 
+// Workgroup b runs on XCD b % 8.  The grid is 1-D: a job's row slices and MM_XG consecutive jobs (an expert's jobs
+// are consecutive) go to one XCD and are dispatched together, so an expert's weight rows come from HBM once for all its
+// jobs in the group and from that XCD's L2 for the rest, and the slices share the staged activation rows.
+constexpr int MM_XG = 4;
+__device__ __forceinline__ void xcd_job(int b, int nsl, int& slice, int& job) {
+    const int x = b % XCDS, k = b / XCDS, m = k / nsl;
+    slice = k % nsl;
+    job = MM_XG * (XCDS * (m / MM_XG) + x) + m % MM_XG;
+}
+inline int xcd_grid(int nsl, int njobs_cap) { return nsl * ((njobs_cap + XCDS * MM_XG - 1) / (XCDS * MM_XG)) * XCDS * MM_XG; }
+
 template <int TYPE>
 __global__ void __launch_bounds__(MM_THREADS) k_moe_mma_gu(const uint8_t* __restrict__ A, size_t sa, int ff, int C,
                                                           const sfnx_bigjob* __restrict__ jobs, const int* __restrict__ njobs,
                                                           const _Float16* __restrict__ x, float* __restrict__ gu,
                                                           _Float16* __restrict__ h16) {
-    const int ji = blockIdx.y;
+    int sl, ji;
+    xcd_job(blockIdx.x, ff / MM_BM, sl, ji);
     if (ji >= *njobs) return;
     __shared__ sfnx_bigjob jb;
     extern __shared__ __align__(16) unsigned char xs_raw[];
@@ -311,15 +324,17 @@ __global__ void __launch_bounds__(MM_THREADS) k_moe_mma_gu(const uint8_t* __rest
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
     const uint8_t* mat = A + (size_t) jb.w * sa;
     _Float16* xs = reinterpret_cast<_Float16*>(xs_raw);
-    if (jb.n > 32) mma_gu_job<TYPE, 2>(mat, ff, C, blockIdx.x * MM_BM, wave, lane, jb, x, xs, gu, h16);
-    else mma_gu_job<TYPE, 1>(mat, ff, C, blockIdx.x * MM_BM, wave, lane, jb, x, xs, gu, h16);
+    if (jb.n > 32) mma_gu_job<TYPE, 2>(mat, ff, C, sl * MM_BM, wave, lane, jb, x, xs, gu, h16);
+    else mma_gu_job<TYPE, 1>(mat, ff, C, sl * MM_BM, wave, lane, jb, x, xs, gu, h16);
 }
 
 template <int TYPE>
 __global__ void __launch_bounds__(MM_THREADS) k_moe_mma(const uint8_t* __restrict__ A, size_t sa, int R, int C, int G,
                                                        const sfnx_bigjob* __restrict__ jobs, const int* __restrict__ njobs,
                                                        const _Float16* __restrict__ x, float* __restrict__ out) {
-    const int ji = blockIdx.y;
+    int sl, ji;
+    xcd_job(blockIdx.x, R / (G * MM_BM), sl, ji);
+    const int pj = sl == 0 && ji < 512 ? ji : -1;
     MPROF(0)
     if (ji >= *njobs) return;
     __shared__ sfnx_bigjob jb;
@@ -329,10 +344,10 @@ __global__ void __launch_bounds__(MM_THREADS) k_moe_mma(const uint8_t* __restric
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
     const uint8_t* mat = A + (size_t) jb.w * sa;
     _Float16* xs = reinterpret_cast<_Float16*>(xs_raw);
-    const int row0 = blockIdx.x * G * MM_BM;
+    const int row0 = sl * G * MM_BM;
     MPROF(1)
-    if (jb.n > 32) mma_job<TYPE, 2>(mat, R, C, row0, G, wave, lane, jb, x, C, xs, out);
-    else mma_job<TYPE, 1>(mat, R, C, row0, G, wave, lane, jb, x, C, xs, out);
+    if (jb.n > 32) mma_job<TYPE, 2>(mat, R, C, row0, G, wave, lane, jb, x, C, xs, out, pj);
+    else mma_job<TYPE, 1>(mat, R, C, row0, G, wave, lane, jb, x, C, xs, out, pj);
     MPROF(18)
 }
 
@@ -359,12 +374,12 @@ void moe_mma(uint32_t type, const void* A, size_t sa, int n_in, int n_out, const
     require(n_out > 0 && n_out % MM_BM == 0, "expert rows must be a multiple of 256");
     require((n_out / MM_BM) % std::max(1, (n_out / MM_BM) / 2) == 0, "row groups must split evenly");
     require(sa >= row_bytes(type, n_in) * (size_t) n_out, "expert stride smaller than a matrix");
-    require(njobs_cap >= 0 && njobs_cap <= 65535, "njobs_cap out of range");
+    require(njobs_cap >= 0 && njobs_cap <= (1 << 20), "njobs_cap out of range");
     if (njobs_cap == 0) return;
     // groups of 256 rows a block: every row in one block when one run covers the input (the activations are staged
     // once); else two blocks a job, for more blocks than compute units
     const int groups = n_out / MM_BM, G = n_in == MM_RUN ? groups : std::max(1, groups / 2);
-    const dim3 grid(groups / G, njobs_cap);
+    const dim3 grid(xcd_grid(groups / G, njobs_cap));
     hipStream_t s = stream_of(st);
     if (type == SFNX_Q4_K)
         k_moe_mma<SFNX_Q4_K><<<grid, MM_THREADS, MM_LDS, s>>>((const uint8_t*) A, sa, n_out, n_in, G, jobs, njobs, (const _Float16*) x16, out);
@@ -378,9 +393,9 @@ void moe_mma_gu(uint32_t type, const void* A, size_t sa, int n_in, int ff, const
     require(n_in > 0 && n_in % 512 == 0, "expert input width must be a multiple of 512");
     require(ff > 0 && ff % MM_BM == 0, "FF must be a multiple of 256");
     require(sa >= row_bytes(type, n_in) * (size_t) (2 * ff), "expert stride smaller than a matrix");
-    require(njobs_cap >= 0 && njobs_cap <= 65535, "njobs_cap out of range");
+    require(njobs_cap >= 0 && njobs_cap <= (1 << 20), "njobs_cap out of range");
     if (njobs_cap == 0) return;
-    const dim3 grid(ff / MM_BM, njobs_cap);
+    const dim3 grid(xcd_grid(ff / MM_BM, njobs_cap));
     hipStream_t s = stream_of(st);
     if (type == SFNX_Q4_K)
         k_moe_mma_gu<SFNX_Q4_K><<<grid, MM_THREADS, MM_LDS, s>>>((const uint8_t*) A, sa, ff, n_in, jobs, njobs,

@@ -120,18 +120,94 @@ __global__ void __launch_bounds__(RR_THREADS) k_router_route(const float* __rest
 }
 
 // any number of tokens: a wavefront per row and token block of up to 8 tokens (the prompt path's router)
+// The xor butterfly of group_sum<64> applied to NV partial sums a lane at once, by recursive halving: at the level of
+// lane bit b a lane keeps the half of its values selected by that bit and adds its partner's copy of them, so each
+// value meets exactly the partners (and tree) group_sum would give it.  Lane l ends with value l >> (6 - log2 NV), in
+// every lane of its group of 64 / NV.
+template <int O, int N> __device__ __forceinline__ void halve(float (&v)[N], int n, int lane) {
+    const bool up = lane & O;
+#pragma unroll
+    for (int j = 0; j < N / 2; ++j)
+        if (j < n / 2) {
+            const float lo = v[j], hi = v[j + n / 2];
+            v[j] = (up ? hi : lo) + lane_xor<O>(up ? lo : hi);
+        }
+}
+template <int NV> __device__ __forceinline__ float reduce_scatter(float (&v)[NV], int lane) {
+    int n = NV;
+    if (n > 1) { halve<32>(v, n, lane); n /= 2; } else v[0] += lane_xor<32>(v[0]);
+    if (n > 1) { halve<16>(v, n, lane); n /= 2; } else v[0] += lane_xor<16>(v[0]);
+    if (n > 1) { halve<8>(v, n, lane); n /= 2; } else v[0] += lane_xor<8>(v[0]);
+    if (n > 1) { halve<4>(v, n, lane); n /= 2; } else v[0] += lane_xor<4>(v[0]);
+    if (n > 1) { halve<2>(v, n, lane); n /= 2; } else v[0] += lane_xor<2>(v[0]);
+    if (n > 1) { halve<1>(v, n, lane); n /= 2; } else v[0] += lane_xor<1>(v[0]);
+    return v[0];
+}
+
+// Prompt-path router logits [T][L] = W x, each (token, row) with row_dot's arithmetic (lane l's fmaf chain over its
+// float4 chunks l + 64 i, then the xor butterfly), register-blocked: a wavefront keeps RT router rows in registers and
+// takes the block's tokens LT_RU at a time from LDS, where the block stages them by asynchronous global -> LDS copies
+// into LT_NBUF buffers (LT_NBUF - 1 groups in flight while one computes); the RT x LT_RU sums of a lane leave through
+// one reduce_scatter.  A block: 4 wavefronts, 4 RT rows, LT_TOK tokens.
+constexpr int LT_THREADS = 256, LT_WAVES = LT_THREADS / WAVE, LT_RU = 4, LT_NBUF = 2, LT_TOK = 128;
 template <int NC>
-__global__ void __launch_bounds__(RR_THREADS) k_router_logits(const float* __restrict__ W, const float* __restrict__ x,
+__global__ void __launch_bounds__(LT_THREADS) k_router_logits(const float* __restrict__ W, const float* __restrict__ x,
                                                              float* __restrict__ logits, int T, int L) {
-    constexpr int H = NC * 4 * WAVE, TB = 8;
+    constexpr int H = NC * 4 * WAVE, RT = NC <= 8 ? 4 : 2, NV = RT * LT_RU;
+    constexpr int PER = LT_RU * H / 4, COPIES = PER / LT_THREADS;   // float4 a group; copies a wavefront issues a group
+    static_assert(PER % LT_THREADS == 0, "a group is whole copies");
+    extern __shared__ __align__(16) unsigned char lds[];
+    float* xs = reinterpret_cast<float*>(lds);   // [LT_NBUF][LT_RU][H]
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-    const int row = blockIdx.x * RR_WAVES + wave, t0 = blockIdx.y * TB;
-    if (row >= L) return;
-    float4 wv[NC];
-    row_load<NC>(W + (size_t) row * H, lane, wv);
-    for (int t = t0; t < min(T, t0 + TB); ++t) {
-        const float s = row_dot<NC>(wv, x + (size_t) t * H, lane);
-        if (lane == 0) logits[(size_t) t * L + row] = s;
+    const int row0 = (blockIdx.x * LT_WAVES + wave) * RT, t0 = blockIdx.y * LT_TOK, nt = min(LT_TOK, T - t0);
+    const int ng = (nt + LT_RU - 1) / LT_RU;
+    // group g's LT_RU token rows into buffer g % LT_NBUF (tokens past the end repeat the last); a wavefront moves 64
+    // float4 a copy
+    auto stage = [&](int g) {
+#pragma unroll
+        for (int k = 0; k < COPIES; ++k) {
+            const int c = (k * LT_WAVES + wave) * WAVE, u = c / (H / 4), col = c % (H / 4);
+            const int t = t0 + min(g * LT_RU + u, nt - 1);
+            __builtin_amdgcn_global_load_lds(x + (size_t) t * H + 4 * (col + lane),
+                                             (__attribute__((address_space(3))) void*) (xs + (size_t) ((g % LT_NBUF) * LT_RU + u) * H + 4 * col),
+                                             16, 0, 0);
+        }
+    };
+    float4 wv[RT][NC];
+#pragma unroll
+    for (int q = 0; q < RT; ++q) row_load<NC>(W + (size_t) min(row0 + q, L - 1) * H, lane, wv[q]);
+    for (int g = 0; g < LT_NBUF - 1; ++g)
+        if (g < ng) stage(g);
+    for (int g = 0; g < ng; ++g) {
+        // group g's copies landed: the ones issued after it (groups g + 1 .. g + LT_NBUF - 2) may still be in flight
+        if (g + LT_NBUF - 2 < ng) __builtin_amdgcn_s_waitcnt(0x0F70 | (COPIES * (LT_NBUF - 2)));
+        else __builtin_amdgcn_s_waitcnt(0x0F70);
+        __syncthreads();   // every wavefront's copies landed; every wavefront is past group g - 1, whose buffer refills
+        if (g + LT_NBUF - 1 < ng) stage(g + LT_NBUF - 1);
+        const float4* xb = reinterpret_cast<const float4*>(xs + (size_t) (g % LT_NBUF) * LT_RU * H);
+        float acc[NV];
+#pragma unroll
+        for (int k = 0; k < NV; ++k) acc[k] = 0.f;
+#pragma unroll
+        for (int i = 0; i < NC; ++i) {
+            float4 xv[LT_RU];
+#pragma unroll
+            for (int u = 0; u < LT_RU; ++u) xv[u] = xb[u * (H / 4) + i * WAVE + lane];
+#pragma unroll
+            for (int q = 0; q < RT; ++q)
+#pragma unroll
+                for (int u = 0; u < LT_RU; ++u) {
+                    float& a = acc[q * LT_RU + u];
+                    a = fmaf(wv[q][i].x, xv[u].x, a);
+                    a = fmaf(wv[q][i].y, xv[u].y, a);
+                    a = fmaf(wv[q][i].z, xv[u].z, a);
+                    a = fmaf(wv[q][i].w, xv[u].w, a);
+                }
+        }
+        const float v = reduce_scatter<NV>(acc, lane);
+        constexpr int SH = NV == 16 ? 2 : NV == 8 ? 3 : 4;   // lane l holds value l >> SH
+        const int k = lane >> SH, q = k / LT_RU, u = k % LT_RU, t = g * LT_RU + u;
+        if ((lane & ((1 << SH) - 1)) == 0 && row0 + q < L && t < nt) logits[(size_t) (t0 + t) * L + row0 + q] = v;
     }
 }
 
@@ -175,44 +251,61 @@ __global__ void k_pf_jobbase(const int* __restrict__ cnt, int* __restrict__ jbas
     if (e < E) jbase[e] = s[e] - nj;
     if (e == (int) blockDim.x - 1) njobs[0] = s[e] + (shared ? (C + SFNX_PF_JOB - 1) / SFNX_PF_JOB : 0);
 }
-// src/prefill.cu:248-279 k_pf_fill: a block per expert scans the pairs in index order, a ballot prefix per pass, so a
-// pair always lands in the same job and slot
-constexpr int PF_FILL_THREADS = 256;
+// src/prefill.cu:248-279 k_pf_fill: a block per expert scans the pairs in index order, 4 consecutive pairs a thread and
+// 1024 a pass, its slots from a prefix over the threads of the pass (ballots of the count bits, then the wavefronts in
+// order), so a pair always lands in the same job and slot
+constexpr int PF_FILL_THREADS = 256, PF_FILL_PASS = 4 * PF_FILL_THREADS;
 __global__ void __launch_bounds__(PF_FILL_THREADS) k_pf_fill(const int* __restrict__ topi, int P, int K,
                                                             const int* __restrict__ cnt, const int* __restrict__ jbase,
                                                             sfnx_bigjob* __restrict__ gu, sfnx_bigjob* __restrict__ dn) {
     const int e = blockIdx.x, tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE;
     const int ce = cnt[e];
     if (ce == 0) return;
-    __shared__ int wcount[PF_FILL_THREADS / WAVE];
+    __shared__ int wcount[2][PF_FILL_THREADS / WAVE];
+    const uint64_t lt = (1ull << lane) - 1ull;
     int base = 0;
-    for (int p0 = 0; p0 < P; p0 += PF_FILL_THREADS) {
-        const int p = p0 + tid;
-        const bool mine = p < P && topi[p] == e;
-        const uint64_t m = __ballot(mine);
-        if (lane == 0) wcount[wave] = __popcll(m);
+    for (int p0 = 0, it = 0; p0 < P; p0 += PF_FILL_PASS, ++it) {
+        const int p = p0 + 4 * tid;
+        int q[4];
+        if (p + 3 < P) {
+            const int4 v = *reinterpret_cast<const int4*>(topi + p);   // P is a multiple of 4 or the tail is scalar
+            q[0] = v.x, q[1] = v.y, q[2] = v.z, q[3] = v.w;
+        } else {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) q[c] = p + c < P ? topi[p + c] : -1;
+        }
+        int mine = 0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) mine += q[c] == e;
+        // this thread's exclusive prefix within its wavefront: the count's bits by ballot
+        const uint64_t b0 = __ballot(mine & 1), b1 = __ballot(mine & 2), b2 = __ballot(mine & 4);
+        const int before_w = __popcll(b0 & lt) + 2 * __popcll(b1 & lt) + 4 * __popcll(b2 & lt);
+        const int total_w = __popcll(b0) + 2 * __popcll(b1) + 4 * __popcll(b2);
+        if (lane == 0) wcount[it & 1][wave] = total_w;
         __syncthreads();
-        int before = 0, total = 0;
+        int before = before_w, total = 0;
 #pragma unroll
         for (int w = 0; w < PF_FILL_THREADS / WAVE; ++w) {
-            before += w < wave ? wcount[w] : 0;
-            total += wcount[w];
+            before += w < wave ? wcount[it & 1][w] : 0;
+            total += wcount[it & 1][w];
         }
-        if (mine) {
-            const int s = base + before + __popcll(m & ((1ull << lane) - 1ull));
-            const int j = jbase[e] + s / SFNX_PF_JOB, k = s % SFNX_PF_JOB;
-            gu[j].y[k] = p / K;
-            gu[j].out[k] = p;
-            dn[j].y[k] = p;
-            dn[j].out[k] = p;
-            if (k == 0) {
-                const int n = min(SFNX_PF_JOB, ce - (s / SFNX_PF_JOB) * SFNX_PF_JOB);
-                gu[j].w = dn[j].w = e;
-                gu[j].n = dn[j].n = n;
+        int s = base + before;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            if (q[c] == e) {
+                const int pc = p + c, j = jbase[e] + s / SFNX_PF_JOB, k = s % SFNX_PF_JOB;
+                gu[j].y[k] = pc / K;
+                gu[j].out[k] = pc;
+                dn[j].y[k] = pc;
+                dn[j].out[k] = pc;
+                if (k == 0) {
+                    const int n = min(SFNX_PF_JOB, ce - (s / SFNX_PF_JOB) * SFNX_PF_JOB);
+                    gu[j].w = dn[j].w = e;
+                    gu[j].n = dn[j].n = n;
+                }
+                ++s;
             }
-        }
         base += total;
-        __syncthreads();
     }
 }
 // the shared expert's jobs after the routed ones: tokens in order, 64 a job
@@ -232,17 +325,38 @@ __global__ void k_pf_shared(int C, int P, int E, const int* __restrict__ njobs, 
 
 // ------------------------------------------------------------------------------------------------ combine
 // src/kernels.cu:797-803 ring_x / src/prefill.cu:476-484 k_pfr_addend
-__global__ void k_combine(const float* __restrict__ part, const float* __restrict__ topw, const int* __restrict__ topi,
-                          const float* __restrict__ logits, float* __restrict__ y, int T, int H, int E, int K, int shared) {
-    const size_t n = (size_t) T * H;
-    for (size_t q = blockIdx.x * (size_t) blockDim.x + threadIdx.x; q < n; q += (size_t) gridDim.x * blockDim.x) {
-        const int t = (int) (q / H), i = (int) (q % H);
-        float s = 0.f;
-        for (int k = 0; k < K; ++k)
-            if (topi[t * K + k] >= 0) s = fmaf(topw[t * K + k], part[((size_t) t * K + k) * H + i], s);
-        if (shared) s = fmaf(sigm_f(logits[(size_t) t * (E + 1) + E]), part[((size_t) T * K + t) * H + i], s);
-        y[q] = s;
+// The combine (src/kernels.cu:797-803, src/prefill.cu:476-484): y[t][i] = fmaf(sigmoid(l[t][E]), part[T K + t][i],
+// sum_k fmaf(w[t][k], part[t K + k][i], .)) in k order, picks of -1 skipped.  A block per (token, 1024 columns): the
+// token's picks and weights are wave-uniform, and a thread's 4 columns of every part row are requested before the chain.
+constexpr int CB_THREADS = 256;
+__global__ void __launch_bounds__(CB_THREADS) k_combine(const float* __restrict__ part, const float* __restrict__ topw,
+                                                       const int* __restrict__ topi, const float* __restrict__ logits,
+                                                       float* __restrict__ y, int T, int H, int E, int K, int shared) {
+    const int t = blockIdx.y, i = (blockIdx.x * CB_THREADS + threadIdx.x) * 4;
+    if (i >= H) return;
+    float4 pv[MAX_K + 1];
+#pragma unroll
+    for (int k = 0; k < MAX_K; ++k)
+        if (k < K) pv[k] = *reinterpret_cast<const float4*>(part + ((size_t) t * K + k) * H + i);
+    if (shared) pv[MAX_K] = *reinterpret_cast<const float4*>(part + ((size_t) T * K + t) * H + i);
+    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int k = 0; k < MAX_K; ++k)
+        if (k < K && topi[t * K + k] >= 0) {
+            const float w = topw[t * K + k];
+            s.x = fmaf(w, pv[k].x, s.x);
+            s.y = fmaf(w, pv[k].y, s.y);
+            s.z = fmaf(w, pv[k].z, s.z);
+            s.w = fmaf(w, pv[k].w, s.w);
+        }
+    if (shared) {
+        const float g = sigm_f(logits[(size_t) t * (E + 1) + E]);
+        s.x = fmaf(g, pv[MAX_K].x, s.x);
+        s.y = fmaf(g, pv[MAX_K].y, s.y);
+        s.z = fmaf(g, pv[MAX_K].z, s.z);
+        s.w = fmaf(g, pv[MAX_K].w, s.w);
     }
+    *reinterpret_cast<float4*>(y + (size_t) t * H + i) = s;
 }
 
 // the stacked-layer driver's glue between MoE layers: x += y, then xn = x / sqrt(mean(x^2) + eps) (an RMSNorm without
@@ -318,13 +432,15 @@ extern "C" int sfnx_router_logits(const float* W, const float* x, float* logits,
     return guarded("sfnx_router_logits", [&] {
         require(H % 256 == 0, "H must be a multiple of 256");
         if (T <= 0 || L <= 0) return;
-        const dim3 g((L + RR_WAVES - 1) / RR_WAVES, (T + 7) / 8);
+        const int rt = H / 256 <= 8 ? 4 : 2;
+        const dim3 g((L + LT_WAVES * rt - 1) / (LT_WAVES * rt), (T + LT_TOK - 1) / LT_TOK);
+        const size_t lds = (size_t) LT_NBUF * LT_RU * H * 4;
         hipStream_t s = stream_of(st);
         switch (H / 256) {
-            case 4: k_router_logits<4><<<g, RR_THREADS, 0, s>>>(W, x, logits, T, L); break;
-            case 8: k_router_logits<8><<<g, RR_THREADS, 0, s>>>(W, x, logits, T, L); break;
-            case 10: k_router_logits<10><<<g, RR_THREADS, 0, s>>>(W, x, logits, T, L); break;
-            case 16: k_router_logits<16><<<g, RR_THREADS, 0, s>>>(W, x, logits, T, L); break;
+            case 4: k_router_logits<4><<<g, LT_THREADS, lds, s>>>(W, x, logits, T, L); break;
+            case 8: k_router_logits<8><<<g, LT_THREADS, lds, s>>>(W, x, logits, T, L); break;
+            case 10: k_router_logits<10><<<g, LT_THREADS, lds, s>>>(W, x, logits, T, L); break;
+            case 16: k_router_logits<16><<<g, LT_THREADS, lds, s>>>(W, x, logits, T, L); break;
             default: throw std::runtime_error("hidden size must be 1024, 2048, 2560 or 4096");
         }
     });
@@ -354,8 +470,11 @@ extern "C" int sfnx_moe_combine(const float* part, const float* topw, const int*
     return guarded("sfnx_moe_combine", [&] {
         if (T <= 0) return;
         const size_t n = (size_t) T * H;
-        k_combine<<<(unsigned) std::min<size_t>((n + 255) / 256, 8192), 256, 0, stream_of(st)>>>(part, topw, topi, logits, y, T,
-                                                                                                 H, E, K, shared);
+        require(H % 4 == 0, "H must be a multiple of 4");
+        require(K >= 1 && K <= MAX_K, "K out of range (1..16)");
+        (void) n;
+        const dim3 g((H / 4 + CB_THREADS - 1) / CB_THREADS, T);
+        k_combine<<<g, CB_THREADS, 0, stream_of(st)>>>(part, topw, topi, logits, y, T, H, E, K, shared);
     });
 }
 
