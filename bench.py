@@ -239,6 +239,9 @@ def bench_prefill(L, s, moe, torch, C=2048, reps=10):
         e1.record()
         torch.cuda.synchronize()
         us[name] = e0.elapsed_time(e1) / reps * 1e3
+    # the whole layer as the prompt path runs it: router logits, the skew's bias, top-k and the job permutation, f16
+    # activations, gate|up + SwiGLU, down, the combine
+    us["layer"] = time_us(torch, lambda: moe.prefill_layer_mma(L, xn, y, b, bias), reps)
     P = C * s.K
     flops = 2 * (P + C) * (2 * s.ff * s.H + s.H * s.ff)   # 2 per multiply-add, routed + shared pairs
     touched = int((cnt > 0).sum()) + 1
@@ -252,6 +255,8 @@ def bench_prefill(L, s, moe, torch, C=2048, reps=10):
             "int8_peak_frac_equiv": round(flops / t_mma / 1e12 / INT8_MFMA_PEAK_TOPS, 4),
             "weight_gbs": round(wbytes / t_mma / 1e9, 1), "hbm_frac": round(wbytes / t_mma / 1e9 / HBM_PEAK_GBS, 4),
             "q8_dot_tops": round(flops / t_q8 / 1e12, 2),
+            "layer_us": round(us["layer"], 1), "layer_tflops": round(flops / (us["layer"] * 1e-6) / 1e12, 1),
+            "layer_hbm_frac": round(wbytes / (us["layer"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "experts_touched": touched, "max_rows_per_expert": int(cnt.max()), "flops": flops, "weight_bytes": wbytes}
 
 

@@ -152,14 +152,14 @@ template <int NV> __device__ __forceinline__ float reduce_scatter(float (&v)[NV]
 constexpr int LT_THREADS = 256, LT_WAVES = LT_THREADS / WAVE, LT_RU = 4, LT_NBUF = 2, LT_TOK = 128;
 template <int NC>
 __global__ void __launch_bounds__(LT_THREADS) k_router_logits(const float* __restrict__ W, const float* __restrict__ x,
-                                                             float* __restrict__ logits, int T, int L) {
+                                                             float* __restrict__ logits, int T, int L, int tok) {
     constexpr int H = NC * 4 * WAVE, RT = NC <= 8 ? 4 : 2, NV = RT * LT_RU;
     constexpr int PER = LT_RU * H / 4, COPIES = PER / LT_THREADS;   // float4 a group; copies a wavefront issues a group
     static_assert(PER % LT_THREADS == 0, "a group is whole copies");
     extern __shared__ __align__(16) unsigned char lds[];
     float* xs = reinterpret_cast<float*>(lds);   // [LT_NBUF][LT_RU][H]
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-    const int row0 = (blockIdx.x * LT_WAVES + wave) * RT, t0 = blockIdx.y * LT_TOK, nt = min(LT_TOK, T - t0);
+    const int row0 = (blockIdx.x * LT_WAVES + wave) * RT, t0 = blockIdx.y * tok, nt = min(tok, T - t0);
     const int ng = (nt + LT_RU - 1) / LT_RU;
     // group g's LT_RU token rows into buffer g % LT_NBUF (tokens past the end repeat the last); a wavefront moves 64
     // float4 a copy
@@ -432,15 +432,18 @@ extern "C" int sfnx_router_logits(const float* W, const float* x, float* logits,
     return guarded("sfnx_router_logits", [&] {
         require(H % 256 == 0, "H must be a multiple of 256");
         if (T <= 0 || L <= 0) return;
-        const int rt = H / 256 <= 8 ? 4 : 2;
-        const dim3 g((L + LT_WAVES * rt - 1) / (LT_WAVES * rt), (T + LT_TOK - 1) / LT_TOK);
+        const int rt = H / 256 <= 8 ? 4 : 2, rb = (L + LT_WAVES * rt - 1) / (LT_WAVES * rt);
+        // tokens a block: LT_TOK, or fewer (a multiple of LT_RU) so that a short prompt still spreads over the chip
+        int tok = LT_TOK;
+        while (tok > LT_RU && (long) rb * ((T + tok - 1) / tok) < 512) tok -= LT_RU;
+        const dim3 g(rb, (T + tok - 1) / tok);
         const size_t lds = (size_t) LT_NBUF * LT_RU * H * 4;
         hipStream_t s = stream_of(st);
         switch (H / 256) {
-            case 4: k_router_logits<4><<<g, LT_THREADS, lds, s>>>(W, x, logits, T, L); break;
-            case 8: k_router_logits<8><<<g, LT_THREADS, lds, s>>>(W, x, logits, T, L); break;
-            case 10: k_router_logits<10><<<g, LT_THREADS, lds, s>>>(W, x, logits, T, L); break;
-            case 16: k_router_logits<16><<<g, LT_THREADS, lds, s>>>(W, x, logits, T, L); break;
+            case 4: k_router_logits<4><<<g, LT_THREADS, lds, s>>>(W, x, logits, T, L, tok); break;
+            case 8: k_router_logits<8><<<g, LT_THREADS, lds, s>>>(W, x, logits, T, L, tok); break;
+            case 10: k_router_logits<10><<<g, LT_THREADS, lds, s>>>(W, x, logits, T, L, tok); break;
+            case 16: k_router_logits<16><<<g, LT_THREADS, lds, s>>>(W, x, logits, T, L, tok); break;
             default: throw std::runtime_error("hidden size must be 1024, 2048, 2560 or 4096");
         }
     });
