@@ -148,8 +148,8 @@ template <int NV> __device__ __forceinline__ float reduce_scatter(float (&v)[NV]
 // float4 chunks l + 64 i, then the xor butterfly), register-blocked: a wavefront keeps RT router rows in registers and
 // takes the block's tokens LT_RU at a time from LDS, where the block stages them by asynchronous global -> LDS copies
 // into LT_NBUF buffers (LT_NBUF - 1 groups in flight while one computes); the RT x LT_RU sums of a lane leave through
-// one reduce_scatter.  A block: 4 wavefronts, 4 RT rows, LT_TOK tokens.
-constexpr int LT_THREADS = 256, LT_WAVES = LT_THREADS / WAVE, LT_RU = 4, LT_NBUF = 2, LT_TOK = 128;
+// one reduce_scatter.  A block: 8 wavefronts of RT rows, and as many tokens as give one block a compute unit.
+constexpr int LT_THREADS = 512, LT_WAVES = LT_THREADS / WAVE, LT_RU = 4, LT_NBUF = 3;
 template <int NC>
 __global__ void __launch_bounds__(LT_THREADS) k_router_logits(const float* __restrict__ W, const float* __restrict__ x,
                                                              float* __restrict__ logits, int T, int L, int tok) {
@@ -433,9 +433,11 @@ extern "C" int sfnx_router_logits(const float* W, const float* x, float* logits,
         require(H % 256 == 0, "H must be a multiple of 256");
         if (T <= 0 || L <= 0) return;
         const int rt = H / 256 <= 8 ? 4 : 2, rb = (L + LT_WAVES * rt - 1) / (LT_WAVES * rt);
-        // tokens a block: LT_TOK, or fewer (a multiple of LT_RU) so that a short prompt still spreads over the chip
-        int tok = LT_TOK;
-        while (tok > LT_RU && (long) rb * ((T + tok - 1) / tok) < 512) tok -= LT_RU;
+        // tokens a block (a multiple of LT_RU): the fewest that keep the grid within one block a compute unit
+        static int ncu = 0;
+        if (!ncu) check(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, 0), "hipDeviceGetAttribute");
+        int tok = LT_RU;
+        while ((long) rb * ((T + tok - 1) / tok) > ncu && tok < T) tok += LT_RU;
         const dim3 g(rb, (T + tok - 1) / tok);
         const size_t lds = (size_t) LT_NBUF * LT_RU * H * 4;
         hipStream_t s = stream_of(st);
