@@ -139,11 +139,12 @@ constexpr size_t MM_XBUF = 64 * MM_XLD;              // halves in one activation
 // run r of the job's activation rows into an LDS buffer by asynchronous global -> LDS copies (no registers): wavefront w
 // moves rows w * 8 .. w * 8 + 7, a row of 512 halves a copy (64 lanes x 16 bytes); rows past n are left as they are
 // (they only feed output rows that are never stored)
+template <int XR = MM_XROWS>
 __device__ __forceinline__ void load_x_async(_Float16* buf, const _Float16* __restrict__ x, int ldx, const int* ys, int n,
                                              int r, int wave, int lane) {
 #pragma unroll
-    for (int i = 0; i < MM_XROWS; ++i) {
-        const int m = wave * MM_XROWS + i;
+    for (int i = 0; i < XR; ++i) {
+        const int m = wave * XR + i;
         if (m < n)
             __builtin_amdgcn_global_load_lds(x + (size_t) ys[m] * ldx + MM_RUN * r + 8 * lane,
                                              (__attribute__((address_space(3))) void*) (buf + (size_t) m * MM_XLD), 16, 0, 0);
@@ -187,15 +188,17 @@ __device__ __forceinline__ void mma_run(const RunW<TYPE>& w, const _Float16* xb,
 // The block's rows are G groups of 256 (a wavefront's 32 rows each); per group the runs of 512 columns, per run 8
 // steps of 64.  Weights stream one run ahead of the steps (registers); each run's activations come into the other LDS
 // buffer while this one is read.  A single run (the down projection) is staged once for every group.
+// rows: ys[0..n) (activation rows) and outs[0..n) (output rows), n <= 32 NT
 template <int TYPE, int NT>
 __device__ __forceinline__ void mma_job(const uint8_t* mat, int R, int C, int row0, int G, int wave, int lane,
-                                        const sfnx_bigjob& jb, const _Float16* __restrict__ x, int ldx, _Float16* xs,
-                                        float* __restrict__ out, int pj) {
+                                        const int* ys, const int* outs, int n, const _Float16* __restrict__ x, int ldx,
+                                        _Float16* xs, float* __restrict__ out, int pj) {
     (void) pj;   // the job's row of phase stamps in the instrumented build, or -1
+    constexpr int XR = NT <= 2 ? MM_XROWS : 4 * NT;   // activation rows a wavefront stages
     const int h = lane / 32, nn = lane % 32, nr = C / MM_RUN, total = G * nr;
     auto row_of = [&](int it) { return row0 + (it / nr) * MM_BM + wave * 32 + nn; };
     RunW<TYPE> w, wn;
-    load_x_async(xs, x, ldx, jb.y, jb.n, 0, wave, lane);
+    load_x_async<XR>(xs, x, ldx, ys, n, 0, wave, lane);
     load_run(w, mat, R, C, row_of(0), 0, h);
     float16v acc[NT];
     for (int it = 0; it < total; ++it) {
@@ -211,7 +214,7 @@ __device__ __forceinline__ void mma_job(const uint8_t* mat, int R, int C, int ro
             wait_vmem();          // this run's activations (and the weights of this step, needed now anyway)
             __syncthreads();      // every wavefront's rows landed; every wavefront is past the previous run
             if (nr > 1 && it + 1 < total)
-                load_x_async(xs + (size_t) ((it + 1) & 1) * MM_XBUF, x, ldx, jb.y, jb.n, (r + 1) % nr, wave, lane);
+                load_x_async<XR>(xs + (size_t) ((it + 1) & 1) * MM_XBUF, x, ldx, ys, n, (r + 1) % nr, wave, lane);
         }
         if (it + 1 < total) load_run(wn, mat, R, C, row_of(it + 1), (it + 1) % nr, h);
         mma_run<TYPE, NT>(w, xb, nn, h, acc);
@@ -223,7 +226,7 @@ __device__ __forceinline__ void mma_job(const uint8_t* mat, int R, int C, int ro
 #pragma unroll
                 for (int q = 0; q < 16; ++q) {
                     const int m = 32 * t + 8 * (q / 4) + 4 * h + q % 4;
-                    if (m < jb.n) out[(size_t) jb.out[m] * R + row] = acc[t][q];
+                    if (m < n) out[(size_t) outs[m] * R + row] = acc[t][q];
                 }
         }
         w = wn;
@@ -346,8 +349,8 @@ __global__ void __launch_bounds__(MM_THREADS) k_moe_mma(const uint8_t* __restric
     _Float16* xs = reinterpret_cast<_Float16*>(xs_raw);
     const int row0 = sl * G * MM_BM;
     MPROF(1)
-    if (jb.n > 32) mma_job<TYPE, 2>(mat, R, C, row0, G, wave, lane, jb, x, C, xs, out, pj);
-    else mma_job<TYPE, 1>(mat, R, C, row0, G, wave, lane, jb, x, C, xs, out, pj);
+    if (jb.n > 32) mma_job<TYPE, 2>(mat, R, C, row0, G, wave, lane, jb.y, jb.out, jb.n, x, C, xs, out, pj);
+    else mma_job<TYPE, 1>(mat, R, C, row0, G, wave, lane, jb.y, jb.out, jb.n, x, C, xs, out, pj);
     MPROF(18)
 }
 
