@@ -168,6 +168,39 @@ int sfnx_residual_rmsnorm(float* x, const float* y, float* xn, int T, int H, flo
 int sfnx_kernel_clock(int enable);
 int sfnx_kernel_clock_read(float* us);
 
+/* ---------------------------------------------------------------------------------------------- GGUF files
+ * A read-only mapping of a GGUF model (every shard of a split "<stem>-0000N-of-0000M.gguf" model), its tensor index
+ * and the first shard's metadata (src/gguf.hpp:20-88 Gguf, TypeInfo, Tensor; src/gguf.cpp).  Lookups return 1 when
+ * found, 0 when missing and a negative status on error. */
+typedef struct sfnx_gguf sfnx_gguf;
+typedef struct sfnx_gguf_tensor {
+    uint32_t type;      /* ggml type id */
+    int n_dims;
+    int64_t ne[4];      /* ne[0]: elements a row */
+    const void* data;   /* in the mapping (host memory) */
+    size_t nbytes;
+    int shard;
+} sfnx_gguf_tensor;
+int sfnx_gguf_type_info(uint32_t type, int* block, int* bytes);                       /* src/gguf.hpp:29 type_info */
+int sfnx_gguf_open(const char* path, sfnx_gguf** g);                                   /* src/gguf.hpp:49 Gguf::Gguf */
+void sfnx_gguf_close(sfnx_gguf* g);                                                    /* src/gguf.hpp:50 ~Gguf */
+int sfnx_gguf_n_tensors(const sfnx_gguf* g);                                           /* src/gguf.hpp:66 tensors() */
+int sfnx_gguf_tensor_at(const sfnx_gguf* g, int i, const char** name, sfnx_gguf_tensor* t);
+int sfnx_gguf_find(const sfnx_gguf* g, const char* name, sfnx_gguf_tensor* t);          /* src/gguf.hpp:52 find */
+int sfnx_gguf_int(const sfnx_gguf* g, const char* key, int64_t* v);                    /* src/gguf.hpp:57 i */
+int sfnx_gguf_float(const sfnx_gguf* g, const char* key, double* v);                   /* src/gguf.hpp:61 num */
+int sfnx_gguf_str(const sfnx_gguf* g, const char* key, const char** v);                /* src/gguf.hpp:59 s */
+
+/* One layer's MoE weights from a GGUF into the device store (src/model.cpp:554-606 expert_rows2 / expert_cols,
+ * 766-809): blk.<layer>.ffn_{gate,up}_exps rows ff0..ff1 stacked [gate ; up] per expert into gu (planar, gu_stride a
+ * matrix), ffn_down_exps columns ff0..ff1 into dn (dn_stride a matrix), the shared expert ffn_*_shexp (when present,
+ * of the same type and FF) as expert E, and the router W = [ffn_gate_inp rows ; ffn_gate_inp_shexp] (f32 [E+1][H]).
+ * Q4_K or Q8_0 experts; ff0 on a block (256 / 32 columns), ff1 - ff0 and H multiples of 512.  info (may be null)
+ * receives type, H, E, ff1 - ff0
+ * and shared.  A loader, not a hot-path call: it allocates a staging buffer and synchronises the stream. */
+int sfnx_gguf_moe_layer(const sfnx_gguf* g, int layer, int ff0, int ff1, void* gu, size_t gu_stride, void* dn,
+                        size_t dn_stride, float* W, int* info, void* st);
+
 #ifdef __cplusplus
 }
 #endif

@@ -49,7 +49,22 @@ SIGNATURES = {
     "sfnx_to_f16": (i32, [vp, vp, sz, vp]),
     "sfnx_moe_decode_workspace": (sz, [i32, i32, i32, i32, i32, vp]),
     "sfnx_moe_decode": (i32, [vp, i32, u32, i32, i32, i32, i32, i32, vp, i32, i32, f32, vp, sz, i32, vp]),
+    "sfnx_gguf_type_info": (i32, [u32, vp, vp]),
+    "sfnx_gguf_open": (i32, [C.c_char_p, vp]),
+    "sfnx_gguf_close": (None, [vp]),
+    "sfnx_gguf_n_tensors": (i32, [vp]),
+    "sfnx_gguf_tensor_at": (i32, [vp, i32, vp, vp]),
+    "sfnx_gguf_find": (i32, [vp, C.c_char_p, vp]),
+    "sfnx_gguf_int": (i32, [vp, C.c_char_p, vp]),
+    "sfnx_gguf_float": (i32, [vp, C.c_char_p, vp]),
+    "sfnx_gguf_str": (i32, [vp, C.c_char_p, vp]),
+    "sfnx_gguf_moe_layer": (i32, [vp, i32, i32, i32, vp, sz, vp, sz, vp, vp, vp]),
 }
+
+
+class GgufTensor(C.Structure):
+    """sfnx_gguf_tensor"""
+    _fields_ = [("type", u32), ("n_dims", i32), ("ne", i64 * 4), ("data", vp), ("nbytes", sz), ("shard", i32)]
 
 
 class LayerW(C.Structure):

@@ -1,6 +1,6 @@
 """Builds the HIP library libsfnx_moe.so in-tree for gfx950 (hipcc; no torch involvement).
 
-Every HIP source under csrc/ is compiled to an object in parallel, then linked into sfnx_amd/libsfnx_moe.so.
+Every HIP source (and host C++ source) under csrc/ is compiled to an object in parallel, then linked into sfnx_amd/libsfnx_moe.so.
 Floating-point contraction is off: every fused multiply-add in the kernels is an explicit fmaf, so each kernel's
 arithmetic is exactly what its source says.  Packed FP32 instructions are disabled (see the flags below).
 """
@@ -43,7 +43,7 @@ def _compile(src: Path) -> Path:
 
 def build(verbose: bool = False) -> Path:
     OBJ.mkdir(exist_ok=True)
-    sources = sorted(CSRC.glob("*.hip"))
+    sources = sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
     with cf.ThreadPoolExecutor(max_workers=min(8, len(sources))) as ex:
         objs = list(ex.map(_compile, sources))
     tmp = LIB.with_suffix(".so.tmp")

@@ -29,6 +29,16 @@ template <typename F> int guarded(const char* what, F&& f) {
         return -1;
     }
 }
+// the same for host-only work (no launch to check, and no GPU needed)
+template <typename F> int guarded_host(const char* what, F&& f) {
+    try {
+        f();
+        return 0;
+    } catch (const std::exception& ex) {
+        set_error(std::string(what) + ": " + ex.what());
+        return -1;
+    }
+}
 inline void require(bool ok, const char* msg) {
     if (!ok) throw std::runtime_error(msg);
 }

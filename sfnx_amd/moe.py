@@ -332,4 +332,88 @@ def prefill_layer_q8(L: MoeLayer, x: torch.Tensor, y: torch.Tensor, b: PrefillBu
     moe_combine(b.part, b.topw, b.topi, b.logits, y, s.E, s.K, s.shared)
 
 
+# ---------------------------------------------------------------------------------------------------- GGUF files
+class Gguf:
+    """A GGUF model mapped read-only (src/gguf.hpp:46-88 Gguf): tensors by name, metadata by key."""
+
+    def __init__(self, path: str):
+        h = C.c_void_p()
+        check(lib().sfnx_gguf_open(str(path).encode(), C.byref(h)))
+        self._h = h
+
+    def close(self) -> None:
+        if self._h:
+            lib().sfnx_gguf_close(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def tensor(self, name: str):
+        """(type, shape ne[0..n_dims), bytes as a numpy view of the mapping) or None when missing"""
+        import numpy as np
+        t = _abi.GgufTensor()
+        r = lib().sfnx_gguf_find(self._h, name.encode(), C.byref(t))
+        if r < 0:
+            check(r)
+        if r == 0:
+            return None
+        buf = (C.c_uint8 * t.nbytes).from_address(t.data) if t.nbytes else b""
+        return t.type, tuple(t.ne[:t.n_dims]), np.frombuffer(buf, dtype=np.uint8)
+
+    def names(self) -> list[str]:
+        out = []
+        for i in range(lib().sfnx_gguf_n_tensors(self._h)):
+            n = C.c_char_p()
+            check(lib().sfnx_gguf_tensor_at(self._h, i, C.byref(n), None))
+            out.append(n.value.decode())
+        return out
+
+    def int(self, key: str):
+        v = C.c_int64()
+        r = lib().sfnx_gguf_int(self._h, key.encode(), C.byref(v))
+        if r < 0:
+            check(r)
+        return v.value if r else None
+
+    def float(self, key: str):
+        v = C.c_double()
+        r = lib().sfnx_gguf_float(self._h, key.encode(), C.byref(v))
+        if r < 0:
+            check(r)
+        return v.value if r else None
+
+    def str(self, key: str):
+        v = C.c_char_p()
+        r = lib().sfnx_gguf_str(self._h, key.encode(), C.byref(v))
+        if r < 0:
+            check(r)
+        return v.value.decode() if r else None
+
+
+def gguf_moe_layer(g: Gguf, layer: int, ff0: int = 0, ff1: int | None = None, K: int = 8) -> "MoeLayer":
+    """blk.<layer>'s experts, shared expert and router from a GGUF into a device MoeLayer (src/model.cpp:766-809)"""
+    ti = g.tensor(f"blk.{layer}.ffn_gate_exps.weight")
+    if ti is None:
+        raise RuntimeError(f"gguf: blk.{layer}.ffn_gate_exps.weight is missing")
+    wtype, (H, FF, E) = ti[0], ti[1]
+    ff1 = FF if ff1 is None else ff1
+    ffs = ff1 - ff0
+    shared = all(g.tensor(f"blk.{layer}.{n}.weight") is not None
+                 for n in ("ffn_gate_shexp", "ffn_up_shexp", "ffn_down_shexp", "ffn_gate_inp_shexp"))
+    E1 = E + (1 if shared else 0)
+    gu_stride = 2 * ffs * row_bytes(wtype, H)
+    dn_stride = H * row_bytes(wtype, ffs)
+    gu = torch.empty(E1 * gu_stride, dtype=torch.uint8, device="cuda")
+    dn = torch.empty(E1 * dn_stride, dtype=torch.uint8, device="cuda")
+    W = torch.zeros((E + 1, H), dtype=torch.float32, device="cuda")   # row E: the shared gate (zero without one)
+    info = (C.c_int * 5)()
+    check(lib().sfnx_gguf_moe_layer(g._h, layer, ff0, ff1, _p(gu), gu_stride, _p(dn), dn_stride, _p(W), info, _st()))
+    s = LayerShape(H=H, E=E, K=K, ff=ffs, wtype=wtype, shared=shared)
+    return MoeLayer(s, W, gu, dn)
+
+
 __all__ = [n for n in dir() if not n.startswith("_")] + ["_abi"]

@@ -49,7 +49,8 @@ def test_cpp_header_compiles():
     import tempfile
     from pathlib import Path
     root = Path(__file__).resolve().parent.parent
-    src = '#include "sfnx/kernels.hpp"\nint main() { return sizeof(sfnx::Job) == 136 && sizeof(sfnx::BigJob) == 520 ? 0 : 1; }\n'
+    src = ('#include "sfnx/kernels.hpp"\n#include "sfnx/gguf.hpp"\n'
+           'int main() { return sizeof(sfnx::Job) == 136 && sizeof(sfnx::BigJob) == 520 ? 0 : 1; }\n')
     with tempfile.TemporaryDirectory() as d:
         f = Path(d) / "t.cpp"
         f.write_text(src)

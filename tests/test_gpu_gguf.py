@@ -1,0 +1,79 @@
+"""A MoE layer loaded from a GGUF file into the device store (sfnx_gguf_moe_layer; src/model.cpp:554-606 and 766-809)
+against the bytes the test wrote: the store unpacked to GGUF layout equals the sliced source tensors byte for byte,
+the router equals [ffn_gate_inp ; ffn_gate_inp_shexp], and one decode window through the loaded layer equals the oracle
+on the same bytes (top-k indices bit-exact, outputs within 2e-3 max relative error)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from sfnx_amd import moe
+from tests import gguf_writer as gw
+from tests.gpu_util import max_rel
+
+pytestmark = pytest.mark.gpu
+
+
+def _layer_bytes(wtype, H, E, ff, seed):
+    rng = np.random.default_rng(seed)
+    q = lambda r, c: orc.quantize(wtype, (0.02 * rng.standard_normal((r, c))).astype(np.float32))
+    gate = np.stack([q(ff, H) for _ in range(E)])
+    up = np.stack([q(ff, H) for _ in range(E)])
+    down = np.stack([q(H, ff) for _ in range(E)])
+    shared = (q(ff, H), q(ff, H), q(H, ff), (0.02 * rng.standard_normal(H)).astype(np.float32))
+    W = (0.02 * rng.standard_normal((E, H))).astype(np.float32)
+    return W, gate, up, down, shared
+
+
+@pytest.mark.parametrize("wtype,H,E,ff,ff0,ff1", [(orc.Q4_K, 1024, 64, 512, 0, 512), (orc.Q4_K, 1024, 64, 1024, 256, 768),
+                                                  (orc.Q8_0, 1024, 64, 512, 0, 512), (orc.Q8_0, 1024, 64, 1024, 32, 544)])
+def test_gguf_layer(tmp_path, wtype, H, E, ff, ff0, ff1):
+    W, gate, up, down, shared = _layer_bytes(wtype, H, E, ff, 11)
+    path = tmp_path / "layer.gguf"
+    gw.write_gguf(path, [("general.architecture", gw.STR, "qwen3moe")],
+                  gw.moe_layer_tensors(3, W, gate, up, down, wtype, H, E, ff, shared))
+    g = moe.Gguf(str(path))
+    L = moe.gguf_moe_layer(g, 3, ff0, ff1, K=4)
+    torch.cuda.synchronize()
+    s = L.s
+    ffs = ff1 - ff0
+    assert s.shared and s.E == E and s.H == H and s.ff == ffs and s.wtype == wtype
+    # the router: routed rows, then the shared gate row
+    assert np.array_equal(L.W.cpu().numpy(), np.vstack([W, shared[3][None]]))
+    # the store, unpacked to GGUF layout, against the sliced source bytes
+    rb_h, rb_f, rb_full = orc.row_bytes(wtype, H), orc.row_bytes(wtype, ffs), orc.row_bytes(wtype, ff)
+    cb = 256 if wtype == orc.Q4_K else 32
+    col0 = (ff0 // cb) * (144 if wtype == orc.Q4_K else 34)
+    gu_g = torch.empty_like(L.gu_w)
+    dn_g = torch.empty_like(L.dn_w)
+    moe.store_unpack(wtype, L.gu_w, gu_g, E + 1, 2 * ffs, H)
+    moe.store_unpack(wtype, L.dn_w, dn_g, E + 1, H, ffs)
+    gu_h = gu_g.cpu().numpy().reshape(E + 1, 2 * ffs, rb_h)
+    dn_h = dn_g.cpu().numpy().reshape(E + 1, H, rb_f)
+    for e in range(E + 1):
+        gt, ut, dt = (shared[0], shared[1], shared[2]) if e == E else (gate[e], up[e], down[e])
+        assert np.array_equal(gu_h[e, :ffs], gt.reshape(ff, rb_h)[ff0:ff1])
+        assert np.array_equal(gu_h[e, ffs:], ut.reshape(ff, rb_h)[ff0:ff1])
+        assert np.array_equal(dn_h[e], dt.reshape(H, rb_full)[:, col0:col0 + rb_f])
+    # one decode window through the loaded layer against the oracle on the same bytes
+    host = orc.LayerWeights(L.W.cpu().numpy(), gu_h.reshape(-1), dn_h.reshape(-1), wtype, H, E, s.K, ffs, True)
+    T = 3
+    x = orc.synth(T * H, 77, 1.0).reshape(T, H)
+    y = torch.empty((T, H), dtype=torch.float32, device="cuda")
+    b = moe.DecodeBuffers(s, T)
+    moe.decode_layer(L, torch.from_numpy(x).cuda(), y, b)
+    torch.cuda.synchronize()
+    oy, _, oi, _, _, _ = orc.layer_decode(host, x)
+    assert np.array_equal(b.topi.cpu().numpy(), oi)
+    assert max_rel(y.cpu().numpy(), oy) < 2e-3
+
+
+def test_gguf_layer_refusals(tmp_path):
+    W, gate, up, down, shared = _layer_bytes(orc.Q4_K, 512, 64, 512, 12)
+    path = tmp_path / "l.gguf"
+    gw.write_gguf(path, [], gw.moe_layer_tensors(0, W, gate, up, down, orc.Q4_K, 512, 64, 512, shared))
+    g = moe.Gguf(str(path))
+    with pytest.raises(RuntimeError, match="missing"):
+        moe.gguf_moe_layer(g, 1)
+    with pytest.raises(RuntimeError, match="whole block"):
+        moe.gguf_moe_layer(g, 0, 128, 512)
