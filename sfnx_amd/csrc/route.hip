@@ -212,9 +212,11 @@ __global__ void __launch_bounds__(LT_THREADS) k_router_logits(const float* __res
 }
 
 // ------------------------------------------------------------------------------------------------ prompt routing
-// src/prefill.cu:191-221 k_pf_top10: a wavefront per token
+// src/prefill.cu:191-221 k_pf_top10 and 223-226 k_pf_count: a wavefront per token, its picks counted per expert
+// (cnt zeroed beforehand; the counts are exact whatever the order of the increments)
 __global__ void __launch_bounds__(RR_THREADS) k_pf_topk(const float* __restrict__ logits, int C, int E, int K,
-                                                       int* __restrict__ topi, float* __restrict__ topw) {
+                                                       int* __restrict__ topi, float* __restrict__ topw,
+                                                       int* __restrict__ cnt) {
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE, t = blockIdx.x * RR_WAVES + wave;
     if (t >= C) return;
     int pick;
@@ -223,42 +225,62 @@ __global__ void __launch_bounds__(RR_THREADS) k_pf_topk(const float* __restrict_
     if (lane < K) {
         topi[(size_t) t * K + lane] = pick;
         topw[(size_t) t * K + lane] = w;
+        if (pick >= 0) atomicAdd(&cnt[pick], 1);
     }
 }
 __global__ void k_fill_int(int* p, int n, int v) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) p[i] = v;
 }
-// src/prefill.cu:223-226 k_pf_count
-__global__ void k_pf_count(const int* __restrict__ topi, int P, int* __restrict__ cnt) {
-    const int p = blockIdx.x * blockDim.x + threadIdx.x;
-    if (p < P && topi[p] >= 0) atomicAdd(&cnt[topi[p]], 1);
-}
-// src/prefill.cu:228-242 k_pf_jobbase: one block of E threads (E <= 1024), an inclusive scan of ceil(cnt / 64)
-__global__ void k_pf_jobbase(const int* __restrict__ cnt, int* __restrict__ jbase, int* __restrict__ njobs, int E, int C,
-                             int shared) {
-    __shared__ int s[MAX_E];
-    const int e = threadIdx.x;
-    const int nj = e < E ? (cnt[e] + SFNX_PF_JOB - 1) / SFNX_PF_JOB : 0;
-    s[e] = nj;
-    __syncthreads();
-    for (int o = 1; o < (int) blockDim.x; o <<= 1) {
-        const int a = e >= o ? s[e - o] : 0;
-        __syncthreads();
-        s[e] += a;
-        __syncthreads();
-    }
-    if (e < E) jbase[e] = s[e] - nj;
-    if (e == (int) blockDim.x - 1) njobs[0] = s[e] + (shared ? (C + SFNX_PF_JOB - 1) / SFNX_PF_JOB : 0);
-}
 // src/prefill.cu:248-279 k_pf_fill: a block per expert scans the pairs in index order, 4 consecutive pairs a thread and
 // 1024 a pass, its slots from a prefix over the threads of the pass (ballots of the count bits, then the wavefronts in
 // order), so a pair always lands in the same job and slot
+// Each block also finds its expert's first job (src/prefill.cu:228-242 k_pf_jobbase: the exclusive prefix of
+// ceil(cnt / 64) in expert order), block 0 writes the job count, and blocks E.. lay out the shared expert's jobs after
+// the routed ones (tokens in order, 64 a job).
 constexpr int PF_FILL_THREADS = 256, PF_FILL_PASS = 4 * PF_FILL_THREADS;
-__global__ void __launch_bounds__(PF_FILL_THREADS) k_pf_fill(const int* __restrict__ topi, int P, int K,
-                                                            const int* __restrict__ cnt, const int* __restrict__ jbase,
-                                                            sfnx_bigjob* __restrict__ gu, sfnx_bigjob* __restrict__ dn) {
-    const int e = blockIdx.x, tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE;
+__global__ void __launch_bounds__(PF_FILL_THREADS) k_pf_fill(const int* __restrict__ topi, int P, int K, int E, int C,
+                                                            int shared, const int* __restrict__ cnt, int* __restrict__ jbase,
+                                                            int* __restrict__ njobs, sfnx_bigjob* __restrict__ gu,
+                                                            sfnx_bigjob* __restrict__ dn) {
+    const int tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE;
+    const int e = min((int) blockIdx.x, E);   // E: a block of the shared expert's jobs
+    __shared__ int wsum[2][PF_FILL_THREADS / WAVE];
+    int jb0 = 0, jall = 0;   // jobs of the experts before e, of all experts
+    for (int i = tid; i < E; i += PF_FILL_THREADS) {
+        const int nj = (cnt[i] + SFNX_PF_JOB - 1) / SFNX_PF_JOB;
+        jb0 += i < e ? nj : 0;
+        jall += nj;
+    }
+    jb0 = group_isum<WAVE>(jb0);
+    jall = group_isum<WAVE>(jall);
+    if (lane == 0) {
+        wsum[0][wave] = jb0;
+        wsum[1][wave] = jall;
+    }
+    __syncthreads();
+    jb0 = jall = 0;
+#pragma unroll
+    for (int w = 0; w < PF_FILL_THREADS / WAVE; ++w) {
+        jb0 += wsum[0][w];
+        jall += wsum[1][w];
+    }
+    if ((int) blockIdx.x >= E) {   // the shared expert's jobs
+        for (int t = ((int) blockIdx.x - E) * PF_FILL_THREADS + tid; t < C; t += ((int) gridDim.x - E) * PF_FILL_THREADS) {
+            const int j = jall + t / SFNX_PF_JOB, k = t % SFNX_PF_JOB;
+            gu[j].y[k] = t;
+            gu[j].out[k] = dn[j].y[k] = dn[j].out[k] = P + t;
+            if (k == 0) {
+                gu[j].w = dn[j].w = E;
+                gu[j].n = dn[j].n = min(SFNX_PF_JOB, C - t);
+            }
+        }
+        return;
+    }
+    if (tid == 0) {
+        jbase[e] = jb0;
+        if (e == 0) njobs[0] = jall + (shared ? (C + SFNX_PF_JOB - 1) / SFNX_PF_JOB : 0);
+    }
     const int ce = cnt[e];
     if (ce == 0) return;
     __shared__ int wcount[2][PF_FILL_THREADS / WAVE];
@@ -293,7 +315,7 @@ __global__ void __launch_bounds__(PF_FILL_THREADS) k_pf_fill(const int* __restri
 #pragma unroll
         for (int c = 0; c < 4; ++c)
             if (q[c] == e) {
-                const int pc = p + c, j = jbase[e] + s / SFNX_PF_JOB, k = s % SFNX_PF_JOB;
+                const int pc = p + c, j = jb0 + s / SFNX_PF_JOB, k = s % SFNX_PF_JOB;
                 gu[j].y[k] = pc / K;
                 gu[j].out[k] = pc;
                 dn[j].y[k] = pc;
@@ -306,20 +328,6 @@ __global__ void __launch_bounds__(PF_FILL_THREADS) k_pf_fill(const int* __restri
                 ++s;
             }
         base += total;
-    }
-}
-// the shared expert's jobs after the routed ones: tokens in order, 64 a job
-__global__ void k_pf_shared(int C, int P, int E, const int* __restrict__ njobs, sfnx_bigjob* __restrict__ gu,
-                            sfnx_bigjob* __restrict__ dn) {
-    const int nsh = (C + SFNX_PF_JOB - 1) / SFNX_PF_JOB, j0 = njobs[0] - nsh;
-    const int t = blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= C) return;
-    const int j = j0 + t / SFNX_PF_JOB, k = t % SFNX_PF_JOB;
-    gu[j].y[k] = t;
-    gu[j].out[k] = dn[j].y[k] = dn[j].out[k] = P + t;
-    if (k == 0) {
-        gu[j].w = dn[j].w = E;
-        gu[j].n = dn[j].n = min(SFNX_PF_JOB, C - t);
     }
 }
 
@@ -459,14 +467,10 @@ extern "C" int sfnx_pf_route(const float* logits, int C, int E, int K, int* topi
         require(K >= 1 && K <= MAX_K && K <= E, "K out of range (1..16)");
         hipStream_t s = stream_of(st);
         const int P = C * K;
-        k_pf_topk<<<(C + RR_WAVES - 1) / RR_WAVES, RR_THREADS, 0, s>>>(logits, C, E, K, topi, topw);
         k_fill_int<<<(E + 255) / 256, 256, 0, s>>>(cnt, E, 0);
-        k_pf_count<<<(P + 255) / 256, 256, 0, s>>>(topi, P, cnt);
-        int nt = 64;
-        while (nt < E) nt *= 2;
-        k_pf_jobbase<<<1, nt, 0, s>>>(cnt, jbase, njobs, E, C, shared);
-        k_pf_fill<<<E, PF_FILL_THREADS, 0, s>>>(topi, P, K, cnt, jbase, jobs_gu, jobs_dn);
-        if (shared) k_pf_shared<<<(C + 255) / 256, 256, 0, s>>>(C, P, E, njobs, jobs_gu, jobs_dn);
+        k_pf_topk<<<(C + RR_WAVES - 1) / RR_WAVES, RR_THREADS, 0, s>>>(logits, C, E, K, topi, topw, cnt);
+        const int nsh = shared ? std::min(8, (C + PF_FILL_THREADS - 1) / PF_FILL_THREADS) : 0;
+        k_pf_fill<<<E + nsh, PF_FILL_THREADS, 0, s>>>(topi, P, K, E, C, shared, cnt, jbase, njobs, jobs_gu, jobs_dn);
     });
 }
 
