@@ -156,24 +156,40 @@ __device__ __forceinline__ void warm_line(const void* p, void* junk) {
 __device__ __forceinline__ void warm_wait() { __builtin_amdgcn_s_waitcnt(0); }
 
 // ------------------------------------------------------------------------------------------------ planar store
-// byte offsets of row r's pieces inside one planar matrix of R rows x C columns
+// Per matrix of R rows (a multiple of 32) x C columns, each plane of the store is tiled by 32 rows and cut into
+// 16-byte pieces: piece p of a row lies 512 bytes after piece p - 1, and piece p of the tile's 32 rows is one 512-byte
+// run.  Any read that gives each of 32 (or 8) consecutive rows' lanes the same piece is a whole number of 128-byte
+// lines: the matrix-core kernels' (a lane per row) and the dot kernels' (8 or 16 lanes per row) alike.
+constexpr int ROWTILE = 32;
+__host__ __device__ __forceinline__ size_t tiled16(int row, size_t row_bytes, int piece) {
+    return (size_t) (row / ROWTILE) * ROWTILE * row_bytes + (size_t) piece * (ROWTILE * 16) + (size_t) (row % ROWTILE) * 16;
+}
+constexpr int PIECE_STRIDE = ROWTILE * 16;   // bytes from one piece of a row to the next
 struct Q4kPlanes {
-    const uint8_t* nib;   // R x C/2
-    const uint8_t* hdr;   // R x C/256 x 16
-    __device__ __forceinline__ const uint8_t* nib_row(int r, int C) const { return nib + (size_t) r * (C / 2); }
-    __device__ __forceinline__ const uint8_t* hdr_row(int r, int C) const { return hdr + (size_t) r * (C / 256) * 16; }
+    const uint8_t* nib;   // R x C/2: a row's runs of 256 bytes (two super-blocks), 16-byte pieces in [half][group] order
+    const uint8_t* hdr;   // R x C/256 x 16: a row's super-block headers, one piece each
+    // piece p (bytes 16 p .. 16 p + 15) of row r's nibble bytes
+    __host__ __device__ __forceinline__ const uint8_t* nib16(int r, int C, int p) const { return nib + tiled16(r, C / 2, p); }
+    // the 16-byte header of super-block b of row r
+    __host__ __device__ __forceinline__ const uint8_t* hdr16(int r, int C, int b) const { return hdr + tiled16(r, C / 16, b); }
 };
 __host__ __device__ __forceinline__ Q4kPlanes q4k_planes(const void* mat, int R, int C) {
     const uint8_t* p = (const uint8_t*) mat;
     return Q4kPlanes{p, p + (size_t) R * (C / 2)};
 }
 struct Q80Planes {
-    const uint8_t* q;     // R x C
-    const uint16_t* d;    // R x C/32
+    const uint8_t* q;     // R x C: a row's 512-byte runs (16 blocks), 16-byte pieces in [half][block] order
+    const uint8_t* d;     // R x C/32 f16: a row's block scales, 8 a piece
+    __host__ __device__ __forceinline__ const uint8_t* q16(int r, int C, int p) const { return q + tiled16(r, C, p); }
+    __host__ __device__ __forceinline__ const uint8_t* d16(int r, int C, int p) const { return d + tiled16(r, C / 16, p); }
+    // the f16 scale of block b of row r
+    __host__ __device__ __forceinline__ const uint16_t* dof(int r, int C, int b) const {
+        return reinterpret_cast<const uint16_t*>(d16(r, C, b / 8) + 2 * (b % 8));
+    }
 };
 __host__ __device__ __forceinline__ Q80Planes q80_planes(const void* mat, int R, int C) {
     const uint8_t* p = (const uint8_t*) mat;
-    return Q80Planes{p, (const uint16_t*) (p + (size_t) R * C)};
+    return Q80Planes{p, p + (size_t) R * C};
 }
 
 inline size_t row_bytes(uint32_t type, int cols) {

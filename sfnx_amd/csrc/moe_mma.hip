@@ -1,32 +1,33 @@
 // The prompt path's routed experts on the matrix cores (src/moe_mma.cuh, src/moe_mma.cu:324-354): per BigJob (one
-// expert, up to 64 token rows) and 256 of the expert's weight rows, out[job.out[m]][row] = sum_k w16[row][k] x16[m][k]
+// expert, up to 64 token rows) and 512 of the expert's weight rows, out[job.out[m]][row] = sum_k w16[row][k] x16[m][k]
 // with f16 weights (Q4_K: hfma2(q, f16(d sc), f16(-(dmin m))); Q8_0: hmul2(q, d)), f16 activations and fp32 accumulation,
 // on v_mfma_f32_32x32x16_f16.
 //
-// Layout on gfx950 (wave64): each wavefront owns 32 weight rows and dequantizes them straight from the planar store into
-// the MFMA's B operand.  The K loop runs over 512-column runs of 8 steps: per run, lane (n = l % 32, h = l / 32) loads
-// one whole 128-byte line of row n (Q4_K: the 16-byte halves h of the run's 8 groups; Q8_0: blocks 8 h .. 8 h + 7) and
-// the step's columns are permuted so that each step's 16 bytes are exactly the lane's 4 x 8 MFMA k-slots (the sum does
-// not depend on the order of k).  The job's activation rows for the run sit in LDS and feed the A operand with the same
-// permutation; the next run's weights and activations are in flight (registers) while this run's 8 steps compute.
-// D[token][row] leaves as 128-byte runs of consecutive rows.
+// Layout on gfx950 (wave64): a block is 16 wavefronts (4 a SIMD, 128 registers each); each wavefront owns 32 weight rows
+// and dequantizes them straight from the planar store into the MFMA's B operand.  The K loop runs over 512-column runs
+// of 8 steps, cut into chunks (Q4_K: 4 steps, one super-block; Q8_0: 2 steps): lane (n = l % 32, h = l / 32) holds row
+// n's 16-byte pieces of the chunk's steps for lane-half h, and each step's 16 bytes are exactly the lane's 4 x 8 MFMA
+// k-slots (the columns are permuted; the sum does not depend on the order of k).  The store's 32-row tiling makes every
+// such request whole 128-byte lines.  The job's activation rows for the run sit in LDS and feed the A operand with the
+// same permutation.  Weight chunks stream through two register slots; the next run's activations come into the other
+// LDS buffer by asynchronous global -> LDS copies.  D[token][row] leaves as 128-byte runs of consecutive rows.
 #include "mv.hpp"
 
 namespace sfnx {
 namespace {
 
-#ifdef SFNX_PHASE_PROF
-__device__ unsigned long long g_mma_prof[512][20];   // wall-clock stamps of blocks (job < 512, slice 0)
-#define MPROF(i) if (threadIdx.x == 0 && pj >= 0) g_mma_prof[pj][i] = wall_clock64();
-#else
-#define MPROF(i)
-#endif
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float float16v __attribute__((ext_vector_type(16)));
 
-constexpr int MM_WAVES = 8, MM_THREADS = MM_WAVES * WAVE, MM_BM = 32 * MM_WAVES;   // 256 weight rows a block
+// SiLU on the prompt path as the reference compiles it (src/moe_mma.cuh:382-388 under --use_fast_math: __expf is
+// 2^(x log2 e) on the hardware exp2, the division a reciprocal): x rcp(1 + 2^(-x log2 e))
+__device__ __forceinline__ float silu_fast(float x) {
+    return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * 1.44269504088896340736f));
+}
+
+constexpr int MM_WAVES = 16, MM_THREADS = MM_WAVES * WAVE, MM_BM = 32 * MM_WAVES;   // 512 weight rows a block
 __device__ __forceinline__ half2v as_h2(uint32_t u) { return __builtin_bit_cast(half2v, u); }
 
 // bytes 0, 1 (SEL 0) or 2, 3 (SEL 1) of w as two f16 values 1024 + byte (0x64 above each byte)
@@ -75,55 +76,63 @@ __device__ __forceinline__ void deq_q80(const uint4& qa, const uint4& qb, half2v
         }
 }
 
-// One lane's raw weights for a run of 512 columns (8 steps of 64): Q4_K: its 128-byte half-line of the row's run (the
-// 16-byte halves h of the run's 8 groups) and the run's two super-block headers; Q8_0: blocks 8 h .. 8 h + 7 of the
-// run's 16 (both 16-byte halves of each, contiguous) and their scales.  Step j pairs lane-half 0's group / block j with
-// lane-half 1's.
-template <int TYPE> struct RunW;
-template <> struct RunW<SFNX_Q4_K> {
-    uint4 q[8], hdr[2];
+// One lane's raw weights for a chunk of a 512-column run (Q4_K: 4 steps of 64 columns, one super-block; Q8_0: 2 steps).
+// Q4_K: 4 of the 16-byte halves h of the run's 8 groups (64 bytes of the lane's 128-byte half-line) and the chunk's
+// super-block header; Q8_0: blocks 8 h + 2 c, 8 h + 2 c + 1 of the run's 16 (both 16-byte halves of each) and their two
+// scales.  Step j of a run pairs lane-half 0's group / block j with lane-half 1's.
+template <int TYPE> struct Chunk;
+template <> struct Chunk<SFNX_Q4_K> {
+    static constexpr int STEPS = 4, LOADS = 5;   // steps a chunk; load instructions a chunk
+    uint4 q[4], hdr;
 };
-template <> struct RunW<SFNX_Q8_0> {
-    uint4 qa[8], qb[8], d;
+template <> struct Chunk<SFNX_Q8_0> {
+    static constexpr int STEPS = 2, LOADS = 5;
+    uint4 qa[2], qb[2];
+    uint32_t d;
 };
 
-__device__ __forceinline__ void load_run(RunW<SFNX_Q4_K>& w, const uint8_t* mat, int R, int C, int row, int r, int h) {
+// Where chunk c (of the run's 8 / STEPS) of run r of the lane's row lies.
+struct ChunkAt {
+    const uint8_t* q;     // the first 16-byte piece (Q4_K: nibbles; Q8_0: first halves); the next one PIECE_STRIDE on
+    const uint8_t* tail;  // Q4_K: the super-block header; Q8_0: the two f16 scales
+};
+__device__ __forceinline__ ChunkAt chunk_at(const Chunk<SFNX_Q4_K>*, const uint8_t* mat, int R, int C, int row, int r, int c, int h) {
     const Q4kPlanes P = q4k_planes(mat, R, C);
-    const uint4* q = reinterpret_cast<const uint4*>(P.nib_row(row, C) + 512 / 2 * r + 128 * h);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) w.q[j] = q[j];
-    const uint4* hd = reinterpret_cast<const uint4*>(P.hdr_row(row, C) + 32 * r);
-    w.hdr[0] = hd[0];
-    w.hdr[1] = hd[1];
+    return ChunkAt{P.nib16(row, C, 16 * r + 8 * h + 4 * c), P.hdr16(row, C, 2 * r + c)};
 }
-__device__ __forceinline__ void load_run(RunW<SFNX_Q8_0>& w, const uint8_t* mat, int R, int C, int row, int r, int h) {
+__device__ __forceinline__ ChunkAt chunk_at(const Chunk<SFNX_Q8_0>*, const uint8_t* mat, int R, int C, int row, int r, int c, int h) {
     const Q80Planes P = q80_planes(mat, R, C);
-    const uint4* qa = reinterpret_cast<const uint4*>(P.q + (size_t) row * C + 512 * r + 128 * h);
-    const uint4* qb = reinterpret_cast<const uint4*>(P.q + (size_t) row * C + 512 * r + 256 + 128 * h);
+    return ChunkAt{P.q16(row, C, 32 * r + 8 * h + 2 * c), P.d16(row, C, 2 * r + h) + 4 * c};
+}
+__device__ __forceinline__ void load_piece(Chunk<SFNX_Q4_K>& w, const ChunkAt& a, int s) {
+    w.q[s] = *reinterpret_cast<const uint4*>(a.q + PIECE_STRIDE * s);
+}
+__device__ __forceinline__ void load_piece(Chunk<SFNX_Q8_0>& w, const ChunkAt& a, int s) {
+    w.qa[s] = *reinterpret_cast<const uint4*>(a.q + PIECE_STRIDE * s);
+    w.qb[s] = *reinterpret_cast<const uint4*>(a.q + PIECE_STRIDE * (16 + s));   // the blocks' second halves
+}
+__device__ __forceinline__ void load_tail(Chunk<SFNX_Q4_K>& w, const ChunkAt& a) { w.hdr = *reinterpret_cast<const uint4*>(a.tail); }
+__device__ __forceinline__ void load_tail(Chunk<SFNX_Q8_0>& w, const ChunkAt& a) { w.d = *reinterpret_cast<const uint32_t*>(a.tail); }
+template <int TYPE> __device__ __forceinline__ void load_chunk(Chunk<TYPE>& w, const ChunkAt& a) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        w.qa[j] = qa[j];
-        w.qb[j] = qb[j];
-    }
-    w.d = *reinterpret_cast<const uint4*>(P.d + (size_t) row * (C / 32) + 16 * r + 8 * h);
+    for (int s = 0; s < Chunk<TYPE>::STEPS; ++s) load_piece(w, a, s);
+    load_tail(w, a);
 }
 
-__device__ __forceinline__ void dequant_step(const RunW<SFNX_Q4_K>& w, int j, half8 (&b)[4]) {
-    const uint4 hd = w.hdr[j / 4];
+// step s of a chunk as the 4 B fragments of its MFMAs
+__device__ __forceinline__ void dequant_step(const Chunk<SFNX_Q4_K>& w, int s, half8 (&b)[4]) {
+    const uint4 hd = w.hdr;
     const float d = h2f((uint16_t) (hd.x & 0xffff)), dmin = h2f((uint16_t) (hd.x >> 16));
-    const int jg = j % 4;
     float sc, m;
-    q4k_scale_min(hd, 2 * jg, sc, m);
+    q4k_scale_min(hd, 2 * s, sc, m);
     const _Float16 d1l = (_Float16) (d * sc), nml = (_Float16) (-(dmin * m));
-    q4k_scale_min(hd, 2 * jg + 1, sc, m);
+    q4k_scale_min(hd, 2 * s + 1, sc, m);
     const _Float16 d1h = (_Float16) (d * sc), nmh = (_Float16) (-(dmin * m));
-    deq_q4k(w.q[j], half2v{d1l, d1l}, half2v{nml, nml}, half2v{d1h, d1h}, half2v{nmh, nmh}, b);
+    deq_q4k(w.q[s], half2v{d1l, d1l}, half2v{nml, nml}, half2v{d1h, d1h}, half2v{nmh, nmh}, b);
 }
-__device__ __forceinline__ void dequant_step(const RunW<SFNX_Q8_0>& w, int j, half8 (&b)[4]) {
-    const uint32_t dw[4] = {w.d.x, w.d.y, w.d.z, w.d.w};
-    const uint16_t db = (uint16_t) (dw[j / 2] >> (16 * (j % 2)));
-    const _Float16 d = __builtin_bit_cast(_Float16, db);
-    deq_q80(w.qa[j], w.qb[j], half2v{d, d}, b);
+__device__ __forceinline__ void dequant_step(const Chunk<SFNX_Q8_0>& w, int s, half8 (&b)[4]) {
+    const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t) (w.d >> (16 * s)));
+    deq_q80(w.qa[s], w.qb[s], half2v{d, d}, b);
 }
 
 // column (within the run's 512) where MFMA k-chunk c of step j starts for lane-half h
@@ -132,170 +141,187 @@ template <int TYPE> __device__ __forceinline__ int run_col(int j, int c, int h) 
     else return 256 * h + 32 * j + 8 * c;
 }
 
+#ifndef MM_SLOTS
+#define MM_SLOTS 2   // weight chunks a wavefront keeps in registers: the one being dotted and the ones in flight
+#endif
 constexpr int MM_RUN = 512, MM_XLD = MM_RUN + 8;   // columns a run; LDS row pitch (16 bytes past the run: rows shift banks)
 constexpr int MM_XROWS = 64 / MM_WAVES;             // activation rows a wavefront moves per run
 constexpr size_t MM_XBUF = 64 * MM_XLD;              // halves in one activation buffer
 
 // run r of the job's activation rows into an LDS buffer by asynchronous global -> LDS copies (no registers): wavefront w
-// moves rows w * 8 .. w * 8 + 7, a row of 512 halves a copy (64 lanes x 16 bytes); rows past n are left as they are
+// moves rows w * 4 .. w * 4 + 3, a row of 512 halves a copy (64 lanes x 16 bytes); rows past n are left as they are
 // (they only feed output rows that are never stored)
-template <int XR = MM_XROWS>
 __device__ __forceinline__ void load_x_async(_Float16* buf, const _Float16* __restrict__ x, int ldx, const int* ys, int n,
                                              int r, int wave, int lane) {
 #pragma unroll
-    for (int i = 0; i < XR; ++i) {
-        const int m = wave * XR + i;
+    for (int i = 0; i < MM_XROWS; ++i) {
+        const int m = wave * MM_XROWS + i;
         if (m < n)
             __builtin_amdgcn_global_load_lds(x + (size_t) ys[m] * ldx + MM_RUN * r + 8 * lane,
                                              (__attribute__((address_space(3))) void*) (buf + (size_t) m * MM_XLD), 16, 0, 0);
     }
 }
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }   // vmcnt(0), others unwaited
+// vmcnt(N), others unwaited (N < 64: bits 3:0 and 15:14)
+template <int N> __device__ __forceinline__ void wait_vmem_below() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
 
-// One run's 8 steps of 64 columns on one wavefront's 32 weight rows: step j's activation fragments are read from LDS
-// first, then step j + 1's weight fragments are dequantized (VALU, covering the LDS latency) interleaved with step j's
-// MFMAs; the scheduling groups keep that order (1 MFMA, then a share of the VALU).
+// One chunk's steps on one wavefront's 32 weight rows: per step the 4 B fragments are dequantized from the registers
+// (VALU), then each of the 4 k-pieces takes the activation fragment from LDS and one MFMA per 32-token tile.  Several
+// wavefronts share each SIMD, so one's dequantization overlaps another's matrix work.
 template <int TYPE, int NT>
-__device__ __forceinline__ void mma_run(const RunW<TYPE>& w, const _Float16* xb, int nn, int h, float16v (&acc)[NT]) {
-    half8 bc[4], bn[4];
-    dequant_step(w, 0, bc);
+__device__ __forceinline__ void mma_chunk(const Chunk<TYPE>& w, int cj, const _Float16* xb, int nn, int h, float16v (&acc)[NT]) {
+    constexpr int S = Chunk<TYPE>::STEPS;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        half8 ac[NT][4];
+    for (int s = 0; s < S; ++s) {
+        half8 b[4];
+        dequant_step(w, s, b);
+        const int j = cj * S + s;
 #pragma unroll
-        for (int t = 0; t < NT; ++t)
+        for (int c = 0; c < 4; ++c) {
+            half8 a[NT];
 #pragma unroll
-            for (int c = 0; c < 4; ++c)
-                ac[t][c] = *reinterpret_cast<const half8*>(xb + (size_t) (32 * t + nn) * MM_XLD + run_col<TYPE>(j, c, h));
-        if (j < 7) dequant_step(w, j + 1, bn);
+            for (int t = 0; t < NT; ++t) a[t] = *reinterpret_cast<const half8*>(xb + (size_t) (32 * t + nn) * MM_XLD + run_col<TYPE>(j, c, h));
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
-#pragma unroll
-            for (int t = 0; t < NT; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ac[t][c], bc[c], acc[t], 0, 0, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 4 * NT, 0);   // the DS reads
-        __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);       // VALU while they land
-#pragma unroll
-        for (int q = 0; q < 4 * NT; ++q) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // an MFMA
-            __builtin_amdgcn_sched_group_barrier(0x002, 48 / (4 * NT), 0);
+            for (int t = 0; t < NT; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[t], b[c], acc[t], 0, 0, 0);
         }
-        if (j < 7)
-#pragma unroll
-            for (int c = 0; c < 4; ++c) bc[c] = bn[c];
     }
 }
 
-// The block's rows are G groups of 256 (a wavefront's 32 rows each); per group the runs of 512 columns, per run 8
-// steps of 64.  Weights stream one run ahead of the steps (registers); each run's activations come into the other LDS
-// buffer while this one is read.  A single run (the down projection) is staged once for every group.
-// rows: ys[0..n) (activation rows) and outs[0..n) (output rows), n <= 32 NT
-template <int TYPE, int NT>
-__device__ __forceinline__ void mma_job(const uint8_t* mat, int R, int C, int row0, int G, int wave, int lane,
-                                        const int* ys, const int* outs, int n, const _Float16* __restrict__ x, int ldx,
-                                        _Float16* xs, float* __restrict__ out, int pj) {
-    (void) pj;   // the job's row of phase stamps in the instrumented build, or -1
-    constexpr int XR = NT <= 2 ? MM_XROWS : 4 * NT;   // activation rows a wavefront stages
-    const int h = lane / 32, nn = lane % 32, nr = C / MM_RUN, total = G * nr;
-    auto row_of = [&](int it) { return row0 + (it / nr) * MM_BM + wave * 32 + nn; };
-    RunW<TYPE> w, wn;
-    load_x_async<XR>(xs, x, ldx, ys, n, 0, wave, lane);
-    load_run(w, mat, R, C, row_of(0), 0, h);
-    float16v acc[NT];
-    for (int it = 0; it < total; ++it) {
-        if (it < 16) { MPROF(2 + it) }
-        const int r = it % nr;
-        if (r == 0) {
+// The chunk walk shared by both kernels.  A wavefront's work is `tiles` row tiles of 32 rows (row_of(it)), each over
+// the nr runs of 512 columns, each run CPR chunks: chunk k = (tile, run, chunk-in-run) in that order.  Weights stream
+// through two register slots, chunk k + 2 requested as soon as chunk k is dotted.  The job's activation rows for a run
+// sit in one of two LDS buffers; run r + 1's are requested (global -> LDS, no registers) when run r starts, so each
+// run start waits only for them, not for the weight chunks requested after them (CPR chunks of LOADS requests each).
+// tile_done(it, acc) takes a tile's accumulators (and they are cleared for the next tile); the last tile's stay in acc.
+template <int TYPE, int NT, typename RowOf, typename TileDone>
+__device__ __forceinline__ void chunk_walk(const uint8_t* mat, int R, int C, int tiles, RowOf row_of, int wave, int lane,
+                                           const int* ys, int n, const _Float16* __restrict__ x, _Float16* xs,
+                                           float16v (&acc)[NT], TileDone tile_done) {
+    constexpr int CPR = 8 / Chunk<TYPE>::STEPS, LD = Chunk<TYPE>::LOADS;
+    const int h = lane / 32, nn = lane % 32, nr = C / MM_RUN, per_tile = nr * CPR, NK = tiles * per_tile;
+    auto at = [&](int k) {
+        const int it = k / per_tile, rc = k % per_tile;
+        return chunk_at((const Chunk<TYPE>*) nullptr, mat, R, C, row_of(it), rc / CPR, rc % CPR, h);
+    };
+    load_x_async(xs, x, C, ys, n, 0, wave, lane);
+    Chunk<TYPE> w[MM_SLOTS];
+#pragma unroll
+    for (int i = 0; i < MM_SLOTS; ++i)
+        if (i < NK) load_chunk(w[i], at(i));
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = float16v{};
+    // one chunk: the run's activations first when the chunk starts a run, then the dots, then the tile's end
+    auto step = [&](const Chunk<TYPE>& w, int k) {
+        const int rc = k % per_tile, r = rc / CPR, cj = rc % CPR, rg = k / CPR;   // rg: runs walked so far
+        _Float16* xb = xs + (size_t) (nr > 1 ? rg & 1 : 0) * MM_XBUF;
+        if (cj == 0 && (nr > 1 || k == 0)) {
+            if (k == 0) wait_vmem();
+            else {
+                // this run's rows: requested before the weight chunks of the CPR chunks since (those past the end
+                // were not requested)
+                const int after = min(CPR, max(0, NK - MM_SLOTS - (k - CPR)));
+                if (after == CPR) wait_vmem_below<CPR * LD>();
+                else if (after >= 2) wait_vmem_below<2 * LD>();
+                else if (after == 1) wait_vmem_below<LD>();
+                else wait_vmem();
+            }
+            __syncthreads();                  // every wavefront's rows landed; every wavefront is past the previous run
+            if (nr > 1 && k + per_tile / nr < NK) load_x_async(xs + (size_t) ((rg + 1) & 1) * MM_XBUF, x, C, ys, n, (r + 1) % nr, wave, lane);
+        }
+        mma_chunk<TYPE, NT>(w, cj, xb, nn, h, acc);
+        if (rc == per_tile - 1 && k + 1 < NK) {
+            tile_done(k / per_tile, acc);
 #pragma unroll
             for (int t = 0; t < NT; ++t) acc[t] = float16v{};
         }
-        // buffers alternate by iteration (one run staged for good when there is only one)
-        _Float16* xb = xs + (size_t) (nr > 1 ? it & 1 : 0) * MM_XBUF;
-        if (nr > 1 || it == 0) {
-            wait_vmem();          // this run's activations (and the weights of this step, needed now anyway)
-            __syncthreads();      // every wavefront's rows landed; every wavefront is past the previous run
-            if (nr > 1 && it + 1 < total)
-                load_x_async<XR>(xs + (size_t) ((it + 1) & 1) * MM_XBUF, x, ldx, ys, n, (r + 1) % nr, wave, lane);
-        }
-        if (it + 1 < total) load_run(wn, mat, R, C, row_of(it + 1), (it + 1) % nr, h);
-        mma_run<TYPE, NT>(w, xb, nn, h, acc);
-        if (r == nr - 1) {
-            // D[token][row]: lane (nn, h), value q at token 8 (q / 4) + 4 h + q % 4 of the tile
-            const int row = row_of(it);
+    };
+    for (int k0 = 0; k0 < NK; k0 += MM_SLOTS) {
 #pragma unroll
-            for (int t = 0; t < NT; ++t)
-#pragma unroll
-                for (int q = 0; q < 16; ++q) {
-                    const int m = 32 * t + 8 * (q / 4) + 4 * h + q % 4;
-                    if (m < n) out[(size_t) outs[m] * R + row] = acc[t][q];
-                }
+        for (int i = 0; i < MM_SLOTS; ++i) {
+            const int k = k0 + i;
+            if (k < NK) {
+                step(w[i], k);
+                if (k + MM_SLOTS < NK) load_chunk(w[i], at(k + MM_SLOTS));
+            }
         }
-        w = wn;
     }
 }
 
-// The gate|up projection by pairs of row groups: a block owns FF indices f0 .. f0 + 255, i.e. gate rows f0 + . and the
-// matching up rows ff + f0 + .; the runs of 512 columns are the outer loop and each run's activations are staged once
-// for both groups.  Epilogue: gu (fp32 rows, when given) and h16 = f16(silu(gate) up) (when given), from the same
-// accumulators, so the fused form equals moe_gate_up_mma followed by swiglu_h16 bit for bit.
+// D[token][row] of a tile: lane (nn, h), value q at token 8 (q / 4) + 4 h + q % 4 of 32-token tile t
+__device__ __forceinline__ int acc_token(int t, int q, int h) { return 32 * t + 8 * (q / 4) + 4 * h + q % 4; }
+
+// rows: ys[0..n) (activation rows) and outs[0..n) (output rows), n <= 32 NT; the block's rows are G tiles of 512
+template <int TYPE, int NT>
+__device__ __forceinline__ void mma_job(const uint8_t* mat, int R, int C, int row0, int G, int wave, int lane,
+                                        const int* ys, const int* outs, int n, const _Float16* __restrict__ x,
+                                        _Float16* xs, float* __restrict__ out) {
+    const int h = lane / 32, nn = lane % 32;
+    auto row_of = [&](int it) { return row0 + it * MM_BM + wave * 32 + nn; };
+    auto store = [&](int it, const float16v (&acc)[NT]) {
+        const int row = row_of(it);
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const int m = acc_token(t, q, h);
+                if (m < n) out[(size_t) outs[m] * R + row] = acc[t][q];
+            }
+    };
+    float16v acc[NT];
+    chunk_walk<TYPE, NT>(mat, R, C, G, row_of, wave, lane, ys, n, x, xs, acc, store);
+    store(G - 1, acc);
+}
+
+// The gate|up projection: a block owns FF indices f0 .. f0 + 255; wavefronts 0-7 take the gate rows f0 + 32 w + .,
+// wavefronts 8-15 the matching up rows ff + f0 + 32 (w - 8) + .  Epilogue: gu (fp32 rows, when given) and h16 =
+// f16(silu(gate) up) (when given), from the same accumulators, so the fused form equals moe_gate_up_mma followed by
+// swiglu_h16 bit for bit.  The up accumulators reach the gate wavefronts through LDS.
+constexpr int MM_FF = MM_BM / 2;   // FF indices a gate|up block owns
 template <int TYPE, int NT>
 __device__ __forceinline__ void mma_gu_job(const uint8_t* mat, int ff, int C, int f0, int wave, int lane,
                                            const sfnx_bigjob& jb, const _Float16* __restrict__ x, _Float16* xs,
                                            float* __restrict__ gu, _Float16* __restrict__ h16) {
-    const int h = lane / 32, nn = lane % 32, nr = C / MM_RUN, R = 2 * ff, f = f0 + wave * 32 + nn;
-    const int rows[2] = {f, ff + f};
-    RunW<TYPE> w, wn;
-    load_x_async(xs, x, C, jb.y, jb.n, 0, wave, lane);
-    load_run(w, mat, R, C, rows[0], 0, h);
-    float16v acc[2][NT];
-#pragma unroll
-    for (int g = 0; g < 2; ++g)
-#pragma unroll
-        for (int t = 0; t < NT; ++t) acc[g][t] = float16v{};
-    for (int r = 0; r < nr; ++r) {
-        _Float16* xb = xs + (size_t) (r & 1) * MM_XBUF;
-#pragma unroll
-        for (int g = 0; g < 2; ++g) {
-            if (g == 0) {
-                wait_vmem();          // this run's activations and gate weights
-                __syncthreads();      // every wavefront's rows landed; every wavefront is past the previous run
-                if (r + 1 < nr) load_x_async(xs + (size_t) ((r + 1) & 1) * MM_XBUF, x, C, jb.y, jb.n, r + 1, wave, lane);
-                load_run(wn, mat, R, C, rows[1], r, h);
-            } else if (r + 1 < nr) {
-                load_run(wn, mat, R, C, rows[0], r + 1, h);
-            }
-            mma_run<TYPE, NT>(w, xb, nn, h, acc[g]);
-            w = wn;
-        }
-    }
+    const int h = lane / 32, nn = lane % 32, R = 2 * ff, up = wave >= MM_WAVES / 2, fl = 32 * (wave % (MM_WAVES / 2)) + nn;
+    const int row = (up ? ff : 0) + f0 + fl;
+    float16v res[NT];
+    chunk_walk<TYPE, NT>(mat, R, C, 1, [&](int) { return row; }, wave, lane, jb.y, jb.n, x, xs, res,
+                         [](int, const float16v (&)[NT]) {});
     if (gu) {
 #pragma unroll
         for (int t = 0; t < NT; ++t)
 #pragma unroll
             for (int q = 0; q < 16; ++q) {
-                const int m = 32 * t + 8 * (q / 4) + 4 * h + q % 4;
-                if (m < jb.n) {
-                    const size_t o = (size_t) jb.out[m];
-                    gu[o * R + rows[0]] = acc[0][t][q];
-                    gu[o * R + rows[1]] = acc[1][t][q];
-                }
+                const int m = acc_token(t, q, h);
+                if (m < jb.n) gu[(size_t) jb.out[m] * R + row] = res[t][q];
             }
     }
     if (h16) {
-        // h through LDS ([token][256 FF indices], the last run's buffer is free once every wavefront is past it), then
-        // 16-byte stores of whole 512-byte row pieces
-        constexpr int HLD = MM_BM + 8;
-        _Float16* hs = xs;
-        __syncthreads();
+        // up rows as fp32 [token][256] at the start of LDS, then h as f16 [token][256 (+8)] after them, then 16-byte
+        // stores of whole 512-byte row pieces
+        constexpr int HLD = MM_FF + 8;
+        float* us = reinterpret_cast<float*>(xs);
+        _Float16* hs = xs + 2 * 64 * MM_FF;
+        __syncthreads();   // every wavefront is past the last run's activations
+        if (up)
 #pragma unroll
-        for (int t = 0; t < NT; ++t)
+            for (int t = 0; t < NT; ++t)
 #pragma unroll
-            for (int q = 0; q < 16; ++q) {
-                const int m = 32 * t + 8 * (q / 4) + 4 * h + q % 4;
-                hs[m * HLD + wave * 32 + nn] = (_Float16) (silu_f(acc[0][t][q]) * acc[1][t][q]);
-            }
+                for (int q = 0; q < 16; ++q) us[acc_token(t, q, h) * MM_FF + fl] = res[t][q];
         __syncthreads();
-        for (int i = threadIdx.x; i < jb.n * (MM_BM / 8); i += MM_THREADS) {
-            const int m = i / (MM_BM / 8), c = i % (MM_BM / 8);
+        if (!up)
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int q = 0; q < 16; ++q) {
+                    const int m = acc_token(t, q, h);
+                    hs[m * HLD + fl] = (_Float16) (silu_fast(res[t][q]) * us[m * MM_FF + fl]);
+                }
+        __syncthreads();
+        for (int i = threadIdx.x; i < jb.n * (MM_FF / 8); i += MM_THREADS) {
+            const int m = i / (MM_FF / 8), c = i % (MM_FF / 8);
             *reinterpret_cast<uint4*>(h16 + (size_t) jb.out[m] * ff + f0 + 8 * c) = *reinterpret_cast<const uint4*>(hs + m * HLD + 8 * c);
         }
     }
@@ -318,7 +344,7 @@ __global__ void __launch_bounds__(MM_THREADS) k_moe_mma_gu(const uint8_t* __rest
                                                           const _Float16* __restrict__ x, float* __restrict__ gu,
                                                           _Float16* __restrict__ h16) {
     int sl, ji;
-    xcd_job(blockIdx.x, ff / MM_BM, sl, ji);
+    xcd_job(blockIdx.x, ff / MM_FF, sl, ji);
     if (ji >= *njobs) return;
     __shared__ sfnx_bigjob jb;
     extern __shared__ __align__(16) unsigned char xs_raw[];
@@ -327,8 +353,8 @@ __global__ void __launch_bounds__(MM_THREADS) k_moe_mma_gu(const uint8_t* __rest
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
     const uint8_t* mat = A + (size_t) jb.w * sa;
     _Float16* xs = reinterpret_cast<_Float16*>(xs_raw);
-    if (jb.n > 32) mma_gu_job<TYPE, 2>(mat, ff, C, sl * MM_BM, wave, lane, jb, x, xs, gu, h16);
-    else mma_gu_job<TYPE, 1>(mat, ff, C, sl * MM_BM, wave, lane, jb, x, xs, gu, h16);
+    if (jb.n > 32) mma_gu_job<TYPE, 2>(mat, ff, C, sl * MM_FF, wave, lane, jb, x, xs, gu, h16);
+    else mma_gu_job<TYPE, 1>(mat, ff, C, sl * MM_FF, wave, lane, jb, x, xs, gu, h16);
 }
 
 template <int TYPE>
@@ -337,8 +363,6 @@ __global__ void __launch_bounds__(MM_THREADS) k_moe_mma(const uint8_t* __restric
                                                        const _Float16* __restrict__ x, float* __restrict__ out) {
     int sl, ji;
     xcd_job(blockIdx.x, R / (G * MM_BM), sl, ji);
-    const int pj = sl == 0 && ji < 512 ? ji : -1;
-    MPROF(0)
     if (ji >= *njobs) return;
     __shared__ sfnx_bigjob jb;
     extern __shared__ __align__(16) unsigned char xs_raw[];
@@ -348,10 +372,8 @@ __global__ void __launch_bounds__(MM_THREADS) k_moe_mma(const uint8_t* __restric
     const uint8_t* mat = A + (size_t) jb.w * sa;
     _Float16* xs = reinterpret_cast<_Float16*>(xs_raw);
     const int row0 = sl * G * MM_BM;
-    MPROF(1)
-    if (jb.n > 32) mma_job<TYPE, 2>(mat, R, C, row0, G, wave, lane, jb.y, jb.out, jb.n, x, C, xs, out, pj);
-    else mma_job<TYPE, 1>(mat, R, C, row0, G, wave, lane, jb.y, jb.out, jb.n, x, C, xs, out, pj);
-    MPROF(18)
+    if (jb.n > 32) mma_job<TYPE, 2>(mat, R, C, row0, G, wave, lane, jb.y, jb.out, jb.n, x, xs, out);
+    else mma_job<TYPE, 1>(mat, R, C, row0, G, wave, lane, jb.y, jb.out, jb.n, x, xs, out);
 }
 
 // k_swiglu_h16 (src/moe_mma.cuh:382-388): h16 = f16(silu(gate) * up) of P rows [gate (ff) | up (ff)]
@@ -359,7 +381,7 @@ __global__ void k_swiglu_h16(const float* __restrict__ gu, int ff, int P, _Float
     const size_t n = (size_t) P * ff;
     for (size_t e = blockIdx.x * (size_t) blockDim.x + threadIdx.x; e < n; e += (size_t) gridDim.x * blockDim.x) {
         const size_t p = e / ff, i = e % ff;
-        h16[e] = (_Float16) (silu_f(gu[p * 2 * ff + i]) * gu[p * 2 * ff + ff + i]);
+        h16[e] = (_Float16) (silu_fast(gu[p * 2 * ff + i]) * gu[p * 2 * ff + ff + i]);
     }
 }
 
@@ -374,14 +396,13 @@ void moe_mma(uint32_t type, const void* A, size_t sa, int n_in, int n_out, const
              int njobs_cap, const void* x16, float* out, void* st) {
     require(type == SFNX_Q4_K || type == SFNX_Q8_0, "expert type must be Q4_K (12) or Q8_0 (8)");
     require(n_in > 0 && n_in % 512 == 0, "expert input width must be a multiple of 512");
-    require(n_out > 0 && n_out % MM_BM == 0, "expert rows must be a multiple of 256");
+    require(n_out > 0 && n_out % MM_BM == 0, "expert rows must be a multiple of 512");
     require((n_out / MM_BM) % std::max(1, (n_out / MM_BM) / 2) == 0, "row groups must split evenly");
     require(sa >= row_bytes(type, n_in) * (size_t) n_out, "expert stride smaller than a matrix");
     require(njobs_cap >= 0 && njobs_cap <= (1 << 20), "njobs_cap out of range");
     if (njobs_cap == 0) return;
-    // groups of 256 rows a block: every row in one block when one run covers the input (the activations are staged
-    // once); else two blocks a job, for more blocks than compute units
-    const int groups = n_out / MM_BM, G = n_in == MM_RUN ? groups : std::max(1, groups / 2);
+    // tiles of 512 rows: two blocks a job (half the tiles each), for more blocks than compute units
+    const int groups = n_out / MM_BM, G = std::max(1, groups / 2);
     const dim3 grid(xcd_grid(groups / G, njobs_cap));
     hipStream_t s = stream_of(st);
     if (type == SFNX_Q4_K)
@@ -394,11 +415,11 @@ void moe_mma_gu(uint32_t type, const void* A, size_t sa, int n_in, int ff, const
                 int njobs_cap, const void* x16, float* gu, uint16_t* h16, void* st) {
     require(type == SFNX_Q4_K || type == SFNX_Q8_0, "expert type must be Q4_K (12) or Q8_0 (8)");
     require(n_in > 0 && n_in % 512 == 0, "expert input width must be a multiple of 512");
-    require(ff > 0 && ff % MM_BM == 0, "FF must be a multiple of 256");
+    require(ff > 0 && ff % MM_FF == 0, "FF must be a multiple of 256");
     require(sa >= row_bytes(type, n_in) * (size_t) (2 * ff), "expert stride smaller than a matrix");
     require(njobs_cap >= 0 && njobs_cap <= (1 << 20), "njobs_cap out of range");
     if (njobs_cap == 0) return;
-    const dim3 grid(xcd_grid(ff / MM_BM, njobs_cap));
+    const dim3 grid(xcd_grid(ff / MM_FF, njobs_cap));
     hipStream_t s = stream_of(st);
     if (type == SFNX_Q4_K)
         k_moe_mma_gu<SFNX_Q4_K><<<grid, MM_THREADS, MM_LDS, s>>>((const uint8_t*) A, sa, ff, n_in, jobs, njobs,
@@ -413,16 +434,11 @@ void moe_mma_gu(uint32_t type, const void* A, size_t sa, int n_in, int ff, const
 
 using namespace sfnx;
 
-#ifdef SFNX_PHASE_PROF
-extern "C" int sfnx_mma_prof_read(unsigned long long* out) {
-    return hipMemcpyFromSymbol(out, HIP_SYMBOL(g_mma_prof), sizeof(g_mma_prof)) == hipSuccess ? 0 : -1;
-}
-#endif
 
 extern "C" int sfnx_moe_gate_up_mma(const void* A, size_t sa, uint32_t type, int n_in, int n_out, const sfnx_bigjob* jobs,
                                     const int* njobs, int njobs_cap, const uint16_t* xh, float* gu, void* st) {
     return guarded("sfnx_moe_gate_up_mma", [&] {
-        if (n_out % (2 * MM_BM) == 0 && n_in > MM_RUN)
+        if (n_out % (2 * MM_FF) == 0 && n_in > MM_RUN)
             moe_mma_gu(type, A, sa, n_in, n_out / 2, jobs, njobs, njobs_cap, xh, gu, nullptr, st);
         else
             moe_mma(type, A, sa, n_in, n_out, jobs, njobs, njobs_cap, xh, gu, st);

@@ -81,13 +81,11 @@ template <int GPL> struct Q4kRow {
     float d[GPL], dmin[GPL], sc0[GPL], m0[GPL], sc1[GPL], m1[GPL];
     // the loads alone (issue several rows' before any prepare, so that their latencies overlap)
     __device__ __forceinline__ void issue(const Q4kPlanes& P, int row, int C, int l8) {
-        const uint8_t* nib = P.nib_row(row, C);
-        const uint8_t* hdr = P.hdr_row(row, C);
 #pragma unroll
         for (int i = 0; i < GPL; ++i) {
-            q0[i] = *reinterpret_cast<const uint4*>(nib + 256 * i + 16 * l8);
-            q1[i] = *reinterpret_cast<const uint4*>(nib + 256 * i + 128 + 16 * l8);
-            h[i] = *reinterpret_cast<const uint4*>(hdr + 16 * (2 * i + (l8 >> 2)));
+            q0[i] = *reinterpret_cast<const uint4*>(P.nib16(row, C, 16 * i + l8));
+            q1[i] = *reinterpret_cast<const uint4*>(P.nib16(row, C, 16 * i + 8 + l8));
+            h[i] = *reinterpret_cast<const uint4*>(P.hdr16(row, C, 2 * i + (l8 >> 2)));
         }
     }
     // the block headers decoded: d, dmin and this lane's two sub-blocks' 6-bit scales and mins
@@ -152,13 +150,11 @@ template <int BPL> struct Q80Row {
     uint16_t dh[BPL];
     float dw[BPL];
     __device__ __forceinline__ void issue(const Q80Planes& P, int row, int C, int l16) {
-        const uint8_t* q = P.q + (size_t) row * C;
-        const uint16_t* d = P.d + (size_t) row * (C / 32);
 #pragma unroll
         for (int i = 0; i < BPL; ++i) {
-            qa[i] = *reinterpret_cast<const uint4*>(q + 512 * i + 16 * l16);
-            qb[i] = *reinterpret_cast<const uint4*>(q + 512 * i + 256 + 16 * l16);
-            dh[i] = d[l16 + 16 * i];
+            qa[i] = *reinterpret_cast<const uint4*>(P.q16(row, C, 32 * i + l16));
+            qb[i] = *reinterpret_cast<const uint4*>(P.q16(row, C, 32 * i + 16 + l16));
+            dh[i] = *P.dof(row, C, l16 + 16 * i);
         }
     }
     __device__ __forceinline__ void prepare(int) {

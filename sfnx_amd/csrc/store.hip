@@ -113,8 +113,8 @@ __global__ void k_pack_q4k(const uint8_t* __restrict__ src, uint8_t* __restrict_
     const int r = (int) ((k % per_mat) / nb), b = (int) (k % nb);
     const size_t mat_bytes = (size_t) R * nb * Q4K_BYTES;
     const size_t gg = m * mat_bytes + ((size_t) r * nb + b) * Q4K_BYTES;                          // GGUF block
-    const size_t nib = m * mat_bytes + (size_t) r * (C / 2) + (size_t) (b / 2) * 256;             // run
-    const size_t hdr = m * mat_bytes + (size_t) R * (C / 2) + ((size_t) r * nb + b) * 16;
+    const Q4kPlanes P = q4k_planes((const uint8_t*) nullptr + m * mat_bytes, R, C);
+    const size_t hdr = (size_t) P.hdr16(r, C, b);
     for (int i = 0; i < 16; ++i) {
         if (PACK) dst[hdr + i] = src[gg + i];
         else dst[gg + i] = src[hdr + i];
@@ -122,7 +122,9 @@ __global__ void k_pack_q4k(const uint8_t* __restrict__ src, uint8_t* __restrict_
     for (int jg = 0; jg < 4; ++jg)
         for (int h = 0; h < 2; ++h)
             for (int x = 0; x < 16; ++x) {
-                const size_t pg = gg + 16 + 32 * jg + 16 * h + x, pp = nib + 128 * h + 16 * ((b % 2) * 4 + jg) + x;
+                // the run's byte 128 h + 16 ((b % 2) 4 + jg) + x
+                const size_t pg = gg + 16 + 32 * jg + 16 * h + x,
+                             pp = (size_t) P.nib16(r, C, 16 * (b / 2) + 8 * h + (b % 2) * 4 + jg) + x;
                 if (PACK) dst[pp] = src[pg];
                 else dst[pg] = src[pp];
             }
@@ -138,15 +140,16 @@ __global__ void k_pack_q80(const uint8_t* __restrict__ src, uint8_t* __restrict_
     const int r = (int) ((k % per_mat) / nb), b = (int) (k % nb);
     const size_t mat_bytes = (size_t) R * nb * Q80_BYTES;
     const size_t gg = m * mat_bytes + ((size_t) r * nb + b) * Q80_BYTES;
-    const size_t qp = m * mat_bytes + (size_t) r * C + (size_t) (b / 16) * 512 + 16 * (b % 16);
-    const size_t dp = m * mat_bytes + (size_t) R * C + ((size_t) r * nb + b) * 2;
+    const Q80Planes P = q80_planes((const uint8_t*) nullptr + m * mat_bytes, R, C);
+    const size_t dp = (size_t) P.dof(r, C, b);
     for (int i = 0; i < 2; ++i) {
         if (PACK) dst[dp + i] = src[gg + i];
         else dst[gg + i] = src[dp + i];
     }
     for (int h = 0; h < 2; ++h)
         for (int x = 0; x < 16; ++x) {
-            const size_t pg = gg + 2 + 16 * h + x, pp = qp + 256 * h + x;
+            // the run's byte 256 h + 16 (b % 16) + x
+            const size_t pg = gg + 2 + 16 * h + x, pp = (size_t) P.q16(r, C, 32 * (b / 16) + 16 * h + b % 16) + x;
             if (PACK) dst[pp] = src[pg];
             else dst[pg] = src[pp];
         }
@@ -162,22 +165,23 @@ __global__ void k_deq_q4k(const uint8_t* __restrict__ src, void* __restrict__ ou
     const int64_t m = k / per_mat;
     const int r = (int) ((k % per_mat) / ns), s = (int) (k % ns), b = s / 8, j = s % 8, jg = j / 2, hi = j % 2;
     const Q4kPlanes P = q4k_planes(src + m * ((size_t) R * (C / 256) * Q4K_BYTES), R, C);
-    const uint4 h = *reinterpret_cast<const uint4*>(P.hdr_row(r, C) + 16 * b);
+    const uint4 h = *reinterpret_cast<const uint4*>(P.hdr16(r, C, b));
     const float d = h2f((uint16_t) (h.x & 0xffff)), dmin = h2f((uint16_t) (h.x >> 16));
     float sc, mm;
     q4k_scale_min(h, j, sc, mm);
-    const uint8_t* run = P.nib_row(r, C) + (size_t) (b / 2) * 256 + 16 * ((b % 2) * 4 + jg);
+    // the run's pieces 4 (b % 2) + jg (values 0-15) and 8 + 4 (b % 2) + jg (values 16-31)
+    const int p0 = 16 * (b / 2) + (b % 2) * 4 + jg;
     const size_t o = (size_t) m * R * C + (size_t) r * C + 32 * s;
     if (F16) {
         const __half d1 = __float2half_rn(d * sc), nm1 = __float2half_rn(-(dmin * mm));
         for (int l = 0; l < 32; ++l) {
-            const int q = (run[128 * (l / 16) + (l % 16)] >> (4 * hi)) & 0xF;
+            const int q = (P.nib16(r, C, p0 + 8 * (l / 16))[l % 16] >> (4 * hi)) & 0xF;
             ((__half*) out)[o + l] = __hfma(__int2half_rn(q), d1, nm1);
         }
     } else {
         const float d1 = d * sc, m1 = dmin * mm;
         for (int l = 0; l < 32; ++l) {
-            const int q = (run[128 * (l / 16) + (l % 16)] >> (4 * hi)) & 0xF;
+            const int q = (P.nib16(r, C, p0 + 8 * (l / 16))[l % 16] >> (4 * hi)) & 0xF;
             ((float*) out)[o + l] = d1 * (float) q - m1;
         }
     }
@@ -190,20 +194,21 @@ __global__ void k_deq_q80(const uint8_t* __restrict__ src, void* __restrict__ ou
     const int64_t m = k / per_mat;
     const int r = (int) ((k % per_mat) / nb), b = (int) (k % nb);
     const Q80Planes P = q80_planes(src + m * ((size_t) R * nb * Q80_BYTES), R, C);
-    const uint16_t dh = P.d[(size_t) r * nb + b];
-    const int8_t* q = (const int8_t*) P.q + (size_t) r * C + (size_t) (b / 16) * 512 + 16 * (b % 16);
+    const uint16_t dh = *P.dof(r, C, b);
+    const int p0 = 32 * (b / 16) + b % 16;   // the block's first half; the second 16 pieces on
     const size_t o = (size_t) m * R * C + (size_t) r * C + 32 * b;
     for (int l = 0; l < 32; ++l) {
-        const int v = q[256 * (l / 16) + (l % 16)];
+        const int v = (int8_t) P.q16(r, C, p0 + 16 * (l / 16))[l % 16];
         if (F16) ((__half*) out)[o + l] = __hmul(__int2half_rn(v), __ushort_as_half(dh));
         else ((float*) out)[o + l] = h2f(dh) * (float) v;
     }
 }
 
 inline unsigned blocks_for(int64_t n, int t) { return (unsigned) ((n + t - 1) / t); }
-void check_type_shape(uint32_t type, int cols) {
+void check_type_shape(uint32_t type, int rows, int cols) {
     require(type == SFNX_Q4_K || type == SFNX_Q8_0, "weight type must be Q4_K (12) or Q8_0 (8)");
     require(cols > 0 && cols % 512 == 0, "columns must be a positive multiple of 512");
+    require(rows >= 0 && rows % ROWTILE == 0, "rows must be a multiple of 32 (the store's row tile)");
 }
 
 }  // namespace
@@ -239,7 +244,7 @@ extern "C" int sfnx_quantize_weights(uint32_t type, const float* x, void* gguf, 
 
 extern "C" int sfnx_store_pack(uint32_t type, const void* gguf, void* planar, int64_t n_mat, int R, int C, void* st) {
     return guarded("sfnx_store_pack", [&] {
-        check_type_shape(type, C);
+        check_type_shape(type, R, C);
         require(gguf != planar, "packing is out of place");
         const int64_t n = n_mat * R * (type == SFNX_Q4_K ? C / 256 : C / 32);
         if (n <= 0) return;
@@ -252,7 +257,7 @@ extern "C" int sfnx_store_pack(uint32_t type, const void* gguf, void* planar, in
 
 extern "C" int sfnx_store_unpack(uint32_t type, const void* planar, void* gguf, int64_t n_mat, int R, int C, void* st) {
     return guarded("sfnx_store_unpack", [&] {
-        check_type_shape(type, C);
+        check_type_shape(type, R, C);
         require(gguf != planar, "unpacking is out of place");
         const int64_t n = n_mat * R * (type == SFNX_Q4_K ? C / 256 : C / 32);
         if (n <= 0) return;
@@ -265,7 +270,7 @@ extern "C" int sfnx_store_unpack(uint32_t type, const void* planar, void* gguf, 
 
 extern "C" int sfnx_dequantize(uint32_t type, const void* planar, float* y, int64_t n_mat, int R, int C, void* st) {
     return guarded("sfnx_dequantize", [&] {
-        check_type_shape(type, C);
+        check_type_shape(type, R, C);
         const int64_t n = n_mat * R * (C / 32);
         if (n <= 0) return;
         if (type == SFNX_Q4_K) k_deq_q4k<false><<<blocks_for(n, 256), 256, 0, stream_of(st)>>>((const uint8_t*) planar, y, n_mat, R, C);
@@ -275,7 +280,7 @@ extern "C" int sfnx_dequantize(uint32_t type, const void* planar, float* y, int6
 
 extern "C" int sfnx_dequantize_f16(uint32_t type, const void* planar, uint16_t* y, int64_t n_mat, int R, int C, void* st) {
     return guarded("sfnx_dequantize_f16", [&] {
-        check_type_shape(type, C);
+        check_type_shape(type, R, C);
         const int64_t n = n_mat * R * (C / 32);
         if (n <= 0) return;
         if (type == SFNX_Q4_K) k_deq_q4k<true><<<blocks_for(n, 256), 256, 0, stream_of(st)>>>((const uint8_t*) planar, y, n_mat, R, C);

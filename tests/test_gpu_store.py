@@ -31,7 +31,7 @@ def test_quantizer_bit_exact(wtype, rows, cols):
 
 @pytest.mark.parametrize("wtype", [orc.Q4_K, orc.Q8_0])
 def test_pack_round_trip_and_dequant(wtype):
-    n_mat, rows, cols = 3, 40, 1024
+    n_mat, rows, cols = 3, 96, 1024
     x = orc.synth(n_mat * rows * cols, 91, 0.02).reshape(n_mat * rows, cols)
     gg = orc.quantize(wtype, x)
     g = torch.from_numpy(gg).cuda()
