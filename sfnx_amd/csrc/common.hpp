@@ -156,22 +156,25 @@ __device__ __forceinline__ void warm_line(const void* p, void* junk) {
 __device__ __forceinline__ void warm_wait() { __builtin_amdgcn_s_waitcnt(0); }
 
 // ------------------------------------------------------------------------------------------------ planar store
-// Per matrix of R rows (a multiple of 32) x C columns, each plane of the store is tiled by 32 rows and cut into
-// 16-byte pieces: piece p of a row lies 512 bytes after piece p - 1, and piece p of the tile's 32 rows is one 512-byte
-// run.  Any read that gives each of 32 (or 8) consecutive rows' lanes the same piece is a whole number of 128-byte
-// lines: the matrix-core kernels' (a lane per row) and the dot kernels' (8 or 16 lanes per row) alike.
-constexpr int ROWTILE = 32;
-__host__ __device__ __forceinline__ size_t tiled16(int row, size_t row_bytes, int piece) {
-    return (size_t) (row / ROWTILE) * ROWTILE * row_bytes + (size_t) piece * (ROWTILE * 16) + (size_t) (row % ROWTILE) * 16;
+// Per matrix of R rows (a multiple of 32) x C columns, each plane of the store is tiled by RT rows and cut into 16-byte
+// pieces: piece p of a row lies 16 RT bytes after piece p - 1, and piece p of the tile's RT rows is one contiguous run.
+// Q4_K is tiled by 32 rows: a request that gives 32 consecutive rows' lanes the same piece (the matrix-core kernels, a
+// lane per row) or 8 consecutive rows' 8 lanes each 8 consecutive pieces (the dot kernels) is whole 128-byte lines.
+// Q8_0 is tiled by 4 rows, for its dot kernels' 16 lanes a row over 4 rows a wavefront (16 pieces x 4 rows, one
+// contiguous KB); its matrix-core requests are then 64-byte halves of lines, the other half the next step's.
+constexpr int ROWTILE = 32;   // rows in every type's tile count
+template <int RT> __host__ __device__ __forceinline__ size_t tiled16(int row, size_t row_bytes, int piece) {
+    return (size_t) (row / RT) * RT * row_bytes + (size_t) piece * (RT * 16) + (size_t) (row % RT) * 16;
 }
-constexpr int PIECE_STRIDE = ROWTILE * 16;   // bytes from one piece of a row to the next
+constexpr int Q4K_RT = 32, Q80_RT = 4;
+constexpr int PIECE_STRIDE = Q4K_RT * 16;   // Q4_K: bytes from one piece of a row to the next
 struct Q4kPlanes {
     const uint8_t* nib;   // R x C/2: a row's runs of 256 bytes (two super-blocks), 16-byte pieces in [half][group] order
     const uint8_t* hdr;   // R x C/256 x 16: a row's super-block headers, one piece each
     // piece p (bytes 16 p .. 16 p + 15) of row r's nibble bytes
-    __host__ __device__ __forceinline__ const uint8_t* nib16(int r, int C, int p) const { return nib + tiled16(r, C / 2, p); }
+    __host__ __device__ __forceinline__ const uint8_t* nib16(int r, int C, int p) const { return nib + tiled16<Q4K_RT>(r, C / 2, p); }
     // the 16-byte header of super-block b of row r
-    __host__ __device__ __forceinline__ const uint8_t* hdr16(int r, int C, int b) const { return hdr + tiled16(r, C / 16, b); }
+    __host__ __device__ __forceinline__ const uint8_t* hdr16(int r, int C, int b) const { return hdr + tiled16<Q4K_RT>(r, C / 16, b); }
 };
 __host__ __device__ __forceinline__ Q4kPlanes q4k_planes(const void* mat, int R, int C) {
     const uint8_t* p = (const uint8_t*) mat;
@@ -180,8 +183,8 @@ __host__ __device__ __forceinline__ Q4kPlanes q4k_planes(const void* mat, int R,
 struct Q80Planes {
     const uint8_t* q;     // R x C: a row's 512-byte runs (16 blocks), 16-byte pieces in [half][block] order
     const uint8_t* d;     // R x C/32 f16: a row's block scales, 8 a piece
-    __host__ __device__ __forceinline__ const uint8_t* q16(int r, int C, int p) const { return q + tiled16(r, C, p); }
-    __host__ __device__ __forceinline__ const uint8_t* d16(int r, int C, int p) const { return d + tiled16(r, C / 16, p); }
+    __host__ __device__ __forceinline__ const uint8_t* q16(int r, int C, int p) const { return q + tiled16<Q80_RT>(r, C, p); }
+    __host__ __device__ __forceinline__ const uint8_t* d16(int r, int C, int p) const { return d + tiled16<Q80_RT>(r, C / 16, p); }
     // the f16 scale of block b of row r
     __host__ __device__ __forceinline__ const uint16_t* dof(int r, int C, int b) const {
         return reinterpret_cast<const uint16_t*>(d16(r, C, b / 8) + 2 * (b % 8));

@@ -93,7 +93,7 @@ template <> struct Chunk<SFNX_Q8_0> {
 
 // Where chunk c (of the run's 8 / STEPS) of run r of the lane's row lies.
 struct ChunkAt {
-    const uint8_t* q;     // the first 16-byte piece (Q4_K: nibbles; Q8_0: first halves); the next one PIECE_STRIDE on
+    const uint8_t* q;     // the first 16-byte piece (Q4_K: nibbles; Q8_0: first halves); the next one a tile's pieces on
     const uint8_t* tail;  // Q4_K: the super-block header; Q8_0: the two f16 scales
 };
 __device__ __forceinline__ ChunkAt chunk_at(const Chunk<SFNX_Q4_K>*, const uint8_t* mat, int R, int C, int row, int r, int c, int h) {
@@ -108,8 +108,8 @@ __device__ __forceinline__ void load_piece(Chunk<SFNX_Q4_K>& w, const ChunkAt& a
     w.q[s] = *reinterpret_cast<const uint4*>(a.q + PIECE_STRIDE * s);
 }
 __device__ __forceinline__ void load_piece(Chunk<SFNX_Q8_0>& w, const ChunkAt& a, int s) {
-    w.qa[s] = *reinterpret_cast<const uint4*>(a.q + PIECE_STRIDE * s);
-    w.qb[s] = *reinterpret_cast<const uint4*>(a.q + PIECE_STRIDE * (16 + s));   // the blocks' second halves
+    w.qa[s] = *reinterpret_cast<const uint4*>(a.q + Q80_RT * 16 * s);
+    w.qb[s] = *reinterpret_cast<const uint4*>(a.q + Q80_RT * 16 * (16 + s));   // the blocks' second halves
 }
 __device__ __forceinline__ void load_tail(Chunk<SFNX_Q4_K>& w, const ChunkAt& a) { w.hdr = *reinterpret_cast<const uint4*>(a.tail); }
 __device__ __forceinline__ void load_tail(Chunk<SFNX_Q8_0>& w, const ChunkAt& a) { w.d = *reinterpret_cast<const uint32_t*>(a.tail); }
@@ -145,17 +145,18 @@ template <int TYPE> __device__ __forceinline__ int run_col(int j, int c, int h) 
 #define MM_SLOTS 2   // weight chunks a wavefront keeps in registers: the one being dotted and the ones in flight
 #endif
 constexpr int MM_RUN = 512, MM_XLD = MM_RUN + 8;   // columns a run; LDS row pitch (16 bytes past the run: rows shift banks)
-constexpr int MM_XROWS = 64 / MM_WAVES;             // activation rows a wavefront moves per run
 constexpr size_t MM_XBUF = 64 * MM_XLD;              // halves in one activation buffer
 
 // run r of the job's activation rows into an LDS buffer by asynchronous global -> LDS copies (no registers): wavefront w
-// moves rows w * 4 .. w * 4 + 3, a row of 512 halves a copy (64 lanes x 16 bytes); rows past n are left as they are
-// (they only feed output rows that are never stored)
+// of W moves rows w * 64 / W .. (w + 1) * 64 / W - 1, a row of 512 halves a copy (64 lanes x 16 bytes); rows past n are
+// left as they are (they only feed output rows that are never stored)
+template <int W>
 __device__ __forceinline__ void load_x_async(_Float16* buf, const _Float16* __restrict__ x, int ldx, const int* ys, int n,
                                              int r, int wave, int lane) {
+    constexpr int XR = 64 / W;
 #pragma unroll
-    for (int i = 0; i < MM_XROWS; ++i) {
-        const int m = wave * MM_XROWS + i;
+    for (int i = 0; i < XR; ++i) {
+        const int m = wave * XR + i;
         if (m < n)
             __builtin_amdgcn_global_load_lds(x + (size_t) ys[m] * ldx + MM_RUN * r + 8 * lane,
                                              (__attribute__((address_space(3))) void*) (buf + (size_t) m * MM_XLD), 16, 0, 0);
@@ -196,7 +197,7 @@ __device__ __forceinline__ void mma_chunk(const Chunk<TYPE>& w, int cj, const _F
 // sit in one of two LDS buffers; run r + 1's are requested (global -> LDS, no registers) when run r starts, so each
 // run start waits only for them, not for the weight chunks requested after them (CPR chunks of LOADS requests each).
 // tile_done(it, acc) takes a tile's accumulators (and they are cleared for the next tile); the last tile's stay in acc.
-template <int TYPE, int NT, typename RowOf, typename TileDone>
+template <int TYPE, int NT, int W, typename RowOf, typename TileDone>
 __device__ __forceinline__ void chunk_walk(const uint8_t* mat, int R, int C, int tiles, RowOf row_of, int wave, int lane,
                                            const int* ys, int n, const _Float16* __restrict__ x, _Float16* xs,
                                            float16v (&acc)[NT], TileDone tile_done) {
@@ -206,7 +207,7 @@ __device__ __forceinline__ void chunk_walk(const uint8_t* mat, int R, int C, int
         const int it = k / per_tile, rc = k % per_tile;
         return chunk_at((const Chunk<TYPE>*) nullptr, mat, R, C, row_of(it), rc / CPR, rc % CPR, h);
     };
-    load_x_async(xs, x, C, ys, n, 0, wave, lane);
+    load_x_async<W>(xs, x, C, ys, n, 0, wave, lane);
     Chunk<TYPE> w[MM_SLOTS];
 #pragma unroll
     for (int i = 0; i < MM_SLOTS; ++i)
@@ -229,7 +230,7 @@ __device__ __forceinline__ void chunk_walk(const uint8_t* mat, int R, int C, int
                 else wait_vmem();
             }
             __syncthreads();                  // every wavefront's rows landed; every wavefront is past the previous run
-            if (nr > 1 && k + per_tile / nr < NK) load_x_async(xs + (size_t) ((rg + 1) & 1) * MM_XBUF, x, C, ys, n, (r + 1) % nr, wave, lane);
+            if (nr > 1 && k + per_tile / nr < NK) load_x_async<W>(xs + (size_t) ((rg + 1) & 1) * MM_XBUF, x, C, ys, n, (r + 1) % nr, wave, lane);
         }
         mma_chunk<TYPE, NT>(w, cj, xb, nn, h, acc);
         if (rc == per_tile - 1 && k + 1 < NK) {
@@ -253,13 +254,13 @@ __device__ __forceinline__ void chunk_walk(const uint8_t* mat, int R, int C, int
 // D[token][row] of a tile: lane (nn, h), value q at token 8 (q / 4) + 4 h + q % 4 of 32-token tile t
 __device__ __forceinline__ int acc_token(int t, int q, int h) { return 32 * t + 8 * (q / 4) + 4 * h + q % 4; }
 
-// rows: ys[0..n) (activation rows) and outs[0..n) (output rows), n <= 32 NT; the block's rows are G tiles of 512
-template <int TYPE, int NT>
+// rows: ys[0..n) (activation rows) and outs[0..n) (output rows), n <= 32 NT; the block's rows are G tiles of 32 W
+template <int TYPE, int NT, int W>
 __device__ __forceinline__ void mma_job(const uint8_t* mat, int R, int C, int row0, int G, int wave, int lane,
                                         const int* ys, const int* outs, int n, const _Float16* __restrict__ x,
                                         _Float16* xs, float* __restrict__ out) {
     const int h = lane / 32, nn = lane % 32;
-    auto row_of = [&](int it) { return row0 + it * MM_BM + wave * 32 + nn; };
+    auto row_of = [&](int it) { return row0 + it * 32 * W + wave * 32 + nn; };
     auto store = [&](int it, const float16v (&acc)[NT]) {
         const int row = row_of(it);
 #pragma unroll
@@ -271,7 +272,7 @@ __device__ __forceinline__ void mma_job(const uint8_t* mat, int R, int C, int ro
             }
     };
     float16v acc[NT];
-    chunk_walk<TYPE, NT>(mat, R, C, G, row_of, wave, lane, ys, n, x, xs, acc, store);
+    chunk_walk<TYPE, NT, W>(mat, R, C, G, row_of, wave, lane, ys, n, x, xs, acc, store);
     store(G - 1, acc);
 }
 
@@ -287,7 +288,7 @@ __device__ __forceinline__ void mma_gu_job(const uint8_t* mat, int ff, int C, in
     const int h = lane / 32, nn = lane % 32, R = 2 * ff, up = wave >= MM_WAVES / 2, fl = 32 * (wave % (MM_WAVES / 2)) + nn;
     const int row = (up ? ff : 0) + f0 + fl;
     float16v res[NT];
-    chunk_walk<TYPE, NT>(mat, R, C, 1, [&](int) { return row; }, wave, lane, jb.y, jb.n, x, xs, res,
+    chunk_walk<TYPE, NT, MM_WAVES>(mat, R, C, 1, [&](int) { return row; }, wave, lane, jb.y, jb.n, x, xs, res,
                          [](int, const float16v (&)[NT]) {});
     if (gu) {
 #pragma unroll
@@ -357,12 +358,16 @@ __global__ void __launch_bounds__(MM_THREADS) k_moe_mma_gu(const uint8_t* __rest
     else mma_gu_job<TYPE, 1>(mat, ff, C, sl * MM_FF, wave, lane, jb, x, xs, gu, h16);
 }
 
+// The other projections (down, and gate|up shapes the paired kernel does not take): blocks of DN_WAVES wavefronts,
+// two a compute unit when one run covers the input (one activation buffer), so one block's start (its activations
+// and first weights in flight) overlaps the other's work.
+constexpr int DN_WAVES = 8, DN_THREADS = DN_WAVES * WAVE, DN_BM = 32 * DN_WAVES;
 template <int TYPE>
-__global__ void __launch_bounds__(MM_THREADS) k_moe_mma(const uint8_t* __restrict__ A, size_t sa, int R, int C, int G,
+__global__ void __launch_bounds__(DN_THREADS, 4) k_moe_mma(const uint8_t* __restrict__ A, size_t sa, int R, int C, int G,
                                                        const sfnx_bigjob* __restrict__ jobs, const int* __restrict__ njobs,
                                                        const _Float16* __restrict__ x, float* __restrict__ out) {
     int sl, ji;
-    xcd_job(blockIdx.x, R / (G * MM_BM), sl, ji);
+    xcd_job(blockIdx.x, R / (G * DN_BM), sl, ji);
     if (ji >= *njobs) return;
     __shared__ sfnx_bigjob jb;
     extern __shared__ __align__(16) unsigned char xs_raw[];
@@ -371,9 +376,9 @@ __global__ void __launch_bounds__(MM_THREADS) k_moe_mma(const uint8_t* __restric
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
     const uint8_t* mat = A + (size_t) jb.w * sa;
     _Float16* xs = reinterpret_cast<_Float16*>(xs_raw);
-    const int row0 = sl * G * MM_BM;
-    if (jb.n > 32) mma_job<TYPE, 2>(mat, R, C, row0, G, wave, lane, jb.y, jb.out, jb.n, x, xs, out);
-    else mma_job<TYPE, 1>(mat, R, C, row0, G, wave, lane, jb.y, jb.out, jb.n, x, xs, out);
+    const int row0 = sl * G * DN_BM;
+    if (jb.n > 32) mma_job<TYPE, 2, DN_WAVES>(mat, R, C, row0, G, wave, lane, jb.y, jb.out, jb.n, x, xs, out);
+    else mma_job<TYPE, 1, DN_WAVES>(mat, R, C, row0, G, wave, lane, jb.y, jb.out, jb.n, x, xs, out);
 }
 
 // k_swiglu_h16 (src/moe_mma.cuh:382-388): h16 = f16(silu(gate) * up) of P rows [gate (ff) | up (ff)]
@@ -396,19 +401,20 @@ void moe_mma(uint32_t type, const void* A, size_t sa, int n_in, int n_out, const
              int njobs_cap, const void* x16, float* out, void* st) {
     require(type == SFNX_Q4_K || type == SFNX_Q8_0, "expert type must be Q4_K (12) or Q8_0 (8)");
     require(n_in > 0 && n_in % 512 == 0, "expert input width must be a multiple of 512");
-    require(n_out > 0 && n_out % MM_BM == 0, "expert rows must be a multiple of 512");
-    require((n_out / MM_BM) % std::max(1, (n_out / MM_BM) / 2) == 0, "row groups must split evenly");
+    require(n_out > 0 && n_out % DN_BM == 0, "expert rows must be a multiple of 256");
+    require((n_out / DN_BM) % std::max(1, (n_out / DN_BM) / 2) == 0, "row groups must split evenly");
     require(sa >= row_bytes(type, n_in) * (size_t) n_out, "expert stride smaller than a matrix");
     require(njobs_cap >= 0 && njobs_cap <= (1 << 20), "njobs_cap out of range");
     if (njobs_cap == 0) return;
-    // tiles of 512 rows: two blocks a job (half the tiles each), for more blocks than compute units
-    const int groups = n_out / MM_BM, G = std::max(1, groups / 2);
+    // tiles of 256 rows: two blocks a job (half the tiles each), for more blocks than compute units
+    const int groups = n_out / DN_BM, G = std::max(1, groups / 2);
     const dim3 grid(xcd_grid(groups / G, njobs_cap));
+    const size_t lds = (n_in == MM_RUN ? 1 : 2) * MM_XBUF * sizeof(_Float16);
     hipStream_t s = stream_of(st);
     if (type == SFNX_Q4_K)
-        k_moe_mma<SFNX_Q4_K><<<grid, MM_THREADS, MM_LDS, s>>>((const uint8_t*) A, sa, n_out, n_in, G, jobs, njobs, (const _Float16*) x16, out);
+        k_moe_mma<SFNX_Q4_K><<<grid, DN_THREADS, lds, s>>>((const uint8_t*) A, sa, n_out, n_in, G, jobs, njobs, (const _Float16*) x16, out);
     else
-        k_moe_mma<SFNX_Q8_0><<<grid, MM_THREADS, MM_LDS, s>>>((const uint8_t*) A, sa, n_out, n_in, G, jobs, njobs, (const _Float16*) x16, out);
+        k_moe_mma<SFNX_Q8_0><<<grid, DN_THREADS, lds, s>>>((const uint8_t*) A, sa, n_out, n_in, G, jobs, njobs, (const _Float16*) x16, out);
 }
 
 void moe_mma_gu(uint32_t type, const void* A, size_t sa, int n_in, int ff, const sfnx_bigjob* jobs, const int* njobs,
