@@ -12,11 +12,14 @@
  * Weight matrices are the "planar" store (sfnx_store_pack): per matrix of R rows x C columns,
  *   Q4_K: a nibble plane of R x C/2 bytes, then a header plane of R x C/256 x 16 bytes (f16 d, f16 dmin, 12 scale
  *         bytes, byte-identical to the GGUF super-block's first 16 bytes).  Within each 256-byte run of a row's nibble
- *         plane (the quants of two super-blocks), the 16-byte halves are ordered [half][group of 64 values], so a
- *         wavefront's 16-byte loads cover whole 128-byte lines.
+ *         plane (the quants of two super-blocks), the 16-byte pieces are ordered [half][group of 64 values].
+ *   Q5_K: as Q4_K, with a fifth-bit plane of R x C/8 bytes (each super-block's 32 qh bytes) between the nibble and
+ *         header planes.
  *   Q8_0: an int8 plane of R x C bytes (16-byte halves of each 512-byte run ordered [half][block]), then an f16 scale
  *         plane of R x C/32.
- * The planar matrix has exactly the GGUF matrix's size; experts sit at base + e * stride.  C % 512 == 0.
+ * Every plane is tiled by rows (32 for the K-quants, 4 for Q8_0): piece p of a row lies one tile's pieces after piece
+ * p - 1, so a wavefront's 16-byte loads over a tile's rows cover whole 128-byte lines.  The planar matrix has exactly
+ * the GGUF matrix's size; experts sit at base + e * stride.  C % 512 == 0, R % 32 == 0.
  */
 #ifndef SFNX_MOE_H
 #define SFNX_MOE_H
@@ -31,7 +34,7 @@ extern "C" {
 #define SFNX_MAXT 16     /* rows of a decode window (src/model.hpp:48 MAXT) */
 #define SFNX_PF_JOB 64   /* rows of a prompt-path job (src/kernels.hpp:26 PF_JOB) */
 
-enum { SFNX_Q8_0 = 8, SFNX_Q4_K = 12 }; /* GgmlType ids, src/gguf.hpp:22-25 */
+enum { SFNX_Q8_0 = 8, SFNX_Q4_K = 12, SFNX_Q5_K = 13 }; /* GgmlType ids, src/gguf.hpp:22-25 (Q5_K: ggml's 13) */
 
 /* src/kernels.hpp:18-23: one expert's matrix applied to up to SFNX_MAXT activation rows */
 typedef struct sfnx_job {
@@ -195,7 +198,7 @@ int sfnx_gguf_str(const sfnx_gguf* g, const char* key, const char** v);         
  * 766-809): blk.<layer>.ffn_{gate,up}_exps rows ff0..ff1 stacked [gate ; up] per expert into gu (planar, gu_stride a
  * matrix), ffn_down_exps columns ff0..ff1 into dn (dn_stride a matrix), the shared expert ffn_*_shexp (when present,
  * of the same type and FF) as expert E, and the router W = [ffn_gate_inp rows ; ffn_gate_inp_shexp] (f32 [E+1][H]).
- * Q4_K or Q8_0 experts; ff0 on a block (256 / 32 columns), ff1 - ff0 and H multiples of 512.  info (may be null)
+ * Q4_K, Q5_K or Q8_0 experts; ff0 on a block (256 / 32 columns), ff1 - ff0 and H multiples of 512.  info (may be null)
  * receives type, H, E, ff1 - ff0
  * and shared.  A loader, not a hot-path call: it allocates a staging buffer and synchronises the stream. */
 int sfnx_gguf_moe_layer(const sfnx_gguf* g, int layer, int ff0, int ff1, void* gu, size_t gu_stride, void* dn,

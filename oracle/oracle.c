@@ -141,7 +141,11 @@ void orc_q4k_scale_min(const uint8_t* s, int j, int* sc, int* m) {
 
 static inline int clampi(int v, int lo, int hi) { return v < lo ? lo : v > hi ? hi : v; }
 
-static void quant_q4k_block(const float* x, uint8_t* b) {
+/* the K-quant super-block of 256 values: Q4_K (q5 = 0: header, qs[128]) or Q5_K (q5 = 1: header, qh[32], qs[128]);
+ * levels 15 or 31 */
+static void quant_kq_block(const float* x, uint8_t* b, int q5) {
+    const float levels = q5 ? 31.0f : 15.0f;
+    const int qmax = q5 ? 31 : 15;
     float scale[8], mn8[8], max_scale = 0.f, max_min = 0.f;
     for (int j = 0; j < 8; ++j) {
         float mn = x[32 * j], mx = x[32 * j];
@@ -150,7 +154,7 @@ static void quant_q4k_block(const float* x, uint8_t* b) {
             if (x[32 * j + l] > mx) mx = x[32 * j + l];
         }
         if (mn > 0.f) mn = 0.f;
-        scale[j] = (mx - mn) / 15.0f;
+        scale[j] = (mx - mn) / levels;
         mn8[j] = mn < 0.f ? -mn : 0.f;
         if (scale[j] > max_scale) max_scale = scale[j];
         if (mn8[j] > max_min) max_min = mn8[j];
@@ -170,13 +174,16 @@ static void quant_q4k_block(const float* x, uint8_t* b) {
         s[j + 4] = (uint8_t) ((m[j] & 63) | ((m[j + 4] >> 4) << 6));
         s[j + 8] = (uint8_t) ((sc[j + 4] & 0xF) | ((m[j + 4] & 0xF) << 4));
     }
-    uint8_t* qs = b + 16;
+    uint8_t* qh = b + 16;
+    uint8_t* qs = b + (q5 ? 48 : 16);
     memset(qs, 0, 128);
+    if (q5) memset(qh, 0, 32);
     for (int j = 0; j < 8; ++j) {
         const float dl = df * (float) sc[j], ml = mf * (float) m[j];
         for (int l = 0; l < 32; ++l) {
-            const int q = dl > 0.f ? clampi((int) roundf((x[32 * j + l] + ml) / dl), 0, 15) : 0;
-            qs[32 * (j / 2) + l] |= (uint8_t) (q << (4 * (j % 2)));
+            const int q = dl > 0.f ? clampi((int) roundf((x[32 * j + l] + ml) / dl), 0, qmax) : 0;
+            qs[32 * (j / 2) + l] |= (uint8_t) ((q & 15) << (4 * (j % 2)));
+            if (q5) qh[l] |= (uint8_t) ((q >> 4) << j);
         }
     }
 }
@@ -186,7 +193,15 @@ void orc_quantize_q4_k(const float* x, void* dst, int64_t rows, int cols) {
 #pragma omp parallel for schedule(static)
     for (int64_t r = 0; r < rows; ++r)
         for (int b = 0; b < nb; ++b)
-            quant_q4k_block(x + r * cols + 256 * b, (uint8_t*) dst + (r * nb + b) * ORC_Q4K_BYTES);
+            quant_kq_block(x + r * cols + 256 * b, (uint8_t*) dst + (r * nb + b) * ORC_Q4K_BYTES, 0);
+}
+
+void orc_quantize_q5_k(const float* x, void* dst, int64_t rows, int cols) {
+    const int nb = cols / 256;
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; ++r)
+        for (int b = 0; b < nb; ++b)
+            quant_kq_block(x + r * cols + 256 * b, (uint8_t*) dst + (r * nb + b) * ORC_Q5K_BYTES, 1);
 }
 
 void orc_quantize_q8_0(const float* x, void* dst, int64_t rows, int cols) {
@@ -208,10 +223,18 @@ void orc_quantize_q8_0(const float* x, void* dst, int64_t rows, int cols) {
     }
 }
 
-void orc_dequant_q4_k(const void* src, float* y, int64_t rows, int cols) {
+/* value l of sub-block j of a K-quant super-block (Q5_K: the fifth bit from qh[l] bit j) */
+static inline int kq_value(const uint8_t* p, int q5, int j, int l) {
+    const uint8_t* qs = p + (q5 ? 48 : 16);
+    const int nib = (qs[32 * (j / 2) + l] >> (4 * (j % 2))) & 0xF;
+    return q5 ? nib | (((p[16 + l] >> j) & 1) << 4) : nib;
+}
+
+static void dequant_kq(const void* src, float* y, int64_t rows, int cols, int q5) {
     const int64_t nblk = rows * (cols / 256);
+    const size_t bb = q5 ? ORC_Q5K_BYTES : ORC_Q4K_BYTES;
     for (int64_t k = 0; k < nblk; ++k) {
-        const uint8_t* p = (const uint8_t*) src + k * ORC_Q4K_BYTES;
+        const uint8_t* p = (const uint8_t*) src + k * bb;
         uint16_t dh, mh;
         memcpy(&dh, p, 2);
         memcpy(&mh, p + 2, 2);
@@ -220,16 +243,16 @@ void orc_dequant_q4_k(const void* src, float* y, int64_t rows, int cols) {
             int sc, m;
             orc_q4k_scale_min(p + 4, j, &sc, &m);
             const float d1 = d * (float) sc, m1 = dmin * (float) m;
-            const uint8_t* q = p + 16 + 32 * (j / 2);
-            for (int l = 0; l < 32; ++l) y[256 * k + 32 * j + l] = d1 * (float) ((q[l] >> (4 * (j % 2))) & 0xF) - m1;
+            for (int l = 0; l < 32; ++l) y[256 * k + 32 * j + l] = d1 * (float) kq_value(p, q5, j, l) - m1;
         }
     }
 }
 
-void orc_dequant_q4_k_f16(const void* src, uint16_t* y, int64_t rows, int cols) {
+static void dequant_kq_f16(const void* src, uint16_t* y, int64_t rows, int cols, int q5) {
     const int64_t nblk = rows * (cols / 256);
+    const size_t bb = q5 ? ORC_Q5K_BYTES : ORC_Q4K_BYTES;
     for (int64_t k = 0; k < nblk; ++k) {
-        const uint8_t* p = (const uint8_t*) src + k * ORC_Q4K_BYTES;
+        const uint8_t* p = (const uint8_t*) src + k * bb;
         uint16_t dh, mh;
         memcpy(&dh, p, 2);
         memcpy(&mh, p + 2, 2);
@@ -238,14 +261,18 @@ void orc_dequant_q4_k_f16(const void* src, uint16_t* y, int64_t rows, int cols) 
             int sc, m;
             orc_q4k_scale_min(p + 4, j, &sc, &m);
             const uint16_t d1 = orc_f32_to_f16(d * (float) sc), nm1 = orc_f32_to_f16(-(dmin * (float) m));
-            const uint8_t* q = p + 16 + 32 * (j / 2);
             for (int l = 0; l < 32; ++l) {
-                const uint16_t qh = orc_f32_to_f16((float) ((q[l] >> (4 * (j % 2))) & 0xF));
+                const uint16_t qh = orc_f32_to_f16((float) kq_value(p, q5, j, l));
                 y[256 * k + 32 * j + l] = orc_f16_fma(qh, d1, nm1);
             }
         }
     }
 }
+
+void orc_dequant_q4_k(const void* src, float* y, int64_t rows, int cols) { dequant_kq(src, y, rows, cols, 0); }
+void orc_dequant_q4_k_f16(const void* src, uint16_t* y, int64_t rows, int cols) { dequant_kq_f16(src, y, rows, cols, 0); }
+void orc_dequant_q5_k(const void* src, float* y, int64_t rows, int cols) { dequant_kq(src, y, rows, cols, 1); }
+void orc_dequant_q5_k_f16(const void* src, uint16_t* y, int64_t rows, int cols) { dequant_kq_f16(src, y, rows, cols, 1); }
 
 void orc_dequant_q8_0(const void* src, float* y, int64_t rows, int cols) {
     const int64_t nblk = rows * (cols / 32);
@@ -434,7 +461,9 @@ int orc_jobs_prefill(const int* topi, int C, int K, int E, int shared, int* cnt,
 }
 
 /* ------------------------------------------------------------------------------------------------ expert dots */
-static float q4k_group_term(const uint8_t* blk, int jg, const uint8_t* ya, const uint8_t* yb) {
+/* group jg (sub-blocks 2 jg, 2 jg + 1) of a K-quant super-block against those two q8_1 blocks, src/moe_q4k.cuh:44-73
+ * (Q5_K: the same combine on 5-bit values) */
+static float kq_group_term(const uint8_t* blk, int q5, int jg, const uint8_t* ya, const uint8_t* yb) {
     uint16_t dh, mh, d8a, d8b;
     memcpy(&dh, blk, 2);
     memcpy(&mh, blk + 2, 2);
@@ -445,12 +474,11 @@ static float q4k_group_term(const uint8_t* blk, int jg, const uint8_t* ya, const
     orc_q4k_scale_min(blk + 4, 2 * jg, &sc0i, &m0i);
     orc_q4k_scale_min(blk + 4, 2 * jg + 1, &sc1i, &m1i);
     const float sc0 = (float) sc0i, m0 = (float) m0i, sc1 = (float) sc1i, m1 = (float) m1i;
-    const uint8_t* q = blk + 16 + 32 * jg;
     int dl = 0, dhi = 0, sl = 0, sh = 0;
     for (int l = 0; l < 32; ++l) {
         const int al = (int8_t) ya[4 + l], ah = (int8_t) yb[4 + l];
-        dl += (q[l] & 15) * al;
-        dhi += (q[l] >> 4) * ah;
+        dl += kq_value(blk, q5, 2 * jg, l) * al;
+        dhi += kq_value(blk, q5, 2 * jg + 1, l) * ah;
         sl += al;
         sh += ah;
     }
@@ -459,20 +487,24 @@ static float q4k_group_term(const uint8_t* blk, int jg, const uint8_t* ya, const
            dmin * (d8l * (m0 * (float) sl) + d8h * (m1 * (float) sh));
 }
 
-float orc_dot_q4_k(const uint8_t* wrow, const uint8_t* yq, int K) {
+/* 8 lanes, lane l8 the groups l8 + 8 i in order, then the xor butterfly (src/moe_q4k.cuh:30-86, src/moe.cuh:224-235) */
+static float dot_kq(const uint8_t* wrow, const uint8_t* yq, int K, int q5) {
     const int gpl = K / 64 / 8;
+    const size_t bb = q5 ? ORC_Q5K_BYTES : ORC_Q4K_BYTES;
     float lane[8];
     for (int l8 = 0; l8 < 8; ++l8) {
         float tmp = 0.f;
         for (int i = 0; i < gpl; ++i) {
             const int g = l8 + 8 * i, b = g >> 2, jg = g & 3;
             const uint8_t* ya = yq + (size_t) (b * 8 + jg * 2) * ORC_Q81_BYTES;
-            tmp += q4k_group_term(wrow + (size_t) b * ORC_Q4K_BYTES, jg, ya, ya + ORC_Q81_BYTES);
+            tmp += kq_group_term(wrow + (size_t) b * bb, q5, jg, ya, ya + ORC_Q81_BYTES);
         }
         lane[l8] = tmp;
     }
     return butterfly_sum(lane, 8);
 }
+float orc_dot_q4_k(const uint8_t* wrow, const uint8_t* yq, int K) { return dot_kq(wrow, yq, K, 0); }
+float orc_dot_q5_k(const uint8_t* wrow, const uint8_t* yq, int K) { return dot_kq(wrow, yq, K, 1); }
 
 float orc_dot_q8_0(const uint8_t* wrow, const uint8_t* yq, int K) {
     const int nb = K / 32;
@@ -495,11 +527,13 @@ float orc_dot_q8_0(const uint8_t* wrow, const uint8_t* yq, int K) {
 }
 
 float orc_dot(int type, const uint8_t* wrow, const uint8_t* yq, int K) {
-    return type == ORC_Q4_K ? orc_dot_q4_k(wrow, yq, K) : orc_dot_q8_0(wrow, yq, K);
+    return type == ORC_Q4_K ? orc_dot_q4_k(wrow, yq, K) : type == ORC_Q5_K ? orc_dot_q5_k(wrow, yq, K) : orc_dot_q8_0(wrow, yq, K);
 }
 
 static size_t row_bytes(int type, int cols) {
-    return type == ORC_Q4_K ? (size_t) cols / 256 * ORC_Q4K_BYTES : (size_t) cols / 32 * ORC_Q80_BYTES;
+    return type == ORC_Q4_K ? (size_t) cols / 256 * ORC_Q4K_BYTES
+           : type == ORC_Q5_K ? (size_t) cols / 256 * ORC_Q5K_BYTES
+                              : (size_t) cols / 32 * ORC_Q80_BYTES;
 }
 
 /* ------------------------------------------------------------------------------------------------ the layer */
@@ -567,6 +601,7 @@ void orc_mma_matvec(const uint8_t* w, int type, int n_in, int n_out, const uint1
     const size_t rb = row_bytes(type, n_in);
     for (int r = 0; r < n_out; ++r) {
         if (type == ORC_Q4_K) orc_dequant_q4_k_f16(w + (size_t) r * rb, row, 1, n_in);
+        else if (type == ORC_Q5_K) orc_dequant_q5_k_f16(w + (size_t) r * rb, row, 1, n_in);
         else orc_dequant_q8_0_f16(w + (size_t) r * rb, row, 1, n_in);
         double s = 0.0;
         for (int k = 0; k < n_in; ++k) s += (double) orc_f16_to_f32(row[k]) * (double) orc_f16_to_f32(x16[k]);

@@ -22,9 +22,10 @@
 extern "C" {
 #endif
 
-enum { ORC_Q8_0 = 8, ORC_Q4_K = 12 };   /* GgmlType ids, src/gguf.hpp:22-25 */
+enum { ORC_Q8_0 = 8, ORC_Q4_K = 12, ORC_Q5_K = 13 };   /* GgmlType ids, src/gguf.hpp:22-25; Q5_K is ggml's 13 */
 #define ORC_QK_K 256
 #define ORC_Q4K_BYTES 144
+#define ORC_Q5K_BYTES 176
 #define ORC_Q80_BYTES 34
 #define ORC_Q81_BYTES 36
 #define ORC_MAXT 16
@@ -51,6 +52,12 @@ void orc_synth_normal(float* out, size_t n, uint64_t seed, uint64_t offset, floa
 void orc_quantize_q4_k(const float* x, void* dst, int64_t rows, int cols);
 /* tools/mtp_experts.py:44-55: d = amax / 127, q = round-half-away(x * (1 / d)), f16 d */
 void orc_quantize_q8_0(const float* x, void* dst, int64_t rows, int cols);
+/* Q5_K (ggml block_q5_K, 176 bytes: f16 d, f16 dmin, 12 scale bytes, qh[32], qs[128]; value l of sub-block j is
+ * (qs[32 (j / 2) + l] >> 4 (j % 2)) & 15 | ((qh[l] >> j) & 1) << 4, src/moe_mma.cuh:84-92,123-136).  The library's
+ * quantizer as for Q4_K with 31 levels: scale = (max - min') / 31, q clamped to 0..31. */
+void orc_quantize_q5_k(const float* x, void* dst, int64_t rows, int cols);
+void orc_dequant_q5_k(const void* src, float* y, int64_t rows, int cols);
+void orc_dequant_q5_k_f16(const void* src, uint16_t* y, int64_t rows, int cols);
 
 /* get_scale_min_k4: src/moe_q4k.cuh:15-23, tools/moe_mma_bench.cu:44-52 */
 void orc_q4k_scale_min(const uint8_t* scales12, int j, int* sc, int* m);
@@ -93,6 +100,9 @@ float orc_dot_q4_k(const uint8_t* wrow, const uint8_t* yq, int K);
 /* Q8_0 row . q8_1 row: per 32-block (d_w d_a) * sum q_w q_a (ggml vec_dot_q8_0_q8_1's closed form); 16 lanes a row,
  * lane l the blocks l, l + 16, ... in order, then xor 8, 4, 2, 1. */
 float orc_dot_q8_0(const uint8_t* wrow, const uint8_t* yq, int K);
+/* Q5_K x q8_1: the Q4_K lane order and combine on 5-bit values (the reference's Q5_K decode dot is ggml's
+ * vec_dot_q5_K_q8_1, not vendored: its order is parity unpinned; this form is pinned by float64 products) */
+float orc_dot_q5_k(const uint8_t* wrow, const uint8_t* yq, int K);
 float orc_dot(int type, const uint8_t* wrow, const uint8_t* yq, int K);
 
 /* k_moe_h, src/moe.cuh:284-295: h = silu(gate) * up of one [gate (ff) | up (ff)] row, as q8_1 */

@@ -14,8 +14,8 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "_build" / "liborc.so"
 
-Q8_0, Q4_K = 8, 12
-Q4K_BYTES, Q80_BYTES, Q81_BYTES = 144, 34, 36
+Q8_0, Q4_K, Q5_K = 8, 12, 13
+Q4K_BYTES, Q5K_BYTES, Q80_BYTES, Q81_BYTES = 144, 176, 34, 36
 MAXT, PF_JOB = 16, 64
 
 JOB_DTYPE = np.dtype([("w", "<i4"), ("n", "<i4"), ("y", "<i4", MAXT), ("out", "<i4", MAXT)])
@@ -56,6 +56,10 @@ def lib() -> C.CDLL:
             "orc_synth_normal": (None, [vp, sz, C.c_uint64, C.c_uint64, f32]),
             "orc_quantize_q4_k": (None, [vp, vp, i64, i32]),
             "orc_quantize_q8_0": (None, [vp, vp, i64, i32]),
+            "orc_quantize_q5_k": (None, [vp, vp, i64, i32]),
+            "orc_dequant_q5_k": (None, [vp, vp, i64, i32]),
+            "orc_dequant_q5_k_f16": (None, [vp, vp, i64, i32]),
+            "orc_dot_q5_k": (f32, [vp, vp, i32]),
             "orc_q4k_scale_min": (None, [vp, i32, vp, vp]),
             "orc_dequant_q4_k": (None, [vp, vp, i64, i32]),
             "orc_dequant_q4_k_f16": (None, [vp, vp, i64, i32]),
@@ -90,7 +94,11 @@ def _p(a: np.ndarray | None):
 
 
 def row_bytes(t: int, cols: int) -> int:
-    return cols // 256 * Q4K_BYTES if t == Q4_K else cols // 32 * Q80_BYTES
+    return {Q4_K: cols // 256 * Q4K_BYTES, Q5_K: cols // 256 * Q5K_BYTES}.get(t, cols // 32 * Q80_BYTES)
+
+
+def _by_type(t: int, q4k: str, q5k: str, q80: str):
+    return getattr(lib(), {Q4_K: q4k, Q5_K: q5k}.get(t, q80))
 
 
 def f16_to_f32(h: int) -> float:
@@ -111,19 +119,19 @@ def quantize(t: int, x: np.ndarray) -> np.ndarray:
     rows, cols = x.shape
     out = np.empty(rows * row_bytes(t, cols), np.uint8)
     x = np.ascontiguousarray(x, np.float32)
-    (lib().orc_quantize_q4_k if t == Q4_K else lib().orc_quantize_q8_0)(_p(x), _p(out), rows, cols)
+    _by_type(t, 'orc_quantize_q4_k', 'orc_quantize_q5_k', 'orc_quantize_q8_0')(_p(x), _p(out), rows, cols)
     return out
 
 
 def dequant(t: int, blocks: np.ndarray, rows: int, cols: int) -> np.ndarray:
     out = np.empty((rows, cols), np.float32)
-    (lib().orc_dequant_q4_k if t == Q4_K else lib().orc_dequant_q8_0)(_p(blocks), _p(out), rows, cols)
+    _by_type(t, 'orc_dequant_q4_k', 'orc_dequant_q5_k', 'orc_dequant_q8_0')(_p(blocks), _p(out), rows, cols)
     return out
 
 
 def dequant_f16(t: int, blocks: np.ndarray, rows: int, cols: int) -> np.ndarray:
     out = np.empty((rows, cols), np.uint16)
-    (lib().orc_dequant_q4_k_f16 if t == Q4_K else lib().orc_dequant_q8_0_f16)(_p(blocks), _p(out), rows, cols)
+    _by_type(t, 'orc_dequant_q4_k_f16', 'orc_dequant_q5_k_f16', 'orc_dequant_q8_0_f16')(_p(blocks), _p(out), rows, cols)
     return out
 
 
@@ -172,7 +180,7 @@ def jobs_prefill(topi: np.ndarray, K: int, E: int, shared: bool):
 
 
 def dot(t: int, wrow: np.ndarray, yq: np.ndarray, K: int) -> float:
-    f = lib().orc_dot_q4_k if t == Q4_K else lib().orc_dot_q8_0
+    f = _by_type(t, 'orc_dot_q4_k', 'orc_dot_q5_k', 'orc_dot_q8_0')
     return f(_p(np.ascontiguousarray(wrow)), _p(np.ascontiguousarray(yq)), K)
 
 

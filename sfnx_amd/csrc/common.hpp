@@ -13,7 +13,7 @@
 namespace sfnx {
 
 constexpr int WAVE = 64;
-constexpr int Q4K_BYTES = 144, Q80_BYTES = 34, Q81_BYTES = 36;
+constexpr int Q4K_BYTES = 144, Q5K_BYTES = 176, Q80_BYTES = 34, Q81_BYTES = 36;
 
 // ------------------------------------------------------------------------------------------------ errors
 void set_error(const std::string& msg);
@@ -168,18 +168,26 @@ template <int RT> __host__ __device__ __forceinline__ size_t tiled16(int row, si
 }
 constexpr int Q4K_RT = 32, Q80_RT = 4;
 constexpr int PIECE_STRIDE = Q4K_RT * 16;   // Q4_K: bytes from one piece of a row to the next
-struct Q4kPlanes {
+// the K-quants (Q4_K, Q5_K): nibble plane, then (Q5_K) the fifth-bit plane, then the header plane
+struct KqPlanes {
     const uint8_t* nib;   // R x C/2: a row's runs of 256 bytes (two super-blocks), 16-byte pieces in [half][group] order
+    const uint8_t* qh;    // Q5_K: R x C/8: a super-block's 32 qh bytes as pieces 2 b, 2 b + 1
     const uint8_t* hdr;   // R x C/256 x 16: a row's super-block headers, one piece each
     // piece p (bytes 16 p .. 16 p + 15) of row r's nibble bytes
     __host__ __device__ __forceinline__ const uint8_t* nib16(int r, int C, int p) const { return nib + tiled16<Q4K_RT>(r, C / 2, p); }
+    // piece p of row r's qh bytes (super-block p / 2, bytes 16 (p % 2) ..)
+    __host__ __device__ __forceinline__ const uint8_t* qh16(int r, int C, int p) const { return qh + tiled16<Q4K_RT>(r, C / 8, p); }
     // the 16-byte header of super-block b of row r
     __host__ __device__ __forceinline__ const uint8_t* hdr16(int r, int C, int b) const { return hdr + tiled16<Q4K_RT>(r, C / 16, b); }
 };
-__host__ __device__ __forceinline__ Q4kPlanes q4k_planes(const void* mat, int R, int C) {
+using Q4kPlanes = KqPlanes;
+template <bool Q5> __host__ __device__ __forceinline__ KqPlanes kq_planes(const void* mat, int R, int C) {
     const uint8_t* p = (const uint8_t*) mat;
-    return Q4kPlanes{p, p + (size_t) R * (C / 2)};
+    const size_t nib = (size_t) R * (C / 2), qh = Q5 ? (size_t) R * (C / 8) : 0;
+    return KqPlanes{p, p + nib, p + nib + qh};
 }
+__host__ __device__ __forceinline__ KqPlanes q4k_planes(const void* mat, int R, int C) { return kq_planes<false>(mat, R, C); }
+__host__ __device__ __forceinline__ KqPlanes q5k_planes(const void* mat, int R, int C) { return kq_planes<true>(mat, R, C); }
 struct Q80Planes {
     const uint8_t* q;     // R x C: a row's 512-byte runs (16 blocks), 16-byte pieces in [half][block] order
     const uint8_t* d;     // R x C/32 f16: a row's block scales, 8 a piece
@@ -195,8 +203,12 @@ __host__ __device__ __forceinline__ Q80Planes q80_planes(const void* mat, int R,
     return Q80Planes{p, p + (size_t) R * C};
 }
 
+inline bool expert_type_ok(uint32_t type) { return type == SFNX_Q4_K || type == SFNX_Q5_K || type == SFNX_Q8_0; }
+inline int block_values(uint32_t type) { return type == SFNX_Q8_0 ? 32 : 256; }
 inline size_t row_bytes(uint32_t type, int cols) {
-    return type == SFNX_Q4_K ? (size_t) cols / 256 * Q4K_BYTES : (size_t) cols / 32 * Q80_BYTES;
+    return type == SFNX_Q4_K ? (size_t) cols / 256 * Q4K_BYTES
+           : type == SFNX_Q5_K ? (size_t) cols / 256 * Q5K_BYTES
+                               : (size_t) cols / 32 * Q80_BYTES;
 }
 
 }  // namespace sfnx

@@ -350,12 +350,12 @@ extern "C" int sfnx_gguf_moe_layer(const sfnx_gguf* g, int layer, int ff0, int f
         const sfnx_gguf_tensor& td = need(g, L + "ffn_down_exps.weight");
         const sfnx_gguf_tensor& ti = need(g, L + "ffn_gate_inp.weight");
         const uint32_t type = tg.type;
-        require(type == SFNX_Q4_K || type == SFNX_Q8_0, "expert tensors must be Q4_K or Q8_0");
+        require(expert_type_ok(type), "expert tensors must be Q4_K, Q5_K or Q8_0");
         require(tu.type == type && td.type == type, "gate, up and down experts differ in type");
         const int64_t H = tg.ne[0], FF = tg.ne[1], E = tg.ne[2];
         require(tu.ne[0] == H && tu.ne[1] == FF && tu.ne[2] == E, "up experts differ in shape from gate experts");
         require(td.ne[0] == FF && td.ne[1] == H && td.ne[2] == E, "down experts are not [FF][H] a expert");
-        const int cb = type == SFNX_Q4_K ? 256 : 32;   // a column slice of the down rows is whole blocks
+        const int cb = block_values(type);   // a column slice of the down rows is whole blocks
         require(0 <= ff0 && ff0 < ff1 && ff1 <= FF && ff0 % cb == 0 && (ff1 - ff0) % 512 == 0,
                 "FF slice must start on a whole block and span a multiple of 512 (the store's runs)");
         require(H % 512 == 0, "the hidden size must be a multiple of 512 (the store's runs)");
@@ -395,7 +395,7 @@ extern "C" int sfnx_gguf_moe_layer(const sfnx_gguf* g, int layer, int ff0, int f
         try {
             uint8_t* h = (uint8_t*) host;
             const size_t rb_full_dn = row_bytes(type, (int) FF);
-            const size_t col0 = (size_t) (ff0 / cb) * (type == SFNX_Q4_K ? Q4K_BYTES : Q80_BYTES);
+            const size_t col0 = row_bytes(type, ff0);
             for (int64_t e = 0; e < NE; ++e) {
                 const bool sh = e == E;
                 const uint8_t* g0 = (const uint8_t*) (sh ? sg->data : tg.data) + (sh ? 0 : e * FF * rb_in);

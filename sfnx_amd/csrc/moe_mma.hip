@@ -35,9 +35,12 @@ template <int SEL> __device__ __forceinline__ half2v bytes_1024(uint32_t w) {
     return as_h2(__builtin_amdgcn_perm(0x64646464u, w, SEL == 0 ? 0x05010400u : 0x05030402u));
 }
 
-// Q4_K: 16 bytes of a group's quants (b0..b15, low nibbles of sub-block 2jg, high of 2jg + 1) -> the 4 B fragments
-__device__ __forceinline__ void deq_q4k(const uint4& q, half2v d1l, half2v nml, half2v d1h, half2v nmh, half8 (&b)[4]) {
+// Q4_K: 16 bytes of a group's quants (b0..b15, low nibbles of sub-block 2jg, high of 2jg + 1) -> the 4 B fragments;
+// Q5_K (qh given): the fifth bit of each value from bit j0 (low nibbles) or j0 + 1 (high) of the matching qh byte
+__device__ __forceinline__ void deq_q4k(const uint4& q, half2v d1l, half2v nml, half2v d1h, half2v nmh, half8 (&b)[4],
+                                        const uint4* qh = nullptr, int j0 = 0) {
     const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+    const uint32_t x[4] = {qh ? qh->x : 0u, qh ? qh->y : 0u, qh ? qh->z : 0u, qh ? qh->w : 0u};
     const half2v k1024 = {(_Float16) 1024.0f, (_Float16) 1024.0f};
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -47,7 +50,8 @@ __device__ __forceinline__ void deq_q4k(const uint4& q, half2v d1l, half2v nml, 
         const half2v d1 = hi ? d1h : d1l, nm = hi ? nmh : nml;
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
-            const uint32_t v = hi ? (w[wi + p] >> 4) & 0x0F0F0F0Fu : w[wi + p] & 0x0F0F0F0Fu;
+            uint32_t v = hi ? (w[wi + p] >> 4) & 0x0F0F0F0Fu : w[wi + p] & 0x0F0F0F0Fu;
+            if (qh) v |= ((x[wi + p] >> (hi ? j0 + 1 : j0)) & 0x01010101u) << 4;
             const half2v q01 = bytes_1024<0>(v) - k1024, q23 = bytes_1024<1>(v) - k1024;
             const half2v r01 = __builtin_elementwise_fma(q01, d1, nm), r23 = __builtin_elementwise_fma(q23, d1, nm);
             b[c][4 * p + 0] = r01[0];
@@ -85,6 +89,10 @@ template <> struct Chunk<SFNX_Q4_K> {
     static constexpr int STEPS = 4, LOADS = 5;   // steps a chunk; load instructions a chunk
     uint4 q[4], hdr;
 };
+template <> struct Chunk<SFNX_Q5_K> {
+    static constexpr int STEPS = 4, LOADS = 6;
+    uint4 q[4], hdr, qh;   // qh: the super-block's qh bytes 16 h .. 16 h + 15 (the fifth bits of the lane's values)
+};
 template <> struct Chunk<SFNX_Q8_0> {
     static constexpr int STEPS = 2, LOADS = 5;
     uint4 qa[2], qb[2];
@@ -93,18 +101,26 @@ template <> struct Chunk<SFNX_Q8_0> {
 
 // Where chunk c (of the run's 8 / STEPS) of run r of the lane's row lies.
 struct ChunkAt {
-    const uint8_t* q;     // the first 16-byte piece (Q4_K: nibbles; Q8_0: first halves); the next one a tile's pieces on
-    const uint8_t* tail;  // Q4_K: the super-block header; Q8_0: the two f16 scales
+    const uint8_t* q;     // the first 16-byte piece (K-quants: nibbles; Q8_0: first halves); the next one a tile's pieces on
+    const uint8_t* tail;  // K-quants: the super-block header; Q8_0: the two f16 scales
+    const uint8_t* qh;    // Q5_K: the lane-half's qh piece
 };
 __device__ __forceinline__ ChunkAt chunk_at(const Chunk<SFNX_Q4_K>*, const uint8_t* mat, int R, int C, int row, int r, int c, int h) {
     const Q4kPlanes P = q4k_planes(mat, R, C);
-    return ChunkAt{P.nib16(row, C, 16 * r + 8 * h + 4 * c), P.hdr16(row, C, 2 * r + c)};
+    return ChunkAt{P.nib16(row, C, 16 * r + 8 * h + 4 * c), P.hdr16(row, C, 2 * r + c), nullptr};
+}
+__device__ __forceinline__ ChunkAt chunk_at(const Chunk<SFNX_Q5_K>*, const uint8_t* mat, int R, int C, int row, int r, int c, int h) {
+    const KqPlanes P = q5k_planes(mat, R, C);
+    return ChunkAt{P.nib16(row, C, 16 * r + 8 * h + 4 * c), P.hdr16(row, C, 2 * r + c), P.qh16(row, C, 2 * (2 * r + c) + h)};
 }
 __device__ __forceinline__ ChunkAt chunk_at(const Chunk<SFNX_Q8_0>*, const uint8_t* mat, int R, int C, int row, int r, int c, int h) {
     const Q80Planes P = q80_planes(mat, R, C);
-    return ChunkAt{P.q16(row, C, 32 * r + 8 * h + 2 * c), P.d16(row, C, 2 * r + h) + 4 * c};
+    return ChunkAt{P.q16(row, C, 32 * r + 8 * h + 2 * c), P.d16(row, C, 2 * r + h) + 4 * c, nullptr};
 }
 __device__ __forceinline__ void load_piece(Chunk<SFNX_Q4_K>& w, const ChunkAt& a, int s) {
+    w.q[s] = *reinterpret_cast<const uint4*>(a.q + PIECE_STRIDE * s);
+}
+__device__ __forceinline__ void load_piece(Chunk<SFNX_Q5_K>& w, const ChunkAt& a, int s) {
     w.q[s] = *reinterpret_cast<const uint4*>(a.q + PIECE_STRIDE * s);
 }
 __device__ __forceinline__ void load_piece(Chunk<SFNX_Q8_0>& w, const ChunkAt& a, int s) {
@@ -112,6 +128,10 @@ __device__ __forceinline__ void load_piece(Chunk<SFNX_Q8_0>& w, const ChunkAt& a
     w.qb[s] = *reinterpret_cast<const uint4*>(a.q + Q80_RT * 16 * (16 + s));   // the blocks' second halves
 }
 __device__ __forceinline__ void load_tail(Chunk<SFNX_Q4_K>& w, const ChunkAt& a) { w.hdr = *reinterpret_cast<const uint4*>(a.tail); }
+__device__ __forceinline__ void load_tail(Chunk<SFNX_Q5_K>& w, const ChunkAt& a) {
+    w.hdr = *reinterpret_cast<const uint4*>(a.tail);
+    w.qh = *reinterpret_cast<const uint4*>(a.qh);
+}
 __device__ __forceinline__ void load_tail(Chunk<SFNX_Q8_0>& w, const ChunkAt& a) { w.d = *reinterpret_cast<const uint32_t*>(a.tail); }
 template <int TYPE> __device__ __forceinline__ void load_chunk(Chunk<TYPE>& w, const ChunkAt& a) {
 #pragma unroll
@@ -130,6 +150,16 @@ __device__ __forceinline__ void dequant_step(const Chunk<SFNX_Q4_K>& w, int s, h
     const _Float16 d1h = (_Float16) (d * sc), nmh = (_Float16) (-(dmin * m));
     deq_q4k(w.q[s], half2v{d1l, d1l}, half2v{nml, nml}, half2v{d1h, d1h}, half2v{nmh, nmh}, b);
 }
+__device__ __forceinline__ void dequant_step(const Chunk<SFNX_Q5_K>& w, int s, half8 (&b)[4]) {
+    const uint4 hd = w.hdr;
+    const float d = h2f((uint16_t) (hd.x & 0xffff)), dmin = h2f((uint16_t) (hd.x >> 16));
+    float sc, m;
+    q4k_scale_min(hd, 2 * s, sc, m);
+    const _Float16 d1l = (_Float16) (d * sc), nml = (_Float16) (-(dmin * m));
+    q4k_scale_min(hd, 2 * s + 1, sc, m);
+    const _Float16 d1h = (_Float16) (d * sc), nmh = (_Float16) (-(dmin * m));
+    deq_q4k(w.q[s], half2v{d1l, d1l}, half2v{nml, nml}, half2v{d1h, d1h}, half2v{nmh, nmh}, b, &w.qh, 2 * s);
+}
 __device__ __forceinline__ void dequant_step(const Chunk<SFNX_Q8_0>& w, int s, half8 (&b)[4]) {
     const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t) (w.d >> (16 * s)));
     deq_q80(w.qa[s], w.qb[s], half2v{d, d}, b);
@@ -137,7 +167,7 @@ __device__ __forceinline__ void dequant_step(const Chunk<SFNX_Q8_0>& w, int s, h
 
 // column (within the run's 512) where MFMA k-chunk c of step j starts for lane-half h
 template <int TYPE> __device__ __forceinline__ int run_col(int j, int c, int h) {
-    if constexpr (TYPE == SFNX_Q4_K) return 64 * j + (c < 2 ? 16 * h + 8 * c : 32 + 16 * h + 8 * (c - 2));
+    if constexpr (TYPE != SFNX_Q8_0) return 64 * j + (c < 2 ? 16 * h + 8 * c : 32 + 16 * h + 8 * (c - 2));
     else return 256 * h + 32 * j + 8 * c;
 }
 
@@ -399,7 +429,7 @@ constexpr size_t MM_LDS = 2 * MM_XBUF * sizeof(_Float16);
 
 void moe_mma(uint32_t type, const void* A, size_t sa, int n_in, int n_out, const sfnx_bigjob* jobs, const int* njobs,
              int njobs_cap, const void* x16, float* out, void* st) {
-    require(type == SFNX_Q4_K || type == SFNX_Q8_0, "expert type must be Q4_K (12) or Q8_0 (8)");
+    require(expert_type_ok(type), "expert type must be Q4_K (12), Q5_K (13) or Q8_0 (8)");
     require(n_in > 0 && n_in % 512 == 0, "expert input width must be a multiple of 512");
     require(n_out > 0 && n_out % DN_BM == 0, "expert rows must be a multiple of 256");
     require((n_out / DN_BM) % std::max(1, (n_out / DN_BM) / 2) == 0, "row groups must split evenly");
@@ -413,13 +443,15 @@ void moe_mma(uint32_t type, const void* A, size_t sa, int n_in, int n_out, const
     hipStream_t s = stream_of(st);
     if (type == SFNX_Q4_K)
         k_moe_mma<SFNX_Q4_K><<<grid, DN_THREADS, lds, s>>>((const uint8_t*) A, sa, n_out, n_in, G, jobs, njobs, (const _Float16*) x16, out);
+    else if (type == SFNX_Q5_K)
+        k_moe_mma<SFNX_Q5_K><<<grid, DN_THREADS, lds, s>>>((const uint8_t*) A, sa, n_out, n_in, G, jobs, njobs, (const _Float16*) x16, out);
     else
         k_moe_mma<SFNX_Q8_0><<<grid, DN_THREADS, lds, s>>>((const uint8_t*) A, sa, n_out, n_in, G, jobs, njobs, (const _Float16*) x16, out);
 }
 
 void moe_mma_gu(uint32_t type, const void* A, size_t sa, int n_in, int ff, const sfnx_bigjob* jobs, const int* njobs,
                 int njobs_cap, const void* x16, float* gu, uint16_t* h16, void* st) {
-    require(type == SFNX_Q4_K || type == SFNX_Q8_0, "expert type must be Q4_K (12) or Q8_0 (8)");
+    require(expert_type_ok(type), "expert type must be Q4_K (12), Q5_K (13) or Q8_0 (8)");
     require(n_in > 0 && n_in % 512 == 0, "expert input width must be a multiple of 512");
     require(ff > 0 && ff % MM_FF == 0, "FF must be a multiple of 256");
     require(sa >= row_bytes(type, n_in) * (size_t) (2 * ff), "expert stride smaller than a matrix");
@@ -429,6 +461,9 @@ void moe_mma_gu(uint32_t type, const void* A, size_t sa, int n_in, int ff, const
     hipStream_t s = stream_of(st);
     if (type == SFNX_Q4_K)
         k_moe_mma_gu<SFNX_Q4_K><<<grid, MM_THREADS, MM_LDS, s>>>((const uint8_t*) A, sa, ff, n_in, jobs, njobs,
+                                                                  (const _Float16*) x16, gu, (_Float16*) h16);
+    else if (type == SFNX_Q5_K)
+        k_moe_mma_gu<SFNX_Q5_K><<<grid, MM_THREADS, MM_LDS, s>>>((const uint8_t*) A, sa, ff, n_in, jobs, njobs,
                                                                   (const _Float16*) x16, gu, (_Float16*) h16);
     else
         k_moe_mma_gu<SFNX_Q8_0><<<grid, MM_THREADS, MM_LDS, s>>>((const uint8_t*) A, sa, ff, n_in, jobs, njobs,

@@ -1,7 +1,8 @@
-// Device building blocks of the expert kernels: jobs and activations in LDS, and a lane group's share of one Q4_K or
-// Q8_0 weight row dotted with int8 activations (v_dot4_i32_i8).  The arithmetic per (row, activation row):
+// Device building blocks of the expert kernels: jobs and activations in LDS, and a lane group's share of one Q4_K,
+// Q5_K or Q8_0 weight row dotted with int8 activations (v_dot4_i32_i8).  The arithmetic per (row, activation row):
 //   Q4_K: 8 lanes a row, lane l8 the 64-value groups l8 + 8 i in order (src/moe_q4k.cuh:30-86), each group
 //         d (d8l (sc0 dl) + d8h (sc1 dh)) - dmin (d8l (m0 sl) + d8h (m1 sh)), then xor 4, 2, 1 (src/moe.cuh:224-235).
+//   Q5_K: the same on the 5-bit values (the fifth bit of value l of sub-block j is bit j of qh[l]).
 //   Q8_0: 16 lanes a row, lane l16 the 32-blocks l16 + 16 i in order, each (d_w d_a) sum(q_w q_a), then xor 8 .. 1.
 #pragma once
 #include "common.hpp"
@@ -75,9 +76,11 @@ __device__ inline void stage_swiglu(const Acts& a, const float* __restrict__ gu,
 }
 
 // ------------------------------------------------------------------------------------------------ Q4_K
-template <int GPL> struct Q4kRow {
+// Q5_K (Q5): the same lanes and combine on 5-bit values, the fifth bits from the qh pieces of the lane's super-block
+template <int GPL, bool Q5 = false> struct Q4kRow {
     uint4 q0[GPL], q1[GPL];
     uint4 h[GPL];
+    uint4 qh0[Q5 ? GPL : 1], qh1[Q5 ? GPL : 1];
     float d[GPL], dmin[GPL], sc0[GPL], m0[GPL], sc1[GPL], m1[GPL];
     // the loads alone (issue several rows' before any prepare, so that their latencies overlap)
     __device__ __forceinline__ void issue(const Q4kPlanes& P, int row, int C, int l8) {
@@ -86,6 +89,10 @@ template <int GPL> struct Q4kRow {
             q0[i] = *reinterpret_cast<const uint4*>(P.nib16(row, C, 16 * i + l8));
             q1[i] = *reinterpret_cast<const uint4*>(P.nib16(row, C, 16 * i + 8 + l8));
             h[i] = *reinterpret_cast<const uint4*>(P.hdr16(row, C, 2 * i + (l8 >> 2)));
+            if constexpr (Q5) {
+                qh0[i] = *reinterpret_cast<const uint4*>(P.qh16(row, C, 2 * (2 * i + (l8 >> 2))));
+                qh1[i] = *reinterpret_cast<const uint4*>(P.qh16(row, C, 2 * (2 * i + (l8 >> 2)) + 1));
+            }
         }
     }
     // the block headers decoded: d, dmin and this lane's two sub-blocks' 6-bit scales and mins
@@ -126,8 +133,15 @@ template <int GPL> struct Q4kRow {
         int dl = 0, dh = 0;
 #pragma unroll
         for (int w = 0; w < 8; ++w) {
-            dl = dot4((int) (qw[w] & 0x0F0F0F0Fu), al[w], dl);
-            dh = dot4((int) ((qw[w] >> 4) & 0x0F0F0F0Fu), ah[w], dh);
+            unsigned lo = qw[w] & 0x0F0F0F0Fu, hi = (qw[w] >> 4) & 0x0F0F0F0Fu;
+            if constexpr (Q5) {
+                const unsigned hw = w < 4 ? (&qh0[i].x)[w] : (&qh1[i].x)[w - 4];
+                const int jg = l8 & 3;
+                lo |= ((hw >> (2 * jg)) & 0x01010101u) << 4;
+                hi |= ((hw >> (2 * jg + 1)) & 0x01010101u) << 4;
+            }
+            dl = dot4((int) lo, al[w], dl);
+            dh = dot4((int) hi, ah[w], dh);
         }
         const int nb = a.K / 32;
         const float d8l = a.d[j * nb + kb0], d8h = a.d[j * nb + kb0 + 1];

@@ -33,13 +33,17 @@ __global__ void k_synth(float* out, size_t n, uint64_t seed, uint64_t offset, fl
 // ------------------------------------------------------------------------------------------------ quantizers
 __device__ __forceinline__ int clampi(int v, int lo, int hi) { return v < lo ? lo : v > hi ? hi : v; }
 
-// one Q4_K super-block per thread: per 32-value sub-block min' = min(0, min x) and scale = (max - min') / 15, d and
-// dmin the largest of each over 63 as f16, 6-bit sc and m against the stored f16, 4-bit q = round((x + dmin m) / (d sc))
-__global__ void k_quant_q4k(const float* __restrict__ x, uint8_t* __restrict__ dst, int64_t nblk) {
+// one K-quant super-block per thread, Q4_K (Q5 false: 15 levels) or Q5_K (31 levels, the fifth bit in qh): per
+// 32-value sub-block min' = min(0, min x) and scale = (max - min') / levels, d and dmin the largest of each over 63 as
+// f16, 6-bit sc and m against the stored f16, q = round((x + dmin m) / (d sc))
+template <bool Q5>
+__global__ void k_quant_kq(const float* __restrict__ x, uint8_t* __restrict__ dst, int64_t nblk) {
     const int64_t k = blockIdx.x * (int64_t) blockDim.x + threadIdx.x;
     if (k >= nblk) return;
+    const float levels = Q5 ? 31.0f : 15.0f;
+    const int qmax = Q5 ? 31 : 15;
     const float* v = x + k * 256;
-    uint8_t* b = dst + k * Q4K_BYTES;
+    uint8_t* b = dst + k * (Q5 ? Q5K_BYTES : Q4K_BYTES);
     float scale[8], mn8[8], max_scale = 0.f, max_min = 0.f;
     for (int j = 0; j < 8; ++j) {
         float mn = v[32 * j], mx = v[32 * j];
@@ -49,7 +53,7 @@ __global__ void k_quant_q4k(const float* __restrict__ x, uint8_t* __restrict__ d
             if (t > mx) mx = t;
         }
         if (mn > 0.f) mn = 0.f;
-        scale[j] = (mx - mn) / 15.0f;
+        scale[j] = (mx - mn) / levels;
         mn8[j] = mn < 0.f ? -mn : 0.f;
         if (scale[j] > max_scale) max_scale = scale[j];
         if (mn8[j] > max_min) max_min = mn8[j];
@@ -70,14 +74,17 @@ __global__ void k_quant_q4k(const float* __restrict__ x, uint8_t* __restrict__ d
         b[8 + j] = (uint8_t) ((m[j] & 63) | ((m[j + 4] >> 4) << 6));
         b[12 + j] = (uint8_t) ((sc[j + 4] & 0xF) | ((m[j + 4] & 0xF) << 4));
     }
+    uint8_t* qh = b + 16;
+    uint8_t* qs = b + (Q5 ? 48 : 16);
     for (int jp = 0; jp < 4; ++jp) {
         const int j0 = 2 * jp, j1 = j0 + 1;
         const float dl0 = df * (float) sc[j0], ml0 = mf * (float) m[j0];
         const float dl1 = df * (float) sc[j1], ml1 = mf * (float) m[j1];
         for (int l = 0; l < 32; ++l) {
-            const int q0 = dl0 > 0.f ? clampi((int) roundf((v[32 * j0 + l] + ml0) / dl0), 0, 15) : 0;
-            const int q1 = dl1 > 0.f ? clampi((int) roundf((v[32 * j1 + l] + ml1) / dl1), 0, 15) : 0;
-            b[16 + 32 * jp + l] = (uint8_t) (q0 | (q1 << 4));
+            const int q0 = dl0 > 0.f ? clampi((int) roundf((v[32 * j0 + l] + ml0) / dl0), 0, qmax) : 0;
+            const int q1 = dl1 > 0.f ? clampi((int) roundf((v[32 * j1 + l] + ml1) / dl1), 0, qmax) : 0;
+            qs[32 * jp + l] = (uint8_t) ((q0 & 15) | ((q1 & 15) << 4));
+            if (Q5) qh[l] = (uint8_t) ((jp ? qh[l] : 0) | ((q0 >> 4) << j0) | ((q1 >> 4) << j1));
         }
     }
 }
@@ -102,32 +109,31 @@ __global__ void k_quant_q80(const float* __restrict__ x, uint8_t* __restrict__ d
 }
 
 // ------------------------------------------------------------------------------------------------ packing
-// Q4_K: thread per (row, super-block).  Nibble bytes 32 jg + 16 h + x of super-block b land in the row's run b / 2 at
-// 128 h + 16 ((b % 2) 4 + jg) + x; the 16 header bytes at the header plane's (row, b).
-template <bool PACK>
-__global__ void k_pack_q4k(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, int64_t n_mat, int R, int C) {
+// K-quants: thread per (row, super-block).  Nibble bytes 32 jg + 16 h + x of super-block b land in piece
+// 16 (b / 2) + 8 h + 4 (b % 2) + jg of the row's nibbles (the run b / 2 in [half][group] order), byte x; the 16 header
+// bytes are header piece b; Q5_K's qh bytes 16 h + x are qh piece 2 b + h.
+template <bool Q5, bool PACK>
+__global__ void k_pack_kq(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, int64_t n_mat, int R, int C) {
+    constexpr int BB = Q5 ? Q5K_BYTES : Q4K_BYTES, QS = Q5 ? 48 : 16;
     const int nb = C / 256;
     const int64_t k = blockIdx.x * (int64_t) blockDim.x + threadIdx.x, per_mat = (int64_t) R * nb;
     if (k >= n_mat * per_mat) return;
     const int64_t m = k / per_mat;
     const int r = (int) ((k % per_mat) / nb), b = (int) (k % nb);
-    const size_t mat_bytes = (size_t) R * nb * Q4K_BYTES;
-    const size_t gg = m * mat_bytes + ((size_t) r * nb + b) * Q4K_BYTES;                          // GGUF block
-    const Q4kPlanes P = q4k_planes((const uint8_t*) nullptr + m * mat_bytes, R, C);
-    const size_t hdr = (size_t) P.hdr16(r, C, b);
-    for (int i = 0; i < 16; ++i) {
-        if (PACK) dst[hdr + i] = src[gg + i];
-        else dst[gg + i] = src[hdr + i];
-    }
+    const size_t mat_bytes = (size_t) R * nb * BB;
+    const size_t gg = m * mat_bytes + ((size_t) r * nb + b) * BB;   // GGUF block
+    const KqPlanes P = kq_planes<Q5>((const uint8_t*) nullptr + m * mat_bytes, R, C);
+    auto mv = [&](size_t pg, size_t pp) {
+        if (PACK) dst[pp] = src[pg];
+        else dst[pg] = src[pp];
+    };
+    for (int i = 0; i < 16; ++i) mv(gg + i, (size_t) P.hdr16(r, C, b) + i);
+    if (Q5)
+        for (int i = 0; i < 32; ++i) mv(gg + 16 + i, (size_t) P.qh16(r, C, 2 * b + i / 16) + i % 16);
     for (int jg = 0; jg < 4; ++jg)
         for (int h = 0; h < 2; ++h)
-            for (int x = 0; x < 16; ++x) {
-                // the run's byte 128 h + 16 ((b % 2) 4 + jg) + x
-                const size_t pg = gg + 16 + 32 * jg + 16 * h + x,
-                             pp = (size_t) P.nib16(r, C, 16 * (b / 2) + 8 * h + (b % 2) * 4 + jg) + x;
-                if (PACK) dst[pp] = src[pg];
-                else dst[pg] = src[pp];
-            }
+            for (int x = 0; x < 16; ++x)
+                mv(gg + QS + 32 * jg + 16 * h + x, (size_t) P.nib16(r, C, 16 * (b / 2) + 8 * h + (b % 2) * 4 + jg) + x);
 }
 // Q8_0: thread per (row, block).  Quant bytes 16 h + x of block b land in the row's 512-byte run b / 16 at
 // 256 h + 16 (b % 16) + x; the scale at the scale plane's (row, b).
@@ -157,33 +163,31 @@ __global__ void k_pack_q80(const uint8_t* __restrict__ src, uint8_t* __restrict_
 
 // ------------------------------------------------------------------------------------------------ dequant
 // thread per (row, 32-value sub-block) of the planar store; F16: the tensor-core path's f16 weight
-template <bool F16>
-__global__ void k_deq_q4k(const uint8_t* __restrict__ src, void* __restrict__ out, int64_t n_mat, int R, int C) {
+template <bool Q5, bool F16>
+__global__ void k_deq_kq(const uint8_t* __restrict__ src, void* __restrict__ out, int64_t n_mat, int R, int C) {
     const int ns = C / 32;
     const int64_t k = blockIdx.x * (int64_t) blockDim.x + threadIdx.x, per_mat = (int64_t) R * ns;
     if (k >= n_mat * per_mat) return;
     const int64_t m = k / per_mat;
     const int r = (int) ((k % per_mat) / ns), s = (int) (k % ns), b = s / 8, j = s % 8, jg = j / 2, hi = j % 2;
-    const Q4kPlanes P = q4k_planes(src + m * ((size_t) R * (C / 256) * Q4K_BYTES), R, C);
+    const KqPlanes P = kq_planes<Q5>(src + m * ((size_t) R * (C / 256) * (Q5 ? Q5K_BYTES : Q4K_BYTES)), R, C);
     const uint4 h = *reinterpret_cast<const uint4*>(P.hdr16(r, C, b));
     const float d = h2f((uint16_t) (h.x & 0xffff)), dmin = h2f((uint16_t) (h.x >> 16));
     float sc, mm;
     q4k_scale_min(h, j, sc, mm);
     // the run's pieces 4 (b % 2) + jg (values 0-15) and 8 + 4 (b % 2) + jg (values 16-31)
     const int p0 = 16 * (b / 2) + (b % 2) * 4 + jg;
+    auto value = [&](int l) {
+        const int nib = (P.nib16(r, C, p0 + 8 * (l / 16))[l % 16] >> (4 * hi)) & 0xF;
+        return Q5 ? nib | (((P.qh16(r, C, 2 * b + l / 16)[l % 16] >> j) & 1) << 4) : nib;
+    };
     const size_t o = (size_t) m * R * C + (size_t) r * C + 32 * s;
     if (F16) {
         const __half d1 = __float2half_rn(d * sc), nm1 = __float2half_rn(-(dmin * mm));
-        for (int l = 0; l < 32; ++l) {
-            const int q = (P.nib16(r, C, p0 + 8 * (l / 16))[l % 16] >> (4 * hi)) & 0xF;
-            ((__half*) out)[o + l] = __hfma(__int2half_rn(q), d1, nm1);
-        }
+        for (int l = 0; l < 32; ++l) ((__half*) out)[o + l] = __hfma(__int2half_rn(value(l)), d1, nm1);
     } else {
         const float d1 = d * sc, m1 = dmin * mm;
-        for (int l = 0; l < 32; ++l) {
-            const int q = (P.nib16(r, C, p0 + 8 * (l / 16))[l % 16] >> (4 * hi)) & 0xF;
-            ((float*) out)[o + l] = d1 * (float) q - m1;
-        }
+        for (int l = 0; l < 32; ++l) ((float*) out)[o + l] = d1 * (float) value(l) - m1;
     }
 }
 template <bool F16>
@@ -206,7 +210,7 @@ __global__ void k_deq_q80(const uint8_t* __restrict__ src, void* __restrict__ ou
 
 inline unsigned blocks_for(int64_t n, int t) { return (unsigned) ((n + t - 1) / t); }
 void check_type_shape(uint32_t type, int rows, int cols) {
-    require(type == SFNX_Q4_K || type == SFNX_Q8_0, "weight type must be Q4_K (12) or Q8_0 (8)");
+    require(expert_type_ok(type), "weight type must be Q4_K (12), Q5_K (13) or Q8_0 (8)");
     require(cols > 0 && cols % 512 == 0, "columns must be a positive multiple of 512");
     require(rows >= 0 && rows % ROWTILE == 0, "rows must be a multiple of 32 (the store's row tile)");
 }
@@ -229,61 +233,51 @@ extern "C" int sfnx_synth_normal(float* out, size_t n, uint64_t seed, uint64_t o
 
 extern "C" int sfnx_quantize_weights(uint32_t type, const float* x, void* gguf, int64_t rows, int cols, void* st) {
     return guarded("sfnx_quantize_weights", [&] {
-        require(type == SFNX_Q4_K || type == SFNX_Q8_0, "weight type must be Q4_K (12) or Q8_0 (8)");
-        require(cols > 0 && cols % (type == SFNX_Q4_K ? 256 : 32) == 0, "columns must be whole blocks");
+        require(expert_type_ok(type), "weight type must be Q4_K (12), Q5_K (13) or Q8_0 (8)");
+        require(cols > 0 && cols % block_values(type) == 0, "columns must be whole blocks");
         if (rows <= 0) return;
-        if (type == SFNX_Q4_K) {
-            const int64_t nb = rows * (cols / 256);
-            k_quant_q4k<<<blocks_for(nb, 128), 128, 0, stream_of(st)>>>(x, (uint8_t*) gguf, nb);
-        } else {
-            const int64_t nb = rows * (cols / 32);
-            k_quant_q80<<<blocks_for(nb, 256), 256, 0, stream_of(st)>>>(x, (uint8_t*) gguf, nb);
-        }
+        const int64_t nb = rows * (cols / block_values(type));
+        if (type == SFNX_Q4_K) k_quant_kq<false><<<blocks_for(nb, 128), 128, 0, stream_of(st)>>>(x, (uint8_t*) gguf, nb);
+        else if (type == SFNX_Q5_K) k_quant_kq<true><<<blocks_for(nb, 128), 128, 0, stream_of(st)>>>(x, (uint8_t*) gguf, nb);
+        else k_quant_q80<<<blocks_for(nb, 256), 256, 0, stream_of(st)>>>(x, (uint8_t*) gguf, nb);
     });
 }
 
+namespace {
+template <bool PACK> void pack(uint32_t type, const void* src, void* dst, int64_t n_mat, int R, int C, void* st) {
+    check_type_shape(type, R, C);
+    require(src != dst, "packing is out of place");
+    const int64_t n = n_mat * R * (C / block_values(type));
+    if (n <= 0) return;
+    const auto* s8 = (const uint8_t*) src;
+    auto* d8 = (uint8_t*) dst;
+    if (type == SFNX_Q4_K) k_pack_kq<false, PACK><<<blocks_for(n, 256), 256, 0, stream_of(st)>>>(s8, d8, n_mat, R, C);
+    else if (type == SFNX_Q5_K) k_pack_kq<true, PACK><<<blocks_for(n, 256), 256, 0, stream_of(st)>>>(s8, d8, n_mat, R, C);
+    else k_pack_q80<PACK><<<blocks_for(n, 256), 256, 0, stream_of(st)>>>(s8, d8, n_mat, R, C);
+}
+template <bool F16> void dequant(uint32_t type, const void* planar, void* y, int64_t n_mat, int R, int C, void* st) {
+    check_type_shape(type, R, C);
+    const int64_t n = n_mat * R * (C / 32);
+    if (n <= 0) return;
+    const auto* p = (const uint8_t*) planar;
+    if (type == SFNX_Q4_K) k_deq_kq<false, F16><<<blocks_for(n, 256), 256, 0, stream_of(st)>>>(p, y, n_mat, R, C);
+    else if (type == SFNX_Q5_K) k_deq_kq<true, F16><<<blocks_for(n, 256), 256, 0, stream_of(st)>>>(p, y, n_mat, R, C);
+    else k_deq_q80<F16><<<blocks_for(n, 256), 256, 0, stream_of(st)>>>(p, y, n_mat, R, C);
+}
+}  // namespace
+
 extern "C" int sfnx_store_pack(uint32_t type, const void* gguf, void* planar, int64_t n_mat, int R, int C, void* st) {
-    return guarded("sfnx_store_pack", [&] {
-        check_type_shape(type, R, C);
-        require(gguf != planar, "packing is out of place");
-        const int64_t n = n_mat * R * (type == SFNX_Q4_K ? C / 256 : C / 32);
-        if (n <= 0) return;
-        if (type == SFNX_Q4_K)
-            k_pack_q4k<true><<<blocks_for(n, 256), 256, 0, stream_of(st)>>>((const uint8_t*) gguf, (uint8_t*) planar, n_mat, R, C);
-        else
-            k_pack_q80<true><<<blocks_for(n, 256), 256, 0, stream_of(st)>>>((const uint8_t*) gguf, (uint8_t*) planar, n_mat, R, C);
-    });
+    return guarded("sfnx_store_pack", [&] { pack<true>(type, gguf, planar, n_mat, R, C, st); });
 }
 
 extern "C" int sfnx_store_unpack(uint32_t type, const void* planar, void* gguf, int64_t n_mat, int R, int C, void* st) {
-    return guarded("sfnx_store_unpack", [&] {
-        check_type_shape(type, R, C);
-        require(gguf != planar, "unpacking is out of place");
-        const int64_t n = n_mat * R * (type == SFNX_Q4_K ? C / 256 : C / 32);
-        if (n <= 0) return;
-        if (type == SFNX_Q4_K)
-            k_pack_q4k<false><<<blocks_for(n, 256), 256, 0, stream_of(st)>>>((const uint8_t*) planar, (uint8_t*) gguf, n_mat, R, C);
-        else
-            k_pack_q80<false><<<blocks_for(n, 256), 256, 0, stream_of(st)>>>((const uint8_t*) planar, (uint8_t*) gguf, n_mat, R, C);
-    });
+    return guarded("sfnx_store_unpack", [&] { pack<false>(type, planar, gguf, n_mat, R, C, st); });
 }
 
 extern "C" int sfnx_dequantize(uint32_t type, const void* planar, float* y, int64_t n_mat, int R, int C, void* st) {
-    return guarded("sfnx_dequantize", [&] {
-        check_type_shape(type, R, C);
-        const int64_t n = n_mat * R * (C / 32);
-        if (n <= 0) return;
-        if (type == SFNX_Q4_K) k_deq_q4k<false><<<blocks_for(n, 256), 256, 0, stream_of(st)>>>((const uint8_t*) planar, y, n_mat, R, C);
-        else k_deq_q80<false><<<blocks_for(n, 256), 256, 0, stream_of(st)>>>((const uint8_t*) planar, y, n_mat, R, C);
-    });
+    return guarded("sfnx_dequantize", [&] { dequant<false>(type, planar, y, n_mat, R, C, st); });
 }
 
 extern "C" int sfnx_dequantize_f16(uint32_t type, const void* planar, uint16_t* y, int64_t n_mat, int R, int C, void* st) {
-    return guarded("sfnx_dequantize_f16", [&] {
-        check_type_shape(type, R, C);
-        const int64_t n = n_mat * R * (C / 32);
-        if (n <= 0) return;
-        if (type == SFNX_Q4_K) k_deq_q4k<true><<<blocks_for(n, 256), 256, 0, stream_of(st)>>>((const uint8_t*) planar, y, n_mat, R, C);
-        else k_deq_q80<true><<<blocks_for(n, 256), 256, 0, stream_of(st)>>>((const uint8_t*) planar, y, n_mat, R, C);
-    });
+    return guarded("sfnx_dequantize_f16", [&] { dequant<true>(type, planar, y, n_mat, R, C, st); });
 }

@@ -17,7 +17,7 @@ namespace sfnx {
 using Job = sfnx_job;         // src/kernels.hpp:18-23
 using BigJob = sfnx_bigjob;   // src/kernels.hpp:25-32
 constexpr int MAXT = SFNX_MAXT, PF_JOB = SFNX_PF_JOB;
-enum GgmlType : uint32_t { T_Q8_0 = SFNX_Q8_0, T_Q4_K = SFNX_Q4_K };   // src/gguf.hpp:22-25
+enum GgmlType : uint32_t { T_Q8_0 = SFNX_Q8_0, T_Q4_K = SFNX_Q4_K, T_Q5_K = SFNX_Q5_K };   // src/gguf.hpp:22-25
 
 // src/model.hpp:78-87 DW: one matrix (or expert 0's of a stack), n_out rows of n_in
 struct DW {

@@ -26,6 +26,7 @@ def _layer_bytes(wtype, H, E, ff, seed):
 
 
 @pytest.mark.parametrize("wtype,H,E,ff,ff0,ff1", [(orc.Q4_K, 1024, 64, 512, 0, 512), (orc.Q4_K, 1024, 64, 1024, 256, 768),
+                                                  (orc.Q5_K, 1024, 64, 1024, 256, 768),
                                                   (orc.Q8_0, 1024, 64, 512, 0, 512), (orc.Q8_0, 1024, 64, 1024, 32, 544)])
 def test_gguf_layer(tmp_path, wtype, H, E, ff, ff0, ff1):
     W, gate, up, down, shared = _layer_bytes(wtype, H, E, ff, 11)
@@ -42,8 +43,7 @@ def test_gguf_layer(tmp_path, wtype, H, E, ff, ff0, ff1):
     assert np.array_equal(L.W.cpu().numpy(), np.vstack([W, shared[3][None]]))
     # the store, unpacked to GGUF layout, against the sliced source bytes
     rb_h, rb_f, rb_full = orc.row_bytes(wtype, H), orc.row_bytes(wtype, ffs), orc.row_bytes(wtype, ff)
-    cb = 256 if wtype == orc.Q4_K else 32
-    col0 = (ff0 // cb) * (144 if wtype == orc.Q4_K else 34)
+    col0 = orc.row_bytes(wtype, ff0)
     gu_g = torch.empty_like(L.gu_w)
     dn_g = torch.empty_like(L.dn_w)
     moe.store_unpack(wtype, L.gu_w, gu_g, E + 1, 2 * ffs, H)

@@ -223,3 +223,86 @@ def test_q8_1_bounds_and_sum(orc):
     assert np.all(np.abs(xb / d32[..., None] - qs) <= 0.5 + 1e-5)
     assert np.allclose(d, d32, rtol=1e-3)
     assert np.allclose(s, xb.sum(axis=2), rtol=2e-3, atol=2e-3)
+
+
+# ------------------------------------------------------------------------------------------------ Q5_K
+def _q5k_block(d_bits, dmin_bits, sc, m, q):
+    """a Q5_K block (ggml block_q5_K): q[j][l] (0..31) is value l of sub-block j; its low 4 bits go where Q4_K keeps
+    them (qs, after a 32-byte qh), its fifth bit is bit j of qh[l]"""
+    qs = bytearray(128)
+    qh = bytearray(32)
+    for j in range(8):
+        for l in range(32):
+            qs[32 * (j // 2) + l] |= (q[j][l] & 15) << (4 * (j % 2))
+            qh[l] |= (q[j][l] >> 4) << j
+    return np.frombuffer(np.uint16([d_bits, dmin_bits]).tobytes() + _pack_scales(sc, m) + bytes(qh) + bytes(qs), np.uint8)
+
+
+def test_q5k_dequant_known_block(orc):
+    sc = [1, 2, 3, 63, 17, 40, 0, 5]
+    m = [0, 1, 7, 63, 32, 9, 2, 44]
+    # every sub-block uses all 32 values, each sub-block a different rotation so that a wrong qh bit index shows
+    q = [[(l * 7 + 5 * j) % 32 for l in range(32)] for j in range(8)]
+    blk = _q5k_block(0x3C00, 0x3800, sc, m, q)  # d = 1, dmin = 0.5
+    assert blk.size == 176
+    got = orc.dequant(orc.Q5_K, blk, 1, 256)[0]
+    want = np.array([sc[j] * q[j][l] - 0.5 * m[j] for j in range(8) for l in range(32)], np.float32)
+    assert np.array_equal(got, want)
+    # the tensor-core form rounds the exact q f16(d sc) - f16(dmin m) once to f16 (above 1024 not every half is one)
+    got16 = orc.dequant_f16(orc.Q5_K, blk, 1, 256)[0].view(np.float16)
+    assert np.array_equal(got16, want.astype(np.float16))
+
+
+def test_q5k_dequant_f16_rounds_once(orc):
+    rng = np.random.default_rng(14)
+    sc = rng.integers(0, 64, 8).tolist()
+    m = rng.integers(0, 64, 8).tolist()
+    q = rng.integers(0, 32, (8, 32)).tolist()
+    blk = _q5k_block(0x1E66, 0x1A3D, sc, m, q)
+    d, dmin = (Fraction(float(np.uint16(b).view(np.float16))) for b in (0x1E66, 0x1A3D))
+    got = orc.dequant_f16(orc.Q5_K, blk, 1, 256)[0]
+    for j in range(8):
+        d1 = Fraction(float(np.float16(np.float32(float(d * sc[j])))))
+        nm1 = Fraction(float(np.float16(np.float32(-float(dmin * m[j])))))
+        for l in range(32):
+            assert got[32 * j + l] == _round_f16_exact(q[j][l] * d1 + nm1) or q[j][l] * d1 + nm1 == 0
+
+
+def test_q5k_quantizer_is_exact_on_its_own_grid(orc):
+    """values on a block's grid (d sc q - dmin m with q spanning 0..31 in every sub-block) come back bit-exact"""
+    rng = np.random.default_rng(15)
+    for _ in range(20):
+        sc = rng.integers(1, 64, 8)
+        sc[int(rng.integers(0, 8))] = 63
+        q = rng.integers(0, 32, (8, 32))
+        q[:, 0], q[:, 1] = 0, 31
+        blk = _q5k_block(0x1400, 0x0000, sc.tolist(), [0] * 8, q.tolist())
+        x = orc.dequant(orc.Q5_K, blk, 1, 256)
+        back = orc.quantize(orc.Q5_K, x)
+        assert np.array_equal(back, blk)
+
+
+def test_q5k_quantizer_round_trip_bound(orc):
+    """per sub-block the error is at most half a step plus what the 6-bit scale and min cost; the 31-level grid
+    halves Q4_K's error on the same data"""
+    rows, cols = 32, 1024
+    x = orc.synth(rows * cols, 11, 0.02).reshape(rows, cols)
+    y5 = orc.dequant(orc.Q5_K, orc.quantize(orc.Q5_K, x), rows, cols)
+    y4 = orc.dequant(orc.Q4_K, orc.quantize(orc.Q4_K, x), rows, cols)
+    e5 = np.sqrt(np.mean((x - y5) ** 2)) / np.std(x)
+    e4 = np.sqrt(np.mean((x - y4) ** 2)) / np.std(x)
+    assert e5 < 0.06 and e5 < 0.6 * e4, (e5, e4)
+    blk = orc.quantize(orc.Q5_K, x).reshape(-1, 176)
+    hdr = blk[:, :4].copy().view(np.float16).astype(np.float64)
+    xs, ys = x.reshape(-1, 8, 32).astype(np.float64), y5.reshape(-1, 8, 32).astype(np.float64)
+    mn = np.minimum(xs.min(axis=2), 0.0)
+    scale = (xs.max(axis=2) - mn) / 31
+    import ctypes
+    for k in range(xs.shape[0]):
+        s12 = (ctypes.c_uint8 * 12).from_buffer_copy(blk[k, 4:16].tobytes())
+        for j in range(8):
+            a, b = ctypes.c_int(), ctypes.c_int()
+            orc.lib().orc_q4k_scale_min(ctypes.addressof(s12), j, ctypes.addressof(a), ctypes.addressof(b))
+            dl, ml = hdr[k, 0] * a.value, hdr[k, 1] * b.value
+            bound = 0.5 * dl + 31 * abs(scale[k, j] - dl) + 2 * abs(ml + mn[k, j]) + 1e-7
+            assert np.max(np.abs(xs[k, j] - ys[k, j])) <= bound
