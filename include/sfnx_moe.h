@@ -17,7 +17,9 @@
  *         header planes.
  *   Q8_0: an int8 plane of R x C bytes (16-byte halves of each 512-byte run ordered [half][block]), then an f16 scale
  *         plane of R x C/32.
- * Every plane is tiled by rows (32 for the K-quants, 4 for Q8_0): piece p of a row lies one tile's pieces after piece
+ *   Q4_0: a nibble plane of R x C/2 (a block's 16 quant bytes as one piece), then an f16 d plane of R x C/16.
+ *   Q5_1: a nibble plane of R x C/2, then a (f16 d, f16 m) plane of R x C/8, then a qh plane of R x C/8.
+ * Every plane is tiled by rows (32 for the K-quants, 4 for the 32-value block types): piece p of a row lies one tile's pieces after piece
  * p - 1, so a wavefront's 16-byte loads over a tile's rows cover whole 128-byte lines.  The planar matrix has exactly
  * the GGUF matrix's size; experts sit at base + e * stride.  C % 512 == 0, R % 32 == 0.
  */
@@ -34,7 +36,7 @@ extern "C" {
 #define SFNX_MAXT 16     /* rows of a decode window (src/model.hpp:48 MAXT) */
 #define SFNX_PF_JOB 64   /* rows of a prompt-path job (src/kernels.hpp:26 PF_JOB) */
 
-enum { SFNX_Q8_0 = 8, SFNX_Q4_K = 12, SFNX_Q5_K = 13 }; /* GgmlType ids, src/gguf.hpp:22-25 (Q5_K: ggml's 13) */
+enum { SFNX_Q4_0 = 2, SFNX_Q5_1 = 7, SFNX_Q8_0 = 8, SFNX_Q4_K = 12, SFNX_Q5_K = 13 }; /* GgmlType ids (src/gguf.hpp:22-25; the others ggml's) */
 
 /* src/kernels.hpp:18-23: one expert's matrix applied to up to SFNX_MAXT activation rows */
 typedef struct sfnx_job {

@@ -223,6 +223,100 @@ void orc_quantize_q8_0(const float* x, void* dst, int64_t rows, int cols) {
     }
 }
 
+/* tools/mtp_experts.py:29-41: d = (the first value of largest magnitude) / -8, q = min(15, trunc(x / d + 8.5)) with
+ * 1 / d in fp32 from the unrounded d; f16 d, then value l in the low nibble of byte l, value l + 16 in its high nibble */
+void orc_quantize_q4_0(const float* x, void* dst, int64_t rows, int cols) {
+    const int64_t nblk = rows * (cols / 32);
+#pragma omp parallel for schedule(static)
+    for (int64_t k = 0; k < nblk; ++k) {
+        const float* v = x + 32 * k;
+        uint8_t* b = (uint8_t*) dst + k * ORC_Q40_BYTES;
+        float amax = fabsf(v[0]), mx = v[0];   /* the first value of largest magnitude (numpy's argmax) */
+        for (int l = 1; l < 32; ++l)
+            if (fabsf(v[l]) > amax) {
+                amax = fabsf(v[l]);
+                mx = v[l];
+            }
+        const float d = mx / -8.0f, idv = d != 0.f ? 1.0f / d : 0.f;
+        const uint16_t dh = orc_f32_to_f16(d);
+        memcpy(b, &dh, 2);
+        for (int l = 0; l < 16; ++l) {
+            const float a = truncf(v[l] * idv + 8.5f), c = truncf(v[l + 16] * idv + 8.5f);
+            const int q0 = (int) (a < 15.f ? a : 15.f), q1 = (int) (c < 15.f ? c : 15.f);
+            b[2 + l] = (uint8_t) (q0 | (q1 << 4));
+        }
+    }
+}
+
+/* Q5_1 (ggml block_q5_1, 24 bytes: f16 d, f16 m, u32 qh, 16 bytes qs): the library's quantizer, ggml's closed form:
+ * m = min, d = (max - min) / 31, q = trunc((x - m) / d + 0.5) with 1 / d in fp32; value l's fifth bit is qh bit l */
+void orc_quantize_q5_1(const float* x, void* dst, int64_t rows, int cols) {
+    const int64_t nblk = rows * (cols / 32);
+#pragma omp parallel for schedule(static)
+    for (int64_t k = 0; k < nblk; ++k) {
+        const float* v = x + 32 * k;
+        uint8_t* b = (uint8_t*) dst + k * ORC_Q51_BYTES;
+        float mn = v[0], mx = v[0];
+        for (int l = 1; l < 32; ++l) {
+            if (v[l] < mn) mn = v[l];
+            if (v[l] > mx) mx = v[l];
+        }
+        const float d = (mx - mn) / 31.0f, idv = d != 0.f ? 1.0f / d : 0.f;
+        const uint16_t dh = orc_f32_to_f16(d), mh = orc_f32_to_f16(mn);
+        memcpy(b, &dh, 2);
+        memcpy(b + 2, &mh, 2);
+        uint32_t qh = 0;
+        for (int l = 0; l < 16; ++l) {
+            const int q0 = (int) truncf((v[l] - mn) * idv + 0.5f), q1 = (int) truncf((v[l + 16] - mn) * idv + 0.5f);
+            b[8 + l] = (uint8_t) ((q0 & 15) | ((q1 & 15) << 4));
+            qh |= (uint32_t) ((q0 >> 4) & 1) << l;
+            qh |= (uint32_t) ((q1 >> 4) & 1) << (l + 16);
+        }
+        memcpy(b + 4, &qh, 4);
+    }
+}
+
+/* value l (0..31) of a Q4_0 (q - 8 comes later) or Q5_1 block */
+static inline int b32_value(const uint8_t* p, int type, int l) {
+    if (type == ORC_Q4_0) return l < 16 ? p[2 + l] & 15 : p[2 + l - 16] >> 4;
+    uint32_t qh;
+    memcpy(&qh, p + 4, 4);
+    const int nib = l < 16 ? p[8 + l] & 15 : p[8 + l - 16] >> 4;
+    return nib | (int) (((qh >> l) & 1) << 4);
+}
+static inline size_t b32_bytes(int type) { return type == ORC_Q4_0 ? ORC_Q40_BYTES : ORC_Q51_BYTES; }
+
+/* fp32: Q4_0 (q - 8) d; Q5_1 d q + m (ggml's dequantize_row_q4_0 / _q5_1) */
+static void dequant_b32(const void* src, float* y, int64_t rows, int cols, int type) {
+    const int64_t nblk = rows * (cols / 32);
+    for (int64_t k = 0; k < nblk; ++k) {
+        const uint8_t* p = (const uint8_t*) src + k * b32_bytes(type);
+        uint16_t dh, mh = 0;
+        memcpy(&dh, p, 2);
+        if (type == ORC_Q5_1) memcpy(&mh, p + 2, 2);
+        const float d = orc_f16_to_f32(dh), m = orc_f16_to_f32(mh);
+        for (int l = 0; l < 32; ++l)
+            y[32 * k + l] = type == ORC_Q4_0 ? (float) (b32_value(p, type, l) - 8) * d : d * (float) b32_value(p, type, l) + m;
+    }
+}
+/* f16: Q4_0 hmul2(q - 8, d); Q5_1 hfma2(q, d, m), src/moe_mma.cuh:137-173 */
+static void dequant_b32_f16(const void* src, uint16_t* y, int64_t rows, int cols, int type) {
+    const int64_t nblk = rows * (cols / 32);
+    for (int64_t k = 0; k < nblk; ++k) {
+        const uint8_t* p = (const uint8_t*) src + k * b32_bytes(type);
+        uint16_t dh, mh;
+        memcpy(&dh, p, 2);
+        memcpy(&mh, p + 2, 2);
+        for (int l = 0; l < 32; ++l)
+            y[32 * k + l] = type == ORC_Q4_0 ? orc_f16_mul(orc_f32_to_f16((float) (b32_value(p, type, l) - 8)), dh)
+                                             : orc_f16_fma(orc_f32_to_f16((float) b32_value(p, type, l)), dh, mh);
+    }
+}
+void orc_dequant_q4_0(const void* src, float* y, int64_t rows, int cols) { dequant_b32(src, y, rows, cols, ORC_Q4_0); }
+void orc_dequant_q4_0_f16(const void* src, uint16_t* y, int64_t rows, int cols) { dequant_b32_f16(src, y, rows, cols, ORC_Q4_0); }
+void orc_dequant_q5_1(const void* src, float* y, int64_t rows, int cols) { dequant_b32(src, y, rows, cols, ORC_Q5_1); }
+void orc_dequant_q5_1_f16(const void* src, uint16_t* y, int64_t rows, int cols) { dequant_b32_f16(src, y, rows, cols, ORC_Q5_1); }
+
 /* value l of sub-block j of a K-quant super-block (Q5_K: the fifth bit from qh[l] bit j) */
 static inline int kq_value(const uint8_t* p, int q5, int j, int l) {
     const uint8_t* qs = p + (q5 ? 48 : 16);
@@ -526,14 +620,57 @@ float orc_dot_q8_0(const uint8_t* wrow, const uint8_t* yq, int K) {
     return butterfly_sum(lane, 16);
 }
 
+/* Q4_0 / Q5_1 x q8_1: 16 lanes, lane l the blocks l + 16 i in order, then the xor butterfly (the Q8_0 lanes).  Per
+ * block, with s = the integer sum of the activation block's int8 values: Q4_0 (d_w d_a) (sum q a - 8 s), i.e. the
+ * exact integer sum (q - 8) a; Q5_1 (d_w d_a) sum q a + (m_w d_a) s.  (The reference's ggml vec_dot_q4_0_q8_1 /
+ * _q5_1_q8_1 use the f16 block sum of the activations instead of d_a s: their bits are parity unpinned; these forms
+ * are pinned by float64 products.) */
+static float dot_b32(const uint8_t* wrow, const uint8_t* yq, int K, int type) {
+    const int nb = K / 32;
+    float lane[16];
+    for (int l = 0; l < 16; ++l) {
+        float acc = 0.f;
+        for (int b = l; b < nb; b += 16) {
+            const uint8_t* w = wrow + (size_t) b * b32_bytes(type);
+            const uint8_t* a = yq + (size_t) b * ORC_Q81_BYTES;
+            uint16_t dw, mw, da;
+            memcpy(&dw, w, 2);
+            memcpy(&mw, w + 2, 2);
+            memcpy(&da, a, 2);
+            int si = 0, sa = 0;
+            for (int k = 0; k < 32; ++k) {
+                si += b32_value(w, type, k) * (int) (int8_t) a[4 + k];
+                sa += (int) (int8_t) a[4 + k];
+            }
+            const float dd = orc_f16_to_f32(dw) * orc_f16_to_f32(da);
+            if (type == ORC_Q4_0) acc += dd * (float) (si - 8 * sa);
+            else acc += dd * (float) si + (orc_f16_to_f32(mw) * orc_f16_to_f32(da)) * (float) sa;
+        }
+        lane[l] = acc;
+    }
+    return butterfly_sum(lane, 16);
+}
+float orc_dot_q4_0(const uint8_t* wrow, const uint8_t* yq, int K) { return dot_b32(wrow, yq, K, ORC_Q4_0); }
+float orc_dot_q5_1(const uint8_t* wrow, const uint8_t* yq, int K) { return dot_b32(wrow, yq, K, ORC_Q5_1); }
+
 float orc_dot(int type, const uint8_t* wrow, const uint8_t* yq, int K) {
-    return type == ORC_Q4_K ? orc_dot_q4_k(wrow, yq, K) : type == ORC_Q5_K ? orc_dot_q5_k(wrow, yq, K) : orc_dot_q8_0(wrow, yq, K);
+    switch (type) {
+        case ORC_Q4_K: return orc_dot_q4_k(wrow, yq, K);
+        case ORC_Q5_K: return orc_dot_q5_k(wrow, yq, K);
+        case ORC_Q4_0: return orc_dot_q4_0(wrow, yq, K);
+        case ORC_Q5_1: return orc_dot_q5_1(wrow, yq, K);
+        default: return orc_dot_q8_0(wrow, yq, K);
+    }
 }
 
 static size_t row_bytes(int type, int cols) {
-    return type == ORC_Q4_K ? (size_t) cols / 256 * ORC_Q4K_BYTES
-           : type == ORC_Q5_K ? (size_t) cols / 256 * ORC_Q5K_BYTES
-                              : (size_t) cols / 32 * ORC_Q80_BYTES;
+    switch (type) {
+        case ORC_Q4_K: return (size_t) cols / 256 * ORC_Q4K_BYTES;
+        case ORC_Q5_K: return (size_t) cols / 256 * ORC_Q5K_BYTES;
+        case ORC_Q4_0: return (size_t) cols / 32 * ORC_Q40_BYTES;
+        case ORC_Q5_1: return (size_t) cols / 32 * ORC_Q51_BYTES;
+        default: return (size_t) cols / 32 * ORC_Q80_BYTES;
+    }
 }
 
 /* ------------------------------------------------------------------------------------------------ the layer */
@@ -602,6 +739,8 @@ void orc_mma_matvec(const uint8_t* w, int type, int n_in, int n_out, const uint1
     for (int r = 0; r < n_out; ++r) {
         if (type == ORC_Q4_K) orc_dequant_q4_k_f16(w + (size_t) r * rb, row, 1, n_in);
         else if (type == ORC_Q5_K) orc_dequant_q5_k_f16(w + (size_t) r * rb, row, 1, n_in);
+        else if (type == ORC_Q4_0) orc_dequant_q4_0_f16(w + (size_t) r * rb, row, 1, n_in);
+        else if (type == ORC_Q5_1) orc_dequant_q5_1_f16(w + (size_t) r * rb, row, 1, n_in);
         else orc_dequant_q8_0_f16(w + (size_t) r * rb, row, 1, n_in);
         double s = 0.0;
         for (int k = 0; k < n_in; ++k) s += (double) orc_f16_to_f32(row[k]) * (double) orc_f16_to_f32(x16[k]);

@@ -22,10 +22,12 @@
 extern "C" {
 #endif
 
-enum { ORC_Q8_0 = 8, ORC_Q4_K = 12, ORC_Q5_K = 13 };   /* GgmlType ids, src/gguf.hpp:22-25; Q5_K is ggml's 13 */
+enum { ORC_Q4_0 = 2, ORC_Q5_1 = 7, ORC_Q8_0 = 8, ORC_Q4_K = 12, ORC_Q5_K = 13 };   /* GgmlType ids (src/gguf.hpp:22-25; the others ggml's) */
 #define ORC_QK_K 256
 #define ORC_Q4K_BYTES 144
 #define ORC_Q5K_BYTES 176
+#define ORC_Q40_BYTES 18
+#define ORC_Q51_BYTES 24
 #define ORC_Q80_BYTES 34
 #define ORC_Q81_BYTES 36
 #define ORC_MAXT 16
@@ -58,6 +60,15 @@ void orc_quantize_q8_0(const float* x, void* dst, int64_t rows, int cols);
 void orc_quantize_q5_k(const float* x, void* dst, int64_t rows, int cols);
 void orc_dequant_q5_k(const void* src, float* y, int64_t rows, int cols);
 void orc_dequant_q5_k_f16(const void* src, uint16_t* y, int64_t rows, int cols);
+/* Q4_0 (18 bytes: f16 d, value l in the low nibble of byte l, l + 16 in its high nibble; (q - 8) d), quantizer
+ * tools/mtp_experts.py:29-41.  Q5_1 (24 bytes: f16 d, f16 m, u32 qh, 16 nibble bytes; d q + m, the fifth bit of value
+ * l is qh bit l), the library's quantizer in ggml's closed form. */
+void orc_quantize_q4_0(const float* x, void* dst, int64_t rows, int cols);
+void orc_quantize_q5_1(const float* x, void* dst, int64_t rows, int cols);
+void orc_dequant_q4_0(const void* src, float* y, int64_t rows, int cols);
+void orc_dequant_q4_0_f16(const void* src, uint16_t* y, int64_t rows, int cols);
+void orc_dequant_q5_1(const void* src, float* y, int64_t rows, int cols);
+void orc_dequant_q5_1_f16(const void* src, uint16_t* y, int64_t rows, int cols);
 
 /* get_scale_min_k4: src/moe_q4k.cuh:15-23, tools/moe_mma_bench.cu:44-52 */
 void orc_q4k_scale_min(const uint8_t* scales12, int j, int* sc, int* m);
@@ -103,6 +114,9 @@ float orc_dot_q8_0(const uint8_t* wrow, const uint8_t* yq, int K);
 /* Q5_K x q8_1: the Q4_K lane order and combine on 5-bit values (the reference's Q5_K decode dot is ggml's
  * vec_dot_q5_K_q8_1, not vendored: its order is parity unpinned; this form is pinned by float64 products) */
 float orc_dot_q5_k(const uint8_t* wrow, const uint8_t* yq, int K);
+/* Q4_0 / Q5_1 x q8_1: the Q8_0 lanes; per block (d_w d_a) sum (q - 8) a, or (d_w d_a) sum q a + (m_w d_a) sum a */
+float orc_dot_q4_0(const uint8_t* wrow, const uint8_t* yq, int K);
+float orc_dot_q5_1(const uint8_t* wrow, const uint8_t* yq, int K);
 float orc_dot(int type, const uint8_t* wrow, const uint8_t* yq, int K);
 
 /* k_moe_h, src/moe.cuh:284-295: h = silu(gate) * up of one [gate (ff) | up (ff)] row, as q8_1 */

@@ -14,8 +14,9 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "_build" / "liborc.so"
 
-Q8_0, Q4_K, Q5_K = 8, 12, 13
-Q4K_BYTES, Q5K_BYTES, Q80_BYTES, Q81_BYTES = 144, 176, 34, 36
+Q4_0, Q5_1, Q8_0, Q4_K, Q5_K = 2, 7, 8, 12, 13
+Q4K_BYTES, Q5K_BYTES, Q40_BYTES, Q51_BYTES, Q80_BYTES, Q81_BYTES = 144, 176, 18, 24, 34, 36
+NAMES = {Q4_0: 'q4_0', Q5_1: 'q5_1', Q8_0: 'q8_0', Q4_K: 'q4_k', Q5_K: 'q5_k'}
 MAXT, PF_JOB = 16, 64
 
 JOB_DTYPE = np.dtype([("w", "<i4"), ("n", "<i4"), ("y", "<i4", MAXT), ("out", "<i4", MAXT)])
@@ -60,6 +61,14 @@ def lib() -> C.CDLL:
             "orc_dequant_q5_k": (None, [vp, vp, i64, i32]),
             "orc_dequant_q5_k_f16": (None, [vp, vp, i64, i32]),
             "orc_dot_q5_k": (f32, [vp, vp, i32]),
+            "orc_quantize_q4_0": (None, [vp, vp, i64, i32]),
+            "orc_dequant_q4_0": (None, [vp, vp, i64, i32]),
+            "orc_dequant_q4_0_f16": (None, [vp, vp, i64, i32]),
+            "orc_dot_q4_0": (f32, [vp, vp, i32]),
+            "orc_quantize_q5_1": (None, [vp, vp, i64, i32]),
+            "orc_dequant_q5_1": (None, [vp, vp, i64, i32]),
+            "orc_dequant_q5_1_f16": (None, [vp, vp, i64, i32]),
+            "orc_dot_q5_1": (f32, [vp, vp, i32]),
             "orc_q4k_scale_min": (None, [vp, i32, vp, vp]),
             "orc_dequant_q4_k": (None, [vp, vp, i64, i32]),
             "orc_dequant_q4_k_f16": (None, [vp, vp, i64, i32]),
@@ -94,10 +103,14 @@ def _p(a: np.ndarray | None):
 
 
 def row_bytes(t: int, cols: int) -> int:
-    return {Q4_K: cols // 256 * Q4K_BYTES, Q5_K: cols // 256 * Q5K_BYTES}.get(t, cols // 32 * Q80_BYTES)
+    return {Q4_K: cols // 256 * Q4K_BYTES, Q5_K: cols // 256 * Q5K_BYTES, Q4_0: cols // 32 * Q40_BYTES,
+            Q5_1: cols // 32 * Q51_BYTES}.get(t, cols // 32 * Q80_BYTES)
 
 
 def _by_type(t: int, q4k: str, q5k: str, q80: str):
+    """the oracle function for type t (the names given are the K-quant / Q8_0 ones; Q4_0 / Q5_1 follow their pattern)"""
+    if t in (Q4_0, Q5_1):
+        return getattr(lib(), q80.replace("q8_0", NAMES[t]))
     return getattr(lib(), {Q4_K: q4k, Q5_K: q5k}.get(t, q80))
 
 

@@ -13,7 +13,7 @@ PKG = Path(__file__).resolve().parent
 LIB_PATH = Path(os.environ.get("SFNX_LIB", PKG / "libsfnx_moe.so"))   # SFNX_LIB: a library built elsewhere
 HEADER = PKG.parent / "include" / "sfnx_moe.h"
 
-Q8_0, Q4_K, Q5_K = 8, 12, 13
+Q4_0, Q5_1, Q8_0, Q4_K, Q5_K = 2, 7, 8, 12, 13
 MAXT, PF_JOB = 16, 64
 JOB_INTS = 2 + 2 * MAXT        # sfnx_job: w, n, y[16], out[16]
 BIGJOB_INTS = 2 + 2 * PF_JOB   # sfnx_bigjob

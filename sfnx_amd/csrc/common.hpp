@@ -13,7 +13,7 @@
 namespace sfnx {
 
 constexpr int WAVE = 64;
-constexpr int Q4K_BYTES = 144, Q5K_BYTES = 176, Q80_BYTES = 34, Q81_BYTES = 36;
+constexpr int Q4K_BYTES = 144, Q5K_BYTES = 176, Q40_BYTES = 18, Q51_BYTES = 24, Q80_BYTES = 34, Q81_BYTES = 36;
 
 // ------------------------------------------------------------------------------------------------ errors
 void set_error(const std::string& msg);
@@ -198,17 +198,51 @@ struct Q80Planes {
         return reinterpret_cast<const uint16_t*>(d16(r, C, b / 8) + 2 * (b % 8));
     }
 };
+// Q4_0 / Q5_1 (tiled like Q8_0, by 4 rows): a nibble plane of R x C/2 (one 16-byte piece a block: value l in the low
+// nibble of byte l, l + 16 in its high nibble), then Q4_0: an f16 d plane of R x C/16; Q5_1: a (d, m) plane of R x C/8
+// and a qh plane of R x C/8 (4 bytes a block each)
+struct NbPlanes {
+    const uint8_t* q;
+    const uint8_t* s;    // Q4_0: d; Q5_1: (d, m)
+    const uint8_t* qh;   // Q5_1
+    __host__ __device__ __forceinline__ const uint8_t* q16(int r, int C, int p) const { return q + tiled16<Q80_RT>(r, C / 2, p); }
+    // Q4_0: block b's f16 d
+    __host__ __device__ __forceinline__ const uint8_t* d_of(int r, int C, int b) const {
+        return s + tiled16<Q80_RT>(r, C / 16, b / 8) + 2 * (b % 8);
+    }
+    // Q5_1: block b's (d, m) and its qh word; 4 blocks a piece
+    __host__ __device__ __forceinline__ const uint8_t* dm_of(int r, int C, int b) const {
+        return s + tiled16<Q80_RT>(r, C / 8, b / 4) + 4 * (b % 4);
+    }
+    __host__ __device__ __forceinline__ const uint8_t* qh_of(int r, int C, int b) const {
+        return qh + tiled16<Q80_RT>(r, C / 8, b / 4) + 4 * (b % 4);
+    }
+};
+template <int TYPE> __host__ __device__ __forceinline__ NbPlanes nb_planes(const void* mat, int R, int C) {
+    const uint8_t* p = (const uint8_t*) mat;
+    const size_t q = (size_t) R * (C / 2), s = TYPE == SFNX_Q4_0 ? (size_t) R * (C / 16) : (size_t) R * (C / 8);
+    return NbPlanes{p, p + q, p + q + s};
+}
+
 __host__ __device__ __forceinline__ Q80Planes q80_planes(const void* mat, int R, int C) {
     const uint8_t* p = (const uint8_t*) mat;
     return Q80Planes{p, p + (size_t) R * C};
 }
 
-inline bool expert_type_ok(uint32_t type) { return type == SFNX_Q4_K || type == SFNX_Q5_K || type == SFNX_Q8_0; }
-inline int block_values(uint32_t type) { return type == SFNX_Q8_0 ? 32 : 256; }
-inline size_t row_bytes(uint32_t type, int cols) {
-    return type == SFNX_Q4_K ? (size_t) cols / 256 * Q4K_BYTES
-           : type == SFNX_Q5_K ? (size_t) cols / 256 * Q5K_BYTES
-                               : (size_t) cols / 32 * Q80_BYTES;
+inline bool expert_type_ok(uint32_t type) {
+    return type == SFNX_Q4_K || type == SFNX_Q5_K || type == SFNX_Q8_0 || type == SFNX_Q4_0 || type == SFNX_Q5_1;
+}
+constexpr const char* TYPE_MSG = "expert type must be Q4_0 (2), Q5_1 (7), Q8_0 (8), Q4_K (12) or Q5_K (13)";
+__host__ __device__ constexpr bool is_kquant(uint32_t type) { return type == SFNX_Q4_K || type == SFNX_Q5_K; }
+inline int block_values(uint32_t type) { return is_kquant(type) ? 256 : 32; }
+__host__ __device__ inline size_t row_bytes(uint32_t type, int cols) {
+    switch (type) {
+        case SFNX_Q4_K: return (size_t) cols / 256 * Q4K_BYTES;
+        case SFNX_Q5_K: return (size_t) cols / 256 * Q5K_BYTES;
+        case SFNX_Q4_0: return (size_t) cols / 32 * Q40_BYTES;
+        case SFNX_Q5_1: return (size_t) cols / 32 * Q51_BYTES;
+        default: return (size_t) cols / 32 * Q80_BYTES;
+    }
 }
 
 }  // namespace sfnx

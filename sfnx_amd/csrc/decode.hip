@@ -38,7 +38,7 @@ __device__ unsigned long long g_blk[3][1024][2];   // every block's first and la
 
 constexpr int D1_THREADS = 128, D1_WAVES = D1_THREADS / WAVE;   // K1: a router row per wavefront
 constexpr int D3_THREADS = 256, D3_ROWS = 8;                    // K3: output rows per block
-template <int TYPE> constexpr int lpr_of() { return TYPE == SFNX_Q8_0 ? 16 : 8; }
+template <int TYPE> constexpr int lpr_of() { return is_kquant(TYPE) ? 8 : 16; }
 template <int TYPE> constexpr int d2_threads() { return 32 * lpr_of<TYPE>(); }   // K2: 32 FF indices a block
 
 struct DecLayout {
@@ -161,6 +161,24 @@ template <int G> struct RowOf<SFNX_Q5_K, G> {
     }
     static __device__ __forceinline__ void issue(R& w, const uint8_t* mat, int nrows, int row, int C, int ln) {
         w.issue(q5k_planes(mat, nrows, C), row, C, ln);
+    }
+};
+template <int G> struct RowOf<SFNX_Q4_0, G> {
+    using R = NbRow<G, SFNX_Q4_0>;
+    static __device__ __forceinline__ void load(R& w, const uint8_t* mat, int nrows, int row, int C, int ln) {
+        w.load(nb_planes<SFNX_Q4_0>(mat, nrows, C), row, C, ln);
+    }
+    static __device__ __forceinline__ void issue(R& w, const uint8_t* mat, int nrows, int row, int C, int ln) {
+        w.issue(nb_planes<SFNX_Q4_0>(mat, nrows, C), row, C, ln);
+    }
+};
+template <int G> struct RowOf<SFNX_Q5_1, G> {
+    using R = NbRow<G, SFNX_Q5_1>;
+    static __device__ __forceinline__ void load(R& w, const uint8_t* mat, int nrows, int row, int C, int ln) {
+        w.load(nb_planes<SFNX_Q5_1>(mat, nrows, C), row, C, ln);
+    }
+    static __device__ __forceinline__ void issue(R& w, const uint8_t* mat, int nrows, int row, int C, int ln) {
+        w.issue(nb_planes<SFNX_Q5_1>(mat, nrows, C), row, C, ln);
     }
 };
 template <int G> struct RowOf<SFNX_Q8_0, G> {
@@ -690,7 +708,7 @@ void launch_k2_tt1(const DecArgs& d, const sfnx_moe_layer_w& w, const DecLayout&
 }
 template <int TYPE, int G2>
 void launch_k3_one(const DecArgs& d, const sfnx_moe_layer_w& w, float* x, const DecLayout& L, char* ws, hipStream_t s) {
-    constexpr int NB = TYPE == SFNX_Q8_0 ? 6 : 3;   // 11 jobs x 8 rows in one batch
+    constexpr int NB = is_kquant(TYPE) ? 3 : 6;   // 11 jobs x 8 rows in one batch
     launch(2, k_dec_down1<TYPE, G2, NB>, dim3(d.H / D3_ROWS), dim3(D3_THREADS), acts_bytes(d.K + 1, d.ff), s,
         (const uint8_t*) w.dn, w.dn_stride, d.H, d.E, d.K, d.ff, d.shared, (const float*) (ws + L.logits),
         (const int*) (ws + L.topi), (const float*) (ws + L.topw), (const int8_t*) (ws + L.hq_q),
@@ -731,7 +749,13 @@ void launch_layer_tt(const DecArgs& d, const sfnx_moe_layer_w& w, float* x, cons
         default: throw std::runtime_error("hidden size must be 1024, 2048, 2560 or 4096"); \
     }
     if (d.phases & 2) {
-        if (d.type == SFNX_Q4_K) { SFNX_K2(SFNX_Q4_K) } else if (d.type == SFNX_Q5_K) { SFNX_K2(SFNX_Q5_K) } else { SFNX_K2(SFNX_Q8_0) }
+        switch (d.type) {
+            case SFNX_Q4_K: SFNX_K2(SFNX_Q4_K) break;
+            case SFNX_Q5_K: SFNX_K2(SFNX_Q5_K) break;
+            case SFNX_Q4_0: SFNX_K2(SFNX_Q4_0) break;
+            case SFNX_Q5_1: SFNX_K2(SFNX_Q5_1) break;
+            default: SFNX_K2(SFNX_Q8_0) break;
+        }
     }
 #undef SFNX_K2
     // down tasks a lane group loads together: every job's 8 rows in one batch at T = 1
@@ -743,6 +767,12 @@ void launch_layer_tt(const DecArgs& d, const sfnx_moe_layer_w& w, float* x, cons
     } else if (d.type == SFNX_Q5_K) {
         if (d.ff == 512) launch_k3<SFNX_Q5_K, 1, NB>(d, w, x, L, ws, s);
         else launch_k3<SFNX_Q5_K, 2, NB>(d, w, x, L, ws, s);
+    } else if (d.type == SFNX_Q4_0) {
+        if (d.ff == 512) launch_k3<SFNX_Q4_0, 1, NB>(d, w, x, L, ws, s);
+        else launch_k3<SFNX_Q4_0, 2, NB>(d, w, x, L, ws, s);
+    } else if (d.type == SFNX_Q5_1) {
+        if (d.ff == 512) launch_k3<SFNX_Q5_1, 1, NB>(d, w, x, L, ws, s);
+        else launch_k3<SFNX_Q5_1, 2, NB>(d, w, x, L, ws, s);
     } else {
         if (d.ff == 512) launch_k3<SFNX_Q8_0, 1, NB>(d, w, x, L, ws, s);
         else launch_k3<SFNX_Q8_0, 2, NB>(d, w, x, L, ws, s);
@@ -798,13 +828,13 @@ extern "C" int sfnx_moe_decode(const sfnx_moe_layer_w* layers, int n_layers, uin
                                int shared, float* x, int T, int norm, float eps, void* ws, size_t ws_bytes, int phases,
                                void* st) {
     return guarded("sfnx_moe_decode", [&] {
-        require(expert_type_ok(type), "expert type must be Q4_K (12), Q5_K (13) or Q8_0 (8)");
+        require(expert_type_ok(type), TYPE_MSG);
         require(T >= 1 && T <= SFNX_MAXT, "T out of range (1..16)");
         require(E >= WAVE && E % WAVE == 0 && E <= MAX_E, "E must be a multiple of 64, at most 1024");
         require(K >= 1 && K <= MAX_K && K <= E, "K out of range (1..16)");
         require(H == 1024 || H == 2048 || H == 2560 || H == 4096, "hidden size must be 1024, 2048, 2560 or 4096");
         require(ff == 512 || ff == 1024, "FF must be 512 or 1024");
-        require(T * K <= (type == SFNX_Q8_0 ? 512 : 256), "T K picks exceed the block");
+        require(T * K <= (is_kquant(type) ? 256 : 512), "T K picks exceed the block");
         const DecLayout L = dec_layout(T, H, E, K, ff);
         require(ws != nullptr && ws_bytes >= L.total, "workspace smaller than sfnx_moe_decode_workspace()");
         require(n_layers >= 0 && (n_layers == 0 || layers != nullptr), "no layers");

@@ -7,7 +7,10 @@
 //   Q4_K: 8 lanes a row, lane l8 the 64-value groups l8 + 8 i in order (src/moe_q4k.cuh:30-86), each group
 //         d (d8l (sc0 dl) + d8h (sc1 dh)) - dmin (d8l (m0 sl) + d8h (m1 sh)), then xor 4, 2, 1 (src/moe.cuh:224-235).
 //   Q5_K: as Q4_K on the 5-bit values.
+//   Q4_0 / Q5_1: the Q8_0 lanes; per block (d_w d_a) sum (q - 8) a, or (d_w d_a) sum q a + (m_w d_a) sum a.
 //   Q8_0: 16 lanes a row, lane l16 the 32-blocks l16 + 16 i in order, each (d_w d_a) sum(q_w q_a), then xor 8 .. 1.
+#include <type_traits>
+
 #include "mv.hpp"
 
 namespace sfnx {
@@ -22,7 +25,7 @@ template <int TYPE, int G, int TT, bool DOWN, typename J>
 __global__ void __launch_bounds__(MV_THREADS) k_moe_mv(const uint8_t* __restrict__ A, size_t sa, int R, int C,
                                                       const J* __restrict__ jobs, const int* __restrict__ njobs,
                                                       const void* __restrict__ in, float* __restrict__ out) {
-    constexpr int LPR = TYPE == SFNX_Q8_0 ? 16 : 8, RPB = MV_THREADS / LPR;
+    constexpr int LPR = is_kquant(TYPE) ? 8 : 16, RPB = MV_THREADS / LPR;
     const int ji = blockIdx.y;
     if (ji >= *njobs) return;
     extern __shared__ __align__(16) unsigned char lds[];
@@ -34,8 +37,13 @@ __global__ void __launch_bounds__(MV_THREADS) k_moe_mv(const uint8_t* __restrict
     const uint8_t* mat = A + (size_t) jb.w * sa;
     const Acts a = acts_in(lds, TT, C);
     if constexpr (TYPE != SFNX_Q8_0) {
-        Q4kRow<G, TYPE == SFNX_Q5_K> w;
-        if (live) w.load(kq_planes<TYPE == SFNX_Q5_K>(mat, R, C), row, C, ln);
+        using Row = std::conditional_t<is_kquant(TYPE), Q4kRow<G, TYPE == SFNX_Q5_K>, NbRow<G, TYPE>>;
+        Row w;
+        if constexpr (is_kquant(TYPE)) {
+            if (live) w.load(kq_planes<TYPE == SFNX_Q5_K>(mat, R, C), row, C, ln);
+        } else {
+            if (live) w.load(nb_planes<TYPE>(mat, R, C), row, C, ln);
+        }
         for (int j0 = 0; j0 < jb.n; j0 += TT) {
             const int nn = min(TT, jb.n - j0);
             if (j0) __syncthreads();
@@ -80,7 +88,7 @@ void launch_g(int G, dim3 grid, size_t lds, hipStream_t s, const uint8_t* A, siz
 template <bool DOWN, typename J>
 void moe_mv(uint32_t type, const void* A, size_t sa, int n_in, int n_out, const J* jobs, const int* njobs, int njobs_max,
             int T, const void* in, float* out, void* st) {
-    require(expert_type_ok(type), "expert type must be Q4_K (12), Q5_K (13) or Q8_0 (8)");
+    require(expert_type_ok(type), TYPE_MSG);
     require(n_in > 0 && n_in % 512 == 0, "expert input width must be a multiple of 512");
     require(n_out > 0, "expert rows must be positive");
     require(sa >= row_bytes(type, n_in) * (size_t) n_out, "expert stride smaller than a matrix");
@@ -90,7 +98,7 @@ void moe_mv(uint32_t type, const void* A, size_t sa, int n_in, int n_out, const 
     const int TT = T <= 1 ? 1 : T <= 4 ? 4 : 16;
     const size_t lds = acts_bytes(TT, n_in);
     require(lds <= 64 * 1024, "activation rows do not fit the LDS budget");
-    const int rpb = MV_THREADS / (type == SFNX_Q8_0 ? 16 : 8);
+    const int rpb = MV_THREADS / (is_kquant(type) ? 8 : 16);
     const dim3 grid((n_out + rpb - 1) / rpb, njobs_max);
     hipStream_t s = stream_of(st);
     const uint8_t* a = (const uint8_t*) A;
@@ -103,6 +111,14 @@ void moe_mv(uint32_t type, const void* A, size_t sa, int n_in, int n_out, const 
         if (TT == 1) SFNX_MV(SFNX_Q5_K, 1);
         else if (TT == 4) SFNX_MV(SFNX_Q5_K, 4);
         else SFNX_MV(SFNX_Q5_K, 16);
+    } else if (type == SFNX_Q4_0) {
+        if (TT == 1) SFNX_MV(SFNX_Q4_0, 1);
+        else if (TT == 4) SFNX_MV(SFNX_Q4_0, 4);
+        else SFNX_MV(SFNX_Q4_0, 16);
+    } else if (type == SFNX_Q5_1) {
+        if (TT == 1) SFNX_MV(SFNX_Q5_1, 1);
+        else if (TT == 4) SFNX_MV(SFNX_Q5_1, 4);
+        else SFNX_MV(SFNX_Q5_1, 16);
     } else {
         if (TT == 1) SFNX_MV(SFNX_Q8_0, 1);
         else if (TT == 4) SFNX_MV(SFNX_Q8_0, 4);

@@ -93,6 +93,15 @@ template <> struct Chunk<SFNX_Q5_K> {
     static constexpr int STEPS = 4, LOADS = 6;
     uint4 q[4], hdr, qh;   // qh: the super-block's qh bytes 16 h .. 16 h + 15 (the fifth bits of the lane's values)
 };
+template <> struct Chunk<SFNX_Q4_0> {
+    static constexpr int STEPS = 4, LOADS = 5;
+    uint4 q[4];   // blocks 8 h + 4 c .. + 3 of the run
+    uint2 d;      // their four f16 d
+};
+template <> struct Chunk<SFNX_Q5_1> {
+    static constexpr int STEPS = 4, LOADS = 6;
+    uint4 q[4], dm, qh;   // the blocks' (f16 d, f16 m) and qh words
+};
 template <> struct Chunk<SFNX_Q8_0> {
     static constexpr int STEPS = 2, LOADS = 5;
     uint4 qa[2], qb[2];
@@ -113,6 +122,19 @@ __device__ __forceinline__ ChunkAt chunk_at(const Chunk<SFNX_Q5_K>*, const uint8
     const KqPlanes P = q5k_planes(mat, R, C);
     return ChunkAt{P.nib16(row, C, 16 * r + 8 * h + 4 * c), P.hdr16(row, C, 2 * r + c), P.qh16(row, C, 2 * (2 * r + c) + h)};
 }
+// Q4_0 / Q5_1: step s of chunk c of run r, lane-half h is block 16 r + 8 h + 4 c + s of the row
+template <int TYPE> __device__ __forceinline__ ChunkAt chunk_at_nb(const uint8_t* mat, int R, int C, int row, int r, int c, int h) {
+    const NbPlanes P = nb_planes<TYPE>(mat, R, C);
+    const int kb = 16 * r + 8 * h + 4 * c;
+    if constexpr (TYPE == SFNX_Q4_0) return ChunkAt{P.q16(row, C, kb), P.d_of(row, C, kb), nullptr};
+    else return ChunkAt{P.q16(row, C, kb), P.dm_of(row, C, kb), P.qh_of(row, C, kb)};
+}
+__device__ __forceinline__ ChunkAt chunk_at(const Chunk<SFNX_Q4_0>*, const uint8_t* mat, int R, int C, int row, int r, int c, int h) {
+    return chunk_at_nb<SFNX_Q4_0>(mat, R, C, row, r, c, h);
+}
+__device__ __forceinline__ ChunkAt chunk_at(const Chunk<SFNX_Q5_1>*, const uint8_t* mat, int R, int C, int row, int r, int c, int h) {
+    return chunk_at_nb<SFNX_Q5_1>(mat, R, C, row, r, c, h);
+}
 __device__ __forceinline__ ChunkAt chunk_at(const Chunk<SFNX_Q8_0>*, const uint8_t* mat, int R, int C, int row, int r, int c, int h) {
     const Q80Planes P = q80_planes(mat, R, C);
     return ChunkAt{P.q16(row, C, 32 * r + 8 * h + 2 * c), P.d16(row, C, 2 * r + h) + 4 * c, nullptr};
@@ -123,6 +145,12 @@ __device__ __forceinline__ void load_piece(Chunk<SFNX_Q4_K>& w, const ChunkAt& a
 __device__ __forceinline__ void load_piece(Chunk<SFNX_Q5_K>& w, const ChunkAt& a, int s) {
     w.q[s] = *reinterpret_cast<const uint4*>(a.q + PIECE_STRIDE * s);
 }
+__device__ __forceinline__ void load_piece(Chunk<SFNX_Q4_0>& w, const ChunkAt& a, int s) {
+    w.q[s] = *reinterpret_cast<const uint4*>(a.q + Q80_RT * 16 * s);
+}
+__device__ __forceinline__ void load_piece(Chunk<SFNX_Q5_1>& w, const ChunkAt& a, int s) {
+    w.q[s] = *reinterpret_cast<const uint4*>(a.q + Q80_RT * 16 * s);
+}
 __device__ __forceinline__ void load_piece(Chunk<SFNX_Q8_0>& w, const ChunkAt& a, int s) {
     w.qa[s] = *reinterpret_cast<const uint4*>(a.q + Q80_RT * 16 * s);
     w.qb[s] = *reinterpret_cast<const uint4*>(a.q + Q80_RT * 16 * (16 + s));   // the blocks' second halves
@@ -130,6 +158,11 @@ __device__ __forceinline__ void load_piece(Chunk<SFNX_Q8_0>& w, const ChunkAt& a
 __device__ __forceinline__ void load_tail(Chunk<SFNX_Q4_K>& w, const ChunkAt& a) { w.hdr = *reinterpret_cast<const uint4*>(a.tail); }
 __device__ __forceinline__ void load_tail(Chunk<SFNX_Q5_K>& w, const ChunkAt& a) {
     w.hdr = *reinterpret_cast<const uint4*>(a.tail);
+    w.qh = *reinterpret_cast<const uint4*>(a.qh);
+}
+__device__ __forceinline__ void load_tail(Chunk<SFNX_Q4_0>& w, const ChunkAt& a) { w.d = *reinterpret_cast<const uint2*>(a.tail); }
+__device__ __forceinline__ void load_tail(Chunk<SFNX_Q5_1>& w, const ChunkAt& a) {
+    w.dm = *reinterpret_cast<const uint4*>(a.tail);
     w.qh = *reinterpret_cast<const uint4*>(a.qh);
 }
 __device__ __forceinline__ void load_tail(Chunk<SFNX_Q8_0>& w, const ChunkAt& a) { w.d = *reinterpret_cast<const uint32_t*>(a.tail); }
@@ -160,6 +193,44 @@ __device__ __forceinline__ void dequant_step(const Chunk<SFNX_Q5_K>& w, int s, h
     const _Float16 d1h = (_Float16) (d * sc), nmh = (_Float16) (-(dmin * m));
     deq_q4k(w.q[s], half2v{d1l, d1l}, half2v{nml, nml}, half2v{d1h, d1h}, half2v{nmh, nmh}, b, &w.qh, 2 * s);
 }
+// Q4_0 / Q5_1: a block's 16 quant bytes (value l in the low nibble of byte l, l + 16 in the high) -> the 4 B
+// fragments, fragment c holding values 8 c .. 8 c + 7; Q4_0 hmul2(q - 8, d), Q5_1 hfma2(q, d, m) with the fifth bits
+template <int TYPE>
+__device__ __forceinline__ void deq_nb(const uint4& q, uint32_t dm, uint32_t qh, half8 (&b)[4]) {
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+    const half2v d = {__builtin_bit_cast(_Float16, (uint16_t) (dm & 0xffff)), __builtin_bit_cast(_Float16, (uint16_t) (dm & 0xffff))};
+    const half2v m = {__builtin_bit_cast(_Float16, (uint16_t) (dm >> 16)), __builtin_bit_cast(_Float16, (uint16_t) (dm >> 16))};
+    const half2v off = TYPE == SFNX_Q4_0 ? half2v{(_Float16) 1032.0f, (_Float16) 1032.0f} : half2v{(_Float16) 1024.0f, (_Float16) 1024.0f};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const bool hi = c >= 2;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const int wi = 2 * (c % 2) + p;   // the dword: values 4 wi .. 4 wi + 3 (+ 16 for the high nibbles)
+            uint32_t v = hi ? (w[wi] >> 4) & 0x0F0F0F0Fu : w[wi] & 0x0F0F0F0Fu;
+            if constexpr (TYPE == SFNX_Q5_1) v |= spread4(qh >> ((hi ? 16 : 0) + 4 * wi));
+            const half2v q01 = bytes_1024<0>(v) - off, q23 = bytes_1024<1>(v) - off;
+            half2v r01, r23;
+            if constexpr (TYPE == SFNX_Q4_0) {
+                r01 = q01 * d;
+                r23 = q23 * d;
+            } else {
+                r01 = __builtin_elementwise_fma(q01, d, m);
+                r23 = __builtin_elementwise_fma(q23, d, m);
+            }
+            b[c][4 * p + 0] = r01[0];
+            b[c][4 * p + 1] = r01[1];
+            b[c][4 * p + 2] = r23[0];
+            b[c][4 * p + 3] = r23[1];
+        }
+    }
+}
+__device__ __forceinline__ void dequant_step(const Chunk<SFNX_Q4_0>& w, int s, half8 (&b)[4]) {
+    deq_nb<SFNX_Q4_0>(w.q[s], (s < 2 ? w.d.x : w.d.y) >> (16 * (s % 2)), 0u, b);
+}
+__device__ __forceinline__ void dequant_step(const Chunk<SFNX_Q5_1>& w, int s, half8 (&b)[4]) {
+    deq_nb<SFNX_Q5_1>(w.q[s], (&w.dm.x)[s], (&w.qh.x)[s], b);
+}
 __device__ __forceinline__ void dequant_step(const Chunk<SFNX_Q8_0>& w, int s, half8 (&b)[4]) {
     const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t) (w.d >> (16 * s)));
     deq_q80(w.qa[s], w.qb[s], half2v{d, d}, b);
@@ -167,7 +238,7 @@ __device__ __forceinline__ void dequant_step(const Chunk<SFNX_Q8_0>& w, int s, h
 
 // column (within the run's 512) where MFMA k-chunk c of step j starts for lane-half h
 template <int TYPE> __device__ __forceinline__ int run_col(int j, int c, int h) {
-    if constexpr (TYPE != SFNX_Q8_0) return 64 * j + (c < 2 ? 16 * h + 8 * c : 32 + 16 * h + 8 * (c - 2));
+    if constexpr (is_kquant(TYPE)) return 64 * j + (c < 2 ? 16 * h + 8 * c : 32 + 16 * h + 8 * (c - 2));
     else return 256 * h + 32 * j + 8 * c;
 }
 
@@ -429,7 +500,7 @@ constexpr size_t MM_LDS = 2 * MM_XBUF * sizeof(_Float16);
 
 void moe_mma(uint32_t type, const void* A, size_t sa, int n_in, int n_out, const sfnx_bigjob* jobs, const int* njobs,
              int njobs_cap, const void* x16, float* out, void* st) {
-    require(expert_type_ok(type), "expert type must be Q4_K (12), Q5_K (13) or Q8_0 (8)");
+    require(expert_type_ok(type), TYPE_MSG);
     require(n_in > 0 && n_in % 512 == 0, "expert input width must be a multiple of 512");
     require(n_out > 0 && n_out % DN_BM == 0, "expert rows must be a multiple of 256");
     require((n_out / DN_BM) % std::max(1, (n_out / DN_BM) / 2) == 0, "row groups must split evenly");
@@ -445,13 +516,17 @@ void moe_mma(uint32_t type, const void* A, size_t sa, int n_in, int n_out, const
         k_moe_mma<SFNX_Q4_K><<<grid, DN_THREADS, lds, s>>>((const uint8_t*) A, sa, n_out, n_in, G, jobs, njobs, (const _Float16*) x16, out);
     else if (type == SFNX_Q5_K)
         k_moe_mma<SFNX_Q5_K><<<grid, DN_THREADS, lds, s>>>((const uint8_t*) A, sa, n_out, n_in, G, jobs, njobs, (const _Float16*) x16, out);
+    else if (type == SFNX_Q4_0)
+        k_moe_mma<SFNX_Q4_0><<<grid, DN_THREADS, lds, s>>>((const uint8_t*) A, sa, n_out, n_in, G, jobs, njobs, (const _Float16*) x16, out);
+    else if (type == SFNX_Q5_1)
+        k_moe_mma<SFNX_Q5_1><<<grid, DN_THREADS, lds, s>>>((const uint8_t*) A, sa, n_out, n_in, G, jobs, njobs, (const _Float16*) x16, out);
     else
         k_moe_mma<SFNX_Q8_0><<<grid, DN_THREADS, lds, s>>>((const uint8_t*) A, sa, n_out, n_in, G, jobs, njobs, (const _Float16*) x16, out);
 }
 
 void moe_mma_gu(uint32_t type, const void* A, size_t sa, int n_in, int ff, const sfnx_bigjob* jobs, const int* njobs,
                 int njobs_cap, const void* x16, float* gu, uint16_t* h16, void* st) {
-    require(expert_type_ok(type), "expert type must be Q4_K (12), Q5_K (13) or Q8_0 (8)");
+    require(expert_type_ok(type), TYPE_MSG);
     require(n_in > 0 && n_in % 512 == 0, "expert input width must be a multiple of 512");
     require(ff > 0 && ff % MM_FF == 0, "FF must be a multiple of 256");
     require(sa >= row_bytes(type, n_in) * (size_t) (2 * ff), "expert stride smaller than a matrix");
@@ -464,6 +539,12 @@ void moe_mma_gu(uint32_t type, const void* A, size_t sa, int n_in, int ff, const
                                                                   (const _Float16*) x16, gu, (_Float16*) h16);
     else if (type == SFNX_Q5_K)
         k_moe_mma_gu<SFNX_Q5_K><<<grid, MM_THREADS, MM_LDS, s>>>((const uint8_t*) A, sa, ff, n_in, jobs, njobs,
+                                                                  (const _Float16*) x16, gu, (_Float16*) h16);
+    else if (type == SFNX_Q4_0)
+        k_moe_mma_gu<SFNX_Q4_0><<<grid, MM_THREADS, MM_LDS, s>>>((const uint8_t*) A, sa, ff, n_in, jobs, njobs,
+                                                                  (const _Float16*) x16, gu, (_Float16*) h16);
+    else if (type == SFNX_Q5_1)
+        k_moe_mma_gu<SFNX_Q5_1><<<grid, MM_THREADS, MM_LDS, s>>>((const uint8_t*) A, sa, ff, n_in, jobs, njobs,
                                                                   (const _Float16*) x16, gu, (_Float16*) h16);
     else
         k_moe_mma_gu<SFNX_Q8_0><<<grid, MM_THREADS, MM_LDS, s>>>((const uint8_t*) A, sa, ff, n_in, jobs, njobs,

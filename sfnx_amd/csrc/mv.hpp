@@ -204,4 +204,74 @@ template <int BPL> struct Q80Row {
     }
 };
 
+// ------------------------------------------------------------------------------------------------ Q4_0, Q5_1
+// bits 0..3 of t to bit 4 of bytes 0..3
+__device__ __forceinline__ uint32_t spread4(uint32_t t) {
+    return ((t & 1u) << 4) | ((t & 2u) << 11) | ((t & 4u) << 18) | ((t & 8u) << 25);
+}
+// The Q8_0 lanes (16 a row, lane l16 the blocks l16 + 16 i in order).  Per block the exact integer dot of the values
+// (Q5_1: the fifth bit of value l is qh bit l) with the activation block, then Q4_0 (d_w d_a) (sum - 8 s), Q5_1
+// (d_w d_a) sum + (m_w d_a) s, with s the block's integer activation sum.
+template <int BPL, int TYPE> struct NbRow {
+    uint4 q[BPL];
+    uint32_t sv[BPL];   // Q4_0: f16 d (low half); Q5_1: f16 d | f16 m << 16
+    uint32_t qh[TYPE == SFNX_Q5_1 ? BPL : 1];
+    float dw[BPL], mw[BPL];
+    __device__ __forceinline__ void issue(const NbPlanes& P, int row, int C, int l16) {
+#pragma unroll
+        for (int i = 0; i < BPL; ++i) {
+            const int b = l16 + 16 * i;
+            q[i] = *reinterpret_cast<const uint4*>(P.q16(row, C, b));
+            if constexpr (TYPE == SFNX_Q4_0) {
+                sv[i] = *reinterpret_cast<const uint16_t*>(P.d_of(row, C, b));
+            } else {
+                sv[i] = *reinterpret_cast<const uint32_t*>(P.dm_of(row, C, b));
+                qh[i] = *reinterpret_cast<const uint32_t*>(P.qh_of(row, C, b));
+            }
+        }
+    }
+    __device__ __forceinline__ void prepare(int) {
+#pragma unroll
+        for (int i = 0; i < BPL; ++i) {
+            dw[i] = h2f((uint16_t) (sv[i] & 0xffff));
+            mw[i] = TYPE == SFNX_Q5_1 ? h2f((uint16_t) (sv[i] >> 16)) : 0.f;
+        }
+    }
+    __device__ __forceinline__ void load(const NbPlanes& P, int row, int C, int l16) {
+        issue(P, row, C, l16);
+        prepare(l16);
+    }
+    __device__ __forceinline__ float dot1(const Acts& a, int l16) {
+        prepare(l16);
+        return dot(a, 0, l16);
+    }
+    __device__ __forceinline__ float dot(const Acts& a, int j, int l16) const {
+        float acc = 0.f;
+        const int nb = a.K / 32;
+#pragma unroll
+        for (int i = 0; i < BPL; ++i) {
+            const int b = l16 + 16 * i;
+            const int4 a0 = a.q4(j, b)[0], a1 = a.q4(j, b)[1];
+            const unsigned qw[4] = {q[i].x, q[i].y, q[i].z, q[i].w};
+            const int al[4] = {a0.x, a0.y, a0.z, a0.w}, ah[4] = {a1.x, a1.y, a1.z, a1.w};
+            int sum = 0;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                unsigned lo = qw[w] & 0x0F0F0F0Fu, hi = (qw[w] >> 4) & 0x0F0F0F0Fu;
+                if constexpr (TYPE == SFNX_Q5_1) {
+                    lo |= spread4(qh[i] >> (4 * w));
+                    hi |= spread4(qh[i] >> (16 + 4 * w));
+                }
+                sum = dot4((int) lo, al[w], sum);
+                sum = dot4((int) hi, ah[w], sum);
+            }
+            const float da = a.d[j * nb + b];
+            const int sa = a.s[j * nb + b];
+            if constexpr (TYPE == SFNX_Q4_0) acc += (dw[i] * da) * (float) (sum - 8 * sa);
+            else acc += (dw[i] * da) * (float) sum + (mw[i] * da) * (float) sa;
+        }
+        return acc;
+    }
+};
+
 }  // namespace sfnx

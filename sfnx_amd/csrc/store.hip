@@ -108,6 +108,59 @@ __global__ void k_quant_q80(const float* __restrict__ x, uint8_t* __restrict__ d
     }
 }
 
+// one Q4_0 block per thread, tools/mtp_experts.py:29-41: d = (the first value of largest magnitude) / -8,
+// q = min(15, trunc(x (1 / d) + 8.5))
+__global__ void k_quant_q40(const float* __restrict__ x, uint8_t* __restrict__ dst, int64_t nblk) {
+    const int64_t k = blockIdx.x * (int64_t) blockDim.x + threadIdx.x;
+    if (k >= nblk) return;
+    const float* v = x + k * 32;
+    uint8_t* b = dst + k * Q40_BYTES;
+    float amax = fabsf(v[0]), mx = v[0];   // the first value of largest magnitude (numpy's argmax)
+    for (int l = 1; l < 32; ++l)
+        if (fabsf(v[l]) > amax) {
+            amax = fabsf(v[l]);
+            mx = v[l];
+        }
+    const float d = mx / -8.0f, idv = d != 0.f ? 1.0f / d : 0.f;
+    // d = mx / -8 is exact; a zero d keeps the opposite of mx's sign (the compiler's fused f32 -> f16 conversion of the
+    // product would give +0 for -0)
+    const uint16_t dh = mx == 0.f ? (uint16_t) (((__float_as_uint(mx) >> 16) & 0x8000u) ^ 0x8000u) : f2h(d);
+    b[0] = dh & 0xff;
+    b[1] = dh >> 8;
+    for (int l = 0; l < 16; ++l) {
+        const float a = truncf(v[l] * idv + 8.5f), c = truncf(v[l + 16] * idv + 8.5f);
+        const int q0 = (int) (a < 15.f ? a : 15.f), q1 = (int) (c < 15.f ? c : 15.f);
+        b[2 + l] = (uint8_t) (q0 | (q1 << 4));
+    }
+}
+
+// one Q5_1 block per thread, ggml's closed form: m = min, d = (max - min) / 31, q = trunc((x - m) (1 / d) + 0.5)
+__global__ void k_quant_q51(const float* __restrict__ x, uint8_t* __restrict__ dst, int64_t nblk) {
+    const int64_t k = blockIdx.x * (int64_t) blockDim.x + threadIdx.x;
+    if (k >= nblk) return;
+    const float* v = x + k * 32;
+    uint8_t* b = dst + k * Q51_BYTES;
+    float mn = v[0], mx = v[0];
+    for (int l = 1; l < 32; ++l) {
+        if (v[l] < mn) mn = v[l];
+        if (v[l] > mx) mx = v[l];
+    }
+    const float d = (mx - mn) / 31.0f, idv = d != 0.f ? 1.0f / d : 0.f;
+    const uint16_t dh = f2h(d), mh = f2h(mn);
+    b[0] = dh & 0xff;
+    b[1] = dh >> 8;
+    b[2] = mh & 0xff;
+    b[3] = mh >> 8;
+    uint32_t qh = 0;
+    for (int l = 0; l < 16; ++l) {
+        const int q0 = (int) truncf((v[l] - mn) * idv + 0.5f), q1 = (int) truncf((v[l + 16] - mn) * idv + 0.5f);
+        b[8 + l] = (uint8_t) ((q0 & 15) | ((q1 & 15) << 4));
+        qh |= (uint32_t) ((q0 >> 4) & 1) << l;
+        qh |= (uint32_t) ((q1 >> 4) & 1) << (l + 16);
+    }
+    for (int i = 0; i < 4; ++i) b[4 + i] = (uint8_t) (qh >> (8 * i));
+}
+
 // ------------------------------------------------------------------------------------------------ packing
 // K-quants: thread per (row, super-block).  Nibble bytes 32 jg + 16 h + x of super-block b land in piece
 // 16 (b / 2) + 8 h + 4 (b % 2) + jg of the row's nibbles (the run b / 2 in [half][group] order), byte x; the 16 header
@@ -161,6 +214,32 @@ __global__ void k_pack_q80(const uint8_t* __restrict__ src, uint8_t* __restrict_
         }
 }
 
+// Q4_0 / Q5_1: thread per (row, block).  The 16 quant bytes are piece b of the row's nibbles; Q4_0's d is at the d
+// plane's (row, b), Q5_1's (d, m) and qh words at those planes' (row, b).
+template <int TYPE, bool PACK>
+__global__ void k_pack_nb(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, int64_t n_mat, int R, int C) {
+    constexpr int BB = TYPE == SFNX_Q4_0 ? Q40_BYTES : Q51_BYTES, QS = TYPE == SFNX_Q4_0 ? 2 : 8;
+    const int nb = C / 32;
+    const int64_t k = blockIdx.x * (int64_t) blockDim.x + threadIdx.x, per_mat = (int64_t) R * nb;
+    if (k >= n_mat * per_mat) return;
+    const int64_t m = k / per_mat;
+    const int r = (int) ((k % per_mat) / nb), b = (int) (k % nb);
+    const size_t mat_bytes = (size_t) R * nb * BB;
+    const size_t gg = m * mat_bytes + ((size_t) r * nb + b) * BB;
+    const NbPlanes P = nb_planes<TYPE>((const uint8_t*) nullptr + m * mat_bytes, R, C);
+    auto mv = [&](size_t pg, size_t pp) {
+        if (PACK) dst[pp] = src[pg];
+        else dst[pg] = src[pp];
+    };
+    if (TYPE == SFNX_Q4_0) {
+        for (int i = 0; i < 2; ++i) mv(gg + i, (size_t) P.d_of(r, C, b) + i);
+    } else {
+        for (int i = 0; i < 4; ++i) mv(gg + i, (size_t) P.dm_of(r, C, b) + i);
+        for (int i = 0; i < 4; ++i) mv(gg + 4 + i, (size_t) P.qh_of(r, C, b) + i);
+    }
+    for (int i = 0; i < 16; ++i) mv(gg + QS + i, (size_t) P.q16(r, C, b) + i);
+}
+
 // ------------------------------------------------------------------------------------------------ dequant
 // thread per (row, 32-value sub-block) of the planar store; F16: the tensor-core path's f16 weight
 template <bool Q5, bool F16>
@@ -208,9 +287,42 @@ __global__ void k_deq_q80(const uint8_t* __restrict__ src, void* __restrict__ ou
     }
 }
 
+// Q4_0 / Q5_1: thread per (row, block); F16: the tensor-core path's weight (Q4_0 hmul2(q - 8, d), Q5_1 hfma2(q, d, m))
+template <int TYPE, bool F16>
+__global__ void k_deq_nb(const uint8_t* __restrict__ src, void* __restrict__ out, int64_t n_mat, int R, int C) {
+    const int nb = C / 32;
+    const int64_t k = blockIdx.x * (int64_t) blockDim.x + threadIdx.x, per_mat = (int64_t) R * nb;
+    if (k >= n_mat * per_mat) return;
+    const int64_t m = k / per_mat;
+    const int r = (int) ((k % per_mat) / nb), b = (int) (k % nb);
+    const NbPlanes P = nb_planes<TYPE>(src + m * row_bytes(TYPE, C) * R, R, C);
+    const uint8_t* q = P.q16(r, C, b);
+    uint16_t dh, mh = 0;
+    uint32_t qh = 0;
+    if (TYPE == SFNX_Q4_0) {
+        dh = *reinterpret_cast<const uint16_t*>(P.d_of(r, C, b));
+    } else {
+        const uint32_t dm = *reinterpret_cast<const uint32_t*>(P.dm_of(r, C, b));
+        dh = (uint16_t) (dm & 0xffff);
+        mh = (uint16_t) (dm >> 16);
+        qh = *reinterpret_cast<const uint32_t*>(P.qh_of(r, C, b));
+    }
+    const size_t o = (size_t) m * R * C + (size_t) r * C + 32 * b;
+    for (int l = 0; l < 32; ++l) {
+        const int nib = l < 16 ? q[l] & 15 : q[l - 16] >> 4;
+        const int v = TYPE == SFNX_Q4_0 ? nib - 8 : nib | (int) (((qh >> l) & 1) << 4);
+        if (F16) {
+            const __half d = __ushort_as_half(dh);
+            ((__half*) out)[o + l] = TYPE == SFNX_Q4_0 ? __hmul(__int2half_rn(v), d) : __hfma(__int2half_rn(v), d, __ushort_as_half(mh));
+        } else {
+            ((float*) out)[o + l] = TYPE == SFNX_Q4_0 ? (float) v * h2f(dh) : h2f(dh) * (float) v + h2f(mh);
+        }
+    }
+}
+
 inline unsigned blocks_for(int64_t n, int t) { return (unsigned) ((n + t - 1) / t); }
 void check_type_shape(uint32_t type, int rows, int cols) {
-    require(expert_type_ok(type), "weight type must be Q4_K (12), Q5_K (13) or Q8_0 (8)");
+    require(expert_type_ok(type), "weight type must be Q4_0 (2), Q5_1 (7), Q8_0 (8), Q4_K (12) or Q5_K (13)");
     require(cols > 0 && cols % 512 == 0, "columns must be a positive multiple of 512");
     require(rows >= 0 && rows % ROWTILE == 0, "rows must be a multiple of 32 (the store's row tile)");
 }
@@ -233,12 +345,14 @@ extern "C" int sfnx_synth_normal(float* out, size_t n, uint64_t seed, uint64_t o
 
 extern "C" int sfnx_quantize_weights(uint32_t type, const float* x, void* gguf, int64_t rows, int cols, void* st) {
     return guarded("sfnx_quantize_weights", [&] {
-        require(expert_type_ok(type), "weight type must be Q4_K (12), Q5_K (13) or Q8_0 (8)");
+        require(expert_type_ok(type), "weight type must be Q4_0 (2), Q5_1 (7), Q8_0 (8), Q4_K (12) or Q5_K (13)");
         require(cols > 0 && cols % block_values(type) == 0, "columns must be whole blocks");
         if (rows <= 0) return;
         const int64_t nb = rows * (cols / block_values(type));
         if (type == SFNX_Q4_K) k_quant_kq<false><<<blocks_for(nb, 128), 128, 0, stream_of(st)>>>(x, (uint8_t*) gguf, nb);
         else if (type == SFNX_Q5_K) k_quant_kq<true><<<blocks_for(nb, 128), 128, 0, stream_of(st)>>>(x, (uint8_t*) gguf, nb);
+        else if (type == SFNX_Q4_0) k_quant_q40<<<blocks_for(nb, 256), 256, 0, stream_of(st)>>>(x, (uint8_t*) gguf, nb);
+        else if (type == SFNX_Q5_1) k_quant_q51<<<blocks_for(nb, 256), 256, 0, stream_of(st)>>>(x, (uint8_t*) gguf, nb);
         else k_quant_q80<<<blocks_for(nb, 256), 256, 0, stream_of(st)>>>(x, (uint8_t*) gguf, nb);
     });
 }
@@ -253,6 +367,8 @@ template <bool PACK> void pack(uint32_t type, const void* src, void* dst, int64_
     auto* d8 = (uint8_t*) dst;
     if (type == SFNX_Q4_K) k_pack_kq<false, PACK><<<blocks_for(n, 256), 256, 0, stream_of(st)>>>(s8, d8, n_mat, R, C);
     else if (type == SFNX_Q5_K) k_pack_kq<true, PACK><<<blocks_for(n, 256), 256, 0, stream_of(st)>>>(s8, d8, n_mat, R, C);
+    else if (type == SFNX_Q4_0) k_pack_nb<SFNX_Q4_0, PACK><<<blocks_for(n, 256), 256, 0, stream_of(st)>>>(s8, d8, n_mat, R, C);
+    else if (type == SFNX_Q5_1) k_pack_nb<SFNX_Q5_1, PACK><<<blocks_for(n, 256), 256, 0, stream_of(st)>>>(s8, d8, n_mat, R, C);
     else k_pack_q80<PACK><<<blocks_for(n, 256), 256, 0, stream_of(st)>>>(s8, d8, n_mat, R, C);
 }
 template <bool F16> void dequant(uint32_t type, const void* planar, void* y, int64_t n_mat, int R, int C, void* st) {
@@ -262,6 +378,8 @@ template <bool F16> void dequant(uint32_t type, const void* planar, void* y, int
     const auto* p = (const uint8_t*) planar;
     if (type == SFNX_Q4_K) k_deq_kq<false, F16><<<blocks_for(n, 256), 256, 0, stream_of(st)>>>(p, y, n_mat, R, C);
     else if (type == SFNX_Q5_K) k_deq_kq<true, F16><<<blocks_for(n, 256), 256, 0, stream_of(st)>>>(p, y, n_mat, R, C);
+    else if (type == SFNX_Q4_0) k_deq_nb<SFNX_Q4_0, F16><<<blocks_for(n, 256), 256, 0, stream_of(st)>>>(p, y, n_mat, R, C);
+    else if (type == SFNX_Q5_1) k_deq_nb<SFNX_Q5_1, F16><<<blocks_for(n, 256), 256, 0, stream_of(st)>>>(p, y, n_mat, R, C);
     else k_deq_q80<F16><<<blocks_for(n, 256), 256, 0, stream_of(st)>>>(p, y, n_mat, R, C);
 }
 }  // namespace

@@ -12,7 +12,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _abi
-from ._abi import BIGJOB_INTS, JOB_INTS, Q4_K, Q5_K, Q8_0, check, lib
+from ._abi import BIGJOB_INTS, JOB_INTS, Q4_0, Q4_K, Q5_1, Q5_K, Q8_0, check, lib
 
 
 def _p(t):

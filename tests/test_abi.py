@@ -29,7 +29,7 @@ def test_row_bytes():
     (lambda L: L.sfnx_router_route(None, None, None, 17, 2048, 512, 10, None, None, None, None, None, 1, None), "T out of range"),
     (lambda L: L.sfnx_router_route(None, None, None, 1, 2048, 500, 10, None, None, None, None, None, 1, None), "E must be"),
     (lambda L: L.sfnx_router_route(None, None, None, 1, 2048, 512, 17, None, None, None, None, None, 1, None), "K out of range"),
-    (lambda L: L.sfnx_moe_gate_up(None, 1 << 30, 5, 2048, 1024, None, None, 11, 1, None, None, None), "Q5_K (13) or Q8_0 (8)"),
+    (lambda L: L.sfnx_moe_gate_up(None, 1 << 30, 5, 2048, 1024, None, None, 11, 1, None, None, None), "Q4_K (12) or Q5_K (13)"),
     (lambda L: L.sfnx_moe_gate_up(None, 1 << 30, 12, 2000, 1024, None, None, 11, 1, None, None, None), "multiple of 512"),
     (lambda L: L.sfnx_moe_gate_up(None, 1000, 12, 2048, 1024, None, None, 11, 1, None, None, None), "stride smaller"),
     (lambda L: L.sfnx_moe_down(None, 1 << 30, 12, 512, 2048, None, None, 11, 0, None, None, None), "T out of range"),

@@ -29,7 +29,7 @@ def unfused_chain(layers, x, norm, bufs):
     return y
 
 
-@pytest.mark.parametrize("wtype", [orc.Q4_K, orc.Q5_K, orc.Q8_0])
+@pytest.mark.parametrize("wtype", [orc.Q4_K, orc.Q5_K, orc.Q4_0, orc.Q5_1, orc.Q8_0])
 @pytest.mark.parametrize("T", [1, 3, 16])
 def test_fused_layer_equals_unfused(wtype, T):
     shape = moe.LayerShape(H=1024, E=64, K=6, ff=512, wtype=wtype, shared=True)
@@ -63,7 +63,7 @@ def test_fused_layer_equals_unfused(wtype, T):
     assert max_rel(yu.cpu().numpy(), oy) < 2e-3
 
 
-@pytest.mark.parametrize("wtype", [orc.Q4_K, orc.Q5_K, orc.Q8_0])
+@pytest.mark.parametrize("wtype", [orc.Q4_K, orc.Q5_K, orc.Q4_0, orc.Q5_1, orc.Q8_0])
 def test_fused_chain_with_norm_equals_unfused(wtype):
     shape = moe.LayerShape(H=2048, E=512, K=10, ff=512, wtype=wtype, shared=True)
     layers = [moe.MoeLayer.synthetic(shape, seed=50 + i) for i in range(3)]

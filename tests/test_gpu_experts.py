@@ -22,7 +22,7 @@ def routed_rows(topi, T, K, shared):
     return rows + ([T * K + t for t in range(T)] if shared else [])
 
 
-@pytest.mark.parametrize("wtype", [orc.Q4_K, orc.Q5_K, orc.Q8_0])
+@pytest.mark.parametrize("wtype", [orc.Q4_K, orc.Q5_K, orc.Q4_0, orc.Q5_1, orc.Q8_0])
 @pytest.mark.parametrize("T", [1, 3, 16])
 def test_decode_layer_small(wtype, T):
     shape = moe.LayerShape(H=1024, E=64, K=6, ff=512, wtype=wtype, shared=True)
@@ -44,7 +44,7 @@ def test_decode_layer_small(wtype, T):
     assert max_rel(y.cpu().numpy(), oy) < TOL
 
 
-@pytest.mark.parametrize("wtype", [orc.Q4_K, orc.Q5_K, orc.Q8_0])
+@pytest.mark.parametrize("wtype", [orc.Q4_K, orc.Q5_K, orc.Q4_0, orc.Q5_1, orc.Q8_0])
 def test_prefill_q8_layer(wtype):
     """the BigJob kernels (prompt path, q8_1 arithmetic) on a skewed chunk: same per-pair arithmetic as decode"""
     shape = moe.LayerShape(H=1024, E=64, K=6, ff=512, wtype=wtype, shared=True)
@@ -66,7 +66,7 @@ def test_prefill_q8_layer(wtype):
     assert max_rel(y.cpu().numpy(), oy) < TOL
 
 
-@pytest.mark.parametrize("wtype", [orc.Q4_K, orc.Q5_K, orc.Q8_0])
+@pytest.mark.parametrize("wtype", [orc.Q4_K, orc.Q5_K, orc.Q4_0, orc.Q5_1, orc.Q8_0])
 def test_decode_layer_baseline_shapes(wtype):
     """The benchmark layer shape (configs 0/1/4): hidden 2048, 512 experts x FF 512, top-10 + shared, one token and a 16-row window"""
     shape = moe.LayerShape(H=2048, E=512, K=10, ff=512, wtype=wtype, shared=True)

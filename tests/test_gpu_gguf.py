@@ -26,7 +26,8 @@ def _layer_bytes(wtype, H, E, ff, seed):
 
 
 @pytest.mark.parametrize("wtype,H,E,ff,ff0,ff1", [(orc.Q4_K, 1024, 64, 512, 0, 512), (orc.Q4_K, 1024, 64, 1024, 256, 768),
-                                                  (orc.Q5_K, 1024, 64, 1024, 256, 768),
+                                                  (orc.Q5_K, 1024, 64, 1024, 256, 768), (orc.Q4_0, 1024, 64, 512, 0, 512),
+                                                  (orc.Q5_1, 1024, 64, 1024, 32, 544),
                                                   (orc.Q8_0, 1024, 64, 512, 0, 512), (orc.Q8_0, 1024, 64, 1024, 32, 544)])
 def test_gguf_layer(tmp_path, wtype, H, E, ff, ff0, ff1):
     W, gate, up, down, shared = _layer_bytes(wtype, H, E, ff, 11)

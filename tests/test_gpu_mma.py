@@ -68,7 +68,7 @@ def check_sampled(host, x, b, nsample, rng):
     return eg / mg, ed / md
 
 
-@pytest.mark.parametrize("wtype", [orc.Q4_K, orc.Q5_K, orc.Q8_0])
+@pytest.mark.parametrize("wtype", [orc.Q4_K, orc.Q5_K, orc.Q4_0, orc.Q5_1, orc.Q8_0])
 def test_mma_small_layer_with_full_jobs(wtype):
     shape = moe.LayerShape(H=1024, E=64, K=6, ff=512, wtype=wtype, shared=True)
     L, host, x, y, b = run_prefill(shape, 70 + wtype, 200, dup=True)
@@ -98,7 +98,7 @@ def test_mma_baseline_prefill_shape():
     assert eg < 2e-3 and ed < 2e-3, (eg, ed)
 
 
-@pytest.mark.parametrize("wtype", [orc.Q4_K, orc.Q5_K, orc.Q8_0])
+@pytest.mark.parametrize("wtype", [orc.Q4_K, orc.Q5_K, orc.Q4_0, orc.Q5_1, orc.Q8_0])
 def test_gate_up_swiglu_fused_equals_two_calls(wtype):
     """sfnx_moe_gate_up_swiglu_mma against moe_gate_up_mma + swiglu_h16 on the same jobs: bit for bit"""
     shape = moe.LayerShape(H=1024, E=64, K=6, ff=512, wtype=wtype, shared=True)

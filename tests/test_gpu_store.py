@@ -17,7 +17,7 @@ def test_synth_bit_exact():
     assert np.array_equal(t.cpu().numpy().view(np.uint32), orc.synth(n, 77, 0.02, offset=off).view(np.uint32))
 
 
-@pytest.mark.parametrize("wtype", [orc.Q4_K, orc.Q5_K, orc.Q8_0])
+@pytest.mark.parametrize("wtype", [orc.Q4_K, orc.Q5_K, orc.Q4_0, orc.Q5_1, orc.Q8_0])
 @pytest.mark.parametrize("rows, cols", [(64, 512), (48, 2048)])
 def test_quantizer_bit_exact(wtype, rows, cols):
     x = orc.synth(rows * cols, 5 + cols, 0.02).reshape(rows, cols)
@@ -29,7 +29,7 @@ def test_quantizer_bit_exact(wtype, rows, cols):
     assert np.array_equal(g.cpu().numpy(), orc.quantize(wtype, x))
 
 
-@pytest.mark.parametrize("wtype", [orc.Q4_K, orc.Q5_K, orc.Q8_0])
+@pytest.mark.parametrize("wtype", [orc.Q4_K, orc.Q5_K, orc.Q4_0, orc.Q5_1, orc.Q8_0])
 def test_pack_round_trip_and_dequant(wtype):
     n_mat, rows, cols = 3, 96, 1024
     x = orc.synth(n_mat * rows * cols, 91, 0.02).reshape(n_mat * rows, cols)

@@ -12,7 +12,7 @@ def q81_values(yq, n):
     return (b[:, 4:].view(np.int8).astype(np.float64) * d[:, None]).reshape(-1)
 
 
-@pytest.mark.parametrize("wtype", [12, 13, 8])
+@pytest.mark.parametrize("wtype", [12, 13, 2, 7, 8])
 @pytest.mark.parametrize("K", [512, 2048])
 def test_dot_against_dequantized_float64(orc, wtype, K):
     rows = 24
@@ -69,7 +69,7 @@ def small_layer(orc, wtype=12, H=1024, E=64, K=6, ff=512, seed=40):
     return orc.LayerWeights(W, gu, dn, wtype, H, E, K, ff, True)
 
 
-@pytest.mark.parametrize("wtype", [12, 13, 8])
+@pytest.mark.parametrize("wtype", [12, 13, 2, 7, 8])
 def test_layer_pieces_are_consistent(orc, wtype):
     L = small_layer(orc, wtype)
     T = 3

@@ -306,3 +306,70 @@ def test_q5k_quantizer_round_trip_bound(orc):
             dl, ml = hdr[k, 0] * a.value, hdr[k, 1] * b.value
             bound = 0.5 * dl + 31 * abs(scale[k, j] - dl) + 2 * abs(ml + mn[k, j]) + 1e-7
             assert np.max(np.abs(xs[k, j] - ys[k, j])) <= bound
+
+
+# ------------------------------------------------------------------------------------------------ Q4_0, Q5_1
+def test_q4_0_dequant_known_block(orc):
+    """value l in the low nibble of byte l, value l + 16 in its high nibble; (q - 8) d"""
+    q = [(5 * l + 3) % 16 for l in range(32)]
+    qs = bytes(q[l] | (q[l + 16] << 4) for l in range(16))
+    blk = np.frombuffer(np.uint16([0x3400]).tobytes() + qs, np.uint8)   # d = 0.25
+    want = (np.array(q, np.float32) - 8) * 0.25
+    assert np.array_equal(orc.dequant(orc.Q4_0, blk, 1, 32)[0], want)
+    assert np.array_equal(orc.dequant_f16(orc.Q4_0, blk, 1, 32)[0].view(np.float16).astype(np.float32), want)
+
+
+def test_q4_0_quantizer_known_answers(orc):
+    """tools/mtp_experts.py:29-41: d = (first value of largest magnitude) / -8, q = min(15, trunc(x / d + 8.5))"""
+    d = 0.125
+    q = np.array([(7 * l + 1) % 16 for l in range(32)])
+    q[5] = 0                                     # the largest magnitude, -8 d: d comes back exactly
+    x = ((q - 8) * d).astype(np.float32).reshape(1, 32)
+    blk = orc.quantize(orc.Q4_0, x)
+    assert blk[:2].copy().view(np.float16)[0] == np.float16(d)
+    assert np.array_equal(orc.dequant(orc.Q4_0, blk, 1, 32), x)
+    # +8 before -8 at equal magnitude: d = 8 / -8 = -1, +8 -> q 0 -> 8; -8 -> q 16, clamped to 15 -> -7
+    x2 = np.zeros((1, 32), np.float32)
+    x2[0, 3], x2[0, 9] = 8.0, -8.0
+    y2 = orc.dequant(orc.Q4_0, orc.quantize(orc.Q4_0, x2), 1, 32)[0]
+    assert y2[3] == 8.0 and y2[9] == -7.0 and y2[0] == 0.0
+
+
+def test_q5_1_dequant_known_block(orc):
+    """value l: low nibble of byte l (l < 16) or high nibble of byte l - 16, fifth bit qh bit l; d q + m"""
+    q = [(11 * l + 4) % 32 for l in range(32)]
+    qh = sum(((q[l] >> 4) & 1) << l for l in range(32))
+    qs = bytes((q[l] & 15) | ((q[l + 16] & 15) << 4) for l in range(16))
+    blk = np.frombuffer(np.uint16([0x3800, 0xC000]).tobytes() + np.uint32([qh]).tobytes() + qs, np.uint8)  # d 0.5, m -2
+    want = np.array(q, np.float32) * 0.5 - 2.0
+    assert blk.size == 24
+    assert np.array_equal(orc.dequant(orc.Q5_1, blk, 1, 32)[0], want)
+    assert np.array_equal(orc.dequant_f16(orc.Q5_1, blk, 1, 32)[0].view(np.float16).astype(np.float32), want)
+
+
+def test_q5_1_quantizer_exact_on_its_grid_and_bounded(orc):
+    """values m + q d (d a power of two, q spanning 0..31) come back exactly; on normal data the error is at most
+    half a step plus the f16 rounding of d and m"""
+    q = np.array([(13 * l + 2) % 32 for l in range(32)])
+    q[0], q[1] = 0, 31
+    x = (-1.5 + q * 0.0625).astype(np.float32).reshape(1, 32)
+    blk = orc.quantize(orc.Q5_1, x)
+    assert np.array_equal(orc.dequant(orc.Q5_1, blk, 1, 32), x)
+    rows, cols = 16, 1024
+    xr = orc.synth(rows * cols, 21, 0.02).reshape(rows, cols)
+    b = orc.quantize(orc.Q5_1, xr).reshape(-1, 24)
+    y = orc.dequant(orc.Q5_1, b.reshape(-1), rows, cols).reshape(-1, 32).astype(np.float64)
+    xs = xr.reshape(-1, 32).astype(np.float64)
+    d = (xs.max(axis=1) - xs.min(axis=1)) / 31
+    dm = b[:, :4].copy().view(np.float16).astype(np.float64)
+    bound = 0.5 * d + 31 * np.abs(dm[:, 0] - d) + np.abs(dm[:, 1] - xs.min(axis=1)) + 1e-9
+    assert np.all(np.abs(xs - y).max(axis=1) <= bound)
+
+
+def test_q4_0_quantizer_zero_block_sign(orc):
+    """an all-zero block: d = x[0] / -8, so +0 data stores d = -0 and -0 data d = +0 (numpy's float32 arithmetic)"""
+    for z, want in ((0.0, 0x8000), (-0.0, 0x0000)):
+        x = np.full((1, 32), z, np.float32)
+        blk = orc.quantize(orc.Q4_0, x)
+        assert int(blk[:2].copy().view(np.uint16)[0]) == want
+        assert np.all(blk[2:] == 0x88)
