@@ -11,7 +11,8 @@ layer at a time) and the dominant one's roofline; the prompt path (config 3: 204
 CPU baseline (the oracle on config 0, on the host's cores) with the GPU's parity against it for that token.
 
 Configs 2 (a 96-row verify window through the whole layer) and 4 (Q8_0 experts: decode through 24 stacked layers and
-a 4096-token prompt chunk) are reported beside it.
+a 4096-token prompt chunk) are reported beside it, and the other expert types the reference decodes (Q5_K, Q4_0,
+Q5_1: decode through 12 stacked layers, a 2048-token prompt chunk).
 
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers 48] [--no-prefill] [--no-cpu] [--no-extra]
 """
@@ -48,6 +49,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-extra", action="store_true", help="skip configs 2 and 4 (verify window, Q8_0)")
     ap.add_argument("--q8-layers", type=int, default=24)
+    ap.add_argument("--type-layers", type=int, default=12, help="stacked layers for the Q5_K / Q4_0 / Q5_1 decode lines")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only copy 1 GiB device-to-device 3 times: the known-size kernel that scales rocprofv3's "
                          "FETCH_SIZE / WRITE_SIZE to bytes")
@@ -177,6 +179,7 @@ def main():
     if not args.no_extra:
         out["verify_window"] = bench_window(layers[0], s, moe, torch)
         out["q8_0"] = bench_q8_0(moe, torch, args.q8_layers, args.steps, args.warmup)
+        out["other_types"] = bench_other_types(moe, torch, args.type_layers, args.steps, args.warmup)
     print(json.dumps(out), flush=True)
     return 0
 
@@ -287,11 +290,11 @@ def bench_window(L, s, moe, torch, C=96, reps=20):
             "gbs": round(nbytes / (us * 1e-6) / 1e9, 1), "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
-def bench_q8_0(moe, torch, NL, steps, warmup):
-    """config 4: the same layer shapes with Q8_0 experts: decode at batch 1 through NL stacked layers (the fused
-    path in a graph, as config 1), and a 4096-token prompt chunk through layer 0 (experts on the matrix cores)"""
-    s = moe.LayerShape(H=2048, E=512, K=10, ff=512, wtype=moe.Q8_0, shared=True)
-    layers = [moe.MoeLayer.synthetic(s, seed=5000 + l) for l in range(NL)]
+def bench_type(moe, torch, wtype, NL, steps, warmup, C, seed0):
+    """one expert type at the bench's layer shapes: decode at batch 1 through NL stacked layers (the fused path in a
+    graph, as config 1) and a C-token prompt chunk through layer 0 (experts on the matrix cores, Zipf-skewed routing)"""
+    s = moe.LayerShape(H=2048, E=512, K=10, ff=512, wtype=wtype, shared=True)
+    layers = [moe.MoeLayer.synthetic(s, seed=seed0 + l) for l in range(NL)]
     x0 = torch.empty((1, s.H), dtype=torch.float32, device="cuda")
     moe.synth_normal(x0, 4343, 1.0)
     x = x0.clone()
@@ -310,7 +313,6 @@ def bench_q8_0(moe, torch, NL, steps, warmup):
     assert torch.isfinite(x).all()
     bytes_tl = (s.E + 1) * s.H * 4 + (s.K + 1) * expert_bytes(s, moe)
     gbs = bytes_tl * NL / (ms * 1e-3) / 1e9
-    C = 4096
     L = layers[0]
     xp = torch.empty((C, s.H), dtype=torch.float32, device="cuda")
     moe.synth_normal(xp, 780, 1.0)
@@ -327,12 +329,31 @@ def bench_q8_0(moe, torch, NL, steps, warmup):
     touched = int((b.cnt.cpu() > 0).sum()) + 1
     wbytes = touched * expert_bytes(s, moe)
     t = (t_gu + t_dn) * 1e-6
-    return {"workload": f"config 4: Q8_0 experts; decode batch 1 through {NL} stacked layers; 4096-token prompt chunk",
-            "decode_us_per_token_layer": round(ms * 1000 / NL, 3), "decode_gbs": round(gbs, 1),
-            "decode_hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_token_layer": bytes_tl,
+    del layers, L, b
+    torch.cuda.empty_cache()
+    return {"decode_layers": NL, "decode_us_per_token_layer": round(ms * 1000 / NL, 3), "decode_gbs": round(gbs, 1),
+            "decode_hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_token_layer": bytes_tl, "prefill_tokens": C,
             "prefill_us": {"mma_gate_up_swiglu": round(t_gu, 1), "mma_down": round(t_dn, 1)},
             "prefill_tflops": round(flops / t / 1e12, 1), "prefill_weight_gbs": round(wbytes / t / 1e9, 1),
             "prefill_hbm_frac": round(wbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
+
+
+def bench_q8_0(moe, torch, NL, steps, warmup):
+    """config 4: the same layer shapes with Q8_0 experts: decode at batch 1 through NL stacked layers and a 4096-token
+    prompt chunk through layer 0"""
+    r = bench_type(moe, torch, moe.Q8_0, NL, steps, warmup, 4096, 5000)
+    r["workload"] = f"config 4: Q8_0 experts; decode batch 1 through {NL} stacked layers; 4096-token prompt chunk"
+    return r
+
+
+def bench_other_types(moe, torch, NL, steps, warmup):
+    """the other expert types the reference decodes (Q5_K, Q4_0, Q5_1) at the same shapes: decode through NL stacked
+    layers, a 2048-token prompt chunk (not BASELINE configs; reported beside them)"""
+    out = {}
+    for name, t, seed in (("q5_k", moe.Q5_K, 6000), ("q4_0", moe.Q4_0, 7000), ("q5_1", moe.Q5_1, 8000)):
+        out[name] = bench_type(moe, torch, t, NL, steps, warmup, 2048, seed)
+        log(f"{name}: decode {out[name]['decode_us_per_token_layer']} us/token-layer, prefill {out[name]['prefill_us']}")
+    return out
 
 
 def cpu_baseline(L, s, moe, torch, x0, seconds):
