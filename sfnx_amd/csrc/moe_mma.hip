@@ -172,26 +172,44 @@ template <int TYPE> __device__ __forceinline__ void load_chunk(Chunk<TYPE>& w, c
     load_tail(w, a);
 }
 
-// step s of a chunk as the 4 B fragments of its MFMAs
-__device__ __forceinline__ void dequant_step(const Chunk<SFNX_Q4_K>& w, int s, half8 (&b)[4]) {
-    const uint4 hd = w.hdr;
-    const float d = h2f((uint16_t) (hd.x & 0xffff)), dmin = h2f((uint16_t) (hd.x >> 16));
-    float sc, m;
-    q4k_scale_min(hd, 2 * s, sc, m);
-    const _Float16 d1l = (_Float16) (d * sc), nml = (_Float16) (-(dmin * m));
-    q4k_scale_min(hd, 2 * s + 1, sc, m);
-    const _Float16 d1h = (_Float16) (d * sc), nmh = (_Float16) (-(dmin * m));
-    deq_q4k(w.q[s], half2v{d1l, d1l}, half2v{nml, nml}, half2v{d1h, d1h}, half2v{nmh, nmh}, b);
+// The 8 sub-blocks' f16(d sc) and f16(-(dmin m)) of a K-quant super-block header, all at once: the 6-bit values of
+// q4k_scale_min as bytes (4 to a dword), 1024 + v as f16 through v_perm, minus 1024, times f16 d (or -dmin) in packed
+// f16.  An f16 times a 6-bit integer is exact in fp32, so this single f16 rounding equals the f16 of the fp32 d * sc.
+struct KScales {
+    half2v D[4], N[4];   // D[k] = {f16(d sc_2k), f16(d sc_2k+1)}; N[k] the same of -(dmin m)
+};
+__device__ __forceinline__ KScales k_scales(const uint4& hd) {
+    const uint32_t sc_lo = hd.y & 0x3F3F3F3Fu, m_lo = hd.z & 0x3F3F3F3Fu;
+    const uint32_t sc_hi = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);
+    const uint32_t m_hi = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
+    const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t) (hd.x & 0xffff));
+    const _Float16 nmin = -__builtin_bit_cast(_Float16, (uint16_t) (hd.x >> 16));
+    const half2v dd = {d, d}, nn = {nmin, nmin}, k1024 = {(_Float16) 1024.0f, (_Float16) 1024.0f};
+    KScales k;
+    k.D[0] = (bytes_1024<0>(sc_lo) - k1024) * dd;
+    k.D[1] = (bytes_1024<1>(sc_lo) - k1024) * dd;
+    k.D[2] = (bytes_1024<0>(sc_hi) - k1024) * dd;
+    k.D[3] = (bytes_1024<1>(sc_hi) - k1024) * dd;
+    k.N[0] = (bytes_1024<0>(m_lo) - k1024) * nn;
+    k.N[1] = (bytes_1024<1>(m_lo) - k1024) * nn;
+    k.N[2] = (bytes_1024<0>(m_hi) - k1024) * nn;
+    k.N[3] = (bytes_1024<1>(m_hi) - k1024) * nn;
+    return k;
 }
-__device__ __forceinline__ void dequant_step(const Chunk<SFNX_Q5_K>& w, int s, half8 (&b)[4]) {
-    const uint4 hd = w.hdr;
-    const float d = h2f((uint16_t) (hd.x & 0xffff)), dmin = h2f((uint16_t) (hd.x >> 16));
-    float sc, m;
-    q4k_scale_min(hd, 2 * s, sc, m);
-    const _Float16 d1l = (_Float16) (d * sc), nml = (_Float16) (-(dmin * m));
-    q4k_scale_min(hd, 2 * s + 1, sc, m);
-    const _Float16 d1h = (_Float16) (d * sc), nmh = (_Float16) (-(dmin * m));
-    deq_q4k(w.q[s], half2v{d1l, d1l}, half2v{nml, nml}, half2v{d1h, d1h}, half2v{nmh, nmh}, b, &w.qh, 2 * s);
+struct NoScales {};
+template <int TYPE> __device__ __forceinline__ auto chunk_scales(const Chunk<TYPE>& w) {
+    if constexpr (is_kquant(TYPE)) return k_scales(w.hdr);
+    else return NoScales{};
+}
+
+// step s of a chunk as the 4 B fragments of its MFMAs
+__device__ __forceinline__ void dequant_step(const Chunk<SFNX_Q4_K>& w, int s, half8 (&b)[4], const KScales& k) {
+    const half2v D = k.D[s], N = k.N[s];
+    deq_q4k(w.q[s], half2v{D[0], D[0]}, half2v{N[0], N[0]}, half2v{D[1], D[1]}, half2v{N[1], N[1]}, b);
+}
+__device__ __forceinline__ void dequant_step(const Chunk<SFNX_Q5_K>& w, int s, half8 (&b)[4], const KScales& k) {
+    const half2v D = k.D[s], N = k.N[s];
+    deq_q4k(w.q[s], half2v{D[0], D[0]}, half2v{N[0], N[0]}, half2v{D[1], D[1]}, half2v{N[1], N[1]}, b, &w.qh, 2 * s);
 }
 // Q4_0 / Q5_1: a block's 16 quant bytes (value l in the low nibble of byte l, l + 16 in the high) -> the 4 B
 // fragments, fragment c holding values 8 c .. 8 c + 7; Q4_0 hmul2(q - 8, d), Q5_1 hfma2(q, d, m) with the fifth bits
@@ -225,13 +243,13 @@ __device__ __forceinline__ void deq_nb(const uint4& q, uint32_t dm, uint32_t qh,
         }
     }
 }
-__device__ __forceinline__ void dequant_step(const Chunk<SFNX_Q4_0>& w, int s, half8 (&b)[4]) {
+__device__ __forceinline__ void dequant_step(const Chunk<SFNX_Q4_0>& w, int s, half8 (&b)[4], NoScales) {
     deq_nb<SFNX_Q4_0>(w.q[s], (s < 2 ? w.d.x : w.d.y) >> (16 * (s % 2)), 0u, b);
 }
-__device__ __forceinline__ void dequant_step(const Chunk<SFNX_Q5_1>& w, int s, half8 (&b)[4]) {
+__device__ __forceinline__ void dequant_step(const Chunk<SFNX_Q5_1>& w, int s, half8 (&b)[4], NoScales) {
     deq_nb<SFNX_Q5_1>(w.q[s], (&w.dm.x)[s], (&w.qh.x)[s], b);
 }
-__device__ __forceinline__ void dequant_step(const Chunk<SFNX_Q8_0>& w, int s, half8 (&b)[4]) {
+__device__ __forceinline__ void dequant_step(const Chunk<SFNX_Q8_0>& w, int s, half8 (&b)[4], NoScales) {
     const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t) (w.d >> (16 * s)));
     deq_q80(w.qa[s], w.qb[s], half2v{d, d}, b);
 }
@@ -276,10 +294,11 @@ template <int N> __device__ __forceinline__ void wait_vmem_below() {
 template <int TYPE, int NT>
 __device__ __forceinline__ void mma_chunk(const Chunk<TYPE>& w, int cj, const _Float16* xb, int nn, int h, float16v (&acc)[NT]) {
     constexpr int S = Chunk<TYPE>::STEPS;
+    const auto sc = chunk_scales(w);
 #pragma unroll
     for (int s = 0; s < S; ++s) {
         half8 b[4];
-        dequant_step(w, s, b);
+        dequant_step(w, s, b, sc);
         const int j = cj * S + s;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
