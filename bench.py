@@ -57,7 +57,7 @@ def parse():
 
 
 def expert_bytes(s, moe):
-    return 2 * s.ff * moe.row_bytes(s.wtype, s.H) + s.H * moe.row_bytes(s.wtype, s.ff)
+    return 2 * s.ff * moe.row_bytes(s.wtype, s.H) + s.H * moe.row_bytes(s.dn_type, s.ff)
 
 
 def main():
@@ -128,7 +128,7 @@ def main():
     # and agrees with rocprofv3's kernel trace.  One eager pass over the 48 layers, 3 repetitions.
     names = ["k_dec_router", "k_dec_experts", "k_dec_down"]
     alg = [(s.E + 1) * s.H * 4, (s.K + 1) * 2 * s.ff * moe.row_bytes(s.wtype, s.H),
-           (s.K + 1) * s.H * moe.row_bytes(s.wtype, s.ff)]
+           (s.K + 1) * s.H * moe.row_bytes(s.dn_type, s.ff)]
     reps = 3
     tot = [0.0, 0.0, 0.0]
     moe.kernel_clock(True)
@@ -225,11 +225,11 @@ def bench_prefill(L, s, moe, torch, C=2048, reps=10):
         "swiglu_h16": lambda: moe.swiglu_h16(b.gu, b.h16, s.ff),
         "mma_gate_up_swiglu": lambda: moe.moe_gate_up_swiglu_mma(L.gu_w, L.gu_stride, s.wtype, s.H, s.ff, b.jobs_gu,
                                                                 b.njobs, b.cap, b.xh, b.h16),
-        "mma_down": lambda: moe.moe_down_mma(L.dn_w, L.dn_stride, s.wtype, s.ff, s.H, b.jobs_dn, b.njobs, b.cap, b.h16,
+        "mma_down": lambda: moe.moe_down_mma(L.dn_w, L.dn_stride, s.dn_type, s.ff, s.H, b.jobs_dn, b.njobs, b.cap, b.h16,
                                              b.part),
         "q8_gate_up": lambda: moe.moe_gate_up_big(L.gu_w, L.gu_stride, s.wtype, s.H, 2 * s.ff, b.jobs_gu, b.njobs, b.cap,
                                                   b.xq, b.gu),
-        "q8_down": lambda: moe.moe_down_big(L.dn_w, L.dn_stride, s.wtype, s.ff, s.H, b.jobs_dn, b.njobs, b.cap, b.gu, b.part),
+        "q8_down": lambda: moe.moe_down_big(L.dn_w, L.dn_stride, s.dn_type, s.ff, s.H, b.jobs_dn, b.njobs, b.cap, b.gu, b.part),
     }
     us = {}
     for name, c in calls.items():
@@ -323,7 +323,7 @@ def bench_type(moe, torch, wtype, NL, steps, warmup, C, seed0):
     moe.to_f16(xn, b.xh)
     t_gu = time_us(torch, lambda: moe.moe_gate_up_swiglu_mma(L.gu_w, L.gu_stride, s.wtype, s.H, s.ff, b.jobs_gu, b.njobs,
                                                              b.cap, b.xh, b.h16), 5)
-    t_dn = time_us(torch, lambda: moe.moe_down_mma(L.dn_w, L.dn_stride, s.wtype, s.ff, s.H, b.jobs_dn, b.njobs, b.cap,
+    t_dn = time_us(torch, lambda: moe.moe_down_mma(L.dn_w, L.dn_stride, s.dn_type, s.ff, s.H, b.jobs_dn, b.njobs, b.cap,
                                                    b.h16, b.part), 5)
     flops = 2 * (C * s.K + C) * 3 * s.ff * s.H
     touched = int((b.cnt.cpu() > 0).sum()) + 1
@@ -366,14 +366,15 @@ def cpu_baseline(L, s, moe, torch, x0, seconds):
     gu_g = torch.empty_like(L.gu_w)
     dn_g = torch.empty_like(L.dn_w)
     moe.store_unpack(s.wtype, L.gu_w, gu_g, E1, 2 * s.ff, s.H)
-    moe.store_unpack(s.wtype, L.dn_w, dn_g, E1, s.H, s.ff)
+    moe.store_unpack(s.dn_type, L.dn_w, dn_g, E1, s.H, s.ff)
     xn = torch.empty_like(x0)
     moe.residual_rmsnorm(x0.clone(), None, xn)
     y = torch.empty_like(x0)
     b = moe.DecodeBuffers(s, 1)
     moe.decode_layer(L, xn, y, b)
     torch.cuda.synchronize()
-    host = orc.LayerWeights(L.W.cpu().numpy(), gu_g.cpu().numpy(), dn_g.cpu().numpy(), s.wtype, s.H, s.E, s.K, s.ff, True)
+    host = orc.LayerWeights(L.W.cpu().numpy(), gu_g.cpu().numpy(), dn_g.cpu().numpy(), s.wtype, s.H, s.E, s.K, s.ff, True,
+                            dn_type=s.dn_type)
     x = xn.cpu().numpy()
     threads = min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", "16")), 16)
     us1, _ = orc.time_layer_decode(host, x, threads, 3, 0)   # one short run to size the sample

@@ -160,6 +160,12 @@ size_t sfnx_moe_decode_workspace(int T, int H, int E, int K, int ff, size_t* off
  * (1 router, 2 gate|up, 4 down + combine), for timing each one alone. */
 int sfnx_moe_decode(const sfnx_moe_layer_w* layers, int n_layers, uint32_t type, int H, int E, int K, int ff, int shared,
                     float* x, int T, int norm, float eps, void* ws, size_t ws_bytes, int phases, void* st);
+/* sfnx_moe_decode with the gate|up and down matrices of different types, as the reference keeps a type per matrix
+ * (src/model.cpp:540-606: gate and up stack into one DW, down is its own): gu_type for every layer's gu store, dn_type
+ * for its dn store. */
+int sfnx_moe_decode2(const sfnx_moe_layer_w* layers, int n_layers, uint32_t gu_type, uint32_t dn_type, int H, int E,
+                     int K, int ff, int shared, float* x, int T, int norm, float eps, void* ws, size_t ws_bytes, int phases,
+                     void* st);
 
 /* the stacked-layer driver's glue between layers (no reference counterpart on the MoE path: the engine's
  * hyper-connection read, src/hc.cuh, normalises the MoE input): x += y (y may be null), then
@@ -200,9 +206,9 @@ int sfnx_gguf_str(const sfnx_gguf* g, const char* key, const char** v);         
  * 766-809): blk.<layer>.ffn_{gate,up}_exps rows ff0..ff1 stacked [gate ; up] per expert into gu (planar, gu_stride a
  * matrix), ffn_down_exps columns ff0..ff1 into dn (dn_stride a matrix), the shared expert ffn_*_shexp (when present,
  * of the same type and FF) as expert E, and the router W = [ffn_gate_inp rows ; ffn_gate_inp_shexp] (f32 [E+1][H]).
- * Q4_K, Q5_K or Q8_0 experts; ff0 on a block (256 / 32 columns), ff1 - ff0 and H multiples of 512.  info (may be null)
- * receives type, H, E, ff1 - ff0
- * and shared.  A loader, not a hot-path call: it allocates a staging buffer and synchronises the stream. */
+ * Q4_0, Q5_1, Q8_0, Q4_K or Q5_K experts, gate and up of one type, down of that or another; ff0 on a block of the
+ * down type (32 or 256 columns), ff1 - ff0 and H multiples of 512.  info (may be null, else 6 ints) receives the
+ * gate|up type, H, E, ff1 - ff0, shared and the down type.  A loader, not a hot-path call: it allocates a staging buffer and synchronises the stream. */
 int sfnx_gguf_moe_layer(const sfnx_gguf* g, int layer, int ff0, int ff1, void* gu, size_t gu_stride, void* dn,
                         size_t dn_stride, float* W, int* info, void* st);
 

@@ -677,7 +677,7 @@ static size_t row_bytes(int type, int cols) {
 void orc_layer_decode(const orc_layer* L, const float* x, int T, float* y, float* logits_out, int* topi_out,
                       float* topw_out, float* gu_out, float* part_out, int nthreads) {
     const int H = L->H, E = L->E, K = L->K, ff = L->ff, P = T * K, NP = P + (L->shared ? T : 0);
-    const size_t gurb = row_bytes(L->type, H), dnrb = row_bytes(L->type, ff);
+    const size_t gurb = row_bytes(L->type, H), dnrb = row_bytes(L->dn_type, ff);
     uint8_t* xq = (uint8_t*) malloc((size_t) T * (H / 32) * ORC_Q81_BYTES);
     float* logits = logits_out ? logits_out : (float*) malloc((size_t) T * (E + 1) * sizeof(float));
     int* topi = topi_out ? topi_out : (int*) malloc((size_t) P * sizeof(int));
@@ -711,7 +711,7 @@ void orc_layer_decode(const orc_layer* L, const float* x, int T, float* y, float
         const int p = (int) (q / H), r = (int) (q % H);
         if (pe[p] < 0) continue;
         const uint8_t* w = L->dn_w + (size_t) pe[p] * L->dn_stride + (size_t) r * dnrb;
-        part[q] = orc_dot(L->type, w, hq + (size_t) p * (ff / 32) * ORC_Q81_BYTES, ff);
+        part[q] = orc_dot(L->dn_type, w, hq + (size_t) p * (ff / 32) * ORC_Q81_BYTES, ff);
     }
     for (int t = 0; t < T; ++t) {
         const float g = L->shared ? sigm_(logits[(size_t) t * (E + 1) + E]) : 0.f;

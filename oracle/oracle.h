@@ -133,8 +133,9 @@ typedef struct {
     size_t gu_stride;
     const uint8_t* dn_w;
     size_t dn_stride;
-    int type;          /* ORC_Q4_K or ORC_Q8_0, both matrices */
+    int type;          /* the gate|up matrices' type (ORC_*) */
     int H, E, K, ff, shared;
+    int dn_type;       /* the down matrices' type */
 } orc_layer;
 void orc_layer_decode(const orc_layer* L, const float* x, int T, float* y, float* logits, int* topi, float* topw,
                       float* gu, float* part, int nthreads);

@@ -27,7 +27,7 @@ class Layer(C.Structure):
     _fields_ = [
         ("W", C.c_void_p), ("gu_w", C.c_void_p), ("gu_stride", C.c_size_t), ("dn_w", C.c_void_p),
         ("dn_stride", C.c_size_t), ("type", C.c_int), ("H", C.c_int), ("E", C.c_int), ("K", C.c_int),
-        ("ff", C.c_int), ("shared", C.c_int),
+        ("ff", C.c_int), ("shared", C.c_int), ("dn_type", C.c_int),
     ]
 
 
@@ -206,15 +206,16 @@ def swiglu_q8_1(gu_row: np.ndarray, ff: int) -> np.ndarray:
 class LayerWeights:
     """A layer in GGUF block layout: router W [E+1][H] fp32, gate|up experts [E+1][2ff][H], down [E+1][H][ff]."""
 
-    def __init__(self, W, gu_w, dn_w, wtype, H, E, K, ff, shared=True):
+    def __init__(self, W, gu_w, dn_w, wtype, H, E, K, ff, shared=True, dn_type=None):
         self.W = np.ascontiguousarray(W, np.float32)
         self.gu_w = np.ascontiguousarray(gu_w, np.uint8)
         self.dn_w = np.ascontiguousarray(dn_w, np.uint8)
         self.type, self.H, self.E, self.K, self.ff, self.shared = wtype, H, E, K, ff, shared
+        self.dn_type = wtype if dn_type is None else dn_type
         self.gu_stride = 2 * ff * row_bytes(wtype, H)
-        self.dn_stride = H * row_bytes(wtype, ff)
+        self.dn_stride = H * row_bytes(self.dn_type, ff)
         self.c = Layer(_p(self.W), _p(self.gu_w), self.gu_stride, _p(self.dn_w), self.dn_stride, wtype, H, E, K, ff,
-                       int(shared))
+                       int(shared), self.dn_type)
 
 
 def layer_decode(L: LayerWeights, x: np.ndarray, nthreads: int = 0):

@@ -49,6 +49,7 @@ SIGNATURES = {
     "sfnx_to_f16": (i32, [vp, vp, sz, vp]),
     "sfnx_moe_decode_workspace": (sz, [i32, i32, i32, i32, i32, vp]),
     "sfnx_moe_decode": (i32, [vp, i32, u32, i32, i32, i32, i32, i32, vp, i32, i32, f32, vp, sz, i32, vp]),
+    "sfnx_moe_decode2": (i32, [vp, i32, u32, u32, i32, i32, i32, i32, i32, vp, i32, i32, f32, vp, sz, i32, vp]),
     "sfnx_gguf_type_info": (i32, [u32, vp, vp]),
     "sfnx_gguf_open": (i32, [C.c_char_p, vp]),
     "sfnx_gguf_close": (None, [vp]),

@@ -648,7 +648,7 @@ __global__ void __launch_bounds__(D3_THREADS) k_dec_down1(const uint8_t* __restr
 
 // ------------------------------------------------------------------------------------------------ launch
 struct DecArgs {
-    uint32_t type;
+    uint32_t gu_type, dn_type;
     int H, E, K, ff, shared, T, norm;
     float eps;
     int phases;
@@ -749,7 +749,7 @@ void launch_layer_tt(const DecArgs& d, const sfnx_moe_layer_w& w, float* x, cons
         default: throw std::runtime_error("hidden size must be 1024, 2048, 2560 or 4096"); \
     }
     if (d.phases & 2) {
-        switch (d.type) {
+        switch (d.gu_type) {
             case SFNX_Q4_K: SFNX_K2(SFNX_Q4_K) break;
             case SFNX_Q5_K: SFNX_K2(SFNX_Q5_K) break;
             case SFNX_Q4_0: SFNX_K2(SFNX_Q4_0) break;
@@ -761,16 +761,16 @@ void launch_layer_tt(const DecArgs& d, const sfnx_moe_layer_w& w, float* x, cons
     // down tasks a lane group loads together: every job's 8 rows in one batch at T = 1
     constexpr int NB = TT == 1 ? 3 : 4;
     if (!(d.phases & 4)) return;
-    if (d.type == SFNX_Q4_K) {
+    if (d.dn_type == SFNX_Q4_K) {
         if (d.ff == 512) launch_k3<SFNX_Q4_K, 1, NB>(d, w, x, L, ws, s);
         else launch_k3<SFNX_Q4_K, 2, NB>(d, w, x, L, ws, s);
-    } else if (d.type == SFNX_Q5_K) {
+    } else if (d.dn_type == SFNX_Q5_K) {
         if (d.ff == 512) launch_k3<SFNX_Q5_K, 1, NB>(d, w, x, L, ws, s);
         else launch_k3<SFNX_Q5_K, 2, NB>(d, w, x, L, ws, s);
-    } else if (d.type == SFNX_Q4_0) {
+    } else if (d.dn_type == SFNX_Q4_0) {
         if (d.ff == 512) launch_k3<SFNX_Q4_0, 1, NB>(d, w, x, L, ws, s);
         else launch_k3<SFNX_Q4_0, 2, NB>(d, w, x, L, ws, s);
-    } else if (d.type == SFNX_Q5_1) {
+    } else if (d.dn_type == SFNX_Q5_1) {
         if (d.ff == 512) launch_k3<SFNX_Q5_1, 1, NB>(d, w, x, L, ws, s);
         else launch_k3<SFNX_Q5_1, 2, NB>(d, w, x, L, ws, s);
     } else {
@@ -824,11 +824,12 @@ extern "C" size_t sfnx_moe_decode_workspace(int T, int H, int E, int K, int ff, 
     return L.total;
 }
 
-extern "C" int sfnx_moe_decode(const sfnx_moe_layer_w* layers, int n_layers, uint32_t type, int H, int E, int K, int ff,
-                               int shared, float* x, int T, int norm, float eps, void* ws, size_t ws_bytes, int phases,
-                               void* st) {
+extern "C" int sfnx_moe_decode2(const sfnx_moe_layer_w* layers, int n_layers, uint32_t gu_type, uint32_t dn_type, int H,
+                                int E, int K, int ff, int shared, float* x, int T, int norm, float eps, void* ws,
+                                size_t ws_bytes, int phases, void* st) {
     return guarded("sfnx_moe_decode", [&] {
-        require(expert_type_ok(type), TYPE_MSG);
+        const uint32_t type = gu_type;
+        require(expert_type_ok(gu_type) && expert_type_ok(dn_type), TYPE_MSG);
         require(T >= 1 && T <= SFNX_MAXT, "T out of range (1..16)");
         require(E >= WAVE && E % WAVE == 0 && E <= MAX_E, "E must be a multiple of 64, at most 1024");
         require(K >= 1 && K <= MAX_K && K <= E, "K out of range (1..16)");
@@ -841,9 +842,9 @@ extern "C" int sfnx_moe_decode(const sfnx_moe_layer_w* layers, int n_layers, uin
         for (int l = 0; l < n_layers; ++l) {
             require(layers[l].W && layers[l].gu && layers[l].dn, "a layer's weights are missing");
             require(layers[l].gu_stride >= row_bytes(type, H) * 2 * (size_t) ff, "gate|up stride smaller than a matrix");
-            require(layers[l].dn_stride >= row_bytes(type, ff) * (size_t) H, "down stride smaller than a matrix");
+            require(layers[l].dn_stride >= row_bytes(dn_type, ff) * (size_t) H, "down stride smaller than a matrix");
         }
-        const DecArgs d{type, H, E, K, ff, shared ? 1 : 0, T, norm ? 1 : 0, eps, phases ? phases : 7, nullptr};
+        const DecArgs d{gu_type, dn_type, H, E, K, ff, shared ? 1 : 0, T, norm ? 1 : 0, eps, phases ? phases : 7, nullptr};
         hipStream_t s = stream_of(st);
         char* w = (char*) ws;
         for (int l = 0; l < n_layers; ++l) {
@@ -854,4 +855,10 @@ extern "C" int sfnx_moe_decode(const sfnx_moe_layer_w* layers, int n_layers, uin
             else launch_layer_tt<16>(dl, layers[l], x, L, w, s);
         }
     });
+}
+
+extern "C" int sfnx_moe_decode(const sfnx_moe_layer_w* layers, int n_layers, uint32_t type, int H, int E, int K, int ff,
+                               int shared, float* x, int T, int norm, float eps, void* ws, size_t ws_bytes, int phases,
+                               void* st) {
+    return sfnx_moe_decode2(layers, n_layers, type, type, H, E, K, ff, shared, x, T, norm, eps, ws, ws_bytes, phases, st);
 }

@@ -349,19 +349,19 @@ extern "C" int sfnx_gguf_moe_layer(const sfnx_gguf* g, int layer, int ff0, int f
         const sfnx_gguf_tensor& tu = need(g, L + "ffn_up_exps.weight");
         const sfnx_gguf_tensor& td = need(g, L + "ffn_down_exps.weight");
         const sfnx_gguf_tensor& ti = need(g, L + "ffn_gate_inp.weight");
-        const uint32_t type = tg.type;
-        require(expert_type_ok(type), "expert tensors must be Q4_K, Q5_K or Q8_0");
-        require(tu.type == type && td.type == type, "gate, up and down experts differ in type");
+        const uint32_t type = tg.type, dtype = td.type;   // gate|up stack into one store; down is its own (src/model.cpp:540-606)
+        require(expert_type_ok(type) && expert_type_ok(dtype), "expert tensors must be Q4_0, Q5_1, Q8_0, Q4_K or Q5_K");
+        require(tu.type == type, "gate and up experts differ in type (they stack into one matrix)");
         const int64_t H = tg.ne[0], FF = tg.ne[1], E = tg.ne[2];
         require(tu.ne[0] == H && tu.ne[1] == FF && tu.ne[2] == E, "up experts differ in shape from gate experts");
         require(td.ne[0] == FF && td.ne[1] == H && td.ne[2] == E, "down experts are not [FF][H] a expert");
-        const int cb = block_values(type);   // a column slice of the down rows is whole blocks
+        const int cb = block_values(dtype);   // a column slice of the down rows is whole blocks
         require(0 <= ff0 && ff0 < ff1 && ff1 <= FF && ff0 % cb == 0 && (ff1 - ff0) % 512 == 0,
                 "FF slice must start on a whole block and span a multiple of 512 (the store's runs)");
         require(H % 512 == 0, "the hidden size must be a multiple of 512 (the store's runs)");
         require(ti.type == 0 && ti.ne[0] == H && ti.ne[1] == E, "ffn_gate_inp must be f32 [E][H]");
         const int ffs = ff1 - ff0;
-        const size_t rb_in = row_bytes(type, (int) H), rb_ff = row_bytes(type, ffs);
+        const size_t rb_in = row_bytes(type, (int) H), rb_ff = row_bytes(dtype, ffs);
         require(gu_stride >= 2 * (size_t) ffs * rb_in && dn_stride >= (size_t) H * rb_ff, "strides smaller than a matrix");
         // the shared expert, when the layer has one of the routed experts' type and FF, is expert E
         const sfnx_gguf_tensor* sg = find(g, L + "ffn_gate_shexp.weight");
@@ -370,8 +370,8 @@ extern "C" int sfnx_gguf_moe_layer(const sfnx_gguf* g, int layer, int ff0, int f
         const sfnx_gguf_tensor* sgi = find(g, L + "ffn_gate_inp_shexp.weight");
         const bool shared = sg && su && sd && sgi;
         if (shared) {
-            require(sg->type == type && su->type == type && sd->type == type,
-                    "the shared expert's type differs from the routed experts' (one store holds one type)");
+            require(sg->type == type && su->type == type && sd->type == dtype,
+                    "the shared expert's types differ from the routed experts' (it is one more expert of their stores)");
             require(sg->ne[0] == H && sg->ne[1] == FF && su->ne[0] == H && su->ne[1] == FF && sd->ne[0] == FF &&
                         sd->ne[1] == H, "the shared expert's shape differs from a routed expert's");
             require(sgi->type == 0 && sgi->ne[0] == H && sgi->ne[1] == 1, "ffn_gate_inp_shexp must be f32 [1][H]");
@@ -394,8 +394,8 @@ extern "C" int sfnx_gguf_moe_layer(const sfnx_gguf* g, int layer, int ff0, int f
         };
         try {
             uint8_t* h = (uint8_t*) host;
-            const size_t rb_full_dn = row_bytes(type, (int) FF);
-            const size_t col0 = row_bytes(type, ff0);
+            const size_t rb_full_dn = row_bytes(dtype, (int) FF);
+            const size_t col0 = row_bytes(dtype, ff0);
             for (int64_t e = 0; e < NE; ++e) {
                 const bool sh = e == E;
                 const uint8_t* g0 = (const uint8_t*) (sh ? sg->data : tg.data) + (sh ? 0 : e * FF * rb_in);
@@ -410,7 +410,7 @@ extern "C" int sfnx_gguf_moe_layer(const sfnx_gguf* g, int layer, int ff0, int f
                 check(hipMemcpyAsync(dev, host, gu_bytes + dn_bytes, hipMemcpyHostToDevice, s), "hipMemcpyAsync");
                 if (sfnx_store_pack(type, dev, (uint8_t*) gu + e * gu_stride, 1, 2 * ffs, (int) H, st) != 0)
                     throw std::runtime_error(sfnx_last_error());
-                if (sfnx_store_pack(type, (uint8_t*) dev + gu_bytes, (uint8_t*) dn + e * dn_stride, 1, (int) H, ffs, st) != 0)
+                if (sfnx_store_pack(dtype, (uint8_t*) dev + gu_bytes, (uint8_t*) dn + e * dn_stride, 1, (int) H, ffs, st) != 0)
                     throw std::runtime_error(sfnx_last_error());
             }
             // router rows, then the shared expert's gate row (src/model.cpp:766-773)
@@ -428,6 +428,7 @@ extern "C" int sfnx_gguf_moe_layer(const sfnx_gguf* g, int layer, int ff0, int f
             info[2] = (int) E;
             info[3] = ffs;
             info[4] = shared ? 1 : 0;
+            info[5] = (int) dtype;
         }
     });
 }

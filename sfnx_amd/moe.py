@@ -145,6 +145,11 @@ class LayerShape:
     ff: int = 512
     wtype: int = Q4_K
     shared: bool = True
+    dn_wtype: int | None = None   # the down matrices' type when it differs from gate|up's (the reference's DW per matrix)
+
+    @property
+    def dn_type(self) -> int:
+        return self.wtype if self.dn_wtype is None else self.dn_wtype
 
 
 class MoeLayer:
@@ -157,7 +162,7 @@ class MoeLayer:
         self.s = shape
         self.W, self.gu_w, self.dn_w = W, gu_w, dn_w
         self.gu_stride = 2 * shape.ff * row_bytes(shape.wtype, shape.H)
-        self.dn_stride = shape.H * row_bytes(shape.wtype, shape.ff)
+        self.dn_stride = shape.H * row_bytes(shape.dn_type, shape.ff)
 
     @staticmethod
     def planar_from_gguf(shape: LayerShape, W: torch.Tensor, gu_gguf: torch.Tensor, dn_gguf: torch.Tensor) -> "MoeLayer":
@@ -165,7 +170,7 @@ class MoeLayer:
         gu = torch.empty_like(gu_gguf)
         dn = torch.empty_like(dn_gguf)
         store_pack(s.wtype, gu_gguf, gu, s.E + 1, 2 * s.ff, s.H)
-        store_pack(s.wtype, dn_gguf, dn, s.E + 1, s.H, s.ff)
+        store_pack(s.dn_type, dn_gguf, dn, s.E + 1, s.H, s.ff)
         return MoeLayer(s, W, gu, dn)
 
     @staticmethod
@@ -176,21 +181,21 @@ class MoeLayer:
         W = torch.empty((E1, s.H), dtype=torch.float32, device=device)
         synth_normal(W, seed * 1000 + 1, 0.02)
         gu_stride = 2 * s.ff * row_bytes(s.wtype, s.H)
-        dn_stride = s.H * row_bytes(s.wtype, s.ff)
+        dn_stride = s.H * row_bytes(s.dn_type, s.ff)
         gu = torch.empty(E1 * gu_stride, dtype=torch.uint8, device=device)
         dn = torch.empty(E1 * dn_stride, dtype=torch.uint8, device=device)
         vals = 2 * s.ff * s.H   # values per expert matrix (gate|up and down hold the same count)
         tmp = torch.empty(chunk_experts * vals, dtype=torch.float32, device=device)
-        blk = torch.empty(chunk_experts * gu_stride, dtype=torch.uint8, device=device)
-        for mat, (rows, cols, stride, dst, sd) in enumerate(
-                [(2 * s.ff, s.H, gu_stride, gu, seed * 1000 + 2), (s.H, s.ff, dn_stride, dn, seed * 1000 + 3)]):
+        blk = torch.empty(chunk_experts * max(gu_stride, dn_stride), dtype=torch.uint8, device=device)
+        for mat, (rows, cols, stride, dst, sd, wt) in enumerate(
+                [(2 * s.ff, s.H, gu_stride, gu, seed * 1000 + 2, s.wtype), (s.H, s.ff, dn_stride, dn, seed * 1000 + 3, s.dn_type)]):
             for e0 in range(0, E1, chunk_experts):
                 ne = min(chunk_experts, E1 - e0)
                 t = tmp[: ne * rows * cols]
                 synth_normal(t, sd, 0.02, offset=e0 * rows * cols)
                 b = blk[: ne * stride]
-                quantize_weights(s.wtype, t.view(ne * rows, cols), b)
-                store_pack(s.wtype, b, dst[e0 * stride:(e0 + ne) * stride], ne, rows, cols)
+                quantize_weights(wt, t.view(ne * rows, cols), b)
+                store_pack(wt, b, dst[e0 * stride:(e0 + ne) * stride], ne, rows, cols)
         del tmp, blk
         return MoeLayer(s, W, gu, dn)
 
@@ -224,7 +229,7 @@ def decode_layer(L: MoeLayer, x: torch.Tensor, y: torch.Tensor, b: DecodeBuffers
     quantize_q8_1(x, b.xq)
     router_route(L.W, x, b.logits, b.topi, b.topw, b.jobs_gu, b.jobs_dn, b.njobs, s.E, s.K, s.shared)
     moe_gate_up(L.gu_w, L.gu_stride, s.wtype, s.H, 2 * s.ff, b.jobs_gu, b.njobs, b.njobs_max, T, b.xq, b.gu)
-    moe_down(L.dn_w, L.dn_stride, s.wtype, s.ff, s.H, b.jobs_dn, b.njobs, b.njobs_max, T, b.gu, b.part)
+    moe_down(L.dn_w, L.dn_stride, s.dn_type, s.ff, s.H, b.jobs_dn, b.njobs, b.njobs_max, T, b.gu, b.part)
     moe_combine(b.part, b.topw, b.topi, b.logits, y, s.E, s.K, s.shared)
 
 
@@ -250,8 +255,8 @@ class FusedDecode:
         s = self.s
         n = len(self.layers) - layer0 if n_layers is None else n_layers
         table = C.cast(self.table, C.c_void_p).value + layer0 * C.sizeof(_abi.LayerW)
-        check(lib().sfnx_moe_decode(table, n, s.wtype, s.H, s.E, s.K, s.ff, int(s.shared), _p(x), x.shape[0],
-                                    int(norm), eps, _p(self.ws), self.ws.numel(), phases, _st()))
+        check(lib().sfnx_moe_decode2(table, n, s.wtype, s.dn_type, s.H, s.E, s.K, s.ff, int(s.shared), _p(x), x.shape[0],
+                                     int(norm), eps, _p(self.ws), self.ws.numel(), phases, _st()))
 
     def piece(self, name: str, dtype, shape) -> torch.Tensor:
         """a view of one workspace piece (the last layer's value)"""
@@ -305,7 +310,7 @@ def prefill_experts_mma(L: "MoeLayer", x: torch.Tensor, y: torch.Tensor, b: "Pre
     to_f16(x, b.xh)
     moe_gate_up_mma(L.gu_w, L.gu_stride, s.wtype, s.H, 2 * s.ff, b.jobs_gu, b.njobs, b.cap, b.xh, b.gu)
     swiglu_h16(b.gu, b.h16, s.ff)
-    moe_down_mma(L.dn_w, L.dn_stride, s.wtype, s.ff, s.H, b.jobs_dn, b.njobs, b.cap, b.h16, b.part)
+    moe_down_mma(L.dn_w, L.dn_stride, s.dn_type, s.ff, s.H, b.jobs_dn, b.njobs, b.cap, b.h16, b.part)
     moe_combine(b.part, b.topw, b.topi, b.logits, y, s.E, s.K, s.shared)
 
 
@@ -317,7 +322,7 @@ def prefill_layer_mma(L: "MoeLayer", x: torch.Tensor, y: torch.Tensor, b: "Prefi
     prefill_route(L, x, b, bias)
     to_f16(x, b.xh)
     moe_gate_up_swiglu_mma(L.gu_w, L.gu_stride, s.wtype, s.H, s.ff, b.jobs_gu, b.njobs, b.cap, b.xh, b.h16)
-    moe_down_mma(L.dn_w, L.dn_stride, s.wtype, s.ff, s.H, b.jobs_dn, b.njobs, b.cap, b.h16, b.part)
+    moe_down_mma(L.dn_w, L.dn_stride, s.dn_type, s.ff, s.H, b.jobs_dn, b.njobs, b.cap, b.h16, b.part)
     moe_combine(b.part, b.topw, b.topi, b.logits, y, s.E, s.K, s.shared)
 
 
@@ -328,7 +333,7 @@ def prefill_layer_q8(L: MoeLayer, x: torch.Tensor, y: torch.Tensor, b: PrefillBu
     router_logits(L.W, x, b.logits)
     pf_route(b.logits, b.topi, b.topw, b.cnt, b.jbase, b.jobs_gu, b.jobs_dn, b.njobs, s.E, s.K, s.shared)
     moe_gate_up_big(L.gu_w, L.gu_stride, s.wtype, s.H, 2 * s.ff, b.jobs_gu, b.njobs, b.cap, b.xq, b.gu)
-    moe_down_big(L.dn_w, L.dn_stride, s.wtype, s.ff, s.H, b.jobs_dn, b.njobs, b.cap, b.gu, b.part)
+    moe_down_big(L.dn_w, L.dn_stride, s.dn_type, s.ff, s.H, b.jobs_dn, b.njobs, b.cap, b.gu, b.part)
     moe_combine(b.part, b.topw, b.topi, b.logits, y, s.E, s.K, s.shared)
 
 
@@ -406,13 +411,14 @@ def gguf_moe_layer(g: Gguf, layer: int, ff0: int = 0, ff1: int | None = None, K:
                  for n in ("ffn_gate_shexp", "ffn_up_shexp", "ffn_down_shexp", "ffn_gate_inp_shexp"))
     E1 = E + (1 if shared else 0)
     gu_stride = 2 * ffs * row_bytes(wtype, H)
-    dn_stride = H * row_bytes(wtype, ffs)
+    td = g.tensor(f"blk.{layer}.ffn_down_exps.weight")
+    dn_stride = H * row_bytes(td[0] if td is not None else wtype, ffs)
     gu = torch.empty(E1 * gu_stride, dtype=torch.uint8, device="cuda")
     dn = torch.empty(E1 * dn_stride, dtype=torch.uint8, device="cuda")
     W = torch.zeros((E + 1, H), dtype=torch.float32, device="cuda")   # row E: the shared gate (zero without one)
-    info = (C.c_int * 5)()
+    info = (C.c_int * 6)()
     check(lib().sfnx_gguf_moe_layer(g._h, layer, ff0, ff1, _p(gu), gu_stride, _p(dn), dn_stride, _p(W), info, _st()))
-    s = LayerShape(H=H, E=E, K=K, ff=ffs, wtype=wtype, shared=shared)
+    s = LayerShape(H=H, E=E, K=K, ff=ffs, wtype=wtype, shared=shared, dn_wtype=None if info[5] == wtype else info[5])
     return MoeLayer(s, W, gu, dn)
 
 

@@ -17,26 +17,27 @@ def make_layer(shape: moe.LayerShape, seed: int, device="cuda"):
     s = shape
     E1 = s.E + 1
     gu_stride = 2 * s.ff * moe.row_bytes(s.wtype, s.H)
-    dn_stride = s.H * moe.row_bytes(s.wtype, s.ff)
+    dn_stride = s.H * moe.row_bytes(s.dn_type, s.ff)
     W = torch.empty((E1, s.H), dtype=torch.float32, device=device)
     moe.synth_normal(W, seed * 1000 + 1, 0.02)
     gu_g = torch.empty(E1 * gu_stride, dtype=torch.uint8, device=device)
     dn_g = torch.empty(E1 * dn_stride, dtype=torch.uint8, device=device)
-    for rows, cols, dst, sd in ((E1 * 2 * s.ff, s.H, gu_g, seed * 1000 + 2), (E1 * s.H, s.ff, dn_g, seed * 1000 + 3)):
+    for rows, cols, dst, sd, wt in ((E1 * 2 * s.ff, s.H, gu_g, seed * 1000 + 2, s.wtype),
+                                    (E1 * s.H, s.ff, dn_g, seed * 1000 + 3, s.dn_type)):
         chunk = 1 << 24
         total = rows * cols
         per = max(cols, chunk // cols * cols)
         tmp = torch.empty(per, dtype=torch.float32, device=device)
-        rb = moe.row_bytes(s.wtype, cols)
+        rb = moe.row_bytes(wt, cols)
         for off in range(0, total, per):
             n = min(per, total - off)
             moe.synth_normal(tmp[:n], sd, 0.02, offset=off)
             r0 = off // cols
-            moe.quantize_weights(s.wtype, tmp[:n].view(n // cols, cols), dst[r0 * rb:(r0 + n // cols) * rb])
+            moe.quantize_weights(wt, tmp[:n].view(n // cols, cols), dst[r0 * rb:(r0 + n // cols) * rb])
     L = moe.MoeLayer.planar_from_gguf(s, W, gu_g, dn_g)
     torch.cuda.synchronize()
     host = orc.LayerWeights(W.cpu().numpy(), gu_g.cpu().numpy(), dn_g.cpu().numpy(), s.wtype, s.H, s.E, s.K, s.ff,
-                            s.shared)
+                            s.shared, dn_type=s.dn_type)
     return L, host
 
 

@@ -93,3 +93,24 @@ def test_fused_chain_with_norm_equals_unfused(wtype):
             g.replay()
             torch.cuda.synchronize()
             assert np.array_equal(bits(xg), bits(xu))
+
+
+@pytest.mark.parametrize("wtype, dn_type", [(orc.Q4_K, orc.Q5_K), (orc.Q4_K, orc.Q8_0), (orc.Q5_1, orc.Q4_0)])
+def test_mixed_gate_up_and_down_types(wtype, dn_type):
+    """gate|up in one type and down in another (the reference's DW per matrix, src/model.cpp:540-606): the fused path
+    equals the unfused one bit for bit, and both match the oracle within 2e-3, at the bench shape for 1 and 16 rows"""
+    shape = moe.LayerShape(H=2048, E=512, K=10, ff=512, wtype=wtype, shared=True, dn_wtype=dn_type)
+    L, host = make_layer(shape, 61)
+    for T in (1, 16):
+        x0 = torch.from_numpy(orc.synth(T * shape.H, 810 + T, 1.0).reshape(T, shape.H)).cuda()
+        b = moe.DecodeBuffers(shape, T)
+        xu = x0.clone()
+        yu = unfused_chain([L], xu, False, [b])
+        f = moe.FusedDecode([L], T)
+        xf = x0.clone()
+        f(xf, norm=False)
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(f.piece("y", torch.float32, (T, shape.H))), bits(yu))
+        oy, _, oi, _, ogu, _ = orc.layer_decode(host, x0.cpu().numpy(), nthreads=8)
+        assert np.array_equal(b.topi.cpu().numpy(), oi)
+        assert max_rel(yu.cpu().numpy(), oy) < 2e-3

@@ -14,41 +14,46 @@ from tests.gpu_util import max_rel
 pytestmark = pytest.mark.gpu
 
 
-def _layer_bytes(wtype, H, E, ff, seed):
+def _layer_bytes(wtype, H, E, ff, seed, dn_type=None):
     rng = np.random.default_rng(seed)
-    q = lambda r, c: orc.quantize(wtype, (0.02 * rng.standard_normal((r, c))).astype(np.float32))
+    dt = wtype if dn_type is None else dn_type
+    q = lambda r, c, t=wtype: orc.quantize(t, (0.02 * rng.standard_normal((r, c))).astype(np.float32))
     gate = np.stack([q(ff, H) for _ in range(E)])
     up = np.stack([q(ff, H) for _ in range(E)])
-    down = np.stack([q(H, ff) for _ in range(E)])
-    shared = (q(ff, H), q(ff, H), q(H, ff), (0.02 * rng.standard_normal(H)).astype(np.float32))
+    down = np.stack([q(H, ff, dt) for _ in range(E)])
+    shared = (q(ff, H), q(ff, H), q(H, ff, dt), (0.02 * rng.standard_normal(H)).astype(np.float32))
     W = (0.02 * rng.standard_normal((E, H))).astype(np.float32)
     return W, gate, up, down, shared
 
 
-@pytest.mark.parametrize("wtype,H,E,ff,ff0,ff1", [(orc.Q4_K, 1024, 64, 512, 0, 512), (orc.Q4_K, 1024, 64, 1024, 256, 768),
-                                                  (orc.Q5_K, 1024, 64, 1024, 256, 768), (orc.Q4_0, 1024, 64, 512, 0, 512),
-                                                  (orc.Q5_1, 1024, 64, 1024, 32, 544),
-                                                  (orc.Q8_0, 1024, 64, 512, 0, 512), (orc.Q8_0, 1024, 64, 1024, 32, 544)])
-def test_gguf_layer(tmp_path, wtype, H, E, ff, ff0, ff1):
-    W, gate, up, down, shared = _layer_bytes(wtype, H, E, ff, 11)
+@pytest.mark.parametrize("wtype,dn,H,E,ff,ff0,ff1", [
+    (orc.Q4_K, None, 1024, 64, 512, 0, 512), (orc.Q4_K, None, 1024, 64, 1024, 256, 768),
+    (orc.Q5_K, None, 1024, 64, 1024, 256, 768), (orc.Q4_0, None, 1024, 64, 512, 0, 512),
+    (orc.Q5_1, None, 1024, 64, 1024, 32, 544), (orc.Q8_0, None, 1024, 64, 512, 0, 512),
+    (orc.Q8_0, None, 1024, 64, 1024, 32, 544),
+    # gate and up in one type, down in another (src/model.cpp:540-606)
+    (orc.Q4_K, orc.Q5_K, 1024, 64, 1024, 256, 768), (orc.Q4_K, orc.Q8_0, 1024, 64, 512, 0, 512)])
+def test_gguf_layer(tmp_path, wtype, dn, H, E, ff, ff0, ff1):
+    W, gate, up, down, shared = _layer_bytes(wtype, H, E, ff, 11, dn)
+    dty = wtype if dn is None else dn
     path = tmp_path / "layer.gguf"
     gw.write_gguf(path, [("general.architecture", gw.STR, "qwen3moe")],
-                  gw.moe_layer_tensors(3, W, gate, up, down, wtype, H, E, ff, shared))
+                  gw.moe_layer_tensors(3, W, gate, up, down, wtype, H, E, ff, shared, dn))
     g = moe.Gguf(str(path))
     L = moe.gguf_moe_layer(g, 3, ff0, ff1, K=4)
     torch.cuda.synchronize()
     s = L.s
     ffs = ff1 - ff0
-    assert s.shared and s.E == E and s.H == H and s.ff == ffs and s.wtype == wtype
+    assert s.shared and s.E == E and s.H == H and s.ff == ffs and s.wtype == wtype and s.dn_type == dty
     # the router: routed rows, then the shared gate row
     assert np.array_equal(L.W.cpu().numpy(), np.vstack([W, shared[3][None]]))
     # the store, unpacked to GGUF layout, against the sliced source bytes
-    rb_h, rb_f, rb_full = orc.row_bytes(wtype, H), orc.row_bytes(wtype, ffs), orc.row_bytes(wtype, ff)
-    col0 = orc.row_bytes(wtype, ff0)
+    rb_h, rb_f, rb_full = orc.row_bytes(wtype, H), orc.row_bytes(dty, ffs), orc.row_bytes(dty, ff)
+    col0 = orc.row_bytes(dty, ff0)
     gu_g = torch.empty_like(L.gu_w)
     dn_g = torch.empty_like(L.dn_w)
     moe.store_unpack(wtype, L.gu_w, gu_g, E + 1, 2 * ffs, H)
-    moe.store_unpack(wtype, L.dn_w, dn_g, E + 1, H, ffs)
+    moe.store_unpack(dty, L.dn_w, dn_g, E + 1, H, ffs)
     gu_h = gu_g.cpu().numpy().reshape(E + 1, 2 * ffs, rb_h)
     dn_h = dn_g.cpu().numpy().reshape(E + 1, H, rb_f)
     for e in range(E + 1):
@@ -57,7 +62,7 @@ def test_gguf_layer(tmp_path, wtype, H, E, ff, ff0, ff1):
         assert np.array_equal(gu_h[e, ffs:], ut.reshape(ff, rb_h)[ff0:ff1])
         assert np.array_equal(dn_h[e], dt.reshape(H, rb_full)[:, col0:col0 + rb_f])
     # one decode window through the loaded layer against the oracle on the same bytes
-    host = orc.LayerWeights(L.W.cpu().numpy(), gu_h.reshape(-1), dn_h.reshape(-1), wtype, H, E, s.K, ffs, True)
+    host = orc.LayerWeights(L.W.cpu().numpy(), gu_h.reshape(-1), dn_h.reshape(-1), wtype, H, E, s.K, ffs, True, dn_type=dty)
     T = 3
     x = orc.synth(T * H, 77, 1.0).reshape(T, H)
     y = torch.empty((T, H), dtype=torch.float32, device="cuda")

@@ -18,7 +18,7 @@ def f16_of(a):
 
 
 def expert_rows(host, e, down):
-    rb = orc.row_bytes(host.type, host.ff if down else host.H)
+    rb = orc.row_bytes(host.dn_type if down else host.type, host.ff if down else host.H)
     if down:
         return host.dn_w[e * host.dn_stride:(e + 1) * host.dn_stride], rb
     return host.gu_w[e * host.gu_stride:(e + 1) * host.gu_stride], rb
@@ -59,7 +59,7 @@ def check_sampled(host, x, b, nsample, rng):
         mg = max(mg, np.abs(ref).max())
         eg = max(eg, np.abs(ref - gu[p]).max())
         wd, _ = expert_rows(host, e, True)
-        refd = orc.mma_matvec(s.type, wd, s.ff, s.H, h16[p].view(np.uint16))
+        refd = orc.mma_matvec(s.dn_type, wd, s.ff, s.H, h16[p].view(np.uint16))
         md = max(md, np.abs(refd).max())
         ed = max(ed, np.abs(refd - part[p]).max())
         # h16 is f16(silu(g) u) of the kernel's own gate|up row
@@ -145,4 +145,13 @@ def test_q8_0_prefill_4096_sampled():
     shape = moe.LayerShape(H=2048, E=512, K=10, ff=512, wtype=orc.Q8_0, shared=True)
     L, host, x, y, b = run_prefill(shape, 23, 4096)
     eg, ed = check_sampled(host, x, b, 16, np.random.default_rng(3))
+    assert eg < 2e-3 and ed < 2e-3, (eg, ed)
+
+
+@pytest.mark.parametrize("wtype, dn_type", [(orc.Q4_K, orc.Q5_K), (orc.Q4_0, orc.Q8_0)])
+def test_mma_mixed_gate_up_and_down_types(wtype, dn_type):
+    """gate|up of one type, down of another, on the matrix cores: sampled rows within 2e-3 of float64 products"""
+    shape = moe.LayerShape(H=1024, E=64, K=6, ff=512, wtype=wtype, shared=True, dn_wtype=dn_type)
+    L, host, x, y, b = run_prefill(shape, 77, 200, dup=True)
+    eg, ed = check_sampled(host, x, b, 30, np.random.default_rng(4))
     assert eg < 2e-3 and ed < 2e-3, (eg, ed)
