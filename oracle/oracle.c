@@ -653,6 +653,30 @@ static float dot_b32(const uint8_t* wrow, const uint8_t* yq, int K, int type) {
 float orc_dot_q4_0(const uint8_t* wrow, const uint8_t* yq, int K) { return dot_b32(wrow, yq, K, ORC_Q4_0); }
 float orc_dot_q5_1(const uint8_t* wrow, const uint8_t* yq, int K) { return dot_b32(wrow, yq, K, ORC_Q5_1); }
 
+/* The shared expert's dense Q8_0 rows, src/dense.cuh:24-154 q8s_block: 32 lanes, lane l the 16-column halves
+ * c = 16 l + 512 i in order, acc = fmaf(d_w d_a, dot of the 16 values, acc), then the xor butterfly 16, 8, 4, 2, 1
+ * (v += shfl_xor(v, o), src/dense.cuh:141-145).  d_a is the q8_1 block's f16 scale (its ds.x; the f16-rounded td
+ * of the SwiGLU rows for the down projection). */
+float orc_dot_q8s(const uint8_t* wrow, const uint8_t* yq, int K) {
+    float lane[32];
+    for (int l = 0; l < 32; ++l) {
+        float acc = 0.f;
+        for (int c = 16 * l; c < K; c += 512) {
+            const int b = c / 32, half = (c / 16) & 1;
+            const uint8_t* w = wrow + (size_t) b * ORC_Q80_BYTES;
+            const uint8_t* a = yq + (size_t) b * ORC_Q81_BYTES;
+            uint16_t dw, da;
+            memcpy(&dw, w, 2);
+            memcpy(&da, a, 2);
+            int s = 0;
+            for (int k = 0; k < 16; ++k) s += (int) (int8_t) w[2 + 16 * half + k] * (int) (int8_t) a[4 + 16 * half + k];
+            acc = fmaf(orc_f16_to_f32(dw) * orc_f16_to_f32(da), (float) s, acc);
+        }
+        lane[l] = acc;
+    }
+    return butterfly_sum(lane, 32);
+}
+
 float orc_dot(int type, const uint8_t* wrow, const uint8_t* yq, int K) {
     switch (type) {
         case ORC_Q4_K: return orc_dot_q4_k(wrow, yq, K);
@@ -700,8 +724,9 @@ void orc_layer_decode(const orc_layer* L, const float* x, int T, float* y, float
     for (int64_t q = 0; q < ngu; ++q) {
         const int p = (int) (q / (2 * ff)), r = (int) (q % (2 * ff)), t = p < P ? p / K : p - P;
         if (pe[p] < 0) continue;
-        const uint8_t* w = L->gu_w + (size_t) pe[p] * L->gu_stride + (size_t) r * gurb;
-        gu[q] = orc_dot(L->type, w, xq + (size_t) t * (H / 32) * ORC_Q81_BYTES, H);
+        const uint8_t* xt = xq + (size_t) t * (H / 32) * ORC_Q81_BYTES;
+        if (L->sh_gu && p >= P) gu[q] = orc_dot_q8s(L->sh_gu + (size_t) r * row_bytes(ORC_Q8_0, H), xt, H);
+        else gu[q] = orc_dot(L->type, L->gu_w + (size_t) pe[p] * L->gu_stride + (size_t) r * gurb, xt, H);
     }
     for (int p = 0; p < NP; ++p)
         if (pe[p] >= 0) orc_swiglu_q8_1(gu + (size_t) p * 2 * ff, ff, hq + (size_t) p * (ff / 32) * ORC_Q81_BYTES);
@@ -710,8 +735,9 @@ void orc_layer_decode(const orc_layer* L, const float* x, int T, float* y, float
     for (int64_t q = 0; q < ndn; ++q) {
         const int p = (int) (q / H), r = (int) (q % H);
         if (pe[p] < 0) continue;
-        const uint8_t* w = L->dn_w + (size_t) pe[p] * L->dn_stride + (size_t) r * dnrb;
-        part[q] = orc_dot(L->dn_type, w, hq + (size_t) p * (ff / 32) * ORC_Q81_BYTES, ff);
+        const uint8_t* hp = hq + (size_t) p * (ff / 32) * ORC_Q81_BYTES;
+        if (L->sh_dn && p >= P) part[q] = orc_dot_q8s(L->sh_dn + (size_t) r * row_bytes(ORC_Q8_0, ff), hp, ff);
+        else part[q] = orc_dot(L->dn_type, L->dn_w + (size_t) pe[p] * L->dn_stride + (size_t) r * dnrb, hp, ff);
     }
     for (int t = 0; t < T; ++t) {
         const float g = L->shared ? sigm_(logits[(size_t) t * (E + 1) + E]) : 0.f;

@@ -115,6 +115,8 @@ float orc_dot_q8_0(const uint8_t* wrow, const uint8_t* yq, int K);
  * vec_dot_q5_K_q8_1, not vendored: its order is parity unpinned; this form is pinned by float64 products) */
 float orc_dot_q5_k(const uint8_t* wrow, const uint8_t* yq, int K);
 /* Q4_0 / Q5_1 x q8_1: the Q8_0 lanes; per block (d_w d_a) sum (q - 8) a, or (d_w d_a) sum q a + (m_w d_a) sum a */
+/* the shared expert's dense Q8_0 rows, src/dense.cuh:24-154 (32 lanes over 16-column halves, fmaf, butterfly) */
+float orc_dot_q8s(const uint8_t* wrow, const uint8_t* yq, int K);
 float orc_dot_q4_0(const uint8_t* wrow, const uint8_t* yq, int K);
 float orc_dot_q5_1(const uint8_t* wrow, const uint8_t* yq, int K);
 float orc_dot(int type, const uint8_t* wrow, const uint8_t* yq, int K);
@@ -136,6 +138,8 @@ typedef struct {
     int type;          /* the gate|up matrices' type (ORC_*) */
     int H, E, K, ff, shared;
     int dn_type;       /* the down matrices' type */
+    const uint8_t* sh_gu;   /* when set: the shared expert's gate|up [2 ff][H] as Q8_0 blocks, computed as the reference's */
+    const uint8_t* sh_dn;   /* dense q8s rows (orc_dot_q8s); its down [H][ff] likewise.  Else it is expert E of gu_w / dn_w */
 } orc_layer;
 void orc_layer_decode(const orc_layer* L, const float* x, int T, float* y, float* logits, int* topi, float* topw,
                       float* gu, float* part, int nthreads);

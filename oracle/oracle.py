@@ -27,7 +27,7 @@ class Layer(C.Structure):
     _fields_ = [
         ("W", C.c_void_p), ("gu_w", C.c_void_p), ("gu_stride", C.c_size_t), ("dn_w", C.c_void_p),
         ("dn_stride", C.c_size_t), ("type", C.c_int), ("H", C.c_int), ("E", C.c_int), ("K", C.c_int),
-        ("ff", C.c_int), ("shared", C.c_int), ("dn_type", C.c_int),
+        ("ff", C.c_int), ("shared", C.c_int), ("dn_type", C.c_int), ("sh_gu", C.c_void_p), ("sh_dn", C.c_void_p),
     ]
 
 
@@ -61,6 +61,7 @@ def lib() -> C.CDLL:
             "orc_dequant_q5_k": (None, [vp, vp, i64, i32]),
             "orc_dequant_q5_k_f16": (None, [vp, vp, i64, i32]),
             "orc_dot_q5_k": (f32, [vp, vp, i32]),
+            "orc_dot_q8s": (f32, [vp, vp, i32]),
             "orc_quantize_q4_0": (None, [vp, vp, i64, i32]),
             "orc_dequant_q4_0": (None, [vp, vp, i64, i32]),
             "orc_dequant_q4_0_f16": (None, [vp, vp, i64, i32]),
@@ -197,6 +198,11 @@ def dot(t: int, wrow: np.ndarray, yq: np.ndarray, K: int) -> float:
     return f(_p(np.ascontiguousarray(wrow)), _p(np.ascontiguousarray(yq)), K)
 
 
+def dot_q8s(wrow: np.ndarray, yq: np.ndarray, K: int) -> float:
+    """the shared expert's dense Q8_0 row dot, src/dense.cuh:24-154 (orc_dot_q8s)"""
+    return lib().orc_dot_q8s(_p(np.ascontiguousarray(wrow)), _p(np.ascontiguousarray(yq)), K)
+
+
 def swiglu_q8_1(gu_row: np.ndarray, ff: int) -> np.ndarray:
     out = np.empty(ff // 32 * Q81_BYTES, np.uint8)
     lib().orc_swiglu_q8_1(_p(np.ascontiguousarray(gu_row, np.float32)), ff, _p(out))
@@ -206,7 +212,7 @@ def swiglu_q8_1(gu_row: np.ndarray, ff: int) -> np.ndarray:
 class LayerWeights:
     """A layer in GGUF block layout: router W [E+1][H] fp32, gate|up experts [E+1][2ff][H], down [E+1][H][ff]."""
 
-    def __init__(self, W, gu_w, dn_w, wtype, H, E, K, ff, shared=True, dn_type=None):
+    def __init__(self, W, gu_w, dn_w, wtype, H, E, K, ff, shared=True, dn_type=None, sh_gu=None, sh_dn=None):
         self.W = np.ascontiguousarray(W, np.float32)
         self.gu_w = np.ascontiguousarray(gu_w, np.uint8)
         self.dn_w = np.ascontiguousarray(dn_w, np.uint8)
@@ -214,8 +220,11 @@ class LayerWeights:
         self.dn_type = wtype if dn_type is None else dn_type
         self.gu_stride = 2 * ff * row_bytes(wtype, H)
         self.dn_stride = H * row_bytes(self.dn_type, ff)
+        # a separate Q8_0 shared expert (GGUF blocks), computed with the reference's dense q8s arithmetic
+        self.sh_gu = None if sh_gu is None else np.ascontiguousarray(sh_gu, np.uint8)
+        self.sh_dn = None if sh_dn is None else np.ascontiguousarray(sh_dn, np.uint8)
         self.c = Layer(_p(self.W), _p(self.gu_w), self.gu_stride, _p(self.dn_w), self.dn_stride, wtype, H, E, K, ff,
-                       int(shared), self.dn_type)
+                       int(shared), self.dn_type, _p(self.sh_gu), _p(self.sh_dn))
 
 
 def layer_decode(L: LayerWeights, x: np.ndarray, nthreads: int = 0):

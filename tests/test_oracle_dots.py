@@ -103,3 +103,37 @@ def test_layer_pieces_are_consistent(orc, wtype):
     # threads change nothing
     y4 = orc.layer_decode(L, x, nthreads=4)[0]
     assert np.array_equal(y, y4)
+
+
+@pytest.mark.parametrize("K", [512, 2048])
+def test_q8s_dot_against_float64_and_its_lane_order(orc, K):
+    """the shared expert's dense Q8_0 dot (src/dense.cuh:24-154): within fp32 rounding of the float64 product of the
+    dequantized operands; and its own order, not the routed Q8_0 dot's: the two differ in the last bits on most rows
+    (a restatement that fell back to the routed lanes would be caught here)"""
+    rows = 32
+    w = orc.quantize(orc.Q8_0, orc.synth(rows * K, 51 + K, 0.02).reshape(rows, K)).reshape(rows, -1)
+    wd = orc.dequant(orc.Q8_0, w.reshape(-1), rows, K).astype(np.float64)
+    yq = orc.quantize_q8_1(orc.synth(K, 52, 1.0).reshape(1, K))
+    a = q81_values(yq, K)
+    differ = 0
+    for r in range(rows):
+        got = orc.dot_q8s(w[r], yq, K)
+        exact = float(wd[r] @ a)
+        assert abs(got - exact) <= 2e-6 * float(np.abs(wd[r]) @ np.abs(a)) + 1e-9
+        differ += got != orc.dot(orc.Q8_0, w[r], yq, K)
+    assert differ >= rows // 4
+
+
+def test_q8s_dot_single_half_block(orc):
+    """one 16-column half in lane 0 only: the dot is exactly (d_w d_a) sum q_w q_a, rounded once"""
+    K = 512
+    w = np.zeros((K // 32, 34), np.uint8)
+    y = np.zeros((K // 32, 36), np.uint8)
+    w[:, :2] = np.frombuffer(np.float16(0.5).tobytes(), np.uint8)
+    y[:, :2] = np.frombuffer(np.float16(0.25).tobytes(), np.uint8)
+    qw = np.arange(1, 17, dtype=np.int8)
+    qa = np.arange(-8, 8, dtype=np.int8)
+    w[0, 2:18] = qw.view(np.uint8)        # columns 0..15: lane 0's first half
+    y[0, 4:20] = qa.view(np.uint8)
+    want = np.float32(0.125) * np.float32(int(qw.astype(np.int32) @ qa.astype(np.int32)))
+    assert orc.dot_q8s(w.reshape(-1), y.reshape(-1), K) == want
