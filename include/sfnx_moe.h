@@ -134,6 +134,16 @@ int sfnx_moe_down_mma(const void* A, size_t sa, uint32_t type, int n_in, int n_o
  * writes them, src/prefill.cu:1160) */
 int sfnx_to_f16(const float* x, uint16_t* y, size_t n, void* st);
 
+/* ---------------------------------------------------------------------------------------------- dense Q8_0 */
+/* src/kernels.hpp:47 q8s_gemv (kernel src/dense.cuh:24-154): out[t][r] (row stride out_stride) for t < T = row r of the
+ * dense Q8_0 matrix W [rows][cols] (planar Q8_0 layout, one matrix; rows % 32 == 0, cols % 512 == 0) dotted with q8_1
+ * row t of y ([T][cols / 32] blocks): 32 lanes a row, lane l the 16-column halves 16 l + 512 i in order, each
+ * acc = fmaf(d_w d_a, sum, acc), then the xor butterfly 16 .. 1. */
+int sfnx_q8s_gemv(const void* W, int rows, int cols, const void* y, float* out, int out_stride, int T, void* st);
+/* src/kernels.cu:1948-2024 swiglu_stacked_q8_1: hq row t ([T][ffs / 32] q8_1 blocks) = silu(gu[t][c]) * gu[t][ffs + c]
+ * quantized per 32 values (d = amax / 127, q = round(v / d), ds = (f16 d, f16 sum)); gu is [T][2 ffs], ffs % 32 == 0 */
+int sfnx_swiglu_stacked_q8_1(const float* gu, void* hq, int ffs, int T, void* st);
+
 /* ---------------------------------------------------------------------------------------------- fused decode */
 /* one layer's weights: router W [E + 1][H] fp32 (row E gates the shared expert), planar gate|up experts (E + 1 of
  * [2 ff][H], the shared expert last) and planar down experts (E + 1 of [H][ff]) */
@@ -166,6 +176,21 @@ int sfnx_moe_decode(const sfnx_moe_layer_w* layers, int n_layers, uint32_t type,
 int sfnx_moe_decode2(const sfnx_moe_layer_w* layers, int n_layers, uint32_t gu_type, uint32_t dn_type, int H, int E,
                      int K, int ff, int shared, float* x, int T, int norm, float eps, void* ws, size_t ws_bytes, int phases,
                      void* st);
+
+/* A layer's shared expert as its own dense Q8_0 matrices, as the reference holds it (src/model.hpp:72-83 Q8S,
+ * src/model.cpp:384-440 q8split: LayerW::sh_gu, sh_down): gu [2 ff][H] and dn [H][ff], each in the planar Q8_0 layout
+ * of sfnx_store_pack (one matrix). */
+typedef struct sfnx_moe_shared_q8s {
+    const void* gu;
+    const void* dn;
+} sfnx_moe_shared_q8s;
+/* sfnx_moe_decode2 with every layer's shared expert from shared_w[l] in the reference's dense q8s arithmetic
+ * (src/dense.cuh:24-154; 32 lanes over 16-column halves, fmaf, xor butterfly), as src/engine.cu:936-945 runs it
+ * (q8s_gemv gate|up, swiglu_stacked_q8_1, q8s_gemv down into part rows P + t); the shared gate is still router row E.
+ * The routed stores need only E experts.  Same values, bit for bit, as sfnx_q8s_gemv + sfnx_swiglu_stacked_q8_1. */
+int sfnx_moe_decode_q8s(const sfnx_moe_layer_w* layers, const sfnx_moe_shared_q8s* shared_w, int n_layers,
+                        uint32_t gu_type, uint32_t dn_type, int H, int E, int K, int ff, float* x, int T, int norm,
+                        float eps, void* ws, size_t ws_bytes, int phases, void* st);
 
 /* the stacked-layer driver's glue between layers (no reference counterpart on the MoE path: the engine's
  * hyper-connection read, src/hc.cuh, normalises the MoE input): x += y (y may be null), then

@@ -50,6 +50,9 @@ SIGNATURES = {
     "sfnx_moe_decode_workspace": (sz, [i32, i32, i32, i32, i32, vp]),
     "sfnx_moe_decode": (i32, [vp, i32, u32, i32, i32, i32, i32, i32, vp, i32, i32, f32, vp, sz, i32, vp]),
     "sfnx_moe_decode2": (i32, [vp, i32, u32, u32, i32, i32, i32, i32, i32, vp, i32, i32, f32, vp, sz, i32, vp]),
+    "sfnx_moe_decode_q8s": (i32, [vp, vp, i32, u32, u32, i32, i32, i32, i32, vp, i32, i32, f32, vp, sz, i32, vp]),
+    "sfnx_q8s_gemv": (i32, [vp, i32, i32, vp, vp, i32, i32, vp]),
+    "sfnx_swiglu_stacked_q8_1": (i32, [vp, vp, i32, i32, vp]),
     "sfnx_gguf_type_info": (i32, [u32, vp, vp]),
     "sfnx_gguf_open": (i32, [C.c_char_p, vp]),
     "sfnx_gguf_close": (None, [vp]),
@@ -71,6 +74,11 @@ class GgufTensor(C.Structure):
 class LayerW(C.Structure):
     """sfnx_moe_layer_w"""
     _fields_ = [("W", vp), ("gu", vp), ("gu_stride", sz), ("dn", vp), ("dn_stride", sz)]
+
+
+class SharedQ8s(C.Structure):
+    """sfnx_moe_shared_q8s"""
+    _fields_ = [("gu", vp), ("dn", vp)]
 
 
 def declared_symbols() -> list[str]:

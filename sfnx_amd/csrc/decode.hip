@@ -196,7 +196,7 @@ __global__ void __launch_bounds__(d2_threads<TYPE>()) k_dec_experts(
     const uint8_t* __restrict__ A, size_t sa, int T, int H, int E, int K, int ff, int shared, const float* __restrict__ logits,
     const uint8_t* __restrict__ xq, int* __restrict__ topi_g, float* __restrict__ topw_g, sfnx_job* __restrict__ jg,
     sfnx_job* __restrict__ jd, int* __restrict__ njobs_g, float* __restrict__ gu, int8_t* __restrict__ hq_q,
-    float* __restrict__ hq_d, int* __restrict__ hq_s) {
+    float* __restrict__ hq_d, int* __restrict__ hq_s, const uint8_t* __restrict__ sh_gu) {
     constexpr int LPR = lpr_of<TYPE>(), NTH = d2_threads<TYPE>(), NW = NTH / WAVE, RPW = WAVE / LPR;
     const int NFB = ff / 32, myjob = blockIdx.x / NFB, fb = blockIdx.x % NFB;
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE, p = threadIdx.x, P = T * K;
@@ -304,18 +304,28 @@ __global__ void __launch_bounds__(d2_threads<TYPE>()) k_dec_experts(
     __syncthreads();
     PROF(1, 3)
     const int rw = lane / LPR, ln = lane % LPR, f = fb * 32 + wave * RPW + rw;
-    const uint8_t* mat = A + (size_t) jb.w * sa;
-    typename RowOf<TYPE, G>::R wg, wu;
-    RowOf<TYPE, G>::load(wg, mat, 2 * ff, f, H, ln);
-    RowOf<TYPE, G>::load(wu, mat, 2 * ff, ff + f, H, ln);
-    for (int s = 0; s < jb.n; ++s) {
-        const int t = jb.y[s];
-        const float gv = group_sum<LPR>(wg.dot(a, t, ln)), uv = group_sum<LPR>(wu.dot(a, t, ln));
+    auto put = [&](int s, float gv, float uv) {
         if (ln == 0) {
             const int o = jb.out[s];
             gu[(size_t) o * 2 * ff + f] = gv;
             gu[(size_t) o * 2 * ff + ff + f] = uv;
             hbuf[s][wave * RPW + rw] = silu_f(gv) * uv;
+        }
+    };
+    if (sh_gu != nullptr && myjob >= nr) {   // the shared expert's own dense Q8_0 matrix, the reference's q8s sums
+        const Q80Planes Ps = q80_planes(sh_gu, 2 * ff, H);
+        for (int s = 0; s < jb.n; ++s) {
+            const int t = jb.y[s];
+            put(s, group_sum<LPR>(q8s_dot<LPR>(Ps, f, H, ln, a, t)), group_sum<LPR>(q8s_dot<LPR>(Ps, ff + f, H, ln, a, t)));
+        }
+    } else {
+        const uint8_t* mat = A + (size_t) jb.w * sa;
+        typename RowOf<TYPE, G>::R wg, wu;
+        RowOf<TYPE, G>::load(wg, mat, 2 * ff, f, H, ln);
+        RowOf<TYPE, G>::load(wu, mat, 2 * ff, ff + f, H, ln);
+        for (int s = 0; s < jb.n; ++s) {
+            const int t = jb.y[s];
+            put(s, group_sum<LPR>(wg.dot(a, t, ln)), group_sum<LPR>(wu.dot(a, t, ln)));
         }
     }
     __syncthreads();
@@ -358,7 +368,7 @@ __global__ void __launch_bounds__(2 * d2_threads<TYPE>()) k_dec_experts1(
     const float* __restrict__ logits,
     const uint8_t* __restrict__ xq, int* __restrict__ topi_g, float* __restrict__ topw_g, sfnx_job* __restrict__ jg,
     sfnx_job* __restrict__ jd, int* __restrict__ njobs_g, float* __restrict__ gu, int8_t* __restrict__ hq_q,
-    float* __restrict__ hq_d, int* __restrict__ hq_s, int* __restrict__ route_x) {
+    float* __restrict__ hq_d, int* __restrict__ hq_s, int* __restrict__ route_x, const uint8_t* __restrict__ sh_gu) {
     constexpr int LPR = lpr_of<TYPE>(), NW = 2 * d2_threads<TYPE>() / WAVE, RPW = WAVE / LPR;
     const int NFB = ff / 32, myjob = blockIdx.x / NFB, fb = blockIdx.x % NFB;
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
@@ -390,8 +400,10 @@ __global__ void __launch_bounds__(2 * d2_threads<TYPE>()) k_dec_experts1(
     const bool up = wave >= NW / 2;
     const int rw = lane / LPR, ln = lane % LPR, fl = (up ? wave - NW / 2 : wave) * RPW + rw, row = (up ? ff : 0) + fb * 32 + fl;
     const uint8_t* mat = A + (size_t) ex * sa;
+    // the shared expert from its own dense Q8_0 matrix when one is given (the reference's q8s sums)
+    const bool q8s = sh_gu != nullptr && myjob == nr;
     typename RowOf<TYPE, G>::R wr;
-    if (myjob < nj) RowOf<TYPE, G>::issue(wr, mat, 2 * ff, row, H, ln);
+    if (myjob < nj && !q8s) RowOf<TYPE, G>::issue(wr, mat, 2 * ff, row, H, ln);
     if (blockIdx.x < XCDS && wave == 0) {   // the routing, published for K3 and the caller, while the rows load
         const float w = topk_weight(pick, pord, K);
         // a copy for K3's workgroups of this XCD (workgroup b on XCD b % 8), read from this XCD's L2
@@ -424,7 +436,8 @@ __global__ void __launch_bounds__(2 * d2_threads<TYPE>()) k_dec_experts1(
     }
     __syncthreads();   // the staged activations
     PROF(1, 3)
-    const float v = group_sum<LPR>(wr.dot1(a, ln));   // each group as it arrives
+    const float v = group_sum<LPR>(q8s ? q8s_dot<LPR>(q80_planes(sh_gu, 2 * ff, H), row, H, ln, a, 0)
+                                       : wr.dot1(a, ln));   // each group as it arrives
     if (ln == 0) {
         gu[(size_t) out * 2 * ff + row] = v;
         (up ? ubuf : gbuf)[fl] = v;
@@ -457,7 +470,7 @@ __global__ void __launch_bounds__(D3_THREADS) k_dec_down(const uint8_t* __restri
                                                         const sfnx_job* __restrict__ jd, const int* __restrict__ njobs,
                                                         const int8_t* __restrict__ hq_q, const float* __restrict__ hq_d,
                                                         const int* __restrict__ hq_s, float* __restrict__ y,
-                                                        float* __restrict__ x, int hq_in_lds) {
+                                                        float* __restrict__ x, int hq_in_lds, const uint8_t* __restrict__ sh_dn) {
     constexpr int LPR = lpr_of<TYPE>(), GROUPS = D3_THREADS / LPR;
     const int row0 = blockIdx.x * D3_ROWS, nj = njobs[0], P = T * K, NP = P + T, nbh = ff / 32;
     PROF(2, 0)
@@ -497,8 +510,18 @@ __global__ void __launch_bounds__(D3_THREADS) k_dec_down(const uint8_t* __restri
         a.K = ff;
     }
     __syncthreads();
-    const int g = threadIdx.x / LPR, ln = threadIdx.x % LPR, ntask = nj * D3_ROWS;
+    const int g = threadIdx.x / LPR, ln = threadIdx.x % LPR;
+    // with its own dense Q8_0 matrix the shared expert's job (the last) runs apart, in the reference's q8s sums
+    const int nq = sh_dn != nullptr && shared ? nj - 1 : nj, ntask = nq * D3_ROWS;
     PROF(2, 1)
+    if (nq < nj) {
+        const Q80Planes Ps = q80_planes(sh_dn, H, ff);
+        for (int task = g; task < T * D3_ROWS; task += GROUPS) {
+            const int t = task / D3_ROWS, r = task % D3_ROWS;
+            const float v = group_sum<LPR>(q8s_dot<LPR>(Ps, row0 + r, ff, ln, a, P + t));
+            if (ln == 0) part[P + t][r] = v;
+        }
+    }
     for (int t0 = g; t0 < ntask; t0 += GROUPS * NB) {
         typename RowOf<TYPE, G2>::R w[NB];
 #pragma unroll
@@ -554,7 +577,8 @@ __global__ void __launch_bounds__(D3_THREADS) k_dec_down1(const uint8_t* __restr
                                                          const int* __restrict__ topi, const float* __restrict__ topw,
                                                          const int8_t* __restrict__ hq_q, const float* __restrict__ hq_d,
                                                          const int* __restrict__ hq_s, float* __restrict__ y,
-                                                         float* __restrict__ x, const int* __restrict__ route_x) {
+                                                         float* __restrict__ x, const int* __restrict__ route_x,
+                                                         const uint8_t* __restrict__ sh_dn) {
     constexpr int LPR = lpr_of<TYPE>(), GROUPS = D3_THREADS / LPR, HQ4 = 5, HQS = 3;
     const int row0 = blockIdx.x * D3_ROWS, nbh = ff / 32, lane = threadIdx.x % WAVE, tid = threadIdx.x;
     const int g = tid / LPR, ln = tid % LPR;
@@ -593,7 +617,8 @@ __global__ void __launch_bounds__(D3_THREADS) k_dec_down1(const uint8_t* __restr
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
         const int task = g + b * GROUPS, r = task % D3_ROWS;
-        if (task < ntask) RowOf<TYPE, G2>::issue(w[b], A + (size_t) (pp[b] < K ? ex[b] : E) * sa, H, row0 + r, ff, ln);
+        if (task < ntask && !(sh_dn != nullptr && pp[b] == K))
+            RowOf<TYPE, G2>::issue(w[b], A + (size_t) (pp[b] < K ? ex[b] : E) * sa, H, row0 + r, ff, ln);
     }
     // the staged activations
     const Acts a = acts_in(lds, NP, ff);
@@ -611,18 +636,33 @@ __global__ void __launch_bounds__(D3_THREADS) k_dec_down1(const uint8_t* __restr
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
         const int task = g + b * GROUPS;
-        if (task < ntask) {
+        if (task < ntask && !(sh_dn != nullptr && pp[b] == K)) {
             w[b].prepare(ln);
             const float v = group_sum<LPR>(w[b].dot(a, pp[b], ln));
             if (ln == 0) part[pp[b]][task % D3_ROWS] = v;
         }
     }
+    if (sh_dn != nullptr) {   // the shared expert's tasks from its own dense Q8_0 matrix (q8s sums), one copy of the code
+#pragma unroll 1
+        for (int b = 0; b < NB; ++b) {
+            const int task = g + b * GROUPS;
+            if (task < ntask && pp[b] == K) {
+                const float v = group_sum<LPR>(q8s_dot<LPR>(q80_planes(sh_dn, H, ff), row0 + task % D3_ROWS, ff, ln, a, K));
+                if (ln == 0) part[K][task % D3_ROWS] = v;
+            }
+        }
+    }
     // windows with more tasks than one batch (K > 11): the rest, a batch at a time
     for (int t0 = g + NB * GROUPS; t0 < ntask; t0 += GROUPS) {
         const int j = t0 / D3_ROWS, r = t0 % D3_ROWS, e = __shfl(tp, j < nr ? j : 0), q = j < nr ? j : K;
-        typename RowOf<TYPE, G2>::R w1;
-        RowOf<TYPE, G2>::load(w1, A + (size_t) (j < nr ? e : E) * sa, H, row0 + r, ff, ln);
-        const float v = group_sum<LPR>(w1.dot(a, q, ln));
+        float v;
+        if (sh_dn != nullptr && j >= nr) {
+            v = group_sum<LPR>(q8s_dot<LPR>(q80_planes(sh_dn, H, ff), row0 + r, ff, ln, a, K));
+        } else {
+            typename RowOf<TYPE, G2>::R w1;
+            RowOf<TYPE, G2>::load(w1, A + (size_t) (j < nr ? e : E) * sa, H, row0 + r, ff, ln);
+            v = group_sum<LPR>(w1.dot(a, q, ln));
+        }
         if (ln == 0) part[q][r] = v;
     }
     __syncthreads();
@@ -653,6 +693,8 @@ struct DecArgs {
     float eps;
     int phases;
     const float* Wn;   // the next layer's router (warmed into L2 for that layer's K1), or null
+    const uint8_t* sh_gu = nullptr;   // this layer's shared expert as its own dense Q8_0 matrices, or null
+    const uint8_t* sh_dn = nullptr;
 };
 
 // Optional kernel clock: when on, each decode kernel is launched with a start/stop event pair that the runtime
@@ -688,7 +730,7 @@ void launch_k2(const DecArgs& d, const sfnx_moe_layer_w& w, const DecLayout& L, 
             (const uint8_t*) w.gu, w.gu_stride, d.T, d.H, d.E, d.K, d.ff, d.shared, (const float*) (ws + L.logits),
             (const uint8_t*) (ws + L.xq), (int*) (ws + L.topi), (float*) (ws + L.topw), (sfnx_job*) (ws + L.jg),
             (sfnx_job*) (ws + L.jd), (int*) (ws + L.njobs), (float*) (ws + L.gu), (int8_t*) (ws + L.hq_q),
-            (float*) (ws + L.hq_d), (int*) (ws + L.hq_s));
+            (float*) (ws + L.hq_d), (int*) (ws + L.hq_s), d.sh_gu);
     }
 }
 template <int TYPE, int G, int NV>
@@ -698,7 +740,7 @@ void launch_k2_one(const DecArgs& d, const sfnx_moe_layer_w& w, const DecLayout&
         (const uint8_t*) w.gu, w.gu_stride, d.Wn, d.H, d.E, d.K, d.ff, d.shared, (const float*) (ws + L.logits),
         (const uint8_t*) (ws + L.xq), (int*) (ws + L.topi), (float*) (ws + L.topw), (sfnx_job*) (ws + L.jg),
         (sfnx_job*) (ws + L.jd), (int*) (ws + L.njobs), (float*) (ws + L.gu), (int8_t*) (ws + L.hq_q),
-        (float*) (ws + L.hq_d), (int*) (ws + L.hq_s), (int*) (ws + L.route_x));
+        (float*) (ws + L.hq_d), (int*) (ws + L.hq_s), (int*) (ws + L.route_x), d.sh_gu);
 }
 template <int TYPE, int G>
 void launch_k2_tt1(const DecArgs& d, const sfnx_moe_layer_w& w, const DecLayout& L, char* ws, hipStream_t s) {
@@ -712,7 +754,8 @@ void launch_k3_one(const DecArgs& d, const sfnx_moe_layer_w& w, float* x, const 
     launch(2, k_dec_down1<TYPE, G2, NB>, dim3(d.H / D3_ROWS), dim3(D3_THREADS), acts_bytes(d.K + 1, d.ff), s,
         (const uint8_t*) w.dn, w.dn_stride, d.H, d.E, d.K, d.ff, d.shared, (const float*) (ws + L.logits),
         (const int*) (ws + L.topi), (const float*) (ws + L.topw), (const int8_t*) (ws + L.hq_q),
-        (const float*) (ws + L.hq_d), (const int*) (ws + L.hq_s), (float*) (ws + L.y), x, (const int*) (ws + L.route_x));
+        (const float*) (ws + L.hq_d), (const int*) (ws + L.hq_s), (float*) (ws + L.y), x, (const int*) (ws + L.route_x),
+        d.sh_dn);
 }
 template <int TYPE, int G2, int NB>
 void launch_k3(const DecArgs& d, const sfnx_moe_layer_w& w, float* x, const DecLayout& L, char* ws, hipStream_t s) {
@@ -727,7 +770,7 @@ void launch_k3(const DecArgs& d, const sfnx_moe_layer_w& w, float* x, const DecL
         (const uint8_t*) w.dn, w.dn_stride, d.T, d.H, d.E, d.K, d.ff, d.shared, (const float*) (ws + L.logits),
         (const int*) (ws + L.topi), (const float*) (ws + L.topw), (const sfnx_job*) (ws + L.jd), (const int*) (ws + L.njobs),
         (const int8_t*) (ws + L.hq_q), (const float*) (ws + L.hq_d), (const int*) (ws + L.hq_s), (float*) (ws + L.y), x,
-        staged ? 1 : 0);
+        staged ? 1 : 0, d.sh_dn);
 }
 
 template <int TT>
@@ -824,10 +867,11 @@ extern "C" size_t sfnx_moe_decode_workspace(int T, int H, int E, int K, int ff, 
     return L.total;
 }
 
-extern "C" int sfnx_moe_decode2(const sfnx_moe_layer_w* layers, int n_layers, uint32_t gu_type, uint32_t dn_type, int H,
-                                int E, int K, int ff, int shared, float* x, int T, int norm, float eps, void* ws,
-                                size_t ws_bytes, int phases, void* st) {
-    return guarded("sfnx_moe_decode", [&] {
+namespace {
+void moe_decode(const sfnx_moe_layer_w* layers, const sfnx_moe_shared_q8s* sh, int n_layers, uint32_t gu_type,
+                uint32_t dn_type, int H, int E, int K, int ff, int shared, float* x, int T, int norm, float eps, void* ws,
+                size_t ws_bytes, int phases, void* st) {
+    {
         const uint32_t type = gu_type;
         require(expert_type_ok(gu_type) && expert_type_ok(dn_type), TYPE_MSG);
         require(T >= 1 && T <= SFNX_MAXT, "T out of range (1..16)");
@@ -843,6 +887,7 @@ extern "C" int sfnx_moe_decode2(const sfnx_moe_layer_w* layers, int n_layers, ui
             require(layers[l].W && layers[l].gu && layers[l].dn, "a layer's weights are missing");
             require(layers[l].gu_stride >= row_bytes(type, H) * 2 * (size_t) ff, "gate|up stride smaller than a matrix");
             require(layers[l].dn_stride >= row_bytes(dn_type, ff) * (size_t) H, "down stride smaller than a matrix");
+            if (sh) require(sh[l].gu != nullptr && sh[l].dn != nullptr, "a layer's shared expert matrices are missing");
         }
         const DecArgs d{gu_type, dn_type, H, E, K, ff, shared ? 1 : 0, T, norm ? 1 : 0, eps, phases ? phases : 7, nullptr};
         hipStream_t s = stream_of(st);
@@ -850,10 +895,32 @@ extern "C" int sfnx_moe_decode2(const sfnx_moe_layer_w* layers, int n_layers, ui
         for (int l = 0; l < n_layers; ++l) {
             DecArgs dl = d;
             dl.Wn = l + 1 < n_layers ? layers[l + 1].W : nullptr;
+            if (sh) {
+                dl.sh_gu = (const uint8_t*) sh[l].gu;
+                dl.sh_dn = (const uint8_t*) sh[l].dn;
+            }
             if (T == 1) launch_layer_tt<1>(dl, layers[l], x, L, w, s);
             else if (T <= 4) launch_layer_tt<4>(dl, layers[l], x, L, w, s);
             else launch_layer_tt<16>(dl, layers[l], x, L, w, s);
         }
+    }
+}
+}  // namespace
+
+extern "C" int sfnx_moe_decode2(const sfnx_moe_layer_w* layers, int n_layers, uint32_t gu_type, uint32_t dn_type, int H,
+                                int E, int K, int ff, int shared, float* x, int T, int norm, float eps, void* ws,
+                                size_t ws_bytes, int phases, void* st) {
+    return guarded("sfnx_moe_decode", [&] {
+        moe_decode(layers, nullptr, n_layers, gu_type, dn_type, H, E, K, ff, shared, x, T, norm, eps, ws, ws_bytes, phases, st);
+    });
+}
+
+extern "C" int sfnx_moe_decode_q8s(const sfnx_moe_layer_w* layers, const sfnx_moe_shared_q8s* shared_w, int n_layers,
+                                   uint32_t gu_type, uint32_t dn_type, int H, int E, int K, int ff, float* x, int T,
+                                   int norm, float eps, void* ws, size_t ws_bytes, int phases, void* st) {
+    return guarded("sfnx_moe_decode_q8s", [&] {
+        require(shared_w != nullptr || n_layers == 0, "no shared expert matrices");
+        moe_decode(layers, shared_w, n_layers, gu_type, dn_type, H, E, K, ff, 1, x, T, norm, eps, ws, ws_bytes, phases, st);
     });
 }
 

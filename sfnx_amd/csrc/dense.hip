@@ -1,0 +1,72 @@
+// The shared expert as the reference runs it when the model holds it as dense Q8_0 matrices (src/engine.cu:936-945):
+// q8s_gemv of the q8_1 activations through gate|up, swiglu_stacked_q8_1, q8s_gemv of h through down into part rows
+// P + t.  The dot is the reference's q8s sum (src/dense.cuh:24-154), here with 32 lanes a row as there; the fused
+// decode computes the same sums on its own lane groups (q8s_dot in mv.hpp).
+#include "mv.hpp"
+
+namespace sfnx {
+namespace {
+
+constexpr int QS_THREADS = 256, QS_LPR = 32, QS_ROWS = QS_THREADS / QS_LPR, QS_TT = 4;
+
+// a block of QS_ROWS rows; the activation rows staged QS_TT at a time
+__global__ void __launch_bounds__(QS_THREADS) k_q8s_gemv(const uint8_t* __restrict__ W, int rows, int cols,
+                                                        const uint8_t* __restrict__ y, float* __restrict__ out,
+                                                        int out_stride, int T) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    const Acts a = acts_in(lds, QS_TT, cols);
+    const Q80Planes P = q80_planes(W, rows, cols);
+    const int row = blockIdx.x * QS_ROWS + threadIdx.x / QS_LPR, ln = threadIdx.x % QS_LPR;
+    for (int t0 = 0; t0 < T; t0 += QS_TT) {
+        const int nn = min(QS_TT, T - t0);
+        if (t0) __syncthreads();
+        stage_q8_1(a, y + (size_t) t0 * (cols / 32) * Q81_BYTES, nullptr, nn);
+        __syncthreads();
+        for (int j = 0; j < nn; ++j) {
+            const float v = group_sum<QS_LPR>(row < rows ? q8s_dot<QS_LPR>(P, row, cols, ln, a, j) : 0.f);
+            if (row < rows && ln == 0) out[(size_t) (t0 + j) * out_stride + row] = v;
+        }
+    }
+}
+
+// src/kernels.cu:1948-1963 k_swiglu_stacked: a half-wave per (row t, 32 values)
+__global__ void k_swiglu_stacked(const float* __restrict__ gu, uint8_t* __restrict__ hq, int ffs, int T) {
+    const int t = blockIdx.y, b = blockIdx.x * (blockDim.x / 32) + threadIdx.x / 32, l = threadIdx.x % 32;
+    if (b >= ffs / 32) return;   // whole half-waves leave together
+    const float* g = gu + (size_t) t * 2 * ffs;
+    const float xi = silu_f(g[32 * b + l]) * g[ffs + 32 * b + l];
+    const float amax = group_max<32>(fabsf(xi)), sum = group_sum<32>(xi);
+    const float d = amax / 127.0f;
+    uint8_t* blk = hq + ((size_t) t * (ffs / 32) + b) * Q81_BYTES;
+    blk[4 + l] = (uint8_t) (int8_t) (amax == 0.0f ? 0 : (int) roundf(xi / d));
+    if (l == 0) *reinterpret_cast<uint32_t*>(blk) = (uint32_t) f2h(d) | ((uint32_t) f2h(sum) << 16);
+}
+
+}  // namespace
+}  // namespace sfnx
+
+using namespace sfnx;
+
+extern "C" int sfnx_q8s_gemv(const void* W, int rows, int cols, const void* y, float* out, int out_stride, int T, void* st) {
+    return guarded("sfnx_q8s_gemv", [&] {
+        require(W != nullptr && y != nullptr && out != nullptr, "null pointer");
+        require(rows > 0 && rows % 32 == 0, "rows must be a positive multiple of 32");
+        require(cols > 0 && cols % 512 == 0, "cols must be a positive multiple of 512");
+        require(T >= 1 && T <= 65535, "T out of range");
+        require(out_stride >= rows, "out_stride smaller than rows");
+        const size_t lds = acts_bytes(QS_TT, cols);
+        require(lds <= 64 * 1024, "cols too wide for the activation staging");
+        k_q8s_gemv<<<(rows + QS_ROWS - 1) / QS_ROWS, QS_THREADS, lds, stream_of(st)>>>(
+            (const uint8_t*) W, rows, cols, (const uint8_t*) y, out, out_stride, T);
+    });
+}
+
+extern "C" int sfnx_swiglu_stacked_q8_1(const float* gu, void* hq, int ffs, int T, void* st) {
+    return guarded("sfnx_swiglu_stacked_q8_1", [&] {
+        require(gu != nullptr && hq != nullptr, "null pointer");
+        require(ffs > 0 && ffs % 32 == 0, "ffs must be a positive multiple of 32");
+        require(T >= 1 && T <= 65535, "T out of range");
+        const dim3 grid((ffs / 32 + 7) / 8, T);
+        k_swiglu_stacked<<<grid, 256, 0, stream_of(st)>>>(gu, (uint8_t*) hq, ffs, T);
+    });
+}

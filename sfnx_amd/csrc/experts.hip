@@ -95,7 +95,9 @@ void moe_mv(uint32_t type, const void* A, size_t sa, int n_in, int n_out, const 
     require(njobs_max >= 0 && njobs_max <= 65535, "njobs_max out of range");
     if (njobs_max == 0) return;
     const int G = n_in / 512;
-    const int TT = T <= 1 ? 1 : T <= 4 ? 4 : 16;
+    // activation rows staged per pass: up to 16 while they fit 64 KiB of LDS (the kernel loops over the passes)
+    int TT = T <= 1 ? 1 : T <= 4 ? 4 : 16;
+    if (acts_bytes(TT, n_in) > 64 * 1024) TT = 4;
     const size_t lds = acts_bytes(TT, n_in);
     require(lds <= 64 * 1024, "activation rows do not fit the LDS budget");
     const int rpb = MV_THREADS / (is_kquant(type) ? 8 : 16);

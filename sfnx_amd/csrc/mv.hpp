@@ -274,4 +274,38 @@ template <int BPL, int TYPE> struct NbRow {
     }
 };
 
+// ------------------------------------------------------------------------------------------------ dense Q8_0 (q8s)
+// The shared expert's dense Q8_0 rows as the reference computes them (src/dense.cuh:24-154 q8s_block): 32 lanes a
+// row, lane L the 16-column halves c = 16 L + 512 i in order, acc_L = fmaf(d_w d_a, sum of the 16 products, acc_L),
+// then v += shfl_xor(v, o) for o = 16 .. 1.  Here LPR physical lanes carry the 32 logical ones, L = ln + LPR k, and
+// fold theirs in the butterfly's order (xor 16 and 8 are k ^ 2 and k ^ 1 for LPR 8, xor 16 is k ^ 1 for LPR 16), so
+// group_sum<LPR> of the result finishes exactly the reference's sum.  Weights in the planar Q8_0 layout: the half h of
+// block b is piece 32 (b / 16) + 16 h + b % 16, so logical lane L's i-th piece is 32 i + 16 (L & 1) + L / 2.  Read
+// straight from memory (the shared expert is one job of a launch; no register copy of the row is kept).
+template <int LPR> __device__ __forceinline__ float q8s_dot(const Q80Planes& P, int row, int C, int ln, const Acts& a, int j) {
+    static_assert(LPR == 8 || LPR == 16 || LPR == 32, "q8s lanes");
+    constexpr int NL = 32 / LPR;
+    const int nb = C / 32;
+    float acc[NL];
+#pragma unroll
+    for (int k = 0; k < NL; ++k) acc[k] = 0.f;
+    for (int i = 0; i < C / 512; ++i) {
+#pragma unroll
+        for (int k = 0; k < NL; ++k) {
+            const int L = ln + LPR * k, h = L & 1, b = 16 * i + L / 2;
+            const uint4 w = *reinterpret_cast<const uint4*>(P.q16(row, C, 32 * i + 16 * h + L / 2));
+            const float dw = h2f(*P.dof(row, C, b));
+            const int4 av = a.q4(j, b)[h];
+            int s = dot4((int) w.x, av.x, 0);
+            s = dot4((int) w.y, av.y, s);
+            s = dot4((int) w.z, av.z, s);
+            s = dot4((int) w.w, av.w, s);
+            acc[k] = fmaf(dw * a.d[j * nb + b], (float) s, acc[k]);
+        }
+    }
+    if constexpr (NL == 4) return (acc[0] + acc[2]) + (acc[1] + acc[3]);
+    else if constexpr (NL == 2) return acc[0] + acc[1];
+    else return acc[0];
+}
+
 }  // namespace sfnx

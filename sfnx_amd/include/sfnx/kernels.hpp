@@ -17,7 +17,9 @@ namespace sfnx {
 using Job = sfnx_job;         // src/kernels.hpp:18-23
 using BigJob = sfnx_bigjob;   // src/kernels.hpp:25-32
 constexpr int MAXT = SFNX_MAXT, PF_JOB = SFNX_PF_JOB;
-enum GgmlType : uint32_t { T_Q8_0 = SFNX_Q8_0, T_Q4_K = SFNX_Q4_K, T_Q5_K = SFNX_Q5_K };   // src/gguf.hpp:22-25
+enum GgmlType : uint32_t {   // src/gguf.hpp:22-25
+    T_Q4_0 = SFNX_Q4_0, T_Q5_1 = SFNX_Q5_1, T_Q8_0 = SFNX_Q8_0, T_Q4_K = SFNX_Q4_K, T_Q5_K = SFNX_Q5_K
+};
 
 // src/model.hpp:78-87 DW: one matrix (or expert 0's of a stack), n_out rows of n_in
 struct DW {
@@ -78,6 +80,18 @@ inline void moe_combine(const MoeShape& s, const float* part, const float* topw,
                         float* y, int T, void* st, bool shared = true) {
     ck(sfnx_moe_combine(part, topw, topi, logits, y, T, s.H, s.E, s.K, shared ? 1 : 0, st));
 }
+
+// src/model.hpp:72-76 Q8S: a dense Q8_0 matrix (here the planar Q8_0 layout of one matrix)
+struct Q8S {
+    const void* p = nullptr;
+};
+
+// src/kernels.hpp:47 (src/dense.cuh:24-154): the shared expert's dense Q8_0 product in the reference's q8s sums
+inline void q8s_gemv(const Q8S& w, int rows, int cols, const void* y, float* out, int out_stride, int T, void* st) {
+    ck(sfnx_q8s_gemv(w.p, rows, cols, y, out, out_stride, T, st));
+}
+// src/kernels.cu:2018-2024
+inline void swiglu_stacked_q8_1(const float* gu, void* hq, int ffs, int T, void* st) { ck(sfnx_swiglu_stacked_q8_1(gu, hq, ffs, T, st)); }
 
 static_assert(sizeof(Job) == 136 && sizeof(BigJob) == 520, "job layouts match the reference's");
 

@@ -12,7 +12,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _abi
-from ._abi import BIGJOB_INTS, JOB_INTS, Q4_0, Q4_K, Q5_1, Q5_K, Q8_0, check, lib
+from ._abi import BIGJOB_INTS, JOB_INTS, PF_JOB, Q4_0, Q4_K, Q5_1, Q5_K, Q8_0, check, lib
 
 
 def _p(t):
@@ -118,6 +118,17 @@ def moe_combine(part, topw, topi, logits, y, E: int, K: int, shared: bool = True
     check(lib().sfnx_moe_combine(_p(part), _p(topw), _p(topi), _p(logits), _p(y), T, H, E, K, int(shared), _st()))
 
 
+def q8s_gemv(W, rows: int, cols: int, y, out, out_stride: int, T: int) -> None:
+    """src/kernels.hpp:47: out[t][r] = dense Q8_0 row r of W (planar, one matrix) . q8_1 row t of y, the reference's
+    q8s sums (src/dense.cuh:24-154); out rows out_stride floats apart"""
+    check(lib().sfnx_q8s_gemv(_p(W), rows, cols, _p(y), _p(out), out_stride, T, _st()))
+
+
+def swiglu_stacked_q8_1(gu, hq, ffs: int, T: int) -> None:
+    """src/kernels.cu:2018: hq row t (q8_1) = silu(gate) * up of gu row t ([gate | up], 2 ffs floats)"""
+    check(lib().sfnx_swiglu_stacked_q8_1(_p(gu), _p(hq), ffs, T, _st()))
+
+
 def residual_rmsnorm(x, y, xn, eps: float = 1e-6) -> None:
     """x += y (y may be None), xn = x / sqrt(mean(x^2) + eps): the glue between stacked layers"""
     T, H = x.shape
@@ -146,6 +157,14 @@ class LayerShape:
     wtype: int = Q4_K
     shared: bool = True
     dn_wtype: int | None = None   # the down matrices' type when it differs from gate|up's (the reference's DW per matrix)
+    # the shared expert as its own dense Q8_0 matrices in the reference's q8s arithmetic (src/model.hpp:83 DW::s,
+    # src/engine.cu:936-945); the routed stores then hold E experts.  Else it is expert E of the routed stores.
+    sh_q8s: bool = False
+
+    @property
+    def n_routed(self) -> int:
+        """experts in the routed stores"""
+        return self.E + (0 if self.sh_q8s else 1)
 
     @property
     def dn_type(self) -> int:
@@ -156,28 +175,41 @@ class MoeLayer:
     """One MoE layer's weights resident in HBM (planar store) plus the buffers its entry points write.
 
     gu_w: experts' gate|up [E+1][2 ff][H] (expert E is the shared one), dn_w: down [E+1][H][ff], W: router [E+1][H].
+    With shape.sh_q8s the stores hold E experts and sh_gu [2 ff][H], sh_dn [H][ff] (planar Q8_0) the shared expert.
     """
 
-    def __init__(self, shape: LayerShape, W: torch.Tensor, gu_w: torch.Tensor, dn_w: torch.Tensor):
+    def __init__(self, shape: LayerShape, W: torch.Tensor, gu_w: torch.Tensor, dn_w: torch.Tensor,
+                 sh_gu: torch.Tensor | None = None, sh_dn: torch.Tensor | None = None):
+        if shape.sh_q8s and (sh_gu is None or sh_dn is None or not shape.shared):
+            raise ValueError("a q8s shared expert needs shared=True and both matrices")
         self.s = shape
         self.W, self.gu_w, self.dn_w = W, gu_w, dn_w
+        self.sh_gu, self.sh_dn = sh_gu, sh_dn
         self.gu_stride = 2 * shape.ff * row_bytes(shape.wtype, shape.H)
         self.dn_stride = shape.H * row_bytes(shape.dn_type, shape.ff)
 
     @staticmethod
-    def planar_from_gguf(shape: LayerShape, W: torch.Tensor, gu_gguf: torch.Tensor, dn_gguf: torch.Tensor) -> "MoeLayer":
+    def planar_from_gguf(shape: LayerShape, W: torch.Tensor, gu_gguf: torch.Tensor, dn_gguf: torch.Tensor,
+                         sh_gu_gguf: torch.Tensor | None = None, sh_dn_gguf: torch.Tensor | None = None) -> "MoeLayer":
+        """the GGUF blocks of n_routed experts (and, with sh_q8s, the shared expert's Q8_0 blocks) into the store"""
         s = shape
         gu = torch.empty_like(gu_gguf)
         dn = torch.empty_like(dn_gguf)
-        store_pack(s.wtype, gu_gguf, gu, s.E + 1, 2 * s.ff, s.H)
-        store_pack(s.dn_type, dn_gguf, dn, s.E + 1, s.H, s.ff)
-        return MoeLayer(s, W, gu, dn)
+        store_pack(s.wtype, gu_gguf, gu, s.n_routed, 2 * s.ff, s.H)
+        store_pack(s.dn_type, dn_gguf, dn, s.n_routed, s.H, s.ff)
+        sh_gu = sh_dn = None
+        if s.sh_q8s:
+            sh_gu, sh_dn = torch.empty_like(sh_gu_gguf), torch.empty_like(sh_dn_gguf)
+            store_pack(Q8_0, sh_gu_gguf, sh_gu, 1, 2 * s.ff, s.H)
+            store_pack(Q8_0, sh_dn_gguf, sh_dn, 1, s.H, s.ff)
+        return MoeLayer(s, W, gu, dn, sh_gu, sh_dn)
 
     @staticmethod
     def synthetic(shape: LayerShape, seed: int, device="cuda", chunk_experts: int = 64) -> "MoeLayer":
-        """Seeded layer: router N(0, 0.02) fp32; experts N(0, 0.02) quantized by the library's quantizer and packed."""
+        """Seeded layer: router N(0, 0.02) fp32; experts N(0, 0.02) quantized by the library's quantizer and packed.
+        A q8s shared expert takes expert E's values of the same streams, quantized to Q8_0."""
         s = shape
-        E1 = s.E + 1
+        E1 = s.n_routed
         W = torch.empty((E1, s.H), dtype=torch.float32, device=device)
         synth_normal(W, seed * 1000 + 1, 0.02)
         gu_stride = 2 * s.ff * row_bytes(s.wtype, s.H)
@@ -196,8 +228,17 @@ class MoeLayer:
                 b = blk[: ne * stride]
                 quantize_weights(wt, t.view(ne * rows, cols), b)
                 store_pack(wt, b, dst[e0 * stride:(e0 + ne) * stride], ne, rows, cols)
+        sh = [None, None]
+        if s.sh_q8s:
+            for mat, (rows, cols, sd) in enumerate([(2 * s.ff, s.H, seed * 1000 + 2), (s.H, s.ff, seed * 1000 + 3)]):
+                t = tmp[: rows * cols]
+                synth_normal(t, sd, 0.02, offset=s.E * rows * cols)
+                b = blk[: rows * row_bytes(Q8_0, cols)]
+                quantize_weights(Q8_0, t.view(rows, cols), b)
+                sh[mat] = torch.empty_like(b)
+                store_pack(Q8_0, b, sh[mat], 1, rows, cols)
         del tmp, blk
-        return MoeLayer(s, W, gu, dn)
+        return MoeLayer(s, W, gu, dn, sh[0], sh[1])
 
 
 class DecodeBuffers:
@@ -220,6 +261,17 @@ class DecodeBuffers:
         self.njobs_max = nj
         self.gu = torch.zeros((NP, 2 * s.ff), dtype=torch.float32, device=device)
         self.part = torch.zeros((NP, s.H), dtype=torch.float32, device=device)
+        self.sh_hq = torch.zeros(T * (s.ff // 32) * 36, dtype=torch.uint8, device=device)   # the shared expert's h (q8_1)
+
+
+def shared_q8s(L: "MoeLayer", T: int, xq, gu, hq, part) -> None:
+    """the shared expert of a q8s layer for T rows, as src/engine.cu:942-944: q8s gate|up into gu rows P + t, SwiGLU to
+    q8_1, q8s down into part rows P + t"""
+    s = L.s
+    P = T * s.K
+    q8s_gemv(L.sh_gu, 2 * s.ff, s.H, xq, gu[P:P + T], 2 * s.ff, T)
+    swiglu_stacked_q8_1(gu[P:P + T], hq, s.ff, T)
+    q8s_gemv(L.sh_dn, s.H, s.ff, hq, part[P:P + T], s.H, T)
 
 
 def decode_layer(L: MoeLayer, x: torch.Tensor, y: torch.Tensor, b: DecodeBuffers) -> None:
@@ -227,9 +279,12 @@ def decode_layer(L: MoeLayer, x: torch.Tensor, y: torch.Tensor, b: DecodeBuffers
     s = L.s
     T = x.shape[0]
     quantize_q8_1(x, b.xq)
-    router_route(L.W, x, b.logits, b.topi, b.topw, b.jobs_gu, b.jobs_dn, b.njobs, s.E, s.K, s.shared)
+    # a q8s shared expert is no job of the routed experts (src/engine.cu:936-945)
+    router_route(L.W, x, b.logits, b.topi, b.topw, b.jobs_gu, b.jobs_dn, b.njobs, s.E, s.K, s.shared and not s.sh_q8s)
     moe_gate_up(L.gu_w, L.gu_stride, s.wtype, s.H, 2 * s.ff, b.jobs_gu, b.njobs, b.njobs_max, T, b.xq, b.gu)
     moe_down(L.dn_w, L.dn_stride, s.dn_type, s.ff, s.H, b.jobs_dn, b.njobs, b.njobs_max, T, b.gu, b.part)
+    if s.sh_q8s:
+        shared_q8s(L, T, b.xq, b.gu, b.sh_hq, b.part)
     moe_combine(b.part, b.topw, b.topi, b.logits, y, s.E, s.K, s.shared)
 
 
@@ -249,12 +304,21 @@ class FusedDecode:
         self.ws = torch.zeros(total, dtype=torch.uint8, device=device)
         self.table = (_abi.LayerW * len(layers))(*[
             _abi.LayerW(L.W.data_ptr(), L.gu_w.data_ptr(), L.gu_stride, L.dn_w.data_ptr(), L.dn_stride) for L in layers])
+        self.sh_table = None
+        if s.sh_q8s:
+            self.sh_table = (_abi.SharedQ8s * len(layers))(*[
+                _abi.SharedQ8s(L.sh_gu.data_ptr(), L.sh_dn.data_ptr()) for L in layers])
 
     def __call__(self, x: torch.Tensor, norm: bool = True, eps: float = 1e-6, layer0: int = 0,
                  n_layers: int | None = None, phases: int = 0) -> None:
         s = self.s
         n = len(self.layers) - layer0 if n_layers is None else n_layers
         table = C.cast(self.table, C.c_void_p).value + layer0 * C.sizeof(_abi.LayerW)
+        if self.sh_table is not None:
+            sh = C.cast(self.sh_table, C.c_void_p).value + layer0 * C.sizeof(_abi.SharedQ8s)
+            check(lib().sfnx_moe_decode_q8s(table, sh, n, s.wtype, s.dn_type, s.H, s.E, s.K, s.ff, _p(x), x.shape[0],
+                                            int(norm), eps, _p(self.ws), self.ws.numel(), phases, _st()))
+            return
         check(lib().sfnx_moe_decode2(table, n, s.wtype, s.dn_type, s.H, s.E, s.K, s.ff, int(s.shared), _p(x), x.shape[0],
                                      int(norm), eps, _p(self.ws), self.ws.numel(), phases, _st()))
 
@@ -291,6 +355,20 @@ class PrefillBuffers:
         self.part = torch.zeros((NP, s.H), dtype=torch.float32, device=device)
         self.xh = torch.zeros((C, s.H), dtype=torch.float16, device=device)
         self.h16 = torch.zeros((NP, s.ff), dtype=torch.float16, device=device)
+        if s.sh_q8s:   # the shared expert's own jobs (rows P + t), the layout k_pf_fill gives them (src/prefill.cu)
+            nsj = (C + PF_JOB - 1) // PF_JOB
+            gu = torch.zeros((nsj, BIGJOB_INTS), dtype=torch.int32)
+            for j in range(nsj):
+                n = min(PF_JOB, C - PF_JOB * j)
+                t = torch.arange(PF_JOB * j, PF_JOB * j + n, dtype=torch.int32)
+                gu[j, 0], gu[j, 1] = 0, n
+                gu[j, 2:2 + n] = t
+                gu[j, 2 + PF_JOB:2 + PF_JOB + n] = P + t
+            dn = gu.clone()
+            dn[:, 2:2 + PF_JOB] = dn[:, 2 + PF_JOB:]
+            self.sh_jobs_gu, self.sh_jobs_dn = gu.reshape(-1).to(device), dn.reshape(-1).to(device)
+            self.sh_njobs = torch.tensor([nsj, nsj], **i32)
+            self.sh_cap = nsj
 
 
 def prefill_route(L: "MoeLayer", x: torch.Tensor, b: "PrefillBuffers", bias: torch.Tensor | None = None) -> None:
@@ -300,7 +378,15 @@ def prefill_route(L: "MoeLayer", x: torch.Tensor, b: "PrefillBuffers", bias: tor
     router_logits(L.W, x, b.logits)
     if bias is not None:
         b.logits[:, : s.E] += bias
-    pf_route(b.logits, b.topi, b.topw, b.cnt, b.jbase, b.jobs_gu, b.jobs_dn, b.njobs, s.E, s.K, s.shared)
+    pf_route(b.logits, b.topi, b.topw, b.cnt, b.jbase, b.jobs_gu, b.jobs_dn, b.njobs, s.E, s.K, s.shared and not s.sh_q8s)
+
+
+def prefill_shared_mma(L: "MoeLayer", b: "PrefillBuffers") -> None:
+    """a q8s layer's shared expert for the chunk on the matrix cores, f16 products of its dequantized Q8_0 rows as the
+    reference's pf_dense_xh + k_pf_swiglu + pf_gemm (src/prefill.cu:1173-1177); needs b.xh"""
+    s = L.s
+    moe_gate_up_swiglu_mma(L.sh_gu, L.sh_gu.numel(), Q8_0, s.H, s.ff, b.sh_jobs_gu, b.sh_njobs, b.sh_cap, b.xh, b.h16)
+    moe_down_mma(L.sh_dn, L.sh_dn.numel(), Q8_0, s.ff, s.H, b.sh_jobs_dn, b.sh_njobs, b.sh_cap, b.h16, b.part)
 
 
 def prefill_experts_mma(L: "MoeLayer", x: torch.Tensor, y: torch.Tensor, b: "PrefillBuffers") -> None:
@@ -311,6 +397,8 @@ def prefill_experts_mma(L: "MoeLayer", x: torch.Tensor, y: torch.Tensor, b: "Pre
     moe_gate_up_mma(L.gu_w, L.gu_stride, s.wtype, s.H, 2 * s.ff, b.jobs_gu, b.njobs, b.cap, b.xh, b.gu)
     swiglu_h16(b.gu, b.h16, s.ff)
     moe_down_mma(L.dn_w, L.dn_stride, s.dn_type, s.ff, s.H, b.jobs_dn, b.njobs, b.cap, b.h16, b.part)
+    if s.sh_q8s:
+        prefill_shared_mma(L, b)
     moe_combine(b.part, b.topw, b.topi, b.logits, y, s.E, s.K, s.shared)
 
 
@@ -323,6 +411,8 @@ def prefill_layer_mma(L: "MoeLayer", x: torch.Tensor, y: torch.Tensor, b: "Prefi
     to_f16(x, b.xh)
     moe_gate_up_swiglu_mma(L.gu_w, L.gu_stride, s.wtype, s.H, s.ff, b.jobs_gu, b.njobs, b.cap, b.xh, b.h16)
     moe_down_mma(L.dn_w, L.dn_stride, s.dn_type, s.ff, s.H, b.jobs_dn, b.njobs, b.cap, b.h16, b.part)
+    if s.sh_q8s:
+        prefill_shared_mma(L, b)
     moe_combine(b.part, b.topw, b.topi, b.logits, y, s.E, s.K, s.shared)
 
 
@@ -331,9 +421,12 @@ def prefill_layer_q8(L: MoeLayer, x: torch.Tensor, y: torch.Tensor, b: PrefillBu
     s = L.s
     quantize_q8_1(x, b.xq)
     router_logits(L.W, x, b.logits)
-    pf_route(b.logits, b.topi, b.topw, b.cnt, b.jbase, b.jobs_gu, b.jobs_dn, b.njobs, s.E, s.K, s.shared)
+    pf_route(b.logits, b.topi, b.topw, b.cnt, b.jbase, b.jobs_gu, b.jobs_dn, b.njobs, s.E, s.K, s.shared and not s.sh_q8s)
     moe_gate_up_big(L.gu_w, L.gu_stride, s.wtype, s.H, 2 * s.ff, b.jobs_gu, b.njobs, b.cap, b.xq, b.gu)
     moe_down_big(L.dn_w, L.dn_stride, s.dn_type, s.ff, s.H, b.jobs_dn, b.njobs, b.cap, b.gu, b.part)
+    if s.sh_q8s:   # the reference's shared expert is the f16 dense path on this path too (src/prefill.cu:1173-1177)
+        to_f16(x, b.xh)
+        prefill_shared_mma(L, b)
     moe_combine(b.part, b.topw, b.topi, b.logits, y, s.E, s.K, s.shared)
 
 

@@ -34,10 +34,21 @@ def make_layer(shape: moe.LayerShape, seed: int, device="cuda"):
             moe.synth_normal(tmp[:n], sd, 0.02, offset=off)
             r0 = off // cols
             moe.quantize_weights(wt, tmp[:n].view(n // cols, cols), dst[r0 * rb:(r0 + n // cols) * rb])
-    L = moe.MoeLayer.planar_from_gguf(s, W, gu_g, dn_g)
+    sh = [None, None]
+    if s.sh_q8s:   # the shared expert as dense Q8_0: expert E's values of the same streams
+        for i, (rows, cols, sd) in enumerate(((2 * s.ff, s.H, seed * 1000 + 2), (s.H, s.ff, seed * 1000 + 3))):
+            tmp = torch.empty(rows * cols, dtype=torch.float32, device=device)
+            moe.synth_normal(tmp, sd, 0.02, offset=s.E * rows * cols)
+            sh[i] = torch.empty(rows * moe.row_bytes(orc.Q8_0, cols), dtype=torch.uint8, device=device)
+            moe.quantize_weights(orc.Q8_0, tmp.view(rows, cols), sh[i])
+        # the routed stores hold E experts: nothing may read an expert E
+        L = moe.MoeLayer.planar_from_gguf(s, W, gu_g[: s.E * gu_stride], dn_g[: s.E * dn_stride], sh[0], sh[1])
+    else:
+        L = moe.MoeLayer.planar_from_gguf(s, W, gu_g, dn_g)
     torch.cuda.synchronize()
     host = orc.LayerWeights(W.cpu().numpy(), gu_g.cpu().numpy(), dn_g.cpu().numpy(), s.wtype, s.H, s.E, s.K, s.ff,
-                            s.shared, dn_type=s.dn_type)
+                            s.shared, dn_type=s.dn_type, sh_gu=None if sh[0] is None else sh[0].cpu().numpy(),
+                            sh_dn=None if sh[1] is None else sh[1].cpu().numpy())
     return L, host
 
 
