@@ -236,6 +236,12 @@ int sfnx_gguf_str(const sfnx_gguf* g, const char* key, const char** v);         
  * gate|up type, H, E, ff1 - ff0, shared and the down type.  A loader, not a hot-path call: it allocates a staging buffer and synchronises the stream. */
 int sfnx_gguf_moe_layer(const sfnx_gguf* g, int layer, int ff0, int ff1, void* gu, size_t gu_stride, void* dn,
                         size_t dn_stride, float* W, int* info, void* st);
+/* sfnx_gguf_moe_layer for the model as the reference loads it (src/model.cpp:807-809): the shared expert must be
+ * present and Q8_0 ("the shared expert is not Q8_0" otherwise) and goes, as dense matrices, to sh_gu ([2 ffs][H]) and
+ * sh_dn ([H][ffs], columns ff0..ff1), each the planar Q8_0 layout of one matrix, for sfnx_moe_decode_q8s and
+ * sfnx_q8s_gemv; gu and dn then receive the E routed experts only.  W and info as sfnx_gguf_moe_layer. */
+int sfnx_gguf_moe_layer_q8s(const sfnx_gguf* g, int layer, int ff0, int ff1, void* gu, size_t gu_stride, void* dn,
+                            size_t dn_stride, float* W, void* sh_gu, void* sh_dn, int* info, void* st);
 
 #ifdef __cplusplus
 }

@@ -63,6 +63,7 @@ SIGNATURES = {
     "sfnx_gguf_float": (i32, [vp, C.c_char_p, vp]),
     "sfnx_gguf_str": (i32, [vp, C.c_char_p, vp]),
     "sfnx_gguf_moe_layer": (i32, [vp, i32, i32, i32, vp, sz, vp, sz, vp, vp, vp]),
+    "sfnx_gguf_moe_layer_q8s": (i32, [vp, i32, i32, i32, vp, sz, vp, sz, vp, vp, vp, vp, vp]),
 }
 
 

@@ -11,6 +11,7 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <algorithm>
 #include <cstring>
 #include <map>
 #include <memory>
@@ -340,95 +341,123 @@ extern "C" int sfnx_gguf_str(const sfnx_gguf* g, const char* key, const char** v
     return st != 0 ? st : found;
 }
 
+namespace {
+// sh_gu null: the shared expert (when present, of the routed types) is expert E of gu / dn.  Else the shared expert
+// must be present and Q8_0 (src/model.cpp:807-809 throws otherwise) and goes to sh_gu [2 ffs][H] / sh_dn [H][ffs].
+void moe_layer(const sfnx_gguf* g, int layer, int ff0, int ff1, void* gu, size_t gu_stride, void* dn, size_t dn_stride,
+               float* W, void* sh_gu, void* sh_dn, int* info, void* st) {
+    require(g != nullptr && gu != nullptr && dn != nullptr && W != nullptr, "null argument");
+    const bool q8s = sh_gu != nullptr;
+    require(!q8s || sh_dn != nullptr, "null argument");
+    const std::string L = "blk." + std::to_string(layer) + ".";
+    const sfnx_gguf_tensor& tg = need(g, L + "ffn_gate_exps.weight");
+    const sfnx_gguf_tensor& tu = need(g, L + "ffn_up_exps.weight");
+    const sfnx_gguf_tensor& td = need(g, L + "ffn_down_exps.weight");
+    const sfnx_gguf_tensor& ti = need(g, L + "ffn_gate_inp.weight");
+    const uint32_t type = tg.type, dtype = td.type;   // gate|up stack into one store; down is its own (src/model.cpp:540-606)
+    require(expert_type_ok(type) && expert_type_ok(dtype), "expert tensors must be Q4_0, Q5_1, Q8_0, Q4_K or Q5_K");
+    require(tu.type == type, "gate and up experts differ in type (they stack into one matrix)");
+    const int64_t H = tg.ne[0], FF = tg.ne[1], E = tg.ne[2];
+    require(tu.ne[0] == H && tu.ne[1] == FF && tu.ne[2] == E, "up experts differ in shape from gate experts");
+    require(td.ne[0] == FF && td.ne[1] == H && td.ne[2] == E, "down experts are not [FF][H] a expert");
+    const int cb = block_values(dtype);   // a column slice of the down rows is whole blocks
+    require(0 <= ff0 && ff0 < ff1 && ff1 <= FF && ff0 % cb == 0 && (ff1 - ff0) % 512 == 0,
+            "FF slice must start on a whole block and span a multiple of 512 (the store's runs)");
+    require(H % 512 == 0, "the hidden size must be a multiple of 512 (the store's runs)");
+    require(ti.type == 0 && ti.ne[0] == H && ti.ne[1] == E, "ffn_gate_inp must be f32 [E][H]");
+    const int ffs = ff1 - ff0;
+    const size_t rb_in = row_bytes(type, (int) H), rb_ff = row_bytes(dtype, ffs);
+    require(gu_stride >= 2 * (size_t) ffs * rb_in && dn_stride >= (size_t) H * rb_ff, "strides smaller than a matrix");
+    const sfnx_gguf_tensor* sg = find(g, L + "ffn_gate_shexp.weight");
+    const sfnx_gguf_tensor* su = find(g, L + "ffn_up_shexp.weight");
+    const sfnx_gguf_tensor* sd = find(g, L + "ffn_down_shexp.weight");
+    const sfnx_gguf_tensor* sgi = find(g, L + "ffn_gate_inp_shexp.weight");
+    const bool shared = sg && su && sd && sgi;
+    require(shared || !q8s, "the layer has no shared expert (ffn_{gate,up,down,gate_inp}_shexp)");
+    // the shared expert's types: Q8_0 for the dense path, else those of the routed stores it joins
+    const uint32_t stype = q8s ? (uint32_t) SFNX_Q8_0 : type, sdtype = q8s ? (uint32_t) SFNX_Q8_0 : dtype;
+    if (shared) {
+        if (q8s)
+            require(sg->type == SFNX_Q8_0 && su->type == SFNX_Q8_0 && sd->type == SFNX_Q8_0, "the shared expert is not Q8_0");
+        else
+            require(sg->type == type && su->type == type && sd->type == dtype,
+                    "the shared expert's types differ from the routed experts' (it is one more expert of their stores)");
+        require(sg->ne[0] == H && sg->ne[1] == FF && su->ne[0] == H && su->ne[1] == FF && sd->ne[0] == FF &&
+                    sd->ne[1] == H, "the shared expert's shape differs from a routed expert's");
+        require(sgi->type == 0 && sgi->ne[0] == H && sgi->ne[1] == 1, "ffn_gate_inp_shexp must be f32 [1][H]");
+    }
+    const int64_t NE = E + (shared ? 1 : 0);
+    hipStream_t s = stream_of(st);
+    // one expert's matrices at a time in GGUF layout through a pinned host buffer and a device buffer, then packed
+    const size_t gu_bytes = 2 * (size_t) ffs * rb_in, dn_bytes = (size_t) H * rb_ff;
+    const size_t sgu_bytes = 2 * (size_t) ffs * row_bytes(stype, (int) H), sdn_bytes = (size_t) H * row_bytes(sdtype, ffs);
+    const size_t stage = std::max(gu_bytes, sgu_bytes) + std::max(dn_bytes, sdn_bytes);
+    void *host = nullptr, *dev = nullptr;
+    check(hipHostMalloc(&host, stage, hipHostMallocDefault), "hipHostMalloc");
+    const hipError_t ea = hipMalloc(&dev, stage);
+    if (ea != hipSuccess) {
+        (void) hipHostFree(host);
+        check(ea, "hipMalloc");
+    }
+    auto cleanup = [&] {
+        (void) hipStreamSynchronize(s);
+        (void) hipFree(dev);
+        (void) hipHostFree(host);
+    };
+    try {
+        uint8_t* h = (uint8_t*) host;
+        for (int64_t e = 0; e < NE; ++e) {
+            const bool sh = e == E;
+            const uint32_t gt = sh ? stype : type, dt = sh ? sdtype : dtype;
+            const size_t rbi = row_bytes(gt, (int) H), rbf = row_bytes(dt, ffs), rb_full_dn = row_bytes(dt, (int) FF);
+            const size_t col0 = row_bytes(dt, ff0), gub = 2 * (size_t) ffs * rbi;
+            const uint8_t* g0 = (const uint8_t*) (sh ? sg->data : tg.data) + (sh ? 0 : e * FF * rbi);
+            const uint8_t* u0 = (const uint8_t*) (sh ? su->data : tu.data) + (sh ? 0 : e * FF * rbi);
+            const uint8_t* d0 = (const uint8_t*) (sh ? sd->data : td.data) + (sh ? 0 : e * H * rb_full_dn);
+            check(hipStreamSynchronize(s), "hipStreamSynchronize");   // the buffers are free again
+            // gate rows ff0..ff1, then up rows ff0..ff1 (src/model.cpp:554-576)
+            std::memcpy(h, g0 + (size_t) ff0 * rbi, (size_t) ffs * rbi);
+            std::memcpy(h + (size_t) ffs * rbi, u0 + (size_t) ff0 * rbi, (size_t) ffs * rbi);
+            // every down row, columns ff0..ff1 (src/model.cpp:586-606)
+            for (int64_t r = 0; r < H; ++r) std::memcpy(h + gub + r * rbf, d0 + r * rb_full_dn + col0, rbf);
+            check(hipMemcpyAsync(dev, host, gub + (size_t) H * rbf, hipMemcpyHostToDevice, s), "hipMemcpyAsync");
+            void* gdst = sh && q8s ? sh_gu : (uint8_t*) gu + e * gu_stride;
+            void* ddst = sh && q8s ? sh_dn : (uint8_t*) dn + e * dn_stride;
+            if (sfnx_store_pack(gt, dev, gdst, 1, 2 * ffs, (int) H, st) != 0) throw std::runtime_error(sfnx_last_error());
+            if (sfnx_store_pack(dt, (uint8_t*) dev + gub, ddst, 1, (int) H, ffs, st) != 0) throw std::runtime_error(sfnx_last_error());
+        }
+        // router rows, then the shared expert's gate row (src/model.cpp:766-773)
+        check(hipMemcpyAsync(W, ti.data, (size_t) E * H * 4, hipMemcpyHostToDevice, s), "hipMemcpyAsync");
+        if (shared) check(hipMemcpyAsync(W + E * H, sgi->data, (size_t) H * 4, hipMemcpyHostToDevice, s), "hipMemcpyAsync");
+        check(hipStreamSynchronize(s), "hipStreamSynchronize");
+    } catch (...) {
+        cleanup();
+        throw;
+    }
+    cleanup();
+    if (info) {
+        info[0] = (int) type;
+        info[1] = (int) H;
+        info[2] = (int) E;
+        info[3] = ffs;
+        info[4] = shared ? 1 : 0;
+        info[5] = (int) dtype;
+    }
+}
+}  // namespace
+
 extern "C" int sfnx_gguf_moe_layer(const sfnx_gguf* g, int layer, int ff0, int ff1, void* gu, size_t gu_stride, void* dn,
                                    size_t dn_stride, float* W, int* info, void* st) {
     return guarded("sfnx_gguf_moe_layer", [&] {
-        require(g != nullptr && gu != nullptr && dn != nullptr && W != nullptr, "null argument");
-        const std::string L = "blk." + std::to_string(layer) + ".";
-        const sfnx_gguf_tensor& tg = need(g, L + "ffn_gate_exps.weight");
-        const sfnx_gguf_tensor& tu = need(g, L + "ffn_up_exps.weight");
-        const sfnx_gguf_tensor& td = need(g, L + "ffn_down_exps.weight");
-        const sfnx_gguf_tensor& ti = need(g, L + "ffn_gate_inp.weight");
-        const uint32_t type = tg.type, dtype = td.type;   // gate|up stack into one store; down is its own (src/model.cpp:540-606)
-        require(expert_type_ok(type) && expert_type_ok(dtype), "expert tensors must be Q4_0, Q5_1, Q8_0, Q4_K or Q5_K");
-        require(tu.type == type, "gate and up experts differ in type (they stack into one matrix)");
-        const int64_t H = tg.ne[0], FF = tg.ne[1], E = tg.ne[2];
-        require(tu.ne[0] == H && tu.ne[1] == FF && tu.ne[2] == E, "up experts differ in shape from gate experts");
-        require(td.ne[0] == FF && td.ne[1] == H && td.ne[2] == E, "down experts are not [FF][H] a expert");
-        const int cb = block_values(dtype);   // a column slice of the down rows is whole blocks
-        require(0 <= ff0 && ff0 < ff1 && ff1 <= FF && ff0 % cb == 0 && (ff1 - ff0) % 512 == 0,
-                "FF slice must start on a whole block and span a multiple of 512 (the store's runs)");
-        require(H % 512 == 0, "the hidden size must be a multiple of 512 (the store's runs)");
-        require(ti.type == 0 && ti.ne[0] == H && ti.ne[1] == E, "ffn_gate_inp must be f32 [E][H]");
-        const int ffs = ff1 - ff0;
-        const size_t rb_in = row_bytes(type, (int) H), rb_ff = row_bytes(dtype, ffs);
-        require(gu_stride >= 2 * (size_t) ffs * rb_in && dn_stride >= (size_t) H * rb_ff, "strides smaller than a matrix");
-        // the shared expert, when the layer has one of the routed experts' type and FF, is expert E
-        const sfnx_gguf_tensor* sg = find(g, L + "ffn_gate_shexp.weight");
-        const sfnx_gguf_tensor* su = find(g, L + "ffn_up_shexp.weight");
-        const sfnx_gguf_tensor* sd = find(g, L + "ffn_down_shexp.weight");
-        const sfnx_gguf_tensor* sgi = find(g, L + "ffn_gate_inp_shexp.weight");
-        const bool shared = sg && su && sd && sgi;
-        if (shared) {
-            require(sg->type == type && su->type == type && sd->type == dtype,
-                    "the shared expert's types differ from the routed experts' (it is one more expert of their stores)");
-            require(sg->ne[0] == H && sg->ne[1] == FF && su->ne[0] == H && su->ne[1] == FF && sd->ne[0] == FF &&
-                        sd->ne[1] == H, "the shared expert's shape differs from a routed expert's");
-            require(sgi->type == 0 && sgi->ne[0] == H && sgi->ne[1] == 1, "ffn_gate_inp_shexp must be f32 [1][H]");
-        }
-        const int64_t NE = E + (shared ? 1 : 0);
-        hipStream_t s = stream_of(st);
-        // one expert's matrices at a time in GGUF layout through a pinned host buffer and a device buffer, then packed
-        const size_t gu_bytes = 2 * (size_t) ffs * rb_in, dn_bytes = (size_t) H * rb_ff;
-        void *host = nullptr, *dev = nullptr;
-        check(hipHostMalloc(&host, gu_bytes + dn_bytes, hipHostMallocDefault), "hipHostMalloc");
-        const hipError_t ea = hipMalloc(&dev, gu_bytes + dn_bytes);
-        if (ea != hipSuccess) {
-            (void) hipHostFree(host);
-            check(ea, "hipMalloc");
-        }
-        auto cleanup = [&] {
-            (void) hipStreamSynchronize(s);
-            (void) hipFree(dev);
-            (void) hipHostFree(host);
-        };
-        try {
-            uint8_t* h = (uint8_t*) host;
-            const size_t rb_full_dn = row_bytes(dtype, (int) FF);
-            const size_t col0 = row_bytes(dtype, ff0);
-            for (int64_t e = 0; e < NE; ++e) {
-                const bool sh = e == E;
-                const uint8_t* g0 = (const uint8_t*) (sh ? sg->data : tg.data) + (sh ? 0 : e * FF * rb_in);
-                const uint8_t* u0 = (const uint8_t*) (sh ? su->data : tu.data) + (sh ? 0 : e * FF * rb_in);
-                const uint8_t* d0 = (const uint8_t*) (sh ? sd->data : td.data) + (sh ? 0 : e * H * rb_full_dn);
-                check(hipStreamSynchronize(s), "hipStreamSynchronize");   // the buffers are free again
-                // gate rows ff0..ff1, then up rows ff0..ff1 (src/model.cpp:554-576)
-                std::memcpy(h, g0 + (size_t) ff0 * rb_in, (size_t) ffs * rb_in);
-                std::memcpy(h + (size_t) ffs * rb_in, u0 + (size_t) ff0 * rb_in, (size_t) ffs * rb_in);
-                // every down row, columns ff0..ff1 (src/model.cpp:586-606)
-                for (int64_t r = 0; r < H; ++r) std::memcpy(h + gu_bytes + r * rb_ff, d0 + r * rb_full_dn + col0, rb_ff);
-                check(hipMemcpyAsync(dev, host, gu_bytes + dn_bytes, hipMemcpyHostToDevice, s), "hipMemcpyAsync");
-                if (sfnx_store_pack(type, dev, (uint8_t*) gu + e * gu_stride, 1, 2 * ffs, (int) H, st) != 0)
-                    throw std::runtime_error(sfnx_last_error());
-                if (sfnx_store_pack(dtype, (uint8_t*) dev + gu_bytes, (uint8_t*) dn + e * dn_stride, 1, (int) H, ffs, st) != 0)
-                    throw std::runtime_error(sfnx_last_error());
-            }
-            // router rows, then the shared expert's gate row (src/model.cpp:766-773)
-            check(hipMemcpyAsync(W, ti.data, (size_t) E * H * 4, hipMemcpyHostToDevice, s), "hipMemcpyAsync");
-            if (shared) check(hipMemcpyAsync(W + E * H, sgi->data, (size_t) H * 4, hipMemcpyHostToDevice, s), "hipMemcpyAsync");
-            check(hipStreamSynchronize(s), "hipStreamSynchronize");
-        } catch (...) {
-            cleanup();
-            throw;
-        }
-        cleanup();
-        if (info) {
-            info[0] = (int) type;
-            info[1] = (int) H;
-            info[2] = (int) E;
-            info[3] = ffs;
-            info[4] = shared ? 1 : 0;
-            info[5] = (int) dtype;
-        }
+        moe_layer(g, layer, ff0, ff1, gu, gu_stride, dn, dn_stride, W, nullptr, nullptr, info, st);
+    });
+}
+
+extern "C" int sfnx_gguf_moe_layer_q8s(const sfnx_gguf* g, int layer, int ff0, int ff1, void* gu, size_t gu_stride,
+                                       void* dn, size_t dn_stride, float* W, void* sh_gu, void* sh_dn, int* info,
+                                       void* st) {
+    return guarded("sfnx_gguf_moe_layer_q8s", [&] {
+        require(sh_gu != nullptr && sh_dn != nullptr, "null argument");
+        moe_layer(g, layer, ff0, ff1, gu, gu_stride, dn, dn_stride, W, sh_gu, sh_dn, info, st);
     });
 }

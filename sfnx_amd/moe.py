@@ -492,8 +492,10 @@ class Gguf:
         return v.value.decode() if r else None
 
 
-def gguf_moe_layer(g: Gguf, layer: int, ff0: int = 0, ff1: int | None = None, K: int = 8) -> "MoeLayer":
-    """blk.<layer>'s experts, shared expert and router from a GGUF into a device MoeLayer (src/model.cpp:766-809)"""
+def gguf_moe_layer(g: Gguf, layer: int, ff0: int = 0, ff1: int | None = None, K: int = 8, q8s: bool = False) -> "MoeLayer":
+    """blk.<layer>'s experts, shared expert and router from a GGUF into a device MoeLayer (src/model.cpp:766-809).
+    q8s: the shared expert as the reference loads it, dense Q8_0 matrices for the q8s sums (it must be Q8_0); else it
+    joins the routed stores as expert E."""
     ti = g.tensor(f"blk.{layer}.ffn_gate_exps.weight")
     if ti is None:
         raise RuntimeError(f"gguf: blk.{layer}.ffn_gate_exps.weight is missing")
@@ -502,7 +504,7 @@ def gguf_moe_layer(g: Gguf, layer: int, ff0: int = 0, ff1: int | None = None, K:
     ffs = ff1 - ff0
     shared = all(g.tensor(f"blk.{layer}.{n}.weight") is not None
                  for n in ("ffn_gate_shexp", "ffn_up_shexp", "ffn_down_shexp", "ffn_gate_inp_shexp"))
-    E1 = E + (1 if shared else 0)
+    E1 = E + (1 if shared and not q8s else 0)
     gu_stride = 2 * ffs * row_bytes(wtype, H)
     td = g.tensor(f"blk.{layer}.ffn_down_exps.weight")
     dn_stride = H * row_bytes(td[0] if td is not None else wtype, ffs)
@@ -510,9 +512,17 @@ def gguf_moe_layer(g: Gguf, layer: int, ff0: int = 0, ff1: int | None = None, K:
     dn = torch.empty(E1 * dn_stride, dtype=torch.uint8, device="cuda")
     W = torch.zeros((E + 1, H), dtype=torch.float32, device="cuda")   # row E: the shared gate (zero without one)
     info = (C.c_int * 6)()
-    check(lib().sfnx_gguf_moe_layer(g._h, layer, ff0, ff1, _p(gu), gu_stride, _p(dn), dn_stride, _p(W), info, _st()))
-    s = LayerShape(H=H, E=E, K=K, ff=ffs, wtype=wtype, shared=shared, dn_wtype=None if info[5] == wtype else info[5])
-    return MoeLayer(s, W, gu, dn)
+    sh_gu = sh_dn = None
+    if q8s:
+        sh_gu = torch.empty(2 * ffs * row_bytes(Q8_0, H), dtype=torch.uint8, device="cuda")
+        sh_dn = torch.empty(H * row_bytes(Q8_0, ffs), dtype=torch.uint8, device="cuda")
+        check(lib().sfnx_gguf_moe_layer_q8s(g._h, layer, ff0, ff1, _p(gu), gu_stride, _p(dn), dn_stride, _p(W),
+                                            _p(sh_gu), _p(sh_dn), info, _st()))
+    else:
+        check(lib().sfnx_gguf_moe_layer(g._h, layer, ff0, ff1, _p(gu), gu_stride, _p(dn), dn_stride, _p(W), info, _st()))
+    s = LayerShape(H=H, E=E, K=K, ff=ffs, wtype=wtype, shared=shared, dn_wtype=None if info[5] == wtype else info[5],
+                   sh_q8s=q8s)
+    return MoeLayer(s, W, gu, dn, sh_gu, sh_dn)
 
 
 __all__ = [n for n in dir() if not n.startswith("_")] + ["_abi"]

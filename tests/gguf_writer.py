@@ -48,9 +48,10 @@ def write_gguf(path, kv: list, tensors: list, alignment: int = 32, version: int 
 
 
 def moe_layer_tensors(layer: int, W: np.ndarray, gate: np.ndarray, up: np.ndarray, down: np.ndarray, wtype: int,
-                      H: int, E: int, ff: int, shared=None, dn_type: int | None = None) -> list:
+                      H: int, E: int, ff: int, shared=None, dn_type: int | None = None, sh_type: int | None = None) -> list:
     """the tensors of one MoE layer as a Qwen3-MoE style GGUF names them: per-expert GGUF blocks (gate, up: [E][ff]
-    rows of H; down: [E][H] rows of ff), router f32 [E][H], and optionally (gate_s, up_s, down_s, gate_row)"""
+    rows of H; down: [E][H] rows of ff), router f32 [E][H], and optionally (gate_s, up_s, down_s, gate_row), the shared
+    matrices in sh_type when given (Q8_0 as the reference's models carry them), else in the routed types"""
     p = f"blk.{layer}."
     dt = wtype if dn_type is None else dn_type
     t = [(p + "ffn_gate_exps.weight", wtype, (H, ff, E), gate.tobytes()),
@@ -59,8 +60,9 @@ def moe_layer_tensors(layer: int, W: np.ndarray, gate: np.ndarray, up: np.ndarra
          (p + "ffn_gate_inp.weight", 0, (H, E), np.ascontiguousarray(W[:E], np.float32).tobytes())]
     if shared is not None:
         gs, us, ds, grow = shared
-        t += [(p + "ffn_gate_shexp.weight", wtype, (H, ff), gs.tobytes()),
-              (p + "ffn_up_shexp.weight", wtype, (H, ff), us.tobytes()),
-              (p + "ffn_down_shexp.weight", dt, (ff, H), ds.tobytes()),
+        st, sdt = (wtype, dt) if sh_type is None else (sh_type, sh_type)
+        t += [(p + "ffn_gate_shexp.weight", st, (H, ff), gs.tobytes()),
+              (p + "ffn_up_shexp.weight", st, (H, ff), us.tobytes()),
+              (p + "ffn_down_shexp.weight", sdt, (ff, H), ds.tobytes()),
               (p + "ffn_gate_inp_shexp.weight", 0, (H, 1), np.ascontiguousarray(grow, np.float32).tobytes())]
     return t

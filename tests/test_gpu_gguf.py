@@ -14,14 +14,15 @@ from tests.gpu_util import max_rel
 pytestmark = pytest.mark.gpu
 
 
-def _layer_bytes(wtype, H, E, ff, seed, dn_type=None):
+def _layer_bytes(wtype, H, E, ff, seed, dn_type=None, sh_type=None):
     rng = np.random.default_rng(seed)
     dt = wtype if dn_type is None else dn_type
     q = lambda r, c, t=wtype: orc.quantize(t, (0.02 * rng.standard_normal((r, c))).astype(np.float32))
     gate = np.stack([q(ff, H) for _ in range(E)])
     up = np.stack([q(ff, H) for _ in range(E)])
     down = np.stack([q(H, ff, dt) for _ in range(E)])
-    shared = (q(ff, H), q(ff, H), q(H, ff, dt), (0.02 * rng.standard_normal(H)).astype(np.float32))
+    st = sh_type or wtype
+    shared = (q(ff, H, st), q(ff, H, st), q(H, ff, sh_type or dt), (0.02 * rng.standard_normal(H)).astype(np.float32))
     W = (0.02 * rng.standard_normal((E, H))).astype(np.float32)
     return W, gate, up, down, shared
 
@@ -83,3 +84,57 @@ def test_gguf_layer_refusals(tmp_path):
         moe.gguf_moe_layer(g, 1)
     with pytest.raises(RuntimeError, match="whole block"):
         moe.gguf_moe_layer(g, 0, 128, 512)
+
+
+@pytest.mark.parametrize("wtype,ff,ff0,ff1", [(orc.Q4_K, 512, 0, 512), (orc.Q4_K, 1024, 256, 768), (orc.Q5_1, 1024, 32, 544)])
+def test_gguf_layer_q8s_shared(tmp_path, wtype, ff, ff0, ff1):
+    """the shared expert as the reference loads it (src/model.cpp:807-809): Q8_0 in the file, dense matrices on the
+    device; the routed stores hold E experts; decode (unfused and fused) against the oracle on the same bytes"""
+    H, E = 1024, 64
+    W, gate, up, down, shared = _layer_bytes(wtype, H, E, ff, 13, sh_type=orc.Q8_0)
+    path = tmp_path / "layer.gguf"
+    gw.write_gguf(path, [], gw.moe_layer_tensors(2, W, gate, up, down, wtype, H, E, ff, shared, sh_type=orc.Q8_0))
+    g = moe.Gguf(str(path))
+    L = moe.gguf_moe_layer(g, 2, ff0, ff1, K=4, q8s=True)
+    torch.cuda.synchronize()
+    s = L.s
+    ffs = ff1 - ff0
+    assert s.sh_q8s and s.shared and L.gu_w.numel() == E * L.gu_stride
+    rb_h, rb_f, rb_full = orc.row_bytes(orc.Q8_0, H), orc.row_bytes(orc.Q8_0, ffs), orc.row_bytes(orc.Q8_0, ff)
+    col0 = orc.row_bytes(orc.Q8_0, ff0)
+    sg = torch.empty_like(L.sh_gu)
+    sd = torch.empty_like(L.sh_dn)
+    moe.store_unpack(orc.Q8_0, L.sh_gu, sg, 1, 2 * ffs, H)
+    moe.store_unpack(orc.Q8_0, L.sh_dn, sd, 1, H, ffs)
+    sg, sd = sg.cpu().numpy(), sd.cpu().numpy()
+    want_g = np.concatenate([shared[0].reshape(ff, rb_h)[ff0:ff1], shared[1].reshape(ff, rb_h)[ff0:ff1]])
+    assert np.array_equal(sg.reshape(2 * ffs, rb_h), want_g)
+    assert np.array_equal(sd.reshape(H, rb_f), shared[2].reshape(H, rb_full)[:, col0:col0 + rb_f])
+    # routed stores unpacked for the oracle
+    gu_g = torch.empty_like(L.gu_w)
+    dn_g = torch.empty_like(L.dn_w)
+    moe.store_unpack(wtype, L.gu_w, gu_g, E, 2 * ffs, H)
+    moe.store_unpack(wtype, L.dn_w, dn_g, E, H, ffs)
+    host = orc.LayerWeights(L.W.cpu().numpy(), gu_g.cpu().numpy(), dn_g.cpu().numpy(), wtype, H, E, s.K, ffs, True,
+                            sh_gu=sg, sh_dn=sd)
+    T = 3
+    x = orc.synth(T * H, 78, 1.0).reshape(T, H)
+    y = torch.empty((T, H), dtype=torch.float32, device="cuda")
+    b = moe.DecodeBuffers(s, T)
+    moe.decode_layer(L, torch.from_numpy(x).cuda(), y, b)
+    xf = torch.from_numpy(x).cuda()
+    moe.FusedDecode([L], T)(xf, norm=False)
+    torch.cuda.synchronize()
+    oy, _, oi, _, ogu, _ = orc.layer_decode(host, x)
+    assert np.array_equal(b.topi.cpu().numpy(), oi)
+    P = T * s.K
+    assert np.array_equal(b.gu.cpu().numpy()[P:].view(np.uint32), ogu[P:].view(np.uint32))
+    assert max_rel(y.cpu().numpy(), oy) < 2e-3
+    # the fused decode: x + y of the unfused layer, bit for bit
+    assert np.array_equal(xf.cpu().numpy().view(np.uint32), (torch.from_numpy(x).cuda() + y).cpu().numpy().view(np.uint32))
+    # a shared expert of another type is refused on this path, as the reference refuses it
+    path2 = tmp_path / "l2.gguf"
+    W2, g2, u2, d2, sh2 = _layer_bytes(wtype, H, E, ff, 14)
+    gw.write_gguf(path2, [], gw.moe_layer_tensors(0, W2, g2, u2, d2, wtype, H, E, ff, sh2))
+    with pytest.raises(RuntimeError, match="not Q8_0"):
+        moe.gguf_moe_layer(moe.Gguf(str(path2)), 0, q8s=True)
