@@ -60,6 +60,13 @@ def expert_bytes(s, moe):
     return 2 * s.ff * moe.row_bytes(s.wtype, s.H) + s.H * moe.row_bytes(s.dn_type, s.ff)
 
 
+def shared_bytes(s, moe):
+    """the shared expert's weight bytes: dense Q8_0 matrices (sh_q8s), else one more expert of the routed types"""
+    if s.sh_q8s:
+        return 2 * s.ff * moe.row_bytes(moe.Q8_0, s.H) + s.H * moe.row_bytes(moe.Q8_0, s.ff)
+    return expert_bytes(s, moe)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -180,6 +187,8 @@ def main():
         out["verify_window"] = bench_window(layers[0], s, moe, torch)
         out["q8_0"] = bench_q8_0(moe, torch, args.q8_layers, args.steps, args.warmup)
         out["other_types"] = bench_other_types(moe, torch, args.type_layers, args.steps, args.warmup)
+        out["q8s_shared"] = bench_q8s_shared(moe, torch, args.type_layers, args.steps, args.warmup)
+        log(f"q8s shared: decode {out['q8s_shared']['decode_us_per_token_layer']} us/token-layer")
     print(json.dumps(out), flush=True)
     return 0
 
@@ -290,10 +299,11 @@ def bench_window(L, s, moe, torch, C=96, reps=20):
             "gbs": round(nbytes / (us * 1e-6) / 1e9, 1), "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
-def bench_type(moe, torch, wtype, NL, steps, warmup, C, seed0):
+def bench_type(moe, torch, wtype, NL, steps, warmup, C, seed0, sh_q8s=False):
     """one expert type at the bench's layer shapes: decode at batch 1 through NL stacked layers (the fused path in a
-    graph, as config 1) and a C-token prompt chunk through layer 0 (experts on the matrix cores, Zipf-skewed routing)"""
-    s = moe.LayerShape(H=2048, E=512, K=10, ff=512, wtype=wtype, shared=True)
+    graph, as config 1) and a C-token prompt chunk through layer 0 (experts on the matrix cores, Zipf-skewed routing).
+    sh_q8s: the shared expert as dense Q8_0 matrices in the reference's q8s sums."""
+    s = moe.LayerShape(H=2048, E=512, K=10, ff=512, wtype=wtype, shared=True, sh_q8s=sh_q8s)
     layers = [moe.MoeLayer.synthetic(s, seed=seed0 + l) for l in range(NL)]
     x0 = torch.empty((1, s.H), dtype=torch.float32, device="cuda")
     moe.synth_normal(x0, 4343, 1.0)
@@ -311,7 +321,7 @@ def bench_type(moe, torch, wtype, NL, steps, warmup, C, seed0):
         f(x)
     ms = time_us(torch, g.replay, max(steps, 5)) / 1e3
     assert torch.isfinite(x).all()
-    bytes_tl = (s.E + 1) * s.H * 4 + (s.K + 1) * expert_bytes(s, moe)
+    bytes_tl = (s.E + 1) * s.H * 4 + s.K * expert_bytes(s, moe) + shared_bytes(s, moe)
     gbs = bytes_tl * NL / (ms * 1e-3) / 1e9
     L = layers[0]
     xp = torch.empty((C, s.H), dtype=torch.float32, device="cuda")
@@ -325,15 +335,17 @@ def bench_type(moe, torch, wtype, NL, steps, warmup, C, seed0):
                                                              b.cap, b.xh, b.h16), 5)
     t_dn = time_us(torch, lambda: moe.moe_down_mma(L.dn_w, L.dn_stride, s.dn_type, s.ff, s.H, b.jobs_dn, b.njobs, b.cap,
                                                    b.h16, b.part), 5)
+    t_sh = time_us(torch, lambda: moe.prefill_shared_mma(L, b), 5) if sh_q8s else 0.0
     flops = 2 * (C * s.K + C) * 3 * s.ff * s.H
-    touched = int((b.cnt.cpu() > 0).sum()) + 1
-    wbytes = touched * expert_bytes(s, moe)
-    t = (t_gu + t_dn) * 1e-6
+    touched = int((b.cnt.cpu() > 0).sum())
+    wbytes = touched * expert_bytes(s, moe) + shared_bytes(s, moe)
+    t = (t_gu + t_dn + t_sh) * 1e-6
     del layers, L, b
     torch.cuda.empty_cache()
     return {"decode_layers": NL, "decode_us_per_token_layer": round(ms * 1000 / NL, 3), "decode_gbs": round(gbs, 1),
             "decode_hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_token_layer": bytes_tl, "prefill_tokens": C,
-            "prefill_us": {"mma_gate_up_swiglu": round(t_gu, 1), "mma_down": round(t_dn, 1)},
+            "prefill_us": {"mma_gate_up_swiglu": round(t_gu, 1), "mma_down": round(t_dn, 1),
+                           **({"shared_q8s": round(t_sh, 1)} if sh_q8s else {})},
             "prefill_tflops": round(flops / t / 1e12, 1), "prefill_weight_gbs": round(wbytes / t / 1e9, 1),
             "prefill_hbm_frac": round(wbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
 
@@ -343,6 +355,14 @@ def bench_q8_0(moe, torch, NL, steps, warmup):
     prompt chunk through layer 0"""
     r = bench_type(moe, torch, moe.Q8_0, NL, steps, warmup, 4096, 5000)
     r["workload"] = f"config 4: Q8_0 experts; decode batch 1 through {NL} stacked layers; 4096-token prompt chunk"
+    return r
+
+
+def bench_q8s_shared(moe, torch, NL, steps, warmup):
+    """config 1's layer shape with the shared expert as the reference's models carry it (dense Q8_0, q8s sums;
+    src/model.cpp:807-809, src/engine.cu:936-945): decode through NL stacked layers, a 2048-token prompt chunk"""
+    r = bench_type(moe, torch, moe.Q4_K, NL, steps, warmup, 2048, 9000, sh_q8s=True)
+    r["workload"] = f"Q4_K experts + dense Q8_0 shared expert; decode batch 1 through {NL} stacked layers; 2048-token chunk"
     return r
 
 

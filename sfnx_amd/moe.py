@@ -180,6 +180,8 @@ class MoeLayer:
 
     def __init__(self, shape: LayerShape, W: torch.Tensor, gu_w: torch.Tensor, dn_w: torch.Tensor,
                  sh_gu: torch.Tensor | None = None, sh_dn: torch.Tensor | None = None):
+        if W.shape[0] != shape.E + 1:
+            raise ValueError("the router has E + 1 rows (row E gates the shared expert)")
         if shape.sh_q8s and (sh_gu is None or sh_dn is None or not shape.shared):
             raise ValueError("a q8s shared expert needs shared=True and both matrices")
         self.s = shape
@@ -210,7 +212,7 @@ class MoeLayer:
         A q8s shared expert takes expert E's values of the same streams, quantized to Q8_0."""
         s = shape
         E1 = s.n_routed
-        W = torch.empty((E1, s.H), dtype=torch.float32, device=device)
+        W = torch.empty((s.E + 1, s.H), dtype=torch.float32, device=device)   # row E: the shared gate
         synth_normal(W, seed * 1000 + 1, 0.02)
         gu_stride = 2 * s.ff * row_bytes(s.wtype, s.H)
         dn_stride = s.H * row_bytes(s.dn_type, s.ff)

@@ -182,3 +182,33 @@ def test_prefill_shared_q8s(path):
     sig = 1 / (1 + np.exp(-b.logits.cpu().numpy()[:, shape.E].astype(np.float64)))
     ref = np.einsum("tk,tkh->th", topw, part[:P].reshape(C, shape.K, -1)) + sig[:, None] * part[P:]
     assert max_rel(y.cpu().numpy(), ref) < 1e-5
+
+
+def test_synthetic_q8s_layer():
+    """MoeLayer.synthetic with a dense shared expert: its matrices are expert E of a Q8_0 layer of the same seed, the
+    routed experts those of the Q4_K layer, and a decode step is finite and equal to the oracle's"""
+    s = moe.LayerShape(H=1024, E=64, K=6, ff=512, wtype=orc.Q4_K, shared=True, sh_q8s=True)
+    L = moe.MoeLayer.synthetic(s, seed=31)
+    R = moe.MoeLayer.synthetic(moe.LayerShape(H=1024, E=64, K=6, ff=512, wtype=orc.Q8_0, shared=True), seed=31)
+    Q = moe.MoeLayer.synthetic(moe.LayerShape(H=1024, E=64, K=6, ff=512, wtype=orc.Q4_K, shared=True), seed=31)
+    assert L.W.shape == (s.E + 1, s.H) and torch.equal(L.W, Q.W)
+    assert torch.equal(L.sh_gu, R.gu_w[s.E * R.gu_stride:(s.E + 1) * R.gu_stride])
+    assert torch.equal(L.sh_dn, R.dn_w[s.E * R.dn_stride:(s.E + 1) * R.dn_stride])
+    assert torch.equal(L.gu_w, Q.gu_w[: s.E * Q.gu_stride]) and torch.equal(L.dn_w, Q.dn_w[: s.E * Q.dn_stride])
+    x = orc.synth(s.H, 990, 1.0).reshape(1, s.H)
+    f = moe.FusedDecode([L], 1)
+    xf = torch.from_numpy(x).cuda()
+    f(xf, norm=False)
+    torch.cuda.synchronize()
+    gu = torch.empty_like(L.gu_w)
+    dn = torch.empty_like(L.dn_w)
+    moe.store_unpack(orc.Q4_K, L.gu_w, gu, s.E, 2 * s.ff, s.H)
+    moe.store_unpack(orc.Q4_K, L.dn_w, dn, s.E, s.H, s.ff)
+    sg, sd = torch.empty_like(L.sh_gu), torch.empty_like(L.sh_dn)
+    moe.store_unpack(orc.Q8_0, L.sh_gu, sg, 1, 2 * s.ff, s.H)
+    moe.store_unpack(orc.Q8_0, L.sh_dn, sd, 1, s.H, s.ff)
+    host = orc.LayerWeights(L.W.cpu().numpy(), gu.cpu().numpy(), dn.cpu().numpy(), s.wtype, s.H, s.E, s.K, s.ff, True,
+                            sh_gu=sg.cpu().numpy(), sh_dn=sd.cpu().numpy())
+    oy = orc.layer_decode(host, x)[0]
+    yf = f.piece("y", torch.float32, (1, s.H)).cpu().numpy()
+    assert np.isfinite(yf).all() and max_rel(yf, oy) < TOL
