@@ -192,6 +192,24 @@ int sfnx_moe_decode_q8s(const sfnx_moe_layer_w* layers, const sfnx_moe_shared_q8
                         uint32_t gu_type, uint32_t dn_type, int H, int E, int K, int ff, float* x, int T, int norm,
                         float eps, void* ws, size_t ws_bytes, int phases, void* st);
 
+/* ---------------------------------------------------------------------------------------------- hc read */
+/* bytes of the workspace sfnx_hc_read needs (windows of up to 16 rows); offsets (may be null, else 6 values) receives
+ * the byte offsets of its pieces, each laid out for 16 rows (row t at t times a row's size): part [16][HC N / 512]
+ * [LR + HC] f32 (the slices' partial down and inject dots), ssp [16][HC N / 512] f32 (the slices' square sums), lo
+ * [16][LR] int8, its scales [16][LR / 32] f32, rs [16][HC] f32, then the total. */
+size_t sfnx_hc_workspace(int N, int HC, int LR, size_t* offsets);
+/* The hyper-connection read that produces the MoE half's input, src/kernels.cu:1054 hc_read (kernel src/hc.cuh:13-380):
+ * R [T][HC N] (HC residual streams, updated to R' when bo is given), bo [T][N] (the last half's output, or null) with
+ * inj_prev [T][HC] (its inject logits), w_norm [HC N] f32, the down Q8S matrix (down_q int8 [LR][HC N], down_d f16
+ * [LR][HC N / 32]), the up Q8S matrix (up_q int8 [HC N][LR], up_d f16 [HC N][LR / 32]) and w_inj bf16 [HC][HC N] (or
+ * null: no inject rows).  Writes mixed [T][N] (the MoE input), inject [T][HC] (when w_inj and inject are given) and,
+ * when xq is given, mixed as q8_1 [T][N / 32] (the expert dots' activations).  1 <= T <= 16, N % 512 == 0,
+ * HC <= 8, LR % 32 == 0 and LR <= 512.  The reference's grid barriers and its err word have no counterpart: three
+ * launches, no waits. */
+int sfnx_hc_read(float* R, const float* bo, const float* inj_prev, const float* w_norm, const void* down_q,
+                 const void* down_d, const void* up_q, const void* up_d, const void* w_inj, float eps, float* mixed,
+                 float* inject, void* xq, int T, int N, int HC, int LR, void* ws, size_t ws_bytes, void* st);
+
 /* the stacked-layer driver's glue between layers (no reference counterpart on the MoE path: the engine's
  * hyper-connection read, src/hc.cuh, normalises the MoE input): x += y (y may be null), then
  * xn = x / sqrt(mean(x^2) + eps) per row of H */

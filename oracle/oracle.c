@@ -812,3 +812,145 @@ double orc_time_layer_decode(const orc_layer* L, const float* x, int nthreads, i
     free(sweep);
     return med;
 }
+
+/* ------------------------------------------------------------------------------------------ hyper-connection read */
+/* src/hc.cuh:13-380 k_hc (with hc_write's fold, src/kernels.cu:1493-1498, as its first step) for T rows, D = HC N
+ * columns of HC residual streams, low rank LR.  Per row t:
+ *   R' = R + bo * 2 sigm(inj_prev / HC) per stream (when bo), xs = R' w_norm;
+ *   per 512-column slice s: the square sums of R' (32-lane butterflies, then the 16 groups in order: hc.cuh:165-180),
+ *   xs as int8 per 32 (q8_block: float d = amax / 127, hc.cuh:60-66), and each down row's partial dot: 8 lanes, lane j
+ *   the 8-value chunks q 8 + j in order, acc = fmaf(d_w d_x, dot8, acc), then xor 1, 2, 4 (hc.cuh:186-209); each
+ *   bf16 inject row on xs itself (hc.cuh:211-226);
+ *   rs_c = 1 / sqrt(sum of stream c's slice sums / N + eps); lo_r = silu(sum_c fmaf(rs_c, sum_s part) / HC) as int8
+ *   per 32; inject_c likewise without silu (hc.cuh:251-289);
+ *   up row c N + i: 16 lanes, lane b < LR / 32 the 32-block b, (d_w d_lo) dot32, xor 1, 2, 4, 8 (hc.cuh:318-344);
+ *   mixed_i = sum_c sigm(up) ((R'_c,i w_norm) rs_c) / HC, then mixed as q8_1 (hc.cuh:346-381).
+ * The reference's rsqrtf and __expf are approximations; here 1 / sqrtf and expf (parity of those bits unpinned). */
+static inline float bf16_f(uint16_t h) {
+    const uint32_t u = (uint32_t) h << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+static float butterfly_up(const float* v, int n) {   /* xor 1, 2, 4, ...: lane 0's value */
+    float a[64], b[64];
+    memcpy(a, v, (size_t) n * sizeof(float));
+    for (int o = 1; o < n; o <<= 1) {
+        for (int l = 0; l < n; ++l) b[l] = a[l] + a[l ^ o];
+        memcpy(a, b, (size_t) n * sizeof(float));
+    }
+    return a[0];
+}
+static void q8_block_f(const float* x, int8_t* q, float* d) {   /* hc.cuh:60-66 */
+    float amax = 0.f;
+    for (int l = 0; l < 32; ++l) amax = fabsf(x[l]) > amax ? fabsf(x[l]) : amax;
+    const float sc = amax / 127.0f;
+    for (int l = 0; l < 32; ++l) q[l] = amax == 0.0f ? 0 : (int8_t) roundf(x[l] / sc);
+    *d = sc;
+}
+
+void orc_hc_read(float* R, const float* bo, const float* inj_prev, const float* w_norm, const int8_t* dq,
+                 const uint16_t* dd, const int8_t* uq, const uint16_t* ud, const uint16_t* w_inj, float eps, int T, int N,
+                 int HC, int LR, float* mixed, float* inject, uint8_t* xq, float* part_out, float* ssp_out) {
+    const int D = HC * N, NS = D / 512, SPS = N / 512, ROWS = LR + HC;
+    float* Rp = (float*) malloc((size_t) D * sizeof(float));
+    float* part = (float*) malloc((size_t) NS * ROWS * sizeof(float));
+    float* ssp = (float*) malloc((size_t) NS * sizeof(float));
+    float* lo = (float*) malloc((size_t) LR * sizeof(float));
+    int8_t* loq = (int8_t*) malloc((size_t) LR);
+    float lod[16], rs[64], gs[64];
+    for (int t = 0; t < T; ++t) {
+        for (int e = 0; e < D; ++e) {
+            const int c = e / N, i = e % N;
+            float r = R[(size_t) t * D + e];
+            if (bo) r = fmaf(bo[(size_t) t * N + i], 2.0f * sigm_(inj_prev[t * HC + c] / (float) HC), r);
+            Rp[e] = r;
+        }
+        for (int s = 0; s < NS; ++s) {
+            const int col0 = s * 512;
+            float xs[512], sq[32], xd[16];
+            int8_t xqs[512];
+            float v = 0.f;
+            for (int w = 0; w < 16; ++w) {
+                for (int l = 0; l < 32; ++l) sq[l] = Rp[col0 + 32 * w + l] * Rp[col0 + 32 * w + l];
+                v += butterfly_sum(sq, 32);
+            }
+            ssp[s] = v;
+            for (int j = 0; j < 512; ++j) xs[j] = Rp[col0 + j] * w_norm[col0 + j];
+            for (int b = 0; b < 16; ++b) q8_block_f(xs + 32 * b, xqs + 32 * b, &xd[b]);
+            for (int row = 0; row < ROWS; ++row) {
+                if (row >= LR && !w_inj) {
+                    part[(size_t) s * ROWS + row] = 0.f;
+                    continue;
+                }
+                float acc[8];
+                for (int j = 0; j < 8; ++j) {
+                    float a = 0.f;
+                    for (int q = 0; q < 8; ++q) {
+                        const int ch = q * 8 + j;
+                        if (row < LR) {
+                            const int8_t* w = dq + (size_t) row * D + col0 + ch * 8;
+                            int dot = 0;
+                            for (int m = 0; m < 8; ++m) dot += (int) w[m] * (int) xqs[ch * 8 + m];
+                            const float wsc = orc_f16_to_f32(dd[((size_t) row * D + col0) / 32 + ch / 4]);
+                            a = fmaf(wsc * xd[ch / 4], (float) dot, a);
+                        } else {
+                            const uint16_t* h = w_inj + (size_t) (row - LR) * D + col0 + ch * 8;
+                            float e = bf16_f(h[0]) * xs[ch * 8];
+                            for (int m = 1; m < 8; ++m) e = e + bf16_f(h[m]) * xs[ch * 8 + m];
+                            a = a + e;
+                        }
+                    }
+                    acc[j] = a;
+                }
+                part[(size_t) s * ROWS + row] = butterfly_up(acc, 8);
+            }
+        }
+        if (part_out) memcpy(part_out + (size_t) t * NS * ROWS, part, (size_t) NS * ROWS * sizeof(float));
+        if (ssp_out) memcpy(ssp_out + (size_t) t * NS, ssp, (size_t) NS * sizeof(float));
+        for (int c = 0; c < HC; ++c) {
+            float v = 0.f;
+            for (int ss = 0; ss < SPS; ++ss) v += ssp[c * SPS + ss];
+            rs[c] = 1.0f / sqrtf(v / (float) N + eps);
+        }
+        for (int r = 0; r < ROWS; ++r) {
+            if (r >= LR && !w_inj) break;
+            float sum = 0.f;
+            for (int c = 0; c < HC; ++c) {
+                float p = 0.f;
+                for (int ss = 0; ss < SPS; ++ss) p += part[(size_t) (c * SPS + ss) * ROWS + r];
+                sum = fmaf(rs[c], p, sum);
+            }
+            if (r < LR) lo[r] = silu_(sum / (float) HC);
+            else if (inject) inject[t * HC + (r - LR)] = sum;
+        }
+        for (int b = 0; b < LR / 32; ++b) q8_block_f(lo + 32 * b, loq + 32 * b, &lod[b]);
+        for (int i = 0; i < N; ++i) {
+            for (int c = 0; c < HC; ++c) {
+                const size_t u = (size_t) c * N + i;
+                float v16[16];
+                for (int L = 0; L < 16; ++L) {
+                    if (L >= LR / 32) {
+                        v16[L] = 0.f;
+                        continue;
+                    }
+                    int dot = 0;
+                    for (int m = 0; m < 32; ++m) dot += (int) uq[u * LR + 32 * L + m] * (int) loq[32 * L + m];
+                    v16[L] = orc_f16_to_f32(ud[u * (LR / 32) + L]) * lod[L] * (float) dot;
+                }
+                const float g = butterfly_up(v16, 16);
+                gs[c] = sigm_(g) * (Rp[u] * w_norm[u] * rs[c]);
+            }
+            float m = gs[0];
+            for (int c = 1; c < HC; ++c) m += gs[c];
+            mixed[(size_t) t * N + i] = m / (float) HC;
+        }
+        if (xq) orc_quantize_q8_1(mixed + (size_t) t * N, xq + (size_t) t * (N / 32) * ORC_Q81_BYTES, N, 1);
+        if (bo) memcpy(R + (size_t) t * D, Rp, (size_t) D * sizeof(float));
+    }
+    free(Rp);
+    free(part);
+    free(ssp);
+    free(lo);
+    free(loq);
+}

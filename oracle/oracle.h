@@ -149,6 +149,14 @@ void orc_layer_decode(const orc_layer* L, const float* x, int T, float* y, float
 void orc_mma_matvec(const uint8_t* w, int type, int n_in, int n_out, const uint16_t* x16, double* out);
 /* k_swiglu_h16, src/moe_mma.cuh:382-388: h16 = f16(silu(gate) * up) of one [gate (ff) | up (ff)] row */
 void orc_swiglu_h16(const float* gu, int ff, uint16_t* h16);
+/* the hyper-connection read, src/hc.cuh:13-380 (k_hc), for T rows: R [T][HC N] (updated to R' when bo), bo [T][N] or
+ * null, inj_prev [T][HC], w_norm [HC N], down Q8S (dq int8 [LR][HC N], dd f16 [LR][HC N / 32]), up Q8S (uq [HC N][LR],
+ * ud [HC N][LR / 32]), w_inj bf16 [HC][HC N] or null; out: mixed [T][N], inject [T][HC] (or null), xq [T][N / 32]
+ * q8_1 (or null), part [T][HC N / 512][LR + HC] and ssp [T][HC N / 512] (or null): the slices' partial dots and
+ * square sums.  N % 512 == 0, LR % 32 == 0, LR <= 512, HC <= 64. */
+void orc_hc_read(float* R, const float* bo, const float* inj_prev, const float* w_norm, const int8_t* dq,
+                 const uint16_t* dd, const int8_t* uq, const uint16_t* ud, const uint16_t* w_inj, float eps, int T, int N,
+                 int HC, int LR, float* mixed, float* inject, uint8_t* xq, float* part, float* ssp);
 
 /* one token through the layer with nthreads threads, median of reps wall times in microseconds (cache swept between
  * runs through a buffer of sweep_bytes) */

@@ -62,6 +62,7 @@ def lib() -> C.CDLL:
             "orc_dequant_q5_k_f16": (None, [vp, vp, i64, i32]),
             "orc_dot_q5_k": (f32, [vp, vp, i32]),
             "orc_dot_q8s": (f32, [vp, vp, i32]),
+            "orc_hc_read": (None, [vp, vp, vp, vp, vp, vp, vp, vp, vp, f32, i32, i32, i32, i32, vp, vp, vp, vp, vp]),
             "orc_quantize_q4_0": (None, [vp, vp, i64, i32]),
             "orc_dequant_q4_0": (None, [vp, vp, i64, i32]),
             "orc_dequant_q4_0_f16": (None, [vp, vp, i64, i32]),
@@ -201,6 +202,35 @@ def dot(t: int, wrow: np.ndarray, yq: np.ndarray, K: int) -> float:
 def dot_q8s(wrow: np.ndarray, yq: np.ndarray, K: int) -> float:
     """the shared expert's dense Q8_0 row dot, src/dense.cuh:24-154 (orc_dot_q8s)"""
     return lib().orc_dot_q8s(_p(np.ascontiguousarray(wrow)), _p(np.ascontiguousarray(yq)), K)
+
+
+class HcWeights:
+    """one hyper-connection read's weights (src/hc.cuh HcArgs): w_norm [HC N] f32, down Q8S (dq int8 [LR][HC N],
+    dd f16 bits [LR][HC N / 32]), up Q8S (uq [HC N][LR], ud [HC N][LR / 32]), w_inj bf16 bits [HC][HC N] or None"""
+
+    def __init__(self, N, HC, LR, w_norm, dq, dd, uq, ud, w_inj=None):
+        self.N, self.HC, self.LR = N, HC, LR
+        self.w_norm = np.ascontiguousarray(w_norm, np.float32)
+        self.dq, self.dd = np.ascontiguousarray(dq, np.int8), np.ascontiguousarray(dd, np.uint16)
+        self.uq, self.ud = np.ascontiguousarray(uq, np.int8), np.ascontiguousarray(ud, np.uint16)
+        self.w_inj = None if w_inj is None else np.ascontiguousarray(w_inj, np.uint16)
+
+
+def hc_read(w: HcWeights, R: np.ndarray, bo=None, inj_prev=None, eps: float = 1e-6):
+    """src/hc.cuh:13-380 for T rows: returns mixed, inject, xq (q8_1), R' (R with bo folded in), part, ssp"""
+    T = R.shape[0]
+    D, NS, ROWS = w.HC * w.N, w.HC * w.N // 512, w.LR + w.HC
+    R = np.array(R, np.float32, copy=True)
+    mixed = np.empty((T, w.N), np.float32)
+    inject = np.zeros((T, w.HC), np.float32)
+    xq = np.empty(T * (w.N // 32) * Q81_BYTES, np.uint8)
+    part = np.empty((T, NS, ROWS), np.float32)
+    ssp = np.empty((T, NS), np.float32)
+    bo_ = None if bo is None else np.ascontiguousarray(bo, np.float32)
+    ij = None if inj_prev is None else np.ascontiguousarray(inj_prev, np.float32)
+    lib().orc_hc_read(_p(R), _p(bo_), _p(ij), _p(w.w_norm), _p(w.dq), _p(w.dd), _p(w.uq), _p(w.ud), _p(w.w_inj), eps, T,
+                      w.N, w.HC, w.LR, _p(mixed), _p(inject), _p(xq), _p(part), _p(ssp))
+    return mixed, inject, xq, R, part, ssp
 
 
 def swiglu_q8_1(gu_row: np.ndarray, ff: int) -> np.ndarray:

@@ -1,0 +1,351 @@
+// The hyper-connection read that feeds the MoE half its input (src/hc.cuh:13-380 k_hc, src/kernels.cu:1054-1090
+// hc_read): HC residual streams of N columns are folded with the last half's output, normalised, mixed through a
+// low-rank pair of dense Q8_0 matrices (down [LR][HC N], up [HC N][LR]) and averaged into `mixed`, the MoE layer's
+// input, with its q8_1 form for the expert dots.  Per row t:
+//   R' = R + bo * 2 sigm(inj_prev / HC) per stream (when bo), xs = R' w_norm
+//   K_A  (slice s of 512 columns, group of 32 rows): the slice's square sums of R' (32-value butterflies, then the 16
+//        groups in order), xs as int8 per 32 (float d = amax / 127), each down row's partial dot (8 lanes, lane j the
+//        8-value chunks 8 q + j in order, acc = fmaf(d_w d_x, dot8, acc), then xor 1, 2, 4) and the bf16 inject rows'
+//        partial dots on xs itself
+//   K_B  rs_c = 1 / sqrt(stream c's square sum / N + eps); lo_r = silu(sum_c fmaf(rs_c, sum_s part) / HC) as int8 per
+//        32; inject_c the same combine without silu
+//   K_C  (32 columns): up row c N + i: 16 lanes, lane b < LR / 32 the 32-block b, (d_w d_lo) dot32, xor 1, 2, 4, 8;
+//        mixed_i = sum_c sigm(up) ((R'_c,i w_norm) rs_c) / HC, R <- R', mixed as q8_1
+// The reference runs the three parts in one launch with two grid barriers; here they are three launches, which cost
+// less than a grid barrier on this part (a kernel boundary in a graph ~1.6 us, a 256-workgroup barrier ~2.8 us).
+#include "common.hpp"
+
+namespace sfnx {
+namespace {
+
+constexpr int HS = 512;              // columns of a slice
+constexpr int HA_THREADS = 256;      // K_A: 32 rows x 8 lanes
+constexpr int HA_ROWS = HA_THREADS / 8;
+constexpr int HC_COLS = 32;          // K_C: 32 columns x 16 lanes
+constexpr int HC_THREADS = HC_COLS * 16;
+constexpr int HC_MAX = 8;            // streams
+constexpr int LR_MAX = 512;          // 16 lanes x 32
+
+struct HcLayout {
+    size_t part, ssp, loq, lod, rs, total;
+};
+// pieces laid out for windows of SFNX_MAXT rows whatever a call's T, so one workspace serves every window size
+HcLayout hc_layout(int N, int HC, int LR) {
+    constexpr size_t T = SFNX_MAXT;
+    const size_t NS = (size_t) HC * N / HS, ROWS = (size_t) LR + HC;
+    size_t o = 0;
+    auto take = [&](size_t bytes) {
+        const size_t r = o;
+        o += (bytes + 255) / 256 * 256;
+        return r;
+    };
+    HcLayout L;
+    L.part = take(T * NS * ROWS * 4);
+    L.ssp = take(T * NS * 4);
+    L.loq = take(T * LR);
+    L.lod = take(T * (LR / 32) * 4);
+    L.rs = take(T * HC * 4);
+    L.total = o;
+    return L;
+}
+
+struct HcArgs {
+    float* R;
+    const float* bo;
+    const float* inj_prev;
+    const float* w_norm;
+    const int8_t* dq;
+    const uint16_t* dd;
+    const int8_t* uq;
+    const uint16_t* ud;
+    const uint16_t* w_inj;
+    float eps;
+    float* mixed;
+    float* inject;
+    uint8_t* xq;
+    int T, N, HC, LR;
+    float* part;   // [T][NS][LR + HC]
+    float* ssp;    // [T][NS]
+    int8_t* loq;   // [T][LR]
+    float* lod;    // [T][LR / 32]
+    float* rs;     // [T][HC]
+};
+
+// the xor butterfly in the reference's order for its hc sums: partner 1, then 2, 4, ... (v += shfl_xor(v, o))
+template <int G> __device__ __forceinline__ float sum_up(float v) {
+    if constexpr (G >= 2) v += lane_xor<1>(v);
+    if constexpr (G >= 4) v += lane_xor<2>(v);
+    if constexpr (G >= 8) v += lane_xor<4>(v);
+    if constexpr (G >= 16) v += lane_xor<8>(v);
+    return v;
+}
+
+// R'[t][c N + i]: R with the last half's output folded in (src/kernels.cu:1493-1498 as src/hc.cuh:68-72 applies it)
+__device__ __forceinline__ float rprime(const HcArgs& a, int t, int c, int i) {
+    const float r = a.R[(size_t) t * a.HC * a.N + (size_t) c * a.N + i];
+    if (!a.bo) return r;
+    return fmaf(a.bo[(size_t) t * a.N + i], 2.0f * sigm_f(a.inj_prev[t * a.HC + c] / (float) a.HC), r);
+}
+
+// one 32-value block to int8 with a float scale (src/hc.cuh:60-66), a half-wave per block
+__device__ __forceinline__ void q8_block32(float v, int8_t* q, float* d) {
+    const int l = threadIdx.x % 32;
+    const float amax = group_max<32>(fabsf(v));
+    const float sc = amax / 127.0f;
+    q[l] = amax == 0.0f ? (int8_t) 0 : (int8_t) roundf(v / sc);
+    if (l == 0) *d = sc;
+}
+
+// ------------------------------------------------------------------------------------------------ K_A
+template <int TT>
+__global__ void __launch_bounds__(HA_THREADS) k_hc_down(HcArgs a) {
+    __shared__ __align__(16) float xs[TT][HS];
+    __shared__ __align__(16) int8_t xq[TT][HS];
+    __shared__ float xd[TT][HS / 32];
+    __shared__ float red[TT][HS / 32];
+    const int T = a.T, s = blockIdx.x, grp = blockIdx.y, tid = threadIdx.x, D = a.HC * a.N;
+    const int NS = D / HS, ROWS = a.LR + a.HC, col0 = s * HS, c = col0 / a.N, i0 = col0 % a.N;
+    // this block's weight row, loaded first: 8 lanes a row, lane j the chunks 8 q + j
+    const int row = grp * HA_ROWS + tid / 8, j = tid % 8;
+    const bool dn_row = row < a.LR, inj_row = row >= a.LR && row < ROWS && a.w_inj != nullptr;
+    uint2 wd[8];
+    uint4 wi[8];
+    float sc[8];
+    if (dn_row) {
+        const uint2* w2 = reinterpret_cast<const uint2*>(a.dq + (size_t) row * D + col0);
+        const uint16_t* ds = a.dd + ((size_t) row * D + col0) / 32;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            wd[q] = w2[q * 8 + j];
+            sc[q] = h2f(ds[(q * 8 + j) / 4]);
+        }
+    } else if (inj_row) {
+        const uint4* w4 = reinterpret_cast<const uint4*>(a.w_inj + (size_t) (row - a.LR) * D + col0);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) wi[q] = w4[q * 8 + j];
+    }
+    // R' and xs for the slice; the square sums (row group 0 only): 32 consecutive columns a half-wave
+    const int hw = tid / 32;
+    for (int t = 0; t < T; ++t) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int x = h * HA_THREADS + tid;
+            const float r = rprime(a, t, c, i0 + x);
+            xs[t][x] = r * a.w_norm[col0 + x];
+            if (grp == 0) {
+                const float v = group_sum<32>(r * r);
+                if (tid % 32 == 0) red[t][h * (HA_THREADS / 32) + hw] = v;
+            }
+        }
+    }
+    __syncthreads();
+    if (grp == 0 && tid < T) {
+        float v = 0.f;
+        for (int w = 0; w < HS / 32; ++w) v += red[tid][w];
+        a.ssp[(size_t) tid * NS + s] = v;
+    }
+    for (int q = hw; q < T * (HS / 32); q += HA_THREADS / 32) {
+        const int t = q / (HS / 32), b = q % (HS / 32);
+        q8_block32(xs[t][32 * b + tid % 32], &xq[t][32 * b], &xd[t][b]);
+    }
+    __syncthreads();
+    if (!dn_row && !inj_row && row >= ROWS) return;   // (whole 8-lane groups: the butterfly stays inside live groups)
+    for (int t = 0; t < T; ++t) {
+        float acc = 0.f;
+        if (dn_row) {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const int ch = q * 8 + j;
+                const int2 xv = *reinterpret_cast<const int2*>(&xq[t][ch * 8]);
+                const int d8 = dot4((int) wd[q].y, xv.y, dot4((int) wd[q].x, xv.x, 0));
+                acc = fmaf(sc[q] * xd[t][ch / 4], (float) d8, acc);
+            }
+        } else if (inj_row) {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const int ch = q * 8 + j;
+                const uint32_t h[4] = {wi[q].x, wi[q].y, wi[q].z, wi[q].w};
+                const float* x = &xs[t][ch * 8];
+                float e = __uint_as_float(h[0] << 16) * x[0];
+                e = e + __uint_as_float(h[0] & 0xffff0000u) * x[1];
+#pragma unroll
+                for (int m = 1; m < 4; ++m) {
+                    e = e + __uint_as_float(h[m] << 16) * x[2 * m];
+                    e = e + __uint_as_float(h[m] & 0xffff0000u) * x[2 * m + 1];
+                }
+                acc = acc + e;
+            }
+        }
+        acc = sum_up<8>(acc);
+        if (j == 0 && row < ROWS) a.part[((size_t) t * NS + s) * ROWS + row] = (dn_row || inj_row) ? acc : 0.f;
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ K_B
+// item (t, b): b < LR / 32 a block of lo, b == LR / 32 the inject rows; a half-wave each
+__global__ void __launch_bounds__(256) k_hc_reduce(HcArgs a) {
+    const int NB = a.LR / 32, items = a.T * (NB + 1), l = threadIdx.x % 32;
+    const int it = blockIdx.x * 8 + threadIdx.x / 32;
+    const int NS = a.HC * a.N / HS, SPS = a.N / HS, ROWS = a.LR + a.HC;
+    if (it >= items) return;   // whole half-waves leave together
+    const int t = it / (NB + 1), b = it % (NB + 1);
+    float rsv[HC_MAX];
+#pragma unroll
+    for (int c = 0; c < HC_MAX; ++c) {
+        if (c >= a.HC) break;
+        float v = 0.f;
+        for (int ss = 0; ss < SPS; ++ss) v += a.ssp[(size_t) t * NS + c * SPS + ss];
+        rsv[c] = 1.0f / sqrtf(v / (float) a.N + a.eps);
+    }
+    if (b == 0 && l < a.HC) a.rs[t * a.HC + l] = rsv[l];
+    const bool inj = b == NB;
+    if (inj && (a.w_inj == nullptr || a.inject == nullptr)) return;
+    const int r = inj ? a.LR + min(l, a.HC - 1) : 32 * b + l;
+    float sum = 0.f;
+#pragma unroll
+    for (int c = 0; c < HC_MAX; ++c) {
+        if (c >= a.HC) break;
+        float p = 0.f;
+        for (int ss = 0; ss < SPS; ++ss) p += a.part[((size_t) t * NS + c * SPS + ss) * ROWS + r];
+        sum = fmaf(rsv[c], p, sum);
+    }
+    if (inj) {
+        if (l < a.HC) a.inject[t * a.HC + l] = sum;
+    } else {
+        q8_block32(silu_f(sum / (float) a.HC), a.loq + (size_t) t * a.LR + 32 * b, a.lod + (size_t) t * NB + b);
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ K_C
+template <int TT>
+__global__ void __launch_bounds__(HC_THREADS) k_hc_up(HcArgs a) {
+    __shared__ __align__(16) int8_t lq[TT][LR_MAX];
+    __shared__ float ld[TT][LR_MAX / 32];
+    __shared__ float rs[TT][HC_MAX];
+    __shared__ float gs[TT][HC_MAX][HC_COLS];
+    __shared__ float ms[TT][HC_COLS];
+    const int T = a.T, tid = threadIdx.x, NB = a.LR / 32, dc0 = blockIdx.x * HC_COLS;
+    const int col = tid / 16, uj = tid % 16;
+    const bool live = uj < NB;
+    // the column's up rows (one 32-block a lane), every stream
+    uint4 w0[HC_MAX], w1[HC_MAX];
+    float wsc[HC_MAX];
+#pragma unroll
+    for (int c = 0; c < HC_MAX; ++c) {
+        if (c >= a.HC) break;
+        const size_t u = (size_t) c * a.N + dc0 + col;
+        if (live) {
+            const uint4* wp = reinterpret_cast<const uint4*>(a.uq + u * a.LR + 32 * uj);
+            w0[c] = wp[0];
+            w1[c] = wp[1];
+            wsc[c] = h2f(a.ud[u * NB + uj]);
+        }
+    }
+    for (int e = tid; e < T * a.LR / 4; e += HC_THREADS)
+        reinterpret_cast<int*>(&lq[e / (a.LR / 4)][0])[e % (a.LR / 4)] = reinterpret_cast<const int*>(a.loq)[e];
+    for (int e = tid; e < T * NB; e += HC_THREADS) ld[e / NB][e % NB] = a.lod[e];
+    for (int e = tid; e < T * a.HC; e += HC_THREADS) rs[e / a.HC][e % a.HC] = a.rs[e];
+    __syncthreads();
+    for (int t = 0; t < T; ++t) {
+        const int4 x0 = live ? reinterpret_cast<const int4*>(&lq[t][32 * uj])[0] : make_int4(0, 0, 0, 0);
+        const int4 x1 = live ? reinterpret_cast<const int4*>(&lq[t][32 * uj])[1] : make_int4(0, 0, 0, 0);
+        const float dl = live ? ld[t][uj] : 0.f;
+#pragma unroll
+        for (int c = 0; c < HC_MAX; ++c) {
+            if (c >= a.HC) break;
+            float v = 0.f;
+            if (live) {
+                int s = dot4((int) w0[c].x, x0.x, 0);
+                s = dot4((int) w0[c].y, x0.y, s);
+                s = dot4((int) w0[c].z, x0.z, s);
+                s = dot4((int) w0[c].w, x0.w, s);
+                s = dot4((int) w1[c].x, x1.x, s);
+                s = dot4((int) w1[c].y, x1.y, s);
+                s = dot4((int) w1[c].z, x1.z, s);
+                s = dot4((int) w1[c].w, x1.w, s);
+                v = (wsc[c] * dl) * (float) s;
+            }
+            v = sum_up<16>(v);
+            if (uj == 0) gs[t][c][col] = v;
+        }
+    }
+    __syncthreads();
+    // item (t, c, column): the gate times the normalised stream, R <- R'
+    for (int e = tid; e < T * a.HC * HC_COLS; e += HC_THREADS) {
+        const int cl = e % HC_COLS, c = (e / HC_COLS) % a.HC, t = e / (HC_COLS * a.HC), dc = dc0 + cl;
+        const float rv = rprime(a, t, c, dc);
+        if (a.bo) a.R[(size_t) t * a.HC * a.N + (size_t) c * a.N + dc] = rv;
+        gs[t][c][cl] = sigm_f(gs[t][c][cl]) * (rv * a.w_norm[(size_t) c * a.N + dc] * rs[t][c]);
+    }
+    __syncthreads();
+    for (int e = tid; e < T * HC_COLS; e += HC_THREADS) {
+        const int cl = e % HC_COLS, t = e / HC_COLS;
+        float m = gs[t][0][cl];
+        for (int c = 1; c < a.HC; ++c) m += gs[t][c][cl];
+        m = m / (float) a.HC;
+        a.mixed[(size_t) t * a.N + dc0 + cl] = m;
+        ms[t][cl] = m;
+    }
+    if (a.xq == nullptr) return;
+    __syncthreads();
+    // mixed as q8_1 (k_quantize's arithmetic): a half-wave per row's block
+    for (int t = tid / 32; t < T; t += HC_THREADS / 32) {
+        const int l = tid % 32;
+        const float xi = ms[t][l];
+        const float amax = group_max<32>(fabsf(xi)), sum = group_sum<32>(xi);
+        const float d = amax / 127.0f;
+        uint8_t* blk = a.xq + ((size_t) t * (a.N / 32) + dc0 / 32) * Q81_BYTES;
+        blk[4 + l] = (uint8_t) (int8_t) (amax == 0.0f ? 0 : (int) roundf(xi / d));
+        if (l == 0) *reinterpret_cast<uint32_t*>(blk) = (uint32_t) f2h(d) | ((uint32_t) f2h(sum) << 16);
+    }
+}
+
+template <int TT> void hc_launch(const HcArgs& a, hipStream_t s) {
+    const int NS = a.HC * a.N / HS, RG = (a.LR + a.HC + HA_ROWS - 1) / HA_ROWS;
+    k_hc_down<TT><<<dim3(NS, RG), HA_THREADS, 0, s>>>(a);
+    check(hipGetLastError(), "k_hc_down launch");
+    const int items = a.T * (a.LR / 32 + 1);
+    k_hc_reduce<<<(items + 7) / 8, 256, 0, s>>>(a);
+    check(hipGetLastError(), "k_hc_reduce launch");
+    k_hc_up<TT><<<a.N / HC_COLS, HC_THREADS, 0, s>>>(a);
+    check(hipGetLastError(), "k_hc_up launch");
+}
+
+}  // namespace
+}  // namespace sfnx
+
+using namespace sfnx;
+
+extern "C" size_t sfnx_hc_workspace(int N, int HC, int LR, size_t* offsets) {
+    const HcLayout L = hc_layout(N, HC, LR);
+    if (offsets) {
+        const size_t o[6] = {L.part, L.ssp, L.loq, L.lod, L.rs, L.total};
+        for (int i = 0; i < 6; ++i) offsets[i] = o[i];
+    }
+    return L.total;
+}
+
+extern "C" int sfnx_hc_read(float* R, const float* bo, const float* inj_prev, const float* w_norm, const void* down_q,
+                            const void* down_d, const void* up_q, const void* up_d, const void* w_inj, float eps,
+                            float* mixed, float* inject, void* xq, int T, int N, int HC, int LR, void* ws,
+                            size_t ws_bytes, void* st) {
+    return guarded("sfnx_hc_read", [&] {
+        require(R && w_norm && down_q && down_d && up_q && up_d && mixed && ws, "null argument");
+        require(!bo || inj_prev, "bo needs inj_prev (the last half's inject logits)");
+        require(T >= 1 && T <= SFNX_MAXT, "T out of range (1..16)");
+        require(N > 0 && N % HS == 0, "N must be a positive multiple of 512");
+        require(HC >= 1 && HC <= HC_MAX, "HC must be 1..8");
+        require(LR > 0 && LR % 32 == 0 && LR <= LR_MAX, "LR must be a multiple of 32, at most 512");
+        const HcLayout L = hc_layout(N, HC, LR);
+        require(ws_bytes >= L.total, "workspace smaller than sfnx_hc_workspace()");
+        char* w = (char*) ws;
+        HcArgs a{R, bo, inj_prev, w_norm, (const int8_t*) down_q, (const uint16_t*) down_d, (const int8_t*) up_q,
+                 (const uint16_t*) up_d, (const uint16_t*) w_inj, eps, mixed, inject, (uint8_t*) xq, T, N, HC, LR,
+                 (float*) (w + L.part), (float*) (w + L.ssp), (int8_t*) (w + L.loq), (float*) (w + L.lod),
+                 (float*) (w + L.rs)};
+        hipStream_t s = stream_of(st);
+        if (T == 1) hc_launch<1>(a, s);
+        else if (T <= 4) hc_launch<4>(a, s);
+        else hc_launch<16>(a, s);
+    });
+}

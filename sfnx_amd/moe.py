@@ -432,6 +432,44 @@ def prefill_layer_q8(L: MoeLayer, x: torch.Tensor, y: torch.Tensor, b: PrefillBu
     moe_combine(b.part, b.topw, b.topi, b.logits, y, s.E, s.K, s.shared)
 
 
+# ---------------------------------------------------------------------------------------------------- hc read
+HC_PIECES = ["part", "ssp", "loq", "lod", "rs"]
+
+
+class HcRead:
+    """The hyper-connection read that produces the MoE half's input (src/kernels.cu:1054 hc_read, src/hc.cuh): one read's
+    weights on the device (w_norm [HC N] f32; the down and up Q8S matrices as int8 values and f16 scale bits; the bf16
+    inject rows or None) and a workspace for windows of up to 16 rows."""
+
+    def __init__(self, N: int, HC: int, LR: int, w_norm, down_q, down_d, up_q, up_d, w_inj=None, device="cuda"):
+        self.N, self.HC, self.LR = N, HC, LR
+        dev = lambda a, dt: torch.as_tensor(a).to(device=device, dtype=dt).contiguous()
+        self.w_norm = dev(w_norm, torch.float32)
+        self.dq, self.uq = dev(down_q, torch.int8), dev(up_q, torch.int8)
+        self.dd = dev(torch.as_tensor(down_d).view(torch.int16), torch.int16)
+        self.ud = dev(torch.as_tensor(up_d).view(torch.int16), torch.int16)
+        self.w_inj = None if w_inj is None else dev(torch.as_tensor(w_inj).view(torch.int16), torch.int16)
+        off = (C.c_size_t * 6)()
+        total = lib().sfnx_hc_workspace(N, HC, LR, off)
+        self.off = list(off)
+        self.ws = torch.zeros(total, dtype=torch.uint8, device=device)
+
+    def __call__(self, R, mixed, xq=None, bo=None, inj_prev=None, inject=None, eps: float = 1e-6) -> None:
+        """R [T][HC N] (R' written back when bo is given), mixed [T][N] out, xq [T][N/32] q8_1 out (or None)"""
+        T = R.shape[0]
+        check(lib().sfnx_hc_read(_p(R), _p(bo), _p(inj_prev), _p(self.w_norm), _p(self.dq), _p(self.dd), _p(self.uq),
+                                 _p(self.ud), _p(self.w_inj), eps, _p(mixed), _p(inject), _p(xq), T, self.N, self.HC,
+                                 self.LR, _p(self.ws), self.ws.numel(), _st()))
+
+    def piece(self, name: str, dtype, shape) -> torch.Tensor:
+        i = HC_PIECES.index(name)
+        n = 1
+        for d in shape:
+            n *= d
+        nbytes = n * torch.tensor([], dtype=dtype).element_size()
+        return self.ws[self.off[i]: self.off[i] + nbytes].view(dtype).view(*shape)
+
+
 # ---------------------------------------------------------------------------------------------------- GGUF files
 class Gguf:
     """A GGUF model mapped read-only (src/gguf.hpp:46-88 Gguf): tensors by name, metadata by key."""

@@ -36,6 +36,16 @@ def test_row_bytes():
     (lambda L: L.sfnx_store_pack(12, None, None, 1, 4, 256, None), "multiple of 512"),
     (lambda L: L.sfnx_quantize_q8_1(None, None, 30, 1, None), "multiple of 32"),
     (lambda L: L.sfnx_pf_route(None, 0, 512, 10, None, None, None, None, None, None, None, 1, None), "C must be positive"),
+    (lambda L: L.sfnx_q8s_gemv(1, 100, 2048, 1, 1, 100, 1, None), "rows must be"),
+    (lambda L: L.sfnx_q8s_gemv(1, 96, 2000, 1, 1, 96, 1, None), "cols must be"),
+    (lambda L: L.sfnx_q8s_gemv(1, 96, 2048, 1, 1, 64, 1, None), "out_stride"),
+    (lambda L: L.sfnx_swiglu_stacked_q8_1(1, 1, 500, 1, None), "ffs must be"),
+    (lambda L: L.sfnx_hc_read(1, None, None, 1, 1, 1, 1, 1, None, 1e-6, 1, None, None, 1, 2000, 4, 320, 1, 1 << 30, None), "N must be"),
+    (lambda L: L.sfnx_hc_read(1, None, None, 1, 1, 1, 1, 1, None, 1e-6, 1, None, None, 1, 2560, 9, 320, 1, 1 << 30, None), "HC must be"),
+    (lambda L: L.sfnx_hc_read(1, None, None, 1, 1, 1, 1, 1, None, 1e-6, 1, None, None, 1, 2560, 4, 330, 1, 1 << 30, None), "LR must be"),
+    (lambda L: L.sfnx_hc_read(1, None, None, 1, 1, 1, 1, 1, None, 1e-6, 1, None, None, 1, 2560, 4, 320, 1, 10, None), "workspace smaller"),
+    (lambda L: L.sfnx_hc_read(1, 1, None, 1, 1, 1, 1, 1, None, 1e-6, 1, None, None, 1, 2560, 4, 320, 1, 1 << 30, None), "inj_prev"),
+    (lambda L: L.sfnx_moe_decode_q8s(1, None, 1, 12, 12, 2048, 512, 10, 512, 1, 1, 1, 1e-6, 1, 1 << 30, 0, None), "no shared expert"),
 ])
 def test_bad_arguments_are_refused(call, msg):
     lib = _abi.lib()
