@@ -188,6 +188,7 @@ def main():
         out["q8_0"] = bench_q8_0(moe, torch, args.q8_layers, args.steps, args.warmup)
         out["other_types"] = bench_other_types(moe, torch, args.type_layers, args.steps, args.warmup)
         out["q8s_shared"] = bench_q8s_shared(moe, torch, args.type_layers, args.steps, args.warmup)
+        out["hc_read"] = bench_hc_read(moe, torch)
         log(f"q8s shared: decode {out['q8s_shared']['decode_us_per_token_layer']} us/token-layer")
     print(json.dumps(out), flush=True)
     return 0
@@ -364,6 +365,44 @@ def bench_q8s_shared(moe, torch, NL, steps, warmup):
     r = bench_type(moe, torch, moe.Q4_K, NL, steps, warmup, 2048, 9000, sh_q8s=True)
     r["workload"] = f"Q4_K experts + dense Q8_0 shared expert; decode batch 1 through {NL} stacked layers; 2048-token chunk"
     return r
+
+
+def bench_hc_read(moe, torch, reps=20):
+    """the hyper-connection read that produces the MoE input (src/hc.cuh), at the reference model's shape (N 2560,
+    4 streams, rank 320; src/model.hpp:39): one read with the last half's output folded in, 20 reads a HIP graph;
+    bytes: both Q8S matrices, the bf16 inject rows, w_norm, R read and written, bo, mixed and its q8_1"""
+    N, HC, LR = 2560, 4, 320
+    D = HC * N
+    g = torch.Generator(device="cuda").manual_seed(77)
+    q = lambda r, c: torch.randint(-127, 128, (r, c), dtype=torch.int8, device="cuda", generator=g)
+    sc = lambda r, c: (torch.rand((r, c), device="cuda", generator=g) * 3e-4 + 1.5e-4).half().view(torch.int16)
+    h = moe.HcRead(N, HC, LR, 1 + 0.1 * torch.randn(D, device="cuda", generator=g), q(LR, D), sc(LR, D // 32),
+                   q(D, LR), sc(D, LR // 32), (0.02 * torch.randn((HC, D), device="cuda", generator=g)).bfloat16().view(torch.int16))
+    out = {"workload": "hc read (src/hc.cuh) at N 2560, 4 streams, rank 320, with the fold; HIP-graph replays"}
+    for T in (1, 16):
+        R0 = torch.randn((T, D), device="cuda", generator=g)
+        R = R0.clone()
+        bo = torch.randn((T, N), device="cuda", generator=g)
+        inj = torch.randn((T, HC), device="cuda", generator=g)
+        mixed = torch.empty((T, N), device="cuda")
+        xq = torch.empty(T * (N // 32) * 36, dtype=torch.uint8, device="cuda")
+        injo = torch.empty((T, HC), device="cuda")
+        st = torch.cuda.Stream()
+        st.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(st):
+            h(R, mixed, xq, bo, inj, injo)
+        torch.cuda.current_stream().wait_stream(st)
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):   # 20 reads a graph, so the graph's launch is not what is timed
+            for _ in range(20):
+                h(R, mixed, xq, bo, inj, injo)
+        us = time_us(torch, gr.replay, reps) / 20
+        assert torch.isfinite(mixed).all()
+        nbytes = 2 * (LR * D + LR * D // 32 * 2) + HC * D * 2 + D * 4 + T * (2 * D * 4 + 2 * N * 4 + N // 32 * 36)
+        out[f"T{T}"] = {"us": round(us, 2), "bytes": nbytes, "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+                        "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    log(f"hc read: {out}")
+    return out
 
 
 def bench_other_types(moe, torch, NL, steps, warmup):

@@ -9,7 +9,8 @@
 //        partial dots on xs itself
 //   K_B  rs_c = 1 / sqrt(stream c's square sum / N + eps); lo_r = silu(sum_c fmaf(rs_c, sum_s part) / HC) as int8 per
 //        32; inject_c the same combine without silu
-//   K_C  (32 columns): up row c N + i: 16 lanes, lane b < LR / 32 the 32-block b, (d_w d_lo) dot32, xor 1, 2, 4, 8;
+//   K_C  (32 columns): up row c N + i: per 32-block b of lo, (d_w d_lo) dot32, folded as the reference's 16-lane xor
+//        butterfly folds them (lane b holds block b; partners 1, 2, 4, 8);
 //        mixed_i = sum_c sigm(up) ((R'_c,i w_norm) rs_c) / HC, R <- R', mixed as q8_1
 // The reference runs the three parts in one launch with two grid barriers; here they are three launches, which cost
 // less than a grid barrier on this part (a kernel boundary in a graph ~1.6 us, a 256-workgroup barrier ~2.8 us).
@@ -21,10 +22,11 @@ namespace {
 constexpr int HS = 512;              // columns of a slice
 constexpr int HA_THREADS = 256;      // K_A: 32 rows x 8 lanes
 constexpr int HA_ROWS = HA_THREADS / 8;
-constexpr int HC_COLS = 32;          // K_C: 32 columns x 16 lanes
-constexpr int HC_THREADS = HC_COLS * 16;
+constexpr int HC_COLS = 32;          // K_C: 32 columns a block
+constexpr int HC_THREADS = 512;
 constexpr int HC_MAX = 8;            // streams
 constexpr int LR_MAX = 512;          // 16 lanes x 32
+constexpr int HCLR_MAX = 2048;       // HC LR: a K_C block's up rows (32 columns of every stream) in 64 KB of LDS
 
 struct HcLayout {
     size_t part, ssp, loq, lod, rs, total;
@@ -80,12 +82,8 @@ template <int G> __device__ __forceinline__ float sum_up(float v) {
     return v;
 }
 
-// R'[t][c N + i]: R with the last half's output folded in (src/kernels.cu:1493-1498 as src/hc.cuh:68-72 applies it)
-__device__ __forceinline__ float rprime(const HcArgs& a, int t, int c, int i) {
-    const float r = a.R[(size_t) t * a.HC * a.N + (size_t) c * a.N + i];
-    if (!a.bo) return r;
-    return fmaf(a.bo[(size_t) t * a.N + i], 2.0f * sigm_f(a.inj_prev[t * a.HC + c] / (float) a.HC), r);
-}
+// R' = R + bo 2 sigm(inj_prev / HC) per stream: hc_write's fold (src/kernels.cu:1493-1498) as src/hc.cuh:68-72
+// applies it, fmaf(bo, 2 sigm(.), R), in K_A (its slice) and K_C (its columns), the same bits in both.
 
 // one 32-value block to int8 with a float scale (src/hc.cuh:60-66), a half-wave per block
 __device__ __forceinline__ void q8_block32(float v, int8_t* q, float* d) {
@@ -124,18 +122,45 @@ __global__ void __launch_bounds__(HA_THREADS) k_hc_down(HcArgs a) {
 #pragma unroll
         for (int q = 0; q < 8; ++q) wi[q] = w4[q * 8 + j];
     }
-    // R' and xs for the slice; the square sums (row group 0 only): 32 consecutive columns a half-wave
+    const float wn0 = a.w_norm[col0 + tid], wn1 = a.w_norm[col0 + HA_THREADS + tid];
+    // R' of the slice into xs, the rows' loads (and the fold's inject logits) issued 8 at a time: batch m, element k
+    // is row 4 m + k / 2, column tid + 256 (k % 2), so a thread takes each row's gate once
+    static_assert(HS == 2 * HA_THREADS, "two columns of a slice a thread");
+    for (int t0 = 0; t0 < T; t0 += 4) {
+        float r[8], b[8], g[4];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int t = t0 + k / 2, x = tid + HA_THREADS * (k % 2);
+            if (t < T) {
+                r[k] = a.R[(size_t) t * D + col0 + x];
+                if (a.bo) {
+                    b[k] = a.bo[(size_t) t * a.N + i0 + x];
+                    if (k % 2 == 0) g[k / 2] = a.inj_prev[t * a.HC + c];
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            if (a.bo && t0 + k < T) g[k] = 2.0f * sigm_f(g[k] / (float) a.HC);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int t = t0 + k / 2, x = tid + HA_THREADS * (k % 2);
+            if (t < T) xs[t][x] = a.bo ? fmaf(b[k], g[k / 2], r[k]) : r[k];
+        }
+    }
+    __syncthreads();
+    // the square sums (row group 0 only): 32 consecutive columns a half-wave; then xs = R' w_norm
     const int hw = tid / 32;
     for (int t = 0; t < T; ++t) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int x = h * HA_THREADS + tid;
-            const float r = rprime(a, t, c, i0 + x);
-            xs[t][x] = r * a.w_norm[col0 + x];
+            const float r = xs[t][x];
             if (grp == 0) {
                 const float v = group_sum<32>(r * r);
                 if (tid % 32 == 0) red[t][h * (HA_THREADS / 32) + hw] = v;
             }
+            xs[t][x] = r * (h ? wn1 : wn0);
         }
     }
     __syncthreads();
@@ -149,7 +174,7 @@ __global__ void __launch_bounds__(HA_THREADS) k_hc_down(HcArgs a) {
         q8_block32(xs[t][32 * b + tid % 32], &xq[t][32 * b], &xd[t][b]);
     }
     __syncthreads();
-    if (!dn_row && !inj_row && row >= ROWS) return;   // (whole 8-lane groups: the butterfly stays inside live groups)
+    if (row >= ROWS) return;   // whole 8-lane groups: the butterfly stays inside live groups
     for (int t = 0; t < T; ++t) {
         float acc = 0.f;
         if (dn_row) {
@@ -177,37 +202,61 @@ __global__ void __launch_bounds__(HA_THREADS) k_hc_down(HcArgs a) {
             }
         }
         acc = sum_up<8>(acc);
-        if (j == 0 && row < ROWS) a.part[((size_t) t * NS + s) * ROWS + row] = (dn_row || inj_row) ? acc : 0.f;
+        if (j == 0) a.part[((size_t) t * NS + s) * ROWS + row] = acc;
     }
 }
 
 // ------------------------------------------------------------------------------------------------ K_B
+// The combine of row r for token t (src/hc.cuh:251-289): rs_c = 1 / sqrt(stream c's slice square sums in order / N +
+// eps), then sum_c fmaf(rs_c, stream c's slice partials in order, sum).  The square sums and the partials are loaded
+// together, 32 slices at a time (one round trip for the reference's 20); rsv receives rs_c.
+__device__ __forceinline__ float hc_combine(const HcArgs& a, int t, int r, float (&rsv)[HC_MAX]) {
+    const int NS = a.HC * a.N / HS, SPS = a.N / HS, ROWS = a.LR + a.HC;
+    float vs = 0.f, p = 0.f, sum = 0.f;
+    int ss = 0, c = 0;   // slice within the stream, stream
+    for (int q0 = 0; q0 < NS; q0 += 32) {
+        float sv[32], pv[32];
+#pragma unroll
+        for (int k = 0; k < 32; ++k) {
+            const int q = q0 + k;
+            sv[k] = q < NS ? a.ssp[(size_t) t * NS + q] : 0.f;
+            pv[k] = q < NS ? a.part[((size_t) t * NS + q) * ROWS + r] : 0.f;
+        }
+#pragma unroll
+        for (int k = 0; k < 32; ++k) {
+            if (q0 + k >= NS) break;
+            vs += sv[k];
+            p += pv[k];
+            if (++ss == SPS) {
+                const float rc = 1.0f / sqrtf(vs / (float) a.N + a.eps);
+#pragma unroll
+                for (int cc = 0; cc < HC_MAX; ++cc)
+                    if (cc == c) rsv[cc] = rc;
+                sum = fmaf(rc, p, sum);
+                vs = 0.f;
+                p = 0.f;
+                ss = 0;
+                ++c;
+            }
+        }
+    }
+    return sum;
+}
+
 // item (t, b): b < LR / 32 a block of lo, b == LR / 32 the inject rows; a half-wave each
 __global__ void __launch_bounds__(256) k_hc_reduce(HcArgs a) {
     const int NB = a.LR / 32, items = a.T * (NB + 1), l = threadIdx.x % 32;
     const int it = blockIdx.x * 8 + threadIdx.x / 32;
-    const int NS = a.HC * a.N / HS, SPS = a.N / HS, ROWS = a.LR + a.HC;
     if (it >= items) return;   // whole half-waves leave together
     const int t = it / (NB + 1), b = it % (NB + 1);
-    float rsv[HC_MAX];
-#pragma unroll
-    for (int c = 0; c < HC_MAX; ++c) {
-        if (c >= a.HC) break;
-        float v = 0.f;
-        for (int ss = 0; ss < SPS; ++ss) v += a.ssp[(size_t) t * NS + c * SPS + ss];
-        rsv[c] = 1.0f / sqrtf(v / (float) a.N + a.eps);
-    }
-    if (b == 0 && l < a.HC) a.rs[t * a.HC + l] = rsv[l];
     const bool inj = b == NB;
     if (inj && (a.w_inj == nullptr || a.inject == nullptr)) return;
-    const int r = inj ? a.LR + min(l, a.HC - 1) : 32 * b + l;
-    float sum = 0.f;
+    float rsv[HC_MAX];
+    const float sum = hc_combine(a, t, inj ? a.LR + min(l, a.HC - 1) : 32 * b + l, rsv);
+    if (b == 0 && l < a.HC) {
 #pragma unroll
-    for (int c = 0; c < HC_MAX; ++c) {
-        if (c >= a.HC) break;
-        float p = 0.f;
-        for (int ss = 0; ss < SPS; ++ss) p += a.part[((size_t) t * NS + c * SPS + ss) * ROWS + r];
-        sum = fmaf(rsv[c], p, sum);
+        for (int c = 0; c < HC_MAX; ++c)
+            if (c == l) a.rs[t * a.HC + l] = rsv[c];
     }
     if (inj) {
         if (l < a.HC) a.inject[t * a.HC + l] = sum;
@@ -217,65 +266,121 @@ __global__ void __launch_bounds__(256) k_hc_reduce(HcArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------------ K_C
-template <int TT>
+// 32 columns a block.  The block's up rows (HC streams x 32 columns, LR int8 each, and their scales) are staged in LDS;
+// thread (c, column) then takes its row whole: the 32-blocks' (d_w d_lo) dot32 values, folded in the order of the
+// reference's 16-lane xor butterfly (partner 1, 2, 4, 8; lanes past LR / 32 hold zeros), so no lane idles in a
+// shuffle.  ONE (one row, LR + HC <= 512): the block makes lo and rs itself from the slices' partials (K_B's sums,
+// the same bits), so the read takes two launches (src/hc.cuh's one-barrier form does the same).
+template <int TT, bool ONE>
 __global__ void __launch_bounds__(HC_THREADS) k_hc_up(HcArgs a) {
+    constexpr int PER = (TT * HC_MAX * HC_COLS + HC_THREADS - 1) / HC_THREADS;   // (t, c, column) items a thread
+    __shared__ __align__(16) int8_t wq[HC_COLS * HCLR_MAX];         // row rr = c 32 + column at rr LR
+    __shared__ float wsl[HC_COLS * HCLR_MAX / 32];
     __shared__ __align__(16) int8_t lq[TT][LR_MAX];
     __shared__ float ld[TT][LR_MAX / 32];
     __shared__ float rs[TT][HC_MAX];
+    __shared__ float sg[TT][HC_MAX];
     __shared__ float gs[TT][HC_MAX][HC_COLS];
     __shared__ float ms[TT][HC_COLS];
     const int T = a.T, tid = threadIdx.x, NB = a.LR / 32, dc0 = blockIdx.x * HC_COLS;
-    const int col = tid / 16, uj = tid % 16;
-    const bool live = uj < NB;
-    // the column's up rows (one 32-block a lane), every stream
-    uint4 w0[HC_MAX], w1[HC_MAX];
-    float wsc[HC_MAX];
-#pragma unroll
-    for (int c = 0; c < HC_MAX; ++c) {
-        if (c >= a.HC) break;
-        const size_t u = (size_t) c * a.N + dc0 + col;
-        if (live) {
-            const uint4* wp = reinterpret_cast<const uint4*>(a.uq + u * a.LR + 32 * uj);
-            w0[c] = wp[0];
-            w1[c] = wp[1];
-            wsc[c] = h2f(a.ud[u * NB + uj]);
+    const int nitem = T * a.HC * HC_COLS, nrow = a.HC * HC_COLS;
+    // every load of the block first: the up rows (16 bytes a thread at a time, 4 in flight), their scales, the
+    // (t, c, column) items' R, bo and w_norm, then lo and rs
+    {
+        const int per_row = a.LR / 16, n16 = nrow * per_row;
+#pragma unroll 4
+        for (int e = tid; e < n16; e += HC_THREADS) {
+            const int rr = e / per_row;
+            const size_t u = (size_t) (rr / HC_COLS) * a.N + dc0 + rr % HC_COLS;
+            reinterpret_cast<uint4*>(wq)[e] = reinterpret_cast<const uint4*>(a.uq + u * a.LR)[e % per_row];
+        }
+        for (int e = tid; e < nrow * NB; e += HC_THREADS) {
+            const int rr = e / NB;
+            wsl[e] = h2f(a.ud[((size_t) (rr / HC_COLS) * a.N + dc0 + rr % HC_COLS) * NB + e % NB]);
         }
     }
-    for (int e = tid; e < T * a.LR / 4; e += HC_THREADS)
-        reinterpret_cast<int*>(&lq[e / (a.LR / 4)][0])[e % (a.LR / 4)] = reinterpret_cast<const int*>(a.loq)[e];
-    for (int e = tid; e < T * NB; e += HC_THREADS) ld[e / NB][e % NB] = a.lod[e];
-    for (int e = tid; e < T * a.HC; e += HC_THREADS) rs[e / a.HC][e % a.HC] = a.rs[e];
-    __syncthreads();
-    for (int t = 0; t < T; ++t) {
-        const int4 x0 = live ? reinterpret_cast<const int4*>(&lq[t][32 * uj])[0] : make_int4(0, 0, 0, 0);
-        const int4 x1 = live ? reinterpret_cast<const int4*>(&lq[t][32 * uj])[1] : make_int4(0, 0, 0, 0);
-        const float dl = live ? ld[t][uj] : 0.f;
+    float rv[PER], bv[PER], wn[PER];
 #pragma unroll
-        for (int c = 0; c < HC_MAX; ++c) {
-            if (c >= a.HC) break;
-            float v = 0.f;
-            if (live) {
-                int s = dot4((int) w0[c].x, x0.x, 0);
-                s = dot4((int) w0[c].y, x0.y, s);
-                s = dot4((int) w0[c].z, x0.z, s);
-                s = dot4((int) w0[c].w, x0.w, s);
-                s = dot4((int) w1[c].x, x1.x, s);
-                s = dot4((int) w1[c].y, x1.y, s);
-                s = dot4((int) w1[c].z, x1.z, s);
-                s = dot4((int) w1[c].w, x1.w, s);
-                v = (wsc[c] * dl) * (float) s;
+    for (int k = 0; k < PER; ++k) {
+        const int e = tid + k * HC_THREADS;
+        if (e < nitem) {
+            const int cl = e % HC_COLS, c = (e / HC_COLS) % a.HC, t = e / (HC_COLS * a.HC), dc = dc0 + cl;
+            rv[k] = a.R[(size_t) t * a.HC * a.N + (size_t) c * a.N + dc];
+            if (a.bo) bv[k] = a.bo[(size_t) t * a.N + dc];
+            wn[k] = a.w_norm[(size_t) c * a.N + dc];
+        }
+    }
+    if constexpr (ONE) {
+        const bool lo_row = tid < a.LR, inj_row = tid >= a.LR && tid < a.LR + a.HC && a.w_inj != nullptr;
+        float rsv[HC_MAX];
+        const float sum = lo_row || inj_row ? hc_combine(a, 0, tid, rsv) : 0.f;
+        if (lo_row) q8_block32(silu_f(sum / (float) a.HC), &lq[0][32 * (tid / 32)], &ld[0][tid / 32]);
+        if (inj_row && blockIdx.x == 0 && a.inject) a.inject[tid - a.LR] = sum;
+        if (tid == 0) {
+#pragma unroll
+            for (int c = 0; c < HC_MAX; ++c)
+                if (c < a.HC) {
+                    rs[0][c] = rsv[c];
+                    if (blockIdx.x == 0) a.rs[c] = rsv[c];
+                }
+        }
+    } else {
+        const int nq = T * a.LR / 4;
+        for (int e0 = tid; e0 < nq; e0 += 4 * HC_THREADS) {
+            int v[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) v[k] = e0 + k * HC_THREADS < nq ? reinterpret_cast<const int*>(a.loq)[e0 + k * HC_THREADS] : 0;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int e = e0 + k * HC_THREADS;
+                if (e < nq) reinterpret_cast<int*>(&lq[e / (a.LR / 4)][0])[e % (a.LR / 4)] = v[k];
             }
-            v = sum_up<16>(v);
-            if (uj == 0) gs[t][c][col] = v;
+        }
+        if (tid < T * NB) ld[tid / NB][tid % NB] = a.lod[tid];
+        if (tid < T * a.HC) rs[tid / a.HC][tid % a.HC] = a.rs[tid];
+    }
+    if (a.bo && tid < T * a.HC) sg[tid / a.HC][tid % a.HC] = 2.0f * sigm_f(a.inj_prev[tid] / (float) a.HC);
+    __syncthreads();
+    // thread (c, column): its up row against lo, row t at a time
+    if (tid < nrow) {
+        const int c = tid / HC_COLS, cl = tid % HC_COLS;
+        for (int t = 0; t < T; ++t) {
+            // block b's (d_w d_lo) dot32, 0 past LR / 32 (the lanes of the reference's butterfly that hold no block)
+            auto blk = [&](int b) {
+                if (b >= NB) return 0.f;
+                const int4* wr = reinterpret_cast<const int4*>(wq + tid * NB * 32 + 32 * b);
+                const int4* xr = reinterpret_cast<const int4*>(&lq[t][32 * b]);
+                const int4 w0 = wr[0], w1 = wr[1], x0 = xr[0], x1 = xr[1];
+                int s = dot4(w0.x, x0.x, 0);
+                s = dot4(w0.y, x0.y, s);
+                s = dot4(w0.z, x0.z, s);
+                s = dot4(w0.w, x0.w, s);
+                s = dot4(w1.x, x1.x, s);
+                s = dot4(w1.y, x1.y, s);
+                s = dot4(w1.z, x1.z, s);
+                s = dot4(w1.w, x1.w, s);
+                return (wsl[tid * NB + b] * ld[t][b]) * (float) s;
+            };
+            // the butterfly's tree: lane 0 ends with ((v0+v1)+(v2+v3)) + ... in pairs at distance 1, 2, 4, 8
+            float u[8], w[4];
+#pragma unroll
+            for (int b = 0; b < 8; ++b) u[b] = blk(2 * b) + blk(2 * b + 1);
+#pragma unroll
+            for (int b = 0; b < 4; ++b) w[b] = u[2 * b] + u[2 * b + 1];
+            gs[t][c][cl] = (w[0] + w[1]) + (w[2] + w[3]);
         }
     }
     __syncthreads();
     // item (t, c, column): the gate times the normalised stream, R <- R'
-    for (int e = tid; e < T * a.HC * HC_COLS; e += HC_THREADS) {
-        const int cl = e % HC_COLS, c = (e / HC_COLS) % a.HC, t = e / (HC_COLS * a.HC), dc = dc0 + cl;
-        const float rv = rprime(a, t, c, dc);
-        if (a.bo) a.R[(size_t) t * a.HC * a.N + (size_t) c * a.N + dc] = rv;
-        gs[t][c][cl] = sigm_f(gs[t][c][cl]) * (rv * a.w_norm[(size_t) c * a.N + dc] * rs[t][c]);
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const int e = tid + k * HC_THREADS;
+        if (e < nitem) {
+            const int cl = e % HC_COLS, c = (e / HC_COLS) % a.HC, t = e / (HC_COLS * a.HC), dc = dc0 + cl;
+            const float r = a.bo ? fmaf(bv[k], sg[t][c], rv[k]) : rv[k];
+            if (a.bo) a.R[(size_t) t * a.HC * a.N + (size_t) c * a.N + dc] = r;
+            gs[t][c][cl] = sigm_f(gs[t][c][cl]) * (r * wn[k] * rs[t][c]);
+        }
     }
     __syncthreads();
     for (int e = tid; e < T * HC_COLS; e += HC_THREADS) {
@@ -304,10 +409,19 @@ template <int TT> void hc_launch(const HcArgs& a, hipStream_t s) {
     const int NS = a.HC * a.N / HS, RG = (a.LR + a.HC + HA_ROWS - 1) / HA_ROWS;
     k_hc_down<TT><<<dim3(NS, RG), HA_THREADS, 0, s>>>(a);
     check(hipGetLastError(), "k_hc_down launch");
-    const int items = a.T * (a.LR / 32 + 1);
-    k_hc_reduce<<<(items + 7) / 8, 256, 0, s>>>(a);
-    check(hipGetLastError(), "k_hc_reduce launch");
-    k_hc_up<TT><<<a.N / HC_COLS, HC_THREADS, 0, s>>>(a);
+    if constexpr (TT == 1) {
+        if (a.LR + a.HC <= HC_THREADS) {
+            k_hc_up<TT, true><<<a.N / HC_COLS, HC_THREADS, 0, s>>>(a);
+            check(hipGetLastError(), "k_hc_up launch");
+            return;
+        }
+    }
+    {
+        const int items = a.T * (a.LR / 32 + 1);
+        k_hc_reduce<<<(items + 7) / 8, 256, 0, s>>>(a);
+        check(hipGetLastError(), "k_hc_reduce launch");
+        k_hc_up<TT, false><<<a.N / HC_COLS, HC_THREADS, 0, s>>>(a);
+    }
     check(hipGetLastError(), "k_hc_up launch");
 }
 
@@ -336,6 +450,7 @@ extern "C" int sfnx_hc_read(float* R, const float* bo, const float* inj_prev, co
         require(N > 0 && N % HS == 0, "N must be a positive multiple of 512");
         require(HC >= 1 && HC <= HC_MAX, "HC must be 1..8");
         require(LR > 0 && LR % 32 == 0 && LR <= LR_MAX, "LR must be a multiple of 32, at most 512");
+        require(HC * LR <= HCLR_MAX, "HC LR must be at most 2048");
         const HcLayout L = hc_layout(N, HC, LR);
         require(ws_bytes >= L.total, "workspace smaller than sfnx_hc_workspace()");
         char* w = (char*) ws;

@@ -43,6 +43,7 @@ def test_row_bytes():
     (lambda L: L.sfnx_hc_read(1, None, None, 1, 1, 1, 1, 1, None, 1e-6, 1, None, None, 1, 2000, 4, 320, 1, 1 << 30, None), "N must be"),
     (lambda L: L.sfnx_hc_read(1, None, None, 1, 1, 1, 1, 1, None, 1e-6, 1, None, None, 1, 2560, 9, 320, 1, 1 << 30, None), "HC must be"),
     (lambda L: L.sfnx_hc_read(1, None, None, 1, 1, 1, 1, 1, None, 1e-6, 1, None, None, 1, 2560, 4, 330, 1, 1 << 30, None), "LR must be"),
+    (lambda L: L.sfnx_hc_read(1, None, None, 1, 1, 1, 1, 1, None, 1e-6, 1, None, None, 1, 2560, 8, 512, 1, 1 << 30, None), "HC LR must be"),
     (lambda L: L.sfnx_hc_read(1, None, None, 1, 1, 1, 1, 1, None, 1e-6, 1, None, None, 1, 2560, 4, 320, 1, 10, None), "workspace smaller"),
     (lambda L: L.sfnx_hc_read(1, 1, None, 1, 1, 1, 1, 1, None, 1e-6, 1, None, None, 1, 2560, 4, 320, 1, 1 << 30, None), "inj_prev"),
     (lambda L: L.sfnx_moe_decode_q8s(1, None, 1, 12, 12, 2048, 512, 10, 512, 1, 1, 1, 1e-6, 1, 1 << 30, 0, None), "no shared expert"),
