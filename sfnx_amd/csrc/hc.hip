@@ -274,7 +274,7 @@ __global__ void __launch_bounds__(256) k_hc_reduce(HcArgs a) {
 template <int TT, bool ONE>
 __global__ void __launch_bounds__(HC_THREADS) k_hc_up(HcArgs a) {
     constexpr int PER = (TT * HC_MAX * HC_COLS + HC_THREADS - 1) / HC_THREADS;   // (t, c, column) items a thread
-    __shared__ __align__(16) int8_t wq[HC_COLS * HCLR_MAX];         // row rr = c 32 + column at rr LR
+    __shared__ __align__(16) int8_t wq[HC_COLS * (HCLR_MAX + 16 * HC_MAX)];   // row rr = c 32 + column at rr (LR + 16)
     __shared__ float wsl[HC_COLS * HCLR_MAX / 32];
     __shared__ __align__(16) int8_t lq[TT][LR_MAX];
     __shared__ float ld[TT][LR_MAX / 32];
@@ -292,7 +292,7 @@ __global__ void __launch_bounds__(HC_THREADS) k_hc_up(HcArgs a) {
         for (int e = tid; e < n16; e += HC_THREADS) {
             const int rr = e / per_row;
             const size_t u = (size_t) (rr / HC_COLS) * a.N + dc0 + rr % HC_COLS;
-            reinterpret_cast<uint4*>(wq)[e] = reinterpret_cast<const uint4*>(a.uq + u * a.LR)[e % per_row];
+            reinterpret_cast<uint4*>(wq)[rr * (per_row + 1) + e % per_row] = reinterpret_cast<const uint4*>(a.uq + u * a.LR)[e % per_row];
         }
         for (int e = tid; e < nrow * NB; e += HC_THREADS) {
             const int rr = e / NB;
@@ -341,14 +341,14 @@ __global__ void __launch_bounds__(HC_THREADS) k_hc_up(HcArgs a) {
     }
     if (a.bo && tid < T * a.HC) sg[tid / a.HC][tid % a.HC] = 2.0f * sigm_f(a.inj_prev[tid] / (float) a.HC);
     __syncthreads();
-    // thread (c, column): its up row against lo, row t at a time
-    if (tid < nrow) {
-        const int c = tid / HC_COLS, cl = tid % HC_COLS;
-        for (int t = 0; t < T; ++t) {
+    // item (t, c, column): the up row c 32 + column of the block against lo row t; the items spread over the block
+    for (int it = tid; it < T * nrow; it += HC_THREADS) {
+        const int t = it / nrow, rr = it % nrow, c = rr / HC_COLS, cl = rr % HC_COLS;
+        {
             // block b's (d_w d_lo) dot32, 0 past LR / 32 (the lanes of the reference's butterfly that hold no block)
             auto blk = [&](int b) {
                 if (b >= NB) return 0.f;
-                const int4* wr = reinterpret_cast<const int4*>(wq + tid * NB * 32 + 32 * b);
+                const int4* wr = reinterpret_cast<const int4*>(wq + rr * (NB * 32 + 16) + 32 * b);
                 const int4* xr = reinterpret_cast<const int4*>(&lq[t][32 * b]);
                 const int4 w0 = wr[0], w1 = wr[1], x0 = xr[0], x1 = xr[1];
                 int s = dot4(w0.x, x0.x, 0);
@@ -359,7 +359,7 @@ __global__ void __launch_bounds__(HC_THREADS) k_hc_up(HcArgs a) {
                 s = dot4(w1.y, x1.y, s);
                 s = dot4(w1.z, x1.z, s);
                 s = dot4(w1.w, x1.w, s);
-                return (wsl[tid * NB + b] * ld[t][b]) * (float) s;
+                return (wsl[rr * NB + b] * ld[t][b]) * (float) s;
             };
             // the butterfly's tree: lane 0 ends with ((v0+v1)+(v2+v3)) + ... in pairs at distance 1, 2, 4, 8
             float u[8], w[4];
