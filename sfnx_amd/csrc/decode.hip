@@ -362,7 +362,8 @@ __device__ inline void warm_router_rows(const float* W, int rows, int H, void* j
 // K2 for a window of one row (the batch-1 decode): the picks of one token are distinct experts, so job j is pick j
 // (n = 1, row 0, output pair j) and the shared expert's job is the last; no numbering is needed.  Every wavefront takes
 // the top-K itself from registers, so the weight loads wait on no barrier after the routing.
-template <int TYPE, int G, int NV>
+// SHQ: a dense Q8_0 shared expert (sh_gu), in an instantiation of its own so the routed-only kernel keeps its registers
+template <int TYPE, int G, int NV, bool SHQ>
 __global__ void __launch_bounds__(2 * d2_threads<TYPE>()) k_dec_experts1(
     const uint8_t* __restrict__ A, size_t sa, const float* __restrict__ Wn, int H, int E, int K, int ff, int shared,
     const float* __restrict__ logits,
@@ -370,8 +371,20 @@ __global__ void __launch_bounds__(2 * d2_threads<TYPE>()) k_dec_experts1(
     sfnx_job* __restrict__ jd, int* __restrict__ njobs_g, float* __restrict__ gu, int8_t* __restrict__ hq_q,
     float* __restrict__ hq_d, int* __restrict__ hq_s, int* __restrict__ route_x, const uint8_t* __restrict__ sh_gu) {
     constexpr int LPR = lpr_of<TYPE>(), NW = 2 * d2_threads<TYPE>() / WAVE, RPW = WAVE / LPR;
-    const int NFB = ff / 32, myjob = blockIdx.x / NFB, fb = blockIdx.x % NFB;
+    const int NFB = ff / 32, fb = blockIdx.x % NFB;
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    // a dense Q8_0 shared expert's job is job 0 here (the routed jobs follow), so its blocks know their rows before the
+    // routing and load them at once: 64 rows of 34 B a block of 32 values against 18 B (Q4_K), it is the longest job
+    constexpr bool sh_first = SHQ;
+    const bool q8s = SHQ && (int) blockIdx.x < NFB;
+    // (held in registers up to 2048 columns; wider rows stream at the dot, as the registers would spill)
+    constexpr bool SHR = SHQ && G <= 4;
+    Q8sRow<LPR, SHR ? G : 1> ws;
+    if constexpr (SHR) {
+        const int up_half = threadIdx.x / WAVE >= NW / 2;
+        const int srow = (up_half ? ff : 0) + fb * 32 + (up_half ? wave - NW / 2 : wave) * RPW + lane / LPR;
+        if (q8s) ws.issue(q80_planes(sh_gu, 2 * ff, H), srow, H, lane % LPR);
+    }
     __shared__ float gbuf[32], ubuf[32];
     __shared__ uint32_t junk[WAVE];
     extern __shared__ __align__(16) unsigned char lds[];
@@ -390,20 +403,21 @@ __global__ void __launch_bounds__(2 * d2_threads<TYPE>()) k_dec_experts1(
     topk_picks<NV>(lv, K, lane, pick, pord);
     const int nr = __popcll(__ballot(lane < K && pick >= 0));
     const int nj = nr + (shared ? 1 : 0);
+    // job of this block: routed pick j = jb, the shared job at jb = nr (or first, when dense: then jb = myjob - 1)
+    const int myjob = blockIdx.x / NFB, jb = sh_first ? (q8s ? nr : myjob - 1) : myjob;
+    const bool has_job = sh_first ? q8s || jb < nr : jb < nj;
     PROF(1, 1)
-    if (myjob >= nj && blockIdx.x >= XCDS) {
+    if (!has_job && blockIdx.x >= XCDS) {
         warm_wait();
         return;
     }
-    const int ex = myjob < nr ? __builtin_amdgcn_readlane(pick, myjob) : E, out = myjob < nr ? myjob : K;
+    const int ex = jb < nr ? __builtin_amdgcn_readlane(pick, jb) : E, out = jb < nr ? jb : K;
     // the first half of the waves take the 32 gate rows, the second half the matching up rows
     const bool up = wave >= NW / 2;
     const int rw = lane / LPR, ln = lane % LPR, fl = (up ? wave - NW / 2 : wave) * RPW + rw, row = (up ? ff : 0) + fb * 32 + fl;
     const uint8_t* mat = A + (size_t) ex * sa;
-    // the shared expert from its own dense Q8_0 matrix when one is given (the reference's q8s sums)
-    const bool q8s = sh_gu != nullptr && myjob == nr;
     typename RowOf<TYPE, G>::R wr;
-    if (myjob < nj && !q8s) RowOf<TYPE, G>::issue(wr, mat, 2 * ff, row, H, ln);
+    if (has_job && !q8s) RowOf<TYPE, G>::issue(wr, mat, 2 * ff, row, H, ln);
     if (blockIdx.x < XCDS && wave == 0) {   // the routing, published for K3 and the caller, while the rows load
         const float w = topk_weight(pick, pord, K);
         // a copy for K3's workgroups of this XCD (workgroup b on XCD b % 8), read from this XCD's L2
@@ -430,14 +444,16 @@ __global__ void __launch_bounds__(2 * d2_threads<TYPE>()) k_dec_experts1(
             njobs_g[1] = 0;
         }
     }
-    if (myjob >= nj) {
+    if (!has_job) {
         warm_wait();
         return;
     }
     __syncthreads();   // the staged activations
     PROF(1, 3)
-    const float v = group_sum<LPR>(q8s ? q8s_dot<LPR>(q80_planes(sh_gu, 2 * ff, H), row, H, ln, a, 0)
-                                       : wr.dot1(a, ln));   // each group as it arrives
+    float v;
+    if constexpr (SHR) v = group_sum<LPR>(q8s ? ws.dot(a, 0, ln) : wr.dot1(a, ln));
+    else if constexpr (SHQ) v = group_sum<LPR>(q8s ? q8s_dot<LPR>(q80_planes(sh_gu, 2 * ff, H), row, H, ln, a, 0) : wr.dot1(a, ln));
+    else v = group_sum<LPR>(wr.dot1(a, ln));   // each group as it arrives
     if (ln == 0) {
         gu[(size_t) out * 2 * ff + row] = v;
         (up ? ubuf : gbuf)[fl] = v;
@@ -571,7 +587,7 @@ __global__ void __launch_bounds__(D3_THREADS) k_dec_down(const uint8_t* __restri
 // K3 for a window of one row: pair k is pick k, so a task's expert comes straight from the picks (job j = pick j, the
 // shared expert's job last) and its weight loads are issued before the activations are staged; every other request
 // of the block (picks, weights, the shared gate's logit, h, the residual rows) is issued up front, with one wait.
-template <int TYPE, int G2, int NB>
+template <int TYPE, int G2, int NB, bool SHQ>
 __global__ void __launch_bounds__(D3_THREADS) k_dec_down1(const uint8_t* __restrict__ A, size_t sa, int H, int E, int K,
                                                          int ff, int shared, const float* __restrict__ logits,
                                                          const int* __restrict__ topi, const float* __restrict__ topw,
@@ -614,11 +630,18 @@ __global__ void __launch_bounds__(D3_THREADS) k_dec_down1(const uint8_t* __restr
         ex[b] = __shfl(tp, j < nr ? j : 0);
         pp[b] = j < nr ? j : K;
     }
+    // a dense shared expert's task (at most one a lane group: its 8 tasks are consecutive) from its own rows
+    Q8sRow<LPR, SHQ ? G2 : 1> wsh;
+    int bsh = -1;
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
         const int task = g + b * GROUPS, r = task % D3_ROWS;
-        if (task < ntask && !(sh_dn != nullptr && pp[b] == K))
+        if (SHQ && task < ntask && pp[b] == K) {
+            wsh.issue(q80_planes(sh_dn, H, ff), row0 + r, ff, ln);
+            bsh = b;
+        } else if (task < ntask) {
             RowOf<TYPE, G2>::issue(w[b], A + (size_t) (pp[b] < K ? ex[b] : E) * sa, H, row0 + r, ff, ln);
+        }
     }
     // the staged activations
     const Acts a = acts_in(lds, NP, ff);
@@ -642,14 +665,10 @@ __global__ void __launch_bounds__(D3_THREADS) k_dec_down1(const uint8_t* __restr
             if (ln == 0) part[pp[b]][task % D3_ROWS] = v;
         }
     }
-    if (sh_dn != nullptr) {   // the shared expert's tasks from its own dense Q8_0 matrix (q8s sums), one copy of the code
-#pragma unroll 1
-        for (int b = 0; b < NB; ++b) {
-            const int task = g + b * GROUPS;
-            if (task < ntask && pp[b] == K) {
-                const float v = group_sum<LPR>(q8s_dot<LPR>(q80_planes(sh_dn, H, ff), row0 + task % D3_ROWS, ff, ln, a, K));
-                if (ln == 0) part[K][task % D3_ROWS] = v;
-            }
+    if constexpr (SHQ) {
+        if (bsh >= 0) {   // the shared expert's task from its own dense Q8_0 rows (q8s sums)
+            const float v = group_sum<LPR>(wsh.dot(a, K, ln));
+            if (ln == 0) part[K][(g + bsh * GROUPS) % D3_ROWS] = v;
         }
     }
     // windows with more tasks than one batch (K > 11): the rest, a batch at a time
@@ -733,10 +752,10 @@ void launch_k2(const DecArgs& d, const sfnx_moe_layer_w& w, const DecLayout& L, 
             (float*) (ws + L.hq_d), (int*) (ws + L.hq_s), d.sh_gu);
     }
 }
-template <int TYPE, int G, int NV>
+template <int TYPE, int G, int NV, bool SHQ>
 void launch_k2_one(const DecArgs& d, const sfnx_moe_layer_w& w, const DecLayout& L, char* ws, hipStream_t s) {
     const int njmax = d.K + (d.shared ? 1 : 0);
-    launch(1, k_dec_experts1<TYPE, G, NV>, dim3(njmax * (d.ff / 32)), dim3(2 * d2_threads<TYPE>()), acts_bytes(1, d.H), s,
+    launch(1, k_dec_experts1<TYPE, G, NV, SHQ>, dim3(njmax * (d.ff / 32)), dim3(2 * d2_threads<TYPE>()), acts_bytes(1, d.H), s,
         (const uint8_t*) w.gu, w.gu_stride, d.Wn, d.H, d.E, d.K, d.ff, d.shared, (const float*) (ws + L.logits),
         (const uint8_t*) (ws + L.xq), (int*) (ws + L.topi), (float*) (ws + L.topw), (sfnx_job*) (ws + L.jg),
         (sfnx_job*) (ws + L.jd), (int*) (ws + L.njobs), (float*) (ws + L.gu), (int8_t*) (ws + L.hq_q),
@@ -744,14 +763,21 @@ void launch_k2_one(const DecArgs& d, const sfnx_moe_layer_w& w, const DecLayout&
 }
 template <int TYPE, int G>
 void launch_k2_tt1(const DecArgs& d, const sfnx_moe_layer_w& w, const DecLayout& L, char* ws, hipStream_t s) {
-    if (d.E <= 256) launch_k2_one<TYPE, G, 4>(d, w, L, ws, s);
-    else if (d.E <= 512) launch_k2_one<TYPE, G, 8>(d, w, L, ws, s);
-    else launch_k2_one<TYPE, G, 16>(d, w, L, ws, s);
+    if (d.sh_gu) {
+        if (d.E <= 256) launch_k2_one<TYPE, G, 4, true>(d, w, L, ws, s);
+        else if (d.E <= 512) launch_k2_one<TYPE, G, 8, true>(d, w, L, ws, s);
+        else launch_k2_one<TYPE, G, 16, true>(d, w, L, ws, s);
+    } else {
+        if (d.E <= 256) launch_k2_one<TYPE, G, 4, false>(d, w, L, ws, s);
+        else if (d.E <= 512) launch_k2_one<TYPE, G, 8, false>(d, w, L, ws, s);
+        else launch_k2_one<TYPE, G, 16, false>(d, w, L, ws, s);
+    }
 }
 template <int TYPE, int G2>
 void launch_k3_one(const DecArgs& d, const sfnx_moe_layer_w& w, float* x, const DecLayout& L, char* ws, hipStream_t s) {
     constexpr int NB = is_kquant(TYPE) ? 3 : 6;   // 11 jobs x 8 rows in one batch
-    launch(2, k_dec_down1<TYPE, G2, NB>, dim3(d.H / D3_ROWS), dim3(D3_THREADS), acts_bytes(d.K + 1, d.ff), s,
+    auto kern = d.sh_dn ? k_dec_down1<TYPE, G2, NB, true> : k_dec_down1<TYPE, G2, NB, false>;
+    launch(2, kern, dim3(d.H / D3_ROWS), dim3(D3_THREADS), acts_bytes(d.K + 1, d.ff), s,
         (const uint8_t*) w.dn, w.dn_stride, d.H, d.E, d.K, d.ff, d.shared, (const float*) (ws + L.logits),
         (const int*) (ws + L.topi), (const float*) (ws + L.topw), (const int8_t*) (ws + L.hq_q),
         (const float*) (ws + L.hq_d), (const int*) (ws + L.hq_s), (float*) (ws + L.y), x, (const int*) (ws + L.route_x),

@@ -282,6 +282,45 @@ template <int BPL, int TYPE> struct NbRow {
 // group_sum<LPR> of the result finishes exactly the reference's sum.  Weights in the planar Q8_0 layout: the half h of
 // block b is piece 32 (b / 16) + 16 h + b % 16, so logical lane L's i-th piece is 32 i + 16 (L & 1) + L / 2.  Read
 // straight from memory (the shared expert is one job of a launch; no register copy of the row is kept).
+// The same sums from registers: issue() loads a row's pieces for the lane's logical lanes (NI = C / 512 each), dot()
+// forms the lane's partial in q8s_dot's order.
+template <int LPR, int NI> struct Q8sRow {
+    static constexpr int NL = 32 / LPR;
+    uint4 w[NL][NI];
+    uint16_t dh[NL][NI];
+    __device__ __forceinline__ void issue(const Q80Planes& P, int row, int C, int ln) {
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+#pragma unroll
+            for (int k = 0; k < NL; ++k) {
+                const int L = ln + LPR * k;
+                w[k][i] = *reinterpret_cast<const uint4*>(P.q16(row, C, 32 * i + 16 * (L & 1) + L / 2));
+                dh[k][i] = *P.dof(row, C, 16 * i + L / 2);
+            }
+    }
+    __device__ __forceinline__ float dot(const Acts& a, int j, int ln) const {
+        const int nb = a.K / 32;
+        float acc[NL];
+#pragma unroll
+        for (int k = 0; k < NL; ++k) acc[k] = 0.f;
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+#pragma unroll
+            for (int k = 0; k < NL; ++k) {
+                const int L = ln + LPR * k, h = L & 1, b = 16 * i + L / 2;
+                const int4 av = a.q4(j, b)[h];
+                int s = dot4((int) w[k][i].x, av.x, 0);
+                s = dot4((int) w[k][i].y, av.y, s);
+                s = dot4((int) w[k][i].z, av.z, s);
+                s = dot4((int) w[k][i].w, av.w, s);
+                acc[k] = fmaf(h2f(dh[k][i]) * a.d[j * nb + b], (float) s, acc[k]);
+            }
+        if constexpr (NL == 4) return (acc[0] + acc[2]) + (acc[1] + acc[3]);
+        else if constexpr (NL == 2) return acc[0] + acc[1];
+        else return acc[0];
+    }
+};
+
 template <int LPR> __device__ __forceinline__ float q8s_dot(const Q80Planes& P, int row, int C, int ln, const Acts& a, int j) {
     static_assert(LPR == 8 || LPR == 16 || LPR == 32, "q8s lanes");
     constexpr int NL = 32 / LPR;
