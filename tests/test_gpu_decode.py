@@ -114,3 +114,34 @@ def test_mixed_gate_up_and_down_types(wtype, dn_type):
         oy, _, oi, _, ogu, _ = orc.layer_decode(host, x0.cpu().numpy(), nthreads=8)
         assert np.array_equal(b.topi.cpu().numpy(), oi)
         assert max_rel(yu.cpu().numpy(), oy) < 2e-3
+
+
+@pytest.mark.parametrize("H, E, K, ff, wtype, T", [
+    (2560, 1024, 16, 1024, orc.Q4_K, 1), (2560, 1024, 16, 1024, orc.Q4_K, 4), (4096, 128, 4, 512, orc.Q5_K, 1),
+    (4096, 128, 4, 512, orc.Q8_0, 16), (1024, 1024, 1, 1024, orc.Q4_0, 2), (2560, 256, 8, 512, orc.Q5_1, 16)])
+def test_fused_decode_edge_shapes(H, E, K, ff, wtype, T):
+    """the fused decode's limits: hidden 2560 and 4096, 1024 experts, top-16 and top-1, FF 1024, windows of 1 to 16
+    rows: equal to the unfused path bit for bit and to the oracle within 2e-3"""
+    shape = moe.LayerShape(H=H, E=E, K=K, ff=ff, wtype=wtype, shared=True)
+    L, host = make_layer(shape, 70 + H % 97 + K)
+    x0 = torch.from_numpy(orc.synth(T * H, 830 + T + K, 1.0).reshape(T, H)).cuda()
+    b = moe.DecodeBuffers(shape, T)
+    xu = x0.clone()
+    yu = unfused_chain([L], xu, False, [b])
+    f = moe.FusedDecode([L], T)
+    xf = x0.clone()
+    f(xf, norm=False)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(f.piece("y", torch.float32, (T, H))), bits(yu))
+    assert np.array_equal(bits(xf), bits(xu))
+    oy, _, oi, _, _, _ = orc.layer_decode(host, x0.cpu().numpy(), nthreads=8)
+    assert np.array_equal(b.topi.cpu().numpy(), oi)
+    assert max_rel(yu.cpu().numpy(), oy) < 2e-3
+
+
+def test_fused_decode_refuses_out_of_range():
+    shape = moe.LayerShape(H=1024, E=64, K=6, ff=512, wtype=orc.Q4_K, shared=True)
+    L, _ = make_layer(shape, 3)
+    f = moe.FusedDecode([L], 16)
+    with pytest.raises(RuntimeError, match="T out of range"):
+        f(torch.zeros((17, 1024), dtype=torch.float32, device="cuda"))
