@@ -43,15 +43,53 @@ constexpr size_t q8_1_bytes(int n) { return (size_t) (n / 32) * 36; }   // src/k
 
 inline void quantize_q8_1(const float* x, void* q, int n, int rows, void* st) { ck(sfnx_quantize_q8_1(x, q, n, rows, st)); }
 
+// src/model.hpp:72-76 Q8S: a dense Q8_0 matrix (here the planar Q8_0 layout of one matrix)
+struct Q8S {
+    const void* p = nullptr;
+};
+
+// src/kernels.hpp:47 (src/dense.cuh:24-154): the shared expert's dense Q8_0 product in the reference's q8s sums
+inline void q8s_gemv(const Q8S& w, int rows, int cols, const void* y, float* out, int out_stride, int T, void* st) {
+    ck(sfnx_q8s_gemv(w.p, rows, cols, y, out, out_stride, T, st));
+}
+// src/kernels.cu:2018-2024
+inline void swiglu_stacked_q8_1(const float* gu, void* hq, int ffs, int T, void* st) { ck(sfnx_swiglu_stacked_q8_1(gu, hq, ffs, T, st)); }
+
 // src/kernels.hpp:276-278; shared: the shared expert (expert E of the stacks) rides as the last job
 inline void router_route(const MoeShape& s, const float* W, const float* x, float* logits, int T, int* topi, float* topw,
                          Job* jobs_gu, Job* jobs_dn, int* njobs, void* st, bool shared = true) {
     ck(sfnx_router_route(W, x, logits, T, s.H, s.E, s.K, topi, topw, jobs_gu, jobs_dn, njobs, shared ? 1 : 0, st));
 }
+// src/kernels.hpp:276-278 with the dense shared expert's gate|up (sh_gu: sh_rows = 2 ffs rows over the q8_1 rows
+// sh_y into sh_out, row stride sh_rows).  The reference runs it in the router's launch; here it is sfnx_q8s_gemv after
+// the routing on the same stream: the same q8s sums, so the same values.  The shared expert is then no routed job.
+inline void router_route(const MoeShape& s, const float* W, const float* x, float* logits, int T, int* topi, float* topw,
+                         Job* jobs_gu, Job* jobs_dn, int* njobs, void* st, const Q8S* sh_gu, int sh_rows, const void* sh_y,
+                         float* sh_out) {
+    router_route(s, W, x, logits, T, topi, topw, jobs_gu, jobs_dn, njobs, st, /*shared=*/false);
+    if (sh_gu) q8s_gemv(*sh_gu, sh_rows, s.H, sh_y, sh_out, sh_rows, T, st);
+}
 // src/kernels.hpp:281-282; T: the window's rows (the reference derives it as njobs_max / TOPK)
 inline void moe_gate_up(const DW& A, size_t sa, const Job* jobs, const int* njobs, int njobs_max, const void* xq, float* gu,
                         void* st, int T) {
     ck(sfnx_moe_gate_up(A.p, sa, A.type, A.n_in, A.n_out, jobs, njobs, njobs_max, T, xq, gu, st));
+}
+// src/kernels.hpp:281-282 with the dense shared expert's SwiGLU and down (sh_down: N rows of sh_ffs; sh_gu [T][2 sh_ffs]
+// into sh_out, row stride N).  The reference runs them in the gate|up launch; here sfnx_swiglu_stacked_q8_1 and
+// sfnx_q8s_gemv follow on the same stream, with the same values.  sh_hq: the caller's [T][sh_ffs / 32] q8_1 rows for h
+// (the reference keeps h in shared memory; a library call that allocates nothing needs the buffer from its caller).
+inline void moe_gate_up(const DW& A, size_t sa, const Job* jobs, const int* njobs, int njobs_max, const void* xq, float* gu,
+                        void* st, int T, const Q8S* sh_down, int sh_ffs, const float* sh_gu, float* sh_out, void* sh_hq) {
+    moe_gate_up(A, sa, jobs, njobs, njobs_max, xq, gu, st, T);
+    if (sh_down) {
+        swiglu_stacked_q8_1(sh_gu, sh_hq, sh_ffs, T, st);
+        q8s_gemv(*sh_down, A.n_in, sh_ffs, sh_hq, sh_out, A.n_in, T, st);
+    }
+}
+// src/kernels.hpp:284: jobs of up to MAXT rows each, njobs_cap of them at most (the prompt path's)
+inline void moe_gate_up_jobs(const DW& A, size_t sa, const Job* jobs, const int* njobs, int njobs_cap, const void* xq,
+                             float* gu, void* st) {
+    moe_gate_up(A, sa, jobs, njobs, njobs_cap, xq, gu, st, MAXT);
 }
 // src/kernels.hpp:305
 inline void moe_down(const DW& A, size_t sa, const Job* jobs, const int* njobs, int njobs_max, const float* gu, float* part,
@@ -81,17 +119,19 @@ inline void moe_combine(const MoeShape& s, const float* part, const float* topw,
     ck(sfnx_moe_combine(part, topw, topi, logits, y, T, s.H, s.E, s.K, shared ? 1 : 0, st));
 }
 
-// src/model.hpp:72-76 Q8S: a dense Q8_0 matrix (here the planar Q8_0 layout of one matrix)
-struct Q8S {
-    const void* p = nullptr;
+// src/model.hpp:72-75 Q8S as the hc read takes it: int8 values [rows][cols] and f16 scale bits [rows][cols / 32]
+struct Q8Split {
+    const int8_t* q = nullptr;
+    const uint16_t* d = nullptr;
 };
-
-// src/kernels.hpp:47 (src/dense.cuh:24-154): the shared expert's dense Q8_0 product in the reference's q8s sums
-inline void q8s_gemv(const Q8S& w, int rows, int cols, const void* y, float* out, int out_stride, int T, void* st) {
-    ck(sfnx_q8s_gemv(w.p, rows, cols, y, out, out_stride, T, st));
+// src/kernels.cu:1054 hc_read: N, HC and LR are the reference's compile-time model constants (src/model.hpp:39);
+// scratch is sfnx_hc_workspace(N, HC, LR) bytes (no barrier counter and no err word: no kernel waits on another)
+inline void hc_read(float* R, const float* bo, const float* inj_prev, const float* w_norm, const Q8Split& w_down,
+                    const Q8Split& w_up, const uint16_t* w_inj, float eps, float* mixed, float* inject, void* scratch,
+                    size_t scratch_bytes, int T, void* st, void* q8, int N, int HC, int LR) {
+    ck(sfnx_hc_read(R, bo, inj_prev, w_norm, w_down.q, w_down.d, w_up.q, w_up.d, w_inj, eps, mixed, inject, q8, T, N, HC,
+                    LR, scratch, scratch_bytes, st));
 }
-// src/kernels.cu:2018-2024
-inline void swiglu_stacked_q8_1(const float* gu, void* hq, int ffs, int T, void* st) { ck(sfnx_swiglu_stacked_q8_1(gu, hq, ffs, T, st)); }
 
 static_assert(sizeof(Job) == 136 && sizeof(BigJob) == 520, "job layouts match the reference's");
 
