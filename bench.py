@@ -179,6 +179,7 @@ def main():
                      "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "algorithmic_bytes_per_launch": alg[dom]},
     }
+    out["decode_window16"] = bench_window16(layers, s, moe, torch, args.steps)
     if not args.no_prefill:
         out["prefill"] = bench_prefill(layers[0], s, moe, torch)
     if not args.no_cpu:
@@ -283,6 +284,36 @@ def time_us(torch, fn, reps):
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / reps * 1e3
+
+
+def bench_window16(layers, s, moe, torch, steps):
+    """a 16-row decode window (a speculative verify window's rows, the reference's MAXT) through the same stacked
+    layers on the fused decode, in a graph: µs per window-layer; the touched experts' bytes counted from the routing of
+    the last layer (each read once a window)"""
+    T = 16
+    x0 = torch.empty((T, s.H), dtype=torch.float32, device="cuda")
+    moe.synth_normal(x0, 4545, 1.0)
+    x = x0.clone()
+    f = moe.FusedDecode(layers, T)
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        f(x)
+    torch.cuda.current_stream().wait_stream(st)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        x.copy_(x0)
+        f(x)
+    ms = time_us(torch, g.replay, max(steps // 5, 5)) / 1e3
+    assert torch.isfinite(x).all()
+    touched = int(f.piece("njobs", torch.int32, (2,))[0])   # distinct experts of the last layer's window + shared
+    nbytes = (s.E + 1) * s.H * 4 + touched * expert_bytes(s, moe)
+    us_l = ms * 1000 / len(layers)
+    return {"workload": f"16-row decode window through {len(layers)} stacked Q4_K layers (fused decode, graph)",
+            "us_per_window_layer": round(us_l, 2), "us_per_token_layer": round(us_l / T, 3),
+            "experts_touched_last_layer": touched, "bytes_per_window_layer": nbytes,
+            "gbs": round(nbytes / (us_l * 1e-6) / 1e9, 1)}
 
 
 def bench_window(L, s, moe, torch, C=96, reps=20):

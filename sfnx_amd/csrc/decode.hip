@@ -191,28 +191,20 @@ template <int G> struct RowOf<SFNX_Q8_0, G> {
     }
 };
 
-template <int TYPE, int G, int TT>
-__global__ void __launch_bounds__(d2_threads<TYPE>()) k_dec_experts(
-    const uint8_t* __restrict__ A, size_t sa, int T, int H, int E, int K, int ff, int shared, const float* __restrict__ logits,
-    const uint8_t* __restrict__ xq, int* __restrict__ topi_g, float* __restrict__ topw_g, sfnx_job* __restrict__ jg,
-    sfnx_job* __restrict__ jd, int* __restrict__ njobs_g, float* __restrict__ gu, int8_t* __restrict__ hq_q,
-    float* __restrict__ hq_d, int* __restrict__ hq_s, const uint8_t* __restrict__ sh_gu) {
-    constexpr int LPR = lpr_of<TYPE>(), NTH = d2_threads<TYPE>(), NW = NTH / WAVE, RPW = WAVE / LPR;
-    const int NFB = ff / 32, myjob = blockIdx.x / NFB, fb = blockIdx.x % NFB;
+// K1b for windows of several rows: the routing once (the top-k of every row, a wavefront a row, then the decode job
+// numbering of src/moe.cuh:164-198), published for K2, K3 and the caller.  At batch 1, K2's blocks take the top-k
+// themselves (k_dec_experts1); with more rows each block would repeat every row's top-k and the numbering.
+constexpr int DR_THREADS = 512;   // a thread per pick (T K <= 512)
+__global__ void __launch_bounds__(DR_THREADS) k_dec_route(int T, int E, int K, int shared, const float* __restrict__ logits,
+                                                          int* __restrict__ topi_g, float* __restrict__ topw_g,
+                                                          sfnx_job* __restrict__ jg, sfnx_job* __restrict__ jd,
+                                                          int* __restrict__ njobs_g) {
+    constexpr int NW = DR_THREADS / WAVE;
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE, p = threadIdx.x, P = T * K;
     __shared__ int ex[MAX_P];
     __shared__ float sw[MAX_P];
     __shared__ unsigned char first[MAX_P];
     __shared__ int jobof[MAX_E];
-    __shared__ sfnx_job jb;
-    __shared__ float hbuf[SFNX_MAXT][32];
-    extern __shared__ __align__(16) unsigned char lds[];
-    PROF(1, 0)
-    PROFB(1, 0)
-    // every token's activations into LDS first: their loads overlap the top-k
-    const Acts a = acts_in(lds, TT, H);
-    stage_q8_1(a, xq, nullptr, T);
-    PROF(1, 7)
     for (int t = wave; t < T; t += NW) {
         int pick;
         float w;
@@ -221,88 +213,58 @@ __global__ void __launch_bounds__(d2_threads<TYPE>()) k_dec_experts(
             ex[t * K + lane] = pick;
             sw[t * K + lane] = w;
         }
-        PROF(1, 8)
     }
     __syncthreads();
     PickSlot ps;
-    __shared__ int s_nr;
-    if (P <= WAVE) {
-        // every pick in one wavefront: the numbering in registers (readlane loops), no LDS loops
-        if (wave == 0) {
-            ps.e = lane < P ? ex[lane] : -1;
-            int firstq = P;
-            for (int q = 0; q < P; ++q) {
-                const int eq = __builtin_amdgcn_readlane(ps.e, q);
-                const bool same = ps.e >= 0 && eq == ps.e;
-                ps.cnt += same;
-                ps.slot += same && q < lane;
-                firstq = same && q < firstq ? q : firstq;
-            }
-            const uint64_t fm = __ballot(ps.e >= 0 && ps.slot == 0);
-            ps.job = ps.e >= 0 ? __popcll(fm & ((1ull << firstq) - 1ull)) : -1;
-            if (lane == 0) s_nr = __popcll(fm);
-        }
-        __syncthreads();
-    } else {
-        const int n = pick_slots(ex, P, first, jobof, ps);
-        if (threadIdx.x == 0) s_nr = n;
-        __syncthreads();
-    }
-    const int nr = s_nr;
-    PROF(1, 1)
-    const int nj = nr + (shared ? 1 : 0);
-    if (blockIdx.x == 0) {   // the routing, published for K3 and the caller
-        if (p < P) {
-            topi_g[p] = ex[p];
-            topw_g[p] = sw[p];
-            if (ps.e >= 0) {
-                const int j = ps.job;
-                if (ps.slot == 0) {
-                    jg[j].w = jd[j].w = ps.e;
-                    jg[j].n = jd[j].n = ps.cnt;
-                }
-                jg[j].y[ps.slot] = p / K;
-                jg[j].out[ps.slot] = jd[j].y[ps.slot] = jd[j].out[ps.slot] = p;
-            }
-        }
-        if (shared) {
-            if (p == 0) {
-                jg[nr].w = jd[nr].w = E;
-                jg[nr].n = jd[nr].n = T;
-            }
-            if (p < T) {
-                jg[nr].y[p] = p;
-                jg[nr].out[p] = jd[nr].y[p] = jd[nr].out[p] = P + p;
-            }
-        }
-        if (p == 0) {
-            njobs_g[0] = nj;
-            njobs_g[1] = 0;
-        }
-    }
-    if (myjob >= nj) return;
-    PROF(1, 2)
-    if (myjob < nr) {
-        if (p < P && ps.job == myjob) {
+    const int nr = pick_slots(ex, P, first, jobof, ps);
+    if (p < P) {
+        topi_g[p] = ex[p];
+        topw_g[p] = sw[p];
+        if (ps.e >= 0) {
+            const int j = ps.job;
             if (ps.slot == 0) {
-                jb.w = ps.e;
-                jb.n = ps.cnt;
+                jg[j].w = jd[j].w = ps.e;
+                jg[j].n = jd[j].n = ps.cnt;
             }
-            jb.y[ps.slot] = p / K;
-            jb.out[ps.slot] = p;
+            jg[j].y[ps.slot] = p / K;
+            jg[j].out[ps.slot] = jd[j].y[ps.slot] = jd[j].out[ps.slot] = p;
         }
-    } else {
+    }
+    if (shared) {
         if (p == 0) {
-            jb.w = E;
-            jb.n = T;
+            jg[nr].w = jd[nr].w = E;
+            jg[nr].n = jd[nr].n = T;
         }
         if (p < T) {
-            jb.y[p] = p;
-            jb.out[p] = P + p;
+            jg[nr].y[p] = p;
+            jg[nr].out[p] = jd[nr].y[p] = jd[nr].out[p] = P + p;
         }
     }
+    if (p == 0) {
+        njobs_g[0] = nr + (shared ? 1 : 0);
+        njobs_g[1] = 0;
+    }
+}
+
+// K2 for windows of several rows: a block is one (job, 32 FF indices) unit of the jobs K1b numbered: the job's
+// activation rows staged, 32 gate and 32 up rows dotted with each of them, SwiGLU, h as q8_1.
+template <int TYPE, int G, int TT>
+__global__ void __launch_bounds__(d2_threads<TYPE>()) k_dec_experts(
+    const uint8_t* __restrict__ A, size_t sa, int H, int E, int ff, const uint8_t* __restrict__ xq,
+    const sfnx_job* __restrict__ jg, const int* __restrict__ njobs_g, float* __restrict__ gu, int8_t* __restrict__ hq_q,
+    float* __restrict__ hq_d, int* __restrict__ hq_s, const uint8_t* __restrict__ sh_gu) {
+    constexpr int LPR = lpr_of<TYPE>(), NTH = d2_threads<TYPE>(), NW = NTH / WAVE, RPW = WAVE / LPR;
+    const int NFB = ff / 32, myjob = blockIdx.x / NFB, fb = blockIdx.x % NFB;
+    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    __shared__ sfnx_job jb;
+    __shared__ float hbuf[SFNX_MAXT][32];
+    extern __shared__ __align__(16) unsigned char lds[];
+    if (myjob >= njobs_g[0]) return;
+    load_job(jb, jg + myjob);
     __syncthreads();
-    PROF(1, 3)
+    // the job's rows of activations (slot s holds row jb.y[s])
+    const Acts a = acts_in(lds, TT, H);
+    stage_q8_1(a, xq, jb.y, jb.n);
     const int rw = lane / LPR, ln = lane % LPR, f = fb * 32 + wave * RPW + rw;
     auto put = [&](int s, float gv, float uv) {
         if (ln == 0) {
@@ -312,24 +274,20 @@ __global__ void __launch_bounds__(d2_threads<TYPE>()) k_dec_experts(
             hbuf[s][wave * RPW + rw] = silu_f(gv) * uv;
         }
     };
-    if (sh_gu != nullptr && myjob >= nr) {   // the shared expert's own dense Q8_0 matrix, the reference's q8s sums
+    if (sh_gu != nullptr && jb.w == E) {   // the shared expert's own dense Q8_0 matrix, the reference's q8s sums
         const Q80Planes Ps = q80_planes(sh_gu, 2 * ff, H);
-        for (int s = 0; s < jb.n; ++s) {
-            const int t = jb.y[s];
-            put(s, group_sum<LPR>(q8s_dot<LPR>(Ps, f, H, ln, a, t)), group_sum<LPR>(q8s_dot<LPR>(Ps, ff + f, H, ln, a, t)));
-        }
+        __syncthreads();
+        for (int s = 0; s < jb.n; ++s)
+            put(s, group_sum<LPR>(q8s_dot<LPR>(Ps, f, H, ln, a, s)), group_sum<LPR>(q8s_dot<LPR>(Ps, ff + f, H, ln, a, s)));
     } else {
         const uint8_t* mat = A + (size_t) jb.w * sa;
         typename RowOf<TYPE, G>::R wg, wu;
         RowOf<TYPE, G>::load(wg, mat, 2 * ff, f, H, ln);
         RowOf<TYPE, G>::load(wu, mat, 2 * ff, ff + f, H, ln);
-        for (int s = 0; s < jb.n; ++s) {
-            const int t = jb.y[s];
-            put(s, group_sum<LPR>(wg.dot(a, t, ln)), group_sum<LPR>(wu.dot(a, t, ln)));
-        }
+        __syncthreads();   // the staged activations
+        for (int s = 0; s < jb.n; ++s) put(s, group_sum<LPR>(wg.dot(a, s, ln)), group_sum<LPR>(wu.dot(a, s, ln)));
     }
     __syncthreads();
-    PROF(1, 5)
     for (int s = threadIdx.x / 32; s < jb.n; s += NTH / 32) {
         const int l = threadIdx.x % 32, o = jb.out[s];
         const float v = hbuf[s][l];
@@ -343,8 +301,6 @@ __global__ void __launch_bounds__(d2_threads<TYPE>()) k_dec_experts(
             hq_s[(size_t) o * NFB + fb] = qs;
         }
     }
-    PROF(1, 6)
-    PROFB(1, 1)
 }
 
 // K1's workgroup b' owns the router rows [D1_WAVES b', D1_WAVES b' + D1_WAVES), on XCD b' % 8.  Workgroup b of a launch
@@ -745,11 +701,14 @@ void launch_k2(const DecArgs& d, const sfnx_moe_layer_w& w, const DecLayout& L, 
         launch_k2_tt1<TYPE, G>(d, w, L, ws, s);
     } else {
         const int njmax = d.T * d.K + (d.shared ? 1 : 0);
+        // the routing once (K1b), then the experts
+        hipLaunchKernelGGL(k_dec_route, dim3(1), dim3(DR_THREADS), 0, s, d.T, d.E, d.K, d.shared,
+            (const float*) (ws + L.logits), (int*) (ws + L.topi), (float*) (ws + L.topw), (sfnx_job*) (ws + L.jg),
+            (sfnx_job*) (ws + L.jd), (int*) (ws + L.njobs));
         launch(1, k_dec_experts<TYPE, G, TT>, dim3(njmax * (d.ff / 32)), dim3(d2_threads<TYPE>()), acts_bytes(TT, d.H), s,
-            (const uint8_t*) w.gu, w.gu_stride, d.T, d.H, d.E, d.K, d.ff, d.shared, (const float*) (ws + L.logits),
-            (const uint8_t*) (ws + L.xq), (int*) (ws + L.topi), (float*) (ws + L.topw), (sfnx_job*) (ws + L.jg),
-            (sfnx_job*) (ws + L.jd), (int*) (ws + L.njobs), (float*) (ws + L.gu), (int8_t*) (ws + L.hq_q),
-            (float*) (ws + L.hq_d), (int*) (ws + L.hq_s), d.sh_gu);
+            (const uint8_t*) w.gu, w.gu_stride, d.H, d.E, d.ff, (const uint8_t*) (ws + L.xq), (const sfnx_job*) (ws + L.jg),
+            (const int*) (ws + L.njobs), (float*) (ws + L.gu), (int8_t*) (ws + L.hq_q), (float*) (ws + L.hq_d),
+            (int*) (ws + L.hq_s), d.sh_gu);
     }
 }
 template <int TYPE, int G, int NV, bool SHQ>
