@@ -750,7 +750,12 @@ void launch_k3(const DecArgs& d, const sfnx_moe_layer_w& w, float* x, const DecL
     }
     const int NP = d.T * d.K + d.T;
     const size_t hq_lds = acts_bytes(NP, d.ff);
-    const bool staged = hq_lds <= 32 * 1024;
+    // every pair's h in LDS when it fits beside the kernel's own ~30 KB (160 KB a workgroup on gfx950; past 64 KB the
+    // kernel must be allowed the larger dynamic size first), else read from L2 per task
+    constexpr size_t HQ_LDS_MAX = 120 * 1024;
+    static bool big_lds = hipFuncSetAttribute((const void*) k_dec_down<TYPE, G2, NB>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                              (int) HQ_LDS_MAX) == hipSuccess;
+    const bool staged = hq_lds <= (big_lds ? HQ_LDS_MAX : 32 * 1024);
     launch(2, k_dec_down<TYPE, G2, NB>, dim3(d.H / D3_ROWS), dim3(D3_THREADS), staged ? hq_lds : 0, s,
         (const uint8_t*) w.dn, w.dn_stride, d.T, d.H, d.E, d.K, d.ff, d.shared, (const float*) (ws + L.logits),
         (const int*) (ws + L.topi), (const float*) (ws + L.topw), (const sfnx_job*) (ws + L.jd), (const int*) (ws + L.njobs),
