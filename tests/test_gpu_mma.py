@@ -155,3 +155,37 @@ def test_mma_mixed_gate_up_and_down_types(wtype, dn_type):
     L, host, x, y, b = run_prefill(shape, 77, 200, dup=True)
     eg, ed = check_sampled(host, x, b, 30, np.random.default_rng(4))
     assert eg < 2e-3 and ed < 2e-3, (eg, ed)
+
+
+@pytest.mark.parametrize("C", [1, 17, 1000])
+def test_mma_extreme_skew_and_tiny_chunks(C):
+    """every token routed to the same 6 experts (a bias of +100 on their logits): each takes C rows, up to 16 BigJobs
+    of one expert in a row; and chunks of 1 and 17 tokens.  Routing against the oracle's on the biased logits, sampled
+    pairs within 2e-3 of float64, the combine of the kernel's own rows"""
+    shape = moe.LayerShape(H=1024, E=64, K=6, ff=512, wtype=orc.Q4_K, shared=True)
+    L, host = make_layer(shape, 123)
+    x = orc.synth(C * shape.H, 124 + C, 1.0).reshape(C, shape.H)
+    xd = torch.from_numpy(x).cuda()
+    bias = np.zeros(shape.E, np.float32)
+    bias[[3, 9, 17, 33, 40, 63]] = 100.0
+    y = torch.empty_like(xd)
+    b = moe.PrefillBuffers(shape, C)
+    moe.prefill_route(L, xd, b, torch.from_numpy(bias).cuda())
+    moe.prefill_experts_mma(L, xd, y, b)
+    torch.cuda.synchronize()
+    lg = orc.router_logits(host.W, x)
+    lg[:, : shape.E] += bias
+    oi, ow, _ = orc.topk(lg, shape.E, shape.K)
+    assert np.array_equal(b.topi.cpu().numpy(), oi)
+    assert sorted(set(oi.reshape(-1).tolist())) == [3, 9, 17, 33, 40, 63]
+    cnt = b.cnt.cpu().numpy()
+    assert cnt[[3, 9, 17, 33, 40, 63]].tolist() == [C] * 6 and cnt.sum() == 6 * C
+    jobs = job_array(b.jobs_gu, True)[: int(b.njobs[0])]
+    assert len(jobs) == 6 * ((C + 63) // 64) + (C + 63) // 64
+    eg, ed = check_sampled(host, x, b, min(40, 7 * C), np.random.default_rng(C))
+    assert eg < 2e-3 and ed < 2e-3, (eg, ed)
+    topw = b.topw.cpu().numpy().astype(np.float64)
+    part = b.part.cpu().numpy().astype(np.float64)
+    sig = 1 / (1 + np.exp(-b.logits.cpu().numpy()[:, shape.E].astype(np.float64)))
+    want = np.einsum("tk,tkh->th", topw, part[: C * shape.K].reshape(C, shape.K, -1)) + sig[:, None] * part[C * shape.K:]
+    assert max_rel(y.cpu().numpy(), want) < 1e-5
