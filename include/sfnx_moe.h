@@ -144,6 +144,14 @@ int sfnx_q8s_gemv(const void* W, int rows, int cols, const void* y, float* out, 
  * quantized per 32 values (d = amax / 127, q = round(v / d), ds = (f16 d, f16 sum)); gu is [T][2 ffs], ffs % 32 == 0 */
 int sfnx_swiglu_stacked_q8_1(const float* gu, void* hq, int ffs, int T, void* st);
 
+/* src/prefill.cu:407-417 pf_dense_xh (the prompt path's dense matrices, the shared expert's among them): out[c][r]
+ * (row stride ldo) = sum_k f16(W[r][k]) xh[c][k] for C f16 rows xh [C][cols], fp32 accumulation.  W is a dense Q8_0
+ * matrix (planar, one matrix), dequantized to f16 into wh (rows * cols * 2 bytes, the caller's) and multiplied in one
+ * rocBLAS gemm_ex, as the reference dequantizes (k_q8s_f16) and calls cublasGemmEx.  The first call on a device
+ * creates that device's rocBLAS handle (the call's only allocation). */
+int sfnx_pf_dense(const void* W, int rows, int cols, const uint16_t* xh, int C, float* out, int ldo, void* wh,
+                  size_t wh_bytes, void* st);
+
 /* ---------------------------------------------------------------------------------------------- fused decode */
 /* one layer's weights: router W [E + 1][H] fp32 (row E gates the shared expert), planar gate|up experts (E + 1 of
  * [2 ff][H], the shared expert last) and planar down experts (E + 1 of [H][ff]) */

@@ -53,6 +53,7 @@ SIGNATURES = {
     "sfnx_moe_decode_q8s": (i32, [vp, vp, i32, u32, u32, i32, i32, i32, i32, vp, i32, i32, f32, vp, sz, i32, vp]),
     "sfnx_q8s_gemv": (i32, [vp, i32, i32, vp, vp, i32, i32, vp]),
     "sfnx_hc_workspace": (sz, [i32, i32, i32, vp]),
+    "sfnx_pf_dense": (i32, [vp, i32, i32, vp, i32, vp, i32, vp, sz, vp]),
     "sfnx_hc_read": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, f32, vp, vp, vp, i32, i32, i32, i32, vp, sz, vp]),
     "sfnx_swiglu_stacked_q8_1": (i32, [vp, vp, i32, i32, vp]),
     "sfnx_gguf_type_info": (i32, [u32, vp, vp]),

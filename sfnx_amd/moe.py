@@ -357,20 +357,8 @@ class PrefillBuffers:
         self.part = torch.zeros((NP, s.H), dtype=torch.float32, device=device)
         self.xh = torch.zeros((C, s.H), dtype=torch.float16, device=device)
         self.h16 = torch.zeros((NP, s.ff), dtype=torch.float16, device=device)
-        if s.sh_q8s:   # the shared expert's own jobs (rows P + t), the layout k_pf_fill gives them (src/prefill.cu)
-            nsj = (C + PF_JOB - 1) // PF_JOB
-            gu = torch.zeros((nsj, BIGJOB_INTS), dtype=torch.int32)
-            for j in range(nsj):
-                n = min(PF_JOB, C - PF_JOB * j)
-                t = torch.arange(PF_JOB * j, PF_JOB * j + n, dtype=torch.int32)
-                gu[j, 0], gu[j, 1] = 0, n
-                gu[j, 2:2 + n] = t
-                gu[j, 2 + PF_JOB:2 + PF_JOB + n] = P + t
-            dn = gu.clone()
-            dn[:, 2:2 + PF_JOB] = dn[:, 2 + PF_JOB:]
-            self.sh_jobs_gu, self.sh_jobs_dn = gu.reshape(-1).to(device), dn.reshape(-1).to(device)
-            self.sh_njobs = torch.tensor([nsj, nsj], **i32)
-            self.sh_cap = nsj
+        if s.sh_q8s:   # f16 staging for the dense shared matrices (the reference's p.wh)
+            self.wh = torch.empty(2 * s.ff * s.H, dtype=torch.float16, device=device)
 
 
 def prefill_route(L: "MoeLayer", x: torch.Tensor, b: "PrefillBuffers", bias: torch.Tensor | None = None) -> None:
@@ -383,12 +371,21 @@ def prefill_route(L: "MoeLayer", x: torch.Tensor, b: "PrefillBuffers", bias: tor
     pf_route(b.logits, b.topi, b.topw, b.cnt, b.jbase, b.jobs_gu, b.jobs_dn, b.njobs, s.E, s.K, s.shared and not s.sh_q8s)
 
 
-def prefill_shared_mma(L: "MoeLayer", b: "PrefillBuffers") -> None:
-    """a q8s layer's shared expert for the chunk on the matrix cores, f16 products of its dequantized Q8_0 rows as the
-    reference's pf_dense_xh + k_pf_swiglu + pf_gemm (src/prefill.cu:1173-1177); needs b.xh"""
+def pf_dense(W, rows: int, cols: int, xh, out, ldo: int, wh) -> None:
+    """src/prefill.cu:407-417 pf_dense_xh: out rows (stride ldo) = f16(W) . xh rows, fp32 (rocBLAS gemm_ex)"""
+    check(lib().sfnx_pf_dense(_p(W), rows, cols, _p(xh), xh.shape[0], _p(out), ldo, _p(wh), wh.numel() * wh.element_size(), _st()))
+
+
+def prefill_shared(L: "MoeLayer", b: "PrefillBuffers") -> None:
+    """a q8s layer's shared expert for the chunk as the reference runs it (src/prefill.cu:1173-1177): its gate|up as one
+    f16 GEMM of the dequantized Q8_0 rows (pf_dense_xh), SwiGLU to f16, its down likewise into part rows P + t; needs
+    b.xh"""
     s = L.s
-    moe_gate_up_swiglu_mma(L.sh_gu, L.sh_gu.numel(), Q8_0, s.H, s.ff, b.sh_jobs_gu, b.sh_njobs, b.sh_cap, b.xh, b.h16)
-    moe_down_mma(L.sh_dn, L.sh_dn.numel(), Q8_0, s.ff, s.H, b.sh_jobs_dn, b.sh_njobs, b.sh_cap, b.h16, b.part)
+    C = b.C
+    P = C * s.K
+    pf_dense(L.sh_gu, 2 * s.ff, s.H, b.xh, b.gu[P:P + C], 2 * s.ff, b.wh)
+    check(lib().sfnx_swiglu_h16(_p(b.gu[P:P + C]), s.ff, C, _p(b.h16[P:P + C]), _st()))
+    pf_dense(L.sh_dn, s.H, s.ff, b.h16[P:P + C], b.part[P:P + C], s.H, b.wh)
 
 
 def prefill_experts_mma(L: "MoeLayer", x: torch.Tensor, y: torch.Tensor, b: "PrefillBuffers") -> None:
@@ -400,7 +397,7 @@ def prefill_experts_mma(L: "MoeLayer", x: torch.Tensor, y: torch.Tensor, b: "Pre
     swiglu_h16(b.gu, b.h16, s.ff)
     moe_down_mma(L.dn_w, L.dn_stride, s.dn_type, s.ff, s.H, b.jobs_dn, b.njobs, b.cap, b.h16, b.part)
     if s.sh_q8s:
-        prefill_shared_mma(L, b)
+        prefill_shared(L, b)
     moe_combine(b.part, b.topw, b.topi, b.logits, y, s.E, s.K, s.shared)
 
 
@@ -414,7 +411,7 @@ def prefill_layer_mma(L: "MoeLayer", x: torch.Tensor, y: torch.Tensor, b: "Prefi
     moe_gate_up_swiglu_mma(L.gu_w, L.gu_stride, s.wtype, s.H, s.ff, b.jobs_gu, b.njobs, b.cap, b.xh, b.h16)
     moe_down_mma(L.dn_w, L.dn_stride, s.dn_type, s.ff, s.H, b.jobs_dn, b.njobs, b.cap, b.h16, b.part)
     if s.sh_q8s:
-        prefill_shared_mma(L, b)
+        prefill_shared(L, b)
     moe_combine(b.part, b.topw, b.topi, b.logits, y, s.E, s.K, s.shared)
 
 
@@ -428,7 +425,7 @@ def prefill_layer_q8(L: MoeLayer, x: torch.Tensor, y: torch.Tensor, b: PrefillBu
     moe_down_big(L.dn_w, L.dn_stride, s.dn_type, s.ff, s.H, b.jobs_dn, b.njobs, b.cap, b.gu, b.part)
     if s.sh_q8s:   # the reference's shared expert is the f16 dense path on this path too (src/prefill.cu:1173-1177)
         to_f16(x, b.xh)
-        prefill_shared_mma(L, b)
+        prefill_shared(L, b)
     moe_combine(b.part, b.topw, b.topi, b.logits, y, s.E, s.K, s.shared)
 
 

@@ -212,3 +212,23 @@ def test_synthetic_q8s_layer():
     oy = orc.layer_decode(host, x)[0]
     yf = f.piece("y", torch.float32, (1, s.H)).cpu().numpy()
     assert np.isfinite(yf).all() and max_rel(yf, oy) < TOL
+
+
+@pytest.mark.parametrize("rows,cols,C", [(1024, 2048, 200), (2048, 512, 33)])
+def test_pf_dense_against_float64(rows, cols, C):
+    """sfnx_pf_dense (src/prefill.cu:407-417): f16(W) . xh rows in fp32, against float64 products of the same f16
+    operands within 2e-3 (the GEMM's own order is rocBLAS's, as the reference's is cuBLAS's); rows of out ldo apart"""
+    g, W = q8_0_matrix(rows, cols, 300 + cols)
+    x = orc.synth(C * cols, 301, 1.0).reshape(C, cols).astype(np.float16)
+    ldo = rows + 64
+    out = torch.full((C, ldo), 5.0, dtype=torch.float32, device="cuda")
+    wh = torch.empty(rows * cols, dtype=torch.float16, device="cuda")
+    moe.pf_dense(W, rows, cols, torch.from_numpy(x).cuda(), out, ldo, wh)
+    torch.cuda.synchronize()
+    w16 = orc.dequant(orc.Q8_0, g.reshape(-1), rows, cols).astype(np.float16).astype(np.float64)
+    want = x.astype(np.float64) @ w16.T
+    got = out.cpu().numpy()
+    assert max_rel(got[:, :rows], want) < 2e-3
+    assert (got[:, rows:] == 5.0).all()
+    # the staging holds the f16 dequantization, bit for bit the oracle's f16 form
+    assert np.array_equal(wh.cpu().numpy().view(np.uint16), orc.dequant_f16(orc.Q8_0, g.reshape(-1), rows, cols).reshape(-1))
