@@ -246,18 +246,19 @@ __global__ void __launch_bounds__(DR_THREADS) k_dec_route(int T, int E, int K, i
     }
 }
 
-// K2 for windows of several rows: a block is one (job, 32 FF indices) unit of the jobs K1b numbered: the job's
-// activation rows staged, 32 gate and 32 up rows dotted with each of them, SwiGLU, h as q8_1.
+// K2 for windows of several rows: a block is one (job, 32 FF indices) unit of the jobs K1b numbered, as at batch 1:
+// the first half of the waves take the 32 gate rows, the second half the matching up rows (a row a lane group, so a
+// lane holds one row's share), each dotted with the job's staged activation rows; SwiGLU and h as q8_1 per slot.
 template <int TYPE, int G, int TT>
-__global__ void __launch_bounds__(d2_threads<TYPE>()) k_dec_experts(
+__global__ void __launch_bounds__(2 * d2_threads<TYPE>()) k_dec_experts(
     const uint8_t* __restrict__ A, size_t sa, int H, int E, int ff, const uint8_t* __restrict__ xq,
     const sfnx_job* __restrict__ jg, const int* __restrict__ njobs_g, float* __restrict__ gu, int8_t* __restrict__ hq_q,
     float* __restrict__ hq_d, int* __restrict__ hq_s, const uint8_t* __restrict__ sh_gu) {
-    constexpr int LPR = lpr_of<TYPE>(), NTH = d2_threads<TYPE>(), NW = NTH / WAVE, RPW = WAVE / LPR;
+    constexpr int LPR = lpr_of<TYPE>(), NTH = 2 * d2_threads<TYPE>(), NW = NTH / WAVE, RPW = WAVE / LPR;
     const int NFB = ff / 32, myjob = blockIdx.x / NFB, fb = blockIdx.x % NFB;
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
     __shared__ sfnx_job jb;
-    __shared__ float hbuf[SFNX_MAXT][32];
+    __shared__ float gbuf[SFNX_MAXT][32], ubuf[SFNX_MAXT][32];
     extern __shared__ __align__(16) unsigned char lds[];
     if (myjob >= njobs_g[0]) return;
     load_job(jb, jg + myjob);
@@ -265,32 +266,28 @@ __global__ void __launch_bounds__(d2_threads<TYPE>()) k_dec_experts(
     // the job's rows of activations (slot s holds row jb.y[s])
     const Acts a = acts_in(lds, TT, H);
     stage_q8_1(a, xq, jb.y, jb.n);
-    const int rw = lane / LPR, ln = lane % LPR, f = fb * 32 + wave * RPW + rw;
-    auto put = [&](int s, float gv, float uv) {
+    const bool up = wave >= NW / 2;
+    const int rw = lane / LPR, ln = lane % LPR, fl = (up ? wave - NW / 2 : wave) * RPW + rw, row = (up ? ff : 0) + fb * 32 + fl;
+    auto put = [&](int s, float v) {
         if (ln == 0) {
-            const int o = jb.out[s];
-            gu[(size_t) o * 2 * ff + f] = gv;
-            gu[(size_t) o * 2 * ff + ff + f] = uv;
-            hbuf[s][wave * RPW + rw] = silu_f(gv) * uv;
+            gu[(size_t) jb.out[s] * 2 * ff + row] = v;
+            (up ? ubuf : gbuf)[s][fl] = v;
         }
     };
     if (sh_gu != nullptr && jb.w == E) {   // the shared expert's own dense Q8_0 matrix, the reference's q8s sums
         const Q80Planes Ps = q80_planes(sh_gu, 2 * ff, H);
         __syncthreads();
-        for (int s = 0; s < jb.n; ++s)
-            put(s, group_sum<LPR>(q8s_dot<LPR>(Ps, f, H, ln, a, s)), group_sum<LPR>(q8s_dot<LPR>(Ps, ff + f, H, ln, a, s)));
+        for (int s = 0; s < jb.n; ++s) put(s, group_sum<LPR>(q8s_dot<LPR>(Ps, row, H, ln, a, s)));
     } else {
-        const uint8_t* mat = A + (size_t) jb.w * sa;
-        typename RowOf<TYPE, G>::R wg, wu;
-        RowOf<TYPE, G>::load(wg, mat, 2 * ff, f, H, ln);
-        RowOf<TYPE, G>::load(wu, mat, 2 * ff, ff + f, H, ln);
+        typename RowOf<TYPE, G>::R w;
+        RowOf<TYPE, G>::load(w, A + (size_t) jb.w * sa, 2 * ff, row, H, ln);
         __syncthreads();   // the staged activations
-        for (int s = 0; s < jb.n; ++s) put(s, group_sum<LPR>(wg.dot(a, s, ln)), group_sum<LPR>(wu.dot(a, s, ln)));
+        for (int s = 0; s < jb.n; ++s) put(s, group_sum<LPR>(w.dot(a, s, ln)));
     }
     __syncthreads();
     for (int s = threadIdx.x / 32; s < jb.n; s += NTH / 32) {
         const int l = threadIdx.x % 32, o = jb.out[s];
-        const float v = hbuf[s][l];
+        const float v = silu_f(gbuf[s][l]) * ubuf[s][l];
         const float amax = group_max<32>(fabsf(v));
         const float d = amax / 127.0f;
         const int q = amax == 0.0f ? 0 : (int) roundf(v / d);
@@ -705,7 +702,7 @@ void launch_k2(const DecArgs& d, const sfnx_moe_layer_w& w, const DecLayout& L, 
         hipLaunchKernelGGL(k_dec_route, dim3(1), dim3(DR_THREADS), 0, s, d.T, d.E, d.K, d.shared,
             (const float*) (ws + L.logits), (int*) (ws + L.topi), (float*) (ws + L.topw), (sfnx_job*) (ws + L.jg),
             (sfnx_job*) (ws + L.jd), (int*) (ws + L.njobs));
-        launch(1, k_dec_experts<TYPE, G, TT>, dim3(njmax * (d.ff / 32)), dim3(d2_threads<TYPE>()), acts_bytes(TT, d.H), s,
+        launch(1, k_dec_experts<TYPE, G, TT>, dim3(njmax * (d.ff / 32)), dim3(2 * d2_threads<TYPE>()), acts_bytes(TT, d.H), s,
             (const uint8_t*) w.gu, w.gu_stride, d.H, d.E, d.ff, (const uint8_t*) (ws + L.xq), (const sfnx_job*) (ws + L.jg),
             (const int*) (ws + L.njobs), (float*) (ws + L.gu), (int8_t*) (ws + L.hq_q), (float*) (ws + L.hq_d),
             (int*) (ws + L.hq_s), d.sh_gu);
