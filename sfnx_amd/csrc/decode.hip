@@ -38,6 +38,7 @@ __device__ unsigned long long g_blk[3][1024][2];   // every block's first and la
 
 constexpr int D1_THREADS = 128, D1_WAVES = D1_THREADS / WAVE;   // K1: a router row per wavefront
 constexpr int D3_THREADS = 256, D3_ROWS = 8;                    // K3: output rows per block
+constexpr int D3W_THREADS = 512;                                 // K3 for windows of several rows
 template <int TYPE> constexpr int lpr_of() { return is_kquant(TYPE) ? 8 : 16; }
 template <int TYPE> constexpr int d2_threads() { return 32 * lpr_of<TYPE>(); }   // K2: 32 FF indices a block
 
@@ -432,15 +433,16 @@ __global__ void __launch_bounds__(2 * d2_threads<TYPE>()) k_dec_experts1(
 }
 
 // ------------------------------------------------------------------------------------------------ K3
+// (windows: 512 threads, twice the lane groups of the batch-1 kernel, so a group takes half the tasks)
 template <int TYPE, int G2, int NB>
-__global__ void __launch_bounds__(D3_THREADS) k_dec_down(const uint8_t* __restrict__ A, size_t sa, int T, int H, int E, int K,
+__global__ void __launch_bounds__(D3W_THREADS) k_dec_down(const uint8_t* __restrict__ A, size_t sa, int T, int H, int E, int K,
                                                         int ff, int shared, const float* __restrict__ logits,
                                                         const int* __restrict__ topi, const float* __restrict__ topw,
                                                         const sfnx_job* __restrict__ jd, const int* __restrict__ njobs,
                                                         const int8_t* __restrict__ hq_q, const float* __restrict__ hq_d,
                                                         const int* __restrict__ hq_s, float* __restrict__ y,
                                                         float* __restrict__ x, int hq_in_lds, const uint8_t* __restrict__ sh_dn) {
-    constexpr int LPR = lpr_of<TYPE>(), GROUPS = D3_THREADS / LPR;
+    constexpr int LPR = lpr_of<TYPE>(), GROUPS = D3W_THREADS / LPR;
     const int row0 = blockIdx.x * D3_ROWS, nj = njobs[0], P = T * K, NP = P + T, nbh = ff / 32;
     PROF(2, 0)
     PROFB(2, 0)
@@ -449,26 +451,26 @@ __global__ void __launch_bounds__(D3_THREADS) k_dec_down(const uint8_t* __restri
     __shared__ int ti[MAX_P];
     __shared__ float tw[MAX_P], sg[SFNX_MAXT];
     extern __shared__ __align__(16) unsigned char lds[];   // every pair's h, when the launch gave room for it
-    for (int i = threadIdx.x; i < nj; i += D3_THREADS) {
+    for (int i = threadIdx.x; i < nj; i += D3W_THREADS) {
         jw[i] = jd[i].w;
         jn[i] = jd[i].n;
         for (int s = 0; s < jd[i].n; ++s) jout[i][s] = jd[i].out[s];
     }
-    for (int i = threadIdx.x; i < P; i += D3_THREADS) {
+    for (int i = threadIdx.x; i < P; i += D3W_THREADS) {
         ti[i] = topi[i];
         tw[i] = topw[i];
     }
     __shared__ float xr[SFNX_MAXT][D3_ROWS];   // the residual rows this block adds to, read with everything else
-    for (int i = threadIdx.x; i < T * D3_ROWS; i += D3_THREADS) xr[i / D3_ROWS][i % D3_ROWS] = x[(size_t) (i / D3_ROWS) * H + row0 + i % D3_ROWS];
+    for (int i = threadIdx.x; i < T * D3_ROWS; i += D3W_THREADS) xr[i / D3_ROWS][i % D3_ROWS] = x[(size_t) (i / D3_ROWS) * H + row0 + i % D3_ROWS];
     if (shared)
-        for (int t = threadIdx.x; t < T; t += D3_THREADS) sg[t] = sigm_f(logits[(size_t) t * (E + 1) + E]);
+        for (int t = threadIdx.x; t < T; t += D3W_THREADS) sg[t] = sigm_f(logits[(size_t) t * (E + 1) + E]);
     Acts a;
     const bool staged = hq_in_lds != 0;
     if (staged) {
         a = acts_in(lds, NP, ff);
         const int4* src = reinterpret_cast<const int4*>(hq_q);
-        for (int i = threadIdx.x; i < NP * ff / 16; i += D3_THREADS) reinterpret_cast<int4*>(a.q)[i] = src[i];
-        for (int i = threadIdx.x; i < NP * nbh; i += D3_THREADS) {
+        for (int i = threadIdx.x; i < NP * ff / 16; i += D3W_THREADS) reinterpret_cast<int4*>(a.q)[i] = src[i];
+        for (int i = threadIdx.x; i < NP * nbh; i += D3W_THREADS) {
             a.d[i] = hq_d[i];
             a.s[i] = hq_s[i];
         }
@@ -516,7 +518,7 @@ __global__ void __launch_bounds__(D3_THREADS) k_dec_down(const uint8_t* __restri
     }
     __syncthreads();
     PROF(2, 2)
-    for (int i = threadIdx.x; i < T * D3_ROWS; i += D3_THREADS) {
+    for (int i = threadIdx.x; i < T * D3_ROWS; i += D3W_THREADS) {
         const int t = i / D3_ROWS, r = i % D3_ROWS, row = row0 + r;
         float pw[MAX_K], pv[MAX_K];
 #pragma unroll
@@ -753,7 +755,7 @@ void launch_k3(const DecArgs& d, const sfnx_moe_layer_w& w, float* x, const DecL
     static bool big_lds = hipFuncSetAttribute((const void*) k_dec_down<TYPE, G2, NB>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                               (int) HQ_LDS_MAX) == hipSuccess;
     const bool staged = hq_lds <= (big_lds ? HQ_LDS_MAX : 32 * 1024);
-    launch(2, k_dec_down<TYPE, G2, NB>, dim3(d.H / D3_ROWS), dim3(D3_THREADS), staged ? hq_lds : 0, s,
+    launch(2, k_dec_down<TYPE, G2, NB>, dim3(d.H / D3_ROWS), dim3(D3W_THREADS), staged ? hq_lds : 0, s,
         (const uint8_t*) w.dn, w.dn_stride, d.T, d.H, d.E, d.K, d.ff, d.shared, (const float*) (ws + L.logits),
         (const int*) (ws + L.topi), (const float*) (ws + L.topw), (const sfnx_job*) (ws + L.jd), (const int*) (ws + L.njobs),
         (const int8_t*) (ws + L.hq_q), (const float*) (ws + L.hq_d), (const int*) (ws + L.hq_s), (float*) (ws + L.y), x,
