@@ -542,15 +542,17 @@ __global__ void __launch_bounds__(D3W_THREADS) k_dec_down(const uint8_t* __restr
 // K3 for a window of one row: pair k is pick k, so a task's expert comes straight from the picks (job j = pick j, the
 // shared expert's job last) and its weight loads are issued before the activations are staged; every other request
 // of the block (picks, weights, the shared gate's logit, h, the residual rows) is issued up front, with one wait.
-template <int TYPE, int G2, int NB, bool SHQ>
-__global__ void __launch_bounds__(D3_THREADS) k_dec_down1(const uint8_t* __restrict__ A, size_t sa, int H, int E, int K,
+template <int TYPE, int G2, int NB, bool SHQ, int NT3>
+__global__ void __launch_bounds__(NT3) k_dec_down1(const uint8_t* __restrict__ A, size_t sa, int H, int E, int K,
                                                          int ff, int shared, const float* __restrict__ logits,
                                                          const int* __restrict__ topi, const float* __restrict__ topw,
                                                          const int8_t* __restrict__ hq_q, const float* __restrict__ hq_d,
                                                          const int* __restrict__ hq_s, float* __restrict__ y,
                                                          float* __restrict__ x, const int* __restrict__ route_x,
                                                          const uint8_t* __restrict__ sh_dn) {
-    constexpr int LPR = lpr_of<TYPE>(), GROUPS = D3_THREADS / LPR, HQ4 = 5, HQS = 3;
+    constexpr int LPR = lpr_of<TYPE>(), GROUPS = NT3 / LPR;
+    // every pair's h (at most 17 rows of 1024) in registers: int4 quants and (scale, sum) words a thread
+    constexpr int HQ4 = (17 * 1024 / 16 + NT3 - 1) / NT3, HQS = (17 * 32 + NT3 - 1) / NT3;
     const int row0 = blockIdx.x * D3_ROWS, nbh = ff / 32, lane = threadIdx.x % WAVE, tid = threadIdx.x;
     const int g = tid / LPR, ln = tid % LPR;
     PROF(2, 0)
@@ -568,10 +570,10 @@ __global__ void __launch_bounds__(D3_THREADS) k_dec_down1(const uint8_t* __restr
     float dv[HQS];
     int sv[HQS];
 #pragma unroll
-    for (int r = 0; r < HQ4; ++r) hv[r] = reinterpret_cast<const int4*>(hq_q)[min(tid + r * D3_THREADS, nq - 1)];
+    for (int r = 0; r < HQ4; ++r) hv[r] = reinterpret_cast<const int4*>(hq_q)[min(tid + r * NT3, nq - 1)];
 #pragma unroll
     for (int r = 0; r < HQS; ++r) {
-        const int i = min(tid + r * D3_THREADS, ns - 1);
+        const int i = min(tid + r * NT3, ns - 1);
         dv[r] = hq_d[i];
         sv[r] = hq_s[i];
     }
@@ -602,10 +604,10 @@ __global__ void __launch_bounds__(D3_THREADS) k_dec_down1(const uint8_t* __restr
     const Acts a = acts_in(lds, NP, ff);
     // (unconditional: a thread past the end writes the last element's own value again, so no load sinks into a branch)
 #pragma unroll
-    for (int r = 0; r < HQ4; ++r) reinterpret_cast<int4*>(a.q)[min(tid + r * D3_THREADS, nq - 1)] = hv[r];
+    for (int r = 0; r < HQ4; ++r) reinterpret_cast<int4*>(a.q)[min(tid + r * NT3, nq - 1)] = hv[r];
 #pragma unroll
     for (int r = 0; r < HQS; ++r) {
-        const int i = min(tid + r * D3_THREADS, ns - 1);
+        const int i = min(tid + r * NT3, ns - 1);
         a.d[i] = dv[r];
         a.s[i] = sv[r];
     }
@@ -733,9 +735,10 @@ void launch_k2_tt1(const DecArgs& d, const sfnx_moe_layer_w& w, const DecLayout&
 }
 template <int TYPE, int G2>
 void launch_k3_one(const DecArgs& d, const sfnx_moe_layer_w& w, float* x, const DecLayout& L, char* ws, hipStream_t s) {
-    constexpr int NB = is_kquant(TYPE) ? 3 : 6;   // 11 jobs x 8 rows in one batch
-    auto kern = d.sh_dn ? k_dec_down1<TYPE, G2, NB, true> : k_dec_down1<TYPE, G2, NB, false>;
-    launch(2, kern, dim3(d.H / D3_ROWS), dim3(D3_THREADS), acts_bytes(d.K + 1, d.ff), s,
+    // 512 threads: 64 lane groups (K-quants) or 32, so 11 jobs x 8 rows are one batch of 2 or 3 tasks a group
+    constexpr int NT3 = 512, NB = is_kquant(TYPE) ? 2 : 3;
+    auto kern = d.sh_dn ? k_dec_down1<TYPE, G2, NB, true, NT3> : k_dec_down1<TYPE, G2, NB, false, NT3>;
+    launch(2, kern, dim3(d.H / D3_ROWS), dim3(NT3), acts_bytes(d.K + 1, d.ff), s,
         (const uint8_t*) w.dn, w.dn_stride, d.H, d.E, d.K, d.ff, d.shared, (const float*) (ws + L.logits),
         (const int*) (ws + L.topi), (const float*) (ws + L.topw), (const int8_t*) (ws + L.hq_q),
         (const float*) (ws + L.hq_d), (const int*) (ws + L.hq_s), (float*) (ws + L.y), x, (const int*) (ws + L.route_x),
