@@ -36,7 +36,7 @@ __device__ unsigned long long g_blk[3][1024][2];   // every block's first and la
 #define PROFB(k, i)
 #endif
 
-constexpr int D1_THREADS = 128, D1_WAVES = D1_THREADS / WAVE;   // K1: a router row per wavefront
+constexpr int D1_THREADS = 64, D1_WAVES = D1_THREADS / WAVE;   // K1: a router row per wavefront
 constexpr int D3_THREADS = 256, D3_ROWS = 8;                    // K3: output rows per block
 constexpr int D3W_THREADS = 512;                                 // K3 for windows of several rows
 template <int TYPE> constexpr int lpr_of() { return is_kquant(TYPE) ? 8 : 16; }
