@@ -14,7 +14,7 @@ Configs 2 (a 96-row verify window through the whole layer) and 4 (Q8_0 experts: 
 a 4096-token prompt chunk) are reported beside it, and the other expert types the reference decodes (Q5_K, Q4_0,
 Q5_1: decode through 12 stacked layers, a 2048-token prompt chunk).
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers 48] [--no-prefill] [--no-cpu] [--no-extra]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers 48] [--no-prefill] [--no-window] [--no-cpu] [--no-extra]
 """
 from __future__ import annotations
 
@@ -45,6 +45,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-window", action="store_true", help="skip the 16-row decode window")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-extra", action="store_true", help="skip configs 2 and 4 (verify window, Q8_0)")
@@ -179,7 +180,8 @@ def main():
                      "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "algorithmic_bytes_per_launch": alg[dom]},
     }
-    out["decode_window16"] = bench_window16(layers, s, moe, torch, args.steps)
+    if not args.no_window:
+        out["decode_window16"] = bench_window16(layers, s, moe, torch, args.steps)
     if not args.no_prefill:
         out["prefill"] = bench_prefill(layers[0], s, moe, torch)
     if not args.no_cpu:
