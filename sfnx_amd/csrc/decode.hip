@@ -195,7 +195,7 @@ template <int G> struct RowOf<SFNX_Q8_0, G> {
 // K1b for windows of several rows: the routing once (the top-k of every row, a wavefront a row, then the decode job
 // numbering of src/moe.cuh:164-198), published for K2, K3 and the caller.  At batch 1, K2's blocks take the top-k
 // themselves (k_dec_experts1); with more rows each block would repeat every row's top-k and the numbering.
-constexpr int DR_THREADS = 512;   // a thread per pick (T K <= 512)
+constexpr int DR_THREADS = 1024;   // a wavefront per row (T <= 16) and a thread per pick
 __global__ void __launch_bounds__(DR_THREADS) k_dec_route(int T, int E, int K, int shared, const float* __restrict__ logits,
                                                           int* __restrict__ topi_g, float* __restrict__ topw_g,
                                                           sfnx_job* __restrict__ jg, sfnx_job* __restrict__ jd,

@@ -149,11 +149,13 @@ template <int NV> __device__ __forceinline__ float reduce_scatter(float (&v)[NV]
 // takes the block's tokens LT_RU at a time from LDS, where the block stages them by asynchronous global -> LDS copies
 // into LT_NBUF buffers (LT_NBUF - 1 groups in flight while one computes); the RT x LT_RU sums of a lane leave through
 // one reduce_scatter.  A block: 8 wavefronts of RT rows, and as many tokens as give one block a compute unit.
-constexpr int LT_THREADS = 512, LT_WAVES = LT_THREADS / WAVE, LT_RU = 4, LT_NBUF = 3;
+constexpr int LT_THREADS = 512, LT_WAVES = LT_THREADS / WAVE, LT_RU = 4;
+// 3 buffers, 2 past H = 2560 (3 x 4 rows of 4096 floats would pass the 160 KB of LDS a workgroup has)
+__host__ __device__ constexpr int lt_nbuf(int NC) { return NC <= 10 ? 3 : 2; }
 template <int NC>
 __global__ void __launch_bounds__(LT_THREADS) k_router_logits(const float* __restrict__ W, const float* __restrict__ x,
                                                              float* __restrict__ logits, int T, int L, int tok) {
-    constexpr int H = NC * 4 * WAVE, RT = NC <= 8 ? 4 : 2, NV = RT * LT_RU;
+    constexpr int H = NC * 4 * WAVE, RT = NC <= 8 ? 4 : 2, NV = RT * LT_RU, LT_NBUF = lt_nbuf(NC);
     constexpr int PER = LT_RU * H / 4, COPIES = PER / LT_THREADS;   // float4 a group; copies a wavefront issues a group
     static_assert(PER % LT_THREADS == 0, "a group is whole copies");
     extern __shared__ __align__(16) unsigned char lds[];
@@ -436,6 +438,16 @@ extern "C" int sfnx_router_route(const float* W, const float* x, float* logits, 
     });
 }
 
+// the kernel allowed its dynamic LDS (up to 120 KB) once, then launched
+template <int NC>
+void launch_logits(dim3 g, hipStream_t s, const float* W, const float* x, float* logits, int T, int L, int tok) {
+    const size_t lds = (size_t) lt_nbuf(NC) * LT_RU * NC * 4 * WAVE * 4;
+    static const hipError_t allowed =
+        hipFuncSetAttribute((const void*) k_router_logits<NC>, hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds);
+    check(allowed, "hipFuncSetAttribute");
+    k_router_logits<NC><<<g, LT_THREADS, lds, s>>>(W, x, logits, T, L, tok);
+}
+
 extern "C" int sfnx_router_logits(const float* W, const float* x, float* logits, int T, int H, int L, void* st) {
     return guarded("sfnx_router_logits", [&] {
         require(H % 256 == 0, "H must be a multiple of 256");
@@ -447,15 +459,15 @@ extern "C" int sfnx_router_logits(const float* W, const float* x, float* logits,
         int tok = LT_RU;
         while ((long) rb * ((T + tok - 1) / tok) > ncu && tok < T) tok += LT_RU;
         const dim3 g(rb, (T + tok - 1) / tok);
-        const size_t lds = (size_t) LT_NBUF * LT_RU * H * 4;
         hipStream_t s = stream_of(st);
         switch (H / 256) {
-            case 4: k_router_logits<4><<<g, LT_THREADS, lds, s>>>(W, x, logits, T, L, tok); break;
-            case 8: k_router_logits<8><<<g, LT_THREADS, lds, s>>>(W, x, logits, T, L, tok); break;
-            case 10: k_router_logits<10><<<g, LT_THREADS, lds, s>>>(W, x, logits, T, L, tok); break;
-            case 16: k_router_logits<16><<<g, LT_THREADS, lds, s>>>(W, x, logits, T, L, tok); break;
+            case 4: launch_logits<4>(g, s, W, x, logits, T, L, tok); break;
+            case 8: launch_logits<8>(g, s, W, x, logits, T, L, tok); break;
+            case 10: launch_logits<10>(g, s, W, x, logits, T, L, tok); break;
+            case 16: launch_logits<16>(g, s, W, x, logits, T, L, tok); break;
             default: throw std::runtime_error("hidden size must be 1024, 2048, 2560 or 4096");
         }
+        check(hipGetLastError(), "k_router_logits launch");
     });
 }
 

@@ -83,9 +83,9 @@ def test_router_route_all_equal():
     assert oi.tolist() == [list(range(K))] * 3
 
 
-@pytest.mark.parametrize("T", [1, 37, 300])
-def test_router_logits_bit_exact(T):
-    H, L = 2048, 513
+@pytest.mark.parametrize("T, H, L", [(1, 2048, 513), (37, 2048, 513), (300, 2048, 513), (16, 1024, 65),
+                                     (40, 2560, 1025), (16, 4096, 129), (300, 4096, 513)])
+def test_router_logits_bit_exact(T, H, L):
     W = orc.synth(L * H, 220, 0.02).reshape(L, H)
     x = orc.synth(T * H, 221, 1.0).reshape(T, H)
     out = torch.empty((T, L), dtype=torch.float32, device="cuda")
