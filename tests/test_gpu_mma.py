@@ -189,3 +189,16 @@ def test_mma_extreme_skew_and_tiny_chunks(C):
     sig = 1 / (1 + np.exp(-b.logits.cpu().numpy()[:, shape.E].astype(np.float64)))
     want = np.einsum("tk,tkh->th", topw, part[: C * shape.K].reshape(C, shape.K, -1)) + sig[:, None] * part[C * shape.K:]
     assert max_rel(y.cpu().numpy(), want) < 1e-5
+
+
+@pytest.mark.parametrize("H, ff, wtype", [(4096, 512, orc.Q4_K), (2560, 1024, orc.Q8_0), (4096, 1024, orc.Q5_1)])
+def test_mma_wide_hidden(H, ff, wtype):
+    """the prompt path at hidden 2560 and 4096 and FF 1024 (the router's widest LDS form, the MMA's 5 and 8 runs a
+    row): routing against the oracle, sampled pairs within 2e-3 of float64"""
+    shape = moe.LayerShape(H=H, E=64, K=6, ff=ff, wtype=wtype, shared=True)
+    L, host, x, y, b = run_prefill(shape, 200 + H % 97, 150)
+    lg = orc.router_logits(host.W, x)
+    oi, _, _ = orc.topk(lg, shape.E, shape.K)
+    assert np.array_equal(b.topi.cpu().numpy(), oi)
+    eg, ed = check_sampled(host, x, b, 24, np.random.default_rng(H))
+    assert eg < 2e-3 and ed < 2e-3, (eg, ed)
