@@ -232,3 +232,32 @@ def test_pf_dense_against_float64(rows, cols, C):
     assert (got[:, rows:] == 5.0).all()
     # the staging holds the f16 dequantization, bit for bit the oracle's f16 form
     assert np.array_equal(wh.cpu().numpy().view(np.uint16), orc.dequant_f16(orc.Q8_0, g.reshape(-1), rows, cols).reshape(-1))
+
+
+def test_prefill_shared_graph_replays():
+    """the dense shared expert's prompt rows (dequantization + rocBLAS GEMMs) captured in a HIP graph, as the bench
+    times them: every replay, with eager work between them, equals the eager result bit for bit"""
+    shape = moe.LayerShape(H=1024, E=64, K=6, ff=512, wtype=orc.Q4_K, shared=True, sh_q8s=True)
+    L, _ = make_layer(shape, 160)
+    C = 96
+    P = C * shape.K
+    b = moe.PrefillBuffers(shape, C)
+    moe.to_f16(torch.from_numpy(orc.synth(C * shape.H, 161, 1.0).reshape(C, shape.H)).cuda(), b.xh)
+    moe.prefill_shared(L, b)
+    torch.cuda.synchronize()
+    want = b.part[P:P + C].clone()
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        moe.prefill_shared(L, b)
+    torch.cuda.current_stream().wait_stream(st)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        moe.prefill_shared(L, b)
+    for i in range(3):
+        b.part[P:P + C].fill_(float(i + 1))   # eager work between the replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(b.part[P:P + C], want), i
