@@ -89,3 +89,37 @@ def test_hc_read_refusals():
     Rd2 = torch.zeros((17, 2048), dtype=torch.float32, device="cuda")
     with pytest.raises(RuntimeError, match="T out of range"):
         h(Rd2, torch.empty((17, 512), dtype=torch.float32, device="cuda"))
+
+
+@pytest.mark.parametrize("T", [1, 5])
+def test_hc_read_graph_replays(T):
+    """the read captured in a HIP graph (as the bench times it): every replay, with eager work between them, gives the
+    eager mixed, xq and inject bit for bit (no fold, so R stays as it is)"""
+    N, HC, LR = 2560, 4, 320
+    w, R, bo, inj = hc_inputs(N, HC, LR, T, 500 + T)
+    h = moe.HcRead(N, HC, LR, w["w_norm"], w["dq"], w["dd"], w["uq"], w["ud"], w["w_inj"])
+    Rd = torch.from_numpy(R).cuda()
+    mixed = torch.empty((T, N), dtype=torch.float32, device="cuda")
+    xq = torch.empty(T * (N // 32) * 36, dtype=torch.uint8, device="cuda")
+    injo = torch.zeros((T, HC), dtype=torch.float32, device="cuda")
+    h(Rd, mixed, xq, inject=injo)
+    torch.cuda.synchronize()
+    want = (mixed.clone(), xq.clone(), injo.clone())
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        h(Rd, mixed, xq, inject=injo)
+    torch.cuda.current_stream().wait_stream(st)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        h(Rd, mixed, xq, inject=injo)
+    for i in range(3):
+        mixed.fill_(float(i))
+        xq.zero_()
+        injo.fill_(-1.0)
+        h.ws.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(mixed, want[0]) and torch.equal(xq, want[1]) and torch.equal(injo, want[2]), i
