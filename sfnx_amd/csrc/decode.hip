@@ -93,17 +93,24 @@ __global__ void __launch_bounds__(D1_THREADS) k_dec_router(const float* __restri
 #pragma unroll
     for (int i = 0; i < NC; ++i) wv[i] = reinterpret_cast<const float4*>(W + (size_t) (live ? row : 0) * H)[i * WAVE + lane];
     __shared__ float rs[SFNX_MAXT];
+    // windows: token t + 1's chunks are loaded while token t's reductions run
+    float4 xn[NC];
+#pragma unroll
+    for (int i = 0; i < NC; ++i) xn[i] = reinterpret_cast<const float4*>(x)[i * WAVE + lane];
 #pragma unroll
     for (int t = 0; t < TT; ++t) {
         if (t >= T) break;
-        const float4* x4 = reinterpret_cast<const float4*>(x + (size_t) t * H);
         float4 xv[NC];
         float ss = 0.f;
 #pragma unroll
-        for (int i = 0; i < NC; ++i) {
-            xv[i] = x4[i * WAVE + lane];
-            ss = rms_lane_add(xv[i], ss);
+        for (int i = 0; i < NC; ++i) xv[i] = xn[i];
+        if (TT > 1 && t + 1 < T) {
+            const float4* x4 = reinterpret_cast<const float4*>(x + (size_t) (t + 1) * H);
+#pragma unroll
+            for (int i = 0; i < NC; ++i) xn[i] = x4[i * WAVE + lane];
         }
+#pragma unroll
+        for (int i = 0; i < NC; ++i) ss = rms_lane_add(xv[i], ss);
         const float r = norm ? rms_from_sum(ss, H, eps) : 1.0f;
         if (threadIdx.x == 0) rs[t] = r;
         float a = 0.f;
