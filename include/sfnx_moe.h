@@ -163,10 +163,12 @@ typedef struct sfnx_moe_layer_w {
     size_t dn_stride;
 } sfnx_moe_layer_w;
 
-/* bytes of the workspace sfnx_moe_decode needs for windows of up to T rows; offsets (may be null) receives the byte
- * offsets of its pieces: logits [T][E+1] f32, xq [T][H/32] q8_1, topi [T][K] i32, topw [T][K] f32, jobs_gu and
- * jobs_dn [T K + 1] sfnx_job, njobs [2] i32, gu [T K + T][2 ff] f32, hq_q [T K + T][ff] i8, hq_d and hq_s
- * [T K + T][ff / 32] (f32 scale, i32 sum), y [T][H] f32, then the total (13 values) */
+/* bytes of the workspace sfnx_moe_decode needs (1 <= T <= 16 is only checked: every piece is laid out for 16 rows, so
+ * one workspace serves windows of any size and the offsets do not depend on T); offsets (may be null) receives the byte
+ * offsets of its pieces, each with room for 16 rows (M = 16): logits [M][E+1] f32, xq [M][H/32] q8_1, topi [M][K] i32,
+ * topw [M][K] f32, jobs_gu and jobs_dn [M K + 1] sfnx_job, njobs [2] i32, gu [M K + M][2 ff] f32, hq_q [M K + M][ff]
+ * i8, hq_d and hq_s [M K + M][ff / 32] (f32 scale, i32 sum), y [M][H] f32, then the total (13 values).  After a
+ * window of T rows, row t of a piece holds that window's row t (pairs p = t K + k, the shared expert's at T K + t). */
 size_t sfnx_moe_decode_workspace(int T, int H, int E, int K, int ff, size_t* offsets);
 
 /* A decode window (1 <= T <= 16 rows) through n_layers stacked MoE layers, replacing the engine's per-layer calls
@@ -226,7 +228,10 @@ int sfnx_residual_rmsnorm(float* x, const float* y, float* xn, int T, int H, flo
 /* Measurement hook (no reference counterpart: for benchmarks that need each kernel's own duration).  While enabled,
  * sfnx_moe_decode launches its three kernels with start/stop events that the runtime stamps at the dispatch's
  * begin and end; sfnx_kernel_clock_read waits for the last such launches and writes their durations in us
- * (router, gate|up, down + combine) to us[3].  Process-wide; not for concurrent callers. */
+ * (router, gate|up, down + combine) to us[3].  Windows of T > 1 rows add a fourth launch per layer, the routing
+ * (k_dec_route, one workgroup) between the router and gate|up: the clock does not cover it, so a window's per-kernel
+ * figures leave it out (the window's whole time comes from timing the layers' launches together).  Process-wide; not
+ * for concurrent callers. */
 int sfnx_kernel_clock(int enable);
 int sfnx_kernel_clock_read(float* us);
 
@@ -259,7 +264,9 @@ int sfnx_gguf_str(const sfnx_gguf* g, const char* key, const char** v);         
  * of the same type and FF) as expert E, and the router W = [ffn_gate_inp rows ; ffn_gate_inp_shexp] (f32 [E+1][H]).
  * Q4_0, Q5_1, Q8_0, Q4_K or Q5_K experts, gate and up of one type, down of that or another; ff0 on a block of the
  * down type (32 or 256 columns), ff1 - ff0 and H multiples of 512.  info (may be null, else 6 ints) receives the
- * gate|up type, H, E, ff1 - ff0, shared and the down type.  A loader, not a hot-path call: it allocates a staging buffer and synchronises the stream. */
+ * gate|up type, H, E, ff1 - ff0, shared and the down type.  A loader, not a hot-path call: it allocates a staging buffer and synchronises the stream.
+ * The buffers' sizes come from the file and cannot be checked here: E is ne[2] of blk.<layer>.ffn_gate_exps
+ * (sfnx_gguf_find), and gu, dn and W must hold E + 1 experts / rows when the shared expert is present (E otherwise). */
 int sfnx_gguf_moe_layer(const sfnx_gguf* g, int layer, int ff0, int ff1, void* gu, size_t gu_stride, void* dn,
                         size_t dn_stride, float* W, int* info, void* st);
 /* sfnx_gguf_moe_layer for the model as the reference loads it (src/model.cpp:807-809): the shared expert must be

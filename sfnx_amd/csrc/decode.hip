@@ -13,28 +13,11 @@
 // two paths agree bit for bit.
 #include <hip/hip_ext.h>
 #include "mv.hpp"
-#ifdef SFNX_PHASE_PROF
-#define SFNX_TOPK_STAMP(i) if (lane == 0 && blockIdx.x == 0) { g_prof_topk[i] = wall_clock64(); }
-__device__ unsigned long long g_prof_topk[4];
-#endif
 #include "topk.hpp"
 
 namespace sfnx {
 namespace {
 
-// SFNX_PHASE_PROF (off in the product build): wall-clock stamps of the kernels' phases, blocks 0 and 100, for
-// finding where a launch's time goes
-#ifdef SFNX_PHASE_PROF
-__device__ unsigned long long g_prof[8][16];
-#define PROF(k, i)                                                                  \
-    if (threadIdx.x == 0 && (blockIdx.x == 0 || blockIdx.x == 100)) g_prof[2 * (k) + (blockIdx.x != 0)][i] = wall_clock64();
-__device__ unsigned long long g_blk[3][1024][2];   // every block's first and last stamp, per kernel
-#define PROFB(k, i) \
-    if (threadIdx.x == 0 && blockIdx.x < 1024) g_blk[k][blockIdx.x][i] = wall_clock64();
-#else
-#define PROF(k, i)
-#define PROFB(k, i)
-#endif
 
 constexpr int D1_THREADS = 64, D1_WAVES = D1_THREADS / WAVE;   // K1: a router row per wavefront
 constexpr int D3_THREADS = 256, D3_ROWS = 8;                    // K3: output rows per block
@@ -45,7 +28,10 @@ template <int TYPE> constexpr int d2_threads() { return 32 * lpr_of<TYPE>(); }  
 struct DecLayout {
     size_t logits, xq, topi, topw, jg, jd, njobs, gu, hq_q, hq_d, hq_s, y, route_x, total;
 };
-DecLayout dec_layout(int T, int H, int E, int K, int ff) {
+// Every piece is laid out for the largest window (SFNX_MAXT rows), so the offsets are the same whatever T a call
+// runs: a workspace sized once serves windows of any size, and a piece's row t always starts at t times its row size.
+DecLayout dec_layout(int H, int E, int K, int ff) {
+    constexpr int T = SFNX_MAXT;
     const size_t P = (size_t) T * K, NP = P + T, nj = P + 1;
     size_t o = 0;
     auto take = [&](size_t bytes) {
@@ -79,7 +65,6 @@ __global__ void __launch_bounds__(D1_THREADS) k_dec_router(const float* __restri
     constexpr int H = NC * 4 * WAVE, NQ = 2;
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE, L = E + 1;
     const int row = blockIdx.x * D1_WAVES + wave;
-    PROFB(0, 0)
     // every load of the launch issued up front: the router row, each token's chunks, this half-wave's q8_1 blocks
     const int nb = H / 32, hw = threadIdx.x / 32, l = threadIdx.x % 32, nslot = gridDim.x * (D1_THREADS / 32);
     float xqv[NQ];
@@ -148,7 +133,6 @@ __global__ void __launch_bounds__(D1_THREADS) k_dec_router(const float* __restri
         blk[4 + l] = (uint8_t) (int8_t) (amax == 0.0f ? 0 : (int) roundf(xi / d));
         if (l == 0) *reinterpret_cast<uint32_t*>(blk) = (uint32_t) f2h(d) | ((uint32_t) f2h(sum) << 16);
     }
-    PROFB(0, 1)
 }
 
 // ------------------------------------------------------------------------------------------------ K2
@@ -349,8 +333,6 @@ __global__ void __launch_bounds__(2 * d2_threads<TYPE>()) k_dec_experts1(
     __shared__ float gbuf[32], ubuf[32];
     __shared__ uint32_t junk[WAVE];
     extern __shared__ __align__(16) unsigned char lds[];
-    PROF(1, 0)
-    PROFB(1, 0)
     // the logits and the activations requested together
     float lv[NV];
     topk_load<NV>(logits, E / WAVE, lane, lv);
@@ -358,7 +340,6 @@ __global__ void __launch_bounds__(2 * d2_threads<TYPE>()) k_dec_experts1(
     stage_q8_1(a, xq, nullptr, 1);
     // the next layer's router rows into this XCD's L2 for that layer's K1, while HBM idles through the top-k
     warm_router_rows(Wn, E + 1, H, junk);
-    PROF(1, 7)
     int pick;
     uint32_t pord;
     topk_picks<NV>(lv, K, lane, pick, pord);
@@ -367,7 +348,6 @@ __global__ void __launch_bounds__(2 * d2_threads<TYPE>()) k_dec_experts1(
     // job of this block: routed pick j = jb, the shared job at jb = nr (or first, when dense: then jb = myjob - 1)
     const int myjob = blockIdx.x / NFB, jb = sh_first ? (q8s ? nr : myjob - 1) : myjob;
     const bool has_job = sh_first ? q8s || jb < nr : jb < nj;
-    PROF(1, 1)
     if (!has_job && blockIdx.x >= XCDS) {
         warm_wait();
         return;
@@ -410,7 +390,6 @@ __global__ void __launch_bounds__(2 * d2_threads<TYPE>()) k_dec_experts1(
         return;
     }
     __syncthreads();   // the staged activations
-    PROF(1, 3)
     float v;
     if constexpr (SHR) v = group_sum<LPR>(q8s ? ws.dot(a, 0, ln) : wr.dot1(a, ln));
     else if constexpr (SHQ) v = group_sum<LPR>(q8s ? q8s_dot<LPR>(q80_planes(sh_gu, 2 * ff, H), row, H, ln, a, 0) : wr.dot1(a, ln));
@@ -420,7 +399,6 @@ __global__ void __launch_bounds__(2 * d2_threads<TYPE>()) k_dec_experts1(
         (up ? ubuf : gbuf)[fl] = v;
     }
     __syncthreads();
-    PROF(1, 5)
     if (threadIdx.x < 32) {
         const int l = threadIdx.x;
         const float v = silu_f(gbuf[l]) * ubuf[l];
@@ -435,8 +413,6 @@ __global__ void __launch_bounds__(2 * d2_threads<TYPE>()) k_dec_experts1(
         }
     }
     warm_wait();
-    PROF(1, 6)
-    PROFB(1, 1)
 }
 
 // ------------------------------------------------------------------------------------------------ K3
@@ -451,8 +427,6 @@ __global__ void __launch_bounds__(D3W_THREADS) k_dec_down(const uint8_t* __restr
                                                         float* __restrict__ x, int hq_in_lds, const uint8_t* __restrict__ sh_dn) {
     constexpr int LPR = lpr_of<TYPE>(), GROUPS = D3W_THREADS / LPR;
     const int row0 = blockIdx.x * D3_ROWS, nj = njobs[0], P = T * K, NP = P + T, nbh = ff / 32;
-    PROF(2, 0)
-    PROFB(2, 0)
     __shared__ int jw[MAX_P + 1], jn[MAX_P + 1], jout[MAX_P + 1][SFNX_MAXT];
     __shared__ float part[MAX_P + SFNX_MAXT][D3_ROWS];
     __shared__ int ti[MAX_P];
@@ -491,7 +465,6 @@ __global__ void __launch_bounds__(D3W_THREADS) k_dec_down(const uint8_t* __restr
     const int g = threadIdx.x / LPR, ln = threadIdx.x % LPR;
     // with its own dense Q8_0 matrix the shared expert's job (the last) runs apart, in the reference's q8s sums
     const int nq = sh_dn != nullptr && shared ? nj - 1 : nj, ntask = nq * D3_ROWS;
-    PROF(2, 1)
     if (nq < nj) {
         const Q80Planes Ps = q80_planes(sh_dn, H, ff);
         for (int task = g; task < T * D3_ROWS; task += GROUPS) {
@@ -524,7 +497,6 @@ __global__ void __launch_bounds__(D3W_THREADS) k_dec_down(const uint8_t* __restr
         }
     }
     __syncthreads();
-    PROF(2, 2)
     for (int i = threadIdx.x; i < T * D3_ROWS; i += D3W_THREADS) {
         const int t = i / D3_ROWS, r = i % D3_ROWS, row = row0 + r;
         float pw[MAX_K], pv[MAX_K];
@@ -542,8 +514,6 @@ __global__ void __launch_bounds__(D3W_THREADS) k_dec_down(const uint8_t* __restr
         y[(size_t) t * H + row] = s;
         x[(size_t) t * H + row] = xr[t][r] + s;
     }
-    PROF(2, 3)
-    PROFB(2, 1)
 }
 
 // K3 for a window of one row: pair k is pick k, so a task's expert comes straight from the picks (job j = pick j, the
@@ -562,8 +532,6 @@ __global__ void __launch_bounds__(NT3) k_dec_down1(const uint8_t* __restrict__ A
     constexpr int HQ4 = (17 * 1024 / 16 + NT3 - 1) / NT3, HQS = (17 * 32 + NT3 - 1) / NT3;
     const int row0 = blockIdx.x * D3_ROWS, nbh = ff / 32, lane = threadIdx.x % WAVE, tid = threadIdx.x;
     const int g = tid / LPR, ln = tid % LPR;
-    PROF(2, 0)
-    PROFB(2, 0)
     __shared__ float part[MAX_K + 1][D3_ROWS];
     extern __shared__ __align__(16) unsigned char lds[];
     // every request first; the picks from the copy K2 left in this XCD's L2
@@ -619,7 +587,6 @@ __global__ void __launch_bounds__(NT3) k_dec_down1(const uint8_t* __restrict__ A
         a.s[i] = sv[r];
     }
     __syncthreads();
-    PROF(2, 1)
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
         const int task = g + b * GROUPS;
@@ -649,7 +616,6 @@ __global__ void __launch_bounds__(NT3) k_dec_down1(const uint8_t* __restrict__ A
         if (ln == 0) part[q][r] = v;
     }
     __syncthreads();
-    PROF(2, 2)
     // the weighted sum in the reference's fmaf order, then the residual
     if (tid < WAVE) {
         const int r = tid % D3_ROWS;
@@ -665,8 +631,6 @@ __global__ void __launch_bounds__(NT3) k_dec_down1(const uint8_t* __restrict__ A
             x[row0 + r] = xr + s;
         }
     }
-    PROF(2, 3)
-    PROFB(2, 1)
 }
 
 // ------------------------------------------------------------------------------------------------ launch
@@ -826,13 +790,6 @@ void launch_layer_tt(const DecArgs& d, const sfnx_moe_layer_w& w, float* x, cons
 
 using namespace sfnx;
 
-#ifdef SFNX_PHASE_PROF
-extern "C" int sfnx_prof_read(unsigned long long* out) {
-    if (hipMemcpyFromSymbol(out, HIP_SYMBOL(g_prof), sizeof(g_prof)) != hipSuccess) return -1;
-    if (hipMemcpyFromSymbol(out + 129, HIP_SYMBOL(g_blk), sizeof(g_blk)) != hipSuccess) return -1;
-    return hipMemcpyFromSymbol(out + 128 + 3 * 2048 + 1, HIP_SYMBOL(g_prof_topk), 32) == hipSuccess ? 0 : -1;
-}
-#endif
 
 extern "C" int sfnx_kernel_clock(int enable) {
     return guarded("sfnx_kernel_clock", [&] {
@@ -858,7 +815,8 @@ extern "C" int sfnx_kernel_clock_read(float* us) {
 }
 
 extern "C" size_t sfnx_moe_decode_workspace(int T, int H, int E, int K, int ff, size_t* offsets) {
-    const DecLayout L = dec_layout(T, H, E, K, ff);
+    if (T < 1 || T > SFNX_MAXT) return 0;
+    const DecLayout L = dec_layout(H, E, K, ff);
     if (offsets) {
         const size_t o[13] = {L.logits, L.xq, L.topi, L.topw, L.jg, L.jd, L.njobs, L.gu, L.hq_q, L.hq_d, L.hq_s, L.y, L.total};
         for (int i = 0; i < 13; ++i) offsets[i] = o[i];
@@ -879,7 +837,7 @@ void moe_decode(const sfnx_moe_layer_w* layers, const sfnx_moe_shared_q8s* sh, i
         require(H == 1024 || H == 2048 || H == 2560 || H == 4096, "hidden size must be 1024, 2048, 2560 or 4096");
         require(ff == 512 || ff == 1024, "FF must be 512 or 1024");
         require(T * K <= (is_kquant(type) ? 256 : 512), "T K picks exceed the block");
-        const DecLayout L = dec_layout(T, H, E, K, ff);
+        const DecLayout L = dec_layout(H, E, K, ff);
         require(ws != nullptr && ws_bytes >= L.total, "workspace smaller than sfnx_moe_decode_workspace()");
         require(n_layers >= 0 && (n_layers == 0 || layers != nullptr), "no layers");
         for (int l = 0; l < n_layers; ++l) {

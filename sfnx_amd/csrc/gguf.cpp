@@ -203,7 +203,13 @@ void load_shard(sfnx_gguf& g, const std::string& path, bool meta) {
         int block, bytes;
         require(type_info(t.info.type, block, bytes), ("gguf: " + t.name + " has an unknown ggml type").c_str());
         require(t.info.ne[0] % block == 0, ("gguf: " + t.name + "'s rows are not whole blocks").c_str());
-        t.info.nbytes = (size_t) (t.info.ne[0] / block) * bytes * (size_t) (t.info.ne[1] * t.info.ne[2] * t.info.ne[3]);
+        // the byte count with every product checked: each dimension may be up to 2^40, so a crafted header's
+        // product can wrap 64 bits and pass a bounds check it should fail
+        uint64_t nb = (uint64_t) (t.info.ne[0] / block), prod = 0;
+        bool wrap = __builtin_mul_overflow(nb, (uint64_t) bytes, &nb);
+        for (int d = 1; d < 4; ++d) wrap |= __builtin_mul_overflow(nb, (uint64_t) t.info.ne[d], &prod), nb = prod;
+        require(!wrap && nb <= m.size, ("gguf: " + t.name + "'s data is larger than the file").c_str());
+        t.info.nbytes = (size_t) nb;
         t.info.shard = shard;
         offs.push_back(r.get<uint64_t>());
         local.push_back(std::move(t));
@@ -211,7 +217,8 @@ void load_shard(sfnx_gguf& g, const std::string& path, bool meta) {
     const uint64_t data0 = ((uint64_t) (r.p - base) + align - 1) / align * align;
     for (size_t i = 0; i < local.size(); ++i) {
         sfnx_gguf::Tensor& t = local[i];
-        require(offs[i] <= m.size && data0 + offs[i] + t.info.nbytes <= m.size,
+        // step by step, so that no sum can wrap: data0 <= size, then offs <= size - data0, then nbytes <= the rest
+        require(data0 <= m.size && offs[i] <= m.size - data0 && t.info.nbytes <= m.size - data0 - offs[i],
                 ("gguf: " + t.name + "'s data runs past the end of " + path).c_str());
         t.info.data = base + data0 + offs[i];
         require(g.index.count(t.name) == 0, ("gguf: tensor " + t.name + " appears twice").c_str());

@@ -108,9 +108,6 @@ __device__ inline void topk_picks(const float (&lv)[NV], int K, int lane, int& p
         const uint32_t o = (uint32_t) (pick_key(lv[i], 0) >> 32);
         tk[i] = o ? (o & 0xFFFFFC00u) | (1023u - (uint32_t) (lane + WAVE * i)) : 0u;
     }
-#ifdef SFNX_TOPK_STAMP
-    SFNX_TOPK_STAMP(0)
-#endif
     // descending bitonic sort of the lane's keys
 #pragma unroll
     for (int k = 2; k <= NV; k *= 2)
@@ -126,9 +123,6 @@ __device__ inline void topk_picks(const float (&lv)[NV], int K, int lane, int& p
                     tk[l] = desc ? min(a, b) : max(a, b);
                 }
             }
-#ifdef SFNX_TOPK_STAMP
-    SFNX_TOPK_STAMP(1)
-#endif
     uint32_t mk = 0;
     for (int k = 0; k < K; ++k) {
         const uint32_t best = wave_max_u32(tk[0]);
@@ -201,9 +195,6 @@ __device__ inline void topk_picks(const float (&lv)[NV], int K, int lane, int& p
             idx[NV - 1] = won ? ~0u : idx[NV - 1];
         }
     }
-#ifdef SFNX_TOPK_STAMP
-    SFNX_TOPK_STAMP(2)
-#endif
     pick = mine ? (int) myidx : -1;
     pord = mine;
 }
@@ -214,10 +205,6 @@ __device__ inline float topk_weight(int pick, uint32_t pord, int K) {
     const float ek = pick >= 0 ? expf(myv - v0) : 0.f;
     float z = 0.f;
     for (int k = 0; k < K; ++k) z += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ek), k));
-#ifdef SFNX_TOPK_STAMP
-    const int lane = __lane_id();
-    SFNX_TOPK_STAMP(3)
-#endif
     return pick < 0 ? 0.f : ek / z;
 }
 template <int NV>

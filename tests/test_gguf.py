@@ -87,6 +87,13 @@ def test_refusals(tmp_path):
     p = _fails(tmp_path, "", tensors=[("t.a", 0, (4,), b"\0" * 16), ("t.a", 0, (4,), b"\0" * 16)])
     with pytest.raises(RuntimeError, match="appears twice"):
         moe.Gguf(str(p))
+    # dimensions whose byte count wraps 64 bits (4 B x 2^32 x 2^32 = 2^66): refused, not read past the mapping
+    p = _fails(tmp_path, "", tensors=[("t.w", 0, (1 << 32, 1 << 32), b"")])
+    with pytest.raises(RuntimeError, match="larger than the file"):
+        moe.Gguf(str(p))
+    p = _fails(tmp_path, "", tensors=[("t.w", 12, (1 << 39, 1 << 39, 1 << 39, 1 << 39), b"")])
+    with pytest.raises(RuntimeError, match="larger than the file"):
+        moe.Gguf(str(p))
     # cut inside the tensor data, then inside the header
     gw.write_gguf(tmp_path / "ok.gguf", _meta(), _tensors(rng))
     full = (tmp_path / "ok.gguf").read_bytes()

@@ -118,10 +118,12 @@ def test_mixed_gate_up_and_down_types(wtype, dn_type):
 
 @pytest.mark.parametrize("H, E, K, ff, wtype, T", [
     (2560, 1024, 16, 1024, orc.Q4_K, 1), (2560, 1024, 16, 1024, orc.Q4_K, 4), (4096, 128, 4, 512, orc.Q5_K, 1),
-    (4096, 128, 4, 512, orc.Q8_0, 16), (1024, 1024, 1, 1024, orc.Q4_0, 2), (2560, 256, 8, 512, orc.Q5_1, 16)])
+    (4096, 128, 4, 512, orc.Q8_0, 16), (1024, 1024, 1, 1024, orc.Q4_0, 2), (2560, 256, 8, 512, orc.Q5_1, 16),
+    (2048, 512, 10, 1024, orc.Q4_K, 16)])
 def test_fused_decode_edge_shapes(H, E, K, ff, wtype, T):
     """the fused decode's limits: hidden 2560 and 4096, 1024 experts, top-16 and top-1, FF 1024, windows of 1 to 16
-    rows: equal to the unfused path bit for bit and to the oracle within 2e-3"""
+    rows: equal to the unfused path bit for bit and to the oracle within 2e-3.  The last case's h (176 pairs of 1024)
+    does not fit in the down kernel's LDS, so its down dots read h from memory (the unstaged branch)."""
     shape = moe.LayerShape(H=H, E=E, K=K, ff=ff, wtype=wtype, shared=True)
     L, host = make_layer(shape, 70 + H % 97 + K)
     x0 = torch.from_numpy(orc.synth(T * H, 830 + T + K, 1.0).reshape(T, H)).cuda()
@@ -145,3 +147,25 @@ def test_fused_decode_refuses_out_of_range():
     f = moe.FusedDecode([L], 16)
     with pytest.raises(RuntimeError, match="T out of range"):
         f(torch.zeros((17, 1024), dtype=torch.float32, device="cuda"))
+
+
+def test_workspace_serves_shorter_windows():
+    """one workspace sized for 16 rows, then windows of 4 and 1 rows: each piece's rows hold that window's values
+    (the layout does not move with T), equal to the unfused path's"""
+    shape = moe.LayerShape(H=1024, E=64, K=6, ff=512, wtype=orc.Q4_K, shared=True)
+    L, host = make_layer(shape, 41)
+    f = moe.FusedDecode([L], 16)
+    for T in (4, 1, 16, 3):
+        x0 = torch.from_numpy(orc.synth(T * shape.H, 860 + T, 1.0).reshape(T, shape.H)).cuda()
+        b = moe.DecodeBuffers(shape, T)
+        xu = x0.clone()
+        yu = unfused_chain([L], xu, False, [b])
+        xf = x0.clone()
+        f(xf, norm=False)
+        torch.cuda.synchronize()
+        K = shape.K
+        assert np.array_equal(f.piece("topi", torch.int32, (T, K)).cpu().numpy(), b.topi.cpu().numpy())
+        assert np.array_equal(bits(f.piece("topw", torch.float32, (T, K))), bits(b.topw))
+        assert np.array_equal(bits(f.piece("logits", torch.float32, (T, shape.E + 1))), bits(b.logits))
+        assert np.array_equal(bits(f.piece("y", torch.float32, (T, shape.H))), bits(yu))
+        assert np.array_equal(bits(xf), bits(xu))
