@@ -180,6 +180,10 @@ def main():
                      "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "algorithmic_bytes_per_launch": alg[dom]},
     }
+    cb = copy_bandwidth(torch)
+    out["hbm_copy_gbs"] = cb
+    out["hbm_frac_of_copy"] = round(gbs / cb, 4)
+    out["roofline"]["frac_of_copy"] = round(ach / cb, 4)
     if not args.no_window:
         out["decode_window16"] = bench_window16(layers, s, moe, torch, args.steps)
     if not args.no_prefill:
@@ -195,6 +199,26 @@ def main():
         log(f"q8s shared: decode {out['q8s_shared']['decode_us_per_token_layer']} us/token-layer")
     print(json.dumps(out), flush=True)
     return 0
+
+
+def copy_bandwidth(torch, nbytes=1 << 30, reps=10):
+    """the HBM bandwidth a plain device copy achieves on this GPU (torch's copy kernel, 1 GiB to 1 GiB): bytes read
+    plus bytes written over the time, the best of reps copies"""
+    a = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    b.copy_(a)
+    torch.cuda.synchronize()
+    best = float("inf")
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        b.copy_(a)
+        e1.record()
+        torch.cuda.synchronize()
+        best = min(best, e0.elapsed_time(e1) * 1e-3)
+    del a, b
+    torch.cuda.empty_cache()
+    return round(2 * nbytes / best / 1e9, 1)
 
 
 def measured_traffic(kernel):
@@ -490,24 +514,38 @@ def cpu_baseline(L, s, moe, torch, x0, seconds):
     host = orc.LayerWeights(L.W.cpu().numpy(), gu_g.cpu().numpy(), dn_g.cpu().numpy(), s.wtype, s.H, s.E, s.K, s.ff, True,
                             dn_type=s.dn_type)
     x = xn.cpu().numpy()
-    threads = min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", "16")), 16)
-    us1, _ = orc.time_layer_decode(host, x, threads, 3, 0)   # one short run to size the sample
-    reps = max(5, min(200, int(seconds * 1e6 / max(us1, 1.0) / 2)))
-    us, _ = orc.time_layer_decode(host, x, threads, reps, 1 << 30)
+    # every core this process may run on (the affinity mask), and beside it the box's stated CPU share for one GPU
+    # (OMP_NUM_THREADS, 16 here): the faster of the two is the baseline, both are recorded
+    nproc = os.cpu_count() or 1
+    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else nproc
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    counts = sorted({c for c in (avail, share) if c > 0})
+    runs = {}
+    for threads in counts:
+        us1, _ = orc.time_layer_decode(host, x, threads, 3, 0)   # one short run to size the sample
+        reps = max(5, min(200, int(seconds / len(counts) * 1e6 / max(us1, 1.0) / 2)))
+        runs[threads] = (orc.time_layer_decode(host, x, threads, reps, 1 << 30)[0], reps)
+    threads = min(runs, key=lambda c: runs[c][0])
+    us, reps = runs[threads]
     oy, _, oi, _, _, _ = orc.layer_decode(host, x, threads)
     err = float(np.max(np.abs(y.cpu().numpy() - oy)) / np.max(np.abs(oy)))
     bytes_tl = E1 * s.H * 4 + (s.K + 1) * expert_bytes(s, moe)
-    cpu = "unknown"
+    info = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu = line.split(":", 1)[1].strip()
-                break
+            k, _, v = line.partition(":")
+            k = k.strip()
+            if k in ("model name", "cpu family", "model", "stepping", "cpu MHz") and k not in info:
+                info[k] = v.strip()
     except OSError:
         pass
+    cpu = f"{info.get('model name', 'unknown')} (family {info.get('cpu family', '?')}, model {info.get('model', '?')}, " \
+          f"stepping {info.get('stepping', '?')})"
     return {"value": round(us, 1), "unit": "us/token-layer", "cores": threads, "kind": "port",
             "sample": f"config 0: one token through one layer (layer 0 of the bench), median of {reps} runs, "
                       f"a 1 GiB sweep between runs",
+            "nproc": nproc, "cores_available": avail, "omp_num_threads_env": share,
+            "us_by_threads": {str(c): round(v[0], 1) for c, v in runs.items()},
             "gbs": round(bytes_tl / (us * 1e-6) / 1e9, 2), "cpu_model": cpu,
             "gpu_vs_cpu_max_rel_err": err, "gpu_vs_cpu_topi_equal": bool(np.array_equal(b.topi.cpu().numpy(), oi))}
 

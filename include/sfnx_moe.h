@@ -143,6 +143,11 @@ int sfnx_q8s_gemv(const void* W, int rows, int cols, const void* y, float* out, 
 /* src/kernels.cu:1948-2024 swiglu_stacked_q8_1: hq row t ([T][ffs / 32] q8_1 blocks) = silu(gu[t][c]) * gu[t][ffs + c]
  * quantized per 32 values (d = amax / 127, q = round(v / d), ds = (f16 d, f16 sum)); gu is [T][2 ffs], ffs % 32 == 0 */
 int sfnx_swiglu_stacked_q8_1(const float* gu, void* hq, int ffs, int T, void* st);
+/* The shared expert's SwiGLU and dense Q8_0 down in one launch, as the reference fuses them into its routed gate|up
+ * launch (src/kernels.hpp:281-282 moe_gate_up's sh_down / sh_ffs / sh_gu / sh_out; src/dense.cuh:156-198): out[t][r] =
+ * W[r] . q8_1(silu(gu[t][0..ffs)) * gu[t][ffs..2 ffs)) for r < rows, t < T.  h never leaves the workgroup, so no
+ * buffer is needed for it; the values equal sfnx_swiglu_stacked_q8_1 followed by sfnx_q8s_gemv, bit for bit. */
+int sfnx_q8s_swiglu_gemv(const void* W, int rows, int ffs, const float* gu, float* out, int out_stride, int T, void* st);
 
 /* src/prefill.cu:407-417 pf_dense_xh (the prompt path's dense matrices, the shared expert's among them): out[c][r]
  * (row stride ldo) = sum_k f16(W[r][k]) xh[c][k] for C f16 rows xh [C][cols], fp32 accumulation.  W is a dense Q8_0

@@ -56,6 +56,7 @@ SIGNATURES = {
     "sfnx_pf_dense": (i32, [vp, i32, i32, vp, i32, vp, i32, vp, sz, vp]),
     "sfnx_hc_read": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, f32, vp, vp, vp, i32, i32, i32, i32, vp, sz, vp]),
     "sfnx_swiglu_stacked_q8_1": (i32, [vp, vp, i32, i32, vp]),
+    "sfnx_q8s_swiglu_gemv": (i32, [vp, i32, i32, vp, vp, i32, i32, vp]),
     "sfnx_gguf_type_info": (i32, [u32, vp, vp]),
     "sfnx_gguf_open": (i32, [C.c_char_p, vp]),
     "sfnx_gguf_close": (None, [vp]),

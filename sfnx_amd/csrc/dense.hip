@@ -14,7 +14,10 @@ namespace {
 
 constexpr int QS_THREADS = 256, QS_LPR = 32, QS_ROWS = QS_THREADS / QS_LPR, QS_TT = 4;
 
-// a block of QS_ROWS rows; the activation rows staged QS_TT at a time
+// a block of QS_ROWS rows; the activation rows staged QS_TT at a time: q8_1 rows y, or (SWIGLU) silu(gate) * up of the
+// f32 rows y = [T][gate (cols) | up (cols)] quantized to q8_1 as they are staged (the same values as
+// swiglu_stacked_q8_1's blocks, so the same sums as that call followed by q8s_gemv)
+template <bool SWIGLU>
 __global__ void __launch_bounds__(QS_THREADS) k_q8s_gemv(const uint8_t* __restrict__ W, int rows, int cols,
                                                         const uint8_t* __restrict__ y, float* __restrict__ out,
                                                         int out_stride, int T) {
@@ -25,7 +28,8 @@ __global__ void __launch_bounds__(QS_THREADS) k_q8s_gemv(const uint8_t* __restri
     for (int t0 = 0; t0 < T; t0 += QS_TT) {
         const int nn = min(QS_TT, T - t0);
         if (t0) __syncthreads();
-        stage_q8_1(a, y + (size_t) t0 * (cols / 32) * Q81_BYTES, nullptr, nn);
+        if constexpr (SWIGLU) stage_swiglu(a, reinterpret_cast<const float*>(y) + (size_t) t0 * 2 * cols, nullptr, nn);
+        else stage_q8_1(a, y + (size_t) t0 * (cols / 32) * Q81_BYTES, nullptr, nn);
         __syncthreads();
         for (int j = 0; j < nn; ++j) {
             const float v = group_sum<QS_LPR>(row < rows ? q8s_dot<QS_LPR>(P, row, cols, ln, a, j) : 0.f);
@@ -74,8 +78,23 @@ extern "C" int sfnx_q8s_gemv(const void* W, int rows, int cols, const void* y, f
         require(out_stride >= rows, "out_stride smaller than rows");
         const size_t lds = acts_bytes(QS_TT, cols);
         require(lds <= 64 * 1024, "cols too wide for the activation staging");
-        k_q8s_gemv<<<(rows + QS_ROWS - 1) / QS_ROWS, QS_THREADS, lds, stream_of(st)>>>(
+        k_q8s_gemv<false><<<(rows + QS_ROWS - 1) / QS_ROWS, QS_THREADS, lds, stream_of(st)>>>(
             (const uint8_t*) W, rows, cols, (const uint8_t*) y, out, out_stride, T);
+    });
+}
+
+extern "C" int sfnx_q8s_swiglu_gemv(const void* W, int rows, int ffs, const float* gu, float* out, int out_stride, int T,
+                                    void* st) {
+    return guarded("sfnx_q8s_swiglu_gemv", [&] {
+        require(W != nullptr && gu != nullptr && out != nullptr, "null pointer");
+        require(rows > 0 && rows % 32 == 0, "rows must be a positive multiple of 32");
+        require(ffs > 0 && ffs % 512 == 0, "ffs must be a positive multiple of 512");
+        require(T >= 1 && T <= 65535, "T out of range");
+        require(out_stride >= rows, "out_stride smaller than rows");
+        const size_t lds = acts_bytes(QS_TT, ffs);
+        require(lds <= 64 * 1024, "ffs too wide for the activation staging");
+        k_q8s_gemv<true><<<(rows + QS_ROWS - 1) / QS_ROWS, QS_THREADS, lds, stream_of(st)>>>(
+            (const uint8_t*) W, rows, ffs, (const uint8_t*) gu, out, out_stride, T);
     });
 }
 

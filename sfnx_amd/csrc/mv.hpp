@@ -55,13 +55,13 @@ __device__ inline void stage_q8_1(const Acts& a, const uint8_t* __restrict__ xq,
     }
 }
 
-// h = silu(gate) * up of gu rows ys[0..n) ([gate (K) | up (K)]) as q8_1 in LDS (k_moe_h, src/moe.cuh:284-295): a
-// half-wave per (row, 32 columns)
+// h = silu(gate) * up of gu rows ys[0..n) (rows 0..n-1 when ys is null; [gate (K) | up (K)]) as q8_1 in LDS (k_moe_h,
+// src/moe.cuh:284-295): a half-wave per (row, 32 columns)
 __device__ inline void stage_swiglu(const Acts& a, const float* __restrict__ gu, const int* ys, int n) {
     const int nb = a.K / 32, hw = threadIdx.x / 32, l = threadIdx.x % 32, nhw = blockDim.x / 32;
     for (int it = hw; it < n * nb; it += nhw) {
         const int j = it / nb, b = it % nb;
-        const float* g = gu + (size_t) ys[j] * 2 * a.K;
+        const float* g = gu + (size_t) (ys ? ys[j] : j) * 2 * a.K;
         const float xi = silu_f(g[32 * b + l]) * g[a.K + 32 * b + l];
         const float amax = group_max<32>(fabsf(xi));
         const float d = amax / 127.0f;

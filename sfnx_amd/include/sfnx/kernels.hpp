@@ -21,11 +21,21 @@ enum GgmlType : uint32_t {   // src/gguf.hpp:22-25
     T_Q4_0 = SFNX_Q4_0, T_Q5_1 = SFNX_Q5_1, T_Q8_0 = SFNX_Q8_0, T_Q4_K = SFNX_Q4_K, T_Q5_K = SFNX_Q5_K
 };
 
-// src/model.hpp:78-87 DW: one matrix (or expert 0's of a stack), n_out rows of n_in
+// src/model.hpp:72-75 Q8S: a dense Q8_0 matrix (here the planar Q8_0 layout of one matrix, in p)
+struct Q8S {
+    const void* p = nullptr;
+};
+
+// src/model.hpp:78-87 DW: one matrix (or expert 0's of a stack), n_out rows of n_in.  row_bytes and s are kept for
+// the reference's field list (row_bytes is derived from type and n_in here; s is the dense form of a matrix).  ep,
+// the per-expert pointer table of the reference's expert cache, is not supported: the calls refuse a DW that sets it.
 struct DW {
     const void* p = nullptr;
     uint32_t type = 0;
     int n_in = 0, n_out = 0;
+    size_t row_bytes = 0;
+    Q8S s;
+    const char* const* ep = nullptr;
 };
 
 // the sizes the reference compiles in
@@ -35,6 +45,20 @@ struct MoeShape {
     int K = 10;      // TOPK
 };
 
+// The reference fixes N, NEXP and TOPK at compile time (src/model.hpp:40-45), so its calls do not pass them.  The
+// overloads below that keep the reference's argument lists exactly read them from here: set once, before the first
+// call, as the reference's build fixes them.  (The overloads that take a MoeShape are the same calls with the shape
+// passed explicitly.)
+inline MoeShape& model_shape() {
+    static MoeShape s;
+    return s;
+}
+inline void set_model_shape(const MoeShape& s) { model_shape() = s; }
+
+// src/model.hpp:98-120 ExpertCache (routed experts kept in host RAM): not supported by this library; the calls that
+// take one refuse a non-null pointer
+struct ExpertCache;
+
 inline void ck(int status) {
     if (status != 0) throw std::runtime_error(sfnx_last_error());
 }
@@ -43,10 +67,6 @@ constexpr size_t q8_1_bytes(int n) { return (size_t) (n / 32) * 36; }   // src/k
 
 inline void quantize_q8_1(const float* x, void* q, int n, int rows, void* st) { ck(sfnx_quantize_q8_1(x, q, n, rows, st)); }
 
-// src/model.hpp:72-76 Q8S: a dense Q8_0 matrix (here the planar Q8_0 layout of one matrix)
-struct Q8S {
-    const void* p = nullptr;
-};
 
 // src/kernels.hpp:47 (src/dense.cuh:24-154): the shared expert's dense Q8_0 product in the reference's q8s sums
 inline void q8s_gemv(const Q8S& w, int rows, int cols, const void* y, float* out, int out_stride, int T, void* st) {
@@ -86,6 +106,63 @@ inline void moe_gate_up(const DW& A, size_t sa, const Job* jobs, const int* njob
         q8s_gemv(*sh_down, A.n_in, sh_ffs, sh_hq, sh_out, A.n_in, T, st);
     }
 }
+// ------------------------------------------------------------------------------------------------ the reference's
+// argument lists (src/kernels.hpp:276-305), N / NEXP / TOPK from model_shape().  As in the reference engine
+// (src/engine.cu:933-978) the shared expert is no routed job here: it is the dense Q8_0 matrices passed through the
+// sh_* arguments, and its rows are part rows T TOPK + t.
+namespace detail {
+inline void no_cache(const ExpertCache* ec, const DW* w = nullptr) {
+    if (ec != nullptr) throw std::runtime_error("expert cache (routed experts in host RAM) is not supported by sfnx_amd");
+    if (w != nullptr && w->ep != nullptr) throw std::runtime_error("DW::ep (per-expert pointer table) is not supported by sfnx_amd");
+}
+// the window's rows from the job grid's size, as the reference's moe_mm does (src/kernels.cu:1931)
+inline int rows_of(int njobs_max) {
+    const int T = njobs_max / model_shape().K;
+    return T < 1 ? 1 : (T > MAXT ? MAXT : T);
+}
+}  // namespace detail
+
+// src/kernels.hpp:276-278
+inline void router_route(const float* W, const float* x, float* logits, int T, int* topi, float* topw, Job* jobs_gu,
+                         Job* jobs_dn, int* njobs, void* st, const ExpertCache* ec = nullptr, int layer = -1,
+                         int* list = nullptr, const Q8S* sh_gu = nullptr, int sh_rows = 0, const void* sh_y = nullptr,
+                         float* sh_out = nullptr) {
+    (void) layer;
+    (void) list;
+    detail::no_cache(ec);
+    const MoeShape& s = model_shape();
+    ck(sfnx_router_route(W, x, logits, T, s.H, s.E, s.K, topi, topw, jobs_gu, jobs_dn, njobs, 0, st));
+    if (sh_gu) ck(sfnx_q8s_gemv(sh_gu->p, sh_rows, s.H, sh_y, sh_out, sh_rows, T, st));
+}
+// src/kernels.hpp:281-282: the shared expert's SwiGLU and down (sh_down: N rows of sh_ffs) from sh_gu ([T][2 sh_ffs])
+// into sh_out (row stride N), as the reference's fused launch computes them; T from njobs_max
+inline void moe_gate_up(const DW& A, size_t sa, const Job* jobs, const int* njobs, int njobs_max, const void* xq, float* gu,
+                        void* st, const Q8S* sh_down = nullptr, int sh_ffs = 0, const float* sh_gu = nullptr,
+                        float* sh_out = nullptr) {
+    detail::no_cache(nullptr, &A);
+    const int T = detail::rows_of(njobs_max);
+    ck(sfnx_moe_gate_up(A.p, sa, A.type, A.n_in, A.n_out, jobs, njobs, njobs_max, T, xq, gu, st));
+    if (sh_down) ck(sfnx_q8s_swiglu_gemv(sh_down->p, A.n_in, sh_ffs, sh_gu, sh_out, A.n_in, T, st));
+}
+// src/kernels.hpp:305
+inline void moe_down(const DW& A, size_t sa, const Job* jobs, const int* njobs, int njobs_max, const float* gu, float* part,
+                     void* st) {
+    detail::no_cache(nullptr, &A);
+    ck(sfnx_moe_down(A.p, sa, A.type, A.n_in, A.n_out, jobs, njobs, njobs_max, detail::rows_of(njobs_max), gu, part, st));
+}
+// src/kernels.hpp:290-292: the prompt path's matrix-core calls (moe_mma.cuh)
+inline void moe_gate_up_mma(const DW& A, size_t sa, const BigJob* jobs, const int* njobs, int njobs_cap, const uint16_t* xh,
+                            float* gu, void* st) {
+    detail::no_cache(nullptr, &A);
+    ck(sfnx_moe_gate_up_mma(A.p, sa, A.type, A.n_in, A.n_out, jobs, njobs, njobs_cap, xh, gu, st));
+}
+inline void swiglu_h16(const float* gu, int ffs, int P, uint16_t* h16, void* st) { ck(sfnx_swiglu_h16(gu, ffs, P, h16, st)); }
+inline void moe_down_mma(const DW& A, size_t sa, const BigJob* jobs, const int* njobs, int njobs_cap, const uint16_t* h16,
+                         float* part, void* st) {
+    detail::no_cache(nullptr, &A);
+    ck(sfnx_moe_down_mma(A.p, sa, A.type, A.n_in, A.n_out, jobs, njobs, njobs_cap, h16, part, st));
+}
+
 // src/kernels.hpp:284: jobs of up to MAXT rows each, njobs_cap of them at most (the prompt path's)
 inline void moe_gate_up_jobs(const DW& A, size_t sa, const Job* jobs, const int* njobs, int njobs_cap, const void* xq,
                              float* gu, void* st) {

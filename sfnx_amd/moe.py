@@ -129,6 +129,12 @@ def swiglu_stacked_q8_1(gu, hq, ffs: int, T: int) -> None:
     check(lib().sfnx_swiglu_stacked_q8_1(_p(gu), _p(hq), ffs, T, _st()))
 
 
+def q8s_swiglu_gemv(W, rows: int, ffs: int, gu, out, out_stride: int, T: int) -> None:
+    """src/kernels.hpp:281-282's shared-expert tail in one launch: out[t][r] = dense Q8_0 row r of W . q8_1 of
+    silu(gate) * up of gu row t ([gate | up], 2 ffs floats); equal to swiglu_stacked_q8_1 then q8s_gemv"""
+    check(lib().sfnx_q8s_swiglu_gemv(_p(W), rows, ffs, _p(gu), _p(out), out_stride, T, _st()))
+
+
 def residual_rmsnorm(x, y, xn, eps: float = 1e-6) -> None:
     """x += y (y may be None), xn = x / sqrt(mean(x^2) + eps): the glue between stacked layers"""
     T, H = x.shape

@@ -1,11 +1,17 @@
 // A decode window through one MoE layer from C++, the way the reference engine calls its MoE half
 // (src/engine.cu:933-978), through the C++ face over the C ABI (sfnx/kernels.hpp): quantize_q8_1, router_route,
-// moe_gate_up, moe_down and the combine; then the same window through the fused decode.  Twice: with the shared
-// expert as expert E of the stores, and as dense Q8_0 matrices through router_route's and moe_gate_up's shared-expert
-// arguments (the reference's fused-shexp calls).  Prints "ok" when the two paths agree bit for bit; exit status 1
-// otherwise.  Built by the package's build step; run by tests/test_gpu_cpp.py.
+// moe_gate_up, moe_down and the combine; then the same window through the fused decode.  Three times: with the shared
+// expert as expert E of the stores, as dense Q8_0 matrices through router_route's and moe_gate_up's shared-expert
+// arguments (the reference's fused-shexp calls), and the latter again through the overloads that keep the reference's
+// argument lists exactly (src/kernels.hpp:276-305; N, NEXP, TOPK from set_model_shape).  Then a prompt chunk through
+// the prompt path's calls under the reference's names (router_logits, pf_route, moe_gate_up_mma, swiglu_h16,
+// moe_down_mma, the combine): equal bit for bit to the fused gate|up + SwiGLU form, and near the int8 BigJob form.
+// Prints "ok" when every check holds; exit status 1 otherwise.  Built by the package's build step; run by
+// tests/test_gpu_cpp.py.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <vector>
@@ -40,7 +46,10 @@ void* synth_store(uint32_t type, int n_mat, int rows, int cols, uint64_t seed, u
     return p;
 }
 
-bool run(bool dense_shared) {
+// mode 0: shared expert as expert E; 1: dense Q8_0 through the MoeShape overloads; 2: dense Q8_0 through the
+// reference's exact argument lists
+bool run(int mode) {
+    const bool dense_shared = mode != 0;
     const MoeShape s{1024, 64, 6};
     const int ff = 512, T = 3, P = T * s.K, NP = P + T;
     const uint32_t type = T_Q4_K;
@@ -67,15 +76,22 @@ bool run(bool dense_shared) {
     float* y = dev<float>((size_t) T * s.H);
     uint8_t* hq = dev<uint8_t>(q8_1_bytes(ff) * T);
     quantize_q8_1(x, xq, s.H, T, nullptr);
-    if (dense_shared) {
+    if (mode == 2) {   // src/engine.cu:952-971, word for word but for the buffers' names
+        set_model_shape(s);
+        router_route(W, x, logits, T, topi, topw, jg, jd, nj, nullptr, nullptr, -1, nullptr, &sh_gu, 2 * ff, xq,
+                     gu + (size_t) P * 2 * ff);
+        moe_gate_up(gu_e, gu_stride, jg, nj, P, xq, gu, nullptr, &sh_dn, ff, gu + (size_t) P * 2 * ff, part + (size_t) P * s.H);
+        moe_down(dn_e, dn_stride, jd, nj, P, gu, part, nullptr);
+    } else if (dense_shared) {
         router_route(s, W, x, logits, T, topi, topw, jg, jd, nj, nullptr, &sh_gu, 2 * ff, xq, gu + (size_t) P * 2 * ff);
         moe_gate_up(gu_e, gu_stride, jg, nj, P + 1, xq, gu, nullptr, T, &sh_dn, ff, gu + (size_t) P * 2 * ff,
                     part + (size_t) P * s.H, hq);
+        moe_down(dn_e, dn_stride, jd, nj, P + 1, gu, part, nullptr, T);
     } else {
         router_route(s, W, x, logits, T, topi, topw, jg, jd, nj, nullptr);
         moe_gate_up(gu_e, gu_stride, jg, nj, P + 1, xq, gu, nullptr, T);
+        moe_down(dn_e, dn_stride, jd, nj, P + 1, gu, part, nullptr, T);
     }
-    moe_down(dn_e, dn_stride, jd, nj, P + 1, gu, part, nullptr, T);
     moe_combine(s, part, topw, topi, logits, y, T, nullptr);
     // the fused decode on a copy of x, norm off: x += y
     float* xf = dev<float>((size_t) T * s.H);
@@ -99,17 +115,88 @@ bool run(bool dense_shared) {
         const float want = hx[i] + hy[i];
         bad += std::memcmp(&want, &hf[i], 4) != 0;
     }
-    std::printf("%s shared expert: %zu of %zu values differ\n", dense_shared ? "dense Q8_0" : "expert E", bad, hx.size());
+    static const char* names[3] = {"expert E", "dense Q8_0", "dense Q8_0, the reference's argument lists"};
+    std::printf("%s shared expert: %zu of %zu values differ\n", names[mode], bad, hx.size());
     return bad == 0;
+}
+
+std::vector<float> host(const float* d, size_t n) {
+    std::vector<float> h(n);
+    hk(hipMemcpy(h.data(), d, n * 4, hipMemcpyDeviceToHost), "copy");
+    return h;
+}
+
+// A prompt chunk of C tokens (src/prefill.cu:1145-1180) through the reference-named prompt calls
+bool run_prompt() {
+    const MoeShape s{1024, 64, 6};
+    const int ff = 512, C = 96, P = C * s.K, NP = P + C;
+    const uint32_t type = T_Q4_K;
+    const size_t gu_stride = 2 * (size_t) ff * sfnx_row_bytes(type, s.H), dn_stride = (size_t) s.H * sfnx_row_bytes(type, ff);
+    float* W = dev<float>((size_t) (s.E + 1) * s.H);
+    ck(sfnx_synth_normal(W, (size_t) (s.E + 1) * s.H, 21, 0, 0.02f, nullptr));
+    const DW gu_e{synth_store(type, s.E + 1, 2 * ff, s.H, 22, 0), type, s.H, 2 * ff};
+    const DW dn_e{synth_store(type, s.E + 1, s.H, ff, 23, 0), type, ff, s.H};
+    float* x = dev<float>((size_t) C * s.H);
+    ck(sfnx_synth_normal(x, (size_t) C * s.H, 24, 0, 1.0f, nullptr));
+    const int cap = P / 64 + s.E + (C + 63) / 64 + 1;
+    float* logits = dev<float>((size_t) C * (s.E + 1));
+    int* topi = dev<int>(P);
+    float* topw = dev<float>(P);
+    int* cnt = dev<int>(s.E);
+    int* jbase = dev<int>(s.E);
+    BigJob* jg = dev<BigJob>(cap);
+    BigJob* jd = dev<BigJob>(cap);
+    int* nj = dev<int>(2);
+    uint16_t* xh = dev<uint16_t>((size_t) C * s.H);
+    float* gu = dev<float>((size_t) NP * 2 * ff);
+    uint16_t* h16 = dev<uint16_t>((size_t) NP * ff);
+    uint16_t* h16f = dev<uint16_t>((size_t) NP * ff);
+    float* part = dev<float>((size_t) NP * s.H);
+    float* y1 = dev<float>((size_t) C * s.H);
+    float* y2 = dev<float>((size_t) C * s.H);
+    float* y3 = dev<float>((size_t) C * s.H);
+    uint8_t* xq = dev<uint8_t>(q8_1_bytes(s.H) * C);
+    router_logits(W, x, logits, C, s.H, s.E + 1, nullptr);
+    pf_route(s, logits, C, topi, topw, cnt, jbase, jg, jd, nj, nullptr);
+    ck(sfnx_to_f16(x, xh, (size_t) C * s.H, nullptr));
+    // src/prefill.cu:1167-1171 as the reference writes it
+    moe_gate_up_mma(gu_e, gu_stride, jg, nj, cap, xh, gu, nullptr);
+    swiglu_h16(gu, ff, NP, h16, nullptr);
+    moe_down_mma(dn_e, dn_stride, jd, nj, cap, h16, part, nullptr);
+    moe_combine(s, part, topw, topi, logits, y1, C, nullptr);
+    // the fused gate|up + SwiGLU form
+    ck(sfnx_moe_gate_up_swiglu_mma(gu_e.p, gu_stride, type, s.H, ff, jg, nj, cap, xh, h16f, nullptr));
+    moe_down_mma(dn_e, dn_stride, jd, nj, cap, h16f, part, nullptr);
+    moe_combine(s, part, topw, topi, logits, y2, C, nullptr);
+    // the int8 BigJob form (FNX_PF_MOE_Q8)
+    quantize_q8_1(x, xq, s.H, C, nullptr);
+    moe_gate_up_big(gu_e, gu_stride, jg, nj, cap, xq, gu, nullptr);
+    moe_down_big(dn_e, dn_stride, jd, nj, cap, gu, part, nullptr);
+    moe_combine(s, part, topw, topi, logits, y3, C, nullptr);
+    hk(hipDeviceSynchronize(), "sync");
+    const size_t n = (size_t) C * s.H;
+    const std::vector<float> a = host(y1, n), b = host(y2, n), c = host(y3, n);
+    size_t bad = 0;
+    double dmax = 0, amax = 0;
+    for (size_t i = 0; i < n; ++i) {
+        bad += std::memcmp(&a[i], &b[i], 4) != 0;
+        dmax = std::max(dmax, (double) std::fabs(a[i] - c[i]));
+        amax = std::max(amax, (double) std::fabs(c[i]));
+    }
+    const double rel = dmax / amax;
+    std::printf("prompt chunk of %d: fused gate|up+SwiGLU differs in %zu of %zu values; f16 vs int8 path max rel %.3g\n", C,
+                bad, n, rel);
+    return bad == 0 && rel < 5e-2;
 }
 
 }  // namespace
 
 int main() {
     try {
-        const bool a = run(false), b = run(true);
-        std::printf("%s\n", a && b ? "ok" : "MISMATCH");
-        return a && b ? 0 : 1;
+        const bool a = run(0), b = run(1), c = run(2), d = run_prompt();
+        const bool ok = a && b && c && d;
+        std::printf("%s\n", ok ? "ok" : "MISMATCH");
+        return ok ? 0 : 1;
     } catch (const std::exception& e) {
         std::printf("error: %s\n", e.what());
         return 2;

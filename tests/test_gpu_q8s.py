@@ -74,6 +74,23 @@ def test_swiglu_stacked_q8_1(ffs):
     assert (blk[2, 0] == 0).all()
 
 
+@pytest.mark.parametrize("ffs, T", [(512, 1), (512, 16), (1024, 5)])
+def test_q8s_swiglu_gemv_equals_two_calls(ffs, T):
+    """the shared expert's SwiGLU and down in one launch (the reference's moe_gate_up sh_down arguments) equals
+    swiglu_stacked_q8_1 followed by q8s_gemv, bit for bit"""
+    rows = 2048
+    _, W = q8_0_matrix(rows, ffs, 90 + ffs + T)
+    gu = torch.from_numpy(orc.synth(T * 2 * ffs, 91 + T, 1.0).reshape(T, 2 * ffs)).cuda()
+    hq = torch.empty(T * ffs // 32 * 36, dtype=torch.uint8, device="cuda")
+    a = torch.full((T, rows), 3.0, dtype=torch.float32, device="cuda")
+    b = torch.full((T, rows), 5.0, dtype=torch.float32, device="cuda")
+    moe.swiglu_stacked_q8_1(gu, hq, ffs, T)
+    moe.q8s_gemv(W, rows, ffs, hq, a, rows, T)
+    moe.q8s_swiglu_gemv(W, rows, ffs, gu, b, rows, T)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(a), bits(b))
+
+
 @pytest.mark.parametrize("wtype", [orc.Q4_K, orc.Q8_0, orc.Q4_0])
 @pytest.mark.parametrize("T", [1, 3, 16])
 def test_unfused_layer_q8s_vs_oracle(wtype, T):
