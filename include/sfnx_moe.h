@@ -177,12 +177,14 @@ typedef struct sfnx_moe_layer_w {
 size_t sfnx_moe_decode_workspace(int T, int H, int E, int K, int ff, size_t* offsets);
 
 /* A decode window (1 <= T <= 16 rows) through n_layers stacked MoE layers, replacing the engine's per-layer calls
- * router_route + moe_gate_up + moe_down + the combine (src/engine.cu:933-978, src/kernels.hpp:269-313) with three
- * launches a layer (four for T > 1: the routing once, in a launch of its own, before gate|up).  x [T][H] is the residual stream, updated in place: per layer x += MoE(norm ? rmsnorm(x) : x)
- * (rmsnorm as sfnx_residual_rmsnorm).  The workspace keeps the last layer's routing and intermediates (see
+ * router_route + moe_gate_up + moe_down + the combine (src/engine.cu:933-978, src/kernels.hpp:269-313).  x [T][H] is
+ * the residual stream, updated in place: per layer x += MoE(norm ? rmsnorm(x) : x) (rmsnorm as
+ * sfnx_residual_rmsnorm).  The workspace keeps the last layer's routing and intermediates (see
  * sfnx_moe_decode_workspace).  Same arithmetic, value for value, as the unfused entry points.  H in {1024, 2048,
- * 2560, 4096}, ff in {512, 1024}.  phases: 0 runs everything; otherwise a mask of the launches to issue per layer
- * (1 router, 2 routing (T > 1) and gate|up, 4 down + combine), for timing each one alone. */
+ * 2560, 4096}, ff in {512, 1024}.
+ * Three launches a layer (four for T > 1: the routing once, in a launch of its own, before gate|up).
+ * phases: 0 runs everything; otherwise a mask of the launches to issue per layer (1 router, 2 routing (T > 1) and
+ * gate|up, 4 down + combine), for timing each one alone. */
 int sfnx_moe_decode(const sfnx_moe_layer_w* layers, int n_layers, uint32_t type, int H, int E, int K, int ff, int shared,
                     float* x, int T, int norm, float eps, void* ws, size_t ws_bytes, int phases, void* st);
 /* sfnx_moe_decode with the gate|up and down matrices of different types, as the reference keeps a type per matrix

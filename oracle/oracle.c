@@ -34,8 +34,8 @@ float orc_f16_to_f32(uint16_t h) {
 static uint16_t f16_round(int neg, unsigned __int128 mag, int e) {
     const uint16_t sg = neg ? 0x8000u : 0u;
     if (mag == 0) return sg;
-    int hb = 127;
-    while (!((mag >> hb) & 1)) --hb;
+    const uint64_t hi = (uint64_t) (mag >> 64), lo = (uint64_t) mag;
+    const int hb = hi ? 127 - __builtin_clzll(hi) : 63 - __builtin_clzll(lo);   /* the highest set bit */
     int q = hb + e - 10;   /* exponent of the result's last mantissa bit */
     if (q < -24) q = -24;
     const int shift = q - e;
@@ -302,6 +302,7 @@ static void dequant_b32(const void* src, float* y, int64_t rows, int cols, int t
 /* f16: Q4_0 hmul2(q - 8, d); Q5_1 hfma2(q, d, m), src/moe_mma.cuh:137-173 */
 static void dequant_b32_f16(const void* src, uint16_t* y, int64_t rows, int cols, int type) {
     const int64_t nblk = rows * (cols / 32);
+#pragma omp parallel for schedule(static)
     for (int64_t k = 0; k < nblk; ++k) {
         const uint8_t* p = (const uint8_t*) src + k * b32_bytes(type);
         uint16_t dh, mh;
@@ -345,6 +346,7 @@ static void dequant_kq(const void* src, float* y, int64_t rows, int cols, int q5
 static void dequant_kq_f16(const void* src, uint16_t* y, int64_t rows, int cols, int q5) {
     const int64_t nblk = rows * (cols / 256);
     const size_t bb = q5 ? ORC_Q5K_BYTES : ORC_Q4K_BYTES;
+#pragma omp parallel for schedule(static)
     for (int64_t k = 0; k < nblk; ++k) {
         const uint8_t* p = (const uint8_t*) src + k * bb;
         uint16_t dh, mh;
@@ -381,6 +383,7 @@ void orc_dequant_q8_0(const void* src, float* y, int64_t rows, int cols) {
 
 void orc_dequant_q8_0_f16(const void* src, uint16_t* y, int64_t rows, int cols) {
     const int64_t nblk = rows * (cols / 32);
+#pragma omp parallel for schedule(static)
     for (int64_t k = 0; k < nblk; ++k) {
         const uint8_t* p = (const uint8_t*) src + k * ORC_Q80_BYTES;
         uint16_t dh;
@@ -760,19 +763,21 @@ void orc_layer_decode(const orc_layer* L, const float* x, int T, float* y, float
 
 /* ------------------------------------------------------------------------------------------------ f16 path */
 void orc_mma_matvec(const uint8_t* w, int type, int n_in, int n_out, const uint16_t* x16, double* out) {
-    uint16_t* row = (uint16_t*) malloc((size_t) n_in * 2);
-    const size_t rb = row_bytes(type, n_in);
+    /* the whole matrix dequantized at once (the dequantizers split rows over threads), then one float64 sum a row */
+    uint16_t* m = (uint16_t*) malloc((size_t) n_in * n_out * 2);
+    if (type == ORC_Q4_K) orc_dequant_q4_k_f16(w, m, n_out, n_in);
+    else if (type == ORC_Q5_K) orc_dequant_q5_k_f16(w, m, n_out, n_in);
+    else if (type == ORC_Q4_0) orc_dequant_q4_0_f16(w, m, n_out, n_in);
+    else if (type == ORC_Q5_1) orc_dequant_q5_1_f16(w, m, n_out, n_in);
+    else orc_dequant_q8_0_f16(w, m, n_out, n_in);
+#pragma omp parallel for schedule(static)
     for (int r = 0; r < n_out; ++r) {
-        if (type == ORC_Q4_K) orc_dequant_q4_k_f16(w + (size_t) r * rb, row, 1, n_in);
-        else if (type == ORC_Q5_K) orc_dequant_q5_k_f16(w + (size_t) r * rb, row, 1, n_in);
-        else if (type == ORC_Q4_0) orc_dequant_q4_0_f16(w + (size_t) r * rb, row, 1, n_in);
-        else if (type == ORC_Q5_1) orc_dequant_q5_1_f16(w + (size_t) r * rb, row, 1, n_in);
-        else orc_dequant_q8_0_f16(w + (size_t) r * rb, row, 1, n_in);
+        const uint16_t* row = m + (size_t) r * n_in;
         double s = 0.0;
         for (int k = 0; k < n_in; ++k) s += (double) orc_f16_to_f32(row[k]) * (double) orc_f16_to_f32(x16[k]);
         out[r] = s;
     }
-    free(row);
+    free(m);
 }
 
 void orc_swiglu_h16(const float* gu, int ff, uint16_t* h16) {

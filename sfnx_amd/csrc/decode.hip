@@ -12,8 +12,7 @@
 // The arithmetic of every value is the unfused entry points' (router_route, moe_gate_up, moe_down, moe_combine), so the
 // two paths agree bit for bit.
 #include <hip/hip_ext.h>
-#include "mv.hpp"
-#include "topk.hpp"
+#include "decode.hpp"
 
 namespace sfnx {
 namespace {
@@ -22,40 +21,7 @@ namespace {
 constexpr int D1_THREADS = 64, D1_WAVES = D1_THREADS / WAVE;   // K1: a router row per wavefront
 constexpr int D3_THREADS = 256, D3_ROWS = 8;                    // K3: output rows per block
 constexpr int D3W_THREADS = 512;                                 // K3 for windows of several rows
-template <int TYPE> constexpr int lpr_of() { return is_kquant(TYPE) ? 8 : 16; }
 template <int TYPE> constexpr int d2_threads() { return 32 * lpr_of<TYPE>(); }   // K2: 32 FF indices a block
-
-struct DecLayout {
-    size_t logits, xq, topi, topw, jg, jd, njobs, gu, hq_q, hq_d, hq_s, y, route_x, total;
-};
-// Every piece is laid out for the largest window (SFNX_MAXT rows), so the offsets are the same whatever T a call
-// runs: a workspace sized once serves windows of any size, and a piece's row t always starts at t times its row size.
-DecLayout dec_layout(int H, int E, int K, int ff) {
-    constexpr int T = SFNX_MAXT;
-    const size_t P = (size_t) T * K, NP = P + T, nj = P + 1;
-    size_t o = 0;
-    auto take = [&](size_t bytes) {
-        const size_t r = o;
-        o += (bytes + 255) / 256 * 256;
-        return r;
-    };
-    DecLayout L;
-    L.logits = take((size_t) T * (E + 1) * 4);
-    L.xq = take((size_t) T * (H / 32) * Q81_BYTES);
-    L.topi = take(P * 4);
-    L.topw = take(P * 4);
-    L.jg = take(nj * sizeof(sfnx_job));
-    L.jd = take(nj * sizeof(sfnx_job));
-    L.njobs = take(8);
-    L.gu = take(NP * 2 * ff * 4);
-    L.hq_q = take(NP * ff);
-    L.hq_d = take(NP * (ff / 32) * 4);
-    L.hq_s = take(NP * (ff / 32) * 4);
-    L.y = take((size_t) T * H * 4);
-    L.route_x = take((size_t) XCDS * 2 * MAX_K * 4);   // batch 1: the picks and weights, a copy an XCD
-    L.total = o;
-    return L;
-}
 
 // ------------------------------------------------------------------------------------------------ K1
 template <int NC, int TT>
@@ -136,53 +102,6 @@ __global__ void __launch_bounds__(D1_THREADS) k_dec_router(const float* __restri
 }
 
 // ------------------------------------------------------------------------------------------------ K2
-template <int TYPE, int G> struct RowOf;
-template <int G> struct RowOf<SFNX_Q4_K, G> {
-    using R = Q4kRow<G>;
-    static __device__ __forceinline__ void load(R& w, const uint8_t* mat, int nrows, int row, int C, int ln) {
-        w.load(q4k_planes(mat, nrows, C), row, C, ln);
-    }
-    static __device__ __forceinline__ void issue(R& w, const uint8_t* mat, int nrows, int row, int C, int ln) {
-        w.issue(q4k_planes(mat, nrows, C), row, C, ln);
-    }
-};
-template <int G> struct RowOf<SFNX_Q5_K, G> {
-    using R = Q4kRow<G, true>;
-    static __device__ __forceinline__ void load(R& w, const uint8_t* mat, int nrows, int row, int C, int ln) {
-        w.load(q5k_planes(mat, nrows, C), row, C, ln);
-    }
-    static __device__ __forceinline__ void issue(R& w, const uint8_t* mat, int nrows, int row, int C, int ln) {
-        w.issue(q5k_planes(mat, nrows, C), row, C, ln);
-    }
-};
-template <int G> struct RowOf<SFNX_Q4_0, G> {
-    using R = NbRow<G, SFNX_Q4_0>;
-    static __device__ __forceinline__ void load(R& w, const uint8_t* mat, int nrows, int row, int C, int ln) {
-        w.load(nb_planes<SFNX_Q4_0>(mat, nrows, C), row, C, ln);
-    }
-    static __device__ __forceinline__ void issue(R& w, const uint8_t* mat, int nrows, int row, int C, int ln) {
-        w.issue(nb_planes<SFNX_Q4_0>(mat, nrows, C), row, C, ln);
-    }
-};
-template <int G> struct RowOf<SFNX_Q5_1, G> {
-    using R = NbRow<G, SFNX_Q5_1>;
-    static __device__ __forceinline__ void load(R& w, const uint8_t* mat, int nrows, int row, int C, int ln) {
-        w.load(nb_planes<SFNX_Q5_1>(mat, nrows, C), row, C, ln);
-    }
-    static __device__ __forceinline__ void issue(R& w, const uint8_t* mat, int nrows, int row, int C, int ln) {
-        w.issue(nb_planes<SFNX_Q5_1>(mat, nrows, C), row, C, ln);
-    }
-};
-template <int G> struct RowOf<SFNX_Q8_0, G> {
-    using R = Q80Row<G>;
-    static __device__ __forceinline__ void load(R& w, const uint8_t* mat, int nrows, int row, int C, int ln) {
-        w.load(q80_planes(mat, nrows, C), row, C, ln);
-    }
-    static __device__ __forceinline__ void issue(R& w, const uint8_t* mat, int nrows, int row, int C, int ln) {
-        w.issue(q80_planes(mat, nrows, C), row, C, ln);
-    }
-};
-
 // K1b for windows of several rows: the routing once (the top-k of every row, a wavefront a row, then the decode job
 // numbering of src/moe.cuh:164-198), published for K2, K3 and the caller.  At batch 1, K2's blocks take the top-k
 // themselves (k_dec_experts1); with more rows each block would repeat every row's top-k and the numbering.

@@ -32,7 +32,7 @@ __device__ __forceinline__ Acts acts_in(unsigned char* lds, int TT, int K) {
     a.K = K;
     return a;
 }
-inline size_t acts_bytes(int TT, int K) { return (size_t) TT * K + (size_t) TT * (K / 32) * 8; }
+__host__ __device__ inline size_t acts_bytes(int TT, int K) { return (size_t) TT * K + (size_t) TT * (K / 32) * 8; }
 
 // rows ys[0..n) (rows 0..n-1 when ys is null) of q8_1 activations (36-byte blocks) into LDS: a thread per (row, block)
 __device__ inline void stage_q8_1(const Acts& a, const uint8_t* __restrict__ xq, const int* ys, int n) {
@@ -83,7 +83,8 @@ template <int GPL, bool Q5 = false> struct Q4kRow {
     uint4 qh0[Q5 ? GPL : 1], qh1[Q5 ? GPL : 1];
     float d[GPL], dmin[GPL], sc0[GPL], m0[GPL], sc1[GPL], m1[GPL];
     // the loads alone (issue several rows' before any prepare, so that their latencies overlap)
-    __device__ __forceinline__ void issue(const Q4kPlanes& P, int row, int C, int l8) {
+    // P: the planar store's planes (Q4kPlanes), or any view with the same accessors (one row staged in LDS)
+    template <typename PL> __device__ __forceinline__ void issue(const PL& P, int row, int C, int l8) {
 #pragma unroll
         for (int i = 0; i < GPL; ++i) {
             q0[i] = *reinterpret_cast<const uint4*>(P.nib16(row, C, 16 * i + l8));
@@ -163,7 +164,7 @@ template <int BPL> struct Q80Row {
     uint4 qa[BPL], qb[BPL];
     uint16_t dh[BPL];
     float dw[BPL];
-    __device__ __forceinline__ void issue(const Q80Planes& P, int row, int C, int l16) {
+    template <typename PL> __device__ __forceinline__ void issue(const PL& P, int row, int C, int l16) {
 #pragma unroll
         for (int i = 0; i < BPL; ++i) {
             qa[i] = *reinterpret_cast<const uint4*>(P.q16(row, C, 32 * i + l16));
@@ -217,7 +218,7 @@ template <int BPL, int TYPE> struct NbRow {
     uint32_t sv[BPL];   // Q4_0: f16 d (low half); Q5_1: f16 d | f16 m << 16
     uint32_t qh[TYPE == SFNX_Q5_1 ? BPL : 1];
     float dw[BPL], mw[BPL];
-    __device__ __forceinline__ void issue(const NbPlanes& P, int row, int C, int l16) {
+    template <typename PL> __device__ __forceinline__ void issue(const PL& P, int row, int C, int l16) {
 #pragma unroll
         for (int i = 0; i < BPL; ++i) {
             const int b = l16 + 16 * i;

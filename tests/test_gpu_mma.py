@@ -24,6 +24,24 @@ def expert_rows(host, e, down):
     return host.gu_w[e * host.gu_stride:(e + 1) * host.gu_stride], rb
 
 
+class F16Experts:
+    """an expert's matrices dequantized to f16 (the oracle's f16 dequantization, src/moe_mma.cuh:56-62 and 121-216),
+    held as float64 for the float64 products; the last expert's only (callers visit each expert's work together)"""
+
+    def __init__(self, host):
+        self.host, self.cache = host, {}
+
+    def __call__(self, e, down):
+        k = (e, down)
+        if k not in self.cache:
+            self.cache = {c: v for c, v in self.cache.items() if c[0] == e}
+            h = self.host
+            w, _ = expert_rows(h, e, down)
+            t, rows, cols = (h.dn_type, h.H, h.ff) if down else (h.type, 2 * h.ff, h.H)
+            self.cache[k] = orc.dequant_f16(t, w, rows, cols).view(np.float16).astype(np.float64).reshape(rows, cols)
+        return self.cache[k]
+
+
 def run_prefill(shape, seed, C, dup=False, bias=None):
     L, host = make_layer(shape, seed)
     x = orc.synth(C * shape.H, seed + 7, 1.0).reshape(C, shape.H)
@@ -48,18 +66,17 @@ def check_sampled(host, x, b, nsample, rng):
     part = b.part.cpu().numpy()
     x16 = f16_of(x)
     eg, mg, ed, md = 0.0, 0.0, 0.0, 0.0
-    for _ in range(nsample):
-        p = int(rng.integers(0, P + C))
+    f16w = F16Experts(host)
+    ps = [int(p) for p in rng.integers(0, P + C, nsample)]
+    for p in sorted(ps, key=lambda p: int(topi.reshape(-1)[p]) if p < P else s.E):   # each expert's samples together
         if p < P:
             e, t = int(topi.reshape(-1)[p]), p // K
         else:
             e, t = s.E, p - P
-        w, rb = expert_rows(host, e, False)
-        ref = orc.mma_matvec(s.type, w, s.H, 2 * s.ff, x16[t].view(np.uint16))
+        ref = f16w(e, False) @ x16[t].astype(np.float64)
         mg = max(mg, np.abs(ref).max())
         eg = max(eg, np.abs(ref - gu[p]).max())
-        wd, _ = expert_rows(host, e, True)
-        refd = orc.mma_matvec(s.dn_type, wd, s.ff, s.H, h16[p].view(np.uint16))
+        refd = f16w(e, True) @ h16[p].astype(np.float64)
         md = max(md, np.abs(refd).max())
         ed = max(ed, np.abs(refd - part[p]).max())
         # h16 is f16(silu(g) u) of the kernel's own gate|up row
@@ -87,15 +104,70 @@ def test_mma_small_layer_with_full_jobs(wtype):
     assert max_rel(y, want) < 1e-5
 
 
+def layer_rows_f64(host, shape, x16, lg, oi, ow, rows):
+    """float64 restatement of the f16 layer for the given tokens: per pick (and the shared expert), the f16 weights
+    times the f16 activations (float64 sums), f16(silu(g) u), the f16 down weights times that, weighted by the routing"""
+    out = np.zeros((len(rows), shape.H))
+    f16w = F16Experts(host)
+    work = []
+    for i, t in enumerate(rows):
+        picks = [(int(e), float(w)) for e, w in zip(oi[t], ow[t]) if e >= 0]
+        picks.append((shape.E, 1 / (1 + np.exp(-float(lg[t, shape.E])))))
+        work += [(e, w, i, t) for e, w in picks]
+    for e, w, i, t in sorted(work):   # each expert dequantized once
+        gu = f16w(e, False) @ x16[t].astype(np.float64)
+        hh = orc.swiglu_h16(gu.astype(np.float32), shape.ff).view(np.float16).astype(np.float64)
+        out[i] += w * (f16w(e, True) @ hh)
+    return out
+
+
+def check_prompt_routing(b, logits, shape):
+    """the prompt path's top-k and BigJobs against the oracle's on the same logits, exactly"""
+    E, K = shape.E, shape.K
+    oi, ow, _ = orc.topk(logits, E, K)
+    assert np.array_equal(b.topi.cpu().numpy(), oi)
+    assert np.allclose(b.topw.cpu().numpy(), ow, rtol=1e-6, atol=1e-7)
+    ocnt, ojb, ogu, odn = orc.jobs_prefill(oi, K, E, shape.shared)
+    assert np.array_equal(b.cnt.cpu().numpy(), ocnt) and np.array_equal(b.jbase.cpu().numpy(), ojb)
+    n = int(b.njobs[0])
+    assert n == len(ogu)
+    g, d = job_array(b.jobs_gu, True)[:n], job_array(b.jobs_dn, True)[:n]
+    for j in range(n):
+        c = ogu[j]["n"]
+        assert (g[j]["w"], g[j]["n"], d[j]["w"], d[j]["n"]) == (ogu[j]["w"], c, odn[j]["w"], c)
+        for f in ("y", "out"):
+            assert np.array_equal(g[j][f][:c], ogu[j][f][:c]) and np.array_equal(d[j][f][:c], odn[j][f][:c])
+    return oi, ow
+
+
 def test_mma_baseline_prefill_shape():
-    """The benchmark prefill shape (config 3): 2048 tokens, hidden 2048, 512 experts x FF 512, top-10 + shared, Zipf-skewed routing"""
+    """The benchmark prefill shape (config 3): 2048 tokens, hidden 2048, 512 experts x FF 512, top-10 + shared,
+    Zipf-skewed routing.  The router logits bit for bit and the top-k and BigJobs exactly against the oracle on the
+    biased logits; 400 sampled (pair, gate|up row set) and (pair, down row set) products within 2e-3 of float64 (the
+    sample size of tools/moe_mma_bench.cu:197-220); the whole layer (fused gate|up + SwiGLU, down, combine) for 64
+    tokens within 2e-3 of its float64 restatement"""
     shape = moe.LayerShape(H=2048, E=512, K=10, ff=512, wtype=orc.Q4_K, shared=True)
     rank = np.random.default_rng(7).permutation(512) + 1
     bias = (0.125 * -1.1 * np.log(rank)).astype(np.float32)
     L, host, x, y, b = run_prefill(shape, 3, 2048, bias=bias)
     assert 150 < int(b.cnt.max()) < 260
-    eg, ed = check_sampled(host, x, b, 24, np.random.default_rng(2))
+    lg = orc.router_logits(host.W, x)
+    got_lg = b.logits.cpu().numpy()
+    lg_biased = lg.copy()
+    lg_biased[:, : shape.E] += bias
+    assert np.array_equal(got_lg.view(np.uint32), lg_biased.view(np.uint32))
+    oi, ow = check_prompt_routing(b, lg_biased, shape)
+    eg, ed = check_sampled(host, x, b, 400, np.random.default_rng(2))
     assert eg < 2e-3 and ed < 2e-3, (eg, ed)
+    # the whole layer as the prompt path runs it
+    xd = torch.from_numpy(x).cuda()
+    yl = torch.empty_like(xd)
+    b2 = moe.PrefillBuffers(shape, 2048)
+    moe.prefill_layer_mma(L, xd, yl, b2, torch.from_numpy(bias).cuda())
+    torch.cuda.synchronize()
+    rows = list(np.random.default_rng(5).choice(2048, 64, replace=False))
+    want = layer_rows_f64(host, shape, f16_of(x), lg_biased, oi, ow, rows)
+    assert max_rel(yl.cpu().numpy()[rows], want) < 2e-3
 
 
 @pytest.mark.parametrize("wtype", [orc.Q4_K, orc.Q5_K, orc.Q4_0, orc.Q5_1, orc.Q8_0])
@@ -112,8 +184,8 @@ def test_gate_up_swiglu_fused_equals_two_calls(wtype):
 
 
 def test_verify_window_whole_layer():
-    """config 2's shape: 96 rows through the whole layer on the prompt path (fused gate|up + SwiGLU), against the
-    combine of float64 products sampled per pair and the oracle's routing"""
+    """config 2's shape: 96 rows through the whole layer on the prompt path (fused gate|up + SwiGLU): routing and
+    BigJobs against the oracle exactly, and every one of the 96 rows against the float64 restatement of the f16 layer"""
     shape = moe.LayerShape(H=2048, E=512, K=10, ff=512, wtype=orc.Q4_K, shared=True)
     L, host = make_layer(shape, 11)
     C = 96
@@ -124,20 +196,12 @@ def test_verify_window_whole_layer():
     moe.prefill_layer_mma(L, xd, y, b)
     torch.cuda.synchronize()
     lg = orc.router_logits(host.W, x)
-    oi, ow, _ = orc.topk(lg, shape.E, shape.K)
-    assert np.array_equal(b.topi.cpu().numpy(), oi)
-    x16 = f16_of(x)
+    assert np.array_equal(b.logits.cpu().numpy().view(np.uint32), lg.view(np.uint32))
+    oi, ow = check_prompt_routing(b, lg, shape)
     yo = y.cpu().numpy()
-    for t in (0, 37, 95):
-        want = np.zeros(shape.H)
-        picks = [(int(e), float(w)) for e, w in zip(oi[t], ow[t])] + [(shape.E, 1 / (1 + np.exp(-float(lg[t, shape.E]))))]
-        for e, w in picks:
-            wg, _ = expert_rows(host, e, False)
-            gu = orc.mma_matvec(shape.wtype, wg, shape.H, 2 * shape.ff, x16[t].view(np.uint16))
-            hh = orc.swiglu_h16(gu.astype(np.float32), shape.ff)
-            wd, _ = expert_rows(host, e, True)
-            want += w * orc.mma_matvec(shape.wtype, wd, shape.ff, shape.H, hh)
-        assert np.abs(yo[t] - want).max() <= 2e-3 * np.abs(want).max(), t
+    want = layer_rows_f64(host, shape, f16_of(x), lg, oi, ow, range(C))
+    for t in range(C):
+        assert np.abs(yo[t] - want[t]).max() <= 2e-3 * np.abs(want[t]).max(), t
 
 
 def test_q8_0_prefill_4096_sampled():
