@@ -194,6 +194,15 @@ int sfnx_moe_decode2(const sfnx_moe_layer_w* layers, int n_layers, uint32_t gu_t
                      int K, int ff, int shared, float* x, int T, int norm, float eps, void* ws, size_t ws_bytes, int phases,
                      void* st);
 
+/* No counterpart in the reference: sfnx_moe_decode2 for callers that cannot allocate (code under HIP graph capture,
+ * serving loops, harnesses that forbid hipMalloc).  The workspace is the library's own file-scope device array of
+ * 4 MiB, one per GPU, held until the process ends; the call allocates nothing and refuses a shape whose workspace
+ * (sfnx_moe_decode_workspace) is larger.  Every call on one GPU shares that array, and the array keeps the last call's
+ * routing and intermediates (nothing in it needs to start at zero): calls that overlap on one GPU (several streams,
+ * several host threads) race.  Same arguments and values as sfnx_moe_decode2 without ws / ws_bytes / phases. */
+int sfnx_moe_decode_noalloc(const sfnx_moe_layer_w* layers, int n_layers, uint32_t gu_type, uint32_t dn_type, int H, int E,
+                            int K, int ff, int shared, float* x, int T, int norm, float eps, void* st);
+
 /* A layer's shared expert as its own dense Q8_0 matrices, as the reference holds it (src/model.hpp:72-83 Q8S,
  * src/model.cpp:384-440 q8split: LayerW::sh_gu, sh_down): gu [2 ff][H] and dn [H][ff], each in the planar Q8_0 layout
  * of sfnx_store_pack (one matrix). */

@@ -49,6 +49,7 @@ SIGNATURES = {
     "sfnx_to_f16": (i32, [vp, vp, sz, vp]),
     "sfnx_moe_decode_workspace": (sz, [i32, i32, i32, i32, i32, vp]),
     "sfnx_moe_decode": (i32, [vp, i32, u32, i32, i32, i32, i32, i32, vp, i32, i32, f32, vp, sz, i32, vp]),
+    "sfnx_moe_decode_noalloc": (i32, [vp, i32, u32, u32, i32, i32, i32, i32, i32, vp, i32, i32, f32, vp]),
     "sfnx_moe_decode2": (i32, [vp, i32, u32, u32, i32, i32, i32, i32, i32, vp, i32, i32, f32, vp, sz, i32, vp]),
     "sfnx_moe_decode_q8s": (i32, [vp, vp, i32, u32, u32, i32, i32, i32, i32, vp, i32, i32, f32, vp, sz, i32, vp]),
     "sfnx_q8s_gemv": (i32, [vp, i32, i32, vp, vp, i32, i32, vp]),

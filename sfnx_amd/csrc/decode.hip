@@ -12,6 +12,9 @@
 // The arithmetic of every value is the unfused entry points' (router_route, moe_gate_up, moe_down, moe_combine), so the
 // two paths agree bit for bit.
 #include <hip/hip_ext.h>
+
+#include <mutex>
+
 #include "decode.hpp"
 
 namespace sfnx {
@@ -804,4 +807,38 @@ extern "C" int sfnx_moe_decode(const sfnx_moe_layer_w* layers, int n_layers, uin
                                int shared, float* x, int T, int norm, float eps, void* ws, size_t ws_bytes, int phases,
                                void* st) {
     return sfnx_moe_decode2(layers, n_layers, type, type, H, E, K, ff, shared, x, T, norm, eps, ws, ws_bytes, phases, st);
+}
+
+// ------------------------------------------------------------------------------------------------ no allocation
+// The decode workspace as a file-scope device array, for callers that cannot allocate.  Its host-side name is no
+// device address: host code uses only the address hipGetSymbolAddress returns, fetched once per device.
+namespace {
+constexpr size_t NOALLOC_BYTES = 4u << 20;
+__device__ __align__(256) unsigned char scratch[NOALLOC_BYTES];
+constexpr int NOALLOC_DEVS = 64;
+void* g_scratch[NOALLOC_DEVS] = {};
+std::mutex g_scratch_mu;
+void* scratch_of_device() {
+    int dev = 0;
+    check(hipGetDevice(&dev), "hipGetDevice");
+    require(dev >= 0 && dev < NOALLOC_DEVS, "device index past the library's table");
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch[dev]) {
+        void* p = nullptr;
+        check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress (decode scratch)");
+        g_scratch[dev] = p;
+    }
+    return g_scratch[dev];
+}
+}  // namespace
+
+extern "C" int sfnx_moe_decode_noalloc(const sfnx_moe_layer_w* layers, int n_layers, uint32_t gu_type, uint32_t dn_type,
+                                       int H, int E, int K, int ff, int shared, float* x, int T, int norm, float eps,
+                                       void* st) {
+    return guarded("sfnx_moe_decode_noalloc", [&] {
+        const DecLayout L = dec_layout(H, E, K, ff);
+        require(L.total <= NOALLOC_BYTES, "shape needs a decode workspace larger than the library's 4 MiB scratch");
+        moe_decode(layers, nullptr, n_layers, gu_type, dn_type, H, E, K, ff, shared, x, T, norm, eps, scratch_of_device(),
+                   NOALLOC_BYTES, 0, st);
+    });
 }
