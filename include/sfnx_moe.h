@@ -151,11 +151,12 @@ int sfnx_q8s_swiglu_gemv(const void* W, int rows, int ffs, const float* gu, floa
 
 /* src/prefill.cu:407-417 pf_dense_xh (the prompt path's dense matrices, the shared expert's among them): out[c][r]
  * (row stride ldo) = sum_k f16(W[r][k]) xh[c][k] for C f16 rows xh [C][cols], fp32 accumulation.  W is a dense Q8_0
- * matrix (planar, one matrix), dequantized to f16 into wh (rows * cols * 2 bytes, the caller's) and multiplied in one
- * rocBLAS gemm_ex, as the reference dequantizes (k_q8s_f16) and calls cublasGemmEx.  The first call on a device
- * creates that device's rocBLAS handle (the call's only allocation). */
-int sfnx_pf_dense(const void* W, int rows, int cols, const uint16_t* xh, int C, float* out, int ldo, void* wh,
-                  size_t wh_bytes, void* st);
+ * matrix (planar, one matrix), run as one expert of the matrix-core kernels (sfnx_moe_down_mma's): its f16 weights are
+ * the reference's k_q8s_f16 values (f16(q d)), made in registers, and the products are summed in fp32 where the
+ * reference calls cublasGemmEx.  wk (16-byte aligned, at least ceil(C / 64) * sizeof(sfnx_bigjob) + 4 bytes, the
+ * caller's; the reference's f16 staging p.wh serves) holds the call's job list.  rows % 256 == 0, cols % 512 == 0. */
+int sfnx_pf_dense(const void* W, int rows, int cols, const uint16_t* xh, int C, float* out, int ldo, void* wk,
+                  size_t wk_bytes, void* st);
 
 /* ---------------------------------------------------------------------------------------------- fused decode */
 /* one layer's weights: router W [E + 1][H] fp32 (row E gates the shared expert), planar gate|up experts (E + 1 of

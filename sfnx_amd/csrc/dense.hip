@@ -2,11 +2,8 @@
 // q8s_gemv of the q8_1 activations through gate|up, swiglu_stacked_q8_1, q8s_gemv of h through down into part rows
 // P + t.  The dot is the reference's q8s sum (src/dense.cuh:24-154), here with 32 lanes a row as there; the fused
 // decode computes the same sums on its own lane groups (q8s_dot in mv.hpp).  On the prompt path the reference runs its
-// dense matrices as f16 GEMMs of the dequantized rows (pf_dense_xh): sfnx_pf_dense, through rocBLAS.
-#include <rocblas/rocblas.h>
-
-#include <mutex>
-
+// dense matrices as f16 GEMMs of the dequantized rows (pf_dense_xh): sfnx_pf_dense, on the matrix-core expert kernels
+// (moe_mma.hip).
 #include "mv.hpp"
 
 namespace sfnx {
@@ -51,19 +48,6 @@ __global__ void k_swiglu_stacked(const float* __restrict__ gu, uint8_t* __restri
     if (l == 0) *reinterpret_cast<uint32_t*>(blk) = (uint32_t) f2h(d) | ((uint32_t) f2h(sum) << 16);
 }
 
-// one rocBLAS handle a device, made on the first prompt-path dense call on it (its only allocation)
-constexpr int BLAS_DEVS = 64;
-rocblas_handle g_blas[BLAS_DEVS] = {};
-std::mutex g_blas_mu;
-rocblas_handle blas_handle() {
-    int dev = 0;
-    check(hipGetDevice(&dev), "hipGetDevice");
-    require(dev >= 0 && dev < BLAS_DEVS, "device index past the library's table");
-    std::lock_guard<std::mutex> lk(g_blas_mu);
-    if (!g_blas[dev]) require(rocblas_create_handle(&g_blas[dev]) == rocblas_status_success, "rocblas_create_handle failed");
-    return g_blas[dev];
-}
-
 }  // namespace
 }  // namespace sfnx
 
@@ -105,26 +89,5 @@ extern "C" int sfnx_swiglu_stacked_q8_1(const float* gu, void* hq, int ffs, int 
         require(T >= 1 && T <= 65535, "T out of range");
         const dim3 grid((ffs / 32 + 7) / 8, T);
         k_swiglu_stacked<<<grid, 256, 0, stream_of(st)>>>(gu, (uint8_t*) hq, ffs, T);
-    });
-}
-
-extern "C" int sfnx_pf_dense(const void* W, int rows, int cols, const uint16_t* xh, int C, float* out, int ldo, void* wh,
-                             size_t wh_bytes, void* st) {
-    return guarded("sfnx_pf_dense", [&] {
-        require(W != nullptr && xh != nullptr && out != nullptr && wh != nullptr, "null pointer");
-        require(rows > 0 && rows % 32 == 0 && cols > 0 && cols % 512 == 0, "rows must be a multiple of 32, cols of 512");
-        require(C >= 1 && ldo >= rows, "C must be positive and ldo at least rows");
-        require(wh_bytes >= (size_t) rows * cols * 2, "f16 staging smaller than the matrix");
-        // the matrix to f16 once (k_q8s_f16, src/prefill.cu:414), then out^T = W . xh^T in column-major terms:
-        // the reference's cublasGemmEx(OP_T, OP_N, rows, C, cols, W f16, xh f16, out f32, compute 32F)
-        if (sfnx_dequantize_f16(SFNX_Q8_0, W, (uint16_t*) wh, 1, rows, cols, st) != 0) throw std::runtime_error(sfnx_last_error());
-        rocblas_handle h = blas_handle();
-        require(rocblas_set_stream(h, stream_of(st)) == rocblas_status_success, "rocblas_set_stream failed");
-        const float one = 1.0f, zero = 0.0f;
-        const rocblas_status r = rocblas_gemm_ex(h, rocblas_operation_transpose, rocblas_operation_none, rows, C, cols, &one, wh,
-                                                 rocblas_datatype_f16_r, cols, xh, rocblas_datatype_f16_r, cols, &zero, out,
-                                                 rocblas_datatype_f32_r, ldo, out, rocblas_datatype_f32_r, ldo,
-                                                 rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
-        require(r == rocblas_status_success, "rocblas_gemm_ex failed");
     });
 }

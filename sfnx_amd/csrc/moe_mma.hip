@@ -288,6 +288,15 @@ template <int N> __device__ __forceinline__ void wait_vmem_below() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
 }
 
+// The block barrier at a run start, without the memory fence of __syncthreads: the fence waits for every vector memory
+// operation of the wavefront (vmcnt(0)), which would drain the weight chunks in flight at every run.  The activation
+// copies a run waits for were checked by the explicit vmcnt above; the previous run's LDS reads all fed matrix
+// instructions before the barrier, so only LDS operations (lgkmcnt) are waited here.
+__device__ __forceinline__ void run_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0); vmcnt and expcnt unwaited
+    __builtin_amdgcn_s_barrier();
+}
+
 // One chunk's steps on one wavefront's 32 weight rows: per step the 4 B fragments are dequantized from the registers
 // (VALU), then each of the 4 k-pieces takes the activation fragment from LDS and one MFMA per 32-token tile.  Several
 // wavefronts share each SIMD, so one's dequantization overlaps another's matrix work.
@@ -349,7 +358,7 @@ __device__ __forceinline__ void chunk_walk(const uint8_t* mat, int R, int C, int
                 else if (after == 1) wait_vmem_below<LD>();
                 else wait_vmem();
             }
-            __syncthreads();                  // every wavefront's rows landed; every wavefront is past the previous run
+            run_barrier();                    // every wavefront's rows landed; every wavefront is past the previous run
             if (nr > 1 && k + per_tile / nr < NK) load_x_async<W>(xs + (size_t) ((rg + 1) & 1) * MM_XBUF, x, C, ys, n, (r + 1) % nr, wave, lane);
         }
         mma_chunk<TYPE, NT>(w, cj, xb, nn, h, acc);
@@ -374,11 +383,12 @@ __device__ __forceinline__ void chunk_walk(const uint8_t* mat, int R, int C, int
 // D[token][row] of a tile: lane (nn, h), value q at token 8 (q / 4) + 4 h + q % 4 of 32-token tile t
 __device__ __forceinline__ int acc_token(int t, int q, int h) { return 32 * t + 8 * (q / 4) + 4 * h + q % 4; }
 
-// rows: ys[0..n) (activation rows) and outs[0..n) (output rows), n <= 32 NT; the block's rows are G tiles of 32 W
+// rows: ys[0..n) (activation rows) and outs[0..n) (output rows, ldo floats apart), n <= 32 NT; the block's rows are G
+// tiles of 32 W
 template <int TYPE, int NT, int W>
 __device__ __forceinline__ void mma_job(const uint8_t* mat, int R, int C, int row0, int G, int wave, int lane,
                                         const int* ys, const int* outs, int n, const _Float16* __restrict__ x,
-                                        _Float16* xs, float* __restrict__ out) {
+                                        _Float16* xs, float* __restrict__ out, int ldo) {
     const int h = lane / 32, nn = lane % 32;
     auto row_of = [&](int it) { return row0 + it * 32 * W + wave * 32 + nn; };
     auto store = [&](int it, const float16v (&acc)[NT]) {
@@ -388,7 +398,7 @@ __device__ __forceinline__ void mma_job(const uint8_t* mat, int R, int C, int ro
 #pragma unroll
             for (int q = 0; q < 16; ++q) {
                 const int m = acc_token(t, q, h);
-                if (m < n) out[(size_t) outs[m] * R + row] = acc[t][q];
+                if (m < n) out[(size_t) outs[m] * ldo + row] = acc[t][q];
             }
     };
     float16v acc[NT];
@@ -485,7 +495,7 @@ constexpr int DN_WAVES = 8, DN_THREADS = DN_WAVES * WAVE, DN_BM = 32 * DN_WAVES;
 template <int TYPE>
 __global__ void __launch_bounds__(DN_THREADS, 4) k_moe_mma(const uint8_t* __restrict__ A, size_t sa, int R, int C, int G,
                                                        const sfnx_bigjob* __restrict__ jobs, const int* __restrict__ njobs,
-                                                       const _Float16* __restrict__ x, float* __restrict__ out) {
+                                                       const _Float16* __restrict__ x, float* __restrict__ out, int ldo) {
     int sl, ji;
     xcd_job(blockIdx.x, R / (G * DN_BM), sl, ji);
     if (ji >= *njobs) return;
@@ -497,8 +507,8 @@ __global__ void __launch_bounds__(DN_THREADS, 4) k_moe_mma(const uint8_t* __rest
     const uint8_t* mat = A + (size_t) jb.w * sa;
     _Float16* xs = reinterpret_cast<_Float16*>(xs_raw);
     const int row0 = sl * G * DN_BM;
-    if (jb.n > 32) mma_job<TYPE, 2, DN_WAVES>(mat, R, C, row0, G, wave, lane, jb.y, jb.out, jb.n, x, xs, out);
-    else mma_job<TYPE, 1, DN_WAVES>(mat, R, C, row0, G, wave, lane, jb.y, jb.out, jb.n, x, xs, out);
+    if (jb.n > 32) mma_job<TYPE, 2, DN_WAVES>(mat, R, C, row0, G, wave, lane, jb.y, jb.out, jb.n, x, xs, out, ldo);
+    else mma_job<TYPE, 1, DN_WAVES>(mat, R, C, row0, G, wave, lane, jb.y, jb.out, jb.n, x, xs, out, ldo);
 }
 
 // k_swiglu_h16 (src/moe_mma.cuh:382-388): h16 = f16(silu(gate) * up) of P rows [gate (ff) | up (ff)]
@@ -517,8 +527,24 @@ __global__ void k_to_f16(const float* __restrict__ x, _Float16* __restrict__ y, 
 
 constexpr size_t MM_LDS = 2 * MM_XBUF * sizeof(_Float16);
 
+// A dense matrix's prompt rows as BigJobs of one "expert": job j takes rows 64 j .. 64 j + 63 (of C) to the same rows
+__global__ void k_dense_jobs(sfnx_bigjob* __restrict__ jobs, int* __restrict__ njobs, int C) {
+    const int j = blockIdx.x, n = min(SFNX_PF_JOB, C - SFNX_PF_JOB * j);
+    for (int m = threadIdx.x; m < SFNX_PF_JOB; m += blockDim.x) {
+        const int t = m < n ? SFNX_PF_JOB * j + m : 0;
+        jobs[j].y[m] = t;
+        jobs[j].out[m] = t;
+    }
+    if (threadIdx.x == 0) {
+        jobs[j].w = 0;
+        jobs[j].n = n;
+        if (j == 0) *njobs = gridDim.x;
+    }
+}
+
+// out rows ldo floats apart (0: n_out); G: 256-row tiles a block walks (0: half of them, for routed jobs, which are many)
 void moe_mma(uint32_t type, const void* A, size_t sa, int n_in, int n_out, const sfnx_bigjob* jobs, const int* njobs,
-             int njobs_cap, const void* x16, float* out, void* st) {
+             int njobs_cap, const void* x16, float* out, void* st, int ldo = 0, int G = 0) {
     require(expert_type_ok(type), TYPE_MSG);
     require(n_in > 0 && n_in % 512 == 0, "expert input width must be a multiple of 512");
     require(n_out > 0 && n_out % DN_BM == 0, "expert rows must be a multiple of 256");
@@ -527,20 +553,23 @@ void moe_mma(uint32_t type, const void* A, size_t sa, int n_in, int n_out, const
     require(njobs_cap >= 0 && njobs_cap <= (1 << 20), "njobs_cap out of range");
     if (njobs_cap == 0) return;
     // tiles of 256 rows: two blocks a job (half the tiles each), for more blocks than compute units
-    const int groups = n_out / DN_BM, G = std::max(1, groups / 2);
+    const int groups = n_out / DN_BM;
+    if (G <= 0) G = std::max(1, groups / 2);
+    require(groups % G == 0, "row groups must split evenly");
+    if (ldo <= 0) ldo = n_out;
     const dim3 grid(xcd_grid(groups / G, njobs_cap));
     const size_t lds = (n_in == MM_RUN ? 1 : 2) * MM_XBUF * sizeof(_Float16);
     hipStream_t s = stream_of(st);
     if (type == SFNX_Q4_K)
-        k_moe_mma<SFNX_Q4_K><<<grid, DN_THREADS, lds, s>>>((const uint8_t*) A, sa, n_out, n_in, G, jobs, njobs, (const _Float16*) x16, out);
+        k_moe_mma<SFNX_Q4_K><<<grid, DN_THREADS, lds, s>>>((const uint8_t*) A, sa, n_out, n_in, G, jobs, njobs, (const _Float16*) x16, out, ldo);
     else if (type == SFNX_Q5_K)
-        k_moe_mma<SFNX_Q5_K><<<grid, DN_THREADS, lds, s>>>((const uint8_t*) A, sa, n_out, n_in, G, jobs, njobs, (const _Float16*) x16, out);
+        k_moe_mma<SFNX_Q5_K><<<grid, DN_THREADS, lds, s>>>((const uint8_t*) A, sa, n_out, n_in, G, jobs, njobs, (const _Float16*) x16, out, ldo);
     else if (type == SFNX_Q4_0)
-        k_moe_mma<SFNX_Q4_0><<<grid, DN_THREADS, lds, s>>>((const uint8_t*) A, sa, n_out, n_in, G, jobs, njobs, (const _Float16*) x16, out);
+        k_moe_mma<SFNX_Q4_0><<<grid, DN_THREADS, lds, s>>>((const uint8_t*) A, sa, n_out, n_in, G, jobs, njobs, (const _Float16*) x16, out, ldo);
     else if (type == SFNX_Q5_1)
-        k_moe_mma<SFNX_Q5_1><<<grid, DN_THREADS, lds, s>>>((const uint8_t*) A, sa, n_out, n_in, G, jobs, njobs, (const _Float16*) x16, out);
+        k_moe_mma<SFNX_Q5_1><<<grid, DN_THREADS, lds, s>>>((const uint8_t*) A, sa, n_out, n_in, G, jobs, njobs, (const _Float16*) x16, out, ldo);
     else
-        k_moe_mma<SFNX_Q8_0><<<grid, DN_THREADS, lds, s>>>((const uint8_t*) A, sa, n_out, n_in, G, jobs, njobs, (const _Float16*) x16, out);
+        k_moe_mma<SFNX_Q8_0><<<grid, DN_THREADS, lds, s>>>((const uint8_t*) A, sa, n_out, n_in, G, jobs, njobs, (const _Float16*) x16, out, ldo);
 }
 
 void moe_mma_gu(uint32_t type, const void* A, size_t sa, int n_in, int ff, const sfnx_bigjob* jobs, const int* njobs,
@@ -612,5 +641,28 @@ extern "C" int sfnx_to_f16(const float* x, uint16_t* y, size_t n, void* st) {
     return guarded("sfnx_to_f16", [&] {
         if (!n) return;
         k_to_f16<<<(unsigned) std::min<size_t>((n + 255) / 256, 16384), 256, 0, stream_of(st)>>>(x, (_Float16*) y, n);
+    });
+}
+
+extern "C" int sfnx_pf_dense(const void* W, int rows, int cols, const uint16_t* xh, int C, float* out, int ldo, void* wk,
+                             size_t wk_bytes, void* st) {
+    return guarded("sfnx_pf_dense", [&] {
+        require(W != nullptr && xh != nullptr && out != nullptr && wk != nullptr, "null pointer");
+        require(rows > 0 && rows % DN_BM == 0 && cols > 0 && cols % MM_RUN == 0, "rows must be a multiple of 256, cols of 512");
+        require(C >= 1 && C <= (1 << 20) && ldo >= rows, "C out of range, or ldo smaller than rows");
+        // the reference dequantizes the matrix to f16 and multiplies in one f16 GEMM with fp32 results (pf_dense_xh,
+        // cublasGemmEx); here the matrix is one expert of the matrix-core kernels, whose weights are the same f16
+        // values (hmul2(q, d)), dotted in fp32 on v_mfma_f32_32x32x16_f16.  The workspace holds the job list.
+        const int nj = (C + SFNX_PF_JOB - 1) / SFNX_PF_JOB;
+        const size_t jb_bytes = (size_t) nj * sizeof(sfnx_bigjob);
+        require(wk_bytes >= jb_bytes + sizeof(int), "workspace smaller than the job list (ceil(C / 64) jobs + 4 bytes)");
+        require(((uintptr_t) wk & 15) == 0, "workspace must be 16-byte aligned");
+        sfnx_bigjob* jobs = (sfnx_bigjob*) wk;
+        int* njobs = (int*) ((char*) wk + jb_bytes);
+        hipStream_t s = stream_of(st);
+        k_dense_jobs<<<nj, 64, 0, s>>>(jobs, njobs, C);
+        const size_t sa = row_bytes(SFNX_Q8_0, cols) * (size_t) rows;
+        // one 256-row tile a block: few jobs, so every tile is a block of its own
+        moe_mma(SFNX_Q8_0, W, sa, cols, rows, jobs, njobs, nj, xh, out, st, ldo, 1);
     });
 }

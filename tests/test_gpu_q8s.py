@@ -231,10 +231,11 @@ def test_synthetic_q8s_layer():
     assert np.isfinite(yf).all() and max_rel(yf, oy) < TOL
 
 
-@pytest.mark.parametrize("rows,cols,C", [(1024, 2048, 200), (2048, 512, 33)])
+@pytest.mark.parametrize("rows,cols,C", [(1024, 2048, 200), (2048, 512, 33), (512, 1024, 1000), (256, 512, 1)])
 def test_pf_dense_against_float64(rows, cols, C):
     """sfnx_pf_dense (src/prefill.cu:407-417): f16(W) . xh rows in fp32, against float64 products of the same f16
-    operands within 2e-3 (the GEMM's own order is rocBLAS's, as the reference's is cuBLAS's); rows of out ldo apart"""
+    operands within 2e-3 (the sum's order is the matrix-core kernel's, as the reference's is cuBLAS's); rows of out
+    ldo apart, the columns past rows untouched"""
     g, W = q8_0_matrix(rows, cols, 300 + cols)
     x = orc.synth(C * cols, 301, 1.0).reshape(C, cols).astype(np.float16)
     ldo = rows + 64
@@ -247,12 +248,10 @@ def test_pf_dense_against_float64(rows, cols, C):
     got = out.cpu().numpy()
     assert max_rel(got[:, :rows], want) < 2e-3
     assert (got[:, rows:] == 5.0).all()
-    # the staging holds the f16 dequantization, bit for bit the oracle's f16 form
-    assert np.array_equal(wh.cpu().numpy().view(np.uint16), orc.dequant_f16(orc.Q8_0, g.reshape(-1), rows, cols).reshape(-1))
 
 
 def test_prefill_shared_graph_replays():
-    """the dense shared expert's prompt rows (dequantization + rocBLAS GEMMs) captured in a HIP graph, as the bench
+    """the dense shared expert's prompt rows (job lists + matrix-core GEMMs) captured in a HIP graph, as the bench
     times them: every replay, with eager work between them, equals the eager result bit for bit"""
     shape = moe.LayerShape(H=1024, E=64, K=6, ff=512, wtype=orc.Q4_K, shared=True, sh_q8s=True)
     L, _ = make_layer(shape, 160)
