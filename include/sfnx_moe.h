@@ -22,6 +22,9 @@
  * Every plane is tiled by rows (32 for the K-quants, 4 for the 32-value block types): piece p of a row lies one tile's pieces after piece
  * p - 1, so a wavefront's 16-byte loads over a tile's rows cover whole 128-byte lines.  The planar matrix has exactly
  * the GGUF matrix's size; experts sit at base + e * stride.  C % 512 == 0, R % 32 == 0.
+ * Every expert store argument (A with its stride sa, and the gu/dn fields of sfnx_moe_layer_w) may instead be a device
+ * table of expert pointers, signalled by a stride of 0: expert e's matrix is ((const void* const*) A)[e], wherever
+ * it lives (src/moe_w.cuh:9 moe_expert over DW::ep, src/model.hpp:85-86).
  */
 #ifndef SFNX_MOE_H
 #define SFNX_MOE_H

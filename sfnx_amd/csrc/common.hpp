@@ -235,6 +235,15 @@ inline bool expert_type_ok(uint32_t type) {
 constexpr const char* TYPE_MSG = "expert type must be Q4_0 (2), Q5_1 (7), Q8_0 (8), Q4_K (12) or Q5_K (13)";
 __host__ __device__ constexpr bool is_kquant(uint32_t type) { return type == SFNX_Q4_K || type == SFNX_Q5_K; }
 inline int block_values(uint32_t type) { return is_kquant(type) ? 256 : 32; }
+// Expert e's matrix of a store (src/moe_w.cuh:9 moe_expert): base + e * sa, or, when sa is 0, the device table of
+// expert pointers at `base` (the reference's DW::ep, src/model.hpp:85-86: each expert wherever it lives, a VRAM slot or
+// mapped page-locked host memory).  sa is a kernel argument, so the branch is uniform.
+__device__ __forceinline__ const uint8_t* expert_at(const uint8_t* base, size_t sa, int e) {
+    return sa ? base + (size_t) e * sa : reinterpret_cast<const uint8_t* const*>(base)[e];
+}
+// a store's stride as the launchers check it: sa == 0 is the pointer table, else at least one matrix
+inline bool stride_ok(size_t sa, size_t matrix_bytes) { return sa == 0 || sa >= matrix_bytes; }
+
 __host__ __device__ inline size_t row_bytes(uint32_t type, int cols) {
     switch (type) {
         case SFNX_Q4_K: return (size_t) cols / 256 * Q4K_BYTES;

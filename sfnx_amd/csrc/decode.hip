@@ -194,7 +194,7 @@ __global__ void __launch_bounds__(2 * d2_threads<TYPE>()) k_dec_experts(
         for (int s = 0; s < jb.n; ++s) put(s, group_sum<LPR>(q8s_dot<LPR>(Ps, row, H, ln, a, s)));
     } else {
         typename RowOf<TYPE, G>::R w;
-        RowOf<TYPE, G>::load(w, A + (size_t) jb.w * sa, 2 * ff, row, H, ln);
+        RowOf<TYPE, G>::load(w, expert_at(A, sa, jb.w), 2 * ff, row, H, ln);
         __syncthreads();   // the staged activations
         for (int s = 0; s < jb.n; ++s) put(s, group_sum<LPR>(w.dot(a, s, ln)));
     }
@@ -278,7 +278,7 @@ __global__ void __launch_bounds__(2 * d2_threads<TYPE>()) k_dec_experts1(
     // the first half of the waves take the 32 gate rows, the second half the matching up rows
     const bool up = wave >= NW / 2;
     const int rw = lane / LPR, ln = lane % LPR, fl = (up ? wave - NW / 2 : wave) * RPW + rw, row = (up ? ff : 0) + fb * 32 + fl;
-    const uint8_t* mat = A + (size_t) ex * sa;
+    const uint8_t* mat = expert_at(A, sa, ex);
     typename RowOf<TYPE, G>::R wr;
     if (has_job && !q8s) RowOf<TYPE, G>::issue(wr, mat, 2 * ff, row, H, ln);
     if (blockIdx.x < XCDS && wave == 0) {   // the routing, published for K3 and the caller, while the rows load
@@ -402,7 +402,7 @@ __global__ void __launch_bounds__(D3W_THREADS) k_dec_down(const uint8_t* __restr
             const int task = t0 + b * GROUPS;
             if (task < ntask) {
                 const int j = task / D3_ROWS, r = task % D3_ROWS;
-                RowOf<TYPE, G2>::load(w[b], A + (size_t) jw[j] * sa, H, row0 + r, ff, ln);
+                RowOf<TYPE, G2>::load(w[b], expert_at(A, sa, jw[j]), H, row0 + r, ff, ln);
             }
         }
 #pragma unroll
@@ -494,7 +494,7 @@ __global__ void __launch_bounds__(NT3) k_dec_down1(const uint8_t* __restrict__ A
             wsh.issue(q80_planes(sh_dn, H, ff), row0 + r, ff, ln);
             bsh = b;
         } else if (task < ntask) {
-            RowOf<TYPE, G2>::issue(w[b], A + (size_t) (pp[b] < K ? ex[b] : E) * sa, H, row0 + r, ff, ln);
+            RowOf<TYPE, G2>::issue(w[b], expert_at(A, sa, pp[b] < K ? ex[b] : E), H, row0 + r, ff, ln);
         }
     }
     // the staged activations
@@ -532,7 +532,7 @@ __global__ void __launch_bounds__(NT3) k_dec_down1(const uint8_t* __restrict__ A
             v = group_sum<LPR>(q8s_dot<LPR>(q80_planes(sh_dn, H, ff), row0 + r, ff, ln, a, K));
         } else {
             typename RowOf<TYPE, G2>::R w1;
-            RowOf<TYPE, G2>::load(w1, A + (size_t) (j < nr ? e : E) * sa, H, row0 + r, ff, ln);
+            RowOf<TYPE, G2>::load(w1, expert_at(A, sa, j < nr ? e : E), H, row0 + r, ff, ln);
             v = group_sum<LPR>(w1.dot(a, q, ln));
         }
         if (ln == 0) part[q][r] = v;
@@ -764,8 +764,8 @@ void moe_decode(const sfnx_moe_layer_w* layers, const sfnx_moe_shared_q8s* sh, i
         require(n_layers >= 0 && (n_layers == 0 || layers != nullptr), "no layers");
         for (int l = 0; l < n_layers; ++l) {
             require(layers[l].W && layers[l].gu && layers[l].dn, "a layer's weights are missing");
-            require(layers[l].gu_stride >= row_bytes(type, H) * 2 * (size_t) ff, "gate|up stride smaller than a matrix");
-            require(layers[l].dn_stride >= row_bytes(dn_type, ff) * (size_t) H, "down stride smaller than a matrix");
+            require(stride_ok(layers[l].gu_stride, row_bytes(type, H) * 2 * (size_t) ff), "gate|up stride smaller than a matrix");
+            require(stride_ok(layers[l].dn_stride, row_bytes(dn_type, ff) * (size_t) H), "down stride smaller than a matrix");
             if (sh) require(sh[l].gu != nullptr && sh[l].dn != nullptr, "a layer's shared expert matrices are missing");
         }
         const DecArgs d{gu_type, dn_type, H, E, K, ff, shared ? 1 : 0, T, norm ? 1 : 0, eps, phases ? phases : 7, nullptr};

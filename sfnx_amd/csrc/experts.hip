@@ -34,7 +34,7 @@ __global__ void __launch_bounds__(MV_THREADS) k_moe_mv(const uint8_t* __restrict
     __syncthreads();
     const int row = blockIdx.x * RPB + threadIdx.x / LPR, ln = threadIdx.x % LPR;
     const bool live = row < R;
-    const uint8_t* mat = A + (size_t) jb.w * sa;
+    const uint8_t* mat = expert_at(A, sa, jb.w);
     const Acts a = acts_in(lds, TT, C);
     if constexpr (TYPE != SFNX_Q8_0) {
         using Row = std::conditional_t<is_kquant(TYPE), Q4kRow<G, TYPE == SFNX_Q5_K>, NbRow<G, TYPE>>;
@@ -91,7 +91,7 @@ void moe_mv(uint32_t type, const void* A, size_t sa, int n_in, int n_out, const 
     require(expert_type_ok(type), TYPE_MSG);
     require(n_in > 0 && n_in % 512 == 0, "expert input width must be a multiple of 512");
     require(n_out > 0, "expert rows must be positive");
-    require(sa >= row_bytes(type, n_in) * (size_t) n_out, "expert stride smaller than a matrix");
+    require(stride_ok(sa, row_bytes(type, n_in) * (size_t) n_out), "expert stride smaller than a matrix");
     require(njobs_max >= 0 && njobs_max <= 65535, "njobs_max out of range");
     if (njobs_max == 0) return;
     const int G = n_in / 512;

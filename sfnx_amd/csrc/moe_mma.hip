@@ -300,14 +300,23 @@ __device__ __forceinline__ void run_barrier() {
 // One chunk's steps on one wavefront's 32 weight rows: per step the 4 B fragments are dequantized from the registers
 // (VALU), then each of the 4 k-pieces takes the activation fragment from LDS and one MFMA per 32-token tile.  Several
 // wavefronts share each SIMD, so one's dequantization overlaps another's matrix work.
+//
+// The registers of the chunk refill with the chunk `next` (k + MM_SLOTS; the last chunks request the final one again,
+// so every chunk issues the same requests) as they free up: piece s right after step s is dequantized, the Q4_K
+// header once its scales are decoded (the other types use their tail in every step, so it follows the last step).
+// Each request then has almost two chunks' time before it is needed, not one, from the same registers.
+template <int TYPE> constexpr bool tail_early() { return TYPE == SFNX_Q4_K; }
 template <int TYPE, int NT>
-__device__ __forceinline__ void mma_chunk(const Chunk<TYPE>& w, int cj, const _Float16* xb, int nn, int h, float16v (&acc)[NT]) {
+__device__ __forceinline__ void mma_chunk(Chunk<TYPE>& w, int cj, const _Float16* xb, int nn, int h, float16v (&acc)[NT],
+                                          const ChunkAt& next) {
     constexpr int S = Chunk<TYPE>::STEPS;
     const auto sc = chunk_scales(w);
+    if constexpr (tail_early<TYPE>()) load_tail(w, next);
 #pragma unroll
     for (int s = 0; s < S; ++s) {
         half8 b[4];
         dequant_step(w, s, b, sc);
+        load_piece(w, next, s);
         const int j = cj * S + s;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
@@ -318,11 +327,12 @@ __device__ __forceinline__ void mma_chunk(const Chunk<TYPE>& w, int cj, const _F
             for (int t = 0; t < NT; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[t], b[c], acc[t], 0, 0, 0);
         }
     }
+    if constexpr (!tail_early<TYPE>()) load_tail(w, next);
 }
 
 // The chunk walk shared by both kernels.  A wavefront's work is `tiles` row tiles of 32 rows (row_of(it)), each over
 // the nr runs of 512 columns, each run CPR chunks: chunk k = (tile, run, chunk-in-run) in that order.  Weights stream
-// through two register slots, chunk k + 2 requested as soon as chunk k is dotted.  The job's activation rows for a run
+// through two register slots, chunk k + 2 requested piece by piece while chunk k is dotted.  The job's activation rows for a run
 // sit in one of two LDS buffers; run r + 1's are requested (global -> LDS, no registers) when run r starts, so each
 // run start waits only for them, not for the weight chunks requested after them (CPR chunks of LOADS requests each).
 // tile_done(it, acc) takes a tile's accumulators (and they are cleared for the next tile); the last tile's stay in acc.
@@ -344,24 +354,17 @@ __device__ __forceinline__ void chunk_walk(const uint8_t* mat, int R, int C, int
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = float16v{};
     // one chunk: the run's activations first when the chunk starts a run, then the dots, then the tile's end
-    auto step = [&](const Chunk<TYPE>& w, int k) {
+    auto step = [&](Chunk<TYPE>& w, int k) {
         const int rc = k % per_tile, r = rc / CPR, cj = rc % CPR, rg = k / CPR;   // rg: runs walked so far
         _Float16* xb = xs + (size_t) (nr > 1 ? rg & 1 : 0) * MM_XBUF;
         if (cj == 0 && (nr > 1 || k == 0)) {
+            // this run's rows: requested before the weight requests of the CPR chunks since
             if (k == 0) wait_vmem();
-            else {
-                // this run's rows: requested before the weight chunks of the CPR chunks since (those past the end
-                // were not requested)
-                const int after = min(CPR, max(0, NK - MM_SLOTS - (k - CPR)));
-                if (after == CPR) wait_vmem_below<CPR * LD>();
-                else if (after >= 2) wait_vmem_below<2 * LD>();
-                else if (after == 1) wait_vmem_below<LD>();
-                else wait_vmem();
-            }
+            else wait_vmem_below<CPR * LD>();
             run_barrier();                    // every wavefront's rows landed; every wavefront is past the previous run
             if (nr > 1 && k + per_tile / nr < NK) load_x_async<W>(xs + (size_t) ((rg + 1) & 1) * MM_XBUF, x, C, ys, n, (r + 1) % nr, wave, lane);
         }
-        mma_chunk<TYPE, NT>(w, cj, xb, nn, h, acc);
+        mma_chunk<TYPE, NT>(w, cj, xb, nn, h, acc, at(min(k + MM_SLOTS, NK - 1)));
         if (rc == per_tile - 1 && k + 1 < NK) {
             tile_done(k / per_tile, acc);
 #pragma unroll
@@ -373,8 +376,7 @@ __device__ __forceinline__ void chunk_walk(const uint8_t* mat, int R, int C, int
         for (int i = 0; i < MM_SLOTS; ++i) {
             const int k = k0 + i;
             if (k < NK) {
-                step(w[i], k);
-                if (k + MM_SLOTS < NK) load_chunk(w[i], at(k + MM_SLOTS));
+                step(w[i], k);   // refills w[i] with chunk k + MM_SLOTS
             }
         }
     }
@@ -482,7 +484,7 @@ __global__ void __launch_bounds__(MM_THREADS) k_moe_mma_gu(const uint8_t* __rest
     load_job(jb, jobs + ji);
     __syncthreads();
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-    const uint8_t* mat = A + (size_t) jb.w * sa;
+    const uint8_t* mat = expert_at(A, sa, jb.w);
     _Float16* xs = reinterpret_cast<_Float16*>(xs_raw);
     if (jb.n > 32) mma_gu_job<TYPE, 2>(mat, ff, C, sl * MM_FF, wave, lane, jb, x, xs, gu, h16);
     else mma_gu_job<TYPE, 1>(mat, ff, C, sl * MM_FF, wave, lane, jb, x, xs, gu, h16);
@@ -504,7 +506,7 @@ __global__ void __launch_bounds__(DN_THREADS, 4) k_moe_mma(const uint8_t* __rest
     load_job(jb, jobs + ji);
     __syncthreads();
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-    const uint8_t* mat = A + (size_t) jb.w * sa;
+    const uint8_t* mat = expert_at(A, sa, jb.w);
     _Float16* xs = reinterpret_cast<_Float16*>(xs_raw);
     const int row0 = sl * G * DN_BM;
     if (jb.n > 32) mma_job<TYPE, 2, DN_WAVES>(mat, R, C, row0, G, wave, lane, jb.y, jb.out, jb.n, x, xs, out, ldo);
@@ -549,7 +551,7 @@ void moe_mma(uint32_t type, const void* A, size_t sa, int n_in, int n_out, const
     require(n_in > 0 && n_in % 512 == 0, "expert input width must be a multiple of 512");
     require(n_out > 0 && n_out % DN_BM == 0, "expert rows must be a multiple of 256");
     require((n_out / DN_BM) % std::max(1, (n_out / DN_BM) / 2) == 0, "row groups must split evenly");
-    require(sa >= row_bytes(type, n_in) * (size_t) n_out, "expert stride smaller than a matrix");
+    require(stride_ok(sa, row_bytes(type, n_in) * (size_t) n_out), "expert stride smaller than a matrix");
     require(njobs_cap >= 0 && njobs_cap <= (1 << 20), "njobs_cap out of range");
     if (njobs_cap == 0) return;
     // tiles of 256 rows: two blocks a job (half the tiles each), for more blocks than compute units
@@ -577,7 +579,7 @@ void moe_mma_gu(uint32_t type, const void* A, size_t sa, int n_in, int ff, const
     require(expert_type_ok(type), TYPE_MSG);
     require(n_in > 0 && n_in % 512 == 0, "expert input width must be a multiple of 512");
     require(ff > 0 && ff % MM_FF == 0, "FF must be a multiple of 256");
-    require(sa >= row_bytes(type, n_in) * (size_t) (2 * ff), "expert stride smaller than a matrix");
+    require(stride_ok(sa, row_bytes(type, n_in) * (size_t) (2 * ff)), "expert stride smaller than a matrix");
     require(njobs_cap >= 0 && njobs_cap <= (1 << 20), "njobs_cap out of range");
     if (njobs_cap == 0) return;
     const dim3 grid(xcd_grid(ff / MM_FF, njobs_cap));

@@ -27,8 +27,9 @@ struct Q8S {
 };
 
 // src/model.hpp:78-87 DW: one matrix (or expert 0's of a stack), n_out rows of n_in.  row_bytes and s are kept for
-// the reference's field list (row_bytes is derived from type and n_in here; s is the dense form of a matrix).  ep,
-// the per-expert pointer table of the reference's expert cache, is not supported: the calls refuse a DW that sets it.
+// the reference's field list (row_bytes is derived from type and n_in here; s is the dense form of a matrix).  ep: a
+// device table of each expert's matrix (the reference's expert-cache tables); when set, the calls pass it across the C
+// boundary as the store with stride 0, and the stride argument is unused, as in moe_expert (src/moe_w.cuh:9).
 struct DW {
     const void* p = nullptr;
     uint32_t type = 0;
@@ -37,6 +38,11 @@ struct DW {
     Q8S s;
     const char* const* ep = nullptr;
 };
+namespace detail {
+// a DW's experts at the C boundary: the pointer table (stride 0) when ep is set, else p and the stride
+inline const void* base_of(const DW& A) { return A.ep ? static_cast<const void*>(A.ep) : A.p; }
+inline size_t stride_of(const DW& A, size_t sa) { return A.ep ? 0 : sa; }
+}  // namespace detail
 
 // the sizes the reference compiles in
 struct MoeShape {
@@ -92,7 +98,7 @@ inline void router_route(const MoeShape& s, const float* W, const float* x, floa
 // src/kernels.hpp:281-282; T: the window's rows (the reference derives it as njobs_max / TOPK)
 inline void moe_gate_up(const DW& A, size_t sa, const Job* jobs, const int* njobs, int njobs_max, const void* xq, float* gu,
                         void* st, int T) {
-    ck(sfnx_moe_gate_up(A.p, sa, A.type, A.n_in, A.n_out, jobs, njobs, njobs_max, T, xq, gu, st));
+    ck(sfnx_moe_gate_up(detail::base_of(A), detail::stride_of(A, sa), A.type, A.n_in, A.n_out, jobs, njobs, njobs_max, T, xq, gu, st));
 }
 // src/kernels.hpp:281-282 with the dense shared expert's SwiGLU and down (sh_down: N rows of sh_ffs; sh_gu [T][2 sh_ffs]
 // into sh_out, row stride N).  The reference runs them in the gate|up launch; here sfnx_swiglu_stacked_q8_1 and
@@ -113,7 +119,7 @@ inline void moe_gate_up(const DW& A, size_t sa, const Job* jobs, const int* njob
 namespace detail {
 inline void no_cache(const ExpertCache* ec, const DW* w = nullptr) {
     if (ec != nullptr) throw std::runtime_error("expert cache (routed experts in host RAM) is not supported by sfnx_amd");
-    if (w != nullptr && w->ep != nullptr) throw std::runtime_error("DW::ep (per-expert pointer table) is not supported by sfnx_amd");
+    (void) w;
 }
 // the window's rows from the job grid's size, as the reference's moe_mm does (src/kernels.cu:1931)
 inline int rows_of(int njobs_max) {
@@ -141,26 +147,26 @@ inline void moe_gate_up(const DW& A, size_t sa, const Job* jobs, const int* njob
                         float* sh_out = nullptr) {
     detail::no_cache(nullptr, &A);
     const int T = detail::rows_of(njobs_max);
-    ck(sfnx_moe_gate_up(A.p, sa, A.type, A.n_in, A.n_out, jobs, njobs, njobs_max, T, xq, gu, st));
+    ck(sfnx_moe_gate_up(detail::base_of(A), detail::stride_of(A, sa), A.type, A.n_in, A.n_out, jobs, njobs, njobs_max, T, xq, gu, st));
     if (sh_down) ck(sfnx_q8s_swiglu_gemv(sh_down->p, A.n_in, sh_ffs, sh_gu, sh_out, A.n_in, T, st));
 }
 // src/kernels.hpp:305
 inline void moe_down(const DW& A, size_t sa, const Job* jobs, const int* njobs, int njobs_max, const float* gu, float* part,
                      void* st) {
     detail::no_cache(nullptr, &A);
-    ck(sfnx_moe_down(A.p, sa, A.type, A.n_in, A.n_out, jobs, njobs, njobs_max, detail::rows_of(njobs_max), gu, part, st));
+    ck(sfnx_moe_down(detail::base_of(A), detail::stride_of(A, sa), A.type, A.n_in, A.n_out, jobs, njobs, njobs_max, detail::rows_of(njobs_max), gu, part, st));
 }
 // src/kernels.hpp:290-292: the prompt path's matrix-core calls (moe_mma.cuh)
 inline void moe_gate_up_mma(const DW& A, size_t sa, const BigJob* jobs, const int* njobs, int njobs_cap, const uint16_t* xh,
                             float* gu, void* st) {
     detail::no_cache(nullptr, &A);
-    ck(sfnx_moe_gate_up_mma(A.p, sa, A.type, A.n_in, A.n_out, jobs, njobs, njobs_cap, xh, gu, st));
+    ck(sfnx_moe_gate_up_mma(detail::base_of(A), detail::stride_of(A, sa), A.type, A.n_in, A.n_out, jobs, njobs, njobs_cap, xh, gu, st));
 }
 inline void swiglu_h16(const float* gu, int ffs, int P, uint16_t* h16, void* st) { ck(sfnx_swiglu_h16(gu, ffs, P, h16, st)); }
 inline void moe_down_mma(const DW& A, size_t sa, const BigJob* jobs, const int* njobs, int njobs_cap, const uint16_t* h16,
                          float* part, void* st) {
     detail::no_cache(nullptr, &A);
-    ck(sfnx_moe_down_mma(A.p, sa, A.type, A.n_in, A.n_out, jobs, njobs, njobs_cap, h16, part, st));
+    ck(sfnx_moe_down_mma(detail::base_of(A), detail::stride_of(A, sa), A.type, A.n_in, A.n_out, jobs, njobs, njobs_cap, h16, part, st));
 }
 
 // src/kernels.hpp:284: jobs of up to MAXT rows each, njobs_cap of them at most (the prompt path's)
@@ -171,16 +177,16 @@ inline void moe_gate_up_jobs(const DW& A, size_t sa, const Job* jobs, const int*
 // src/kernels.hpp:305
 inline void moe_down(const DW& A, size_t sa, const Job* jobs, const int* njobs, int njobs_max, const float* gu, float* part,
                      void* st, int T) {
-    ck(sfnx_moe_down(A.p, sa, A.type, A.n_in, A.n_out, jobs, njobs, njobs_max, T, gu, part, st));
+    ck(sfnx_moe_down(detail::base_of(A), detail::stride_of(A, sa), A.type, A.n_in, A.n_out, jobs, njobs, njobs_max, T, gu, part, st));
 }
 // src/kernels.hpp:286-287
 inline void moe_gate_up_big(const DW& A, size_t sa, const BigJob* jobs, const int* njobs, int njobs_cap, const void* xq,
                             float* gu, void* st) {
-    ck(sfnx_moe_gate_up_big(A.p, sa, A.type, A.n_in, A.n_out, jobs, njobs, njobs_cap, xq, gu, st));
+    ck(sfnx_moe_gate_up_big(detail::base_of(A), detail::stride_of(A, sa), A.type, A.n_in, A.n_out, jobs, njobs, njobs_cap, xq, gu, st));
 }
 inline void moe_down_big(const DW& A, size_t sa, const BigJob* jobs, const int* njobs, int njobs_cap, const float* gu,
                          float* part, void* st) {
-    ck(sfnx_moe_down_big(A.p, sa, A.type, A.n_in, A.n_out, jobs, njobs, njobs_cap, gu, part, st));
+    ck(sfnx_moe_down_big(detail::base_of(A), detail::stride_of(A, sa), A.type, A.n_in, A.n_out, jobs, njobs, njobs_cap, gu, part, st));
 }
 // the prompt path's routing (src/prefill.cu:1163-1167: router sgemm, k_pf_top10, k_pf_count, k_pf_jobbase, k_pf_fill)
 inline void router_logits(const float* W, const float* x, float* logits, int T, int H, int L, void* st) {

@@ -57,3 +57,27 @@ def max_rel(got, want) -> float:
     got = np.asarray(got, np.float64)
     want = np.asarray(want, np.float64)
     return float(np.max(np.abs(got - want)) / max(np.max(np.abs(want)), 1e-30))
+
+
+def tabled(L: moe.MoeLayer, seed: int = 0):
+    """the same layer with its experts moved and reached through device pointer tables (stride 0; the reference's
+    DW::ep): each expert's matrices copied to a new, shuffled place in one fresh buffer, the tables pointing there.
+    Returns (layer view, the buffers it holds) - keep the buffers alive while the view is used."""
+    import copy
+    s = L.s
+    n = L.gu_w.numel() // L.gu_stride
+    perm = np.random.default_rng(seed).permutation(n)
+    keep = []
+    view = copy.copy(L)
+    for name, stride in (("gu_w", L.gu_stride), ("dn_w", L.dn_stride)):
+        src = getattr(L, name)
+        pitch = (stride + 255) // 256 * 256 + 256   # gaps between the moved matrices
+        dst = torch.full((n * pitch,), 0xEE, dtype=torch.uint8, device=src.device)
+        for e in range(n):
+            dst[perm[e] * pitch: perm[e] * pitch + stride].copy_(src[e * stride:(e + 1) * stride])
+        table = torch.tensor([dst.data_ptr() + int(perm[e]) * pitch for e in range(n)], dtype=torch.int64,
+                             device=src.device)
+        keep += [dst, table]
+        setattr(view, name, table)
+        setattr(view, name.replace("_w", "_stride"), 0)
+    return view, keep
