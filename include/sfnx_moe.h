@@ -296,6 +296,52 @@ int sfnx_gguf_moe_layer(const sfnx_gguf* g, int layer, int ff0, int ff1, void* g
 int sfnx_gguf_moe_layer_q8s(const sfnx_gguf* g, int layer, int ff0, int ff1, void* gu, size_t gu_stride, void* dn,
                             size_t dn_stride, float* W, void* sh_gu, void* sh_dn, int* info, void* st);
 
+/* ---------------------------------------------------------------------------------------------- expert cache */
+/* src/model.hpp:95-116 ExpertCache, src/moe.cuh:19-71 cache_plan, src/kernels.cu:1636-1668: routed experts kept in
+ * page-locked host memory (device-visible, sfnx_host_alloc), with VRAM slots for the ones in use.  A pool's slots hold
+ * whole experts of one size (gate|up at 0, down at dn_off); layers whose experts have that size share the pool.  The
+ * tables ep_gu / ep_dn ([n_layers * n_experts] device pointers) say where each expert's matrices are now, a slot or
+ * its host copy; a layer's rows of them are the expert stores the calls above take with stride 0.  The arena fields
+ * of the reference (slots lent to its K/V pool) have no counterpart: no pool here lends its slots. */
+#define SFNX_EC_POOLS 4
+#define SFNX_EC_LAYERS 128
+typedef struct sfnx_expert_cache {
+    int n_slots;                          /* all pools' */
+    int n_pools;
+    int n_layers, n_experts;              /* the tables' shape (the reference's NL, NEXP) */
+    int pool_of[SFNX_EC_LAYERS];          /* each layer's pool */
+    int s0[SFNX_EC_POOLS], n[SFNX_EC_POOLS];   /* a pool's slots: [s0, s0 + n) of the slot numbers */
+    size_t slot_bytes[SFNX_EC_POOLS], dn_off[SFNX_EC_POOLS];
+    void* pool[SFNX_EC_POOLS];            /* device: a pool's slots, slot_bytes apart */
+    const void** ep_gu;                   /* device [n_layers * n_experts]: where each expert's gate|up is now */
+    const void** ep_dn;
+    const void* const* host_gu;           /* device [n_layers * n_experts]: its host copy (device-visible address) */
+    const void* const* host_dn;
+    int* slot_of;                         /* device [n_layers * n_experts]: its slot, or -1 */
+    int* owner;                           /* device [n_slots]: the expert in it (layer * n_experts + e), or -1 */
+    unsigned char* ref;                   /* device [n_slots]: 0 free to take, 1 used since the hand passed, 2 the layer's */
+    int* hand;                            /* device [SFNX_EC_POOLS]: each pool's CLOCK hand, a slot number in it */
+} sfnx_expert_cache;
+
+/* page-locked host memory the GPU reads directly (the reference's mapped host copies): *host and *dev receive the host
+ * and device addresses of `bytes` bytes; sfnx_host_free releases them */
+int sfnx_host_alloc(size_t bytes, void** host, void** dev);
+int sfnx_host_free(void* host);
+/* src/moe.cuh:22-71 cache_plan (k_cache_plan, src/kernels.cu:1637): one wavefront plans the window's slots for layer
+ * `layer`: every job whose expert is in a slot keeps it; each other one takes the slot of the layer's pool that the
+ * pool's CLOCK hand reaches first with ref 0, a ref 1 it passes dropping to 0, 32 slots a sweep step as the reference's
+ * warp; the slot's old expert points back at its host copy.  list (1 + njobs ints) receives the number of experts
+ * that took a slot, then their ids (layer * n_experts + e), in job order.  A pool with fewer free slots than misses
+ * writes list[0] = -1 and leaves the misses unplanned (the reference would spin). */
+int sfnx_cache_plan(const sfnx_job* jobs, const int* njobs, int layer, const sfnx_expert_cache* ec, int* list, void* st);
+/* src/kernels.cu:1642-1658 k_cache_copy / cache_copy: the listed experts' matrices from their host copies into their
+ * slots of pool p */
+int sfnx_cache_copy(const sfnx_expert_cache* ec, int p, const int* list, void* st);
+/* src/kernels.cu:1659-1668 moe_cache: the plan (when jobs is given) and the copy for `layer`, after checking that the
+ * layer's expert strides are its pool's */
+int sfnx_moe_cache(int layer, size_t gu_stride, size_t dn_stride, const sfnx_expert_cache* ec, int* list,
+                   const sfnx_job* jobs, const int* njobs, void* st);
+
 #ifdef __cplusplus
 }
 #endif

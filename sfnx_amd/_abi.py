@@ -69,6 +69,11 @@ SIGNATURES = {
     "sfnx_gguf_str": (i32, [vp, C.c_char_p, vp]),
     "sfnx_gguf_moe_layer": (i32, [vp, i32, i32, i32, vp, sz, vp, sz, vp, vp, vp]),
     "sfnx_gguf_moe_layer_q8s": (i32, [vp, i32, i32, i32, vp, sz, vp, sz, vp, vp, vp, vp, vp]),
+    "sfnx_host_alloc": (i32, [sz, vp, vp]),
+    "sfnx_host_free": (i32, [vp]),
+    "sfnx_cache_plan": (i32, [vp, vp, i32, vp, vp, vp]),
+    "sfnx_cache_copy": (i32, [vp, i32, vp, vp]),
+    "sfnx_moe_cache": (i32, [i32, sz, sz, vp, vp, vp, vp, vp]),
 }
 
 
@@ -85,6 +90,18 @@ class LayerW(C.Structure):
 class SharedQ8s(C.Structure):
     """sfnx_moe_shared_q8s"""
     _fields_ = [("gu", vp), ("dn", vp)]
+
+
+EC_POOLS, EC_LAYERS = 4, 128
+
+
+class ExpertCacheC(C.Structure):
+    """sfnx_expert_cache"""
+    _fields_ = [("n_slots", i32), ("n_pools", i32), ("n_layers", i32), ("n_experts", i32),
+                ("pool_of", i32 * EC_LAYERS), ("s0", i32 * EC_POOLS), ("n", i32 * EC_POOLS),
+                ("slot_bytes", sz * EC_POOLS), ("dn_off", sz * EC_POOLS), ("pool", vp * EC_POOLS),
+                ("ep_gu", vp), ("ep_dn", vp), ("host_gu", vp), ("host_dn", vp),
+                ("slot_of", vp), ("owner", vp), ("ref", vp), ("hand", vp)]
 
 
 def declared_symbols() -> list[str]:

@@ -61,9 +61,9 @@ inline MoeShape& model_shape() {
 }
 inline void set_model_shape(const MoeShape& s) { model_shape() = s; }
 
-// src/model.hpp:98-120 ExpertCache (routed experts kept in host RAM): not supported by this library; the calls that
-// take one refuse a non-null pointer
-struct ExpertCache;
+// src/model.hpp:95-116 ExpertCache (routed experts kept in host RAM, VRAM slots for the ones in use): the C struct,
+// whose fields keep the reference's names (its arena fields, slots lent to a K/V pool, have no counterpart)
+using ExpertCache = sfnx_expert_cache;
 
 inline void ck(int status) {
     if (status != 0) throw std::runtime_error(sfnx_last_error());
@@ -118,7 +118,7 @@ inline void moe_gate_up(const DW& A, size_t sa, const Job* jobs, const int* njob
 // sh_* arguments, and its rows are part rows T TOPK + t.
 namespace detail {
 inline void no_cache(const ExpertCache* ec, const DW* w = nullptr) {
-    if (ec != nullptr) throw std::runtime_error("expert cache (routed experts in host RAM) is not supported by sfnx_amd");
+    (void) ec;
     (void) w;
 }
 // the window's rows from the job grid's size, as the reference's moe_mm does (src/kernels.cu:1931)
@@ -133,12 +133,19 @@ inline void router_route(const float* W, const float* x, float* logits, int T, i
                          Job* jobs_dn, int* njobs, void* st, const ExpertCache* ec = nullptr, int layer = -1,
                          int* list = nullptr, const Q8S* sh_gu = nullptr, int sh_rows = 0, const void* sh_y = nullptr,
                          float* sh_out = nullptr) {
-    (void) layer;
-    (void) list;
-    detail::no_cache(ec);
     const MoeShape& s = model_shape();
+    if (ec && (layer < 0 || !list)) throw std::runtime_error("router_route: a cache plan needs its layer and list");
     ck(sfnx_router_route(W, x, logits, T, s.H, s.E, s.K, topi, topw, jobs_gu, jobs_dn, njobs, 0, st));
+    // the reference plans in the router launch's last block; here the plan is the next launch on the stream
+    if (ec) ck(sfnx_cache_plan(jobs_gu, njobs, layer, ec, list, st));
     if (sh_gu) ck(sfnx_q8s_gemv(sh_gu->p, sh_rows, s.H, sh_y, sh_out, sh_rows, T, st));
+}
+// src/kernels.cu:1655-1668 cache_copy / moe_cache: the planned experts into their slots (moe_cache plans first when
+// given the jobs)
+inline void cache_copy(const ExpertCache& ec, int p, const int* list, void* st) { ck(sfnx_cache_copy(&ec, p, list, st)); }
+inline void moe_cache(int layer, size_t gu_stride, size_t dn_stride, const ExpertCache& ec, int* list, void* st,
+                      const Job* jobs = nullptr, const int* njobs = nullptr) {
+    ck(sfnx_moe_cache(layer, gu_stride, dn_stride, &ec, list, jobs, njobs, st));
 }
 // src/kernels.hpp:281-282: the shared expert's SwiGLU and down (sh_down: N rows of sh_ffs) from sh_gu ([T][2 sh_ffs])
 // into sh_out (row stride N), as the reference's fused launch computes them; T from njobs_max

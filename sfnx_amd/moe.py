@@ -570,3 +570,99 @@ def gguf_moe_layer(g: Gguf, layer: int, ff0: int = 0, ff1: int | None = None, K:
 
 
 __all__ = [n for n in dir() if not n.startswith("_")] + ["_abi"]
+
+
+# ---------------------------------------------------------------------------------------------------- expert cache
+class ExpertCache:
+    """src/model.hpp:95-116 ExpertCache over a stack of layers of one expert size: every expert (the shared one among
+    them when it is expert E of the stores) copied to page-locked host memory the GPU reads, n_slots VRAM slots in one
+    pool, the tables ep_gu / ep_dn pointing at each expert's host copy until a plan gives it a slot.  The slots start
+    empty (owner -1, ref 0), the hand at slot 0; the reference fills them at load with the hottest experts by a profile.
+    layer_view(l) is layer l with its stores replaced by its rows of the tables (stride 0)."""
+
+    def __init__(self, layers: list, n_slots: int, device="cuda"):
+        import copy
+        import numpy as np
+        L0 = layers[0]
+        self.layers, self.n_layers = layers, len(layers)
+        self.n_experts = L0.gu_w.numel() // L0.gu_stride
+        self.gu_bytes, self.dn_bytes = L0.gu_stride, L0.dn_stride
+        for L in layers:
+            if (L.gu_stride, L.dn_stride, L.gu_w.numel() // L.gu_stride) != (self.gu_bytes, self.dn_bytes, self.n_experts):
+                raise ValueError("one pool: every layer's experts must have the same sizes")
+        NL, E = self.n_layers, self.n_experts
+        self.slot_bytes = self.gu_bytes + self.dn_bytes
+        self.pool = torch.zeros(n_slots * self.slot_bytes, dtype=torch.uint8, device=device)
+        self._host = []
+        host_gu, host_dn = [], []
+        for L in layers:
+            for src, nbytes, dst in ((L.gu_w, self.gu_bytes, host_gu), (L.dn_w, self.dn_bytes, host_dn)):
+                h, d = C.c_void_p(), C.c_void_p()
+                check(lib().sfnx_host_alloc(E * nbytes, C.byref(h), C.byref(d)))
+                self._host.append(h.value)
+                arr = np.ctypeslib.as_array((C.c_uint8 * (E * nbytes)).from_address(h.value))
+                arr[:] = src[: E * nbytes].cpu().numpy()
+                dst += [d.value + e * nbytes for e in range(E)]
+        i64 = dict(dtype=torch.int64, device=device)
+        self.host_gu, self.host_dn = torch.tensor(host_gu, **i64), torch.tensor(host_dn, **i64)
+        self.ep_gu, self.ep_dn = self.host_gu.clone(), self.host_dn.clone()
+        self.slot_of = torch.full((NL * E,), -1, dtype=torch.int32, device=device)
+        self.owner = torch.full((n_slots,), -1, dtype=torch.int32, device=device)
+        self.ref = torch.zeros(n_slots, dtype=torch.uint8, device=device)
+        self.hand = torch.zeros(_abi.EC_POOLS, dtype=torch.int32, device=device)
+        c = _abi.ExpertCacheC()
+        c.n_slots, c.n_pools, c.n_layers, c.n_experts = n_slots, 1, NL, E
+        c.s0[0], c.n[0], c.slot_bytes[0], c.dn_off[0], c.pool[0] = 0, n_slots, self.slot_bytes, self.gu_bytes, _p(self.pool)
+        c.ep_gu, c.ep_dn, c.host_gu, c.host_dn = _p(self.ep_gu), _p(self.ep_dn), _p(self.host_gu), _p(self.host_dn)
+        c.slot_of, c.owner, c.ref, c.hand = _p(self.slot_of), _p(self.owner), _p(self.ref), _p(self.hand)
+        self.c = c
+        torch.cuda.synchronize()
+        self._views = []
+        for l, L in enumerate(layers):
+            v = copy.copy(L)
+            v.gu_w, v.gu_stride = self.ep_gu[l * E:(l + 1) * E], 0
+            v.dn_w, v.dn_stride = self.ep_dn[l * E:(l + 1) * E], 0
+            self._views.append(v)
+
+    def layer_view(self, l: int) -> "MoeLayer":
+        return self._views[l]
+
+    def plan(self, jobs, njobs, layer: int, out_list) -> None:
+        check(lib().sfnx_cache_plan(_p(jobs), _p(njobs), layer, C.byref(self.c), _p(out_list), _st()))
+
+    def copy(self, out_list) -> None:
+        check(lib().sfnx_cache_copy(C.byref(self.c), 0, _p(out_list), _st()))
+
+    def moe_cache(self, layer: int, out_list, jobs=None, njobs=None) -> None:
+        """src/kernels.cu:1659-1668 moe_cache: the plan (when jobs is given) and the copy-in"""
+        check(lib().sfnx_moe_cache(layer, self.gu_bytes, self.dn_bytes, C.byref(self.c), _p(out_list), _p(jobs), _p(njobs),
+                                   _st()))
+
+    def close(self) -> None:
+        torch.cuda.synchronize()
+        for h in self._host:
+            check(lib().sfnx_host_free(h))
+        self._host = []
+
+    def __del__(self):
+        try:
+            if self._host:
+                self.close()
+        except Exception:
+            pass
+
+
+def decode_layer_cached(cache: ExpertCache, l: int, x: torch.Tensor, y: torch.Tensor, b: DecodeBuffers, out_list) -> None:
+    """decode_layer with the layer's experts behind the expert cache (src/engine.cu:947-971): the routing, the window's
+    slots planned and the planned experts copied in (moe_cache), then the expert calls through the layer's tables"""
+    V = cache.layer_view(l)
+    s = V.s
+    T = x.shape[0]
+    quantize_q8_1(x, b.xq)
+    router_route(V.W, x, b.logits, b.topi, b.topw, b.jobs_gu, b.jobs_dn, b.njobs, s.E, s.K, s.shared and not s.sh_q8s)
+    cache.moe_cache(l, out_list, b.jobs_gu, b.njobs)
+    moe_gate_up(V.gu_w, 0, s.wtype, s.H, 2 * s.ff, b.jobs_gu, b.njobs, b.njobs_max, T, b.xq, b.gu)
+    moe_down(V.dn_w, 0, s.dn_type, s.ff, s.H, b.jobs_dn, b.njobs, b.njobs_max, T, b.gu, b.part)
+    if s.sh_q8s:
+        shared_q8s(V, T, b.xq, b.gu, b.sh_hq, b.part)
+    moe_combine(b.part, b.topw, b.topi, b.logits, y, s.E, s.K, s.shared)

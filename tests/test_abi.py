@@ -1,6 +1,7 @@
 """The C-ABI library: it loads, exports every symbol include/sfnx_moe.h declares, and rejects bad arguments with a
 status and a message before touching the GPU (src/kernels.cu:31-34 and src/moe.cuh:473-494 throw on the same)."""
 import ctypes as C
+from pathlib import Path
 
 import pytest
 
@@ -71,3 +72,20 @@ def test_cpp_header_compiles():
                             f"-I{root / 'include'}", "-I/opt/rocm/include", "-D__HIP_PLATFORM_AMD__", str(f)],
                            capture_output=True, text=True)
         assert r.returncode == 0, r.stderr
+
+
+def test_expert_cache_struct_layout_matches_the_header(tmp_path):
+    """the ctypes mirror of sfnx_expert_cache has the C compiler's size and field offsets"""
+    import ctypes as C
+    import subprocess
+    fields = [f[0] for f in _abi.ExpertCacheC._fields_]
+    src = tmp_path / "ec.c"
+    src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "sfnx_moe.h"\nint main(void) {\n'
+                   '  printf("%zu\\n", sizeof(sfnx_expert_cache));\n' +
+                   "".join(f'  printf("%zu\\n", offsetof(sfnx_expert_cache, {f}));\n' for f in fields) + "  return 0;\n}\n")
+    exe = tmp_path / "ec"
+    inc = Path(__file__).resolve().parents[1] / "include"
+    subprocess.run(["gcc", "-std=c99", "-I", str(inc), str(src), "-o", str(exe)], check=True)
+    out = [int(v) for v in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()]
+    assert out[0] == C.sizeof(_abi.ExpertCacheC)
+    assert out[1:] == [getattr(_abi.ExpertCacheC, f).offset for f in fields]

@@ -1,0 +1,88 @@
+"""The expert cache (src/moe.cuh:19-71, src/kernels.cu:1636-1668): routed experts in page-locked host memory, VRAM
+slots planned per decode window by one wavefront (CLOCK) and filled by the copy kernel.  Each window through the cached
+layer gives the same bits as the resident layer, and the device's plan (slots, owners, refs, hand, list) equals the
+CPU restatement's (oracle/cache.py) window after window, for a pool larger and one smaller than the 32-lane sweep."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from oracle.cache import PoolState, cache_plan
+from sfnx_amd import moe
+from tests.gpu_util import job_array, make_layer
+
+pytestmark = pytest.mark.gpu
+
+
+def bits(t):
+    return t.detach().cpu().numpy().view(np.uint32)
+
+
+@pytest.mark.parametrize("n_slots", [40, 24])
+def test_cached_decode_windows(n_slots):
+    shape = moe.LayerShape(H=1024, E=64, K=6, ff=512, wtype=orc.Q4_K, shared=True)
+    layers = [make_layer(shape, 90 + l)[0] for l in range(2)]
+    cache = moe.ExpertCache(layers, n_slots)
+    E1 = cache.n_experts
+    st = PoolState(len(layers), E1, n_slots)
+    lst = torch.zeros(1 + 16 * shape.K + 16, dtype=torch.int32, device="cuda")
+    rng = np.random.default_rng(n_slots)
+    try:
+        for w in range(24):
+            l = w % 2
+            T = int(rng.integers(1, 4))
+            x = torch.from_numpy(orc.synth(T * shape.H, 1000 + w, 1.0).reshape(T, shape.H)).cuda()
+            b0, b1 = moe.DecodeBuffers(shape, T), moe.DecodeBuffers(shape, T)
+            y0, y1 = torch.empty_like(x), torch.empty_like(x)
+            moe.decode_layer(layers[l], x, y0, b0)
+            moe.decode_layer_cached(cache, l, x, y1, b1, lst)
+            torch.cuda.synchronize()
+            assert np.array_equal(bits(y0), bits(y1)), f"window {w}"
+            nj = int(b1.njobs[0])
+            jobs = [int(v) for v in job_array(b1.jobs_gu)[:nj]["w"]]
+            taken = cache_plan(st, jobs, l)
+            assert taken is not None
+            got = lst.cpu().numpy()
+            assert got[0] == len(taken) and list(got[1:1 + len(taken)]) == taken, f"window {w}"
+            assert cache.slot_of.cpu().tolist() == st.slot_of
+            assert cache.owner.cpu().tolist() == st.owner
+            assert cache.ref.cpu().tolist() == st.ref
+            assert int(cache.hand[0]) == st.hand
+            # the tables: each expert at its slot or its host copy
+            epg, hg = cache.ep_gu.cpu().numpy(), cache.host_gu.cpu().numpy()
+            base = cache.pool.data_ptr()
+            for g, s in enumerate(st.slot_of):
+                want = base + s * cache.slot_bytes if s >= 0 else hg[g]
+                assert epg[g] == want
+    finally:
+        cache.close()
+
+
+def test_plan_reports_a_pool_too_small():
+    shape = moe.LayerShape(H=1024, E=64, K=6, ff=512, wtype=orc.Q4_K, shared=True)
+    layers = [make_layer(shape, 95)[0]]
+    cache = moe.ExpertCache(layers, 4)   # a window of 7 jobs cannot fit
+    lst = torch.zeros(64, dtype=torch.int32, device="cuda")
+    try:
+        x = torch.from_numpy(orc.synth(shape.H, 1100, 1.0).reshape(1, shape.H)).cuda()
+        b = moe.DecodeBuffers(shape, 1)
+        moe.quantize_q8_1(x, b.xq)
+        moe.router_route(layers[0].W, x, b.logits, b.topi, b.topw, b.jobs_gu, b.jobs_dn, b.njobs, shape.E, shape.K, True)
+        cache.plan(b.jobs_gu, b.njobs, 0, lst)
+        torch.cuda.synchronize()
+        assert int(lst[0]) == -1
+    finally:
+        cache.close()
+
+
+def test_moe_cache_refuses_a_layer_of_another_size():
+    shape = moe.LayerShape(H=1024, E=64, K=6, ff=512, wtype=orc.Q4_K, shared=True)
+    layers = [make_layer(shape, 96)[0]]
+    cache = moe.ExpertCache(layers, 8)
+    lst = torch.zeros(64, dtype=torch.int32, device="cuda")
+    try:
+        with pytest.raises(RuntimeError, match="pool's size"):
+            moe.check(moe.lib().sfnx_moe_cache(0, cache.gu_bytes + 16, cache.dn_bytes, moe.C.byref(cache.c), lst.data_ptr(),
+                                               None, None, moe._st()))
+    finally:
+        cache.close()
