@@ -51,6 +51,10 @@ def parse():
     ap.add_argument("--no-extra", action="store_true", help="skip configs 2 and 4 (verify window, Q8_0)")
     ap.add_argument("--q8-layers", type=int, default=24)
     ap.add_argument("--type-layers", type=int, default=12, help="stacked layers for the Q5_K / Q4_0 / Q5_1 decode lines")
+    ap.add_argument("--trace-summary", metavar="CSV",
+                    help="only summarise a rocprofv3 kernel trace (run_kernel_trace.csv) of the decode-only bench "
+                         "(--no-prefill --no-window --no-extra): each decode kernel's average duration over the timed "
+                         "graph replays and over the clocked eager passes, in the lines bench.py reads back from profiles/")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only copy 1 GiB device-to-device 3 times: the known-size kernel that scales rocprofv3's "
                          "FETCH_SIZE / WRITE_SIZE to bytes")
@@ -70,6 +74,8 @@ def shared_bytes(s, moe):
 
 def main():
     args = parse()
+    if args.trace_summary:
+        return trace_summary(args.trace_summary, args.layers)
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: every GPU box here has one, and no multi-GPU path is "
                                    "built (the path would shard by experts or by FF slices; this bench measures one GPU's share)", "n_gpus": args.gpus}))
@@ -180,6 +186,13 @@ def main():
                      "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "algorithmic_bytes_per_launch": alg[dom]},
     }
+    rp = rocprof_avg(names[dom])
+    if rp is not None:
+        # the same kernel's average from the committed rocprofv3 trace of the decode-only bench: over the same clocked
+        # eager passes, and over the timed graph replays (tracing adds its per-dispatch cost to both)
+        out["roofline"]["rocprof"] = {"source": "profiles/kernel_stats_decode48_q4k.md", "eager_avg_us": rp[0],
+                                      "graph_avg_us": rp[1], "frac_eager": round(alg[dom] / (rp[0] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                                      "frac_graph": round(alg[dom] / (rp[1] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
     cb = copy_bandwidth(torch)
     out["hbm_copy_gbs"] = cb
     out["hbm_frac_of_copy"] = round(gbs / cb, 4)
@@ -219,6 +232,44 @@ def copy_bandwidth(torch, nbytes=1 << 30, reps=10):
     del a, b
     torch.cuda.empty_cache()
     return round(2 * nbytes / best / 1e9, 1)
+
+
+DECODE_KERNELS = {"k_dec_router": "k_dec_router", "k_dec_experts1": "k_dec_experts", "k_dec_down1": "k_dec_down"}
+CLOCK_REPS = 3   # the eager passes bench.py clocks each decode kernel over, after the timed graph replays
+
+
+def trace_summary(path, NL):
+    """rocprofv3's per-dispatch kernel trace of the decode-only bench, split by regime: the clocked eager passes are each
+    decode kernel's last CLOCK_REPS x NL dispatches (they run after the timed loop), the rest are graph replays (plus
+    the warm pass).  Prints `rocprof <kernel> eager_avg_us E graph_avg_us G n_eager NE n_graph NG` lines."""
+    import csv
+    durs = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            name = DECODE_KERNELS.get(r["Kernel_Name"].split("(")[0])
+            if name:
+                durs.setdefault(name, []).append((int(r["Start_Timestamp"]), int(r["End_Timestamp"])))
+    ne = CLOCK_REPS * NL
+    for name, v in sorted(durs.items()):
+        v.sort()
+        d = [(e - s) / 1e3 for s, e in v]
+        eager, graph = d[-ne:], d[:-ne]
+        print(f"rocprof {name} eager_avg_us {sum(eager) / len(eager):.3f} graph_avg_us {sum(graph) / max(1, len(graph)):.3f} "
+              f"n_eager {len(eager)} n_graph {len(graph)}")
+    return 0
+
+
+def rocprof_avg(kernel):
+    """the committed rocprofv3 averages of a decode kernel (profiles/kernel_stats_decode48_q4k.md, lines written by
+    bench.py --trace-summary): (eager_avg_us, graph_avg_us) or None"""
+    p = ROOT / "profiles" / "kernel_stats_decode48_q4k.md"
+    if not p.exists():
+        return None
+    for line in p.read_text().splitlines():
+        f = line.split()
+        if len(f) >= 6 and f[0] == "rocprof" and f[1] == kernel:
+            return float(f[3]), float(f[5])
+    return None
 
 
 def measured_traffic(kernel):

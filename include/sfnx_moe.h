@@ -156,8 +156,8 @@ int sfnx_q8s_swiglu_gemv(const void* W, int rows, int ffs, const float* gu, floa
  * (row stride ldo) = sum_k f16(W[r][k]) xh[c][k] for C f16 rows xh [C][cols], fp32 accumulation.  W is a dense Q8_0
  * matrix (planar, one matrix), run as one expert of the matrix-core kernels (sfnx_moe_down_mma's): its f16 weights are
  * the reference's k_q8s_f16 values (f16(q d)), made in registers, and the products are summed in fp32 where the
- * reference calls cublasGemmEx.  wk (16-byte aligned, at least ceil(C / 64) * sizeof(sfnx_bigjob) + 4 bytes, the
- * caller's; the reference's f16 staging p.wh serves) holds the call's job list.  rows % 256 == 0, cols % 512 == 0. */
+ * reference calls cublasGemmEx; the C rows are taken 64 at a time.  wk / wk_bytes keep the reference's argument list
+ * (its f16 staging p.wh) and are not used.  rows % 256 == 0, cols % 512 == 0. */
 int sfnx_pf_dense(const void* W, int rows, int cols, const uint16_t* xh, int C, float* out, int ldo, void* wk,
                   size_t wk_bytes, void* st);
 

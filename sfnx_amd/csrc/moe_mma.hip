@@ -493,17 +493,33 @@ __global__ void __launch_bounds__(MM_THREADS) k_moe_mma_gu(const uint8_t* __rest
 // The other projections (down, and gate|up shapes the paired kernel does not take): blocks of DN_WAVES wavefronts,
 // two a compute unit when one run covers the input (one activation buffer), so one block's start (its activations
 // and first weights in flight) overlaps the other's work.
+// A dense matrix's prompt rows as the BigJobs of one "expert": job j takes rows 64 j .. 64 j + 63 of C to the same rows
+__device__ __forceinline__ void dense_job(sfnx_bigjob& jb, int j, int C) {
+    const int n = min(SFNX_PF_JOB, C - SFNX_PF_JOB * j);
+    for (int m = threadIdx.x; m < SFNX_PF_JOB; m += blockDim.x) {
+        const int t = m < n ? SFNX_PF_JOB * j + m : 0;
+        jb.y[m] = t;
+        jb.out[m] = t;
+    }
+    if (threadIdx.x == 0) {
+        jb.w = 0;
+        jb.n = n;
+    }
+}
+
 constexpr int DN_WAVES = 8, DN_THREADS = DN_WAVES * WAVE, DN_BM = 32 * DN_WAVES;
 template <int TYPE>
 __global__ void __launch_bounds__(DN_THREADS, 4) k_moe_mma(const uint8_t* __restrict__ A, size_t sa, int R, int C, int G,
                                                        const sfnx_bigjob* __restrict__ jobs, const int* __restrict__ njobs,
-                                                       const _Float16* __restrict__ x, float* __restrict__ out, int ldo) {
+                                                       const _Float16* __restrict__ x, float* __restrict__ out, int ldo,
+                                                       int dense_c) {
     int sl, ji;
     xcd_job(blockIdx.x, R / (G * DN_BM), sl, ji);
-    if (ji >= *njobs) return;
+    if (ji >= (dense_c > 0 ? (dense_c + SFNX_PF_JOB - 1) / SFNX_PF_JOB : *njobs)) return;
     __shared__ sfnx_bigjob jb;
     extern __shared__ __align__(16) unsigned char xs_raw[];
-    load_job(jb, jobs + ji);
+    if (dense_c > 0) dense_job(jb, ji, dense_c);
+    else load_job(jb, jobs + ji);
     __syncthreads();
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
     const uint8_t* mat = expert_at(A, sa, jb.w);
@@ -529,24 +545,11 @@ __global__ void k_to_f16(const float* __restrict__ x, _Float16* __restrict__ y, 
 
 constexpr size_t MM_LDS = 2 * MM_XBUF * sizeof(_Float16);
 
-// A dense matrix's prompt rows as BigJobs of one "expert": job j takes rows 64 j .. 64 j + 63 (of C) to the same rows
-__global__ void k_dense_jobs(sfnx_bigjob* __restrict__ jobs, int* __restrict__ njobs, int C) {
-    const int j = blockIdx.x, n = min(SFNX_PF_JOB, C - SFNX_PF_JOB * j);
-    for (int m = threadIdx.x; m < SFNX_PF_JOB; m += blockDim.x) {
-        const int t = m < n ? SFNX_PF_JOB * j + m : 0;
-        jobs[j].y[m] = t;
-        jobs[j].out[m] = t;
-    }
-    if (threadIdx.x == 0) {
-        jobs[j].w = 0;
-        jobs[j].n = n;
-        if (j == 0) *njobs = gridDim.x;
-    }
-}
 
-// out rows ldo floats apart (0: n_out); G: 256-row tiles a block walks (0: half of them, for routed jobs, which are many)
+// out rows ldo floats apart (0: n_out); G: 256-row tiles a block walks (0: half of them, for routed jobs, which are many);
+// dense_c > 0: no job list, the rows of one matrix (A) as jobs of 64 rows (dense_job)
 void moe_mma(uint32_t type, const void* A, size_t sa, int n_in, int n_out, const sfnx_bigjob* jobs, const int* njobs,
-             int njobs_cap, const void* x16, float* out, void* st, int ldo = 0, int G = 0) {
+             int njobs_cap, const void* x16, float* out, void* st, int ldo = 0, int G = 0, int dense_c = 0) {
     require(expert_type_ok(type), TYPE_MSG);
     require(n_in > 0 && n_in % 512 == 0, "expert input width must be a multiple of 512");
     require(n_out > 0 && n_out % DN_BM == 0, "expert rows must be a multiple of 256");
@@ -563,15 +566,15 @@ void moe_mma(uint32_t type, const void* A, size_t sa, int n_in, int n_out, const
     const size_t lds = (n_in == MM_RUN ? 1 : 2) * MM_XBUF * sizeof(_Float16);
     hipStream_t s = stream_of(st);
     if (type == SFNX_Q4_K)
-        k_moe_mma<SFNX_Q4_K><<<grid, DN_THREADS, lds, s>>>((const uint8_t*) A, sa, n_out, n_in, G, jobs, njobs, (const _Float16*) x16, out, ldo);
+        k_moe_mma<SFNX_Q4_K><<<grid, DN_THREADS, lds, s>>>((const uint8_t*) A, sa, n_out, n_in, G, jobs, njobs, (const _Float16*) x16, out, ldo, dense_c);
     else if (type == SFNX_Q5_K)
-        k_moe_mma<SFNX_Q5_K><<<grid, DN_THREADS, lds, s>>>((const uint8_t*) A, sa, n_out, n_in, G, jobs, njobs, (const _Float16*) x16, out, ldo);
+        k_moe_mma<SFNX_Q5_K><<<grid, DN_THREADS, lds, s>>>((const uint8_t*) A, sa, n_out, n_in, G, jobs, njobs, (const _Float16*) x16, out, ldo, dense_c);
     else if (type == SFNX_Q4_0)
-        k_moe_mma<SFNX_Q4_0><<<grid, DN_THREADS, lds, s>>>((const uint8_t*) A, sa, n_out, n_in, G, jobs, njobs, (const _Float16*) x16, out, ldo);
+        k_moe_mma<SFNX_Q4_0><<<grid, DN_THREADS, lds, s>>>((const uint8_t*) A, sa, n_out, n_in, G, jobs, njobs, (const _Float16*) x16, out, ldo, dense_c);
     else if (type == SFNX_Q5_1)
-        k_moe_mma<SFNX_Q5_1><<<grid, DN_THREADS, lds, s>>>((const uint8_t*) A, sa, n_out, n_in, G, jobs, njobs, (const _Float16*) x16, out, ldo);
+        k_moe_mma<SFNX_Q5_1><<<grid, DN_THREADS, lds, s>>>((const uint8_t*) A, sa, n_out, n_in, G, jobs, njobs, (const _Float16*) x16, out, ldo, dense_c);
     else
-        k_moe_mma<SFNX_Q8_0><<<grid, DN_THREADS, lds, s>>>((const uint8_t*) A, sa, n_out, n_in, G, jobs, njobs, (const _Float16*) x16, out, ldo);
+        k_moe_mma<SFNX_Q8_0><<<grid, DN_THREADS, lds, s>>>((const uint8_t*) A, sa, n_out, n_in, G, jobs, njobs, (const _Float16*) x16, out, ldo, dense_c);
 }
 
 void moe_mma_gu(uint32_t type, const void* A, size_t sa, int n_in, int ff, const sfnx_bigjob* jobs, const int* njobs,
@@ -649,22 +652,18 @@ extern "C" int sfnx_to_f16(const float* x, uint16_t* y, size_t n, void* st) {
 extern "C" int sfnx_pf_dense(const void* W, int rows, int cols, const uint16_t* xh, int C, float* out, int ldo, void* wk,
                              size_t wk_bytes, void* st) {
     return guarded("sfnx_pf_dense", [&] {
-        require(W != nullptr && xh != nullptr && out != nullptr && wk != nullptr, "null pointer");
+        require(W != nullptr && xh != nullptr && out != nullptr, "null pointer");
         require(rows > 0 && rows % DN_BM == 0 && cols > 0 && cols % MM_RUN == 0, "rows must be a multiple of 256, cols of 512");
         require(C >= 1 && C <= (1 << 20) && ldo >= rows, "C out of range, or ldo smaller than rows");
         // the reference dequantizes the matrix to f16 and multiplies in one f16 GEMM with fp32 results (pf_dense_xh,
         // cublasGemmEx); here the matrix is one expert of the matrix-core kernels, whose weights are the same f16
-        // values (hmul2(q, d)), dotted in fp32 on v_mfma_f32_32x32x16_f16.  The workspace holds the job list.
+        // values (hmul2(q, d)), dotted in fp32 on v_mfma_f32_32x32x16_f16, its rows the jobs of 64 rows each block
+        // makes for itself.  The workspace (the reference's f16 staging) is not needed.
+        (void) wk;
+        (void) wk_bytes;
         const int nj = (C + SFNX_PF_JOB - 1) / SFNX_PF_JOB;
-        const size_t jb_bytes = (size_t) nj * sizeof(sfnx_bigjob);
-        require(wk_bytes >= jb_bytes + sizeof(int), "workspace smaller than the job list (ceil(C / 64) jobs + 4 bytes)");
-        require(((uintptr_t) wk & 15) == 0, "workspace must be 16-byte aligned");
-        sfnx_bigjob* jobs = (sfnx_bigjob*) wk;
-        int* njobs = (int*) ((char*) wk + jb_bytes);
-        hipStream_t s = stream_of(st);
-        k_dense_jobs<<<nj, 64, 0, s>>>(jobs, njobs, C);
         const size_t sa = row_bytes(SFNX_Q8_0, cols) * (size_t) rows;
         // one 256-row tile a block: few jobs, so every tile is a block of its own
-        moe_mma(SFNX_Q8_0, W, sa, cols, rows, jobs, njobs, nj, xh, out, st, ldo, 1);
+        moe_mma(SFNX_Q8_0, W, sa, cols, rows, nullptr, nullptr, nj, xh, out, st, ldo, 1, C);
     });
 }

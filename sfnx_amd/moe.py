@@ -379,7 +379,7 @@ def prefill_route(L: "MoeLayer", x: torch.Tensor, b: "PrefillBuffers", bias: tor
 
 def pf_dense(W, rows: int, cols: int, xh, out, ldo: int, wh) -> None:
     """src/prefill.cu:407-417 pf_dense_xh: out rows (stride ldo) = f16(W) . xh rows, fp32, on the matrix-core kernels
-    (wh, the reference's f16 staging buffer, holds the call's job list)"""
+    (wh, the reference's f16 staging buffer, is kept in the argument list and not used)"""
     check(lib().sfnx_pf_dense(_p(W), rows, cols, _p(xh), xh.shape[0], _p(out), ldo, _p(wh), wh.numel() * wh.element_size(), _st()))
 
 

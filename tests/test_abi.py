@@ -42,7 +42,7 @@ def test_row_bytes():
     (lambda L: L.sfnx_q8s_gemv(1, 96, 2048, 1, 1, 64, 1, None), "out_stride"),
     (lambda L: L.sfnx_swiglu_stacked_q8_1(1, 1, 500, 1, None), "ffs must be"),
     (lambda L: L.sfnx_pf_dense(1, 1024, 2000, 1, 10, 1, 1024, 1, 1 << 30, None), "cols of 512"),
-    (lambda L: L.sfnx_pf_dense(1, 1024, 2048, 1, 10, 1, 1024, 1, 100, None), "workspace smaller"),
+    (lambda L: L.sfnx_pf_dense(1, 1000, 2048, 1, 10, 1, 1024, 1, 100, None), "multiple of 256"),
     (lambda L: L.sfnx_hc_read(1, None, None, 1, 1, 1, 1, 1, None, 1e-6, 1, None, None, 1, 2000, 4, 320, 1, 1 << 30, None), "N must be"),
     (lambda L: L.sfnx_hc_read(1, None, None, 1, 1, 1, 1, 1, None, 1e-6, 1, None, None, 1, 2560, 9, 320, 1, 1 << 30, None), "HC must be"),
     (lambda L: L.sfnx_hc_read(1, None, None, 1, 1, 1, 1, 1, None, 1e-6, 1, None, None, 1, 2560, 4, 330, 1, 1 << 30, None), "LR must be"),
