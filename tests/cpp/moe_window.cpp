@@ -6,6 +6,9 @@
 // argument lists exactly (src/kernels.hpp:276-305; N, NEXP, TOPK from set_model_shape).  Then a prompt chunk through
 // the prompt path's calls under the reference's names (router_logits, pf_route, moe_gate_up_mma, swiglu_h16,
 // moe_down_mma, the combine): equal bit for bit to the fused gate|up + SwiGLU form, and near the int8 BigJob form.
+// Then windows through an ExpertCache (the routed experts in page-locked host memory, VRAM slots planned by
+// router_route and filled by moe_cache, the expert calls reading the cache's tables through DW::ep), each equal bit
+// for bit to the same window through the resident store.
 // Prints "ok" when every check holds; exit status 1 otherwise.  Built by the package's build step; run by
 // tests/test_gpu_cpp.py.
 #include <hip/hip_runtime.h>
@@ -189,12 +192,111 @@ bool run_prompt() {
     return bad == 0 && rel < 5e-2;
 }
 
+// Windows through the expert cache, the engine's sequence (src/engine.cu:947-971) with `ec` live: router_route plans
+// the window's slots, moe_cache copies the planned experts in, moe_gate_up / moe_down read the tables (DW::ep)
+bool run_cached() {
+    const MoeShape s{1024, 64, 6};
+    const int ff = 512, T = 3, P = T * s.K, NP = P + T, n_slots = 24;
+    const uint32_t type = T_Q4_K;
+    set_model_shape(s);
+    const size_t gu_stride = 2 * (size_t) ff * sfnx_row_bytes(type, s.H), dn_stride = (size_t) s.H * sfnx_row_bytes(type, ff);
+    float* W = dev<float>((size_t) (s.E + 1) * s.H);
+    ck(sfnx_synth_normal(W, (size_t) (s.E + 1) * s.H, 31, 0, 0.02f, nullptr));
+    const DW gu_e{synth_store(type, s.E, 2 * ff, s.H, 32, 0), type, s.H, 2 * ff};
+    const DW dn_e{synth_store(type, s.E, s.H, ff, 33, 0), type, ff, s.H};
+    const Q8S sh_gu{synth_store(T_Q8_0, 1, 2 * ff, s.H, 32, (uint64_t) s.E * 2 * ff * s.H)};
+    const Q8S sh_dn{synth_store(T_Q8_0, 1, s.H, ff, 33, (uint64_t) s.E * s.H * ff)};
+    // the cache: host copies of every expert, one pool of n_slots empty slots, the tables at the host copies
+    void *hg = nullptr, *hgd = nullptr, *hd = nullptr, *hdd = nullptr;
+    ck(sfnx_host_alloc(gu_stride * s.E, &hg, &hgd));
+    ck(sfnx_host_alloc(dn_stride * s.E, &hd, &hdd));
+    hk(hipMemcpy(hg, gu_e.p, gu_stride * s.E, hipMemcpyDeviceToHost), "copy");
+    hk(hipMemcpy(hd, dn_e.p, dn_stride * s.E, hipMemcpyDeviceToHost), "copy");
+    std::vector<const void*> tg(s.E), td(s.E);
+    for (int e = 0; e < s.E; ++e) {
+        tg[e] = (const char*) hgd + (size_t) e * gu_stride;
+        td[e] = (const char*) hdd + (size_t) e * dn_stride;
+    }
+    ExpertCache ec{};
+    ec.n_slots = n_slots;
+    ec.n_pools = 1;
+    ec.n_layers = 1;
+    ec.n_experts = s.E;
+    ec.pool_of[0] = 0;
+    ec.s0[0] = 0;
+    ec.n[0] = n_slots;
+    ec.slot_bytes[0] = gu_stride + dn_stride;
+    ec.dn_off[0] = gu_stride;
+    ec.pool[0] = dev<uint8_t>((gu_stride + dn_stride) * n_slots);
+    const void** ep_gu = dev<const void*>(s.E);
+    const void** ep_dn = dev<const void*>(s.E);
+    const void** host_gu = dev<const void*>(s.E);
+    const void** host_dn = dev<const void*>(s.E);
+    for (const void** t : {ep_gu, host_gu}) hk(hipMemcpy(t, tg.data(), s.E * sizeof(void*), hipMemcpyHostToDevice), "copy");
+    for (const void** t : {ep_dn, host_dn}) hk(hipMemcpy(t, td.data(), s.E * sizeof(void*), hipMemcpyHostToDevice), "copy");
+    ec.ep_gu = ep_gu;
+    ec.ep_dn = ep_dn;
+    ec.host_gu = host_gu;
+    ec.host_dn = host_dn;
+    ec.slot_of = dev<int>(s.E);
+    ec.owner = dev<int>(n_slots);
+    hk(hipMemset(ec.slot_of, 0xff, s.E * sizeof(int)), "memset");
+    hk(hipMemset(ec.owner, 0xff, n_slots * sizeof(int)), "memset");
+    ec.ref = dev<unsigned char>(n_slots);
+    ec.hand = dev<int>(SFNX_EC_POOLS);
+    DW gu_c = gu_e, dn_c = dn_e;   // the layer's experts through the cache's tables
+    gu_c.p = dn_c.p = nullptr;
+    gu_c.ep = (const char* const*) ep_gu;
+    dn_c.ep = (const char* const*) ep_dn;
+    uint8_t* xq = dev<uint8_t>(q8_1_bytes(s.H) * T);
+    float* logits = dev<float>((size_t) T * (s.E + 1));
+    int* topi = dev<int>(P);
+    float* topw = dev<float>(P);
+    Job* jg = dev<Job>(P + 1);
+    Job* jd = dev<Job>(P + 1);
+    int* nj = dev<int>(2);
+    int* list = dev<int>(P + 2);
+    float* gu = dev<float>((size_t) NP * 2 * ff);
+    float* part = dev<float>((size_t) NP * s.H);
+    float* y0 = dev<float>((size_t) T * s.H);
+    float* y1 = dev<float>((size_t) T * s.H);
+    float* x = dev<float>((size_t) T * s.H);
+    size_t bad = 0;
+    int planned = 0;
+    for (int w = 0; w < 4; ++w) {
+        ck(sfnx_synth_normal(x, (size_t) T * s.H, 40 + w, 0, 1.0f, nullptr));
+        quantize_q8_1(x, xq, s.H, T, nullptr);
+        for (int cached = 0; cached < 2; ++cached) {
+            float* y = cached ? y1 : y0;
+            router_route(W, x, logits, T, topi, topw, jg, jd, nj, nullptr, cached ? &ec : nullptr, 0, list, &sh_gu, 2 * ff,
+                         xq, gu + (size_t) P * 2 * ff);
+            if (cached) moe_cache(0, gu_stride, dn_stride, ec, list, nullptr);
+            moe_gate_up(cached ? gu_c : gu_e, gu_stride, jg, nj, P, xq, gu, nullptr, &sh_dn, ff, gu + (size_t) P * 2 * ff,
+                        part + (size_t) P * s.H);
+            moe_down(cached ? dn_c : dn_e, dn_stride, jd, nj, P, gu, part, nullptr);
+            moe_combine(s, part, topw, topi, logits, y, T, nullptr);
+        }
+        hk(hipDeviceSynchronize(), "sync");
+        const std::vector<float> a = host(y0, (size_t) T * s.H), b = host(y1, (size_t) T * s.H);
+        for (size_t i = 0; i < a.size(); ++i) bad += std::memcmp(&a[i], &b[i], 4) != 0;
+        int n = 0;
+        hk(hipMemcpy(&n, list, sizeof(int), hipMemcpyDeviceToHost), "copy");
+        if (n < 0) ++bad;
+        planned += n;
+    }
+    ck(sfnx_host_free(hg));
+    ck(sfnx_host_free(hd));
+    std::printf("expert cache (%d slots for %d experts): 4 windows, %d experts copied in, %zu values differ from the resident store\n",
+                n_slots, s.E, planned, bad);
+    return bad == 0 && planned > 0;
+}
+
 }  // namespace
 
 int main() {
     try {
-        const bool a = run(0), b = run(1), c = run(2), d = run_prompt();
-        const bool ok = a && b && c && d;
+        const bool a = run(0), b = run(1), c = run(2), d = run_prompt(), e = run_cached();
+        const bool ok = a && b && c && d && e;
         std::printf("%s\n", ok ? "ok" : "MISMATCH");
         return ok ? 0 : 1;
     } catch (const std::exception& e) {

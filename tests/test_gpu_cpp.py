@@ -1,6 +1,8 @@
 """The C++ face (sfnx/kernels.hpp) from a C++ host program, as the reference engine would call it: a decode window
 through the unfused calls (with the shared expert as expert E, and as dense Q8_0 through router_route's and
-moe_gate_up's shared-expert arguments) against the fused decode, bit for bit (tests/cpp/moe_window.cpp)."""
+moe_gate_up's shared-expert arguments) against the fused decode, bit for bit; a prompt chunk through the prompt
+path's calls; and decode windows through an ExpertCache (router_route's plan, moe_cache, DW::ep tables) against the
+resident store, bit for bit (tests/cpp/moe_window.cpp)."""
 import subprocess
 from pathlib import Path
 
