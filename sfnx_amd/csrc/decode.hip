@@ -23,7 +23,6 @@ namespace {
 
 constexpr int D1_THREADS = 64, D1_WAVES = D1_THREADS / WAVE;   // K1: a router row per wavefront
 constexpr int D3_THREADS = 256, D3_ROWS = 8;                    // K3: output rows per block
-constexpr int D3W_THREADS = 512;                                 // K3 for windows of several rows
 template <int TYPE> constexpr int d2_threads() { return 32 * lpr_of<TYPE>(); }   // K2: 32 FF indices a block
 
 // ------------------------------------------------------------------------------------------------ K1
@@ -339,44 +338,53 @@ __global__ void __launch_bounds__(2 * d2_threads<TYPE>()) k_dec_experts1(
 
 // ------------------------------------------------------------------------------------------------ K3
 // (windows: 512 threads, twice the lane groups of the batch-1 kernel, so a group takes half the tasks)
-template <int TYPE, int G2, int NB>
-__global__ void __launch_bounds__(D3W_THREADS) k_dec_down(const uint8_t* __restrict__ A, size_t sa, int T, int H, int E, int K,
+template <int TYPE, int G2, int NB, int NT>
+__global__ void __launch_bounds__(NT) k_dec_down(const uint8_t* __restrict__ A, size_t sa, int T, int H, int E, int K,
                                                         int ff, int shared, const float* __restrict__ logits,
                                                         const int* __restrict__ topi, const float* __restrict__ topw,
                                                         const sfnx_job* __restrict__ jd, const int* __restrict__ njobs,
                                                         const int8_t* __restrict__ hq_q, const float* __restrict__ hq_d,
                                                         const int* __restrict__ hq_s, float* __restrict__ y,
                                                         float* __restrict__ x, int hq_in_lds, const uint8_t* __restrict__ sh_dn) {
-    constexpr int LPR = lpr_of<TYPE>(), GROUPS = D3W_THREADS / LPR;
+    constexpr int LPR = lpr_of<TYPE>(), GROUPS = NT / LPR;
     const int row0 = blockIdx.x * D3_ROWS, nj = njobs[0], P = T * K, NP = P + T, nbh = ff / 32;
     __shared__ int jw[MAX_P + 1], jn[MAX_P + 1], jout[MAX_P + 1][SFNX_MAXT];
     __shared__ float part[MAX_P + SFNX_MAXT][D3_ROWS];
     __shared__ int ti[MAX_P];
     __shared__ float tw[MAX_P], sg[SFNX_MAXT];
     extern __shared__ __align__(16) unsigned char lds[];   // every pair's h, when the launch gave room for it
-    for (int i = threadIdx.x; i < nj; i += D3W_THREADS) {
+    for (int i = threadIdx.x; i < nj; i += NT) {
         jw[i] = jd[i].w;
         jn[i] = jd[i].n;
         for (int s = 0; s < jd[i].n; ++s) jout[i][s] = jd[i].out[s];
     }
-    for (int i = threadIdx.x; i < P; i += D3W_THREADS) {
+    for (int i = threadIdx.x; i < P; i += NT) {
         ti[i] = topi[i];
         tw[i] = topw[i];
     }
     __shared__ float xr[SFNX_MAXT][D3_ROWS];   // the residual rows this block adds to, read with everything else
-    for (int i = threadIdx.x; i < T * D3_ROWS; i += D3W_THREADS) xr[i / D3_ROWS][i % D3_ROWS] = x[(size_t) (i / D3_ROWS) * H + row0 + i % D3_ROWS];
+    for (int i = threadIdx.x; i < T * D3_ROWS; i += NT) xr[i / D3_ROWS][i % D3_ROWS] = x[(size_t) (i / D3_ROWS) * H + row0 + i % D3_ROWS];
     if (shared)
-        for (int t = threadIdx.x; t < T; t += D3W_THREADS) sg[t] = sigm_f(logits[(size_t) t * (E + 1) + E]);
+        for (int t = threadIdx.x; t < T; t += NT) sg[t] = sigm_f(logits[(size_t) t * (E + 1) + E]);
     Acts a;
     const bool staged = hq_in_lds != 0;
     if (staged) {
+        // every pair's h into LDS by asynchronous global -> LDS copies, all issued before one wait (a copy loop through
+        // registers would wait for each of its ~11 rounds in turn): wavefront w copies chunks of 64 lanes, 16 bytes
+        // (values) or 4 bytes (scales, sums) a lane
         a = acts_in(lds, NP, ff);
-        const int4* src = reinterpret_cast<const int4*>(hq_q);
-        for (int i = threadIdx.x; i < NP * ff / 16; i += D3W_THREADS) reinterpret_cast<int4*>(a.q)[i] = src[i];
-        for (int i = threadIdx.x; i < NP * nbh; i += D3W_THREADS) {
-            a.d[i] = hq_d[i];
-            a.s[i] = hq_s[i];
-        }
+        const int wv = threadIdx.x / WAVE, ln64 = threadIdx.x % WAVE;
+        constexpr int NWV = NT / WAVE;
+        for (int c = wv; c * WAVE < NP * ff / 16; c += NWV)
+            if (c * WAVE + ln64 < NP * ff / 16)
+                __builtin_amdgcn_global_load_lds(hq_q + 16 * ((size_t) c * WAVE + ln64),
+                                                 (__attribute__((address_space(3))) void*) (a.q + 16 * (size_t) c * WAVE), 16, 0, 0);
+        for (int c = wv; c * WAVE < NP * nbh; c += NWV)
+            if (c * WAVE + ln64 < NP * nbh) {
+                __builtin_amdgcn_global_load_lds(hq_d + c * WAVE + ln64, (__attribute__((address_space(3))) void*) (a.d + c * WAVE), 4, 0, 0);
+                __builtin_amdgcn_global_load_lds(hq_s + c * WAVE + ln64, (__attribute__((address_space(3))) void*) (a.s + c * WAVE), 4, 0, 0);
+            }
+        __builtin_amdgcn_s_waitcnt(0);   // the copies landed (vmcnt), before the barrier below
     } else {
         a.q = const_cast<int8_t*>(hq_q);
         a.d = const_cast<float*>(hq_d);
@@ -419,7 +427,7 @@ __global__ void __launch_bounds__(D3W_THREADS) k_dec_down(const uint8_t* __restr
         }
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < T * D3_ROWS; i += D3W_THREADS) {
+    for (int i = threadIdx.x; i < T * D3_ROWS; i += NT) {
         const int t = i / D3_ROWS, r = i % D3_ROWS, row = row0 + r;
         float pw[MAX_K], pv[MAX_K];
 #pragma unroll
@@ -648,10 +656,13 @@ void launch_k3(const DecArgs& d, const sfnx_moe_layer_w& w, float* x, const DecL
     // every pair's h in LDS when it fits beside the kernel's own ~30 KB (160 KB a workgroup on gfx950; past 64 KB the
     // kernel must be allowed the larger dynamic size first), else read from L2 per task
     constexpr size_t HQ_LDS_MAX = 120 * 1024;
-    static bool big_lds = hipFuncSetAttribute((const void*) k_dec_down<TYPE, G2, NB>, hipFuncAttributeMaxDynamicSharedMemorySize,
+    // 1024 threads (4 wavefronts a SIMD: the per-pair dot chains are latency-bound) where 128 registers hold a lane's
+    // tasks (FF 512; not Q5_K, whose rows carry their fifth bits)
+    constexpr int NT = G2 == 1 && TYPE != SFNX_Q5_K ? 1024 : 512;
+    static bool big_lds = hipFuncSetAttribute((const void*) k_dec_down<TYPE, G2, NB, NT>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                               (int) HQ_LDS_MAX) == hipSuccess;
     const bool staged = hq_lds <= (big_lds ? HQ_LDS_MAX : 32 * 1024);
-    launch(2, k_dec_down<TYPE, G2, NB>, dim3(d.H / D3_ROWS), dim3(D3W_THREADS), staged ? hq_lds : 0, s,
+    launch(2, k_dec_down<TYPE, G2, NB, NT>, dim3(d.H / D3_ROWS), dim3(NT), staged ? hq_lds : 0, s,
         (const uint8_t*) w.dn, w.dn_stride, d.T, d.H, d.E, d.K, d.ff, d.shared, (const float*) (ws + L.logits),
         (const int*) (ws + L.topi), (const float*) (ws + L.topw), (const sfnx_job*) (ws + L.jd), (const int*) (ws + L.njobs),
         (const int8_t*) (ws + L.hq_q), (const float*) (ws + L.hq_d), (const int*) (ws + L.hq_s), (float*) (ws + L.y), x,
@@ -687,23 +698,23 @@ void launch_layer_tt(const DecArgs& d, const sfnx_moe_layer_w& w, float* x, cons
     }
 #undef SFNX_K2
     // down tasks a lane group loads together: every job's 8 rows in one batch at T = 1
-    constexpr int NB = TT == 1 ? 3 : 4;
+    constexpr int NB = TT == 1 ? 3 : 4, NB2 = NB;
     if (!(d.phases & 4)) return;
     if (d.dn_type == SFNX_Q4_K) {
         if (d.ff == 512) launch_k3<SFNX_Q4_K, 1, NB>(d, w, x, L, ws, s);
-        else launch_k3<SFNX_Q4_K, 2, NB>(d, w, x, L, ws, s);
+        else launch_k3<SFNX_Q4_K, 2, NB2>(d, w, x, L, ws, s);
     } else if (d.dn_type == SFNX_Q5_K) {
         if (d.ff == 512) launch_k3<SFNX_Q5_K, 1, NB>(d, w, x, L, ws, s);
-        else launch_k3<SFNX_Q5_K, 2, NB>(d, w, x, L, ws, s);
+        else launch_k3<SFNX_Q5_K, 2, NB2>(d, w, x, L, ws, s);
     } else if (d.dn_type == SFNX_Q4_0) {
         if (d.ff == 512) launch_k3<SFNX_Q4_0, 1, NB>(d, w, x, L, ws, s);
-        else launch_k3<SFNX_Q4_0, 2, NB>(d, w, x, L, ws, s);
+        else launch_k3<SFNX_Q4_0, 2, NB2>(d, w, x, L, ws, s);
     } else if (d.dn_type == SFNX_Q5_1) {
         if (d.ff == 512) launch_k3<SFNX_Q5_1, 1, NB>(d, w, x, L, ws, s);
-        else launch_k3<SFNX_Q5_1, 2, NB>(d, w, x, L, ws, s);
+        else launch_k3<SFNX_Q5_1, 2, NB2>(d, w, x, L, ws, s);
     } else {
         if (d.ff == 512) launch_k3<SFNX_Q8_0, 1, NB>(d, w, x, L, ws, s);
-        else launch_k3<SFNX_Q8_0, 2, NB>(d, w, x, L, ws, s);
+        else launch_k3<SFNX_Q8_0, 2, NB2>(d, w, x, L, ws, s);
     }
 }
 
