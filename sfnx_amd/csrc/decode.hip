@@ -116,8 +116,8 @@ __global__ void __launch_bounds__(DR_THREADS) k_dec_route(int T, int E, int K, i
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE, p = threadIdx.x, P = T * K;
     __shared__ int ex[MAX_P];
     __shared__ float sw[MAX_P];
-    __shared__ unsigned char first[MAX_P];
-    __shared__ int jobof[MAX_E];
+    __shared__ unsigned rows[MAX_E];
+    __shared__ int jobof[MAX_E], wsum[MAX_P / WAVE];
     for (int t = wave; t < T; t += NW) {
         int pick;
         float w;
@@ -129,7 +129,7 @@ __global__ void __launch_bounds__(DR_THREADS) k_dec_route(int T, int E, int K, i
     }
     __syncthreads();
     PickSlot ps;
-    const int nr = pick_slots(ex, P, first, jobof, ps);
+    const int nr = pick_slots(ex, P, K, rows, jobof, wsum, ps);
     if (p < P) {
         topi_g[p] = ex[p];
         topw_g[p] = sw[p];

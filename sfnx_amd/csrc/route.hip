@@ -88,10 +88,10 @@ __global__ void __launch_bounds__(RR_THREADS) k_router_route(const float* __rest
     __syncthreads();
     // jobs: a job per distinct expert in first-pick order, rows in pair order
     const int P = T * K;
-    __shared__ unsigned char first[MAX_P];
-    __shared__ int jobof[MAX_E];
+    __shared__ unsigned rows[MAX_E];
+    __shared__ int jobof[MAX_E], wsum[MAX_P / WAVE];
     PickSlot ps;
-    const int nr = pick_slots(ex, P, first, jobof, ps);
+    const int nr = pick_slots(ex, P, K, rows, jobof, wsum, ps);
     const int p = threadIdx.x;
     if (p < P && ps.e >= 0) {
         const int j = ps.job;

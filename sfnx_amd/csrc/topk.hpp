@@ -239,29 +239,38 @@ __device__ inline void topk_wave_e(const float* lg, int E, int K, int lane, int&
 struct PickSlot {
     int e = -1, slot = 0, cnt = 0, job = -1;
 };
-__device__ inline int pick_slots(const int* ex, int P, unsigned char* first, int* jobof, PickSlot& ps) {
-    const int p = threadIdx.x;
+// Each pick's slot in its expert's job: its rank among the picks of that expert (pair order), the job's row count, and
+// the job's index (jobs numbered by first pick, pair order).  A row picks an expert at most once, so an expert's picks
+// are told apart by their rows: a bit per row (T <= 32) in rows[e], the slot the bits below the pick's row.  The
+// first picks are numbered by wavefront ballots.  Every thread of the block calls it (three barriers); the block holds
+// at least P <= MAX_P threads; rows: MAX_E words of LDS, wsum: MAX_P / 64 ints of LDS.  Returns the number of jobs.
+__device__ inline int pick_slots(const int* ex, int P, int K, unsigned* rows, int* jobof, int* wsum, PickSlot& ps) {
+    const int p = threadIdx.x, lane = p % WAVE, wv = p / WAVE;
     ps = PickSlot{};
-    if (p < P) {
-        ps.e = ex[p];
-        if (ps.e >= 0)
-            for (int q = 0; q < P; ++q) {
-                const bool same = ex[q] == ps.e;
-                ps.slot += same && q < p;
-                ps.cnt += same;
-            }
-        first[p] = ps.e >= 0 && ps.slot == 0;
-    }
+    const int e = p < P ? ex[p] : -1;
+    if (e >= 0) rows[e] = 0u;
     __syncthreads();
-    if (p < P && first[p]) {
-        int j = 0;
-        for (int q = 0; q < p; ++q) j += first[q];
-        jobof[ps.e] = j;
-    }
-    int n = 0;
-    for (int q = 0; q < P; ++q) n += first[q];
+    if (e >= 0) atomicOr(&rows[e], 1u << (p / K));
     __syncthreads();
-    if (p < P && ps.e >= 0) ps.job = jobof[ps.e];
+    bool first = false;
+    if (e >= 0) {
+        const unsigned m = rows[e];
+        ps.e = e;
+        ps.slot = __popc(m & ((1u << (p / K)) - 1u));
+        ps.cnt = __popc(m);
+        first = ps.slot == 0;
+    }
+    const unsigned long long b = __ballot(first);
+    if (lane == 0 && wv < MAX_P / WAVE) wsum[wv] = __popcll(b);
+    __syncthreads();
+    int off = 0, n = 0;
+    for (int w = 0; w * WAVE < P; ++w) {
+        off += w < wv ? wsum[w] : 0;
+        n += wsum[w];
+    }
+    if (first) jobof[e] = off + __popcll(b & ((1ull << lane) - 1ull));
+    __syncthreads();
+    if (e >= 0) ps.job = jobof[e];
     return n;
 }
 
