@@ -176,9 +176,6 @@ __global__ void __launch_bounds__(2 * d2_threads<TYPE>()) k_dec_experts(
     if (myjob >= njobs_g[0]) return;
     load_job(jb, jg + myjob);
     __syncthreads();
-    // the job's rows of activations (slot s holds row jb.y[s])
-    const Acts a = acts_in(lds, TT, H);
-    stage_q8_1(a, xq, jb.y, jb.n);
     const bool up = wave >= NW / 2;
     const int rw = lane / LPR, ln = lane % LPR, fl = (up ? wave - NW / 2 : wave) * RPW + rw, row = (up ? ff : 0) + fb * 32 + fl;
     auto put = [&](int s, float v) {
@@ -187,14 +184,18 @@ __global__ void __launch_bounds__(2 * d2_threads<TYPE>()) k_dec_experts(
             (up ? ubuf : gbuf)[s][fl] = v;
         }
     };
-    if (sh_gu != nullptr && jb.w == E) {   // the shared expert's own dense Q8_0 matrix, the reference's q8s sums
+    // the weight rows are requested first, then the job's rows of activations staged (slot s holds row jb.y[s]): the
+    // two fetches overlap instead of following each other
+    const bool dense_sh = sh_gu != nullptr && jb.w == E;   // the shared expert's own dense Q8_0 matrix
+    typename RowOf<TYPE, G>::R w;
+    if (!dense_sh) RowOf<TYPE, G>::load(w, expert_at(A, sa, jb.w), 2 * ff, row, H, ln);
+    const Acts a = acts_in(lds, TT, H);
+    stage_q8_1(a, xq, jb.y, jb.n);
+    __syncthreads();   // the staged activations
+    if (dense_sh) {   // the reference's q8s sums
         const Q80Planes Ps = q80_planes(sh_gu, 2 * ff, H);
-        __syncthreads();
         for (int s = 0; s < jb.n; ++s) put(s, group_sum<LPR>(q8s_dot<LPR>(Ps, row, H, ln, a, s)));
     } else {
-        typename RowOf<TYPE, G>::R w;
-        RowOf<TYPE, G>::load(w, expert_at(A, sa, jb.w), 2 * ff, row, H, ln);
-        __syncthreads();   // the staged activations
         for (int s = 0; s < jb.n; ++s) put(s, group_sum<LPR>(w.dot(a, s, ln)));
     }
     __syncthreads();
