@@ -101,8 +101,11 @@ __global__ void __launch_bounds__(256) k_cache_copy(sfnx_expert_cache ec, int p,
         const int k = (int) (i / per), g = list[1 + k];
         const size_t o = i % per;
         char* at = static_cast<char*>(ec.pool[p]) + (size_t) (ec.slot_of[g] - ec.s0[p]) * ec.slot_bytes[p];
-        if (o < ug) reinterpret_cast<uint4*>(at)[o] = reinterpret_cast<const uint4*>(ec.host_gu[g])[o];
-        else reinterpret_cast<uint4*>(at + ec.dn_off[p])[o - ug] = reinterpret_cast<const uint4*>(ec.host_dn[g])[o - ug];
+        // the host copies' table entries read as global-memory pointers (loads through them global, not flat)
+        const auto* hg = reinterpret_cast<const global_u8_ptr*>(ec.host_gu);
+        const auto* hd = reinterpret_cast<const global_u8_ptr*>(ec.host_dn);
+        if (o < ug) reinterpret_cast<uint4*>(at)[o] = reinterpret_cast<const uint4*>((const uint8_t*) hg[g])[o];
+        else reinterpret_cast<uint4*>(at + ec.dn_off[p])[o - ug] = reinterpret_cast<const uint4*>((const uint8_t*) hd[g])[o - ug];
     }
 }
 

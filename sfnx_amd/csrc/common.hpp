@@ -143,17 +143,39 @@ __device__ __forceinline__ float load_agent(const float* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// ------------------------------------------------------------------------------------------------ L2 warm-up
-// Workgroup i of a launch runs on XCD i % 8, each XCD has its own 4 MB L2, and the L2 keeps clean lines across kernel
-// boundaries: a later launch's workgroup reads lines that an earlier launch's workgroup of the same XCD read from L2
-// instead of HBM.  A kernel warms lines for a later one by loading one dword of each 128-byte line straight into LDS
-// (global_load_lds: no register is written, the load cannot be dropped or moved); warm_wait() before the wavefront
-// ends, because the LDS it writes belongs to the workgroup.  `junk` is 256 bytes of LDS whose contents nobody reads.
-constexpr int XCDS = 8, LINE = 128;
-__device__ __forceinline__ void warm_line(const void* p, void* junk) {
-    __builtin_amdgcn_global_load_lds(p, (__attribute__((address_space(3))) void*) junk, 4, 0, 0);
+// ------------------------------------------------------------------------------------------------ async LDS copies
+// Global -> LDS copies (global_load_lds) issued as inline assembly, so the compiler does not track them: it tracks such
+// copies per wavefront, not per LDS object, and with one in flight it makes the next LDS read wait for every vector
+// memory operation in flight (vmcnt(0)), which would drain weight requests issued long before.  The caller waits for
+// its copies itself (vm_wait, then lds_barrier for other wavefronts' copies).  lds: wave-uniform; lane l's bytes land
+// at lds + BYTES l.
+template <int BYTES> __device__ __forceinline__ void lds_copy_async(const void* g, const void* lds) {
+    static_assert(BYTES == 4 || BYTES == 16, "4 or 16 bytes a lane");
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+        (uint32_t) reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*) lds));
+    if constexpr (BYTES == 16)
+        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0) : "memory", "m0");
+    else
+        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(m0) : "memory", "m0");
 }
-__device__ __forceinline__ void warm_wait() { __builtin_amdgcn_s_waitcnt(0); }
+// vmcnt(N), the other counters unwaited, as a compiler memory barrier (no memory access moves across it)
+template <int N> __device__ __forceinline__ void vm_wait() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// the workgroup barrier after this wavefront's LDS operations, without the wait for vector memory that __syncthreads'
+// fence adds; a compiler memory barrier
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// ------------------------------------------------------------------------------------------------ warm-up
+// Workgroup i of a launch runs on XCD i % 8.  A kernel warms lines for a later launch by loading one dword of each
+// 128-byte line straight into LDS (no register is written, the load cannot be dropped or moved).  Measured: the lines
+// are not in the L2 a kernel boundary later, but in the MALL behind it, which still serves them faster than HBM.
+// warm_wait() before the wavefront ends, because the LDS it writes belongs to the workgroup.  `junk` is 256 bytes of
+// LDS whose contents nobody reads.
+constexpr int XCDS = 8, LINE = 128;
+__device__ __forceinline__ void warm_line(const void* p, void* junk) { lds_copy_async<4>(p, junk); }
+__device__ __forceinline__ void warm_wait() { vm_wait<0>(); }
 
 // ------------------------------------------------------------------------------------------------ planar store
 // Per matrix of R rows (a multiple of 32) x C columns, each plane of the store is tiled by RT rows and cut into 16-byte
@@ -237,9 +259,13 @@ __host__ __device__ constexpr bool is_kquant(uint32_t type) { return type == SFN
 inline int block_values(uint32_t type) { return is_kquant(type) ? 256 : 32; }
 // Expert e's matrix of a store (src/moe_w.cuh:9 moe_expert): base + e * sa, or, when sa is 0, the device table of
 // expert pointers at `base` (the reference's DW::ep, src/model.hpp:85-86: each expert wherever it lives, a VRAM slot or
-// mapped page-locked host memory).  sa is a kernel argument, so the branch is uniform.
+// mapped page-locked host memory).  sa is a kernel argument, so the branch is uniform.  The table's entries are read
+// as global-memory pointers: a pointer loaded from memory is otherwise generic, and every load through it a flat
+// load, which the compiler can only wait for with vmcnt(0) and lgkmcnt(0).
+typedef const __attribute__((address_space(1))) uint8_t* global_u8_ptr;
 __device__ __forceinline__ const uint8_t* expert_at(const uint8_t* base, size_t sa, int e) {
-    return sa ? base + (size_t) e * sa : reinterpret_cast<const uint8_t* const*>(base)[e];
+    if (sa) return base + (size_t) e * sa;
+    return (const uint8_t*) reinterpret_cast<const global_u8_ptr*>(base)[e];
 }
 // a store's stride as the launchers check it: sa == 0 is the pointer table, else at least one matrix
 inline bool stride_ok(size_t sa, size_t matrix_bytes) { return sa == 0 || sa >= matrix_bytes; }

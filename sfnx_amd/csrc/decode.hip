@@ -311,7 +311,9 @@ __global__ void __launch_bounds__(2 * d2_threads<TYPE>()) k_dec_experts1(
         warm_wait();
         return;
     }
-    __syncthreads();   // the staged activations
+    // the staged activations; no memory fence, so each row's groups are dotted as they arrive (the compiler waits for
+    // each one) instead of after all of them
+    lds_barrier();
     float v;
     if constexpr (SHR) v = group_sum<LPR>(q8s ? ws.dot(a, 0, ln) : wr.dot1(a, ln));
     else if constexpr (SHQ) v = group_sum<LPR>(q8s ? q8s_dot<LPR>(q80_planes(sh_gu, 2 * ff, H), row, H, ln, a, 0) : wr.dot1(a, ln));
@@ -386,16 +388,14 @@ __global__ void __launch_bounds__(NT) k_dec_down(const uint8_t* __restrict__ A, 
                 __builtin_amdgcn_global_load_lds(hq_s + c * WAVE + ln64, (__attribute__((address_space(3))) void*) (a.s + c * WAVE), 4, 0, 0);
             }
         __builtin_amdgcn_s_waitcnt(0);   // the copies landed (vmcnt), before the barrier below
-    } else {
-        a.q = const_cast<int8_t*>(hq_q);
-        a.d = const_cast<float*>(hq_d);
-        a.s = const_cast<int*>(hq_s);
-        a.K = ff;
     }
     __syncthreads();
     const int g = threadIdx.x / LPR, ln = threadIdx.x % LPR;
     // with its own dense Q8_0 matrix the shared expert's job (the last) runs apart, in the reference's q8s sums
     const int nq = sh_dn != nullptr && shared ? nj - 1 : nj, ntask = nq * D3_ROWS;
+    // the dots, inlined once for h in LDS and once for h in global memory: a pointer that may be either is generic,
+    // and every load through it a flat load
+    auto dots = [&](const Acts& a) __attribute__((always_inline)) {
     if (nq < nj) {
         const Q80Planes Ps = q80_planes(sh_dn, H, ff);
         for (int task = g; task < T * D3_ROWS; task += GROUPS) {
@@ -427,6 +427,9 @@ __global__ void __launch_bounds__(NT) k_dec_down(const uint8_t* __restrict__ A, 
             }
         }
     }
+    };
+    if (staged) dots(a);
+    else dots(Acts{const_cast<int8_t*>(hq_q), const_cast<float*>(hq_d), const_cast<int*>(hq_s), ff});
     __syncthreads();
     for (int i = threadIdx.x; i < T * D3_ROWS; i += NT) {
         const int t = i / D3_ROWS, r = i % D3_ROWS, row = row0 + r;

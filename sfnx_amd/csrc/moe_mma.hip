@@ -166,10 +166,14 @@ __device__ __forceinline__ void load_tail(Chunk<SFNX_Q5_1>& w, const ChunkAt& a)
     w.qh = *reinterpret_cast<const uint4*>(a.qh);
 }
 __device__ __forceinline__ void load_tail(Chunk<SFNX_Q8_0>& w, const ChunkAt& a) { w.d = *reinterpret_cast<const uint32_t*>(a.tail); }
+template <int TYPE> constexpr bool tail_early();
+// a chunk's requests in the order mma_chunk's refill makes them, so the compiler's count of requests in flight is the
+// same for each slot on entry to the walk as on every later chunk, and its waits can count exactly
 template <int TYPE> __device__ __forceinline__ void load_chunk(Chunk<TYPE>& w, const ChunkAt& a) {
+    if constexpr (tail_early<TYPE>()) load_tail(w, a);
 #pragma unroll
     for (int s = 0; s < Chunk<TYPE>::STEPS; ++s) load_piece(w, a, s);
-    load_tail(w, a);
+    if constexpr (!tail_early<TYPE>()) load_tail(w, a);
 }
 
 // The 8 sub-blocks' f16(d sc) and f16(-(dmin m)) of a K-quant super-block header, all at once: the 6-bit values of
@@ -276,25 +280,8 @@ __device__ __forceinline__ void load_x_async(_Float16* buf, const _Float16* __re
 #pragma unroll
     for (int i = 0; i < XR; ++i) {
         const int m = wave * XR + i;
-        if (m < n)
-            __builtin_amdgcn_global_load_lds(x + (size_t) ys[m] * ldx + MM_RUN * r + 8 * lane,
-                                             (__attribute__((address_space(3))) void*) (buf + (size_t) m * MM_XLD), 16, 0, 0);
+        if (m < n) lds_copy_async<16>(x + (size_t) ys[m] * ldx + MM_RUN * r + 8 * lane, buf + (size_t) m * MM_XLD);
     }
-}
-__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }   // vmcnt(0), others unwaited
-// vmcnt(N), others unwaited (N < 64: bits 3:0 and 15:14)
-template <int N> __device__ __forceinline__ void wait_vmem_below() {
-    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
-}
-
-// The block barrier at a run start, without the memory fence of __syncthreads: the fence waits for every vector memory
-// operation of the wavefront (vmcnt(0)), which would drain the weight chunks in flight at every run.  The activation
-// copies a run waits for were checked by the explicit vmcnt above; the previous run's LDS reads all fed matrix
-// instructions before the barrier, so only LDS operations (lgkmcnt) are waited here.
-__device__ __forceinline__ void run_barrier() {
-    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0); vmcnt and expcnt unwaited
-    __builtin_amdgcn_s_barrier();
 }
 
 // One chunk's steps on one wavefront's 32 weight rows: per step the 4 B fragments are dequantized from the registers
@@ -341,6 +328,7 @@ __device__ __forceinline__ void chunk_walk(const uint8_t* mat, int R, int C, int
                                            const int* ys, int n, const _Float16* __restrict__ x, _Float16* xs,
                                            float16v (&acc)[NT], TileDone tile_done) {
     constexpr int CPR = 8 / Chunk<TYPE>::STEPS, LD = Chunk<TYPE>::LOADS;
+    static_assert(CPR % MM_SLOTS == 0, "a run's chunks fill the register slots evenly, so every slot steps every time");
     const int h = lane / 32, nn = lane % 32, nr = C / MM_RUN, per_tile = nr * CPR, NK = tiles * per_tile;
     auto at = [&](int k) {
         const int it = k / per_tile, rc = k % per_tile;
@@ -358,10 +346,13 @@ __device__ __forceinline__ void chunk_walk(const uint8_t* mat, int R, int C, int
         const int rc = k % per_tile, r = rc / CPR, cj = rc % CPR, rg = k / CPR;   // rg: runs walked so far
         _Float16* xb = xs + (size_t) (nr > 1 ? rg & 1 : 0) * MM_XBUF;
         if (cj == 0 && (nr > 1 || k == 0)) {
-            // this run's rows: requested before the weight requests of the CPR chunks since
-            if (k == 0) wait_vmem();
-            else wait_vmem_below<CPR * LD>();
-            run_barrier();                    // every wavefront's rows landed; every wavefront is past the previous run
+            // this run's rows: requested before the weight requests of the CPR chunks since (the copies are not
+            // tracked by the compiler, so this wait is theirs).  Then the block barrier without the memory fence of
+            // __syncthreads, which would drain the weight chunks in flight: every wavefront's rows landed, and every
+            // wavefront's reads of the previous run's buffer fed its matrix instructions
+            if (k == 0) vm_wait<0>();
+            else vm_wait<CPR * LD>();
+            lds_barrier();
             if (nr > 1 && k + per_tile / nr < NK) load_x_async<W>(xs + (size_t) ((rg + 1) & 1) * MM_XBUF, x, C, ys, n, (r + 1) % nr, wave, lane);
         }
         mma_chunk<TYPE, NT>(w, cj, xb, nn, h, acc, at(min(k + MM_SLOTS, NK - 1)));
@@ -373,12 +364,7 @@ __device__ __forceinline__ void chunk_walk(const uint8_t* mat, int R, int C, int
     };
     for (int k0 = 0; k0 < NK; k0 += MM_SLOTS) {
 #pragma unroll
-        for (int i = 0; i < MM_SLOTS; ++i) {
-            const int k = k0 + i;
-            if (k < NK) {
-                step(w[i], k);   // refills w[i] with chunk k + MM_SLOTS
-            }
-        }
+        for (int i = 0; i < MM_SLOTS; ++i) step(w[i], k0 + i);   // refills w[i] with chunk k + MM_SLOTS
     }
 }
 
