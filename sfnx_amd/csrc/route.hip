@@ -170,9 +170,7 @@ __global__ void __launch_bounds__(LT_THREADS) k_router_logits(const float* __res
         for (int k = 0; k < COPIES; ++k) {
             const int c = (k * LT_WAVES + wave) * WAVE, u = c / (H / 4), col = c % (H / 4);
             const int t = t0 + min(g * LT_RU + u, nt - 1);
-            __builtin_amdgcn_global_load_lds(x + (size_t) t * H + 4 * (col + lane),
-                                             (__attribute__((address_space(3))) void*) (xs + (size_t) ((g % LT_NBUF) * LT_RU + u) * H + 4 * col),
-                                             16, 0, 0);
+            lds_copy_async<16>(x + (size_t) t * H + 4 * (col + lane), xs + (size_t) ((g % LT_NBUF) * LT_RU + u) * H + 4 * col);
         }
     };
     float4 wv[RT][NC];
@@ -182,9 +180,12 @@ __global__ void __launch_bounds__(LT_THREADS) k_router_logits(const float* __res
         if (g < ng) stage(g);
     for (int g = 0; g < ng; ++g) {
         // group g's copies landed: the ones issued after it (groups g + 1 .. g + LT_NBUF - 2) may still be in flight
-        if (g + LT_NBUF - 2 < ng) __builtin_amdgcn_s_waitcnt(0x0F70 | (COPIES * (LT_NBUF - 2)));
-        else __builtin_amdgcn_s_waitcnt(0x0F70);
-        __syncthreads();   // every wavefront's copies landed; every wavefront is past group g - 1, whose buffer refills
+        // (the logits stores issued since only make this wait longer).  The barrier has no memory fence, which would
+        // wait for those too: every wavefront's copies of group g landed; every wavefront is past group g - 1, whose
+        // buffer refills
+        if (g + LT_NBUF - 2 < ng) vm_wait<COPIES * (LT_NBUF - 2)>();
+        else vm_wait<0>();
+        lds_barrier();
         if (g + LT_NBUF - 1 < ng) stage(g + LT_NBUF - 1);
         const float4* xb = reinterpret_cast<const float4*>(xs + (size_t) (g % LT_NBUF) * LT_RU * H);
         float acc[NV];
