@@ -267,6 +267,21 @@ __device__ __forceinline__ const uint8_t* expert_at(const uint8_t* base, size_t 
     if (sa) return base + (size_t) e * sa;
     return (const uint8_t*) reinterpret_cast<const global_u8_ptr*>(base)[e];
 }
+// N experts' matrices at once.  With a pointer table, every entry is requested and then waited for here, inside the
+// table's branch: a table load left in flight past the branch would make the compiler wait for every earlier vector
+// memory request at each later use on both sides (it cannot count a load issued on one side of a branch only).
+// (global-memory pointers: the caller may pass them to statements the compiler cannot see into and still have its
+// loads through them global)
+template <int N> __device__ __forceinline__ void experts_at(const uint8_t* base, size_t sa, const int (&e)[N], global_u8_ptr (&m)[N]) {
+    if (sa) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) m[i] = (global_u8_ptr) base + (size_t) e[i] * sa;
+    } else {
+#pragma unroll
+        for (int i = 0; i < N; ++i) m[i] = reinterpret_cast<const global_u8_ptr*>(base)[e[i]];
+        __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): the entries (and whatever was requested before them)
+    }
+}
 // a store's stride as the launchers check it: sa == 0 is the pointer table, else at least one matrix
 inline bool stride_ok(size_t sa, size_t matrix_bytes) { return sa == 0 || sa >= matrix_bytes; }
 

@@ -451,8 +451,9 @@ __global__ void __launch_bounds__(NT) k_dec_down(const uint8_t* __restrict__ A, 
 }
 
 // K3 for a window of one row: pair k is pick k, so a task's expert comes straight from the picks (job j = pick j, the
-// shared expert's job last) and its weight loads are issued before the activations are staged; every other request
-// of the block (picks, weights, the shared gate's logit, h, the residual rows) is issued up front, with one wait.
+// shared expert's job last).  Every request of the block is issued up front, with one wait: h straight into LDS by
+// untracked asynchronous copies (first, so no register holds it and no later wait depends on where the compiler puts
+// its loads), the picks, the shared gate's logit, the residual rows, then the weight rows of the picks.
 template <int TYPE, int G2, int NB, bool SHQ, int NT3>
 __global__ void __launch_bounds__(NT3) k_dec_down1(const uint8_t* __restrict__ A, size_t sa, int H, int E, int K,
                                                          int ff, int shared, const float* __restrict__ logits,
@@ -462,30 +463,27 @@ __global__ void __launch_bounds__(NT3) k_dec_down1(const uint8_t* __restrict__ A
                                                          float* __restrict__ x, const int* __restrict__ route_x,
                                                          const uint8_t* __restrict__ sh_dn) {
     constexpr int LPR = lpr_of<TYPE>(), GROUPS = NT3 / LPR;
-    // every pair's h (at most 17 rows of 1024) in registers: int4 quants and (scale, sum) words a thread
-    constexpr int HQ4 = (17 * 1024 / 16 + NT3 - 1) / NT3, HQS = (17 * 32 + NT3 - 1) / NT3;
     const int row0 = blockIdx.x * D3_ROWS, nbh = ff / 32, lane = threadIdx.x % WAVE, tid = threadIdx.x;
     const int g = tid / LPR, ln = tid % LPR;
     __shared__ float part[MAX_K + 1][D3_ROWS];
     extern __shared__ __align__(16) unsigned char lds[];
-    // every request first; the picks from the copy K2 left in this XCD's L2
+    const int NP = K + 1, nq = NP * ff / 16, ns = NP * nbh;
+    // every pair's h into LDS: 16 bytes of quants a lane, then the (scale, sum) words, wavefront w moving chunks
+    // w, w + NT3 / 64, ... of 64 lanes
+    const Acts a = acts_in(lds, NP, ff);
+    for (int c = tid / WAVE; c * WAVE < nq; c += NT3 / WAVE)
+        if (c * WAVE + lane < nq) lds_copy_async<16>(hq_q + 16 * ((size_t) c * WAVE + lane), a.q + 16 * (size_t) c * WAVE);
+    for (int c = tid / WAVE; c * WAVE < ns; c += NT3 / WAVE)
+        if (c * WAVE + lane < ns) {
+            lds_copy_async<4>(hq_d + c * WAVE + lane, a.d + c * WAVE);
+            lds_copy_async<4>(hq_s + c * WAVE + lane, a.s + c * WAVE);
+        }
+    // the picks from the copy K2 left for this XCD
     const int* rx = route_x + (blockIdx.x % XCDS) * 2 * MAX_K;
     const int tp = lane < K ? rx[lane] : -1;
     const float twv = lane < K ? __int_as_float(rx[MAX_K + lane]) : 0.f;
     const float gl = shared ? logits[E] : 0.f;
     const float xr = tid < D3_ROWS ? x[row0 + tid] : 0.f;
-    const int NP = K + 1, nq = NP * ff / 16, ns = NP * nbh;
-    int4 hv[HQ4];
-    float dv[HQS];
-    int sv[HQS];
-#pragma unroll
-    for (int r = 0; r < HQ4; ++r) hv[r] = reinterpret_cast<const int4*>(hq_q)[min(tid + r * NT3, nq - 1)];
-#pragma unroll
-    for (int r = 0; r < HQS; ++r) {
-        const int i = min(tid + r * NT3, ns - 1);
-        dv[r] = hq_d[i];
-        sv[r] = hq_s[i];
-    }
     // the picks, then this group's weight rows: task (j, r) = job j's row row0 + r
     const int nr = __popcll(__ballot(lane < K && tp >= 0)), nj = nr + (shared ? 1 : 0), ntask = nj * D3_ROWS;
     typename RowOf<TYPE, G2>::R w[NB];
@@ -496,7 +494,13 @@ __global__ void __launch_bounds__(NT3) k_dec_down1(const uint8_t* __restrict__ A
         ex[b] = __shfl(tp, j < nr ? j : 0);
         pp[b] = j < nr ? j : K;
     }
-    // a dense shared expert's task (at most one a lane group: its 8 tasks are consecutive) from its own rows
+    // a dense shared expert's task (at most one a lane group: its 8 tasks are consecutive) from its own rows.  Every
+    // task's matrix first (with a pointer table, every entry requested before one wait for all)
+    global_u8_ptr mats[NB];
+    int exb[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) exb[b] = pp[b] < K ? ex[b] : E;
+    experts_at<NB>(A, sa, exb, mats);
     Q8sRow<LPR, SHQ ? G2 : 1> wsh;
     int bsh = -1;
 #pragma unroll
@@ -506,21 +510,17 @@ __global__ void __launch_bounds__(NT3) k_dec_down1(const uint8_t* __restrict__ A
             wsh.issue(q80_planes(sh_dn, H, ff), row0 + r, ff, ln);
             bsh = b;
         } else if (task < ntask) {
-            RowOf<TYPE, G2>::issue(w[b], expert_at(A, sa, pp[b] < K ? ex[b] : E), H, row0 + r, ff, ln);
+            RowOf<TYPE, G2>::issue(w[b], (const uint8_t*) mats[b], H, row0 + r, ff, ln);
         }
     }
-    // the staged activations
-    const Acts a = acts_in(lds, NP, ff);
-    // (unconditional: a thread past the end writes the last element's own value again, so no load sinks into a branch)
+    // The matrices' addresses escape into an empty statement that may write memory, so no weight load moves below it
+    // (the compiler may otherwise sink a load to its use, past the wait, and issue it only then); the one wait (h and
+    // every request above), then the barrier for the other wavefronts' copies of h
 #pragma unroll
-    for (int r = 0; r < HQ4; ++r) reinterpret_cast<int4*>(a.q)[min(tid + r * NT3, nq - 1)] = hv[r];
-#pragma unroll
-    for (int r = 0; r < HQS; ++r) {
-        const int i = min(tid + r * NT3, ns - 1);
-        a.d[i] = dv[r];
-        a.s[i] = sv[r];
-    }
-    __syncthreads();
+    for (int b = 0; b < NB; ++b) asm volatile("" ::"v"(mats[b]) : "memory");
+    if constexpr (SHQ) asm volatile("" ::"v"((global_u8_ptr) sh_dn) : "memory");
+    vm_wait<0>();
+    lds_barrier();
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
         const int task = g + b * GROUPS;

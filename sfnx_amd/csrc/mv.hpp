@@ -162,7 +162,7 @@ template <int GPL, bool Q5 = false> struct Q4kRow {
 // ------------------------------------------------------------------------------------------------ Q8_0
 template <int BPL> struct Q80Row {
     uint4 qa[BPL], qb[BPL];
-    uint16_t dh[BPL];
+    uint32_t dh[BPL];   // (32-bit: a 16-bit register half would be filled by a load that waits for the other half's)
     float dw[BPL];
     template <typename PL> __device__ __forceinline__ void issue(const PL& P, int row, int C, int l16) {
 #pragma unroll
@@ -174,7 +174,12 @@ template <int BPL> struct Q80Row {
     }
     __device__ __forceinline__ void prepare(int) {
 #pragma unroll
-        for (int i = 0; i < BPL; ++i) dw[i] = h2f(dh[i]);
+        for (int i = 0; i < BPL; ++i) {
+            // (opaque: the conversion stays here, where the caller put it, instead of rising to the load and making
+            // every later request of the caller wait for this one)
+            asm volatile("" : "+v"(dh[i]));
+            dw[i] = h2f((uint16_t) dh[i]);
+        }
     }
     __device__ __forceinline__ void load(const Q80Planes& P, int row, int C, int l16) {
         issue(P, row, C, l16);
