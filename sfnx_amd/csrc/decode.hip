@@ -216,11 +216,13 @@ __global__ void __launch_bounds__(2 * d2_threads<TYPE>()) k_dec_experts(
 
 // K1's workgroup b' owns the router rows [D1_WAVES b', D1_WAVES b' + D1_WAVES), on XCD b' % 8.  Workgroup b of a launch
 // whose grid is a multiple of 8 warms the next layer's router rows of the K1 workgroups b' = b (mod the grid).
-__device__ inline void warm_router_rows(const float* W, int rows, int H, void* junk) {
+// NTH: the block's threads, a constant (blockDim.x is read from memory, and in this loop the read was repeated and
+// waited for, with every warm-up request before it, at each turn)
+template <int NTH> __device__ inline void warm_router_rows(const float* W, int rows, int H, void* junk) {
     if (W == nullptr || gridDim.x % XCDS != 0) return;
     const int per_row = H * 4 / LINE, per_blk = D1_WAVES * per_row, nk1 = (rows + D1_WAVES - 1) / D1_WAVES;
     const int mine = (nk1 - (int) blockIdx.x + (int) gridDim.x - 1) / (int) gridDim.x;
-    for (int li = threadIdx.x; li < mine * per_blk; li += blockDim.x) {
+    for (int li = threadIdx.x; li < mine * per_blk; li += NTH) {
         const int b1 = blockIdx.x + gridDim.x * (li / per_blk), row = D1_WAVES * b1 + (li % per_blk) / per_row;
         if (row < rows) warm_line(reinterpret_cast<const uint8_t*>(W + (size_t) row * H) + LINE * (li % per_row), junk);
     }
@@ -261,7 +263,7 @@ __global__ void __launch_bounds__(2 * d2_threads<TYPE>()) k_dec_experts1(
     const Acts a = acts_in(lds, 1, H);
     stage_q8_1(a, xq, nullptr, 1);
     // the next layer's router rows into this XCD's L2 for that layer's K1, while HBM idles through the top-k
-    warm_router_rows(Wn, E + 1, H, junk);
+    warm_router_rows<2 * d2_threads<TYPE>()>(Wn, E + 1, H, junk);
     int pick;
     uint32_t pord;
     topk_picks<NV>(lv, K, lane, pick, pord);
