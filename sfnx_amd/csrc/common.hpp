@@ -147,18 +147,17 @@ __device__ __forceinline__ float load_agent(const float* p) {
 // Global -> LDS copies (global_load_lds) issued as inline assembly, so the compiler does not track them: it tracks such
 // copies per wavefront, not per LDS object, and with one in flight it makes the next LDS read wait for every vector
 // memory operation in flight (vmcnt(0)), which would drain weight requests issued long before.  The caller waits for
-// its copies itself (vm_wait, then lds_barrier for other wavefronts' copies; both are compiler memory barriers, so no
-// read of the copied bytes moves above them).  The copy itself declares no memory effect: with one, every value the
-// compiler keeps in memory (the work-group size, the job's rows in LDS) would be read again after each copy, and the
-// read waited for with every copy in flight.  lds: wave-uniform; lane l's bytes land at lds + BYTES l.
+// its copies itself (vm_wait, then lds_barrier for other wavefronts' copies).  The copy is a compiler memory barrier
+// as well, so values the compiler keeps in memory are read again after it: read blockDim.x and the like before a loop
+// of copies.  lds: wave-uniform; lane l's bytes land at lds + BYTES l.
 template <int BYTES> __device__ __forceinline__ void lds_copy_async(const void* g, const void* lds) {
     static_assert(BYTES == 4 || BYTES == 16, "4 or 16 bytes a lane");
     const uint32_t m0 = __builtin_amdgcn_readfirstlane(
         (uint32_t) reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*) lds));
     if constexpr (BYTES == 16)
-        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0) : "m0");
+        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0) : "memory", "m0");
     else
-        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(m0) : "m0");
+        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(m0) : "memory", "m0");
 }
 // vmcnt(N), the other counters unwaited, as a compiler memory barrier (no memory access moves across it)
 template <int N> __device__ __forceinline__ void vm_wait() {
