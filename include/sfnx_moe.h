@@ -90,7 +90,9 @@ int sfnx_quantize_q8_1(const float* x, void* q, int n, int rows, void* st);
  * write topi -1, topw 0 and leave the pair out of the jobs. */
 int sfnx_router_route(const float* W, const float* x, float* logits, int T, int H, int E, int K, int* topi, float* topw,
                       sfnx_job* jobs_gu, sfnx_job* jobs_dn, int* njobs, int shared, void* st);
-/* the router's logits alone, [T][L] = W [L][H] . x[t], any T (the prompt path's sgemm, src/prefill.cu:1163) */
+/* the router's logits alone, [T][L] = W [L][H] . x[t], any T (the prompt path's sgemm, src/prefill.cu:1163).  From
+ * 512 tokens on the fp32 matrix cores: each of 8 slices of H / 8 columns one fmaf chain, the slices added in order;
+ * fewer tokens in sfnx_router_route's order.  H % 256 == 0. */
 int sfnx_router_logits(const float* W, const float* x, float* logits, int T, int H, int L, void* st);
 /* src/prefill.cu:189-279 (k_pf_top10, k_pf_count, k_pf_jobbase, k_pf_fill): top-K of rows of E + 1 logits, cnt[E],
  * jbase[E] (exclusive scan of ceil(cnt / 64)), BigJobs of each expert's pairs in pair order.  shared != 0: ceil(C/64)

@@ -449,6 +449,34 @@ void orc_router_logits(const float* W, const float* x, float* logits, int T, int
         for (int t = 0; t < T; ++t) logits[(size_t) t * L + r] = router_dot(W + (size_t) r * H, x + (size_t) t * H, H);
 }
 
+/* src/prefill.cu:1163 (the prompt path's router sgemm) in the matrix-core kernel's order (see oracle.h) */
+static float router_dot_mm(const float* w, const float* x, int H) {
+    const int KW = H / 8;
+    float sum = 0.f;
+    for (int s = 0; s < 8; ++s) {
+        float p = 0.f;
+        for (int j = 0; j < KW / 16; ++j)
+            for (int i = 0; i < 4; ++i)
+                for (int g = 0; g < 4; ++g) {
+                    const int k = s * KW + 16 * j + 4 * g + i;
+                    p = fmaf(x[k], w[k], p);
+                }
+        sum = s == 0 ? p : sum + p;
+    }
+    return sum;
+}
+
+void orc_router_logits_mm(const float* W, const float* x, float* logits, int T, int H, int L) {
+#pragma omp parallel for schedule(static)
+    for (int r = 0; r < L; ++r)
+        for (int t = 0; t < T; ++t) logits[(size_t) t * L + r] = router_dot_mm(W + (size_t) r * H, x + (size_t) t * H, H);
+}
+
+void orc_router_logits_prompt(const float* W, const float* x, float* logits, int T, int H, int L) {
+    if (T >= ORC_ROUTER_MM_MIN_T) orc_router_logits_mm(W, x, logits, T, H, L);
+    else orc_router_logits(W, x, logits, T, H, L);
+}
+
 int orc_topk(const float* logits, int T, int E, int ld, int K, int* topi, float* topw) {
     int missing = 0;
     unsigned char* taken = (unsigned char*) malloc((size_t) E);
@@ -701,8 +729,8 @@ static size_t row_bytes(int type, int cols) {
 }
 
 /* ------------------------------------------------------------------------------------------------ the layer */
-void orc_layer_decode(const orc_layer* L, const float* x, int T, float* y, float* logits_out, int* topi_out,
-                      float* topw_out, float* gu_out, float* part_out, int nthreads) {
+static void layer_impl(const orc_layer* L, const float* x, int T, float* y, float* logits_out, int* topi_out,
+                       float* topw_out, float* gu_out, float* part_out, int nthreads, int prompt) {
     const int H = L->H, E = L->E, K = L->K, ff = L->ff, P = T * K, NP = P + (L->shared ? T : 0);
     const size_t gurb = row_bytes(L->type, H), dnrb = row_bytes(L->dn_type, ff);
     uint8_t* xq = (uint8_t*) malloc((size_t) T * (H / 32) * ORC_Q81_BYTES);
@@ -719,7 +747,9 @@ void orc_layer_decode(const orc_layer* L, const float* x, int T, float* y, float
     orc_quantize_q8_1(x, xq, H, T);
 #pragma omp parallel for schedule(static) if (nthreads > 1)
     for (int r = 0; r < E + 1; ++r)
-        for (int t = 0; t < T; ++t) logits[(size_t) t * (E + 1) + r] = router_dot(L->W + (size_t) r * H, x + (size_t) t * H, H);
+        for (int t = 0; t < T; ++t)
+            logits[(size_t) t * (E + 1) + r] = prompt && T >= ORC_ROUTER_MM_MIN_T ? router_dot_mm(L->W + (size_t) r * H, x + (size_t) t * H, H)
+                                                      : router_dot(L->W + (size_t) r * H, x + (size_t) t * H, H);
     orc_topk(logits, T, E, E + 1, K, topi, topw);
     for (int p = 0; p < NP; ++p) pe[p] = p < P ? topi[p] : E;
     const int64_t ngu = (int64_t) NP * 2 * ff;
@@ -793,6 +823,15 @@ static double now_us(void) {
 static int cmp_d(const void* a, const void* b) {
     const double x = *(const double*) a, y = *(const double*) b;
     return x < y ? -1 : x > y;
+}
+
+void orc_layer_decode(const orc_layer* L, const float* x, int T, float* y, float* logits, int* topi, float* topw,
+                      float* gu, float* part, int nthreads) {
+    layer_impl(L, x, T, y, logits, topi, topw, gu, part, nthreads, 0);
+}
+void orc_layer_prompt(const orc_layer* L, const float* x, int T, float* y, float* logits, int* topi, float* topw,
+                      float* gu, float* part, int nthreads) {
+    layer_impl(L, x, T, y, logits, topi, topw, gu, part, nthreads, 1);
 }
 double orc_time_layer_decode(const orc_layer* L, const float* x, int nthreads, int reps, size_t sweep_bytes, float* y) {
     double* t = (double*) malloc((size_t) reps * sizeof(double));

@@ -88,6 +88,16 @@ void orc_quantize_q8_1(const float* x, void* q, int n, int rows);
  * under fast-math contraction cannot be recovered, src/moe.cuh:80-120): 64 lanes, lane l takes the float4 chunks
  * l, l + 64, ... as an fmaf chain, then a xor butterfly 32, 16, 8, 4, 2, 1. */
 void orc_router_logits(const float* W, const float* x, float* logits, int T, int H, int L);
+/* The prompt path's router logits (src/prefill.cu:1163, the engine's sgemm) in the order of the HIP matrix-core
+ * kernel, H % 128 == 0: the hidden dimension in 8 slices of H / 8; slice s is one fmaf chain from 0 over
+ * k = s H / 8 + 16 j + 4 g + i in the order j, i, g (j the step of 16 columns, i = 0..3, g = 0..3: a chain of
+ * v_mfma_f32_16x16x4_f32, which sums its 4 k-slots as fmaf in slot order g); the logit is
+ * ((((((p0 + p1) + p2) + p3) + p4) + p5) + p6) + p7. */
+void orc_router_logits_mm(const float* W, const float* x, float* logits, int T, int H, int L);
+/* sfnx_router_logits: chunks of ORC_ROUTER_MM_MIN_T tokens or more in the matrix-core order, fewer in the VALU
+ * kernel's (orc_router_logits) */
+#define ORC_ROUTER_MM_MIN_T 512
+void orc_router_logits_prompt(const float* W, const float* x, float* logits, int T, int H, int L);
 
 /* Top-k per row, src/moe.cuh:128-162 / src/prefill.cu:191-221: k rounds of the largest untaken logit among the first
  * E of each row (stride ld), ties to the lower index, NaN and -inf never taken; weight exp(l - l_top1) / sum.
@@ -142,6 +152,10 @@ typedef struct {
     const uint8_t* sh_dn;   /* dense q8s rows (orc_dot_q8s); its down [H][ff] likewise.  Else it is expert E of gu_w / dn_w */
 } orc_layer;
 void orc_layer_decode(const orc_layer* L, const float* x, int T, float* y, float* logits, int* topi, float* topw,
+                      float* gu, float* part, int nthreads);
+/* orc_layer_decode with the prompt path's router order (orc_router_logits_prompt): a chunk through the layer as the
+ * prompt-path kernels route it */
+void orc_layer_prompt(const orc_layer* L, const float* x, int T, float* y, float* logits, int* topi, float* topw,
                       float* gu, float* part, int nthreads);
 
 /* The f16 tensor-core path (src/moe_mma.cuh, src/prefill.cu:1164-1168) in float64: out[r] = sum_k w16[r][k] x16[k]

@@ -78,6 +78,8 @@ def lib() -> C.CDLL:
             "orc_dequant_q8_0_f16": (None, [vp, vp, i64, i32]),
             "orc_quantize_q8_1": (None, [vp, vp, i32, i32]),
             "orc_router_logits": (None, [vp, vp, vp, i32, i32, i32]),
+            "orc_router_logits_mm": (None, [vp, vp, vp, i32, i32, i32]),
+            "orc_router_logits_prompt": (None, [vp, vp, vp, i32, i32, i32]),
             "orc_topk": (i32, [vp, i32, i32, i32, i32, vp, vp]),
             "orc_jobs_decode": (i32, [vp, i32, i32, i32, i32, vp, vp]),
             "orc_jobs_prefill": (i32, [vp, i32, i32, i32, i32, vp, vp, vp, vp]),
@@ -85,6 +87,7 @@ def lib() -> C.CDLL:
             "orc_dot_q8_0": (f32, [vp, vp, i32]),
             "orc_swiglu_q8_1": (None, [vp, i32, vp]),
             "orc_layer_decode": (None, [C.POINTER(Layer), vp, i32, vp, vp, vp, vp, vp, vp, i32]),
+            "orc_layer_prompt": (None, [C.POINTER(Layer), vp, i32, vp, vp, vp, vp, vp, vp, i32]),
             "orc_mma_matvec": (None, [vp, i32, i32, i32, vp, vp]),
             "orc_swiglu_h16": (None, [vp, i32, vp]),
             "orc_time_layer_decode": (C.c_double, [C.POINTER(Layer), vp, i32, i32, sz, vp]),
@@ -163,6 +166,28 @@ def router_logits(W: np.ndarray, x: np.ndarray) -> np.ndarray:
     T = x.shape[0]
     out = np.empty((T, L), np.float32)
     lib().orc_router_logits(_p(W), _p(np.ascontiguousarray(x)), _p(out), T, H, L)
+    return out
+
+
+def router_logits_mm(W: np.ndarray, x: np.ndarray) -> np.ndarray:
+    """the prompt path's router logits in the matrix-core kernel's summation order"""
+    L, H = W.shape
+    T = x.shape[0]
+    out = np.empty((T, L), np.float32)
+    lib().orc_router_logits_mm(_p(W), _p(np.ascontiguousarray(x)), _p(out), T, H, L)
+    return out
+
+
+ROUTER_MM_MIN_T = 512   # oracle.h ORC_ROUTER_MM_MIN_T
+
+
+def router_logits_prompt(W: np.ndarray, x: np.ndarray) -> np.ndarray:
+    """sfnx_router_logits' order for this many tokens: the matrix-core order from ROUTER_MM_MIN_T tokens, else the
+    VALU kernel's (router_logits)"""
+    L, H = W.shape
+    T = x.shape[0]
+    out = np.empty((T, L), np.float32)
+    lib().orc_router_logits_prompt(_p(W), _p(np.ascontiguousarray(x)), _p(out), T, H, L)
     return out
 
 
@@ -257,8 +282,9 @@ class LayerWeights:
                        int(shared), self.dn_type, _p(self.sh_gu), _p(self.sh_dn))
 
 
-def layer_decode(L: LayerWeights, x: np.ndarray, nthreads: int = 0):
-    """Returns y, logits, topi, topw, gu, part (src/engine.cu:933-978's MoE half for T tokens)."""
+def layer_decode(L: LayerWeights, x: np.ndarray, nthreads: int = 0, prompt: bool = False):
+    """Returns y, logits, topi, topw, gu, part (src/engine.cu:933-978's MoE half for T tokens); prompt: routed with the
+    prompt path's router order (router_logits_prompt)."""
     T = x.shape[0]
     NP = T * L.K + (T if L.shared else 0)
     y = np.empty((T, L.H), np.float32)
@@ -268,7 +294,8 @@ def layer_decode(L: LayerWeights, x: np.ndarray, nthreads: int = 0):
     gu = np.zeros((NP, 2 * L.ff), np.float32)
     part = np.zeros((NP, L.H), np.float32)
     x = np.ascontiguousarray(x, np.float32)
-    lib().orc_layer_decode(C.byref(L.c), _p(x), T, _p(y), _p(logits), _p(topi), _p(topw), _p(gu), _p(part), nthreads)
+    fn = lib().orc_layer_prompt if prompt else lib().orc_layer_decode
+    fn(C.byref(L.c), _p(x), T, _p(y), _p(logits), _p(topi), _p(topw), _p(gu), _p(part), nthreads)
     return y, logits, topi, topw, gu, part
 
 

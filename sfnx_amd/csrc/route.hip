@@ -119,7 +119,6 @@ __global__ void __launch_bounds__(RR_THREADS) k_router_route(const float* __rest
     }
 }
 
-// any number of tokens: a wavefront per row and token block of up to 8 tokens (the prompt path's router)
 // The xor butterfly of group_sum<64> applied to NV partial sums a lane at once, by recursive halving: at the level of
 // lane bit b a lane keeps the half of its values selected by that bit and adds its partner's copy of them, so each
 // value meets exactly the partners (and tree) group_sum would give it.  Lane l ends with value l >> (6 - log2 NV), in
@@ -144,7 +143,7 @@ template <int NV> __device__ __forceinline__ float reduce_scatter(float (&v)[NV]
     return v[0];
 }
 
-// Prompt-path router logits [T][L] = W x, each (token, row) with row_dot's arithmetic (lane l's fmaf chain over its
+// Prompt-path router logits [T][L] = W x for chunks under RM_MIN_T tokens, each (token, row) with row_dot's arithmetic (lane l's fmaf chain over its
 // float4 chunks l + 64 i, then the xor butterfly), register-blocked: a wavefront keeps RT router rows in registers and
 // takes the block's tokens LT_RU at a time from LDS, where the block stages them by asynchronous global -> LDS copies
 // into LT_NBUF buffers (LT_NBUF - 1 groups in flight while one computes); the RT x LT_RU sums of a lane leave through
@@ -211,6 +210,94 @@ __global__ void __launch_bounds__(LT_THREADS) k_router_logits(const float* __res
         constexpr int SH = NV == 16 ? 2 : NV == 8 ? 3 : 4;   // lane l holds value l >> SH
         const int k = lane >> SH, q = k / LT_RU, u = k % LT_RU, t = g * LT_RU + u;
         if ((lane & ((1 << SH) - 1)) == 0 && row0 + q < L && t < nt) logits[(size_t) (t0 + t) * L + row0 + q] = v;
+    }
+}
+
+// The prompt path's router logits [T][L] = W x (src/prefill.cu:1163, the engine's sgemm) on the fp32 matrix cores, for
+// chunks of RM_MIN_T tokens or more (fewer leave most compute units idle; they take k_router_logits above).
+// v_mfma_f32_16x16x4_f32 adds its 4 k-slots to the accumulator as fmaf in slot order (measured bit for bit on gfx950),
+// so a chain of them is an fmaf chain whose order the CPU restatement can follow exactly.  A workgroup owns 32 tokens x
+// 64 router rows (2 x 4 tiles of 16 x 16) and its 8 wavefronts split the hidden dimension into 8 slices of H / 8: a
+// wavefront's lane (m, g) = (lane % 16, lane / 16) takes the float4 at column 16 j + 4 g of its token row and of its
+// router row, so MFMA i of step j sums columns 16 j + 4 g + i over g = 0..3.  The 8 slices' sums are added in slice
+// order.  Rows past L and tokens past T repeat the last one and are not stored.
+constexpr int RM_MIN_T = 512;
+constexpr int RM_WAVES = 8, RM_THREADS = RM_WAVES * WAVE, RM_TOK = 32, RM_ROWS = 64, RM_PITCH = RM_ROWS + 1, RM_SLOTS = 2;
+typedef float float4v __attribute__((ext_vector_type(4)));
+__global__ void __launch_bounds__(RM_THREADS) k_router_mm(const float* __restrict__ W, const float* __restrict__ x,
+                                                         float* __restrict__ logits, int T, int H, int L) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    float* part = reinterpret_cast<float*>(lds);   // [RM_WAVES / 2][RM_TOK][RM_PITCH]
+    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE, m = lane % 16, g = lane / 16;
+    const int r0 = blockIdx.x * RM_ROWS, t0 = blockIdx.y * RM_TOK, KW = H / RM_WAVES, k0 = wave * KW + 4 * g;
+    const float4v* xa[2];
+    const float4v* wb[4];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) xa[u] = reinterpret_cast<const float4v*>(x + (size_t) min(t0 + 16 * u + m, T - 1) * H + k0);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) wb[q] = reinterpret_cast<const float4v*>(W + (size_t) min(r0 + 16 * q + m, L - 1) * H + k0);
+    float4v acc[2][4];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[u][q] = float4v{0.f, 0.f, 0.f, 0.f};
+    // Steps of 16 columns, their operands through a ring of RM_SLOTS register slots: step j + RM_SLOTS - 1 is
+    // requested when step j starts (the steps a slice has, H / 128, are a multiple of RM_SLOTS)
+    const int steps = KW / 16;
+    float4v a[RM_SLOTS][2], b[RM_SLOTS][4];
+    auto request = [&](int slot, int j) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) a[slot][u] = xa[u][4 * j];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) b[slot][q] = wb[q][4 * j];
+    };
+#pragma unroll
+    for (int sl = 0; sl < RM_SLOTS - 1; ++sl) request(sl, sl);
+    for (int j0 = 0; j0 < steps; j0 += RM_SLOTS) {
+#pragma unroll
+        for (int sl = 0; sl < RM_SLOTS; ++sl) {
+            const int j = j0 + sl;
+            request((sl + RM_SLOTS - 1) % RM_SLOTS, min(j + RM_SLOTS - 1, steps - 1));
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int u = 0; u < 2; ++u)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        acc[u][q] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[sl][u][i], b[sl][q][i], acc[u][q], 0, 0, 0);
+        }
+    }
+    // The slices' sums meet in LDS in two halves (half the LDS, so three workgroups share a compute unit): slices 0-3,
+    // then 4-7, each output's sum running through them in slice order.  Accumulator element i of tile (u, q) is token
+    // 16 u + 4 g + i, router row 16 q + m.
+    constexpr int PER = RM_TOK * RM_ROWS / RM_THREADS;   // outputs a thread sums
+    float sum[PER];
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+        if (wave / (RM_WAVES / 2) == half)
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        part[((wave % (RM_WAVES / 2)) * RM_TOK + 16 * u + 4 * g + i) * RM_PITCH + 16 * q + m] = acc[u][q][i];
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < PER; ++c) {
+            const int o = threadIdx.x + c * RM_THREADS, t = o / RM_ROWS, r = o % RM_ROWS;
+#pragma unroll
+            for (int w = 0; w < RM_WAVES / 2; ++w) {
+                const float p = part[(w * RM_TOK + t) * RM_PITCH + r];
+                sum[c] = half == 0 && w == 0 ? p : sum[c] + p;
+            }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int c = 0; c < PER; ++c) {
+        const int o = threadIdx.x + c * RM_THREADS, t = o / RM_ROWS, r = o % RM_ROWS;
+        if (t0 + t < T && r0 + r < L) logits[(size_t) (t0 + t) * L + r0 + r] = sum[c];
     }
 }
 
@@ -453,22 +540,29 @@ extern "C" int sfnx_router_logits(const float* W, const float* x, float* logits,
     return guarded("sfnx_router_logits", [&] {
         require(H % 256 == 0, "H must be a multiple of 256");
         if (T <= 0 || L <= 0) return;
-        const int rt = H / 256 <= 8 ? 4 : 2, rb = (L + LT_WAVES * rt - 1) / (LT_WAVES * rt);
-        // tokens a block (a multiple of LT_RU): the fewest that keep the grid within one block a compute unit
-        static int ncu = 0;
-        if (!ncu) check(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, 0), "hipDeviceGetAttribute");
-        int tok = LT_RU;
-        while ((long) rb * ((T + tok - 1) / tok) > ncu && tok < T) tok += LT_RU;
-        const dim3 g(rb, (T + tok - 1) / tok);
-        hipStream_t s = stream_of(st);
-        switch (H / 256) {
-            case 4: launch_logits<4>(g, s, W, x, logits, T, L, tok); break;
-            case 8: launch_logits<8>(g, s, W, x, logits, T, L, tok); break;
-            case 10: launch_logits<10>(g, s, W, x, logits, T, L, tok); break;
-            case 16: launch_logits<16>(g, s, W, x, logits, T, L, tok); break;
-            default: throw std::runtime_error("hidden size must be 1024, 2048, 2560 or 4096");
+        if (T < RM_MIN_T) {   // the VALU kernel (row_dot's order)
+            const int rt = H / 256 <= 8 ? 4 : 2, rb = (L + LT_WAVES * rt - 1) / (LT_WAVES * rt);
+            // tokens a block (a multiple of LT_RU): the fewest that keep the grid within one block a compute unit
+            static int ncu = 0;
+            if (!ncu) check(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, 0), "hipDeviceGetAttribute");
+            int tok = LT_RU;
+            while ((long) rb * ((T + tok - 1) / tok) > ncu && tok < T) tok += LT_RU;
+            const dim3 g(rb, (T + tok - 1) / tok);
+            hipStream_t s = stream_of(st);
+            switch (H / 256) {
+                case 4: launch_logits<4>(g, s, W, x, logits, T, L, tok); break;
+                case 8: launch_logits<8>(g, s, W, x, logits, T, L, tok); break;
+                case 10: launch_logits<10>(g, s, W, x, logits, T, L, tok); break;
+                case 16: launch_logits<16>(g, s, W, x, logits, T, L, tok); break;
+                default: throw std::runtime_error("hidden size must be 1024, 2048, 2560 or 4096");
+            }
+            check(hipGetLastError(), "k_router_logits launch");
+            return;
         }
-        check(hipGetLastError(), "k_router_logits launch");
+        constexpr size_t lds = (size_t) RM_WAVES / 2 * RM_TOK * RM_PITCH * 4;
+        const dim3 g((L + RM_ROWS - 1) / RM_ROWS, (T + RM_TOK - 1) / RM_TOK);
+        k_router_mm<<<g, RM_THREADS, lds, stream_of(st)>>>(W, x, logits, T, H, L);
+        check(hipGetLastError(), "k_router_mm launch");
     });
 }
 

@@ -57,7 +57,7 @@ def test_prefill_q8_layer(wtype):
     b = moe.PrefillBuffers(shape, C)
     moe.prefill_layer_q8(L, torch.from_numpy(x).cuda(), y, b)
     torch.cuda.synchronize()
-    oy, ol, oi, ow, ogu, opart = orc.layer_decode(host, x, nthreads=8)
+    oy, ol, oi, ow, ogu, opart = orc.layer_decode(host, x, nthreads=8, prompt=True)
     assert np.array_equal(b.topi.cpu().numpy(), oi)
     assert int(b.cnt.max()) > 64
     rows = routed_rows(oi, C, shape.K, True)

@@ -151,7 +151,7 @@ def test_mma_baseline_prefill_shape():
     bias = (0.125 * -1.1 * np.log(rank)).astype(np.float32)
     L, host, x, y, b = run_prefill(shape, 3, 2048, bias=bias)
     assert 150 < int(b.cnt.max()) < 260
-    lg = orc.router_logits(host.W, x)
+    lg = orc.router_logits_prompt(host.W, x)
     got_lg = b.logits.cpu().numpy()
     lg_biased = lg.copy()
     lg_biased[:, : shape.E] += bias
@@ -195,7 +195,7 @@ def test_verify_window_whole_layer():
     b = moe.PrefillBuffers(shape, C)
     moe.prefill_layer_mma(L, xd, y, b)
     torch.cuda.synchronize()
-    lg = orc.router_logits(host.W, x)
+    lg = orc.router_logits_prompt(host.W, x)
     assert np.array_equal(b.logits.cpu().numpy().view(np.uint32), lg.view(np.uint32))
     oi, ow = check_prompt_routing(b, lg, shape)
     yo = y.cpu().numpy()
@@ -237,7 +237,7 @@ def test_mma_extreme_skew_and_tiny_chunks(C):
     moe.prefill_route(L, xd, b, torch.from_numpy(bias).cuda())
     moe.prefill_experts_mma(L, xd, y, b)
     torch.cuda.synchronize()
-    lg = orc.router_logits(host.W, x)
+    lg = orc.router_logits_prompt(host.W, x)
     lg[:, : shape.E] += bias
     oi, ow, _ = orc.topk(lg, shape.E, shape.K)
     assert np.array_equal(b.topi.cpu().numpy(), oi)
@@ -261,7 +261,7 @@ def test_mma_wide_hidden(H, ff, wtype):
     row): routing against the oracle, sampled pairs within 2e-3 of float64"""
     shape = moe.LayerShape(H=H, E=64, K=6, ff=ff, wtype=wtype, shared=True)
     L, host, x, y, b = run_prefill(shape, 200 + H % 97, 150)
-    lg = orc.router_logits(host.W, x)
+    lg = orc.router_logits_prompt(host.W, x)
     oi, _, _ = orc.topk(lg, shape.E, shape.K)
     assert np.array_equal(b.topi.cpu().numpy(), oi)
     eg, ed = check_sampled(host, x, b, 24, np.random.default_rng(H))

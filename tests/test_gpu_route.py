@@ -84,13 +84,16 @@ def test_router_route_all_equal():
 
 
 @pytest.mark.parametrize("T, H, L", [(1, 2048, 513), (37, 2048, 513), (300, 2048, 513), (16, 1024, 65),
-                                     (40, 2560, 1025), (16, 4096, 129), (300, 4096, 513)])
+                                     (40, 2560, 1025), (16, 4096, 129), (300, 4096, 513),
+                                     # the matrix-core kernel (512 tokens or more): partial token and row tiles
+                                     (512, 2048, 513), (600, 2048, 513), (530, 1024, 65), (777, 2560, 1025),
+                                     (520, 4096, 129), (2048, 2048, 513)])
 def test_router_logits_bit_exact(T, H, L):
     W = orc.synth(L * H, 220, 0.02).reshape(L, H)
     x = orc.synth(T * H, 221, 1.0).reshape(T, H)
     out = torch.empty((T, L), dtype=torch.float32, device="cuda")
     moe.router_logits(torch.from_numpy(W).cuda(), torch.from_numpy(x).cuda(), out)
-    assert np.array_equal(out.cpu().numpy().view(np.uint32), orc.router_logits(W, x).view(np.uint32))
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), orc.router_logits_prompt(W, x).view(np.uint32))
 
 
 def pf_route_case(logits, E, K, shared):

@@ -49,6 +49,28 @@ def test_router_logits_against_float64(orc):
     assert np.array_equal(l1, np.stack([x[:, 7], 2 * x[:, 2047], -0.5 * x[:, 1000]], 1))
 
 
+@pytest.mark.parametrize("H", [1024, 2048, 2560, 4096])
+def test_router_logits_mm_against_float64(orc, H):
+    """the prompt path's order (8 slices of fmaf chains, added in slice order): within the fp32 summation bound of the
+    float64 product, exact on one-hot rows and on integer data (every partial sum exact)"""
+    L, T = 67, 5
+    W = orc.synth(L * H, 23, 0.02).reshape(L, H)
+    x = orc.synth(T * H, 24, 1.0).reshape(T, H)
+    got = orc.router_logits_mm(W, x)
+    exact = x.astype(np.float64) @ W.astype(np.float64).T
+    bound = (H / 8 + 8) * 2.0 ** -24 * (np.abs(x).astype(np.float64) @ np.abs(W).astype(np.float64).T)
+    assert np.all(np.abs(got - exact) <= bound)
+    W1 = np.zeros((3, H), np.float32)
+    W1[0, 7], W1[1, H - 1], W1[2, H // 2 + 3] = 1, 2, -0.5
+    assert np.array_equal(orc.router_logits_mm(W1, x), np.stack([x[:, 7], 2 * x[:, H - 1], -0.5 * x[:, H // 2 + 3]], 1))
+    rng = np.random.default_rng(H)
+    Wi = rng.integers(-8, 9, (L, H)).astype(np.float32)
+    xi = rng.integers(-8, 9, (T, H)).astype(np.float32)
+    assert np.array_equal(orc.router_logits_mm(Wi, xi), (xi.astype(np.int64) @ Wi.astype(np.int64).T).astype(np.float32))
+    # a different order from the decode router's: the two agree within the bound, not bit for bit everywhere
+    assert np.all(np.abs(orc.router_logits(W, x) - got) <= 2 * bound)
+
+
 def test_topk_random_rows(orc):
     rng = np.random.default_rng(7)
     check_rows(orc, rng.normal(0, 3, (12, E + 1)))
@@ -148,3 +170,13 @@ def test_jobs_prefill_properties(orc):
             sh = gu[nj.sum():]
             assert all(j["w"] == E for j in sh)
             assert np.concatenate([j["y"][: j["n"]] for j in sh]).tolist() == list(range(C))
+
+
+def test_router_logits_prompt_dispatch(orc):
+    """sfnx_router_logits' order by chunk size: the VALU order under 512 tokens, the matrix-core order from 512"""
+    H, L = 1024, 65
+    W = orc.synth(L * H, 25, 0.02).reshape(L, H)
+    for T in (orc.ROUTER_MM_MIN_T - 1, orc.ROUTER_MM_MIN_T):
+        x = orc.synth(T * H, 26, 1.0).reshape(T, H)
+        want = orc.router_logits_mm(W, x) if T >= orc.ROUTER_MM_MIN_T else orc.router_logits(W, x)
+        assert np.array_equal(orc.router_logits_prompt(W, x), want)
