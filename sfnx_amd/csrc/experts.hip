@@ -17,32 +17,56 @@ namespace sfnx {
 namespace {
 
 constexpr int MV_THREADS = 256;
+#ifndef MV_THREADS_DOWN
+#define MV_THREADS_DOWN 1024
+#endif
+#ifndef MV_RPL_DOWN
+#define MV_RPL_DOWN 4
+#endif
+
+// The prompt path's BigJobs (up to 64 activation rows a job): down of FF 512 on 1024-thread workgroups, 4 rows a lane
+// group, so the job's h (recomputed from gate|up by every workgroup while staging it) is computed by a sixteenth as
+// many workgroups, and each activation read serves 4 rows.  Decode windows (a few rows a job, few jobs) keep 256
+// threads and a row a lane group, for their parallelism.
+constexpr bool mv_big_down(uint32_t type, int G, bool down, bool big) { return big && down && G == 1 && type != SFNX_Q8_0; }
+template <int TYPE, int G, bool DOWN, bool BIG> constexpr int mv_threads() {
+    return mv_big_down(TYPE, G, DOWN, BIG) ? MV_THREADS_DOWN : MV_THREADS;
+}
+template <int TYPE, int G, bool DOWN, bool BIG> constexpr int mv_rows_per_lane() {
+    return mv_big_down(TYPE, G, DOWN, BIG) ? MV_RPL_DOWN : 1;
+}
 
 // ------------------------------------------------------------------------------------------------ the kernel
 // TYPE: SFNX_Q4_K / SFNX_Q5_K (8 lanes a row) or SFNX_Q8_0 (16 lanes a row); G: groups or blocks per lane = C / 512;
 // TT: activation rows per pass; DOWN: activations from gu rows through swiglu (else q8_1 rows).
 template <int TYPE, int G, int TT, bool DOWN, typename J>
-__global__ void __launch_bounds__(MV_THREADS) k_moe_mv(const uint8_t* __restrict__ A, size_t sa, int R, int C,
-                                                      const J* __restrict__ jobs, const int* __restrict__ njobs,
-                                                      const void* __restrict__ in, float* __restrict__ out) {
-    constexpr int LPR = is_kquant(TYPE) ? 8 : 16, RPB = MV_THREADS / LPR;
+__global__ void __launch_bounds__((mv_threads<TYPE, G, DOWN, std::is_same_v<J, sfnx_bigjob>>()))
+k_moe_mv(const uint8_t* __restrict__ A, size_t sa, int R, int C, const J* __restrict__ jobs, const int* __restrict__ njobs,
+         const void* __restrict__ in, float* __restrict__ out) {
+    constexpr bool BIG = std::is_same_v<J, sfnx_bigjob>;
+    constexpr int LPR = is_kquant(TYPE) ? 8 : 16, RPB = mv_threads<TYPE, G, DOWN, BIG>() / LPR;
+    constexpr int RPL = mv_rows_per_lane<TYPE, G, DOWN, BIG>();
     const int ji = blockIdx.y;
     if (ji >= *njobs) return;
     extern __shared__ __align__(16) unsigned char lds[];
     __shared__ J jb;
     load_job(jb, jobs + ji);
     __syncthreads();
-    const int row = blockIdx.x * RPB + threadIdx.x / LPR, ln = threadIdx.x % LPR;
+    const int row = blockIdx.x * RPB * RPL + threadIdx.x / LPR, ln = threadIdx.x % LPR;   // (and row + RPB r, r < RPL)
     const bool live = row < R;
     const uint8_t* mat = expert_at(A, sa, jb.w);
     const Acts a = acts_in(lds, TT, C);
     if constexpr (TYPE != SFNX_Q8_0) {
         using Row = std::conditional_t<is_kquant(TYPE), Q4kRow<G, TYPE == SFNX_Q5_K>, NbRow<G, TYPE>>;
-        Row w;
-        if constexpr (is_kquant(TYPE)) {
-            if (live) w.load(kq_planes<TYPE == SFNX_Q5_K>(mat, R, C), row, C, ln);
-        } else {
-            if (live) w.load(nb_planes<TYPE>(mat, R, C), row, C, ln);
+        Row w[RPL];
+#pragma unroll
+        for (int r = 0; r < RPL; ++r) {
+            const int rr = row + RPB * r;
+            if constexpr (is_kquant(TYPE)) {
+                if (rr < R) w[r].load(kq_planes<TYPE == SFNX_Q5_K>(mat, R, C), rr, C, ln);
+            } else {
+                if (rr < R) w[r].load(nb_planes<TYPE>(mat, R, C), rr, C, ln);
+            }
         }
         for (int j0 = 0; j0 < jb.n; j0 += TT) {
             const int nn = min(TT, jb.n - j0);
@@ -51,8 +75,13 @@ __global__ void __launch_bounds__(MV_THREADS) k_moe_mv(const uint8_t* __restrict
             else stage_q8_1(a, (const uint8_t*) in, jb.y + j0, nn);
             __syncthreads();
             for (int j = 0; j < nn; ++j) {
-                const float v = group_sum<LPR>(live ? w.dot(a, j, ln) : 0.f);
-                if (live && ln == 0) out[(size_t) jb.out[j0 + j] * R + row] = v;
+                float v[RPL];
+#pragma unroll
+                for (int r = 0; r < RPL; ++r) v[r] = group_sum<LPR>(row + RPB * r < R ? w[r].dot(a, j, ln) : 0.f);
+                if (ln == 0)
+#pragma unroll
+                    for (int r = 0; r < RPL; ++r)
+                        if (row + RPB * r < R) out[(size_t) jb.out[j0 + j] * R + row + RPB * r] = v[r];
             }
         }
     } else {
@@ -75,12 +104,13 @@ __global__ void __launch_bounds__(MV_THREADS) k_moe_mv(const uint8_t* __restrict
 template <int TYPE, int TT, bool DOWN, typename J>
 void launch_g(int G, dim3 grid, size_t lds, hipStream_t s, const uint8_t* A, size_t sa, int R, int C, const J* jobs,
               const int* njobs, const void* in, float* out) {
+    constexpr bool BIGJ = std::is_same_v<J, sfnx_bigjob>;
     switch (G) {
-        case 1: k_moe_mv<TYPE, 1, TT, DOWN, J><<<grid, MV_THREADS, lds, s>>>(A, sa, R, C, jobs, njobs, in, out); break;
-        case 2: k_moe_mv<TYPE, 2, TT, DOWN, J><<<grid, MV_THREADS, lds, s>>>(A, sa, R, C, jobs, njobs, in, out); break;
-        case 4: k_moe_mv<TYPE, 4, TT, DOWN, J><<<grid, MV_THREADS, lds, s>>>(A, sa, R, C, jobs, njobs, in, out); break;
-        case 5: k_moe_mv<TYPE, 5, TT, DOWN, J><<<grid, MV_THREADS, lds, s>>>(A, sa, R, C, jobs, njobs, in, out); break;
-        case 8: k_moe_mv<TYPE, 8, TT, DOWN, J><<<grid, MV_THREADS, lds, s>>>(A, sa, R, C, jobs, njobs, in, out); break;
+        case 1: k_moe_mv<TYPE, 1, TT, DOWN, J><<<grid, mv_threads<TYPE, 1, DOWN, BIGJ>(), lds, s>>>(A, sa, R, C, jobs, njobs, in, out); break;
+        case 2: k_moe_mv<TYPE, 2, TT, DOWN, J><<<grid, mv_threads<TYPE, 2, DOWN, BIGJ>(), lds, s>>>(A, sa, R, C, jobs, njobs, in, out); break;
+        case 4: k_moe_mv<TYPE, 4, TT, DOWN, J><<<grid, mv_threads<TYPE, 4, DOWN, BIGJ>(), lds, s>>>(A, sa, R, C, jobs, njobs, in, out); break;
+        case 5: k_moe_mv<TYPE, 5, TT, DOWN, J><<<grid, mv_threads<TYPE, 5, DOWN, BIGJ>(), lds, s>>>(A, sa, R, C, jobs, njobs, in, out); break;
+        case 8: k_moe_mv<TYPE, 8, TT, DOWN, J><<<grid, mv_threads<TYPE, 8, DOWN, BIGJ>(), lds, s>>>(A, sa, R, C, jobs, njobs, in, out); break;
         default: throw std::runtime_error("input width must be 512, 1024, 2048, 2560 or 4096");
     }
 }
@@ -100,7 +130,8 @@ void moe_mv(uint32_t type, const void* A, size_t sa, int n_in, int n_out, const 
     if (acts_bytes(TT, n_in) > 64 * 1024) TT = 4;
     const size_t lds = acts_bytes(TT, n_in);
     require(lds <= 64 * 1024, "activation rows do not fit the LDS budget");
-    const int rpb = MV_THREADS / (is_kquant(type) ? 8 : 16);
+    const bool bd = mv_big_down(type, G, DOWN, std::is_same_v<J, sfnx_bigjob>);
+    const int rpb = (bd ? MV_THREADS_DOWN : MV_THREADS) / (is_kquant(type) ? 8 : 16) * (bd ? MV_RPL_DOWN : 1);
     const dim3 grid((n_out + rpb - 1) / rpb, njobs_max);
     hipStream_t s = stream_of(st);
     const uint8_t* a = (const uint8_t*) A;
