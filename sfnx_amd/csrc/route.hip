@@ -217,12 +217,14 @@ __global__ void __launch_bounds__(LT_THREADS) k_router_logits(const float* __res
 // chunks of RM_MIN_T tokens or more (fewer leave most compute units idle; they take k_router_logits above).
 // v_mfma_f32_16x16x4_f32 adds its 4 k-slots to the accumulator as fmaf in slot order (measured bit for bit on gfx950),
 // so a chain of them is an fmaf chain whose order the CPU restatement can follow exactly.  A workgroup owns 32 tokens x
-// 64 router rows (2 x 4 tiles of 16 x 16) and its 8 wavefronts split the hidden dimension into 8 slices of H / 8: a
-// wavefront's lane (m, g) = (lane % 16, lane / 16) takes the float4 at column 16 j + 4 g of its token row and of its
-// router row, so MFMA i of step j sums columns 16 j + 4 g + i over g = 0..3.  The 8 slices' sums are added in slice
-// order.  Rows past L and tokens past T repeat the last one and are not stored.
+// 48 router rows (2 x 3 tiles of 16 x 16: 513 rows pad to 528, and 11 x 64 workgroups spread evenly over 256 CUs);
+// its 8 wavefronts split the hidden dimension into 8 slices of H / 8.  A wavefront's lane (m, g) = (lane % 16,
+// lane / 16) takes the float4 at column 16 j + 4 g of its token row and of its router row, so MFMA i of step j sums
+// columns 16 j + 4 g + i over g = 0..3.  The 8 slices' sums are added in slice order.  Rows past L and tokens past T
+// repeat the last one and are not stored.
 constexpr int RM_MIN_T = 512;
-constexpr int RM_WAVES = 8, RM_THREADS = RM_WAVES * WAVE, RM_TOK = 32, RM_ROWS = 64, RM_PITCH = RM_ROWS + 1, RM_SLOTS = 2;
+constexpr int RM_WAVES = 8, RM_THREADS = RM_WAVES * WAVE, RM_TOK = 32, RM_RT = 3, RM_ROWS = 16 * RM_RT;
+constexpr int RM_PITCH = RM_ROWS + 1, RM_SLOTS = 2;
 typedef float float4v __attribute__((ext_vector_type(4)));
 __global__ void __launch_bounds__(RM_THREADS) k_router_mm(const float* __restrict__ W, const float* __restrict__ x,
                                                          float* __restrict__ logits, int T, int H, int L) {
@@ -231,25 +233,25 @@ __global__ void __launch_bounds__(RM_THREADS) k_router_mm(const float* __restric
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE, m = lane % 16, g = lane / 16;
     const int r0 = blockIdx.x * RM_ROWS, t0 = blockIdx.y * RM_TOK, KW = H / RM_WAVES, k0 = wave * KW + 4 * g;
     const float4v* xa[2];
-    const float4v* wb[4];
+    const float4v* wb[RM_RT];
 #pragma unroll
     for (int u = 0; u < 2; ++u) xa[u] = reinterpret_cast<const float4v*>(x + (size_t) min(t0 + 16 * u + m, T - 1) * H + k0);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) wb[q] = reinterpret_cast<const float4v*>(W + (size_t) min(r0 + 16 * q + m, L - 1) * H + k0);
-    float4v acc[2][4];
+    for (int q = 0; q < RM_RT; ++q) wb[q] = reinterpret_cast<const float4v*>(W + (size_t) min(r0 + 16 * q + m, L - 1) * H + k0);
+    float4v acc[2][RM_RT];
 #pragma unroll
     for (int u = 0; u < 2; ++u)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) acc[u][q] = float4v{0.f, 0.f, 0.f, 0.f};
+        for (int q = 0; q < RM_RT; ++q) acc[u][q] = float4v{0.f, 0.f, 0.f, 0.f};
     // Steps of 16 columns, their operands through a ring of RM_SLOTS register slots: step j + RM_SLOTS - 1 is
     // requested when step j starts (the steps a slice has, H / 128, are a multiple of RM_SLOTS)
     const int steps = KW / 16;
-    float4v a[RM_SLOTS][2], b[RM_SLOTS][4];
+    float4v a[RM_SLOTS][2], b[RM_SLOTS][RM_RT];
     auto request = [&](int slot, int j) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) a[slot][u] = xa[u][4 * j];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) b[slot][q] = wb[q][4 * j];
+        for (int q = 0; q < RM_RT; ++q) b[slot][q] = wb[q][4 * j];
     };
 #pragma unroll
     for (int sl = 0; sl < RM_SLOTS - 1; ++sl) request(sl, sl);
@@ -263,7 +265,7 @@ __global__ void __launch_bounds__(RM_THREADS) k_router_mm(const float* __restric
 #pragma unroll
                 for (int u = 0; u < 2; ++u)
 #pragma unroll
-                    for (int q = 0; q < 4; ++q)
+                    for (int q = 0; q < RM_RT; ++q)
                         acc[u][q] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[sl][u][i], b[sl][q][i], acc[u][q], 0, 0, 0);
         }
     }
@@ -278,7 +280,7 @@ __global__ void __launch_bounds__(RM_THREADS) k_router_mm(const float* __restric
 #pragma unroll
             for (int u = 0; u < 2; ++u)
 #pragma unroll
-                for (int q = 0; q < 4; ++q)
+                for (int q = 0; q < RM_RT; ++q)
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
                         part[((wave % (RM_WAVES / 2)) * RM_TOK + 16 * u + 4 * g + i) * RM_PITCH + 16 * q + m] = acc[u][q][i];
