@@ -217,7 +217,7 @@ __global__ void __launch_bounds__(LT_THREADS) k_router_logits(const float* __res
 // chunks of RM_MIN_T tokens or more (fewer leave most compute units idle; they take k_router_logits above).
 // v_mfma_f32_16x16x4_f32 adds its 4 k-slots to the accumulator as fmaf in slot order (measured bit for bit on gfx950),
 // so a chain of them is an fmaf chain whose order the CPU restatement can follow exactly.  A workgroup owns 32 tokens x
-// 48 router rows (2 x 3 tiles of 16 x 16: 513 rows pad to 528, and 11 x 64 workgroups spread evenly over 256 CUs);
+// 48 router rows (2 x 3 tiles of 16 x 16: 513 rows pad to 528; 11 x 64 workgroups, at most 3 a CU);
 // its 8 wavefronts split the hidden dimension into 8 slices of H / 8.  A wavefront's lane (m, g) = (lane % 16,
 // lane / 16) takes the float4 at column 16 j + 4 g of its token row and of its router row, so MFMA i of step j sums
 // columns 16 j + 4 g + i over g = 0..3.  The 8 slices' sums are added in slice order.  Rows past L and tokens past T
