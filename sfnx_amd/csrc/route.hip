@@ -330,7 +330,7 @@ __global__ void k_fill_int(int* p, int n, int v) {
 // Each block also finds its expert's first job (src/prefill.cu:228-242 k_pf_jobbase: the exclusive prefix of
 // ceil(cnt / 64) in expert order), block 0 writes the job count, and blocks E.. lay out the shared expert's jobs after
 // the routed ones (tokens in order, 64 a job).
-constexpr int PF_FILL_THREADS = 256, PF_FILL_PASS = 4 * PF_FILL_THREADS;
+constexpr int PF_FILL_THREADS = 1024, PF_FILL_PASS = 4 * PF_FILL_THREADS;   // 4,096 pairs a pass (a quarter of the barriers of 256)
 __global__ void __launch_bounds__(PF_FILL_THREADS) k_pf_fill(const int* __restrict__ topi, int P, int K, int E, int C,
                                                             int shared, const int* __restrict__ cnt, int* __restrict__ jbase,
                                                             int* __restrict__ njobs, sfnx_bigjob* __restrict__ gu,
