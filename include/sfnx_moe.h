@@ -94,6 +94,10 @@ int sfnx_router_route(const float* W, const float* x, float* logits, int T, int 
  * 512 tokens on the fp32 matrix cores: each of 8 slices of H / 8 columns one fmaf chain, the slices added in order;
  * fewer tokens in sfnx_router_route's order.  H % 256 == 0. */
 int sfnx_router_logits(const float* W, const float* x, float* logits, int T, int H, int L, void* st);
+/* No counterpart in the reference: sfnx_router_logits that also writes xh = f16(x) (sfnx_to_f16's values, bit for bit)
+ * from the router's own reads of x, for a prompt path that needs both (from 512 tokens it saves the conversion's
+ * launch and its second read of x). */
+int sfnx_router_logits_xh(const float* W, const float* x, float* logits, uint16_t* xh, int T, int H, int L, void* st);
 /* src/prefill.cu:189-279 (k_pf_top10, k_pf_count, k_pf_jobbase, k_pf_fill): top-K of rows of E + 1 logits, cnt[E],
  * jbase[E] (exclusive scan of ceil(cnt / 64)), BigJobs of each expert's pairs in pair order.  shared != 0: ceil(C/64)
  * more jobs of expert E, rows t -> C K + t.  Job capacity needed: C K / 64 + E + ceil(C / 64). */

@@ -33,6 +33,7 @@ SIGNATURES = {
     "sfnx_quantize_q8_1": (i32, [vp, vp, i32, i32, vp]),
     "sfnx_router_route": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, vp, vp, i32, vp]),
     "sfnx_router_logits": (i32, [vp, vp, vp, i32, i32, i32, vp]),
+    "sfnx_router_logits_xh": (i32, [vp, vp, vp, vp, i32, i32, i32, vp]),
     "sfnx_pf_route": (i32, [vp, i32, i32, i32, vp, vp, vp, vp, vp, vp, vp, i32, vp]),
     "sfnx_moe_gate_up": (i32, [vp, sz, u32, i32, i32, vp, vp, i32, i32, vp, vp, vp]),
     "sfnx_moe_down": (i32, [vp, sz, u32, i32, i32, vp, vp, i32, i32, vp, vp, vp]),

@@ -226,8 +226,11 @@ constexpr int RM_MIN_T = 512;
 constexpr int RM_WAVES = 8, RM_THREADS = RM_WAVES * WAVE, RM_TOK = 32, RM_RT = 3, RM_ROWS = 16 * RM_RT;
 constexpr int RM_PITCH = RM_ROWS + 1, RM_SLOTS = 2;
 typedef float float4v __attribute__((ext_vector_type(4)));
+// xh (may be null): x as f16 (round to nearest even) as well, written by the workgroups of the first row tile, whose
+// wavefronts between them read every value of their tokens' rows once
 __global__ void __launch_bounds__(RM_THREADS) k_router_mm(const float* __restrict__ W, const float* __restrict__ x,
-                                                         float* __restrict__ logits, int T, int H, int L) {
+                                                         float* __restrict__ logits, int T, int H, int L,
+                                                         _Float16* __restrict__ xh) {
     extern __shared__ __align__(16) unsigned char lds[];
     float* part = reinterpret_cast<float*>(lds);   // [RM_WAVES / 2][RM_TOK][RM_PITCH]
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE, m = lane % 16, g = lane / 16;
@@ -267,6 +270,14 @@ __global__ void __launch_bounds__(RM_THREADS) k_router_mm(const float* __restric
 #pragma unroll
                     for (int q = 0; q < RM_RT; ++q)
                         acc[u][q] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[sl][u][i], b[sl][q][i], acc[u][q], 0, 0, 0);
+            if (xh != nullptr && blockIdx.x == 0)
+#pragma unroll
+                for (int u = 0; u < 2; ++u)
+                    if (t0 + 16 * u + m < T) {
+                        typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+                        const half4v hv = {(_Float16) a[sl][u][0], (_Float16) a[sl][u][1], (_Float16) a[sl][u][2], (_Float16) a[sl][u][3]};
+                        *reinterpret_cast<half4v*>(xh + (size_t) (t0 + 16 * u + m) * H + k0 + 16 * j) = hv;
+                    }
         }
     }
     // The slices' sums meet in LDS in two halves (half the LDS, so three workgroups share a compute unit): slices 0-3,
@@ -538,8 +549,10 @@ void launch_logits(dim3 g, hipStream_t s, const float* W, const float* x, float*
     k_router_logits<NC><<<g, LT_THREADS, lds, s>>>(W, x, logits, T, L, tok);
 }
 
-extern "C" int sfnx_router_logits(const float* W, const float* x, float* logits, int T, int H, int L, void* st) {
-    return guarded("sfnx_router_logits", [&] {
+namespace {
+// sfnx_router_logits(_xh): the VALU kernel under RM_MIN_T tokens (xh then by a conversion launch), else k_router_mm
+void router_logits(const float* W, const float* x, float* logits, int T, int H, int L, _Float16* xh, hipStream_t st) {
+    {
         require(H % 256 == 0, "H must be a multiple of 256");
         if (T <= 0 || L <= 0) return;
         if (T < RM_MIN_T) {   // the VALU kernel (row_dot's order)
@@ -550,7 +563,7 @@ extern "C" int sfnx_router_logits(const float* W, const float* x, float* logits,
             int tok = LT_RU;
             while ((long) rb * ((T + tok - 1) / tok) > ncu && tok < T) tok += LT_RU;
             const dim3 g(rb, (T + tok - 1) / tok);
-            hipStream_t s = stream_of(st);
+            hipStream_t s = st;
             switch (H / 256) {
                 case 4: launch_logits<4>(g, s, W, x, logits, T, L, tok); break;
                 case 8: launch_logits<8>(g, s, W, x, logits, T, L, tok); break;
@@ -559,12 +572,26 @@ extern "C" int sfnx_router_logits(const float* W, const float* x, float* logits,
                 default: throw std::runtime_error("hidden size must be 1024, 2048, 2560 or 4096");
             }
             check(hipGetLastError(), "k_router_logits launch");
+            if (xh) require(sfnx_to_f16(x, (uint16_t*) xh, (size_t) T * H, st) == 0, "sfnx_to_f16 failed");
             return;
         }
         constexpr size_t lds = (size_t) RM_WAVES / 2 * RM_TOK * RM_PITCH * 4;
         const dim3 g((L + RM_ROWS - 1) / RM_ROWS, (T + RM_TOK - 1) / RM_TOK);
-        k_router_mm<<<g, RM_THREADS, lds, stream_of(st)>>>(W, x, logits, T, H, L);
+        k_router_mm<<<g, RM_THREADS, lds, st>>>(W, x, logits, T, H, L, xh);
         check(hipGetLastError(), "k_router_mm launch");
+    }
+}
+}  // namespace
+
+extern "C" int sfnx_router_logits(const float* W, const float* x, float* logits, int T, int H, int L, void* st) {
+    return guarded("sfnx_router_logits", [&] { router_logits(W, x, logits, T, H, L, nullptr, stream_of(st)); });
+}
+
+extern "C" int sfnx_router_logits_xh(const float* W, const float* x, float* logits, uint16_t* xh, int T, int H, int L,
+                                     void* st) {
+    return guarded("sfnx_router_logits_xh", [&] {
+        require(xh != nullptr, "xh is null");
+        router_logits(W, x, logits, T, H, L, reinterpret_cast<_Float16*>(xh), stream_of(st));
     });
 }
 

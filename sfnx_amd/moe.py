@@ -70,6 +70,12 @@ def router_logits(W, x, logits) -> None:
     check(lib().sfnx_router_logits(_p(W), _p(x), _p(logits), T, H, W.shape[0], _st()))
 
 
+def router_logits_xh(W, x, logits, xh) -> None:
+    """router_logits and xh = f16(x) from one read of x"""
+    T, H = x.shape
+    check(lib().sfnx_router_logits_xh(_p(W), _p(x), _p(logits), _p(xh), T, H, W.shape[0], _st()))
+
+
 def pf_route(logits, topi, topw, cnt, jbase, jobs_gu, jobs_dn, njobs, E: int, K: int, shared: bool = True) -> None:
     C = logits.shape[0]
     check(lib().sfnx_pf_route(_p(logits), C, E, K, _p(topi), _p(topw), _p(cnt), _p(jbase), _p(jobs_gu), _p(jobs_dn),
@@ -367,11 +373,15 @@ class PrefillBuffers:
             self.wh = torch.empty(2 * s.ff * s.H, dtype=torch.float16, device=device)
 
 
-def prefill_route(L: "MoeLayer", x: torch.Tensor, b: "PrefillBuffers", bias: torch.Tensor | None = None) -> None:
-    """the prompt path's routing: router logits, an optional bias on the routed logits (the benchmark's skew), then
-    top-k and the BigJob permutation (src/prefill.cu:1163-1167)"""
+def prefill_route(L: "MoeLayer", x: torch.Tensor, b: "PrefillBuffers", bias: torch.Tensor | None = None,
+                  xh: bool = False) -> None:
+    """the prompt path's routing: router logits (and, with xh, b.xh = f16(x) from the same read), an optional bias on
+    the routed logits (the benchmark's skew), then top-k and the BigJob permutation (src/prefill.cu:1163-1167)"""
     s = L.s
-    router_logits(L.W, x, b.logits)
+    if xh:
+        router_logits_xh(L.W, x, b.logits, b.xh)
+    else:
+        router_logits(L.W, x, b.logits)
     if bias is not None:
         b.logits[:, : s.E] += bias
     pf_route(b.logits, b.topi, b.topw, b.cnt, b.jbase, b.jobs_gu, b.jobs_dn, b.njobs, s.E, s.K, s.shared and not s.sh_q8s)
@@ -413,8 +423,7 @@ def prefill_layer_mma(L: "MoeLayer", x: torch.Tensor, y: torch.Tensor, b: "Prefi
     """A prompt chunk (or a verify window of many rows) through the whole layer on the matrix cores: routing, f16
     activations, gate|up with SwiGLU fused into its epilogue, down, the combine (src/prefill.cu:1145-1180)"""
     s = L.s
-    prefill_route(L, x, b, bias)
-    to_f16(x, b.xh)
+    prefill_route(L, x, b, bias, xh=True)   # the f16 activations b.xh from the router's read of x
     moe_gate_up_swiglu_mma(L.gu_w, L.gu_stride, s.wtype, s.H, s.ff, b.jobs_gu, b.njobs, b.cap, b.xh, b.h16)
     moe_down_mma(L.dn_w, L.dn_stride, s.dn_type, s.ff, s.H, b.jobs_dn, b.njobs, b.cap, b.h16, b.part)
     if s.sh_q8s:

@@ -96,6 +96,21 @@ def test_router_logits_bit_exact(T, H, L):
     assert np.array_equal(out.cpu().numpy().view(np.uint32), orc.router_logits_prompt(W, x).view(np.uint32))
 
 
+@pytest.mark.parametrize("T, H, L", [(300, 2048, 513), (600, 2048, 513), (777, 2560, 1025), (2048, 4096, 129)])
+def test_router_logits_xh(T, H, L):
+    """sfnx_router_logits_xh: the same logits as sfnx_router_logits, and xh equal to sfnx_to_f16's, bit for bit"""
+    W = torch.from_numpy(orc.synth(L * H, 222, 0.02).reshape(L, H)).cuda()
+    x = torch.from_numpy(orc.synth(T * H, 223, 1.0).reshape(T, H)).cuda()
+    l0, l1 = (torch.empty((T, L), dtype=torch.float32, device="cuda") for _ in range(2))
+    h0, h1 = torch.empty((T, H), dtype=torch.float16, device="cuda"), torch.full((T, H), 7.0, dtype=torch.float16, device="cuda")
+    moe.router_logits(W, x, l0)
+    moe.to_f16(x, h0)
+    moe.router_logits_xh(W, x, l1, h1)
+    torch.cuda.synchronize()
+    assert torch.equal(l0.view(torch.int32), l1.view(torch.int32))
+    assert torch.equal(h0.view(torch.int16), h1.view(torch.int16))
+
+
 def pf_route_case(logits, E, K, shared):
     C = logits.shape[0]
     cap = C * K // 64 + E + (C + 63) // 64 + 1
