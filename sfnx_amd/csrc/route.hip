@@ -315,11 +315,9 @@ __global__ void __launch_bounds__(RM_THREADS) k_router_mm(const float* __restric
 }
 
 // ------------------------------------------------------------------------------------------------ prompt routing
-// src/prefill.cu:191-221 k_pf_top10 and 223-226 k_pf_count: a wavefront per token, its picks counted per expert
-// (cnt zeroed beforehand; the counts are exact whatever the order of the increments)
+// src/prefill.cu:191-221 k_pf_top10: a wavefront per token (the picks are counted by k_pf_fill)
 __global__ void __launch_bounds__(RR_THREADS) k_pf_topk(const float* __restrict__ logits, int C, int E, int K,
-                                                       int* __restrict__ topi, float* __restrict__ topw,
-                                                       int* __restrict__ cnt) {
+                                                       int* __restrict__ topi, float* __restrict__ topw) {
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE, t = blockIdx.x * RR_WAVES + wave;
     if (t >= C) return;
     int pick;
@@ -328,30 +326,43 @@ __global__ void __launch_bounds__(RR_THREADS) k_pf_topk(const float* __restrict_
     if (lane < K) {
         topi[(size_t) t * K + lane] = pick;
         topw[(size_t) t * K + lane] = w;
-        if (pick >= 0) atomicAdd(&cnt[pick], 1);
     }
-}
-__global__ void k_fill_int(int* p, int n, int v) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) p[i] = v;
 }
 // src/prefill.cu:248-279 k_pf_fill: a block per expert scans the pairs in index order, 4 consecutive pairs a thread and
 // 1024 a pass, its slots from a prefix over the threads of the pass (ballots of the count bits, then the wavefronts in
 // order), so a pair always lands in the same job and slot
-// Each block also finds its expert's first job (src/prefill.cu:228-242 k_pf_jobbase: the exclusive prefix of
-// ceil(cnt / 64) in expert order), block 0 writes the job count, and blocks E.. lay out the shared expert's jobs after
-// the routed ones (tokens in order, 64 a job).
+// Each block first counts every expert's picks in LDS (src/prefill.cu:223-226 k_pf_count; block e writes cnt[e]: no
+// global atomics, which serialised on the experts many tokens pick), then finds its expert's first job
+// (src/prefill.cu:228-242 k_pf_jobbase: the exclusive prefix of ceil(cnt / 64) in expert order); block 0 writes the
+// job count, and blocks E.. lay out the shared expert's jobs after the routed ones (tokens in order, 64 a job).
 constexpr int PF_FILL_THREADS = 1024, PF_FILL_PASS = 4 * PF_FILL_THREADS;   // 4,096 pairs a pass (a quarter of the barriers of 256)
 __global__ void __launch_bounds__(PF_FILL_THREADS) k_pf_fill(const int* __restrict__ topi, int P, int K, int E, int C,
-                                                            int shared, const int* __restrict__ cnt, int* __restrict__ jbase,
+                                                            int shared, int* __restrict__ cnt, int* __restrict__ jbase,
                                                             int* __restrict__ njobs, sfnx_bigjob* __restrict__ gu,
                                                             sfnx_bigjob* __restrict__ dn) {
     const int tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE;
     const int e = min((int) blockIdx.x, E);   // E: a block of the shared expert's jobs
     __shared__ int wsum[2][PF_FILL_THREADS / WAVE];
+    __shared__ int hist[MAX_E];
+    for (int i = tid; i < E; i += PF_FILL_THREADS) hist[i] = 0;
+    __syncthreads();
+    for (int p = 4 * tid; p < P; p += PF_FILL_PASS) {
+        int q[4];
+        if (p + 3 < P) {
+            const int4 v = *reinterpret_cast<const int4*>(topi + p);
+            q[0] = v.x, q[1] = v.y, q[2] = v.z, q[3] = v.w;
+        } else {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) q[c] = p + c < P ? topi[p + c] : -1;
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            if (q[c] >= 0) atomicAdd(&hist[q[c]], 1);
+    }
+    __syncthreads();
     int jb0 = 0, jall = 0;   // jobs of the experts before e, of all experts
     for (int i = tid; i < E; i += PF_FILL_THREADS) {
-        const int nj = (cnt[i] + SFNX_PF_JOB - 1) / SFNX_PF_JOB;
+        const int nj = (hist[i] + SFNX_PF_JOB - 1) / SFNX_PF_JOB;
         jb0 += i < e ? nj : 0;
         jall += nj;
     }
@@ -380,11 +391,12 @@ __global__ void __launch_bounds__(PF_FILL_THREADS) k_pf_fill(const int* __restri
         }
         return;
     }
+    const int ce = hist[e];
     if (tid == 0) {
+        cnt[e] = ce;
         jbase[e] = jb0;
         if (e == 0) njobs[0] = jall + (shared ? (C + SFNX_PF_JOB - 1) / SFNX_PF_JOB : 0);
     }
-    const int ce = cnt[e];
     if (ce == 0) return;
     __shared__ int wcount[2][PF_FILL_THREADS / WAVE];
     const uint64_t lt = (1ull << lane) - 1ull;
@@ -603,8 +615,7 @@ extern "C" int sfnx_pf_route(const float* logits, int C, int E, int K, int* topi
         require(K >= 1 && K <= MAX_K && K <= E, "K out of range (1..16)");
         hipStream_t s = stream_of(st);
         const int P = C * K;
-        k_fill_int<<<(E + 255) / 256, 256, 0, s>>>(cnt, E, 0);
-        k_pf_topk<<<(C + RR_WAVES - 1) / RR_WAVES, RR_THREADS, 0, s>>>(logits, C, E, K, topi, topw, cnt);
+        k_pf_topk<<<(C + RR_WAVES - 1) / RR_WAVES, RR_THREADS, 0, s>>>(logits, C, E, K, topi, topw);
         const int nsh = shared ? std::min(8, (C + PF_FILL_THREADS - 1) / PF_FILL_THREADS) : 0;
         k_pf_fill<<<E + nsh, PF_FILL_THREADS, 0, s>>>(topi, P, K, E, C, shared, cnt, jbase, njobs, jobs_gu, jobs_dn);
     });
