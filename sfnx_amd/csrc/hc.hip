@@ -123,13 +123,14 @@ __global__ void __launch_bounds__(HA_THREADS) k_hc_down(HcArgs a) {
         for (int q = 0; q < 8; ++q) wi[q] = w4[q * 8 + j];
     }
     const float wn0 = a.w_norm[col0 + tid], wn1 = a.w_norm[col0 + HA_THREADS + tid];
-    // R' of the slice into xs, the rows' loads (and the fold's inject logits) issued 8 at a time: batch m, element k
-    // is row 4 m + k / 2, column tid + 256 (k % 2), so a thread takes each row's gate once
+    // R' of the slice into xs, the rows' loads (and the fold's inject logits) issued RB at a time: batch m, element k
+    // is row RB / 2 m + k / 2, column tid + 256 (k % 2), so a thread takes each row's gate once
     static_assert(HS == 2 * HA_THREADS, "two columns of a slice a thread");
-    for (int t0 = 0; t0 < T; t0 += 4) {
-        float r[8], b[8], g[4];
+    constexpr int RB = TT >= 8 ? 16 : 8;
+    for (int t0 = 0; t0 < T; t0 += RB / 2) {
+        float r[RB], b[RB], g[RB / 2];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
+        for (int k = 0; k < RB; ++k) {
             const int t = t0 + k / 2, x = tid + HA_THREADS * (k % 2);
             if (t < T) {
                 r[k] = a.R[(size_t) t * D + col0 + x];
@@ -140,10 +141,10 @@ __global__ void __launch_bounds__(HA_THREADS) k_hc_down(HcArgs a) {
             }
         }
 #pragma unroll
-        for (int k = 0; k < 4; ++k)
+        for (int k = 0; k < RB / 2; ++k)
             if (a.bo && t0 + k < T) g[k] = 2.0f * sigm_f(g[k] / (float) a.HC);
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
+        for (int k = 0; k < RB; ++k) {
             const int t = t0 + k / 2, x = tid + HA_THREADS * (k % 2);
             if (t < T) xs[t][x] = a.bo ? fmaf(b[k], g[k / 2], r[k]) : r[k];
         }
@@ -151,7 +152,9 @@ __global__ void __launch_bounds__(HA_THREADS) k_hc_down(HcArgs a) {
     __syncthreads();
     // the square sums (row group 0 only): 32 consecutive columns a half-wave; then xs = R' w_norm
     const int hw = tid / 32;
-    for (int t = 0; t < T; ++t) {
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+        if (t >= T) break;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int x = h * HA_THREADS + tid;
@@ -169,13 +172,25 @@ __global__ void __launch_bounds__(HA_THREADS) k_hc_down(HcArgs a) {
         for (int w = 0; w < HS / 32; ++w) v += red[tid][w];
         a.ssp[(size_t) tid * NS + s] = v;
     }
-    for (int q = hw; q < T * (HS / 32); q += HA_THREADS / 32) {
-        const int t = q / (HS / 32), b = q % (HS / 32);
-        q8_block32(xs[t][32 * b + tid % 32], &xq[t][32 * b], &xd[t][b]);
+    // xs as int8 per 32 (q8_block32's arithmetic: an exact maximum, then each value on its own): 8 threads a block,
+    // 4 consecutive values each, so a pass covers 32 blocks
+    for (int q = tid / 8; q < T * (HS / 32); q += HA_THREADS / 8) {
+        const int t = q / (HS / 32), b = q % (HS / 32), l8 = tid % 8;
+        const float4 v = *reinterpret_cast<const float4*>(&xs[t][32 * b + 4 * l8]);
+        const float amax = group_max<8>(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        const float sc = amax / 127.0f;
+        const float vv[4] = {v.x, v.y, v.z, v.w};
+        uint32_t pk = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) pk |= (uint32_t) (uint8_t) (amax == 0.0f ? (int8_t) 0 : (int8_t) roundf(vv[k] / sc)) << (8 * k);
+        *reinterpret_cast<uint32_t*>(&xq[t][32 * b + 4 * l8]) = pk;
+        if (l8 == 0) xd[t][b] = sc;
     }
     __syncthreads();
     if (row >= ROWS) return;   // whole 8-lane groups: the butterfly stays inside live groups
-    for (int t = 0; t < T; ++t) {
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+        if (t >= T) break;
         float acc = 0.f;
         if (dn_row) {
 #pragma unroll
