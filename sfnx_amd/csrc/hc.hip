@@ -356,7 +356,33 @@ __global__ void __launch_bounds__(HC_THREADS) k_hc_up(HcArgs a) {
     }
     if (a.bo && tid < T * a.HC) sg[tid / a.HC][tid % a.HC] = 2.0f * sigm_f(a.inj_prev[tid] / (float) a.HC);
     __syncthreads();
-    // item (t, c, column): the up row c 32 + column of the block against lo row t; the items spread over the block
+    // item (t, c, column): the up row c 32 + column of the block against lo row t.  With few items (one row: 4 streams
+    // x 32 columns for 512 threads) 4 consecutive lanes share an item, lane q taking leaves 4 q .. 4 q + 3 of the tree
+    // below and lane exchanges (partners 1, then 2) making its last two levels: the same sums in the same pairs
+    if (T * nrow * 4 <= HC_THREADS) {
+        const int it = tid / 4, q = tid % 4;
+        const bool live = it < T * nrow;
+        const int t = live ? it / nrow : 0, rr = live ? it % nrow : 0, c = rr / HC_COLS, cl = rr % HC_COLS;
+        auto blk = [&](int b) {
+            if (b >= NB) return 0.f;
+            const int4* wr = reinterpret_cast<const int4*>(wq + rr * (NB * 32 + 16) + 32 * b);
+            const int4* xr = reinterpret_cast<const int4*>(&lq[t][32 * b]);
+            const int4 w0 = wr[0], w1 = wr[1], x0 = xr[0], x1 = xr[1];
+            int s = dot4(w0.x, x0.x, 0);
+            s = dot4(w0.y, x0.y, s);
+            s = dot4(w0.z, x0.z, s);
+            s = dot4(w0.w, x0.w, s);
+            s = dot4(w1.x, x1.x, s);
+            s = dot4(w1.y, x1.y, s);
+            s = dot4(w1.z, x1.z, s);
+            s = dot4(w1.w, x1.w, s);
+            return (wsl[rr * NB + b] * ld[t][b]) * (float) s;
+        };
+        float w = (blk(4 * q) + blk(4 * q + 1)) + (blk(4 * q + 2) + blk(4 * q + 3));
+        w = w + lane_xor<1>(w);
+        w = w + lane_xor<2>(w);
+        if (live && q == 0) gs[t][c][cl] = w;
+    } else
     for (int it = tid; it < T * nrow; it += HC_THREADS) {
         const int t = it / nrow, rr = it % nrow, c = rr / HC_COLS, cl = rr % HC_COLS;
         {
