@@ -216,43 +216,45 @@ __global__ void __launch_bounds__(LT_THREADS) k_router_logits(const float* __res
 // The prompt path's router logits [T][L] = W x (src/prefill.cu:1163, the engine's sgemm) on the fp32 matrix cores, for
 // chunks of RM_MIN_T tokens or more (fewer leave most compute units idle; they take k_router_logits above).
 // v_mfma_f32_16x16x4_f32 adds its 4 k-slots to the accumulator as fmaf in slot order (measured bit for bit on gfx950),
-// so a chain of them is an fmaf chain whose order the CPU restatement can follow exactly.  A workgroup owns 32 tokens x
-// 48 router rows (2 x 3 tiles of 16 x 16: 513 rows pad to 528; 11 x 64 workgroups, at most 3 a CU);
+// so a chain of them is an fmaf chain whose order the CPU restatement can follow exactly.  A workgroup owns TOK tokens
+// (32, 48 or 64: TOK / 16 tiles of 16) x 48 router rows (3 tiles of 16: 513 rows pad to 528, 11 row tiles);
 // its 8 wavefronts split the hidden dimension into 8 slices of H / 8.  A wavefront's lane (m, g) = (lane % 16,
 // lane / 16) takes the float4 at column 16 j + 4 g of its token row and of its router row, so MFMA i of step j sums
 // columns 16 j + 4 g + i over g = 0..3.  The 8 slices' sums are added in slice order.  Rows past L and tokens past T
 // repeat the last one and are not stored.
 constexpr int RM_MIN_T = 512;
-constexpr int RM_WAVES = 8, RM_THREADS = RM_WAVES * WAVE, RM_TOK = 32, RM_RT = 3, RM_ROWS = 16 * RM_RT;
+constexpr int RM_WAVES = 8, RM_THREADS = RM_WAVES * WAVE, RM_RT = 3, RM_ROWS = 16 * RM_RT;
 constexpr int RM_PITCH = RM_ROWS + 1, RM_SLOTS = 2;
 typedef float float4v __attribute__((ext_vector_type(4)));
 // xh (may be null): x as f16 (round to nearest even) as well, written by the workgroups of the first row tile, whose
 // wavefronts between them read every value of their tokens' rows once
+template <int TOK>
 __global__ void __launch_bounds__(RM_THREADS) k_router_mm(const float* __restrict__ W, const float* __restrict__ x,
                                                          float* __restrict__ logits, int T, int H, int L,
                                                          _Float16* __restrict__ xh) {
+    constexpr int TU = TOK / 16;
     extern __shared__ __align__(16) unsigned char lds[];
-    float* part = reinterpret_cast<float*>(lds);   // [RM_WAVES / 2][RM_TOK][RM_PITCH]
+    float* part = reinterpret_cast<float*>(lds);   // [RM_WAVES / 2][TOK][RM_PITCH]
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE, m = lane % 16, g = lane / 16;
-    const int r0 = blockIdx.x * RM_ROWS, t0 = blockIdx.y * RM_TOK, KW = H / RM_WAVES, k0 = wave * KW + 4 * g;
-    const float4v* xa[2];
+    const int r0 = blockIdx.x * RM_ROWS, t0 = blockIdx.y * TOK, KW = H / RM_WAVES, k0 = wave * KW + 4 * g;
+    const float4v* xa[TU];
     const float4v* wb[RM_RT];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) xa[u] = reinterpret_cast<const float4v*>(x + (size_t) min(t0 + 16 * u + m, T - 1) * H + k0);
+    for (int u = 0; u < TU; ++u) xa[u] = reinterpret_cast<const float4v*>(x + (size_t) min(t0 + 16 * u + m, T - 1) * H + k0);
 #pragma unroll
     for (int q = 0; q < RM_RT; ++q) wb[q] = reinterpret_cast<const float4v*>(W + (size_t) min(r0 + 16 * q + m, L - 1) * H + k0);
-    float4v acc[2][RM_RT];
+    float4v acc[TU][RM_RT];
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
+    for (int u = 0; u < TU; ++u)
 #pragma unroll
         for (int q = 0; q < RM_RT; ++q) acc[u][q] = float4v{0.f, 0.f, 0.f, 0.f};
     // Steps of 16 columns, their operands through a ring of RM_SLOTS register slots: step j + RM_SLOTS - 1 is
     // requested when step j starts (the steps a slice has, H / 128, are a multiple of RM_SLOTS)
     const int steps = KW / 16;
-    float4v a[RM_SLOTS][2], b[RM_SLOTS][RM_RT];
+    float4v a[RM_SLOTS][TU], b[RM_SLOTS][RM_RT];
     auto request = [&](int slot, int j) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u) a[slot][u] = xa[u][4 * j];
+        for (int u = 0; u < TU; ++u) a[slot][u] = xa[u][4 * j];
 #pragma unroll
         for (int q = 0; q < RM_RT; ++q) b[slot][q] = wb[q][4 * j];
     };
@@ -266,13 +268,13 @@ __global__ void __launch_bounds__(RM_THREADS) k_router_mm(const float* __restric
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int u = 0; u < 2; ++u)
+                for (int u = 0; u < TU; ++u)
 #pragma unroll
                     for (int q = 0; q < RM_RT; ++q)
                         acc[u][q] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[sl][u][i], b[sl][q][i], acc[u][q], 0, 0, 0);
             if (xh != nullptr && blockIdx.x == 0)
 #pragma unroll
-                for (int u = 0; u < 2; ++u)
+                for (int u = 0; u < TU; ++u)
                     if (t0 + 16 * u + m < T) {
                         typedef _Float16 half4v __attribute__((ext_vector_type(4)));
                         const half4v hv = {(_Float16) a[sl][u][0], (_Float16) a[sl][u][1], (_Float16) a[sl][u][2], (_Float16) a[sl][u][3]};
@@ -283,25 +285,26 @@ __global__ void __launch_bounds__(RM_THREADS) k_router_mm(const float* __restric
     // The slices' sums meet in LDS in two halves (half the LDS, so three workgroups share a compute unit): slices 0-3,
     // then 4-7, each output's sum running through them in slice order.  Accumulator element i of tile (u, q) is token
     // 16 u + 4 g + i, router row 16 q + m.
-    constexpr int PER = RM_TOK * RM_ROWS / RM_THREADS;   // outputs a thread sums
+    constexpr int PER = (TOK * RM_ROWS + RM_THREADS - 1) / RM_THREADS;   // outputs a thread sums
     float sum[PER];
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
         if (wave / (RM_WAVES / 2) == half)
 #pragma unroll
-            for (int u = 0; u < 2; ++u)
+            for (int u = 0; u < TU; ++u)
 #pragma unroll
                 for (int q = 0; q < RM_RT; ++q)
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
-                        part[((wave % (RM_WAVES / 2)) * RM_TOK + 16 * u + 4 * g + i) * RM_PITCH + 16 * q + m] = acc[u][q][i];
+                        part[((wave % (RM_WAVES / 2)) * TOK + 16 * u + 4 * g + i) * RM_PITCH + 16 * q + m] = acc[u][q][i];
         __syncthreads();
 #pragma unroll
         for (int c = 0; c < PER; ++c) {
             const int o = threadIdx.x + c * RM_THREADS, t = o / RM_ROWS, r = o % RM_ROWS;
+            if (o >= TOK * RM_ROWS) break;
 #pragma unroll
             for (int w = 0; w < RM_WAVES / 2; ++w) {
-                const float p = part[(w * RM_TOK + t) * RM_PITCH + r];
+                const float p = part[(w * TOK + t) * RM_PITCH + r];
                 sum[c] = half == 0 && w == 0 ? p : sum[c] + p;
             }
         }
@@ -310,7 +313,7 @@ __global__ void __launch_bounds__(RM_THREADS) k_router_mm(const float* __restric
 #pragma unroll
     for (int c = 0; c < PER; ++c) {
         const int o = threadIdx.x + c * RM_THREADS, t = o / RM_ROWS, r = o % RM_ROWS;
-        if (t0 + t < T && r0 + r < L) logits[(size_t) (t0 + t) * L + r0 + r] = sum[c];
+        if (o < TOK * RM_ROWS && t0 + t < T && r0 + r < L) logits[(size_t) (t0 + t) * L + r0 + r] = sum[c];
     }
 }
 
@@ -587,9 +590,26 @@ void router_logits(const float* W, const float* x, float* logits, int T, int H, 
             if (xh) require(sfnx_to_f16(x, (uint16_t*) xh, (size_t) T * H, st) == 0, "sfnx_to_f16 failed");
             return;
         }
-        constexpr size_t lds = (size_t) RM_WAVES / 2 * RM_TOK * RM_PITCH * 4;
-        const dim3 g((L + RM_ROWS - 1) / RM_ROWS, (T + RM_TOK - 1) / RM_TOK);
-        k_router_mm<<<g, RM_THREADS, lds, st>>>(W, x, logits, T, H, L, xh);
+        // tokens a workgroup: taller tiles load fewer operands a multiply-add (measured 1, 0.93, 0.8 of the time a
+        // token at 32, 48, 64) but make fewer workgroups; the estimate is the rounds of workgroups over the compute
+        // units times the tile's time
+        static int ncu = 0;
+        if (!ncu) check(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, 0), "hipDeviceGetAttribute");
+        const int rb = (L + RM_ROWS - 1) / RM_ROWS;
+        int tok = 32;
+        double best = 0.0;
+        for (const auto& [tk, eff] : {std::pair<int, double>{32, 1.0}, {48, 0.93}, {64, 0.8}}) {
+            const long nb = (long) rb * ((T + tk - 1) / tk);
+            const double cost = (double) ((nb + ncu - 1) / ncu) * tk * eff;
+            if (tk == 32 || cost < best) tok = tk, best = cost;
+        }
+        const dim3 g(rb, (T + tok - 1) / tok);
+        const size_t lds = (size_t) RM_WAVES / 2 * tok * RM_PITCH * 4;
+        switch (tok) {
+            case 32: k_router_mm<32><<<g, RM_THREADS, lds, st>>>(W, x, logits, T, H, L, xh); break;
+            case 48: k_router_mm<48><<<g, RM_THREADS, lds, st>>>(W, x, logits, T, H, L, xh); break;
+            default: k_router_mm<64><<<g, RM_THREADS, lds, st>>>(W, x, logits, T, H, L, xh); break;
+        }
         check(hipGetLastError(), "k_router_mm launch");
     }
 }

@@ -87,7 +87,9 @@ def test_router_route_all_equal():
                                      (40, 2560, 1025), (16, 4096, 129), (300, 4096, 513),
                                      # the matrix-core kernel (512 tokens or more): partial token and row tiles
                                      (512, 2048, 513), (600, 2048, 513), (530, 1024, 65), (777, 2560, 1025),
-                                     (520, 4096, 129), (2048, 2048, 513)])
+                                     (520, 4096, 129), (2048, 2048, 513),
+                                     # token tiles of 32, 48 and 64 (the shapes above, and this one) give the same bits
+                                     (1200, 1024, 1025)])
 def test_router_logits_bit_exact(T, H, L):
     W = orc.synth(L * H, 220, 0.02).reshape(L, H)
     x = orc.synth(T * H, 221, 1.0).reshape(T, H)
@@ -96,7 +98,8 @@ def test_router_logits_bit_exact(T, H, L):
     assert np.array_equal(out.cpu().numpy().view(np.uint32), orc.router_logits_prompt(W, x).view(np.uint32))
 
 
-@pytest.mark.parametrize("T, H, L", [(300, 2048, 513), (600, 2048, 513), (777, 2560, 1025), (2048, 4096, 129)])
+@pytest.mark.parametrize("T, H, L", [(300, 2048, 513), (600, 2048, 513), (777, 2560, 1025), (2048, 4096, 129),
+                                     (1200, 1024, 1025)])
 def test_router_logits_xh(T, H, L):
     """sfnx_router_logits_xh: the same logits as sfnx_router_logits, and xh equal to sfnx_to_f16's, bit for bit"""
     W = torch.from_numpy(orc.synth(L * H, 222, 0.02).reshape(L, H)).cuda()
