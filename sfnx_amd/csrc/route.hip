@@ -217,7 +217,7 @@ __global__ void __launch_bounds__(LT_THREADS) k_router_logits(const float* __res
 // chunks of RM_MIN_T tokens or more (fewer leave most compute units idle; they take k_router_logits above).
 // v_mfma_f32_16x16x4_f32 adds its 4 k-slots to the accumulator as fmaf in slot order (measured bit for bit on gfx950),
 // so a chain of them is an fmaf chain whose order the CPU restatement can follow exactly.  A workgroup owns TOK tokens
-// (32, 48 or 64: TOK / 16 tiles of 16) x 48 router rows (3 tiles of 16: 513 rows pad to 528, 11 row tiles);
+// (32, 48, 64 or 96: TOK / 16 tiles of 16) x 48 router rows (3 tiles of 16: 513 rows pad to 528, 11 row tiles);
 // its 8 wavefronts split the hidden dimension into 8 slices of H / 8.  A wavefront's lane (m, g) = (lane % 16,
 // lane / 16) takes the float4 at column 16 j + 4 g of its token row and of its router row, so MFMA i of step j sums
 // columns 16 j + 4 g + i over g = 0..3.  The 8 slices' sums are added in slice order.  Rows past L and tokens past T
@@ -590,17 +590,20 @@ void router_logits(const float* W, const float* x, float* logits, int T, int H, 
             if (xh) require(sfnx_to_f16(x, (uint16_t*) xh, (size_t) T * H, st) == 0, "sfnx_to_f16 failed");
             return;
         }
-        // tokens a workgroup: taller tiles load fewer operands a multiply-add (measured 1, 0.93, 0.8 of the time a
-        // token at 32, 48, 64) but make fewer workgroups; the estimate is the rounds of workgroups over the compute
-        // units times the tile's time
+        // tokens a workgroup: a taller tile requests fewer operands a multiply-add but makes fewer workgroups.  The
+        // estimate: rounds of workgroups over the compute units times a round's time for the tile (measured at 2048
+        // columns, the ratios hold for the others: 26, 34, 40, 60 us at 32, 48, 64, 96 tokens)
         static int ncu = 0;
-        if (!ncu) check(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, 0), "hipDeviceGetAttribute");
+        if (!ncu) {
+            check(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, 0), "hipDeviceGetAttribute");
+            check(hipFuncSetAttribute((const void*) k_router_mm<96>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      RM_WAVES / 2 * 96 * RM_PITCH * 4), "hipFuncSetAttribute");
+        }
         const int rb = (L + RM_ROWS - 1) / RM_ROWS;
         int tok = 32;
-        double best = 0.0;
-        for (const auto& [tk, eff] : {std::pair<int, double>{32, 1.0}, {48, 0.93}, {64, 0.8}}) {
-            const long nb = (long) rb * ((T + tk - 1) / tk);
-            const double cost = (double) ((nb + ncu - 1) / ncu) * tk * eff;
+        long best = 0;
+        for (const auto& [tk, round_us] : {std::pair<int, long>{32, 26}, {48, 34}, {64, 40}, {96, 60}}) {
+            const long nb = (long) rb * ((T + tk - 1) / tk), cost = (nb + ncu - 1) / ncu * round_us;
             if (tk == 32 || cost < best) tok = tk, best = cost;
         }
         const dim3 g(rb, (T + tok - 1) / tok);
@@ -608,7 +611,8 @@ void router_logits(const float* W, const float* x, float* logits, int T, int H, 
         switch (tok) {
             case 32: k_router_mm<32><<<g, RM_THREADS, lds, st>>>(W, x, logits, T, H, L, xh); break;
             case 48: k_router_mm<48><<<g, RM_THREADS, lds, st>>>(W, x, logits, T, H, L, xh); break;
-            default: k_router_mm<64><<<g, RM_THREADS, lds, st>>>(W, x, logits, T, H, L, xh); break;
+            case 64: k_router_mm<64><<<g, RM_THREADS, lds, st>>>(W, x, logits, T, H, L, xh); break;
+            default: k_router_mm<96><<<g, RM_THREADS, lds, st>>>(W, x, logits, T, H, L, xh); break;
         }
         check(hipGetLastError(), "k_router_mm launch");
     }
