@@ -573,8 +573,11 @@ void router_logits(const float* W, const float* x, float* logits, int T, int H, 
         if (T < RM_MIN_T) {   // the VALU kernel (row_dot's order)
             const int rt = H / 256 <= 8 ? 4 : 2, rb = (L + LT_WAVES * rt - 1) / (LT_WAVES * rt);
             // tokens a block (a multiple of LT_RU): the fewest that keep the grid within one block a compute unit
-            static int ncu = 0;
-            if (!ncu) check(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, 0), "hipDeviceGetAttribute");
+            static const int ncu = [] {
+                int n = 0;
+                check(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, 0), "hipDeviceGetAttribute");
+                return n;
+            }();
             int tok = LT_RU;
             while ((long) rb * ((T + tok - 1) / tok) > ncu && tok < T) tok += LT_RU;
             const dim3 g(rb, (T + tok - 1) / tok);
@@ -593,12 +596,13 @@ void router_logits(const float* W, const float* x, float* logits, int T, int H, 
         // tokens a workgroup: a taller tile requests fewer operands a multiply-add but makes fewer workgroups.  The
         // estimate: rounds of workgroups over the compute units times a round's time for the tile (measured at 2048
         // columns, the ratios hold for the others: 26, 34, 40, 60 us at 32, 48, 64, 96 tokens)
-        static int ncu = 0;
-        if (!ncu) {
-            check(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, 0), "hipDeviceGetAttribute");
+        static const int ncu = [] {   // once (a static initializer: thread-safe), with the 96-token tile's LDS allowed
+            int n = 0;
+            check(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, 0), "hipDeviceGetAttribute");
             check(hipFuncSetAttribute((const void*) k_router_mm<96>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                       RM_WAVES / 2 * 96 * RM_PITCH * 4), "hipFuncSetAttribute");
-        }
+            return n;
+        }();
         const int rb = (L + RM_ROWS - 1) / RM_ROWS;
         int tok = 32;
         long best = 0;
