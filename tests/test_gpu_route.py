@@ -99,7 +99,7 @@ def test_router_logits_bit_exact(T, H, L):
 
 
 @pytest.mark.parametrize("T, H, L", [(300, 2048, 513), (600, 2048, 513), (777, 2560, 1025), (2048, 4096, 129),
-                                     (1200, 1024, 1025)])
+                                     (1000, 1024, 513), (1200, 1024, 1025)])
 def test_router_logits_xh(T, H, L):
     """sfnx_router_logits_xh: the same logits as sfnx_router_logits, and xh equal to sfnx_to_f16's, bit for bit"""
     W = torch.from_numpy(orc.synth(L * H, 222, 0.02).reshape(L, H)).cuda()
