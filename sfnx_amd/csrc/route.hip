@@ -331,36 +331,65 @@ __global__ void __launch_bounds__(RR_THREADS) k_pf_topk(const float* __restrict_
         topw[(size_t) t * K + lane] = w;
     }
 }
-// src/prefill.cu:248-279 k_pf_fill: a block per expert scans the pairs in index order, 4 consecutive pairs a thread and
-// 1024 a pass, its slots from a prefix over the threads of the pass (ballots of the count bits, then the wavefronts in
-// order), so a pair always lands in the same job and slot
-// Each block first counts every expert's picks in LDS (src/prefill.cu:223-226 k_pf_count; block e writes cnt[e]: no
-// global atomics, which serialised on the experts many tokens pick), then finds its expert's first job
-// (src/prefill.cu:228-242 k_pf_jobbase: the exclusive prefix of ceil(cnt / 64) in expert order); block 0 writes the
-// job count, and blocks E.. lay out the shared expert's jobs after the routed ones (tokens in order, 64 a job).
-constexpr int PF_FILL_THREADS = 1024, PF_FILL_PASS = 4 * PF_FILL_THREADS;   // 4,096 pairs a pass (a quarter of the barriers of 256)
+// src/prefill.cu:248-279 k_pf_fill: a block per expert ranks its pairs in index order, 4 consecutive pairs a thread and
+// 4,096 a pass, its slots from a prefix over the threads of the pass (ballots of the count bits, then the wavefronts in
+// order), so a pair always lands in the same job and slot.  The same scan counts every expert's picks in LDS
+// (src/prefill.cu:223-226 k_pf_count; block e writes cnt[e]: no global atomics, which serialised on the experts many
+// tokens pick); then the block finds its expert's first job (src/prefill.cu:228-242 k_pf_jobbase: the exclusive prefix
+// of ceil(cnt / 64) in expert order) and writes the jobs from its ranked list, a pair a thread (a second scan places
+// them when more than PF_OWN_MAX tokens pick the expert).  Block 0 writes the job count, and the blocks together lay
+// out the shared expert's jobs after the routed ones (tokens in order, 64 a job).
+constexpr int PF_FILL_THREADS = 1024, PF_FILL_PASS = 4 * PF_FILL_THREADS, PF_OWN_MAX = 4096;
 __global__ void __launch_bounds__(PF_FILL_THREADS) k_pf_fill(const int* __restrict__ topi, int P, int K, int E, int C,
                                                             int shared, int* __restrict__ cnt, int* __restrict__ jbase,
                                                             int* __restrict__ njobs, sfnx_bigjob* __restrict__ gu,
                                                             sfnx_bigjob* __restrict__ dn) {
     const int tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE;
-    const int e = min((int) blockIdx.x, E);   // E: a block of the shared expert's jobs
+    const int e = blockIdx.x;
     __shared__ int wsum[2][PF_FILL_THREADS / WAVE];
     __shared__ int hist[MAX_E];
     for (int i = tid; i < E; i += PF_FILL_THREADS) hist[i] = 0;
     __syncthreads();
-    for (int p = 4 * tid; p < P; p += PF_FILL_PASS) {
-        int q[4];
-        if (p + 3 < P) {
-            const int4 v = *reinterpret_cast<const int4*>(topi + p);
-            q[0] = v.x, q[1] = v.y, q[2] = v.z, q[3] = v.w;
-        } else {
+    // one scan: every pair counted, and this expert's pairs ranked in index order (ballot prefixes within a
+    // wavefront, then the wavefronts in order) into `own`
+    __shared__ int own[PF_OWN_MAX];
+    __shared__ int wc1[2][PF_FILL_THREADS / WAVE];
+    const uint64_t lt1 = (1ull << lane) - 1ull;
+    // a pass's 4 pairs a thread (P is a multiple of 4 or the tail is scalar); the next pass's are requested before
+    // this pass's barrier
+    auto pairs_at = [&](int p) {
+        if (p + 3 < P) return *reinterpret_cast<const int4*>(topi + p);
+        return make_int4(p < P ? topi[p] : -1, p + 1 < P ? topi[p + 1] : -1, p + 2 < P ? topi[p + 2] : -1, -1);
+    };
+    int ce = 0;
+    int4 nxt = pairs_at(4 * tid);
+    for (int p0 = 0, it = 0; p0 < P; p0 += PF_FILL_PASS, ++it) {
+        const int p = p0 + 4 * tid;
+        const int q[4] = {nxt.x, nxt.y, nxt.z, nxt.w};
+        if (p0 + PF_FILL_PASS < P) nxt = pairs_at(p + PF_FILL_PASS);
+        int mine = 0;
 #pragma unroll
-            for (int c = 0; c < 4; ++c) q[c] = p + c < P ? topi[p + c] : -1;
+        for (int c = 0; c < 4; ++c) {
+            if (q[c] >= 0) atomicAdd(&hist[q[c]], 1);
+            mine += q[c] == e;
         }
+        const uint64_t b0 = __ballot(mine & 1), b1 = __ballot(mine & 2), b2 = __ballot(mine & 4);
+        if (lane == 0) wc1[it & 1][wave] = __popcll(b0) + 2 * __popcll(b1) + 4 * __popcll(b2);
+        __syncthreads();
+        int before = __popcll(b0 & lt1) + 2 * __popcll(b1 & lt1) + 4 * __popcll(b2 & lt1), total = 0;
+#pragma unroll
+        for (int w = 0; w < PF_FILL_THREADS / WAVE; ++w) {
+            before += w < wave ? wc1[it & 1][w] : 0;
+            total += wc1[it & 1][w];
+        }
+        int r = ce + before;
 #pragma unroll
         for (int c = 0; c < 4; ++c)
-            if (q[c] >= 0) atomicAdd(&hist[q[c]], 1);
+            if (q[c] == e) {
+                if (r < PF_OWN_MAX) own[r] = p + c;
+                ++r;
+            }
+        ce += total;
     }
     __syncthreads();
     int jb0 = 0, jall = 0;   // jobs of the experts before e, of all experts
@@ -382,8 +411,8 @@ __global__ void __launch_bounds__(PF_FILL_THREADS) k_pf_fill(const int* __restri
         jb0 += wsum[0][w];
         jall += wsum[1][w];
     }
-    if ((int) blockIdx.x >= E) {   // the shared expert's jobs
-        for (int t = ((int) blockIdx.x - E) * PF_FILL_THREADS + tid; t < C; t += ((int) gridDim.x - E) * PF_FILL_THREADS) {
+    if (shared) {   // the shared expert's jobs, its tokens spread over the blocks
+        for (int t = e * PF_FILL_THREADS + tid; t < C; t += E * PF_FILL_THREADS) {
             const int j = jall + t / SFNX_PF_JOB, k = t % SFNX_PF_JOB;
             gu[j].y[k] = t;
             gu[j].out[k] = dn[j].y[k] = dn[j].out[k] = P + t;
@@ -392,15 +421,28 @@ __global__ void __launch_bounds__(PF_FILL_THREADS) k_pf_fill(const int* __restri
                 gu[j].n = dn[j].n = min(SFNX_PF_JOB, C - t);
             }
         }
-        return;
     }
-    const int ce = hist[e];
     if (tid == 0) {
         cnt[e] = ce;
         jbase[e] = jb0;
         if (e == 0) njobs[0] = jall + (shared ? (C + SFNX_PF_JOB - 1) / SFNX_PF_JOB : 0);
     }
     if (ce == 0) return;
+    if (ce <= PF_OWN_MAX) {   // the jobs straight from the ranked list, a pair a thread
+        for (int r = tid; r < ce; r += PF_FILL_THREADS) {
+            const int pc = own[r], j = jb0 + r / SFNX_PF_JOB, k = r % SFNX_PF_JOB;
+            gu[j].y[k] = pc / K;
+            gu[j].out[k] = pc;
+            dn[j].y[k] = pc;
+            dn[j].out[k] = pc;
+            if (k == 0) {
+                gu[j].w = dn[j].w = e;
+                gu[j].n = dn[j].n = min(SFNX_PF_JOB, ce - r);
+            }
+        }
+        return;
+    }
+    // more pairs than the list holds: a second scan places them
     __shared__ int wcount[2][PF_FILL_THREADS / WAVE];
     const uint64_t lt = (1ull << lane) - 1ull;
     int base = 0;
@@ -644,8 +686,7 @@ extern "C" int sfnx_pf_route(const float* logits, int C, int E, int K, int* topi
         hipStream_t s = stream_of(st);
         const int P = C * K;
         k_pf_topk<<<(C + RR_WAVES - 1) / RR_WAVES, RR_THREADS, 0, s>>>(logits, C, E, K, topi, topw);
-        const int nsh = shared ? std::min(8, (C + PF_FILL_THREADS - 1) / PF_FILL_THREADS) : 0;
-        k_pf_fill<<<E + nsh, PF_FILL_THREADS, 0, s>>>(topi, P, K, E, C, shared, cnt, jbase, njobs, jobs_gu, jobs_dn);
+        k_pf_fill<<<E, PF_FILL_THREADS, 0, s>>>(topi, P, K, E, C, shared, cnt, jbase, njobs, jobs_gu, jobs_dn);
     });
 }
 

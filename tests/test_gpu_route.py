@@ -153,12 +153,17 @@ def test_topk_near_ties_across_lanes():
     assert np.allclose(topw, ow, rtol=1e-6, atol=1e-7)
 
 
-@pytest.mark.parametrize("C, shared", [(300, True), (2048, False), (1, True)])
-def test_pf_route_bit_exact(C, shared):
+@pytest.mark.parametrize("C, shared, hot", [(300, True, False), (2048, False, False), (1, True, False),
+                                             (4096, True, True), (5000, False, True)])
+def test_pf_route_bit_exact(C, shared, hot):
+    """hot: every token picks expert 7, so its pairs fill the fill kernel's ranked list exactly (4096) or overflow it
+    into the second scan (5000)"""
     E, K = 512, 10
     rng = np.random.default_rng(C)
     logits = rng.normal(0, 1, (C, E + 1)).astype(np.float32)
     logits[:, :E] += (1.1 * -np.log(rng.permutation(E) + 1.0)).astype(np.float32) * 0.8   # skew towards some experts
+    if hot:
+        logits[:, 7] += 100.0
     if C > 1:
         logits[1, 3:40] = logits[1, 2]   # ties
     cap = C * K // 64 + E + (C + 63) // 64 + 1
