@@ -95,13 +95,18 @@ __device__ __forceinline__ void q8_block32(float v, int8_t* q, float* d) {
 }
 
 // ------------------------------------------------------------------------------------------------ K_A
+// windows of 8 rows or more run HA_TG groups of HA_THREADS threads a block: group g takes its share of the rows in the
+// slice's set-up and rows g, g + HA_TG, ... in the dots (each output's lanes and order as with one group)
+template <int TT> constexpr int ha_tg() { return TT >= 8 ? 4 : 1; }
 template <int TT>
-__global__ void __launch_bounds__(HA_THREADS) k_hc_down(HcArgs a) {
+__global__ void __launch_bounds__(HA_THREADS * ha_tg<TT>()) k_hc_down(HcArgs a) {
+    constexpr int TG = ha_tg<TT>();
     __shared__ __align__(16) float xs[TT][HS];
     __shared__ __align__(16) int8_t xq[TT][HS];
     __shared__ float xd[TT][HS / 32];
     __shared__ float red[TT][HS / 32];
-    const int T = a.T, s = blockIdx.x, grp = blockIdx.y, tid = threadIdx.x, D = a.HC * a.N;
+    const int T = a.T, s = blockIdx.x, grp = blockIdx.y, tid = threadIdx.x % HA_THREADS, tg = threadIdx.x / HA_THREADS;
+    const int D = a.HC * a.N;
     const int NS = D / HS, ROWS = a.LR + a.HC, col0 = s * HS, c = col0 / a.N, i0 = col0 % a.N;
     // this block's weight row, loaded first: 8 lanes a row, lane j the chunks 8 q + j
     const int row = grp * HA_ROWS + tid / 8, j = tid % 8;
@@ -126,8 +131,8 @@ __global__ void __launch_bounds__(HA_THREADS) k_hc_down(HcArgs a) {
     // R' of the slice into xs, the rows' loads (and the fold's inject logits) issued RB at a time: batch m, element k
     // is row RB / 2 m + k / 2, column tid + 256 (k % 2), so a thread takes each row's gate once
     static_assert(HS == 2 * HA_THREADS, "two columns of a slice a thread");
-    constexpr int RB = TT >= 8 ? 16 : 8;
-    for (int t0 = 0; t0 < T; t0 += RB / 2) {
+    constexpr int RB = TG > 1 ? 8 : TT >= 8 ? 16 : 8;
+    for (int t0 = tg * (RB / 2); t0 < T; t0 += TG * (RB / 2)) {
         float r[RB], b[RB], g[RB / 2];
 #pragma unroll
         for (int k = 0; k < RB; ++k) {
@@ -153,7 +158,8 @@ __global__ void __launch_bounds__(HA_THREADS) k_hc_down(HcArgs a) {
     // the square sums (row group 0 only): 32 consecutive columns a half-wave; then xs = R' w_norm
     const int hw = tid / 32;
 #pragma unroll
-    for (int t = 0; t < TT; ++t) {
+    for (int t0 = 0; t0 < TT; t0 += TG) {
+        const int t = t0 + tg;
         if (t >= T) break;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -167,14 +173,14 @@ __global__ void __launch_bounds__(HA_THREADS) k_hc_down(HcArgs a) {
         }
     }
     __syncthreads();
-    if (grp == 0 && tid < T) {
+    if (grp == 0 && tg == 0 && tid < T) {
         float v = 0.f;
         for (int w = 0; w < HS / 32; ++w) v += red[tid][w];
         a.ssp[(size_t) tid * NS + s] = v;
     }
     // xs as int8 per 32 (q8_block32's arithmetic: an exact maximum, then each value on its own): 8 threads a block,
     // 4 consecutive values each, so a pass covers 32 blocks
-    for (int q = tid / 8; q < T * (HS / 32); q += HA_THREADS / 8) {
+    for (int q = (int) threadIdx.x / 8; q < T * (HS / 32); q += TG * HA_THREADS / 8) {
         const int t = q / (HS / 32), b = q % (HS / 32), l8 = tid % 8;
         const float4 v = *reinterpret_cast<const float4*>(&xs[t][32 * b + 4 * l8]);
         const float amax = group_max<8>(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
@@ -189,7 +195,8 @@ __global__ void __launch_bounds__(HA_THREADS) k_hc_down(HcArgs a) {
     __syncthreads();
     if (row >= ROWS) return;   // whole 8-lane groups: the butterfly stays inside live groups
 #pragma unroll
-    for (int t = 0; t < TT; ++t) {
+    for (int t0 = 0; t0 < TT; t0 += TG) {
+        const int t = t0 + tg;
         if (t >= T) break;
         float acc = 0.f;
         if (dn_row) {
@@ -448,7 +455,7 @@ __global__ void __launch_bounds__(HC_THREADS) k_hc_up(HcArgs a) {
 
 template <int TT> void hc_launch(const HcArgs& a, hipStream_t s) {
     const int NS = a.HC * a.N / HS, RG = (a.LR + a.HC + HA_ROWS - 1) / HA_ROWS;
-    k_hc_down<TT><<<dim3(NS, RG), HA_THREADS, 0, s>>>(a);
+    k_hc_down<TT><<<dim3(NS, RG), HA_THREADS * ha_tg<TT>(), 0, s>>>(a);
     check(hipGetLastError(), "k_hc_down launch");
     if constexpr (TT == 1) {
         if (a.LR + a.HC <= HC_THREADS) {
