@@ -293,9 +293,12 @@ __global__ void __launch_bounds__(256) k_hc_reduce(HcArgs a) {
 // reference's 16-lane xor butterfly (partner 1, 2, 4, 8; lanes past LR / 32 hold zeros), so no lane idles in a
 // shuffle.  ONE (one row, LR + HC <= 512): the block makes lo and rs itself from the slices' partials (K_B's sums,
 // the same bits), so the read takes two launches (src/hc.cuh's one-barrier form does the same).
+// windows of 8 rows or more take 1024 threads a block (fewer dot items a thread)
+template <int TT> constexpr int hc_up_threads() { return TT >= 8 ? 1024 : HC_THREADS; }
 template <int TT, bool ONE>
-__global__ void __launch_bounds__(HC_THREADS) k_hc_up(HcArgs a) {
-    constexpr int PER = (TT * HC_MAX * HC_COLS + HC_THREADS - 1) / HC_THREADS;   // (t, c, column) items a thread
+__global__ void __launch_bounds__(hc_up_threads<TT>()) k_hc_up(HcArgs a) {
+    constexpr int NTH = hc_up_threads<TT>();
+    constexpr int PER = (TT * HC_MAX * HC_COLS + NTH - 1) / NTH;   // (t, c, column) items a thread
     __shared__ __align__(16) int8_t wq[HC_COLS * (HCLR_MAX + 16 * HC_MAX)];   // row rr = c 32 + column at rr (LR + 16)
     __shared__ float wsl[HC_COLS * HCLR_MAX / 32];
     __shared__ __align__(16) int8_t lq[TT][LR_MAX];
@@ -311,12 +314,12 @@ __global__ void __launch_bounds__(HC_THREADS) k_hc_up(HcArgs a) {
     {
         const int per_row = a.LR / 16, n16 = nrow * per_row;
 #pragma unroll 4
-        for (int e = tid; e < n16; e += HC_THREADS) {
+        for (int e = tid; e < n16; e += NTH) {
             const int rr = e / per_row;
             const size_t u = (size_t) (rr / HC_COLS) * a.N + dc0 + rr % HC_COLS;
             reinterpret_cast<uint4*>(wq)[rr * (per_row + 1) + e % per_row] = reinterpret_cast<const uint4*>(a.uq + u * a.LR)[e % per_row];
         }
-        for (int e = tid; e < nrow * NB; e += HC_THREADS) {
+        for (int e = tid; e < nrow * NB; e += NTH) {
             const int rr = e / NB;
             wsl[e] = h2f(a.ud[((size_t) (rr / HC_COLS) * a.N + dc0 + rr % HC_COLS) * NB + e % NB]);
         }
@@ -324,7 +327,7 @@ __global__ void __launch_bounds__(HC_THREADS) k_hc_up(HcArgs a) {
     float rv[PER], bv[PER], wn[PER];
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
-        const int e = tid + k * HC_THREADS;
+        const int e = tid + k * NTH;
         if (e < nitem) {
             const int cl = e % HC_COLS, c = (e / HC_COLS) % a.HC, t = e / (HC_COLS * a.HC), dc = dc0 + cl;
             rv[k] = a.R[(size_t) t * a.HC * a.N + (size_t) c * a.N + dc];
@@ -348,13 +351,13 @@ __global__ void __launch_bounds__(HC_THREADS) k_hc_up(HcArgs a) {
         }
     } else {
         const int nq = T * a.LR / 4;
-        for (int e0 = tid; e0 < nq; e0 += 4 * HC_THREADS) {
+        for (int e0 = tid; e0 < nq; e0 += 4 * NTH) {
             int v[4];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) v[k] = e0 + k * HC_THREADS < nq ? reinterpret_cast<const int*>(a.loq)[e0 + k * HC_THREADS] : 0;
+            for (int k = 0; k < 4; ++k) v[k] = e0 + k * NTH < nq ? reinterpret_cast<const int*>(a.loq)[e0 + k * NTH] : 0;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                const int e = e0 + k * HC_THREADS;
+                const int e = e0 + k * NTH;
                 if (e < nq) reinterpret_cast<int*>(&lq[e / (a.LR / 4)][0])[e % (a.LR / 4)] = v[k];
             }
         }
@@ -366,7 +369,7 @@ __global__ void __launch_bounds__(HC_THREADS) k_hc_up(HcArgs a) {
     // item (t, c, column): the up row c 32 + column of the block against lo row t.  With few items (one row: 4 streams
     // x 32 columns for 512 threads) 4 consecutive lanes share an item, lane q taking leaves 4 q .. 4 q + 3 of the tree
     // below and lane exchanges (partners 1, then 2) making its last two levels: the same sums in the same pairs
-    if (T * nrow * 4 <= HC_THREADS) {
+    if (T * nrow * 4 <= NTH) {
         const int it = tid / 4, q = tid % 4;
         const bool live = it < T * nrow;
         const int t = live ? it / nrow : 0, rr = live ? it % nrow : 0, c = rr / HC_COLS, cl = rr % HC_COLS;
@@ -390,7 +393,7 @@ __global__ void __launch_bounds__(HC_THREADS) k_hc_up(HcArgs a) {
         w = w + lane_xor<2>(w);
         if (live && q == 0) gs[t][c][cl] = w;
     } else
-    for (int it = tid; it < T * nrow; it += HC_THREADS) {
+    for (int it = tid; it < T * nrow; it += NTH) {
         const int t = it / nrow, rr = it % nrow, c = rr / HC_COLS, cl = rr % HC_COLS;
         {
             // block b's (d_w d_lo) dot32, 0 past LR / 32 (the lanes of the reference's butterfly that hold no block)
@@ -422,7 +425,7 @@ __global__ void __launch_bounds__(HC_THREADS) k_hc_up(HcArgs a) {
     // item (t, c, column): the gate times the normalised stream, R <- R'
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
-        const int e = tid + k * HC_THREADS;
+        const int e = tid + k * NTH;
         if (e < nitem) {
             const int cl = e % HC_COLS, c = (e / HC_COLS) % a.HC, t = e / (HC_COLS * a.HC), dc = dc0 + cl;
             const float r = a.bo ? fmaf(bv[k], sg[t][c], rv[k]) : rv[k];
@@ -431,7 +434,7 @@ __global__ void __launch_bounds__(HC_THREADS) k_hc_up(HcArgs a) {
         }
     }
     __syncthreads();
-    for (int e = tid; e < T * HC_COLS; e += HC_THREADS) {
+    for (int e = tid; e < T * HC_COLS; e += NTH) {
         const int cl = e % HC_COLS, t = e / HC_COLS;
         float m = gs[t][0][cl];
         for (int c = 1; c < a.HC; ++c) m += gs[t][c][cl];
@@ -442,7 +445,7 @@ __global__ void __launch_bounds__(HC_THREADS) k_hc_up(HcArgs a) {
     if (a.xq == nullptr) return;
     __syncthreads();
     // mixed as q8_1 (k_quantize's arithmetic): a half-wave per row's block
-    for (int t = tid / 32; t < T; t += HC_THREADS / 32) {
+    for (int t = tid / 32; t < T; t += NTH / 32) {
         const int l = tid % 32;
         const float xi = ms[t][l];
         const float amax = group_max<32>(fabsf(xi)), sum = group_sum<32>(xi);
@@ -459,7 +462,7 @@ template <int TT> void hc_launch(const HcArgs& a, hipStream_t s) {
     check(hipGetLastError(), "k_hc_down launch");
     if constexpr (TT == 1) {
         if (a.LR + a.HC <= HC_THREADS) {
-            k_hc_up<TT, true><<<a.N / HC_COLS, HC_THREADS, 0, s>>>(a);
+            k_hc_up<TT, true><<<a.N / HC_COLS, hc_up_threads<TT>(), 0, s>>>(a);
             check(hipGetLastError(), "k_hc_up launch");
             return;
         }
@@ -468,7 +471,7 @@ template <int TT> void hc_launch(const HcArgs& a, hipStream_t s) {
         const int items = a.T * (a.LR / 32 + 1);
         k_hc_reduce<<<(items + 7) / 8, 256, 0, s>>>(a);
         check(hipGetLastError(), "k_hc_reduce launch");
-        k_hc_up<TT, false><<<a.N / HC_COLS, HC_THREADS, 0, s>>>(a);
+        k_hc_up<TT, false><<<a.N / HC_COLS, hc_up_threads<TT>(), 0, s>>>(a);
     }
     check(hipGetLastError(), "k_hc_up launch");
 }
