@@ -31,7 +31,7 @@ def run(N, HC, LR, T, seed, fold, inject=True):
 
 
 @pytest.mark.parametrize("N,HC,LR", [(2560, 4, 320), (512, 2, 96), (1024, 8, 256), (512, 1, 512)])
-@pytest.mark.parametrize("T", [1, 5, 16])
+@pytest.mark.parametrize("T", [1, 3, 5, 16])
 def test_hc_read_against_oracle_no_fold(N, HC, LR, T):
     h, Rd, mixed, xq, injo, (om, oi, oxq, oR, opart, ossp) = run(N, HC, LR, T, 100 + T + N, fold=False)
     NS = HC * N // 512
