@@ -519,7 +519,7 @@ def bench_hc_read(moe, torch, reps=20):
     h = moe.HcRead(N, HC, LR, 1 + 0.1 * torch.randn(D, device="cuda", generator=g), q(LR, D), sc(LR, D // 32),
                    q(D, LR), sc(D, LR // 32), (0.02 * torch.randn((HC, D), device="cuda", generator=g)).bfloat16().view(torch.int16))
     out = {"workload": "hc read (src/hc.cuh) at N 2560, 4 streams, rank 320, with the fold; HIP-graph replays"}
-    for T in (1, 16):
+    for T in (1, 4, 16):
         R0 = torch.randn((T, D), device="cuda", generator=g)
         R = R0.clone()
         bo = torch.randn((T, N), device="cuda", generator=g)

@@ -95,9 +95,9 @@ __device__ __forceinline__ void q8_block32(float v, int8_t* q, float* d) {
 }
 
 // ------------------------------------------------------------------------------------------------ K_A
-// windows of 8 rows or more run HA_TG groups of HA_THREADS threads a block: group g takes its share of the rows in the
+// windows of more than one row run 4 groups of HA_THREADS threads a block: group g takes its share of the rows in the
 // slice's set-up and rows g, g + HA_TG, ... in the dots (each output's lanes and order as with one group)
-template <int TT> constexpr int ha_tg() { return TT >= 8 ? 4 : 1; }
+template <int TT> constexpr int ha_tg() { return TT >= 4 ? 4 : 1; }
 template <int TT>
 __global__ void __launch_bounds__(HA_THREADS * ha_tg<TT>()) k_hc_down(HcArgs a) {
     constexpr int TG = ha_tg<TT>();
@@ -131,7 +131,7 @@ __global__ void __launch_bounds__(HA_THREADS * ha_tg<TT>()) k_hc_down(HcArgs a) 
     // R' of the slice into xs, the rows' loads (and the fold's inject logits) issued RB at a time: batch m, element k
     // is row RB / 2 m + k / 2, column tid + 256 (k % 2), so a thread takes each row's gate once
     static_assert(HS == 2 * HA_THREADS, "two columns of a slice a thread");
-    constexpr int RB = TG > 1 ? 8 : TT >= 8 ? 16 : 8;
+    constexpr int RB = TG > 1 ? 2 * (TT / TG) : 8;   // a group's rows of a window in one batch
     for (int t0 = tg * (RB / 2); t0 < T; t0 += TG * (RB / 2)) {
         float r[RB], b[RB], g[RB / 2];
 #pragma unroll
