@@ -26,19 +26,23 @@ constexpr int D3_THREADS = 256, D3_ROWS = 8;                    // K3: output ro
 template <int TYPE> constexpr int d2_threads() { return 32 * lpr_of<TYPE>(); }   // K2: 32 FF indices a block
 
 // ------------------------------------------------------------------------------------------------ K1
+// windows: 4 wavefronts a block on the block's row, wavefront g taking tokens g, g + 4, ... (each logit's lanes and
+// order as with one wavefront)
+template <int TT> constexpr int d1_groups() { return TT > 1 ? 4 : 1; }
 template <int NC, int TT>
-__global__ void __launch_bounds__(D1_THREADS) k_dec_router(const float* __restrict__ W, const float* __restrict__ x, int T,
+__global__ void __launch_bounds__(D1_THREADS * d1_groups<TT>()) k_dec_router(const float* __restrict__ W, const float* __restrict__ x, int T,
                                                           int E, float eps, int norm, float* __restrict__ logits,
                                                           uint8_t* __restrict__ xq) {
-    constexpr int H = NC * 4 * WAVE, NQ = 2;
-    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE, L = E + 1;
-    const int row = blockIdx.x * D1_WAVES + wave;
+    constexpr int H = NC * 4 * WAVE, NQ = 2, TG = d1_groups<TT>(), NTH = D1_THREADS * TG;
+    static_assert(D1_WAVES == 1, "a router row a block");
+    const int tg = threadIdx.x / WAVE, lane = threadIdx.x % WAVE, L = E + 1;
+    const int row = blockIdx.x;
     // every load of the launch issued up front: the router row, each token's chunks, this half-wave's q8_1 blocks
-    const int nb = H / 32, hw = threadIdx.x / 32, l = threadIdx.x % 32, nslot = gridDim.x * (D1_THREADS / 32);
+    const int nb = H / 32, hw = threadIdx.x / 32, l = threadIdx.x % 32, nslot = gridDim.x * (NTH / 32);
     float xqv[NQ];
 #pragma unroll
     for (int k = 0; k < NQ; ++k) {
-        const int q = blockIdx.x * (D1_THREADS / 32) + hw + k * nslot;
+        const int q = blockIdx.x * (NTH / 32) + hw + k * nslot;
         xqv[k] = q < T * nb ? x[(size_t) (q / nb) * H + 32 * (q % nb) + l] : 0.f;
     }
     const bool live = row < L;
@@ -46,26 +50,27 @@ __global__ void __launch_bounds__(D1_THREADS) k_dec_router(const float* __restri
 #pragma unroll
     for (int i = 0; i < NC; ++i) wv[i] = reinterpret_cast<const float4*>(W + (size_t) (live ? row : 0) * H)[i * WAVE + lane];
     __shared__ float rs[SFNX_MAXT];
-    // windows: token t + 1's chunks are loaded while token t's reductions run
+    // windows: the wavefront's next token's chunks are loaded while this token's reductions run
     float4 xn[NC];
 #pragma unroll
-    for (int i = 0; i < NC; ++i) xn[i] = reinterpret_cast<const float4*>(x)[i * WAVE + lane];
+    for (int i = 0; i < NC; ++i) xn[i] = reinterpret_cast<const float4*>(x + (size_t) min(tg, T - 1) * H)[i * WAVE + lane];
 #pragma unroll
-    for (int t = 0; t < TT; ++t) {
+    for (int t0 = 0; t0 < TT; t0 += TG) {
+        const int t = t0 + tg;
         if (t >= T) break;
         float4 xv[NC];
         float ss = 0.f;
 #pragma unroll
         for (int i = 0; i < NC; ++i) xv[i] = xn[i];
-        if (TT > 1 && t + 1 < T) {
-            const float4* x4 = reinterpret_cast<const float4*>(x + (size_t) (t + 1) * H);
+        if (TT > 1 && t + TG < T) {
+            const float4* x4 = reinterpret_cast<const float4*>(x + (size_t) (t + TG) * H);
 #pragma unroll
             for (int i = 0; i < NC; ++i) xn[i] = x4[i * WAVE + lane];
         }
 #pragma unroll
         for (int i = 0; i < NC; ++i) ss = rms_lane_add(xv[i], ss);
         const float r = norm ? rms_from_sum(ss, H, eps) : 1.0f;
-        if (threadIdx.x == 0) rs[t] = r;
+        if (lane == 0) rs[t] = r;
         float a = 0.f;
 #pragma unroll
         for (int i = 0; i < NC; ++i) {
@@ -81,7 +86,7 @@ __global__ void __launch_bounds__(D1_THREADS) k_dec_router(const float* __restri
     // the normalised rows as q8_1 (k_quantize's arithmetic), a half-wave per 32-block, spread over the grid
 #pragma unroll
     for (int k = 0; k < NQ; ++k) {
-        const int q = blockIdx.x * (D1_THREADS / 32) + hw + k * nslot;
+        const int q = blockIdx.x * (NTH / 32) + hw + k * nslot;
         if (q >= T * nb) break;
         const int t = q / nb;
         const float xi = xqv[k] * rs[t];
@@ -92,7 +97,7 @@ __global__ void __launch_bounds__(D1_THREADS) k_dec_router(const float* __restri
         if (l == 0) *reinterpret_cast<uint32_t*>(blk) = (uint32_t) f2h(d) | ((uint32_t) f2h(sum) << 16);
     }
     // small grids: the blocks past the preloaded ones
-    for (int q = blockIdx.x * (D1_THREADS / 32) + hw + NQ * nslot; q < T * nb; q += nslot) {
+    for (int q = blockIdx.x * (NTH / 32) + hw + NQ * nslot; q < T * nb; q += nslot) {
         const int t = q / nb;
         const float xi = x[(size_t) t * H + 32 * (q % nb) + l] * rs[t];
         const float amax = group_max<32>(fabsf(xi)), sum = group_sum<32>(xi);
@@ -599,7 +604,7 @@ void launch(int idx, F kern, dim3 grid, dim3 block, size_t shmem, hipStream_t s,
 template <int NC, int TT>
 void launch_k1(const DecArgs& d, const sfnx_moe_layer_w& w, float* x, const DecLayout& L, char* ws, hipStream_t s) {
     const int rows = d.E + 1;
-    launch(0, k_dec_router<NC, TT>, dim3((rows + D1_WAVES - 1) / D1_WAVES), dim3(D1_THREADS), 0, s,
+    launch(0, k_dec_router<NC, TT>, dim3((rows + D1_WAVES - 1) / D1_WAVES), dim3(D1_THREADS * d1_groups<TT>()), 0, s,
         w.W, x, d.T, d.E, d.eps, d.norm, (float*) (ws + L.logits), (uint8_t*) (ws + L.xq));
 }
 template <int TYPE, int G> void launch_k2_tt1(const DecArgs&, const sfnx_moe_layer_w&, const DecLayout&, char*, hipStream_t);
