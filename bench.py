@@ -547,7 +547,7 @@ def bench_hc_read(moe, torch, reps=20):
 
 def bench_other_types(moe, torch, NL, steps, warmup):
     """the other expert types the reference decodes (Q5_K, Q4_0, Q5_1) at the same shapes: decode through NL stacked
-    layers, a 2048-token prompt chunk (not BASELINE configs; reported beside them)"""
+    layers, a 2048-token prompt chunk (not among the benchmark configurations; reported beside them)"""
     out = {}
     for name, t, seed in (("q5_k", moe.Q5_K, 6000), ("q4_0", moe.Q4_0, 7000), ("q5_1", moe.Q5_1, 8000)):
         out[name] = bench_type(moe, torch, t, NL, steps, warmup, 2048, seed)
