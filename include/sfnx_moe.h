@@ -57,6 +57,14 @@ typedef struct sfnx_bigjob {
     int out[SFNX_PF_JOB];
 } sfnx_bigjob;
 
+/* src/model.hpp:71-74 Q8S: a dense Q8_0 matrix [rows][cols] in the reference's split layout (src/model.cpp:384-440
+ * q8split): int8 values q [rows][cols] row-major and the f16 scale bits d [rows][cols / 32] of each 32-value block.
+ * The shared expert's dense matrices cross the boundary in it (DW::s). */
+typedef struct sfnx_q8s {
+    int8_t* q;
+    uint16_t* d;
+} sfnx_q8s;
+
 /* ---------------------------------------------------------------------------------------------- errors */
 const char* sfnx_last_error(void);
 int sfnx_abi_version(void);
@@ -145,10 +153,13 @@ int sfnx_to_f16(const float* x, uint16_t* y, size_t n, void* st);
 
 /* ---------------------------------------------------------------------------------------------- dense Q8_0 */
 /* src/kernels.hpp:47 q8s_gemv (kernel src/dense.cuh:24-154): out[t][r] (row stride out_stride) for t < T = row r of the
- * dense Q8_0 matrix W [rows][cols] (planar Q8_0 layout, one matrix; rows % 32 == 0, cols % 512 == 0) dotted with q8_1
- * row t of y ([T][cols / 32] blocks): 32 lanes a row, lane l the 16-column halves 16 l + 512 i in order, each
+ * dense Q8_0 matrix W [rows][cols] (sfnx_q8s split layout; rows % 32 == 0, cols % 512 == 0) dotted with q8_1 row t of
+ * y ([T][cols / 32] blocks): 32 lanes a row, lane l the 16-column halves 16 l + 512 i in order, each
  * acc = fmaf(d_w d_a, sum, acc), then the xor butterfly 16 .. 1. */
-int sfnx_q8s_gemv(const void* W, int rows, int cols, const void* y, float* out, int out_stride, int T, void* st);
+int sfnx_q8s_gemv(const sfnx_q8s* W, int rows, int cols, const void* y, float* out, int out_stride, int T, void* st);
+/* src/model.cpp:384-440 q8split: GGUF Q8_0 blocks [rows][cols / 32] (34 bytes: f16 d, 32 int8) into the split planes
+ * of W (cols % 32 == 0).  The loader's conversion, done on the device. */
+int sfnx_q8s_split(const void* blocks, int rows, int cols, const sfnx_q8s* W, void* st);
 /* src/kernels.cu:1948-2024 swiglu_stacked_q8_1: hq row t ([T][ffs / 32] q8_1 blocks) = silu(gu[t][c]) * gu[t][ffs + c]
  * quantized per 32 values (d = amax / 127, q = round(v / d), ds = (f16 d, f16 sum)); gu is [T][2 ffs], ffs % 32 == 0 */
 int sfnx_swiglu_stacked_q8_1(const float* gu, void* hq, int ffs, int T, void* st);
@@ -156,15 +167,17 @@ int sfnx_swiglu_stacked_q8_1(const float* gu, void* hq, int ffs, int T, void* st
  * launch (src/kernels.hpp:281-282 moe_gate_up's sh_down / sh_ffs / sh_gu / sh_out; src/dense.cuh:156-198): out[t][r] =
  * W[r] . q8_1(silu(gu[t][0..ffs)) * gu[t][ffs..2 ffs)) for r < rows, t < T.  h never leaves the workgroup, so no
  * buffer is needed for it; the values equal sfnx_swiglu_stacked_q8_1 followed by sfnx_q8s_gemv, bit for bit. */
-int sfnx_q8s_swiglu_gemv(const void* W, int rows, int ffs, const float* gu, float* out, int out_stride, int T, void* st);
+int sfnx_q8s_swiglu_gemv(const sfnx_q8s* W, int rows, int ffs, const float* gu, float* out, int out_stride, int T,
+                         void* st);
 
 /* src/prefill.cu:407-417 pf_dense_xh (the prompt path's dense matrices, the shared expert's among them): out[c][r]
  * (row stride ldo) = sum_k f16(W[r][k]) xh[c][k] for C f16 rows xh [C][cols], fp32 accumulation.  W is a dense Q8_0
- * matrix (planar, one matrix), run as one expert of the matrix-core kernels (sfnx_moe_down_mma's): its f16 weights are
- * the reference's k_q8s_f16 values (f16(q d)), made in registers, and the products are summed in fp32 where the
- * reference calls cublasGemmEx; the C rows are taken 64 at a time.  wk / wk_bytes keep the reference's argument list
- * (its f16 staging p.wh) and are not used.  rows % 256 == 0, cols % 512 == 0. */
-int sfnx_pf_dense(const void* W, int rows, int cols, const uint16_t* xh, int C, float* out, int ldo, void* wk,
+ * matrix (sfnx_q8s).  As the reference first converts W into its staging buffer wk (k_q8s_f16 into p.wh), W is first
+ * repacked into wk here, into the planar Q8_0 layout of one matrix (rows * cols * 34 / 32 bytes; the reference sizes
+ * wk for f16, twice that), and then run as one expert of the matrix-core kernels (sfnx_moe_down_mma's): its f16
+ * weights are the reference's k_q8s_f16 values (f16(q d)), made in registers, and the products are summed in fp32 where
+ * the reference calls cublasGemmEx; the C rows are taken 64 at a time.  rows % 256 == 0, cols % 512 == 0. */
+int sfnx_pf_dense(const sfnx_q8s* W, int rows, int cols, const uint16_t* xh, int C, float* out, int ldo, void* wk,
                   size_t wk_bytes, void* st);
 
 /* ---------------------------------------------------------------------------------------------- fused decode */
@@ -213,12 +226,11 @@ int sfnx_moe_decode2(const sfnx_moe_layer_w* layers, int n_layers, uint32_t gu_t
 int sfnx_moe_decode_noalloc(const sfnx_moe_layer_w* layers, int n_layers, uint32_t gu_type, uint32_t dn_type, int H, int E,
                             int K, int ff, int shared, float* x, int T, int norm, float eps, void* st);
 
-/* A layer's shared expert as its own dense Q8_0 matrices, as the reference holds it (src/model.hpp:72-83 Q8S,
- * src/model.cpp:384-440 q8split: LayerW::sh_gu, sh_down): gu [2 ff][H] and dn [H][ff], each in the planar Q8_0 layout
- * of sfnx_store_pack (one matrix). */
+/* A layer's shared expert as its own dense Q8_0 matrices, as the reference holds it (src/model.hpp:71-83 Q8S,
+ * src/model.cpp:384-440 q8split: LayerW::sh_gu.s, sh_down.s): gu [2 ff][H] and dn [H][ff], each in the split layout. */
 typedef struct sfnx_moe_shared_q8s {
-    const void* gu;
-    const void* dn;
+    sfnx_q8s gu;
+    sfnx_q8s dn;
 } sfnx_moe_shared_q8s;
 /* sfnx_moe_decode2 with every layer's shared expert from shared_w[l] in the reference's dense q8s arithmetic
  * (src/dense.cuh:24-154; 32 lanes over 16-column halves, fmaf, xor butterfly), as src/engine.cu:936-945 runs it
@@ -290,17 +302,21 @@ int sfnx_gguf_str(const sfnx_gguf* g, const char* key, const char** v);         
  * of the same type and FF) as expert E, and the router W = [ffn_gate_inp rows ; ffn_gate_inp_shexp] (f32 [E+1][H]).
  * Q4_0, Q5_1, Q8_0, Q4_K or Q5_K experts, gate and up of one type, down of that or another; ff0 on a block of the
  * down type (32 or 256 columns), ff1 - ff0 and H multiples of 512.  info (may be null, else 6 ints) receives the
- * gate|up type, H, E, ff1 - ff0, shared and the down type.  A loader, not a hot-path call: it allocates a staging buffer and synchronises the stream.
- * The buffers' sizes come from the file and cannot be checked here: E is ne[2] of blk.<layer>.ffn_gate_exps
- * (sfnx_gguf_find), and gu, dn and W must hold E + 1 experts / rows when the shared expert is present (E otherwise). */
-int sfnx_gguf_moe_layer(const sfnx_gguf* g, int layer, int ff0, int ff1, void* gu, size_t gu_stride, void* dn,
-                        size_t dn_stride, float* W, int* info, void* st);
+ * gate|up type, H, E, ff1 - ff0, shared and the down type.  A loader, not a hot-path call: it allocates a staging
+ * buffer and synchronises the stream.  E comes from the file (ne[2] of blk.<layer>.ffn_gate_exps, sfnx_gguf_find):
+ * gu_bytes and dn_bytes are the sizes of the caller's gu and dn buffers, and w_rows the rows W holds; the call refuses
+ * a layer whose experts (E + 1 with a shared expert that joins the stores, E otherwise) or router rows (E + 1) do not
+ * fit, before it writes anything. */
+int sfnx_gguf_moe_layer(const sfnx_gguf* g, int layer, int ff0, int ff1, void* gu, size_t gu_stride, size_t gu_bytes,
+                        void* dn, size_t dn_stride, size_t dn_bytes, float* W, int w_rows, int* info, void* st);
 /* sfnx_gguf_moe_layer for the model as the reference loads it (src/model.cpp:807-809): the shared expert must be
- * present and Q8_0 ("the shared expert is not Q8_0" otherwise) and goes, as dense matrices, to sh_gu ([2 ffs][H]) and
- * sh_dn ([H][ffs], columns ff0..ff1), each the planar Q8_0 layout of one matrix, for sfnx_moe_decode_q8s and
- * sfnx_q8s_gemv; gu and dn then receive the E routed experts only.  W and info as sfnx_gguf_moe_layer. */
-int sfnx_gguf_moe_layer_q8s(const sfnx_gguf* g, int layer, int ff0, int ff1, void* gu, size_t gu_stride, void* dn,
-                            size_t dn_stride, float* W, void* sh_gu, void* sh_dn, int* info, void* st);
+ * present and Q8_0 ("the shared expert is not Q8_0" otherwise) and goes, as dense matrices in the split layout
+ * (src/model.cpp:384-440 q8split), to sh_gu ([2 ffs][H]) and sh_dn ([H][ffs], columns ff0..ff1), for
+ * sfnx_moe_decode_q8s, sfnx_q8s_gemv and sfnx_pf_dense; gu and dn then receive the E routed experts only.  W, the
+ * buffer sizes and info as sfnx_gguf_moe_layer. */
+int sfnx_gguf_moe_layer_q8s(const sfnx_gguf* g, int layer, int ff0, int ff1, void* gu, size_t gu_stride, size_t gu_bytes,
+                            void* dn, size_t dn_stride, size_t dn_bytes, float* W, int w_rows, const sfnx_q8s* sh_gu,
+                            const sfnx_q8s* sh_dn, int* info, void* st);
 
 /* ---------------------------------------------------------------------------------------------- expert cache */
 /* src/model.hpp:95-116 ExpertCache, src/moe.cuh:19-71 cache_plan, src/kernels.cu:1636-1668: routed experts kept in
@@ -327,6 +343,9 @@ typedef struct sfnx_expert_cache {
     int* owner;                           /* device [n_slots]: the expert in it (layer * n_experts + e), or -1 */
     unsigned char* ref;                   /* device [n_slots]: 0 free to take, 1 used since the hand passed, 2 the layer's */
     int* hand;                            /* device [SFNX_EC_POOLS]: each pool's CLOCK hand, a slot number in it */
+    int* status;                          /* device [2] or null: [0] the misses the last plan left on their host copies
+                                             (0 when every job got a slot), [1] their running total (no counterpart in
+                                             the reference, whose plan spins until a slot frees) */
 } sfnx_expert_cache;
 
 /* page-locked host memory the GPU reads directly (the reference's mapped host copies): *host and *dev receive the host
@@ -337,8 +356,11 @@ int sfnx_host_free(void* host);
  * `layer`: every job whose expert is in a slot keeps it; each other one takes the slot of the layer's pool that the
  * pool's CLOCK hand reaches first with ref 0, a ref 1 it passes dropping to 0, 32 slots a sweep step as the reference's
  * warp; the slot's old expert points back at its host copy.  list (1 + njobs ints) receives the number of experts
- * that took a slot, then their ids (layer * n_experts + e), in job order.  A pool with fewer free slots than misses
- * writes list[0] = -1 and leaves the misses unplanned (the reference would spin). */
+ * that took a slot, then their ids (layer * n_experts + e), in job order.  When every slot of the pool is held by the
+ * window, a miss finds no victim: it and the misses after it stay on their host copies (their table entries point
+ * there, so the expert calls read them over the bus and compute the same values), the misses planned before it keep
+ * their slots, and status[0] receives the count (the reference's plan would spin).  Every slot the window holds ends
+ * at ref 1 either way. */
 int sfnx_cache_plan(const sfnx_job* jobs, const int* njobs, int layer, const sfnx_expert_cache* ec, int* list, void* st);
 /* src/kernels.cu:1642-1658 k_cache_copy / cache_copy: the listed experts' matrices from their host copies into their
  * slots of pool p */

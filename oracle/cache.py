@@ -5,7 +5,9 @@ cache_plan follows src/moe.cuh:22-71 (cache_plan, one warp): the window's jobs w
 each other job, in job order, takes the first slot of the layer's pool that the CLOCK hand reaches with ref 0, looking
 at 32 slots a step (the warp's lanes, slot (hand + lane) mod n), the ref-1 slots before the found one in that step
 dropping to 0; a step without a ref-0 slot drops all its ref-1 slots and moves the hand 32 on.  The victim's old expert
-goes back to its host copy.  Afterwards every job's slot is ref 1 and the hand is stored.
+goes back to its host copy.  Afterwards every job's slot is ref 1 and the hand is stored.  A miss that finds no victim
+(every slot of the pool held by the window: two full turns of the hand see only ref 2) stays on its host copy, and so
+do the misses after it; the state keeps the count in `left` (the library's status[0]; the reference's plan spins).
 
 Pinned in tests/test_oracle_cache.py by: a case worked by hand (a pool of 5 slots, fewer than 32, where the 32-lane
 steps alias slots), invariants over random windows (every job's expert in a slot, owner and slot_of inverse, the list
@@ -27,18 +29,19 @@ class PoolState:
         self.owner = [-1] * (s0 + n)
         self.ref = [0] * (s0 + n)
         self.hand = s0
+        self.left = 0
 
     def copy(self) -> "PoolState":
         c = PoolState.__new__(PoolState)
         c.E, c.n, c.s0 = self.E, self.n, self.s0
         c.slot_of, c.owner, c.ref, c.hand = list(self.slot_of), list(self.owner), list(self.ref), self.hand
+        c.left = self.left
         return c
 
 
-def cache_plan(st: PoolState, job_experts: list[int], layer: int) -> list[int] | None:
+def cache_plan(st: PoolState, job_experts: list[int], layer: int) -> list[int]:
     """src/moe.cuh:22-71 for one layer whose pool is st; job_experts: each job's expert, in job order.  Returns the
-    experts (layer * E + e) that took a slot, in job order, or None when the pool has no victim left (the library
-    reports list[0] = -1 there; the reference would spin)"""
+    experts (layer * E + e) that took a slot, in job order; st.left receives the misses left on their host copies"""
     base, s0, n = layer * st.E, st.s0, st.n
     for e in job_experts:
         s = st.slot_of[base + e]
@@ -48,16 +51,21 @@ def cache_plan(st: PoolState, job_experts: list[int], layer: int) -> list[int] |
     if hand < 0 or hand >= n:
         hand = 0
     taken = []
-    slots = {}
+    left = 0
+    failed = False
     for j0 in range(0, len(job_experts), SWEEP):
         group = job_experts[j0:j0 + SWEEP]
         misses = [j0 + i for i, e in enumerate(group) if st.slot_of[base + e] < 0]
-        for j in misses:
+        if failed:
+            left += len(misses)
+            continue
+        for mi, j in enumerate(misses):
             g = base + job_experts[j]
             victim, steps = -1, 0
             while victim < 0:
                 if steps > 2 * (n // SWEEP + 2):
-                    return None
+                    failed = True
+                    break
                 steps += 1
                 idx = [(hand + lane) % n for lane in range(SWEEP)]
                 r = [st.ref[s0 + i] for i in idx]   # every lane reads before any writes
@@ -68,6 +76,9 @@ def cache_plan(st: PoolState, job_experts: list[int], layer: int) -> list[int] |
                 if f < SWEEP:
                     victim = (hand + f) % n
                 hand = (hand + (f + 1 if f < SWEEP else SWEEP)) % n
+            if failed:
+                left += len(misses) - mi
+                break
             vs = s0 + victim
             o = st.owner[vs]
             if o >= 0:
@@ -75,9 +86,10 @@ def cache_plan(st: PoolState, job_experts: list[int], layer: int) -> list[int] |
             st.owner[vs] = g
             st.slot_of[g] = vs
             st.ref[vs] = 2
-            slots[j] = vs
             taken.append(g)
     for e in job_experts:
-        st.ref[st.slot_of[base + e]] = 1
+        if st.slot_of[base + e] >= 0:
+            st.ref[st.slot_of[base + e]] = 1
     st.hand = s0 + hand
+    st.left = left
     return taken

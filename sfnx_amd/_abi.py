@@ -54,6 +54,7 @@ SIGNATURES = {
     "sfnx_moe_decode2": (i32, [vp, i32, u32, u32, i32, i32, i32, i32, i32, vp, i32, i32, f32, vp, sz, i32, vp]),
     "sfnx_moe_decode_q8s": (i32, [vp, vp, i32, u32, u32, i32, i32, i32, i32, vp, i32, i32, f32, vp, sz, i32, vp]),
     "sfnx_q8s_gemv": (i32, [vp, i32, i32, vp, vp, i32, i32, vp]),
+    "sfnx_q8s_split": (i32, [vp, i32, i32, vp, vp]),
     "sfnx_hc_workspace": (sz, [i32, i32, i32, vp]),
     "sfnx_pf_dense": (i32, [vp, i32, i32, vp, i32, vp, i32, vp, sz, vp]),
     "sfnx_hc_read": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, f32, vp, vp, vp, i32, i32, i32, i32, vp, sz, vp]),
@@ -68,8 +69,8 @@ SIGNATURES = {
     "sfnx_gguf_int": (i32, [vp, C.c_char_p, vp]),
     "sfnx_gguf_float": (i32, [vp, C.c_char_p, vp]),
     "sfnx_gguf_str": (i32, [vp, C.c_char_p, vp]),
-    "sfnx_gguf_moe_layer": (i32, [vp, i32, i32, i32, vp, sz, vp, sz, vp, vp, vp]),
-    "sfnx_gguf_moe_layer_q8s": (i32, [vp, i32, i32, i32, vp, sz, vp, sz, vp, vp, vp, vp, vp]),
+    "sfnx_gguf_moe_layer": (i32, [vp, i32, i32, i32, vp, sz, sz, vp, sz, sz, vp, i32, vp, vp]),
+    "sfnx_gguf_moe_layer_q8s": (i32, [vp, i32, i32, i32, vp, sz, sz, vp, sz, sz, vp, i32, vp, vp, vp, vp]),
     "sfnx_host_alloc": (i32, [sz, vp, vp]),
     "sfnx_host_free": (i32, [vp]),
     "sfnx_cache_plan": (i32, [vp, vp, i32, vp, vp, vp]),
@@ -88,9 +89,14 @@ class LayerW(C.Structure):
     _fields_ = [("W", vp), ("gu", vp), ("gu_stride", sz), ("dn", vp), ("dn_stride", sz)]
 
 
+class Q8S(C.Structure):
+    """sfnx_q8s (src/model.hpp:71-74 Q8S): int8 values q [rows][cols], f16 scale bits d [rows][cols / 32]"""
+    _fields_ = [("q", vp), ("d", vp)]
+
+
 class SharedQ8s(C.Structure):
     """sfnx_moe_shared_q8s"""
-    _fields_ = [("gu", vp), ("dn", vp)]
+    _fields_ = [("gu", Q8S), ("dn", Q8S)]
 
 
 EC_POOLS, EC_LAYERS = 4, 128
@@ -102,7 +108,7 @@ class ExpertCacheC(C.Structure):
                 ("pool_of", i32 * EC_LAYERS), ("s0", i32 * EC_POOLS), ("n", i32 * EC_POOLS),
                 ("slot_bytes", sz * EC_POOLS), ("dn_off", sz * EC_POOLS), ("pool", vp * EC_POOLS),
                 ("ep_gu", vp), ("ep_dn", vp), ("host_gu", vp), ("host_dn", vp),
-                ("slot_of", vp), ("owner", vp), ("ref", vp), ("hand", vp)]
+                ("slot_of", vp), ("owner", vp), ("ref", vp), ("hand", vp), ("status", vp)]
 
 
 def declared_symbols() -> list[str]:

@@ -19,8 +19,14 @@ __global__ void __launch_bounds__(WAVE) k_cache_plan(const sfnx_job* __restrict_
     __shared__ int jslot[EC_MAX_JOBS];   // each job's slot, pool-relative
     const int lane = threadIdx.x, nj = *njobs;
     const int base = layer * ec.n_experts, p = ec.pool_of[layer], s0 = ec.s0[p], n = ec.n[p];
-    if (nj < 0 || nj > EC_MAX_JOBS) {
-        if (lane == 0) list[0] = -1;
+    if (nj < 0 || nj > EC_MAX_JOBS) {   // a count past what a plan takes: nothing planned, every miss from its host copy
+        if (lane == 0) {
+            list[0] = 0;
+            if (ec.status) {
+                ec.status[0] = max(nj, 0);
+                ec.status[1] += max(nj, 0);
+            }
+        }
         return;
     }
     for (int i = lane; i < n; i += WAVE) ref[i] = ec.ref[s0 + i];
@@ -34,12 +40,20 @@ __global__ void __launch_bounds__(WAVE) k_cache_plan(const sfnx_job* __restrict_
     __syncthreads();
     int hand = ec.hand[p] - s0, k = 0;
     if (hand < 0 || hand >= n) hand = 0;
+    // A miss finds no victim only when every slot of the pool is held by this window (ref 2).  It then stays on its
+    // host copy, where its table entries already point (the expert kernels read it there, over the bus), and so do
+    // the misses after it; the experts planned before it keep their slots and are copied in.
     bool fail = false;
+    int left = 0;
     const bool sweeper = lane < SWEEP;
     // the misses, SWEEP jobs at a time (found side by side), taken in job order
-    for (int j0 = 0; j0 < nj && !fail; j0 += SWEEP) {
+    for (int j0 = 0; j0 < nj; j0 += SWEEP) {
         unsigned long long miss = __ballot(sweeper && j0 + lane < nj && jslot[j0 + lane] < 0);
-        while (miss && !fail) {
+        if (fail) {
+            left += __popcll(miss);
+            continue;
+        }
+        while (miss) {
             const int jm = j0 + __ffsll(miss) - 1;
             miss &= miss - 1;
             const int g = base + jobs[jm].w;
@@ -59,7 +73,10 @@ __global__ void __launch_bounds__(WAVE) k_cache_plan(const sfnx_job* __restrict_
                 if (fr) victim = (hand + f) % n;
                 hand = (hand + (fr ? f + 1 : SWEEP)) % n;
             }
-            if (fail) break;
+            if (fail) {
+                left += 1 + __popcll(miss);   // this miss and the rest of its group
+                break;
+            }
             if (lane == 0) {
                 const int vs = s0 + victim, o = ec.owner[vs];
                 if (o >= 0) {   // the victim's expert back to its host copy
@@ -81,13 +98,19 @@ __global__ void __launch_bounds__(WAVE) k_cache_plan(const sfnx_job* __restrict_
         }
     }
     __syncthreads();
-    if (!fail)   // the window's slots are used: ref 1 for the next plans
-        for (int j = lane; j < nj; j += WAVE) ref[jslot[j]] = 1;
+    // the window's slots are used: ref 1 for the next plans, whether or not every miss found a slot (a ref 2 left
+    // behind would make its slot unevictable)
+    for (int j = lane; j < nj; j += WAVE)
+        if (jslot[j] >= 0) ref[jslot[j]] = 1;
     __syncthreads();
     for (int i = lane; i < n; i += WAVE) ec.ref[s0 + i] = ref[i];
     if (lane == 0) {
         ec.hand[p] = s0 + hand;
-        list[0] = fail ? -1 : k;
+        list[0] = k;
+        if (ec.status) {
+            ec.status[0] = left;
+            ec.status[1] += left;
+        }
     }
 }
 

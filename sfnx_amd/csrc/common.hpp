@@ -252,6 +252,23 @@ __host__ __device__ __forceinline__ Q80Planes q80_planes(const void* mat, int R,
     return Q80Planes{p, p + (size_t) R * C};
 }
 
+// A dense Q8_0 matrix in the reference's split layout (src/model.hpp:71-74 Q8S, filled by src/model.cpp:384-440
+// q8split): int8 values [R][C] row-major and the f16 scale bits of each 32-value block [R][C / 32].  The shared expert's
+// dense matrices cross the boundary in it.
+struct Q8sPlanes {
+    const int8_t* q;
+    const uint16_t* d;
+    // the 16 values of row r from column c (c % 16 == 0)
+    __host__ __device__ __forceinline__ const uint8_t* q16(int r, int C, int c) const {
+        return reinterpret_cast<const uint8_t*>(q) + (size_t) r * C + c;
+    }
+    __host__ __device__ __forceinline__ const uint16_t* dof(int r, int C, int b) const { return d + (size_t) r * (C / 32) + b; }
+};
+
+// a dense Q8_0 matrix (split layout) into the planar Q8_0 layout of one matrix at dst, on stream s (dense.hip)
+size_t q8s_planar_bytes(int rows, int cols);
+void q8s_to_planar(const sfnx_q8s& W, int rows, int cols, void* dst, hipStream_t s);
+
 inline bool expert_type_ok(uint32_t type) {
     return type == SFNX_Q4_K || type == SFNX_Q5_K || type == SFNX_Q8_0 || type == SFNX_Q4_0 || type == SFNX_Q5_1;
 }

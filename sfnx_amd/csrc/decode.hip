@@ -171,7 +171,7 @@ template <int TYPE, int G, int TT>
 __global__ void __launch_bounds__(2 * d2_threads<TYPE>()) k_dec_experts(
     const uint8_t* __restrict__ A, size_t sa, int H, int E, int ff, const uint8_t* __restrict__ xq,
     const sfnx_job* __restrict__ jg, const int* __restrict__ njobs_g, float* __restrict__ gu, int8_t* __restrict__ hq_q,
-    float* __restrict__ hq_d, int* __restrict__ hq_s, const uint8_t* __restrict__ sh_gu) {
+    float* __restrict__ hq_d, int* __restrict__ hq_s, Q8sPlanes sh_gu) {
     constexpr int LPR = lpr_of<TYPE>(), NTH = 2 * d2_threads<TYPE>(), NW = NTH / WAVE, RPW = WAVE / LPR;
     const int NFB = ff / 32, myjob = blockIdx.x / NFB, fb = blockIdx.x % NFB;
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
@@ -191,14 +191,14 @@ __global__ void __launch_bounds__(2 * d2_threads<TYPE>()) k_dec_experts(
     };
     // the weight rows are requested first, then the job's rows of activations staged (slot s holds row jb.y[s]): the
     // two fetches overlap instead of following each other
-    const bool dense_sh = sh_gu != nullptr && jb.w == E;   // the shared expert's own dense Q8_0 matrix
+    const bool dense_sh = sh_gu.q != nullptr && jb.w == E;   // the shared expert's own dense Q8_0 matrix
     typename RowOf<TYPE, G>::R w;
     if (!dense_sh) RowOf<TYPE, G>::load(w, expert_at(A, sa, jb.w), 2 * ff, row, H, ln);
     const Acts a = acts_in(lds, TT, H);
     stage_q8_1(a, xq, jb.y, jb.n);
     __syncthreads();   // the staged activations
     if (dense_sh) {   // the reference's q8s sums
-        const Q80Planes Ps = q80_planes(sh_gu, 2 * ff, H);
+        const Q8sPlanes Ps = sh_gu;
         for (int s = 0; s < jb.n; ++s) put(s, group_sum<LPR>(q8s_dot<LPR>(Ps, row, H, ln, a, s)));
     } else {
         for (int s = 0; s < jb.n; ++s) put(s, group_sum<LPR>(w.dot(a, s, ln)));
@@ -243,7 +243,7 @@ __global__ void __launch_bounds__(2 * d2_threads<TYPE>()) k_dec_experts1(
     const float* __restrict__ logits,
     const uint8_t* __restrict__ xq, int* __restrict__ topi_g, float* __restrict__ topw_g, sfnx_job* __restrict__ jg,
     sfnx_job* __restrict__ jd, int* __restrict__ njobs_g, float* __restrict__ gu, int8_t* __restrict__ hq_q,
-    float* __restrict__ hq_d, int* __restrict__ hq_s, int* __restrict__ route_x, const uint8_t* __restrict__ sh_gu) {
+    float* __restrict__ hq_d, int* __restrict__ hq_s, int* __restrict__ route_x, Q8sPlanes sh_gu) {
     constexpr int LPR = lpr_of<TYPE>(), NW = 2 * d2_threads<TYPE>() / WAVE, RPW = WAVE / LPR;
     const int NFB = ff / 32, fb = blockIdx.x % NFB;
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
@@ -257,7 +257,7 @@ __global__ void __launch_bounds__(2 * d2_threads<TYPE>()) k_dec_experts1(
     if constexpr (SHR) {
         const int up_half = threadIdx.x / WAVE >= NW / 2;
         const int srow = (up_half ? ff : 0) + fb * 32 + (up_half ? wave - NW / 2 : wave) * RPW + lane / LPR;
-        if (q8s) ws.issue(q80_planes(sh_gu, 2 * ff, H), srow, H, lane % LPR);
+        if (q8s) ws.issue(sh_gu, srow, H, lane % LPR);
     }
     __shared__ float gbuf[32], ubuf[32];
     __shared__ uint32_t junk[WAVE];
@@ -323,7 +323,7 @@ __global__ void __launch_bounds__(2 * d2_threads<TYPE>()) k_dec_experts1(
     lds_barrier();
     float v;
     if constexpr (SHR) v = group_sum<LPR>(q8s ? ws.dot(a, 0, ln) : wr.dot1(a, ln));
-    else if constexpr (SHQ) v = group_sum<LPR>(q8s ? q8s_dot<LPR>(q80_planes(sh_gu, 2 * ff, H), row, H, ln, a, 0) : wr.dot1(a, ln));
+    else if constexpr (SHQ) v = group_sum<LPR>(q8s ? q8s_dot<LPR>(sh_gu, row, H, ln, a, 0) : wr.dot1(a, ln));
     else v = group_sum<LPR>(wr.dot1(a, ln));   // each group as it arrives
     if (ln == 0) {
         gu[(size_t) out * 2 * ff + row] = v;
@@ -355,7 +355,7 @@ __global__ void __launch_bounds__(NT) k_dec_down(const uint8_t* __restrict__ A, 
                                                         const sfnx_job* __restrict__ jd, const int* __restrict__ njobs,
                                                         const int8_t* __restrict__ hq_q, const float* __restrict__ hq_d,
                                                         const int* __restrict__ hq_s, float* __restrict__ y,
-                                                        float* __restrict__ x, int hq_in_lds, const uint8_t* __restrict__ sh_dn) {
+                                                        float* __restrict__ x, int hq_in_lds, Q8sPlanes sh_dn) {
     constexpr int LPR = lpr_of<TYPE>(), GROUPS = NT / LPR;
     const int row0 = blockIdx.x * D3_ROWS, nj = njobs[0], P = T * K, NP = P + T, nbh = ff / 32;
     __shared__ int jw[MAX_P + 1], jn[MAX_P + 1], jout[MAX_P + 1][SFNX_MAXT];
@@ -399,12 +399,12 @@ __global__ void __launch_bounds__(NT) k_dec_down(const uint8_t* __restrict__ A, 
     __syncthreads();
     const int g = threadIdx.x / LPR, ln = threadIdx.x % LPR;
     // with its own dense Q8_0 matrix the shared expert's job (the last) runs apart, in the reference's q8s sums
-    const int nq = sh_dn != nullptr && shared ? nj - 1 : nj, ntask = nq * D3_ROWS;
+    const int nq = sh_dn.q != nullptr && shared ? nj - 1 : nj, ntask = nq * D3_ROWS;
     // the dots, inlined once for h in LDS and once for h in global memory: a pointer that may be either is generic,
     // and every load through it a flat load
     auto dots = [&](const Acts& a) __attribute__((always_inline)) {
     if (nq < nj) {
-        const Q80Planes Ps = q80_planes(sh_dn, H, ff);
+        const Q8sPlanes Ps = sh_dn;
         for (int task = g; task < T * D3_ROWS; task += GROUPS) {
             const int t = task / D3_ROWS, r = task % D3_ROWS;
             const float v = group_sum<LPR>(q8s_dot<LPR>(Ps, row0 + r, ff, ln, a, P + t));
@@ -468,7 +468,7 @@ __global__ void __launch_bounds__(NT3) k_dec_down1(const uint8_t* __restrict__ A
                                                          const int8_t* __restrict__ hq_q, const float* __restrict__ hq_d,
                                                          const int* __restrict__ hq_s, float* __restrict__ y,
                                                          float* __restrict__ x, const int* __restrict__ route_x,
-                                                         const uint8_t* __restrict__ sh_dn) {
+                                                         Q8sPlanes sh_dn) {
     constexpr int LPR = lpr_of<TYPE>(), GROUPS = NT3 / LPR;
     const int row0 = blockIdx.x * D3_ROWS, nbh = ff / 32, lane = threadIdx.x % WAVE, tid = threadIdx.x;
     const int g = tid / LPR, ln = tid % LPR;
@@ -514,7 +514,7 @@ __global__ void __launch_bounds__(NT3) k_dec_down1(const uint8_t* __restrict__ A
     for (int b = 0; b < NB; ++b) {
         const int task = g + b * GROUPS, r = task % D3_ROWS;
         if (SHQ && task < ntask && pp[b] == K) {
-            wsh.issue(q80_planes(sh_dn, H, ff), row0 + r, ff, ln);
+            wsh.issue(sh_dn, row0 + r, ff, ln);
             bsh = b;
         } else if (task < ntask) {
             RowOf<TYPE, G2>::issue(w[b], (const uint8_t*) mats[b], H, row0 + r, ff, ln);
@@ -525,13 +525,13 @@ __global__ void __launch_bounds__(NT3) k_dec_down1(const uint8_t* __restrict__ A
     // every request above), then the barrier for the other wavefronts' copies of h
 #pragma unroll
     for (int b = 0; b < NB; ++b) asm volatile("" ::"v"(mats[b]) : "memory");
-    if constexpr (SHQ) asm volatile("" ::"v"((global_u8_ptr) sh_dn) : "memory");
+    if constexpr (SHQ) asm volatile("" ::"v"((global_u8_ptr) sh_dn.q), "v"((const void*) sh_dn.d) : "memory");
     vm_wait<0>();
     lds_barrier();
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
         const int task = g + b * GROUPS;
-        if (task < ntask && !(sh_dn != nullptr && pp[b] == K)) {
+        if (task < ntask && !(sh_dn.q != nullptr && pp[b] == K)) {
             w[b].prepare(ln);
             const float v = group_sum<LPR>(w[b].dot(a, pp[b], ln));
             if (ln == 0) part[pp[b]][task % D3_ROWS] = v;
@@ -547,8 +547,8 @@ __global__ void __launch_bounds__(NT3) k_dec_down1(const uint8_t* __restrict__ A
     for (int t0 = g + NB * GROUPS; t0 < ntask; t0 += GROUPS) {
         const int j = t0 / D3_ROWS, r = t0 % D3_ROWS, e = __shfl(tp, j < nr ? j : 0), q = j < nr ? j : K;
         float v;
-        if (sh_dn != nullptr && j >= nr) {
-            v = group_sum<LPR>(q8s_dot<LPR>(q80_planes(sh_dn, H, ff), row0 + r, ff, ln, a, K));
+        if (sh_dn.q != nullptr && j >= nr) {
+            v = group_sum<LPR>(q8s_dot<LPR>(sh_dn, row0 + r, ff, ln, a, K));
         } else {
             typename RowOf<TYPE, G2>::R w1;
             RowOf<TYPE, G2>::load(w1, expert_at(A, sa, j < nr ? e : E), H, row0 + r, ff, ln);
@@ -581,8 +581,8 @@ struct DecArgs {
     float eps;
     int phases;
     const float* Wn;   // the next layer's router (warmed into L2 for that layer's K1), or null
-    const uint8_t* sh_gu = nullptr;   // this layer's shared expert as its own dense Q8_0 matrices, or null
-    const uint8_t* sh_dn = nullptr;
+    Q8sPlanes sh_gu{};   // this layer's shared expert as its own dense Q8_0 matrices, or null planes
+    Q8sPlanes sh_dn{};
 };
 
 // Optional kernel clock: when on, each decode kernel is launched with a start/stop event pair that the runtime
@@ -635,7 +635,7 @@ void launch_k2_one(const DecArgs& d, const sfnx_moe_layer_w& w, const DecLayout&
 }
 template <int TYPE, int G>
 void launch_k2_tt1(const DecArgs& d, const sfnx_moe_layer_w& w, const DecLayout& L, char* ws, hipStream_t s) {
-    if (d.sh_gu) {
+    if (d.sh_gu.q) {
         if (d.E <= 256) launch_k2_one<TYPE, G, 4, true>(d, w, L, ws, s);
         else if (d.E <= 512) launch_k2_one<TYPE, G, 8, true>(d, w, L, ws, s);
         else launch_k2_one<TYPE, G, 16, true>(d, w, L, ws, s);
@@ -649,7 +649,7 @@ template <int TYPE, int G2>
 void launch_k3_one(const DecArgs& d, const sfnx_moe_layer_w& w, float* x, const DecLayout& L, char* ws, hipStream_t s) {
     // 512 threads: 64 lane groups (K-quants) or 32, so 11 jobs x 8 rows are one batch of 2 or 3 tasks a group
     constexpr int NT3 = 512, NB = is_kquant(TYPE) ? 2 : 3;
-    auto kern = d.sh_dn ? k_dec_down1<TYPE, G2, NB, true, NT3> : k_dec_down1<TYPE, G2, NB, false, NT3>;
+    auto kern = d.sh_dn.q ? k_dec_down1<TYPE, G2, NB, true, NT3> : k_dec_down1<TYPE, G2, NB, false, NT3>;
     launch(2, kern, dim3(d.H / D3_ROWS), dim3(NT3), acts_bytes(d.K + 1, d.ff), s,
         (const uint8_t*) w.dn, w.dn_stride, d.H, d.E, d.K, d.ff, d.shared, (const float*) (ws + L.logits),
         (const int*) (ws + L.topi), (const float*) (ws + L.topw), (const int8_t*) (ws + L.hq_q),
@@ -788,7 +788,7 @@ void moe_decode(const sfnx_moe_layer_w* layers, const sfnx_moe_shared_q8s* sh, i
             require(layers[l].W && layers[l].gu && layers[l].dn, "a layer's weights are missing");
             require(stride_ok(layers[l].gu_stride, row_bytes(type, H) * 2 * (size_t) ff), "gate|up stride smaller than a matrix");
             require(stride_ok(layers[l].dn_stride, row_bytes(dn_type, ff) * (size_t) H), "down stride smaller than a matrix");
-            if (sh) require(sh[l].gu != nullptr && sh[l].dn != nullptr, "a layer's shared expert matrices are missing");
+            if (sh) require(sh[l].gu.q && sh[l].gu.d && sh[l].dn.q && sh[l].dn.d, "a layer's shared expert matrices are missing");
         }
         const DecArgs d{gu_type, dn_type, H, E, K, ff, shared ? 1 : 0, T, norm ? 1 : 0, eps, phases ? phases : 7, nullptr};
         hipStream_t s = stream_of(st);
@@ -797,8 +797,8 @@ void moe_decode(const sfnx_moe_layer_w* layers, const sfnx_moe_shared_q8s* sh, i
             DecArgs dl = d;
             dl.Wn = l + 1 < n_layers ? layers[l + 1].W : nullptr;
             if (sh) {
-                dl.sh_gu = (const uint8_t*) sh[l].gu;
-                dl.sh_dn = (const uint8_t*) sh[l].dn;
+                dl.sh_gu = Q8sPlanes{sh[l].gu.q, sh[l].gu.d};
+                dl.sh_dn = Q8sPlanes{sh[l].dn.q, sh[l].dn.d};
             }
             if (T == 1) launch_layer_tt<1>(dl, layers[l], x, L, w, s);
             else if (T <= 4) launch_layer_tt<4>(dl, layers[l], x, L, w, s);

@@ -15,12 +15,10 @@ constexpr int QS_THREADS = 256, QS_LPR = 32, QS_ROWS = QS_THREADS / QS_LPR, QS_T
 // f32 rows y = [T][gate (cols) | up (cols)] quantized to q8_1 as they are staged (the same values as
 // swiglu_stacked_q8_1's blocks, so the same sums as that call followed by q8s_gemv)
 template <bool SWIGLU>
-__global__ void __launch_bounds__(QS_THREADS) k_q8s_gemv(const uint8_t* __restrict__ W, int rows, int cols,
-                                                        const uint8_t* __restrict__ y, float* __restrict__ out,
-                                                        int out_stride, int T) {
+__global__ void __launch_bounds__(QS_THREADS) k_q8s_gemv(Q8sPlanes P, int rows, int cols, const uint8_t* __restrict__ y,
+                                                        float* __restrict__ out, int out_stride, int T) {
     extern __shared__ __align__(16) unsigned char lds[];
     const Acts a = acts_in(lds, QS_TT, cols);
-    const Q80Planes P = q80_planes(W, rows, cols);
     const int row = blockIdx.x * QS_ROWS + threadIdx.x / QS_LPR, ln = threadIdx.x % QS_LPR;
     for (int t0 = 0; t0 < T; t0 += QS_TT) {
         const int nn = min(QS_TT, T - t0);
@@ -48,14 +46,53 @@ __global__ void k_swiglu_stacked(const float* __restrict__ gu, uint8_t* __restri
     if (l == 0) *reinterpret_cast<uint32_t*>(blk) = (uint32_t) f2h(d) | ((uint32_t) f2h(sum) << 16);
 }
 
+// src/model.cpp:384-440 q8split: GGUF Q8_0 blocks into the split planes, a thread a block
+__global__ void k_q8s_split(const uint8_t* __restrict__ blocks, int rows, int cols, int8_t* __restrict__ q,
+                            uint16_t* __restrict__ d) {
+    const int nb = cols / 32;
+    const size_t i = (size_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t) rows * nb) return;
+    const uint8_t* b = blocks + i * Q80_BYTES;
+    d[i] = (uint16_t) (b[0] | (b[1] << 8));
+    int4* dst = reinterpret_cast<int4*>(q + i * 32);
+    int w[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) w[k] = b[2 + 4 * k] | (b[3 + 4 * k] << 8) | (b[4 + 4 * k] << 16) | (b[5 + 4 * k] << 24);
+    dst[0] = make_int4(w[0], w[1], w[2], w[3]);
+    dst[1] = make_int4(w[4], w[5], w[6], w[7]);
+}
+
+// the split planes into the planar Q8_0 layout of one matrix (the matrix-core kernels' operand), a thread a block:
+// its two 16-value halves to their pieces, its scale to the scale plane
+__global__ void k_q8s_to_planar(Q8sPlanes W, int rows, int cols, uint8_t* __restrict__ dst) {
+    const int nb = cols / 32;
+    const size_t i = (size_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t) rows * nb) return;
+    const int r = (int) (i / nb), b = (int) (i % nb);
+    const Q80Planes P = q80_planes(dst, rows, cols);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+        *reinterpret_cast<int4*>(const_cast<uint8_t*>(P.q16(r, cols, 32 * (b / 16) + 16 * h + b % 16))) =
+            *reinterpret_cast<const int4*>(W.q16(r, cols, 32 * b + 16 * h));
+    *const_cast<uint16_t*>(P.dof(r, cols, b)) = *W.dof(r, cols, b);
+}
+
 }  // namespace
+
+// bytes of one matrix's planar Q8_0 staging (rows x cols values)
+size_t q8s_planar_bytes(int rows, int cols) { return (size_t) rows * row_bytes(SFNX_Q8_0, cols); }
+void q8s_to_planar(const sfnx_q8s& W, int rows, int cols, void* dst, hipStream_t s) {
+    const size_t n = (size_t) rows * (cols / 32);
+    k_q8s_to_planar<<<(unsigned) ((n + 255) / 256), 256, 0, s>>>(Q8sPlanes{W.q, W.d}, rows, cols, (uint8_t*) dst);
+}
 }  // namespace sfnx
 
 using namespace sfnx;
 
-extern "C" int sfnx_q8s_gemv(const void* W, int rows, int cols, const void* y, float* out, int out_stride, int T, void* st) {
+extern "C" int sfnx_q8s_gemv(const sfnx_q8s* W, int rows, int cols, const void* y, float* out, int out_stride, int T,
+                             void* st) {
     return guarded("sfnx_q8s_gemv", [&] {
-        require(W != nullptr && y != nullptr && out != nullptr, "null pointer");
+        require(W != nullptr && W->q != nullptr && W->d != nullptr && y != nullptr && out != nullptr, "null pointer");
         require(rows > 0 && rows % 32 == 0, "rows must be a positive multiple of 32");
         require(cols > 0 && cols % 512 == 0, "cols must be a positive multiple of 512");
         require(T >= 1 && T <= 65535, "T out of range");
@@ -63,14 +100,14 @@ extern "C" int sfnx_q8s_gemv(const void* W, int rows, int cols, const void* y, f
         const size_t lds = acts_bytes(QS_TT, cols);
         require(lds <= 64 * 1024, "cols too wide for the activation staging");
         k_q8s_gemv<false><<<(rows + QS_ROWS - 1) / QS_ROWS, QS_THREADS, lds, stream_of(st)>>>(
-            (const uint8_t*) W, rows, cols, (const uint8_t*) y, out, out_stride, T);
+            Q8sPlanes{W->q, W->d}, rows, cols, (const uint8_t*) y, out, out_stride, T);
     });
 }
 
-extern "C" int sfnx_q8s_swiglu_gemv(const void* W, int rows, int ffs, const float* gu, float* out, int out_stride, int T,
-                                    void* st) {
+extern "C" int sfnx_q8s_swiglu_gemv(const sfnx_q8s* W, int rows, int ffs, const float* gu, float* out, int out_stride,
+                                    int T, void* st) {
     return guarded("sfnx_q8s_swiglu_gemv", [&] {
-        require(W != nullptr && gu != nullptr && out != nullptr, "null pointer");
+        require(W != nullptr && W->q != nullptr && W->d != nullptr && gu != nullptr && out != nullptr, "null pointer");
         require(rows > 0 && rows % 32 == 0, "rows must be a positive multiple of 32");
         require(ffs > 0 && ffs % 512 == 0, "ffs must be a positive multiple of 512");
         require(T >= 1 && T <= 65535, "T out of range");
@@ -78,7 +115,7 @@ extern "C" int sfnx_q8s_swiglu_gemv(const void* W, int rows, int ffs, const floa
         const size_t lds = acts_bytes(QS_TT, ffs);
         require(lds <= 64 * 1024, "ffs too wide for the activation staging");
         k_q8s_gemv<true><<<(rows + QS_ROWS - 1) / QS_ROWS, QS_THREADS, lds, stream_of(st)>>>(
-            (const uint8_t*) W, rows, ffs, (const uint8_t*) gu, out, out_stride, T);
+            Q8sPlanes{W->q, W->d}, rows, ffs, (const uint8_t*) gu, out, out_stride, T);
     });
 }
 
@@ -89,5 +126,14 @@ extern "C" int sfnx_swiglu_stacked_q8_1(const float* gu, void* hq, int ffs, int 
         require(T >= 1 && T <= 65535, "T out of range");
         const dim3 grid((ffs / 32 + 7) / 8, T);
         k_swiglu_stacked<<<grid, 256, 0, stream_of(st)>>>(gu, (uint8_t*) hq, ffs, T);
+    });
+}
+
+extern "C" int sfnx_q8s_split(const void* blocks, int rows, int cols, const sfnx_q8s* W, void* st) {
+    return guarded("sfnx_q8s_split", [&] {
+        require(blocks != nullptr && W != nullptr && W->q != nullptr && W->d != nullptr, "null pointer");
+        require(rows > 0 && cols > 0 && cols % 32 == 0, "rows must be positive and cols a positive multiple of 32");
+        const size_t n = (size_t) rows * (cols / 32);
+        k_q8s_split<<<(unsigned) ((n + 255) / 256), 256, 0, stream_of(st)>>>((const uint8_t*) blocks, rows, cols, W->q, W->d);
     });
 }

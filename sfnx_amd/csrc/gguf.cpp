@@ -350,12 +350,14 @@ extern "C" int sfnx_gguf_str(const sfnx_gguf* g, const char* key, const char** v
 
 namespace {
 // sh_gu null: the shared expert (when present, of the routed types) is expert E of gu / dn.  Else the shared expert
-// must be present and Q8_0 (src/model.cpp:807-809 throws otherwise) and goes to sh_gu [2 ffs][H] / sh_dn [H][ffs].
-void moe_layer(const sfnx_gguf* g, int layer, int ff0, int ff1, void* gu, size_t gu_stride, void* dn, size_t dn_stride,
-               float* W, void* sh_gu, void* sh_dn, int* info, void* st) {
+// must be present and Q8_0 (src/model.cpp:807-809 throws otherwise) and goes to sh_gu [2 ffs][H] / sh_dn [H][ffs] in
+// the split layout (src/model.cpp:384-440 q8split).
+void moe_layer(const sfnx_gguf* g, int layer, int ff0, int ff1, void* gu, size_t gu_stride, size_t gu_cap, void* dn,
+               size_t dn_stride, size_t dn_cap, float* W, int w_rows, const sfnx_q8s* sh_gu, const sfnx_q8s* sh_dn,
+               int* info, void* st) {
     require(g != nullptr && gu != nullptr && dn != nullptr && W != nullptr, "null argument");
     const bool q8s = sh_gu != nullptr;
-    require(!q8s || sh_dn != nullptr, "null argument");
+    require(!q8s || (sh_dn != nullptr && sh_gu->q && sh_gu->d && sh_dn->q && sh_dn->d), "null argument");
     const std::string L = "blk." + std::to_string(layer) + ".";
     const sfnx_gguf_tensor& tg = need(g, L + "ffn_gate_exps.weight");
     const sfnx_gguf_tensor& tu = need(g, L + "ffn_up_exps.weight");
@@ -393,7 +395,13 @@ void moe_layer(const sfnx_gguf* g, int layer, int ff0, int ff1, void* gu, size_t
                     sd->ne[1] == H, "the shared expert's shape differs from a routed expert's");
         require(sgi->type == 0 && sgi->ne[0] == H && sgi->ne[1] == 1, "ffn_gate_inp_shexp must be f32 [1][H]");
     }
-    const int64_t NE = E + (shared ? 1 : 0);
+    const int64_t NE = E + (shared && !q8s ? 1 : 0);   // experts the routed stores receive
+    // the caller's buffers, checked against what the file holds before anything is written
+    require((uint64_t) (NE - 1) * gu_stride + 2 * (size_t) ffs * rb_in <= gu_cap,
+            "gu buffer too small for the layer's experts (E from the file, plus the shared expert when it joins)");
+    require((uint64_t) (NE - 1) * dn_stride + (size_t) H * rb_ff <= dn_cap,
+            "dn buffer too small for the layer's experts (E from the file, plus the shared expert when it joins)");
+    require((int64_t) w_rows >= E + 1, "W holds fewer than E + 1 router rows");
     hipStream_t s = stream_of(st);
     // one expert's matrices at a time in GGUF layout through a pinned host buffer and a device buffer, then packed
     const size_t gu_bytes = 2 * (size_t) ffs * rb_in, dn_bytes = (size_t) H * rb_ff;
@@ -413,7 +421,7 @@ void moe_layer(const sfnx_gguf* g, int layer, int ff0, int ff1, void* gu, size_t
     };
     try {
         uint8_t* h = (uint8_t*) host;
-        for (int64_t e = 0; e < NE; ++e) {
+        for (int64_t e = 0; e < E + (shared ? 1 : 0); ++e) {
             const bool sh = e == E;
             const uint32_t gt = sh ? stype : type, dt = sh ? sdtype : dtype;
             const size_t rbi = row_bytes(gt, (int) H), rbf = row_bytes(dt, ffs), rb_full_dn = row_bytes(dt, (int) FF);
@@ -428,8 +436,13 @@ void moe_layer(const sfnx_gguf* g, int layer, int ff0, int ff1, void* gu, size_t
             // every down row, columns ff0..ff1 (src/model.cpp:586-606)
             for (int64_t r = 0; r < H; ++r) std::memcpy(h + gub + r * rbf, d0 + r * rb_full_dn + col0, rbf);
             check(hipMemcpyAsync(dev, host, gub + (size_t) H * rbf, hipMemcpyHostToDevice, s), "hipMemcpyAsync");
-            void* gdst = sh && q8s ? sh_gu : (uint8_t*) gu + e * gu_stride;
-            void* ddst = sh && q8s ? sh_dn : (uint8_t*) dn + e * dn_stride;
+            if (sh && q8s) {   // the dense shared expert: the reference's split planes
+                if (sfnx_q8s_split(dev, 2 * ffs, (int) H, sh_gu, st) != 0) throw std::runtime_error(sfnx_last_error());
+                if (sfnx_q8s_split((uint8_t*) dev + gub, (int) H, ffs, sh_dn, st) != 0) throw std::runtime_error(sfnx_last_error());
+                continue;
+            }
+            void* gdst = (uint8_t*) gu + e * gu_stride;
+            void* ddst = (uint8_t*) dn + e * dn_stride;
             if (sfnx_store_pack(gt, dev, gdst, 1, 2 * ffs, (int) H, st) != 0) throw std::runtime_error(sfnx_last_error());
             if (sfnx_store_pack(dt, (uint8_t*) dev + gub, ddst, 1, (int) H, ffs, st) != 0) throw std::runtime_error(sfnx_last_error());
         }
@@ -453,18 +466,19 @@ void moe_layer(const sfnx_gguf* g, int layer, int ff0, int ff1, void* gu, size_t
 }
 }  // namespace
 
-extern "C" int sfnx_gguf_moe_layer(const sfnx_gguf* g, int layer, int ff0, int ff1, void* gu, size_t gu_stride, void* dn,
-                                   size_t dn_stride, float* W, int* info, void* st) {
+extern "C" int sfnx_gguf_moe_layer(const sfnx_gguf* g, int layer, int ff0, int ff1, void* gu, size_t gu_stride,
+                                   size_t gu_bytes, void* dn, size_t dn_stride, size_t dn_bytes, float* W, int w_rows,
+                                   int* info, void* st) {
     return guarded("sfnx_gguf_moe_layer", [&] {
-        moe_layer(g, layer, ff0, ff1, gu, gu_stride, dn, dn_stride, W, nullptr, nullptr, info, st);
+        moe_layer(g, layer, ff0, ff1, gu, gu_stride, gu_bytes, dn, dn_stride, dn_bytes, W, w_rows, nullptr, nullptr, info, st);
     });
 }
 
 extern "C" int sfnx_gguf_moe_layer_q8s(const sfnx_gguf* g, int layer, int ff0, int ff1, void* gu, size_t gu_stride,
-                                       void* dn, size_t dn_stride, float* W, void* sh_gu, void* sh_dn, int* info,
-                                       void* st) {
+                                       size_t gu_bytes, void* dn, size_t dn_stride, size_t dn_bytes, float* W,
+                                       int w_rows, const sfnx_q8s* sh_gu, const sfnx_q8s* sh_dn, int* info, void* st) {
     return guarded("sfnx_gguf_moe_layer_q8s", [&] {
         require(sh_gu != nullptr && sh_dn != nullptr, "null argument");
-        moe_layer(g, layer, ff0, ff1, gu, gu_stride, dn, dn_stride, W, sh_gu, sh_dn, info, st);
+        moe_layer(g, layer, ff0, ff1, gu, gu_stride, gu_bytes, dn, dn_stride, dn_bytes, W, w_rows, sh_gu, sh_dn, info, st);
     });
 }

@@ -635,21 +635,23 @@ extern "C" int sfnx_to_f16(const float* x, uint16_t* y, size_t n, void* st) {
     });
 }
 
-extern "C" int sfnx_pf_dense(const void* W, int rows, int cols, const uint16_t* xh, int C, float* out, int ldo, void* wk,
-                             size_t wk_bytes, void* st) {
+extern "C" int sfnx_pf_dense(const sfnx_q8s* W, int rows, int cols, const uint16_t* xh, int C, float* out, int ldo,
+                             void* wk, size_t wk_bytes, void* st) {
     return guarded("sfnx_pf_dense", [&] {
-        require(W != nullptr && xh != nullptr && out != nullptr, "null pointer");
+        require(W != nullptr && W->q != nullptr && W->d != nullptr && xh != nullptr && out != nullptr && wk != nullptr,
+                "null pointer");
         require(rows > 0 && rows % DN_BM == 0 && cols > 0 && cols % MM_RUN == 0, "rows must be a multiple of 256, cols of 512");
         require(C >= 1 && C <= (1 << 20) && ldo >= rows, "C out of range, or ldo smaller than rows");
-        // the reference dequantizes the matrix to f16 and multiplies in one f16 GEMM with fp32 results (pf_dense_xh,
-        // cublasGemmEx); here the matrix is one expert of the matrix-core kernels, whose weights are the same f16
-        // values (hmul2(q, d)), dotted in fp32 on v_mfma_f32_32x32x16_f16, its rows the jobs of 64 rows each block
-        // makes for itself.  The workspace (the reference's f16 staging) is not needed.
-        (void) wk;
-        (void) wk_bytes;
+        require(wk_bytes >= q8s_planar_bytes(rows, cols), "wk smaller than the matrix's Q8_0 staging (rows * cols * 34 / 32 bytes)");
+        // the reference converts the matrix into its staging buffer (k_q8s_f16 into p.wh) and multiplies in one f16
+        // GEMM with fp32 results (pf_dense_xh, cublasGemmEx); here the staging is the planar Q8_0 layout, run as one
+        // expert of the matrix-core kernels, whose weights are the same f16 values (hmul2(q, d)), dotted in fp32 on
+        // v_mfma_f32_32x32x16_f16, its rows the jobs of 64 rows each block makes for itself
+        hipStream_t s = stream_of(st);
+        q8s_to_planar(*W, rows, cols, wk, s);
         const int nj = (C + SFNX_PF_JOB - 1) / SFNX_PF_JOB;
-        const size_t sa = row_bytes(SFNX_Q8_0, cols) * (size_t) rows;
+        const size_t sa = q8s_planar_bytes(rows, cols);
         // one 256-row tile a block: few jobs, so every tile is a block of its own
-        moe_mma(SFNX_Q8_0, W, sa, cols, rows, nullptr, nullptr, nj, xh, out, st, ldo, 1, C);
+        moe_mma(SFNX_Q8_0, wk, sa, cols, rows, nullptr, nullptr, nj, xh, out, st, ldo, 1, C);
     });
 }

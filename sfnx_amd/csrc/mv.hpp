@@ -285,22 +285,23 @@ template <int BPL, int TYPE> struct NbRow {
 // row, lane L the 16-column halves c = 16 L + 512 i in order, acc_L = fmaf(d_w d_a, sum of the 16 products, acc_L),
 // then v += shfl_xor(v, o) for o = 16 .. 1.  Here LPR physical lanes carry the 32 logical ones, L = ln + LPR k, and
 // fold theirs in the butterfly's order (xor 16 and 8 are k ^ 2 and k ^ 1 for LPR 8, xor 16 is k ^ 1 for LPR 16), so
-// group_sum<LPR> of the result finishes exactly the reference's sum.  Weights in the planar Q8_0 layout: the half h of
-// block b is piece 32 (b / 16) + 16 h + b % 16, so logical lane L's i-th piece is 32 i + 16 (L & 1) + L / 2.  Read
-// straight from memory (the shared expert is one job of a launch; no register copy of the row is kept).
-// The same sums from registers: issue() loads a row's pieces for the lane's logical lanes (NI = C / 512 each), dot()
+// group_sum<LPR> of the result finishes exactly the reference's sum.  Weights in the reference's split layout
+// (Q8sPlanes): logical lane L's i-th 16 values are columns 512 i + 16 L of the row, block b = 16 i + L / 2, so the 32
+// lanes of a row read 512 contiguous bytes.  Read straight from memory (the shared expert is one job of a launch; no
+// register copy of the row is kept).
+// The same sums from registers: issue() loads a row's values for the lane's logical lanes (NI = C / 512 each), dot()
 // forms the lane's partial in q8s_dot's order.
 template <int LPR, int NI> struct Q8sRow {
     static constexpr int NL = 32 / LPR;
     uint4 w[NL][NI];
     uint16_t dh[NL][NI];
-    __device__ __forceinline__ void issue(const Q80Planes& P, int row, int C, int ln) {
+    __device__ __forceinline__ void issue(const Q8sPlanes& P, int row, int C, int ln) {
 #pragma unroll
         for (int i = 0; i < NI; ++i)
 #pragma unroll
             for (int k = 0; k < NL; ++k) {
                 const int L = ln + LPR * k;
-                w[k][i] = *reinterpret_cast<const uint4*>(P.q16(row, C, 32 * i + 16 * (L & 1) + L / 2));
+                w[k][i] = *reinterpret_cast<const uint4*>(P.q16(row, C, 512 * i + 16 * L));
                 dh[k][i] = *P.dof(row, C, 16 * i + L / 2);
             }
     }
@@ -327,7 +328,7 @@ template <int LPR, int NI> struct Q8sRow {
     }
 };
 
-template <int LPR> __device__ __forceinline__ float q8s_dot(const Q80Planes& P, int row, int C, int ln, const Acts& a, int j) {
+template <int LPR> __device__ __forceinline__ float q8s_dot(const Q8sPlanes& P, int row, int C, int ln, const Acts& a, int j) {
     static_assert(LPR == 8 || LPR == 16 || LPR == 32, "q8s lanes");
     constexpr int NL = 32 / LPR;
     const int nb = C / 32;
@@ -338,7 +339,7 @@ template <int LPR> __device__ __forceinline__ float q8s_dot(const Q80Planes& P, 
 #pragma unroll
         for (int k = 0; k < NL; ++k) {
             const int L = ln + LPR * k, h = L & 1, b = 16 * i + L / 2;
-            const uint4 w = *reinterpret_cast<const uint4*>(P.q16(row, C, 32 * i + 16 * h + L / 2));
+            const uint4 w = *reinterpret_cast<const uint4*>(P.q16(row, C, 512 * i + 16 * L));
             const float dw = h2f(*P.dof(row, C, b));
             const int4 av = a.q4(j, b)[h];
             int s = dot4((int) w.x, av.x, 0);

@@ -21,10 +21,9 @@ enum GgmlType : uint32_t {   // src/gguf.hpp:22-25
     T_Q4_0 = SFNX_Q4_0, T_Q5_1 = SFNX_Q5_1, T_Q8_0 = SFNX_Q8_0, T_Q4_K = SFNX_Q4_K, T_Q5_K = SFNX_Q5_K
 };
 
-// src/model.hpp:72-75 Q8S: a dense Q8_0 matrix (here the planar Q8_0 layout of one matrix, in p)
-struct Q8S {
-    const void* p = nullptr;
-};
+// src/model.hpp:71-74 Q8S: a dense Q8_0 matrix in the split layout, int8 values q [rows][cols] and f16 scale bits
+// d [rows][cols / 32] (the C struct, so the reference's fields and their types)
+using Q8S = sfnx_q8s;
 
 // src/model.hpp:78-87 DW: one matrix (or expert 0's of a stack), n_out rows of n_in.  row_bytes and s are kept for
 // the reference's field list (row_bytes is derived from type and n_in here; s is the dense form of a matrix).  ep: a
@@ -76,7 +75,7 @@ inline void quantize_q8_1(const float* x, void* q, int n, int rows, void* st) { 
 
 // src/kernels.hpp:47 (src/dense.cuh:24-154): the shared expert's dense Q8_0 product in the reference's q8s sums
 inline void q8s_gemv(const Q8S& w, int rows, int cols, const void* y, float* out, int out_stride, int T, void* st) {
-    ck(sfnx_q8s_gemv(w.p, rows, cols, y, out, out_stride, T, st));
+    ck(sfnx_q8s_gemv(&w, rows, cols, y, out, out_stride, T, st));
 }
 // src/kernels.cu:2018-2024
 inline void swiglu_stacked_q8_1(const float* gu, void* hq, int ffs, int T, void* st) { ck(sfnx_swiglu_stacked_q8_1(gu, hq, ffs, T, st)); }
@@ -138,7 +137,7 @@ inline void router_route(const float* W, const float* x, float* logits, int T, i
     ck(sfnx_router_route(W, x, logits, T, s.H, s.E, s.K, topi, topw, jobs_gu, jobs_dn, njobs, 0, st));
     // the reference plans in the router launch's last block; here the plan is the next launch on the stream
     if (ec) ck(sfnx_cache_plan(jobs_gu, njobs, layer, ec, list, st));
-    if (sh_gu) ck(sfnx_q8s_gemv(sh_gu->p, sh_rows, s.H, sh_y, sh_out, sh_rows, T, st));
+    if (sh_gu) ck(sfnx_q8s_gemv(sh_gu, sh_rows, s.H, sh_y, sh_out, sh_rows, T, st));
 }
 // src/kernels.cu:1655-1668 cache_copy / moe_cache: the planned experts into their slots (moe_cache plans first when
 // given the jobs)
@@ -155,7 +154,7 @@ inline void moe_gate_up(const DW& A, size_t sa, const Job* jobs, const int* njob
     detail::no_cache(nullptr, &A);
     const int T = detail::rows_of(njobs_max);
     ck(sfnx_moe_gate_up(detail::base_of(A), detail::stride_of(A, sa), A.type, A.n_in, A.n_out, jobs, njobs, njobs_max, T, xq, gu, st));
-    if (sh_down) ck(sfnx_q8s_swiglu_gemv(sh_down->p, A.n_in, sh_ffs, sh_gu, sh_out, A.n_in, T, st));
+    if (sh_down) ck(sfnx_q8s_swiglu_gemv(sh_down, A.n_in, sh_ffs, sh_gu, sh_out, A.n_in, T, st));
 }
 // src/kernels.hpp:305
 inline void moe_down(const DW& A, size_t sa, const Job* jobs, const int* njobs, int njobs_max, const float* gu, float* part,
@@ -209,15 +208,10 @@ inline void moe_combine(const MoeShape& s, const float* part, const float* topw,
     ck(sfnx_moe_combine(part, topw, topi, logits, y, T, s.H, s.E, s.K, shared ? 1 : 0, st));
 }
 
-// src/model.hpp:72-75 Q8S as the hc read takes it: int8 values [rows][cols] and f16 scale bits [rows][cols / 32]
-struct Q8Split {
-    const int8_t* q = nullptr;
-    const uint16_t* d = nullptr;
-};
 // src/kernels.cu:1054 hc_read: N, HC and LR are the reference's compile-time model constants (src/model.hpp:39);
 // scratch is sfnx_hc_workspace(N, HC, LR) bytes (no barrier counter and no err word: no kernel waits on another)
-inline void hc_read(float* R, const float* bo, const float* inj_prev, const float* w_norm, const Q8Split& w_down,
-                    const Q8Split& w_up, const uint16_t* w_inj, float eps, float* mixed, float* inject, void* scratch,
+inline void hc_read(float* R, const float* bo, const float* inj_prev, const float* w_norm, const Q8S& w_down,
+                    const Q8S& w_up, const uint16_t* w_inj, float eps, float* mixed, float* inject, void* scratch,
                     size_t scratch_bytes, int T, void* st, void* q8, int N, int HC, int LR) {
     ck(sfnx_hc_read(R, bo, inj_prev, w_norm, w_down.q, w_down.d, w_up.q, w_up.d, w_inj, eps, mixed, inject, q8, T, N, HC,
                     LR, scratch, scratch_bytes, st));

@@ -124,10 +124,38 @@ def moe_combine(part, topw, topi, logits, y, E: int, K: int, shared: bool = True
     check(lib().sfnx_moe_combine(_p(part), _p(topw), _p(topi), _p(logits), _p(y), T, H, E, K, int(shared), _st()))
 
 
-def q8s_gemv(W, rows: int, cols: int, y, out, out_stride: int, T: int) -> None:
-    """src/kernels.hpp:47: out[t][r] = dense Q8_0 row r of W (planar, one matrix) . q8_1 row t of y, the reference's
-    q8s sums (src/dense.cuh:24-154); out rows out_stride floats apart"""
-    check(lib().sfnx_q8s_gemv(_p(W), rows, cols, _p(y), _p(out), out_stride, T, _st()))
+class Q8sMatrix:
+    """src/model.hpp:71-74 Q8S: a dense Q8_0 matrix [rows][cols] in the reference's split layout (src/model.cpp:384-440
+    q8split): int8 values q [rows][cols] and the f16 scale bits d [rows][cols / 32] (held as int16), two allocations.
+    `c` is the sfnx_q8s struct the C ABI takes (by address, ptr())."""
+
+    def __init__(self, rows: int, cols: int, device="cuda"):
+        self.rows, self.cols = rows, cols
+        self.q = torch.empty((rows, cols), dtype=torch.int8, device=device)
+        self.d = torch.empty((rows, cols // 32), dtype=torch.int16, device=device)
+        self.c = _abi.Q8S(self.q.data_ptr(), self.d.data_ptr())
+
+    def ptr(self) -> int:
+        return C.addressof(self.c)
+
+    @staticmethod
+    def from_gguf(blocks: torch.Tensor, rows: int, cols: int) -> "Q8sMatrix":
+        """GGUF Q8_0 blocks [rows][cols / 32] split on the device (sfnx_q8s_split)"""
+        m = Q8sMatrix(rows, cols, device=blocks.device)
+        check(lib().sfnx_q8s_split(_p(blocks), rows, cols, m.ptr(), _st()))
+        return m
+
+    def to_gguf(self) -> torch.Tensor:
+        """the GGUF Q8_0 blocks (uint8 [rows * cols / 32 * 34]) of the matrix"""
+        d = self.d.reshape(-1, 1).view(torch.uint8).reshape(-1, 2)
+        q = self.q.reshape(-1, 32).view(torch.uint8)
+        return torch.cat([d, q], dim=1).reshape(-1)
+
+
+def q8s_gemv(W: "Q8sMatrix", rows: int, cols: int, y, out, out_stride: int, T: int) -> None:
+    """src/kernels.hpp:47: out[t][r] = dense Q8_0 row r of W (split layout) . q8_1 row t of y, the reference's q8s sums
+    (src/dense.cuh:24-154); out rows out_stride floats apart"""
+    check(lib().sfnx_q8s_gemv(W.ptr(), rows, cols, _p(y), _p(out), out_stride, T, _st()))
 
 
 def swiglu_stacked_q8_1(gu, hq, ffs: int, T: int) -> None:
@@ -138,7 +166,7 @@ def swiglu_stacked_q8_1(gu, hq, ffs: int, T: int) -> None:
 def q8s_swiglu_gemv(W, rows: int, ffs: int, gu, out, out_stride: int, T: int) -> None:
     """src/kernels.hpp:281-282's shared-expert tail in one launch: out[t][r] = dense Q8_0 row r of W . q8_1 of
     silu(gate) * up of gu row t ([gate | up], 2 ffs floats); equal to swiglu_stacked_q8_1 then q8s_gemv"""
-    check(lib().sfnx_q8s_swiglu_gemv(_p(W), rows, ffs, _p(gu), _p(out), out_stride, T, _st()))
+    check(lib().sfnx_q8s_swiglu_gemv(W.ptr(), rows, ffs, _p(gu), _p(out), out_stride, T, _st()))
 
 
 def residual_rmsnorm(x, y, xn, eps: float = 1e-6) -> None:
@@ -187,11 +215,12 @@ class MoeLayer:
     """One MoE layer's weights resident in HBM (planar store) plus the buffers its entry points write.
 
     gu_w: experts' gate|up [E+1][2 ff][H] (expert E is the shared one), dn_w: down [E+1][H][ff], W: router [E+1][H].
-    With shape.sh_q8s the stores hold E experts and sh_gu [2 ff][H], sh_dn [H][ff] (planar Q8_0) the shared expert.
+    With shape.sh_q8s the stores hold E experts and sh_gu [2 ff][H], sh_dn [H][ff] (Q8sMatrix, the reference's split
+    Q8_0 layout) the shared expert.
     """
 
     def __init__(self, shape: LayerShape, W: torch.Tensor, gu_w: torch.Tensor, dn_w: torch.Tensor,
-                 sh_gu: torch.Tensor | None = None, sh_dn: torch.Tensor | None = None):
+                 sh_gu: "Q8sMatrix | None" = None, sh_dn: "Q8sMatrix | None" = None):
         if W.shape[0] != shape.E + 1:
             raise ValueError("the router has E + 1 rows (row E gates the shared expert)")
         if shape.sh_q8s and (sh_gu is None or sh_dn is None or not shape.shared):
@@ -213,9 +242,8 @@ class MoeLayer:
         store_pack(s.dn_type, dn_gguf, dn, s.n_routed, s.H, s.ff)
         sh_gu = sh_dn = None
         if s.sh_q8s:
-            sh_gu, sh_dn = torch.empty_like(sh_gu_gguf), torch.empty_like(sh_dn_gguf)
-            store_pack(Q8_0, sh_gu_gguf, sh_gu, 1, 2 * s.ff, s.H)
-            store_pack(Q8_0, sh_dn_gguf, sh_dn, 1, s.H, s.ff)
+            sh_gu = Q8sMatrix.from_gguf(sh_gu_gguf, 2 * s.ff, s.H)
+            sh_dn = Q8sMatrix.from_gguf(sh_dn_gguf, s.H, s.ff)
         return MoeLayer(s, W, gu, dn, sh_gu, sh_dn)
 
     @staticmethod
@@ -249,8 +277,7 @@ class MoeLayer:
                 synth_normal(t, sd, 0.02, offset=s.E * rows * cols)
                 b = blk[: rows * row_bytes(Q8_0, cols)]
                 quantize_weights(Q8_0, t.view(rows, cols), b)
-                sh[mat] = torch.empty_like(b)
-                store_pack(Q8_0, b, sh[mat], 1, rows, cols)
+                sh[mat] = Q8sMatrix.from_gguf(b, rows, cols)
         del tmp, blk
         return MoeLayer(s, W, gu, dn, sh[0], sh[1])
 
@@ -321,7 +348,7 @@ class FusedDecode:
         self.sh_table = None
         if s.sh_q8s:
             self.sh_table = (_abi.SharedQ8s * len(layers))(*[
-                _abi.SharedQ8s(L.sh_gu.data_ptr(), L.sh_dn.data_ptr()) for L in layers])
+                _abi.SharedQ8s(L.sh_gu.c, L.sh_dn.c) for L in layers])
 
     def __call__(self, x: torch.Tensor, norm: bool = True, eps: float = 1e-6, layer0: int = 0,
                  n_layers: int | None = None, phases: int = 0) -> None:
@@ -369,7 +396,7 @@ class PrefillBuffers:
         self.part = torch.zeros((NP, s.H), dtype=torch.float32, device=device)
         self.xh = torch.zeros((C, s.H), dtype=torch.float16, device=device)
         self.h16 = torch.zeros((NP, s.ff), dtype=torch.float16, device=device)
-        if s.sh_q8s:   # f16 staging for the dense shared matrices (the reference's p.wh)
+        if s.sh_q8s:   # staging for the dense shared matrices (the reference's p.wh, sized for their f16 values)
             self.wh = torch.empty(2 * s.ff * s.H, dtype=torch.float16, device=device)
 
 
@@ -387,10 +414,10 @@ def prefill_route(L: "MoeLayer", x: torch.Tensor, b: "PrefillBuffers", bias: tor
     pf_route(b.logits, b.topi, b.topw, b.cnt, b.jbase, b.jobs_gu, b.jobs_dn, b.njobs, s.E, s.K, s.shared and not s.sh_q8s)
 
 
-def pf_dense(W, rows: int, cols: int, xh, out, ldo: int, wh) -> None:
-    """src/prefill.cu:407-417 pf_dense_xh: out rows (stride ldo) = f16(W) . xh rows, fp32, on the matrix-core kernels
-    (wh, the reference's f16 staging buffer, is kept in the argument list and not used)"""
-    check(lib().sfnx_pf_dense(_p(W), rows, cols, _p(xh), xh.shape[0], _p(out), ldo, _p(wh), wh.numel() * wh.element_size(), _st()))
+def pf_dense(W: "Q8sMatrix", rows: int, cols: int, xh, out, ldo: int, wh) -> None:
+    """src/prefill.cu:407-417 pf_dense_xh: out rows (stride ldo) = f16(W) . xh rows, fp32, on the matrix-core kernels;
+    wh (the reference's staging buffer) receives W repacked for them (rows * cols * 34 / 32 bytes at least)"""
+    check(lib().sfnx_pf_dense(W.ptr(), rows, cols, _p(xh), xh.shape[0], _p(out), ldo, _p(wh), wh.numel() * wh.element_size(), _st()))
 
 
 def prefill_shared(L: "MoeLayer", b: "PrefillBuffers") -> None:
@@ -567,12 +594,12 @@ def gguf_moe_layer(g: Gguf, layer: int, ff0: int = 0, ff1: int | None = None, K:
     info = (C.c_int * 6)()
     sh_gu = sh_dn = None
     if q8s:
-        sh_gu = torch.empty(2 * ffs * row_bytes(Q8_0, H), dtype=torch.uint8, device="cuda")
-        sh_dn = torch.empty(H * row_bytes(Q8_0, ffs), dtype=torch.uint8, device="cuda")
-        check(lib().sfnx_gguf_moe_layer_q8s(g._h, layer, ff0, ff1, _p(gu), gu_stride, _p(dn), dn_stride, _p(W),
-                                            _p(sh_gu), _p(sh_dn), info, _st()))
+        sh_gu, sh_dn = Q8sMatrix(2 * ffs, H), Q8sMatrix(H, ffs)
+        check(lib().sfnx_gguf_moe_layer_q8s(g._h, layer, ff0, ff1, _p(gu), gu_stride, gu.numel(), _p(dn), dn_stride,
+                                            dn.numel(), _p(W), W.shape[0], sh_gu.ptr(), sh_dn.ptr(), info, _st()))
     else:
-        check(lib().sfnx_gguf_moe_layer(g._h, layer, ff0, ff1, _p(gu), gu_stride, _p(dn), dn_stride, _p(W), info, _st()))
+        check(lib().sfnx_gguf_moe_layer(g._h, layer, ff0, ff1, _p(gu), gu_stride, gu.numel(), _p(dn), dn_stride, dn.numel(),
+                                        _p(W), W.shape[0], info, _st()))
     s = LayerShape(H=H, E=E, K=K, ff=ffs, wtype=wtype, shared=shared, dn_wtype=None if info[5] == wtype else info[5],
                    sh_q8s=q8s)
     return MoeLayer(s, W, gu, dn, sh_gu, sh_dn)
@@ -619,11 +646,13 @@ class ExpertCache:
         self.owner = torch.full((n_slots,), -1, dtype=torch.int32, device=device)
         self.ref = torch.zeros(n_slots, dtype=torch.uint8, device=device)
         self.hand = torch.zeros(_abi.EC_POOLS, dtype=torch.int32, device=device)
+        self.status = torch.zeros(2, dtype=torch.int32, device=device)
         c = _abi.ExpertCacheC()
         c.n_slots, c.n_pools, c.n_layers, c.n_experts = n_slots, 1, NL, E
         c.s0[0], c.n[0], c.slot_bytes[0], c.dn_off[0], c.pool[0] = 0, n_slots, self.slot_bytes, self.gu_bytes, _p(self.pool)
         c.ep_gu, c.ep_dn, c.host_gu, c.host_dn = _p(self.ep_gu), _p(self.ep_dn), _p(self.host_gu), _p(self.host_dn)
         c.slot_of, c.owner, c.ref, c.hand = _p(self.slot_of), _p(self.owner), _p(self.ref), _p(self.hand)
+        c.status = _p(self.status)
         self.c = c
         torch.cuda.synchronize()
         self._views = []
@@ -635,6 +664,11 @@ class ExpertCache:
 
     def layer_view(self, l: int) -> "MoeLayer":
         return self._views[l]
+
+    def host_misses(self) -> tuple[int, int]:
+        """(the misses the last plan left on their host copies, their running total); synchronises"""
+        v = self.status.cpu().tolist()
+        return int(v[0]), int(v[1])
 
     def plan(self, jobs, njobs, layer: int, out_list) -> None:
         check(lib().sfnx_cache_plan(_p(jobs), _p(njobs), layer, C.byref(self.c), _p(out_list), _st()))

@@ -49,6 +49,31 @@ void* synth_store(uint32_t type, int n_mat, int rows, int cols, uint64_t seed, u
     return p;
 }
 
+// a dense Q8_0 matrix of rows x cols, N(0, 0.02) from seed, quantized and split on the host into the two planes the
+// reference's loader fills (src/model.cpp:384-440 q8split: int8 values [rows][cols], f16 scale bits [rows][cols / 32]),
+// each its own device allocation
+Q8S synth_q8s(int rows, int cols, uint64_t seed, uint64_t offset) {
+    const size_t vals = (size_t) rows * cols, nb = vals / 32;
+    float* f = dev<float>(vals);
+    uint8_t* g = dev<uint8_t>(nb * 34);
+    ck(sfnx_synth_normal(f, vals, seed, offset, 0.02f, nullptr));
+    ck(sfnx_quantize_weights(T_Q8_0, f, g, rows, cols, nullptr));
+    std::vector<uint8_t> blocks(nb * 34);
+    hk(hipMemcpy(blocks.data(), g, blocks.size(), hipMemcpyDeviceToHost), "copy");
+    hk(hipFree(f), "hipFree");
+    hk(hipFree(g), "hipFree");
+    std::vector<int8_t> q(vals);
+    std::vector<uint16_t> d(nb);
+    for (size_t b = 0; b < nb; ++b) {
+        std::memcpy(&d[b], &blocks[b * 34], 2);
+        std::memcpy(&q[b * 32], &blocks[b * 34 + 2], 32);
+    }
+    Q8S m{dev<int8_t>(vals), dev<uint16_t>(nb)};
+    hk(hipMemcpy(m.q, q.data(), vals, hipMemcpyHostToDevice), "copy");
+    hk(hipMemcpy(m.d, d.data(), nb * 2, hipMemcpyHostToDevice), "copy");
+    return m;
+}
+
 // mode 0: shared expert as expert E; 1: dense Q8_0 through the MoeShape overloads; 2: dense Q8_0 through the
 // reference's exact argument lists
 bool run(int mode) {
@@ -62,8 +87,8 @@ bool run(int mode) {
     ck(sfnx_synth_normal(W, (size_t) (s.E + 1) * s.H, 11, 0, 0.02f, nullptr));
     const DW gu_e{synth_store(type, E_store, 2 * ff, s.H, 12, 0), type, s.H, 2 * ff};
     const DW dn_e{synth_store(type, E_store, s.H, ff, 13, 0), type, ff, s.H};
-    const Q8S sh_gu{dense_shared ? synth_store(T_Q8_0, 1, 2 * ff, s.H, 12, (uint64_t) s.E * 2 * ff * s.H) : nullptr};
-    const Q8S sh_dn{dense_shared ? synth_store(T_Q8_0, 1, s.H, ff, 13, (uint64_t) s.E * s.H * ff) : nullptr};
+    const Q8S sh_gu = dense_shared ? synth_q8s(2 * ff, s.H, 12, (uint64_t) s.E * 2 * ff * s.H) : Q8S{nullptr, nullptr};
+    const Q8S sh_dn = dense_shared ? synth_q8s(s.H, ff, 13, (uint64_t) s.E * s.H * ff) : Q8S{nullptr, nullptr};
     float* x = dev<float>((size_t) T * s.H);
     ck(sfnx_synth_normal(x, (size_t) T * s.H, 14, 0, 1.0f, nullptr));
     // the unfused calls
@@ -103,7 +128,7 @@ bool run(int mode) {
     uint8_t* ws = dev<uint8_t>(wsb);
     const sfnx_moe_layer_w lw{W, gu_e.p, gu_stride, dn_e.p, dn_stride};
     if (dense_shared) {
-        const sfnx_moe_shared_q8s shw{sh_gu.p, sh_dn.p};
+        const sfnx_moe_shared_q8s shw{sh_gu, sh_dn};
         ck(sfnx_moe_decode_q8s(&lw, &shw, 1, type, type, s.H, s.E, s.K, ff, xf, T, 0, 1e-6f, ws, wsb, 0, nullptr));
     } else {
         ck(sfnx_moe_decode(&lw, 1, type, s.H, s.E, s.K, ff, 1, xf, T, 0, 1e-6f, ws, wsb, 0, nullptr));
@@ -204,8 +229,8 @@ bool run_cached() {
     ck(sfnx_synth_normal(W, (size_t) (s.E + 1) * s.H, 31, 0, 0.02f, nullptr));
     const DW gu_e{synth_store(type, s.E, 2 * ff, s.H, 32, 0), type, s.H, 2 * ff};
     const DW dn_e{synth_store(type, s.E, s.H, ff, 33, 0), type, ff, s.H};
-    const Q8S sh_gu{synth_store(T_Q8_0, 1, 2 * ff, s.H, 32, (uint64_t) s.E * 2 * ff * s.H)};
-    const Q8S sh_dn{synth_store(T_Q8_0, 1, s.H, ff, 33, (uint64_t) s.E * s.H * ff)};
+    const Q8S sh_gu = synth_q8s(2 * ff, s.H, 32, (uint64_t) s.E * 2 * ff * s.H);
+    const Q8S sh_dn = synth_q8s(s.H, ff, 33, (uint64_t) s.E * s.H * ff);
     // the cache: host copies of every expert, one pool of n_slots empty slots, the tables at the host copies
     void *hg = nullptr, *hgd = nullptr, *hd = nullptr, *hdd = nullptr;
     ck(sfnx_host_alloc(gu_stride * s.E, &hg, &hgd));

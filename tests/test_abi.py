@@ -25,6 +25,11 @@ def test_row_bytes():
     assert lib.sfnx_row_bytes(_abi.Q8_0, 2048) == 2176
 
 
+# a host sfnx_q8s whose (never dereferenced) device pointers are non-null: the calls below fail their checks first
+_Q8S = _abi.Q8S(1, 1)
+_Q8S_PTR = C.addressof(_Q8S)
+
+
 @pytest.mark.parametrize("call, msg", [
     (lambda L: L.sfnx_router_route(None, None, None, 0, 2048, 512, 10, None, None, None, None, None, 1, None), "T out of range"),
     (lambda L: L.sfnx_router_route(None, None, None, 17, 2048, 512, 10, None, None, None, None, None, 1, None), "T out of range"),
@@ -37,12 +42,15 @@ def test_row_bytes():
     (lambda L: L.sfnx_store_pack(12, None, None, 1, 4, 256, None), "multiple of 512"),
     (lambda L: L.sfnx_quantize_q8_1(None, None, 30, 1, None), "multiple of 32"),
     (lambda L: L.sfnx_pf_route(None, 0, 512, 10, None, None, None, None, None, None, None, 1, None), "C must be positive"),
-    (lambda L: L.sfnx_q8s_gemv(1, 100, 2048, 1, 1, 100, 1, None), "rows must be"),
-    (lambda L: L.sfnx_q8s_gemv(1, 96, 2000, 1, 1, 96, 1, None), "cols must be"),
-    (lambda L: L.sfnx_q8s_gemv(1, 96, 2048, 1, 1, 64, 1, None), "out_stride"),
+    (lambda L: L.sfnx_q8s_gemv(_Q8S_PTR, 100, 2048, 1, 1, 100, 1, None), "rows must be"),
+    (lambda L: L.sfnx_q8s_gemv(_Q8S_PTR, 96, 2000, 1, 1, 96, 1, None), "cols must be"),
+    (lambda L: L.sfnx_q8s_gemv(_Q8S_PTR, 96, 2048, 1, 1, 64, 1, None), "out_stride"),
+    (lambda L: L.sfnx_q8s_gemv(None, 96, 2048, 1, 1, 96, 1, None), "null pointer"),
+    (lambda L: L.sfnx_q8s_split(1, 96, 2000, _Q8S_PTR, None), "multiple of 32"),
     (lambda L: L.sfnx_swiglu_stacked_q8_1(1, 1, 500, 1, None), "ffs must be"),
-    (lambda L: L.sfnx_pf_dense(1, 1024, 2000, 1, 10, 1, 1024, 1, 1 << 30, None), "cols of 512"),
-    (lambda L: L.sfnx_pf_dense(1, 1000, 2048, 1, 10, 1, 1024, 1, 100, None), "multiple of 256"),
+    (lambda L: L.sfnx_pf_dense(_Q8S_PTR, 1024, 2000, 1, 10, 1, 1024, 1, 1 << 30, None), "cols of 512"),
+    (lambda L: L.sfnx_pf_dense(_Q8S_PTR, 1000, 2048, 1, 10, 1, 1024, 1, 100, None), "multiple of 256"),
+    (lambda L: L.sfnx_pf_dense(_Q8S_PTR, 1024, 2048, 1, 10, 1, 1024, 1, 100, None), "wk smaller"),
     (lambda L: L.sfnx_hc_read(1, None, None, 1, 1, 1, 1, 1, None, 1e-6, 1, None, None, 1, 2000, 4, 320, 1, 1 << 30, None), "N must be"),
     (lambda L: L.sfnx_hc_read(1, None, None, 1, 1, 1, 1, 1, None, 1e-6, 1, None, None, 1, 2560, 9, 320, 1, 1 << 30, None), "HC must be"),
     (lambda L: L.sfnx_hc_read(1, None, None, 1, 1, 1, 1, 1, None, 1e-6, 1, None, None, 1, 2560, 4, 330, 1, 1 << 30, None), "LR must be"),

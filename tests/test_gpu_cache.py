@@ -58,19 +58,54 @@ def test_cached_decode_windows(n_slots):
         cache.close()
 
 
-def test_plan_reports_a_pool_too_small():
+def test_pool_too_small_leaves_misses_on_host():
+    """a window of 3 rows (more distinct experts than the pool's 12 slots) through the cache: the first 12 misses take
+    the slots and are copied in, the others stay on their host copies (status[0]); the layer through the tables still
+    equals the resident layer bit for bit, every table entry points at a slot holding that expert's bytes or at the
+    expert's host copy, no ref is left at 2, the state equals the CPU restatement's; and the next windows of one row
+    (7 jobs), which fit, plan and run as usual"""
     shape = moe.LayerShape(H=1024, E=64, K=6, ff=512, wtype=orc.Q4_K, shared=True)
     layers = [make_layer(shape, 95)[0]]
-    cache = moe.ExpertCache(layers, 4)   # a window of 7 jobs cannot fit
+    cache = moe.ExpertCache(layers, 12)
+    E1 = cache.n_experts
+    st = PoolState(1, E1, 12)
     lst = torch.zeros(64, dtype=torch.int32, device="cuda")
     try:
-        x = torch.from_numpy(orc.synth(shape.H, 1100, 1.0).reshape(1, shape.H)).cuda()
-        b = moe.DecodeBuffers(shape, 1)
-        moe.quantize_q8_1(x, b.xq)
-        moe.router_route(layers[0].W, x, b.logits, b.topi, b.topw, b.jobs_gu, b.jobs_dn, b.njobs, shape.E, shape.K, True)
-        cache.plan(b.jobs_gu, b.njobs, 0, lst)
-        torch.cuda.synchronize()
-        assert int(lst[0]) == -1
+        lefts = []
+        for w, T in enumerate((3, 1, 1, 2)):
+            x = torch.from_numpy(orc.synth(T * shape.H, 1100 + w, 1.0).reshape(T, shape.H)).cuda()
+            b0, b1 = moe.DecodeBuffers(shape, T), moe.DecodeBuffers(shape, T)
+            y0, y1 = torch.empty_like(x), torch.empty_like(x)
+            moe.decode_layer(layers[0], x, y0, b0)
+            moe.decode_layer_cached(cache, 0, x, y1, b1, lst)
+            torch.cuda.synchronize()
+            assert np.array_equal(bits(y0), bits(y1)), f"window {w}"
+            nj = int(b1.njobs[0])
+            jobs = [int(v) for v in job_array(b1.jobs_gu)[:nj]["w"]]
+            taken = cache_plan(st, jobs, 0)
+            got = lst.cpu().numpy()
+            assert got[0] == len(taken) and list(got[1:1 + len(taken)]) == taken
+            assert cache.host_misses()[0] == st.left
+            lefts.append(st.left)
+            if w == 0:
+                assert nj > 12 and st.left == nj - 12
+            if T == 1:
+                assert st.left == 0
+            assert cache.slot_of.cpu().tolist() == st.slot_of
+            assert cache.owner.cpu().tolist() == st.owner
+            assert cache.ref.cpu().tolist() == st.ref and 2 not in st.ref
+            assert int(cache.hand[0]) == st.hand
+            epg, hg = cache.ep_gu.cpu().numpy(), cache.host_gu.cpu().numpy()
+            pool = cache.pool.cpu().numpy()
+            gu_host = layers[0].gu_w.cpu().numpy()
+            for g, s in enumerate(st.slot_of):
+                if s >= 0:
+                    assert epg[g] == cache.pool.data_ptr() + s * cache.slot_bytes
+                    sl = pool[s * cache.slot_bytes: s * cache.slot_bytes + cache.gu_bytes]
+                    assert np.array_equal(sl, gu_host[g * cache.gu_bytes:(g + 1) * cache.gu_bytes])
+                else:
+                    assert epg[g] == hg[g]
+        assert cache.host_misses()[1] == sum(lefts)
     finally:
         cache.close()
 

@@ -84,6 +84,21 @@ def test_gguf_layer_refusals(tmp_path):
         moe.gguf_moe_layer(g, 1)
     with pytest.raises(RuntimeError, match="whole block"):
         moe.gguf_moe_layer(g, 0, 128, 512)
+    # the caller's buffers against the file's E (64 routed + the shared expert): one expert short of each is refused
+    # before anything is written
+    H, E, ff = 512, 64, 512
+    gs, ds = 2 * ff * orc.row_bytes(orc.Q4_K, H), H * orc.row_bytes(orc.Q4_K, ff)
+    gu = torch.full(((E + 1) * gs,), 7, dtype=torch.uint8, device="cuda")
+    dn = torch.full(((E + 1) * ds,), 7, dtype=torch.uint8, device="cuda")
+    Wt = torch.zeros((E + 1, H), dtype=torch.float32, device="cuda")
+    lib, p = moe.lib(), moe._p
+    for gb, db, wr, msg in [(E * gs, (E + 1) * ds, E + 1, "gu buffer too small"), ((E + 1) * gs, E * ds, E + 1, "dn buffer too small"),
+                            ((E + 1) * gs, (E + 1) * ds, E, "router rows")]:
+        assert lib.sfnx_gguf_moe_layer(g._h, 0, 0, ff, p(gu), gs, gb, p(dn), ds, db, p(Wt), wr, None, None) == -1
+        assert msg in lib.sfnx_last_error().decode()
+    torch.cuda.synchronize()
+    assert (gu == 7).all() and (dn == 7).all()
+    assert lib.sfnx_gguf_moe_layer(g._h, 0, 0, ff, p(gu), gs, gu.numel(), p(dn), ds, dn.numel(), p(Wt), E + 1, None, None) == 0
 
 
 @pytest.mark.parametrize("wtype,ff,ff0,ff1", [(orc.Q4_K, 512, 0, 512), (orc.Q4_K, 1024, 256, 768), (orc.Q5_1, 1024, 32, 544)])
@@ -102,11 +117,7 @@ def test_gguf_layer_q8s_shared(tmp_path, wtype, ff, ff0, ff1):
     assert s.sh_q8s and s.shared and L.gu_w.numel() == E * L.gu_stride
     rb_h, rb_f, rb_full = orc.row_bytes(orc.Q8_0, H), orc.row_bytes(orc.Q8_0, ffs), orc.row_bytes(orc.Q8_0, ff)
     col0 = orc.row_bytes(orc.Q8_0, ff0)
-    sg = torch.empty_like(L.sh_gu)
-    sd = torch.empty_like(L.sh_dn)
-    moe.store_unpack(orc.Q8_0, L.sh_gu, sg, 1, 2 * ffs, H)
-    moe.store_unpack(orc.Q8_0, L.sh_dn, sd, 1, H, ffs)
-    sg, sd = sg.cpu().numpy(), sd.cpu().numpy()
+    sg, sd = L.sh_gu.to_gguf().cpu().numpy(), L.sh_dn.to_gguf().cpu().numpy()
     want_g = np.concatenate([shared[0].reshape(ff, rb_h)[ff0:ff1], shared[1].reshape(ff, rb_h)[ff0:ff1]])
     assert np.array_equal(sg.reshape(2 * ffs, rb_h), want_g)
     assert np.array_equal(sd.reshape(H, rb_f), shared[2].reshape(H, rb_full)[:, col0:col0 + rb_f])

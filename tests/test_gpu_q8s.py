@@ -1,5 +1,5 @@
-"""The shared expert as its own dense Q8_0 matrices (the reference's Q8S, src/model.hpp:72-83) in the reference's q8s
-arithmetic (src/dense.cuh:24-154): sfnx_q8s_gemv and sfnx_swiglu_stacked_q8_1 against the oracle bit for bit; the
+"""The shared expert as its own dense Q8_0 matrices (the reference's Q8S, src/model.hpp:71-83: split int8 and f16-scale
+planes) in the reference's q8s arithmetic (src/dense.cuh:24-154): sfnx_q8s_gemv and sfnx_swiglu_stacked_q8_1 against the oracle bit for bit; the
 unfused layer against the oracle (gate|up bit-exact, down and the layer within 2e-3 max relative error, as every
 layer test: silu uses the device's expf); the fused decode (sfnx_moe_decode_q8s) against the unfused chain bit for
 bit; the prompt paths' shared rows (f16 products of the dequantized rows, as the reference's pf_dense_xh) against
@@ -25,9 +25,19 @@ def q8_0_matrix(rows, cols, seed, std=0.02):
     t = torch.from_numpy(orc.synth(rows * cols, seed, std)).cuda()
     g = torch.empty(rows * orc.row_bytes(orc.Q8_0, cols), dtype=torch.uint8, device="cuda")
     moe.quantize_weights(orc.Q8_0, t.view(rows, cols), g)
-    p = torch.empty_like(g)
-    moe.store_pack(orc.Q8_0, g, p, 1, rows, cols)
-    return g.cpu().numpy().reshape(rows, -1), p
+    return g.cpu().numpy().reshape(rows, -1), moe.Q8sMatrix.from_gguf(g, rows, cols)
+
+
+@pytest.mark.parametrize("rows,cols", [(32, 512), (96, 2048), (2048, 1024)])
+def test_q8s_split_planes(rows, cols):
+    """sfnx_q8s_split (src/model.cpp:384-440 q8split): the int8 plane holds each block's 32 values in row order, the
+    scale plane each block's f16 bits, [rows][cols / 32]; and the planes give the blocks back"""
+    g, W = q8_0_matrix(rows, cols, 17 + rows)
+    torch.cuda.synchronize()
+    blk = g.reshape(rows, cols // 32, 34)
+    assert np.array_equal(W.q.cpu().numpy().view(np.uint8), blk[:, :, 2:].reshape(rows, cols))
+    assert np.array_equal(W.d.cpu().numpy().view(np.uint16), blk[:, :, :2].copy().view(np.uint16).reshape(rows, cols // 32))
+    assert np.array_equal(W.to_gguf().cpu().numpy(), g.reshape(-1))
 
 
 @pytest.mark.parametrize("cols", [512, 2048, 4096])
@@ -209,8 +219,10 @@ def test_synthetic_q8s_layer():
     R = moe.MoeLayer.synthetic(moe.LayerShape(H=1024, E=64, K=6, ff=512, wtype=orc.Q8_0, shared=True), seed=31)
     Q = moe.MoeLayer.synthetic(moe.LayerShape(H=1024, E=64, K=6, ff=512, wtype=orc.Q4_K, shared=True), seed=31)
     assert L.W.shape == (s.E + 1, s.H) and torch.equal(L.W, Q.W)
-    assert torch.equal(L.sh_gu, R.gu_w[s.E * R.gu_stride:(s.E + 1) * R.gu_stride])
-    assert torch.equal(L.sh_dn, R.dn_w[s.E * R.dn_stride:(s.E + 1) * R.dn_stride])
+    rg, rd = torch.empty(R.gu_stride, dtype=torch.uint8, device="cuda"), torch.empty(R.dn_stride, dtype=torch.uint8, device="cuda")
+    moe.store_unpack(orc.Q8_0, R.gu_w[s.E * R.gu_stride:(s.E + 1) * R.gu_stride], rg, 1, 2 * s.ff, s.H)
+    moe.store_unpack(orc.Q8_0, R.dn_w[s.E * R.dn_stride:(s.E + 1) * R.dn_stride], rd, 1, s.H, s.ff)
+    assert torch.equal(L.sh_gu.to_gguf(), rg) and torch.equal(L.sh_dn.to_gguf(), rd)
     assert torch.equal(L.gu_w, Q.gu_w[: s.E * Q.gu_stride]) and torch.equal(L.dn_w, Q.dn_w[: s.E * Q.dn_stride])
     x = orc.synth(s.H, 990, 1.0).reshape(1, s.H)
     f = moe.FusedDecode([L], 1)
@@ -221,9 +233,7 @@ def test_synthetic_q8s_layer():
     dn = torch.empty_like(L.dn_w)
     moe.store_unpack(orc.Q4_K, L.gu_w, gu, s.E, 2 * s.ff, s.H)
     moe.store_unpack(orc.Q4_K, L.dn_w, dn, s.E, s.H, s.ff)
-    sg, sd = torch.empty_like(L.sh_gu), torch.empty_like(L.sh_dn)
-    moe.store_unpack(orc.Q8_0, L.sh_gu, sg, 1, 2 * s.ff, s.H)
-    moe.store_unpack(orc.Q8_0, L.sh_dn, sd, 1, s.H, s.ff)
+    sg, sd = L.sh_gu.to_gguf(), L.sh_dn.to_gguf()
     host = orc.LayerWeights(L.W.cpu().numpy(), gu.cpu().numpy(), dn.cpu().numpy(), s.wtype, s.H, s.E, s.K, s.ff, True,
                             sh_gu=sg.cpu().numpy(), sh_dn=sd.cpu().numpy())
     oy = orc.layer_decode(host, x)[0]
@@ -248,6 +258,15 @@ def test_pf_dense_against_float64(rows, cols, C):
     got = out.cpu().numpy()
     assert max_rel(got[:, :rows], want) < 2e-3
     assert (got[:, rows:] == 5.0).all()
+
+
+def test_pf_dense_refuses_a_small_staging_buffer():
+    _, W = q8_0_matrix(256, 512, 5)
+    xh = torch.zeros((4, 512), dtype=torch.float16, device="cuda")
+    out = torch.empty((4, 256), dtype=torch.float32, device="cuda")
+    wh = torch.empty(256 * 512 // 2, dtype=torch.float16, device="cuda")   # 256 KB, below 256 * 512 * 34 / 32 bytes
+    with pytest.raises(RuntimeError, match="wk smaller"):
+        moe.pf_dense(W, 256, 512, xh, out, 256, wh)
 
 
 def test_prefill_shared_graph_replays():

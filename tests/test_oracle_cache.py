@@ -24,9 +24,22 @@ def test_hand_worked_pool_of_five():
     assert st.slot_of[1] == -1 and st.slot_of[4] == -1 and st.slot_of[5] == 2 and st.slot_of[6] == 3
 
 
-def test_no_victim_is_reported():
+def test_no_victim_leaves_the_rest_on_host():
+    """three misses, two slots: the first two take the slots, the third finds every slot held by the window (five
+    32-lane steps, the hand back at slot 0) and stays on its host copy; the window's slots end at ref 1, so the next
+    window evicts as usual"""
     st = PoolState(n_layers=1, n_experts=10, n=2)
-    assert cache_plan(st, [0, 1, 2], 0) is None              # three misses, two slots
+    assert cache_plan(st, [0, 1, 2], 0) == [0, 1]
+    assert (st.owner, st.ref, st.hand, st.left) == ([0, 1], [1, 1], 0, 1)
+    assert st.slot_of[2] == -1
+    # every slot ref 1: the first step clears both and moves 32 on (slot 0); the second takes slot 0 (expert 0 out)
+    assert cache_plan(st, [2], 0) == [2]
+    assert (st.owner, st.ref, st.hand, st.left) == ([2, 1], [1, 0], 1, 0)
+    assert st.slot_of[0] == -1
+    # misses past the failing one in a later sweep group count too
+    st = PoolState(n_layers=1, n_experts=80, n=1)
+    assert cache_plan(st, list(range(40)), 0) == [0]
+    assert st.left == 39 and st.ref == [1]
 
 
 def clock_sequential(st: PoolState, jobs, layer):
