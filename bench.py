@@ -186,13 +186,33 @@ def main():
                      "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "algorithmic_bytes_per_launch": alg[dom]},
     }
+    # The same kernel's average from the committed rocprofv3 trace of the decode-only bench, taken on this build (its
+    # sources' hash recorded with it): over the timed graph replays, the regime the step time measures, and over the
+    # clocked eager passes.  When it describes this build, roofline.frac and achieved are the graph average's, the
+    # event clock's figure beside them; otherwise the event clock's, and the profile is reported as stale.
+    src = source_hash()
+    out["build_source"] = src
     rp = rocprof_avg(names[dom])
     if rp is not None:
-        # the same kernel's average from the committed rocprofv3 trace of the decode-only bench: over the same clocked
-        # eager passes, and over the timed graph replays (tracing adds its per-dispatch cost to both)
-        out["roofline"]["rocprof"] = {"source": "profiles/kernel_stats_decode48_q4k.md", "eager_avg_us": rp[0],
-                                      "graph_avg_us": rp[1], "frac_eager": round(alg[dom] / (rp[0] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                                      "frac_graph": round(alg[dom] / (rp[1] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        eager_us, graph_us, prof_src = rp
+        fresh = prof_src == src
+        out["roofline"]["rocprof"] = {"source": "profiles/kernel_stats_decode48_q4k.md", "profile_build": prof_src,
+                                      "matches_build": fresh, "eager_avg_us": eager_us, "graph_avg_us": graph_us,
+                                      "frac_eager": round(alg[dom] / (eager_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                                      "frac_graph": round(alg[dom] / (graph_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        out["roofline"]["frac_event"] = round(ach / HBM_PEAK_GBS, 4)
+        out["roofline"]["achieved_event"] = round(ach, 1)
+        if fresh:
+            ach = alg[dom] / (graph_us * 1e-6) / 1e9
+            out["roofline"]["achieved"] = round(ach, 1)
+            out["roofline"]["frac"] = round(ach / HBM_PEAK_GBS, 4)
+            out["roofline"]["timing"] = "rocprofv3 graph-replay average of this build (profiles/)"
+        else:
+            out["roofline"]["timing"] = "dispatch-stamped events (eager); the committed profile is of another build"
+    tr_src = traffic_source()
+    if traffic is not None and tr_src != src:
+        out["roofline"]["traffic_stale"] = {"bytes": traffic, "profile_build": tr_src}
+        out["roofline"]["traffic"] = None
     cb = copy_bandwidth(torch)
     out["hbm_copy_gbs"] = cb
     out["hbm_frac_of_copy"] = round(gbs / cb, 4)
@@ -238,37 +258,78 @@ DECODE_KERNELS = {"k_dec_router": "k_dec_router", "k_dec_experts1": "k_dec_exper
 CLOCK_REPS = 3   # the eager passes bench.py clocks each decode kernel over, after the timed graph replays
 
 
+def source_hash():
+    """a short hash of the library's sources (sfnx_amd/csrc, the headers): names the build a committed profile was
+    taken on, so the bench can tell whether it describes the build it runs"""
+    import hashlib
+    h = hashlib.sha256()
+    files = sorted(list((ROOT / "sfnx_amd" / "csrc").glob("*")) + list((ROOT / "include").glob("*.h")))
+    for f in files:
+        if f.is_file():
+            h.update(f.name.encode())
+            h.update(f.read_bytes())
+    return h.hexdigest()[:12]
+
+
 def trace_summary(path, NL):
     """rocprofv3's per-dispatch kernel trace of the decode-only bench, split by regime: the clocked eager passes are each
     decode kernel's last CLOCK_REPS x NL dispatches (they run after the timed loop), the rest are graph replays (plus
-    the warm pass).  Prints `rocprof <kernel> eager_avg_us E graph_avg_us G n_eager NE n_graph NG` lines."""
+    the warm pass).  Prints `rocprof <kernel> eager_avg_us E graph_avg_us G n_eager NE n_graph NG` lines, the build's
+    source hash, and, over the graph replays, the period of the router's dispatches (one a layer: the traced time a
+    layer takes) and how far each dispatch's start stamp precedes the previous decode dispatch's end stamp."""
     import csv
-    durs = {}
+    durs, seq = {}, []
     with open(path) as f:
         for r in csv.DictReader(f):
             name = DECODE_KERNELS.get(r["Kernel_Name"].split("(")[0])
             if name:
-                durs.setdefault(name, []).append((int(r["Start_Timestamp"]), int(r["End_Timestamp"])))
+                se = (int(r["Start_Timestamp"]), int(r["End_Timestamp"]))
+                durs.setdefault(name, []).append(se)
+                seq.append((se[0], se[1], name))
     ne = CLOCK_REPS * NL
+    print(f"rocprof-source {source_hash()}")
     for name, v in sorted(durs.items()):
         v.sort()
         d = [(e - s) / 1e3 for s, e in v]
         eager, graph = d[-ne:], d[:-ne]
         print(f"rocprof {name} eager_avg_us {sum(eager) / len(eager):.3f} graph_avg_us {sum(graph) / max(1, len(graph)):.3f} "
               f"n_eager {len(eager)} n_graph {len(graph)}")
+    seq.sort()
+    g = seq[: len(seq) - 3 * ne]   # the graph replays and the warm pass, in dispatch order
+    starts = [s for s, e, n in g if n == "k_dec_router"]
+    per = [(b - a) / 1e3 for a, b in zip(starts, starts[1:]) if (b - a) < 100e3]   # within a replay (no host gap)
+    ov = [(e0 - s1) / 1e3 for (s0, e0, _), (s1, e1, _) in zip(g, g[1:]) if s1 - e0 < 100e3]
+    if per and ov:
+        print(f"rocprof-graph layer_period_us {sum(per) / len(per):.3f} start_before_prev_end_us {sum(ov) / len(ov):.3f} "
+              f"n {len(per)}")
     return 0
 
 
 def rocprof_avg(kernel):
     """the committed rocprofv3 averages of a decode kernel (profiles/kernel_stats_decode48_q4k.md, lines written by
-    bench.py --trace-summary): (eager_avg_us, graph_avg_us) or None"""
+    bench.py --trace-summary): (eager_avg_us, graph_avg_us, source hash of the profiled build) or None"""
     p = ROOT / "profiles" / "kernel_stats_decode48_q4k.md"
+    if not p.exists():
+        return None
+    src, got = None, None
+    for line in p.read_text().splitlines():
+        f = line.split()
+        if len(f) == 2 and f[0] == "rocprof-source":
+            src = f[1]
+        if len(f) >= 6 and f[0] == "rocprof" and f[1] == kernel:
+            got = float(f[3]), float(f[5])
+    return None if got is None else (got[0], got[1], src)
+
+
+def traffic_source():
+    """the source hash of the build profiles/traffic.txt was measured on (its `source <hash>` line), or None"""
+    p = ROOT / "profiles" / "traffic.txt"
     if not p.exists():
         return None
     for line in p.read_text().splitlines():
         f = line.split()
-        if len(f) >= 6 and f[0] == "rocprof" and f[1] == kernel:
-            return float(f[3]), float(f[5])
+        if len(f) == 2 and f[0] == "source":
+            return f[1]
     return None
 
 

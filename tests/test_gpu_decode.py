@@ -169,3 +169,33 @@ def test_workspace_serves_shorter_windows():
         assert np.array_equal(bits(f.piece("logits", torch.float32, (T, shape.E + 1))), bits(b.logits))
         assert np.array_equal(bits(f.piece("y", torch.float32, (T, shape.H))), bits(yu))
         assert np.array_equal(bits(xf), bits(xu))
+
+
+def test_fused_chain_drift_against_oracle():
+    """config 1's chain, 12 of its stacked layers (x_{l+1} = x_l + MoE_l(rmsnorm(x_l)), each layer's weights seeded
+    on their own), through the fused decode against the oracle run layer by layer on the CPU: the last layer's
+    router indices equal the oracle's, and its output and the residual stream after 12 layers stay within 2e-3
+    (max relative error) of the oracle's chain.  The oracle's rmsnorm is float64 rounded to float32, so the two
+    chains' inputs may differ by an ulp from the second layer on: this bounds the drift, it is no bit comparison."""
+    shape = moe.LayerShape(H=2048, E=512, K=10, ff=512, wtype=orc.Q4_K, shared=True)
+    NL, eps = 12, 1e-6
+    layers, hosts = [], []
+    for l in range(NL):
+        L, h = make_layer(shape, 500 + l)
+        layers.append(L)
+        hosts.append(h)
+    x0 = orc.synth(shape.H, 4343, 1.0).reshape(1, shape.H)
+    f = moe.FusedDecode(layers, 1)
+    xf = torch.from_numpy(x0).cuda()
+    f(xf, norm=True, eps=eps)
+    torch.cuda.synchronize()
+    x = x0.astype(np.float32)
+    for h in hosts:
+        ss = np.sum(x.astype(np.float64) ** 2, axis=1)
+        r = (1.0 / np.sqrt(ss / shape.H + eps)).astype(np.float32)
+        xn = (x * r[:, None]).astype(np.float32)
+        oy, ol, oi, ow, ogu, opart = orc.layer_decode(h, xn, nthreads=8)
+        x = (x + oy).astype(np.float32)
+    assert np.array_equal(f.piece("topi", torch.int32, (1, shape.K)).cpu().numpy(), oi)
+    assert max_rel(f.piece("y", torch.float32, (1, shape.H)).cpu().numpy(), oy) < 2e-3
+    assert max_rel(xf.cpu().numpy(), x) < 2e-3

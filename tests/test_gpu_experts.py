@@ -66,6 +66,57 @@ def test_prefill_q8_layer(wtype):
     assert max_rel(y.cpu().numpy(), oy) < TOL
 
 
+def test_prefill_q8_bigjobs_config3():
+    """the q8 BigJob kernels (FNX_PF_MOE_Q8, src/moe.cuh:360-443) at config 3's shape: 2048 tokens, hidden 2048, 512
+    experts x FF 512, top-10 + shared, Zipf-skewed routing.  For 56 sampled pairs: 16 of the hottest expert's first and
+    16 of its last BigJob (it takes more than 64 rows), 8 of the shared expert's first job and 16 at random: every gate|up row
+    bit for bit against the oracle's dot of the same q8_1 activations, and every down row within 2e-3 (bit-equal on most)
+    of the oracle's dot of the kernel's own h (q8_1 of SwiGLU of its gate|up row)"""
+    shape = moe.LayerShape(H=2048, E=512, K=10, ff=512, wtype=orc.Q4_K, shared=True)
+    L, host = make_layer(shape, 3)
+    C, s = 2048, shape
+    rank = np.random.default_rng(7).permutation(512) + 1
+    bias = torch.from_numpy((0.125 * -1.1 * np.log(rank)).astype(np.float32)).cuda()
+    x = torch.from_numpy(orc.synth(C * s.H, 10, 1.0).reshape(C, s.H)).cuda()
+    b = moe.PrefillBuffers(s, C)
+    moe.quantize_q8_1(x, b.xq)
+    moe.prefill_route(L, x, b, bias)
+    moe.moe_gate_up_big(L.gu_w, L.gu_stride, s.wtype, s.H, 2 * s.ff, b.jobs_gu, b.njobs, b.cap, b.xq, b.gu)
+    moe.moe_down_big(L.dn_w, L.dn_stride, s.dn_type, s.ff, s.H, b.jobs_dn, b.njobs, b.cap, b.gu, b.part)
+    torch.cuda.synchronize()
+    from tests.gpu_util import job_array
+    jobs = job_array(b.jobs_gu, True)[: int(b.njobs[0])]
+    cnt = b.cnt.cpu().numpy()
+    hot = int(np.argmax(cnt))
+    assert cnt[hot] > 64
+    hj = [j for j in jobs if j["w"] == hot]
+    sj = [j for j in jobs if j["w"] == s.E]
+    assert len(hj) >= 2
+    pairs = set(hj[0]["out"][:16].tolist()) | set(hj[-1]["out"][max(0, hj[-1]["n"] - 16): hj[-1]["n"]].tolist())
+    pairs |= set(sj[0]["out"][:8].tolist())
+    pairs |= set(np.random.default_rng(11).integers(0, C * s.K, 16).tolist())
+    P = C * s.K
+    topi = b.topi.cpu().numpy().reshape(-1)
+    xq = b.xq.cpu().numpy().reshape(C, -1)
+    gu, part = b.gu.cpu().numpy(), b.part.cpu().numpy()
+    rb_g, rb_d = orc.row_bytes(s.wtype, s.H), orc.row_bytes(s.dn_type, s.ff)
+    eq = tot = 0
+    err = 0.0
+    for p in sorted(pairs):
+        e, t = (int(topi[p]), p // s.K) if p < P else (s.E, p - P)
+        gw = host.gu_w[e * host.gu_stride:(e + 1) * host.gu_stride].reshape(2 * s.ff, rb_g)
+        want = np.array([orc.dot(s.wtype, gw[r], xq[t], s.H) for r in range(2 * s.ff)], np.float32)
+        assert np.array_equal(gu[p].view(np.uint32), want.view(np.uint32)), f"pair {p} (expert {e})"
+        hq = orc.swiglu_q8_1(gu[p], s.ff)
+        dw = host.dn_w[e * host.dn_stride:(e + 1) * host.dn_stride].reshape(s.H, rb_d)
+        wd = np.array([orc.dot(s.dn_type, dw[r], hq, s.ff) for r in range(s.H)], np.float32)
+        err = max(err, max_rel(part[p], wd))
+        eq += int(np.sum(part[p] == wd))
+        tot += s.H
+    assert err < TOL, err
+    assert eq / tot > 0.5, eq / tot
+
+
 @pytest.mark.parametrize("wtype", [orc.Q4_K, orc.Q5_K, orc.Q4_0, orc.Q5_1, orc.Q8_0])
 def test_decode_layer_baseline_shapes(wtype):
     """The benchmark layer shape (configs 0/1/4): hidden 2048, 512 experts x FF 512, top-10 + shared, one token and a 16-row window"""

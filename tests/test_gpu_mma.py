@@ -204,12 +204,31 @@ def test_verify_window_whole_layer():
         assert np.abs(yo[t] - want[t]).max() <= 2e-3 * np.abs(want[t]).max(), t
 
 
-def test_q8_0_prefill_4096_sampled():
-    """config 4's prompt chunk: 4096 tokens through Q8_0 experts on the matrix cores, sampled pairs"""
+def test_q8_0_prefill_4096():
+    """config 4's prompt chunk as the bench runs it: 4096 tokens through Q8_0 experts on the matrix cores with the
+    bench's Zipf-skewed routing.  The router logits bit for bit and the top-k and BigJobs exactly against the oracle on
+    the biased logits; 400 sampled (pair, gate|up row set) and (pair, down row set) products within 2e-3 of float64;
+    the whole layer (fused gate|up + SwiGLU, down, combine) for 64 tokens within 2e-3 of its float64 restatement"""
     shape = moe.LayerShape(H=2048, E=512, K=10, ff=512, wtype=orc.Q8_0, shared=True)
-    L, host, x, y, b = run_prefill(shape, 23, 4096)
-    eg, ed = check_sampled(host, x, b, 16, np.random.default_rng(3))
+    rank = np.random.default_rng(7).permutation(512) + 1
+    bias = (0.125 * -1.1 * np.log(rank)).astype(np.float32)
+    C = 4096
+    L, host, x, y, b = run_prefill(shape, 23, C, bias=bias)
+    assert int(b.cnt.max()) > 300   # the skew's hottest experts take several 64-row jobs
+    lg = orc.router_logits_prompt(host.W, x)
+    lg[:, : shape.E] += bias
+    assert np.array_equal(b.logits.cpu().numpy().view(np.uint32), lg.view(np.uint32))
+    oi, ow = check_prompt_routing(b, lg, shape)
+    eg, ed = check_sampled(host, x, b, 400, np.random.default_rng(3))
     assert eg < 2e-3 and ed < 2e-3, (eg, ed)
+    xd = torch.from_numpy(x).cuda()
+    yl = torch.empty_like(xd)
+    b2 = moe.PrefillBuffers(shape, C)
+    moe.prefill_layer_mma(L, xd, yl, b2, torch.from_numpy(bias).cuda())
+    torch.cuda.synchronize()
+    rows = list(np.random.default_rng(6).choice(C, 64, replace=False))
+    want = layer_rows_f64(host, shape, f16_of(x), lg, oi, ow, rows)
+    assert max_rel(yl.cpu().numpy()[rows], want) < 2e-3
 
 
 @pytest.mark.parametrize("wtype, dn_type", [(orc.Q4_K, orc.Q5_K), (orc.Q4_0, orc.Q8_0)])
