@@ -221,8 +221,11 @@ int sfnx_moe_decode2(const sfnx_moe_layer_w* layers, int n_layers, uint32_t gu_t
  * serving loops, harnesses that forbid hipMalloc).  The workspace is the library's own file-scope device array of
  * 4 MiB, one per GPU, held until the process ends; the call allocates nothing and refuses a shape whose workspace
  * (sfnx_moe_decode_workspace) is larger.  Every call on one GPU shares that array, and the array keeps the last call's
- * routing and intermediates (nothing in it needs to start at zero): calls that overlap on one GPU (several streams,
- * several host threads) race.  Same arguments and values as sfnx_moe_decode2 without ws / ws_bytes / phases. */
+ * routing and intermediates (nothing in it needs to start at zero).  Calls that overlap on one GPU would race on it:
+ * a call on another stream than the previous (uncaptured) call's is refused ("a call on another stream still runs")
+ * while that call has not finished; calls on one stream are ordered by it.  Under HIP graph capture the check is the
+ * caller's: captured calls run at replay.  Same arguments and values as sfnx_moe_decode2 without ws / ws_bytes /
+ * phases. */
 int sfnx_moe_decode_noalloc(const sfnx_moe_layer_w* layers, int n_layers, uint32_t gu_type, uint32_t dn_type, int H, int E,
                             int K, int ff, int shared, float* x, int T, int norm, float eps, void* st);
 

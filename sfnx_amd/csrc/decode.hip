@@ -839,16 +839,23 @@ constexpr size_t NOALLOC_BYTES = 4u << 20;
 __device__ __align__(256) unsigned char scratch[NOALLOC_BYTES];
 constexpr int NOALLOC_DEVS = 64;
 void* g_scratch[NOALLOC_DEVS] = {};
+// the guard against calls that overlap on one GPU: an event recorded after each (uncaptured) call, and its stream
+hipEvent_t g_done[NOALLOC_DEVS] = {};
+hipStream_t g_last[NOALLOC_DEVS] = {};
+bool g_used[NOALLOC_DEVS] = {};
 std::mutex g_scratch_mu;
-void* scratch_of_device() {
+int device_index() {
     int dev = 0;
     check(hipGetDevice(&dev), "hipGetDevice");
     require(dev >= 0 && dev < NOALLOC_DEVS, "device index past the library's table");
-    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    return dev;
+}
+void* scratch_of_device(int dev) {
     if (!g_scratch[dev]) {
         void* p = nullptr;
         check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress (decode scratch)");
         g_scratch[dev] = p;
+        check(hipEventCreateWithFlags(&g_done[dev], hipEventDisableTiming), "hipEventCreateWithFlags (decode scratch)");
     }
     return g_scratch[dev];
 }
@@ -860,7 +867,27 @@ extern "C" int sfnx_moe_decode_noalloc(const sfnx_moe_layer_w* layers, int n_lay
     return guarded("sfnx_moe_decode_noalloc", [&] {
         const DecLayout L = dec_layout(H, E, K, ff);
         require(L.total <= NOALLOC_BYTES, "shape needs a decode workspace larger than the library's 4 MiB scratch");
-        moe_decode(layers, nullptr, n_layers, gu_type, dn_type, H, E, K, ff, shared, x, T, norm, eps, scratch_of_device(),
-                   NOALLOC_BYTES, 0, st);
+        // Every call on a GPU shares the one scratch array.  A call on another stream than the last uncaptured call's
+        // is refused while that call still runs (the two would race on the array); calls on one stream are ordered by
+        // the stream.  Under graph capture the check is left to the caller (the captured work runs at replay).
+        hipStream_t s = stream_of(st);
+        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+        check(hipStreamIsCapturing(s, &cap), "hipStreamIsCapturing");
+        const bool captured = cap != hipStreamCaptureStatusNone;
+        std::lock_guard<std::mutex> lk(g_scratch_mu);
+        const int dev = device_index();
+        void* ws = scratch_of_device(dev);
+        if (!captured && g_used[dev] && g_last[dev] != s) {
+            const hipError_t q = hipEventQuery(g_done[dev]);
+            if (q == hipErrorNotReady)
+                throw std::runtime_error("a call on another stream still runs on this GPU's scratch array (calls that overlap on one GPU race)");
+            if (q != hipSuccess) check(q, "hipEventQuery");
+        }
+        moe_decode(layers, nullptr, n_layers, gu_type, dn_type, H, E, K, ff, shared, x, T, norm, eps, ws, NOALLOC_BYTES, 0, st);
+        if (!captured) {
+            check(hipEventRecord(g_done[dev], s), "hipEventRecord");
+            g_last[dev] = s;
+            g_used[dev] = true;
+        }
     });
 }

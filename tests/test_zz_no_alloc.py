@@ -48,3 +48,31 @@ def test_noalloc_refuses_bad_arguments():
     layers = [moe.MoeLayer.synthetic(shape, seed=800)]
     with pytest.raises(RuntimeError, match="T out of range"):
         noalloc(layers, torch.zeros((17, 1024), dtype=torch.float32, device="cuda"))
+
+
+def test_noalloc_refuses_a_call_that_overlaps_another_streams():
+    """two streams on one GPU share the scratch array: a call on stream B while stream A's call is still queued behind
+    long work is refused with a clear error (instead of racing on the array); once A's call has finished, B's runs and
+    equals the workspace path"""
+    shape = moe.LayerShape(H=1024, E=64, K=6, ff=512, wtype=orc.Q4_K, shared=True)
+    layers = [moe.MoeLayer.synthetic(shape, seed=900)]
+    x0 = torch.from_numpy(orc.synth(2 * shape.H, 901, 1.0).reshape(2, shape.H)).cuda()
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    m = torch.randn(4096, 4096, device="cuda")
+    torch.cuda.synchronize()
+    xa, xb = x0.clone(), x0.clone()
+    with torch.cuda.stream(sa):
+        for _ in range(40):   # ~tens of ms of work ahead of A's call
+            m = m @ m * 1e-3
+        noalloc(layers, xa)
+    with torch.cuda.stream(sb):
+        with pytest.raises(RuntimeError, match="another stream still runs"):
+            noalloc(layers, xb)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(sb):
+        noalloc(layers, xb)
+    xw = x0.clone()
+    with_workspace(layers, xw)
+    torch.cuda.synchronize()
+    assert np.array_equal(xa.cpu().numpy().view(np.uint32), xw.cpu().numpy().view(np.uint32))
+    assert np.array_equal(xb.cpu().numpy().view(np.uint32), xw.cpu().numpy().view(np.uint32))
