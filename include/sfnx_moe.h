@@ -365,6 +365,13 @@ int sfnx_host_free(void* host);
  * their slots, and status[0] receives the count (the reference's plan would spin).  Every slot the window holds ends
  * at ref 1 either way. */
 int sfnx_cache_plan(const sfnx_job* jobs, const int* njobs, int layer, const sfnx_expert_cache* ec, int* list, void* st);
+/* src/kernels.hpp:269-278 router_route with an ExpertCache (src/moe.cuh:128-198): sfnx_router_route, and then, in
+ * the same launch, its last block's first wavefront plans the window's slots for `layer` as sfnx_cache_plan does (the
+ * same slots, list, tables, refs, hand and status), so a cached layer's plan takes no launch of its own.  With shared
+ * != 0 the shared job (expert E) is planned like the others, so the cache's tables need E + 1 experts a layer. */
+int sfnx_router_route_plan(const float* W, const float* x, float* logits, int T, int H, int E, int K, int* topi,
+                           float* topw, sfnx_job* jobs_gu, sfnx_job* jobs_dn, int* njobs, int shared,
+                           const sfnx_expert_cache* ec, int layer, int* list, void* st);
 /* src/kernels.cu:1642-1658 k_cache_copy / cache_copy: the listed experts' matrices from their host copies into their
  * slots of pool p */
 int sfnx_cache_copy(const sfnx_expert_cache* ec, int p, const int* list, void* st);

@@ -74,6 +74,7 @@ SIGNATURES = {
     "sfnx_host_alloc": (i32, [sz, vp, vp]),
     "sfnx_host_free": (i32, [vp]),
     "sfnx_cache_plan": (i32, [vp, vp, i32, vp, vp, vp]),
+    "sfnx_router_route_plan": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, vp, vp, i32, vp, i32, vp, vp]),
     "sfnx_cache_copy": (i32, [vp, i32, vp, vp]),
     "sfnx_moe_cache": (i32, [i32, sz, sz, vp, vp, vp, vp, vp]),
 }

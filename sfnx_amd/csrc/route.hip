@@ -1,5 +1,6 @@
 // Activations and routing: q8_1 quantization, the decode router (logits, top-k, jobs in one launch), the prompt path's
 // router logits and permutation, and the weighted combine.
+#include "cache.hpp"
 #include "topk.hpp"
 
 namespace sfnx {
@@ -47,13 +48,13 @@ __device__ __forceinline__ float row_dot(const float4 (&wv)[NC], const float* __
 
 constexpr int RR_THREADS = 256, RR_WAVES = RR_THREADS / WAVE;
 // src/moe.cuh:73-202 k_router_route: the router's rows a wavefront each, the shared gate row E included; the last
-// block to finish takes the top-K of every token and builds the jobs (first-pick order, rows in pair order)
+// block to finish takes the top-K of every token and builds the jobs (first-pick order, rows in pair order).  Returns
+// the job count in the last block, -1 in the others.
 template <int NC, int TT>
-__global__ void __launch_bounds__(RR_THREADS) k_router_route(const float* __restrict__ W, const float* __restrict__ x,
-                                                            float* __restrict__ logits, int T, int E, int K,
-                                                            int* __restrict__ topi, float* __restrict__ topw,
-                                                            sfnx_job* __restrict__ gu, sfnx_job* __restrict__ dn,
-                                                            int* __restrict__ njobs, int shared) {
+__device__ __forceinline__ int router_route_body(const float* __restrict__ W, const float* __restrict__ x,
+                                                 float* __restrict__ logits, int T, int E, int K, int* __restrict__ topi,
+                                                 float* __restrict__ topw, sfnx_job* __restrict__ gu,
+                                                 sfnx_job* __restrict__ dn, int* __restrict__ njobs, int shared) {
     constexpr int H = NC * 4 * WAVE;
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE, L = E + 1;
     const int row = blockIdx.x * RR_WAVES + wave;
@@ -72,7 +73,7 @@ __global__ void __launch_bounds__(RR_THREADS) k_router_route(const float* __rest
     __syncthreads();
     if (threadIdx.x == 0) last = atomicAdd(njobs + 1, 1) == (int) gridDim.x - 1;
     __syncthreads();
-    if (!last) return;
+    if (!last) return -1;
     __threadfence();
     __shared__ int ex[MAX_P];
     for (int t = wave; t < T; t += RR_WAVES) {
@@ -117,6 +118,33 @@ __global__ void __launch_bounds__(RR_THREADS) k_router_route(const float* __rest
         njobs[0] = nj + (shared ? 1 : 0);
         njobs[1] = 0;
     }
+    return nj + (shared ? 1 : 0);
+}
+
+template <int NC, int TT>
+__global__ void __launch_bounds__(RR_THREADS) k_router_route(const float* __restrict__ W, const float* __restrict__ x,
+                                                            float* __restrict__ logits, int T, int E, int K,
+                                                            int* __restrict__ topi, float* __restrict__ topw,
+                                                            sfnx_job* __restrict__ gu, sfnx_job* __restrict__ dn,
+                                                            int* __restrict__ njobs, int shared) {
+    router_route_body<NC, TT>(W, x, logits, T, E, K, topi, topw, gu, dn, njobs, shared);
+}
+
+// The same with an expert cache: the last block's first wavefront then plans the window's slots for `layer`
+// (src/moe.cuh:128-198: the reference's router plans in its last block too), once the block's jobs are written, so a
+// cached layer takes no launch of its own for the plan.
+template <int NC, int TT>
+__global__ void __launch_bounds__(RR_THREADS) k_router_route_plan(const float* __restrict__ W, const float* __restrict__ x,
+                                                                 float* __restrict__ logits, int T, int E, int K,
+                                                                 int* __restrict__ topi, float* __restrict__ topw,
+                                                                 sfnx_job* __restrict__ gu, sfnx_job* __restrict__ dn,
+                                                                 int* __restrict__ njobs, int shared,
+                                                                 sfnx_expert_cache ec, int layer, int* __restrict__ list) {
+    const int nj = router_route_body<NC, TT>(W, x, logits, T, E, K, topi, topw, gu, dn, njobs, shared);
+    if (nj < 0) return;
+    __syncthreads();   // every job of the block written
+    if (threadIdx.x >= WAVE) return;
+    plan_window(gu, nj, layer, ec, list, threadIdx.x, WaveSync{});
 }
 
 // The xor butterfly of group_sum<64> applied to NV partial sums a lane at once, by recursive halving: at the level of
@@ -566,6 +594,21 @@ void launch_router_tt(int nc, dim3 g, hipStream_t s, const float* W, const float
     }
 }
 
+template <int TT>
+void launch_router_plan_tt(int nc, dim3 g, hipStream_t s, const float* W, const float* x, float* logits, int T, int E,
+                           int K, int* topi, float* topw, sfnx_job* gu, sfnx_job* dn, int* njobs, int shared,
+                           const sfnx_expert_cache& ec, int layer, int* list) {
+#define SFNX_RRP(NCV) k_router_route_plan<NCV, TT><<<g, RR_THREADS, 0, s>>>(W, x, logits, T, E, K, topi, topw, gu, dn, njobs, shared, ec, layer, list)
+    switch (nc) {
+        case 4: SFNX_RRP(4); break;
+        case 8: SFNX_RRP(8); break;
+        case 10: SFNX_RRP(10); break;
+        case 16: SFNX_RRP(16); break;
+        default: throw std::runtime_error("hidden size must be 1024, 2048, 2560 or 4096");
+    }
+#undef SFNX_RRP
+}
+
 }  // namespace
 }  // namespace sfnx
 
@@ -593,6 +636,27 @@ extern "C" int sfnx_router_route(const float* W, const float* x, float* logits, 
         if (T == 1) launch_router_tt<1>(nc, g, s, W, x, logits, T, E, K, topi, topw, jobs_gu, jobs_dn, njobs, shared);
         else if (T <= 4) launch_router_tt<4>(nc, g, s, W, x, logits, T, E, K, topi, topw, jobs_gu, jobs_dn, njobs, shared);
         else launch_router_tt<16>(nc, g, s, W, x, logits, T, E, K, topi, topw, jobs_gu, jobs_dn, njobs, shared);
+    });
+}
+
+extern "C" int sfnx_router_route_plan(const float* W, const float* x, float* logits, int T, int H, int E, int K, int* topi,
+                                      float* topw, sfnx_job* jobs_gu, sfnx_job* jobs_dn, int* njobs, int shared,
+                                      const sfnx_expert_cache* ec, int layer, int* list, void* st) {
+    return guarded("sfnx_router_route_plan", [&] {
+        require(T >= 1 && T <= SFNX_MAXT, "T out of range (1..16)");
+        require(E >= WAVE && E % WAVE == 0 && E <= MAX_E, "E must be a multiple of 64, at most 1024");
+        require(K >= 1 && K <= MAX_K && K <= E, "K out of range (1..16)");
+        require(H % 256 == 0, "H must be a multiple of 256");
+        require(list != nullptr, "null list");
+        check_cache(ec);
+        check_layer(ec, layer);
+        require(E + (shared ? 1 : 0) <= ec->n_experts, "the layer's experts (and its shared expert) pass the cache's tables");
+        const dim3 g((E + 1 + RR_WAVES - 1) / RR_WAVES);
+        const int nc = H / 256;
+        hipStream_t s = stream_of(st);
+        if (T == 1) launch_router_plan_tt<1>(nc, g, s, W, x, logits, T, E, K, topi, topw, jobs_gu, jobs_dn, njobs, shared, *ec, layer, list);
+        else if (T <= 4) launch_router_plan_tt<4>(nc, g, s, W, x, logits, T, E, K, topi, topw, jobs_gu, jobs_dn, njobs, shared, *ec, layer, list);
+        else launch_router_plan_tt<16>(nc, g, s, W, x, logits, T, E, K, topi, topw, jobs_gu, jobs_dn, njobs, shared, *ec, layer, list);
     });
 }
 

@@ -134,9 +134,9 @@ inline void router_route(const float* W, const float* x, float* logits, int T, i
                          float* sh_out = nullptr) {
     const MoeShape& s = model_shape();
     if (ec && (layer < 0 || !list)) throw std::runtime_error("router_route: a cache plan needs its layer and list");
-    ck(sfnx_router_route(W, x, logits, T, s.H, s.E, s.K, topi, topw, jobs_gu, jobs_dn, njobs, 0, st));
-    // the reference plans in the router launch's last block; here the plan is the next launch on the stream
-    if (ec) ck(sfnx_cache_plan(jobs_gu, njobs, layer, ec, list, st));
+    // with a cache, the router launch's last block plans the window's slots, as the reference's does
+    if (ec) ck(sfnx_router_route_plan(W, x, logits, T, s.H, s.E, s.K, topi, topw, jobs_gu, jobs_dn, njobs, 0, ec, layer, list, st));
+    else ck(sfnx_router_route(W, x, logits, T, s.H, s.E, s.K, topi, topw, jobs_gu, jobs_dn, njobs, 0, st));
     if (sh_gu) ck(sfnx_q8s_gemv(sh_gu, sh_rows, s.H, sh_y, sh_out, sh_rows, T, st));
 }
 // src/kernels.cu:1655-1668 cache_copy / moe_cache: the planned experts into their slots (moe_cache plans first when

@@ -59,10 +59,19 @@ def quantize_q8_1(x: torch.Tensor, q: torch.Tensor) -> None:
     check(lib().sfnx_quantize_q8_1(_p(x), _p(q), n, rows, _st()))
 
 
-def router_route(W, x, logits, topi, topw, jobs_gu, jobs_dn, njobs, E: int, K: int, shared: bool = True) -> None:
+def router_route(W, x, logits, topi, topw, jobs_gu, jobs_dn, njobs, E: int, K: int, shared: bool = True,
+                 plan=None) -> None:
+    """src/kernels.hpp:269-278 router_route; plan = (cache, layer, list): the same launch's last block also plans the
+    window's slots in the ExpertCache (sfnx_router_route_plan)"""
     T, H = x.shape
-    check(lib().sfnx_router_route(_p(W), _p(x), _p(logits), T, H, E, K, _p(topi), _p(topw), _p(jobs_gu), _p(jobs_dn),
-                                  _p(njobs), int(shared), _st()))
+    if plan is None:
+        check(lib().sfnx_router_route(_p(W), _p(x), _p(logits), T, H, E, K, _p(topi), _p(topw), _p(jobs_gu),
+                                      _p(jobs_dn), _p(njobs), int(shared), _st()))
+    else:
+        cache, layer, out_list = plan
+        check(lib().sfnx_router_route_plan(_p(W), _p(x), _p(logits), T, H, E, K, _p(topi), _p(topw), _p(jobs_gu),
+                                           _p(jobs_dn), _p(njobs), int(shared), C.byref(cache.c), layer, _p(out_list),
+                                           _st()))
 
 
 def router_logits(W, x, logits) -> None:
@@ -695,15 +704,23 @@ class ExpertCache:
             pass
 
 
-def decode_layer_cached(cache: ExpertCache, l: int, x: torch.Tensor, y: torch.Tensor, b: DecodeBuffers, out_list) -> None:
-    """decode_layer with the layer's experts behind the expert cache (src/engine.cu:947-971): the routing, the window's
-    slots planned and the planned experts copied in (moe_cache), then the expert calls through the layer's tables"""
+def decode_layer_cached(cache: ExpertCache, l: int, x: torch.Tensor, y: torch.Tensor, b: DecodeBuffers, out_list,
+                        plan_in_router: bool = True) -> None:
+    """decode_layer with the layer's experts behind the expert cache (src/engine.cu:947-971): the routing with the
+    window's slots planned in its last block (or, plan_in_router=False, the plan as a launch of its own), the planned
+    experts copied in (moe_cache), then the expert calls through the layer's tables"""
     V = cache.layer_view(l)
     s = V.s
     T = x.shape[0]
     quantize_q8_1(x, b.xq)
-    router_route(V.W, x, b.logits, b.topi, b.topw, b.jobs_gu, b.jobs_dn, b.njobs, s.E, s.K, s.shared and not s.sh_q8s)
-    cache.moe_cache(l, out_list, b.jobs_gu, b.njobs)
+    shared = s.shared and not s.sh_q8s
+    if plan_in_router:
+        router_route(V.W, x, b.logits, b.topi, b.topw, b.jobs_gu, b.jobs_dn, b.njobs, s.E, s.K, shared,
+                     plan=(cache, l, out_list))
+        cache.moe_cache(l, out_list)
+    else:
+        router_route(V.W, x, b.logits, b.topi, b.topw, b.jobs_gu, b.jobs_dn, b.njobs, s.E, s.K, shared)
+        cache.moe_cache(l, out_list, b.jobs_gu, b.njobs)
     moe_gate_up(V.gu_w, 0, s.wtype, s.H, 2 * s.ff, b.jobs_gu, b.njobs, b.njobs_max, T, b.xq, b.gu)
     moe_down(V.dn_w, 0, s.dn_type, s.ff, s.H, b.jobs_dn, b.njobs, b.njobs_max, T, b.gu, b.part)
     if s.sh_q8s:

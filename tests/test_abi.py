@@ -35,6 +35,10 @@ _Q8S_PTR = C.addressof(_Q8S)
     (lambda L: L.sfnx_router_route(None, None, None, 17, 2048, 512, 10, None, None, None, None, None, 1, None), "T out of range"),
     (lambda L: L.sfnx_router_route(None, None, None, 1, 2048, 500, 10, None, None, None, None, None, 1, None), "E must be"),
     (lambda L: L.sfnx_router_route(None, None, None, 1, 2048, 512, 17, None, None, None, None, None, 1, None), "K out of range"),
+    (lambda L: L.sfnx_router_route_plan(None, None, None, 1, 2048, 512, 10, None, None, None, None, None, 0, None, 0, None,
+                                        None), "null list"),
+    (lambda L: L.sfnx_router_route_plan(None, None, None, 1, 2048, 512, 10, None, None, None, None, None, 0, None, 0,
+                                        C.c_void_p(8), None), "null expert cache"),
     (lambda L: L.sfnx_moe_gate_up(None, 1 << 30, 5, 2048, 1024, None, None, 11, 1, None, None, None), "Q4_K (12) or Q5_K (13)"),
     (lambda L: L.sfnx_moe_gate_up(None, 1 << 30, 12, 2000, 1024, None, None, 11, 1, None, None, None), "multiple of 512"),
     (lambda L: L.sfnx_moe_gate_up(None, 1000, 12, 2048, 1024, None, None, 11, 1, None, None, None), "stride smaller"),
@@ -97,3 +101,16 @@ def test_expert_cache_struct_layout_matches_the_header(tmp_path):
     out = [int(v) for v in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()]
     assert out[0] == C.sizeof(_abi.ExpertCacheC)
     assert out[1:] == [getattr(_abi.ExpertCacheC, f).offset for f in fields]
+
+
+def test_router_plan_refuses_tables_without_the_shared_expert():
+    """a cache whose tables hold only the E routed experts a layer cannot plan a window with the shared job (expert E);
+    refused on the host, before any launch"""
+    c = _abi.ExpertCacheC()
+    c.n_slots, c.n_pools, c.n_layers, c.n_experts = 8, 1, 1, 64
+    c.s0[0], c.n[0], c.slot_bytes[0], c.dn_off[0], c.pool[0] = 0, 8, 32, 16, 16
+    c.ep_gu = c.ep_dn = c.host_gu = c.host_dn = c.slot_of = c.owner = c.ref = c.hand = 16
+    L = _abi.lib()
+    args = (None, None, None, 1, 1024, 64, 6, None, None, None, None, None)
+    assert L.sfnx_router_route_plan(*args, 1, C.byref(c), 0, C.c_void_p(16), None) != 0
+    assert "pass the cache's tables" in L.sfnx_last_error().decode()

@@ -1,5 +1,6 @@
 """The expert cache (src/moe.cuh:19-71, src/kernels.cu:1636-1668): routed experts in page-locked host memory, VRAM
-slots planned per decode window by one wavefront (CLOCK) and filled by the copy kernel.  Each window through the cached
+slots planned per decode window by one wavefront (CLOCK), in the router launch's last block as the reference's
+(src/moe.cuh:128-198) or as a launch of its own, and filled by the copy kernel.  Each window through the cached
 layer gives the same bits as the resident layer, and the device's plan (slots, owners, refs, hand, list) equals the
 CPU restatement's (oracle/cache.py) window after window, for a pool larger and one smaller than the 32-lane sweep."""
 import numpy as np
@@ -18,8 +19,9 @@ def bits(t):
     return t.detach().cpu().numpy().view(np.uint32)
 
 
+@pytest.mark.parametrize("plan_in_router", [True, False])
 @pytest.mark.parametrize("n_slots", [40, 24])
-def test_cached_decode_windows(n_slots):
+def test_cached_decode_windows(n_slots, plan_in_router):
     shape = moe.LayerShape(H=1024, E=64, K=6, ff=512, wtype=orc.Q4_K, shared=True)
     layers = [make_layer(shape, 90 + l)[0] for l in range(2)]
     cache = moe.ExpertCache(layers, n_slots)
@@ -35,9 +37,10 @@ def test_cached_decode_windows(n_slots):
             b0, b1 = moe.DecodeBuffers(shape, T), moe.DecodeBuffers(shape, T)
             y0, y1 = torch.empty_like(x), torch.empty_like(x)
             moe.decode_layer(layers[l], x, y0, b0)
-            moe.decode_layer_cached(cache, l, x, y1, b1, lst)
+            moe.decode_layer_cached(cache, l, x, y1, b1, lst, plan_in_router)
             torch.cuda.synchronize()
             assert np.array_equal(bits(y0), bits(y1)), f"window {w}"
+            assert int(b1.njobs[1]) == 0   # the router's block counter left at zero
             nj = int(b1.njobs[0])
             jobs = [int(v) for v in job_array(b1.jobs_gu)[:nj]["w"]]
             taken = cache_plan(st, jobs, l)
@@ -58,7 +61,8 @@ def test_cached_decode_windows(n_slots):
         cache.close()
 
 
-def test_pool_too_small_leaves_misses_on_host():
+@pytest.mark.parametrize("plan_in_router", [True, False])
+def test_pool_too_small_leaves_misses_on_host(plan_in_router):
     """a window of 3 rows (more distinct experts than the pool's 12 slots) through the cache: the first 12 misses take
     the slots and are copied in, the others stay on their host copies (status[0]); the layer through the tables still
     equals the resident layer bit for bit, every table entry points at a slot holding that expert's bytes or at the
@@ -77,7 +81,7 @@ def test_pool_too_small_leaves_misses_on_host():
             b0, b1 = moe.DecodeBuffers(shape, T), moe.DecodeBuffers(shape, T)
             y0, y1 = torch.empty_like(x), torch.empty_like(x)
             moe.decode_layer(layers[0], x, y0, b0)
-            moe.decode_layer_cached(cache, 0, x, y1, b1, lst)
+            moe.decode_layer_cached(cache, 0, x, y1, b1, lst, plan_in_router)
             torch.cuda.synchronize()
             assert np.array_equal(bits(y0), bits(y1)), f"window {w}"
             nj = int(b1.njobs[0])
@@ -121,3 +125,4 @@ def test_moe_cache_refuses_a_layer_of_another_size():
                                                None, None, moe._st()))
     finally:
         cache.close()
+
