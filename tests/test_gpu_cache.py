@@ -126,3 +126,38 @@ def test_moe_cache_refuses_a_layer_of_another_size():
     finally:
         cache.close()
 
+
+
+@pytest.mark.parametrize("plan_in_router", [True, False])
+def test_cached_full_windows(plan_in_router):
+    """16-row windows (the most a window holds: up to 97 jobs, several 32-job sweep groups a plan) over two layers
+    through a 90-slot pool: outputs equal the resident layers' bit for bit, the plan equals the restatement's"""
+    shape = moe.LayerShape(H=1024, E=64, K=6, ff=512, wtype=orc.Q4_K, shared=True)
+    layers = [make_layer(shape, 120 + l)[0] for l in range(2)]
+    cache = moe.ExpertCache(layers, 90)
+    st = PoolState(len(layers), cache.n_experts, 90)
+    lst = torch.zeros(1 + 16 * shape.K + 16, dtype=torch.int32, device="cuda")
+    T = 16
+    try:
+        for w in range(6):
+            l = w % 2
+            x = torch.from_numpy(orc.synth(T * shape.H, 1200 + w, 1.0).reshape(T, shape.H)).cuda()
+            b0, b1 = moe.DecodeBuffers(shape, T), moe.DecodeBuffers(shape, T)
+            y0, y1 = torch.empty_like(x), torch.empty_like(x)
+            moe.decode_layer(layers[l], x, y0, b0)
+            moe.decode_layer_cached(cache, l, x, y1, b1, lst, plan_in_router)
+            torch.cuda.synchronize()
+            assert np.array_equal(bits(y0), bits(y1)), f"window {w}"
+            nj = int(b1.njobs[0])
+            assert nj > 32   # more than one sweep group
+            jobs = [int(v) for v in job_array(b1.jobs_gu)[:nj]["w"]]
+            taken = cache_plan(st, jobs, l)
+            got = lst.cpu().numpy()
+            assert got[0] == len(taken) and list(got[1:1 + len(taken)]) == taken, f"window {w}"
+            assert cache.host_misses()[0] == st.left == 0
+            assert cache.slot_of.cpu().tolist() == st.slot_of
+            assert cache.owner.cpu().tolist() == st.owner
+            assert cache.ref.cpu().tolist() == st.ref
+            assert int(cache.hand[0]) == st.hand
+    finally:
+        cache.close()
