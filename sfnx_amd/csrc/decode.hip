@@ -173,12 +173,15 @@ __global__ void __launch_bounds__(2 * d2_threads<TYPE>()) k_dec_experts(
     const sfnx_job* __restrict__ jg, const int* __restrict__ njobs_g, float* __restrict__ gu, int8_t* __restrict__ hq_q,
     float* __restrict__ hq_d, int* __restrict__ hq_s, Q8sPlanes sh_gu) {
     constexpr int LPR = lpr_of<TYPE>(), NTH = 2 * d2_threads<TYPE>(), NW = NTH / WAVE, RPW = WAVE / LPR;
-    const int NFB = ff / 32, myjob = blockIdx.x / NFB, fb = blockIdx.x % NFB;
+    const int NFB = ff / 32, fb = blockIdx.x % NFB, nj = njobs_g[0];
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
     __shared__ sfnx_job jb;
     __shared__ float gbuf[SFNX_MAXT][32], ubuf[SFNX_MAXT][32];
     extern __shared__ __align__(16) unsigned char lds[];
-    if (myjob >= njobs_g[0]) return;
+    if ((int) blockIdx.x / NFB >= nj) return;
+    // the last job first: with a shared expert it is the shared job, which holds every row of the window and so takes
+    // the longest (2.5x a routed job's blocks at 16 rows); dispatched last, its blocks ran alone at the kernel's end
+    const int myjob = ((int) blockIdx.x / NFB + nj - 1) % nj;
     load_job(jb, jg + myjob);
     __syncthreads();
     const bool up = wave >= NW / 2;
