@@ -199,3 +199,24 @@ def test_fused_chain_drift_against_oracle():
     assert np.array_equal(f.piece("topi", torch.int32, (1, shape.K)).cpu().numpy(), oi)
     assert max_rel(f.piece("y", torch.float32, (1, shape.H)).cpu().numpy(), oy) < 2e-3
     assert max_rel(xf.cpu().numpy(), x) < 2e-3
+
+
+@pytest.mark.parametrize("T", [1, 4])
+def test_fused_window_with_no_picks(T):
+    """rows whose logits are all NaN pick nothing: with no shared expert the window has no job at all, and the fused
+    decode's kernels (whose gate|up blocks map to jobs modulo the job count) still finish, and agree with the unfused
+    path: every pick -1, a zero job count, y = 0"""
+    shape = moe.LayerShape(H=1024, E=64, K=6, ff=512, wtype=orc.Q4_K, shared=False)
+    L, _ = make_layer(shape, 71)
+    x0 = torch.full((T, shape.H), float("nan"), dtype=torch.float32, device="cuda")
+    b = moe.DecodeBuffers(shape, T)
+    y = torch.empty_like(x0)
+    moe.decode_layer(L, x0, y, b)
+    f = moe.FusedDecode([L], T)
+    xf = x0.clone()
+    f(xf, norm=False)
+    torch.cuda.synchronize()
+    assert (b.topi == -1).all() and int(b.njobs[0]) == 0
+    assert (f.piece("topi", torch.int32, (T, shape.K)) == -1).all()
+    assert int(f.piece("njobs", torch.int32, (2,))[0]) == 0
+    assert (y == 0).all() and (f.piece("y", torch.float32, (T, shape.H)) == 0).all()
