@@ -46,8 +46,11 @@ k_moe_mv(const uint8_t* __restrict__ A, size_t sa, int R, int C, const J* __rest
     constexpr bool BIG = std::is_same_v<J, sfnx_bigjob>;
     constexpr int LPR = is_kquant(TYPE) ? 8 : 16, RPB = mv_threads<TYPE, G, DOWN, BIG>() / LPR;
     constexpr int RPL = mv_rows_per_lane<TYPE, G, DOWN, BIG>();
-    const int ji = blockIdx.y;
-    if (ji >= *njobs) return;
+    // the last job first: with a shared expert it is the shared one, which holds every row of the window (or, on the
+    // prompt path, a run of full 64-row jobs); dispatched last, its blocks ran alone at the launch's end
+    const int nj = *njobs;
+    if ((int) blockIdx.y >= nj) return;
+    const int ji = ((int) blockIdx.y + nj - 1) % nj;
     extern __shared__ __align__(16) unsigned char lds[];
     __shared__ J jb;
     load_job(jb, jobs + ji);
